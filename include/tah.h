@@ -1,0 +1,142 @@
+/*
+ * tah.h - C ABI of libtah_hip.so, the MI355X (gfx950) accelerator for tabicl-anywhere's in-context hot path.
+ *
+ * It is the native side of the reference's two accelerator plugin traits and its card handle:
+ *
+ *   fit::Attend          src/fit.rs:45-74       (attend, attend_fits, in_context)
+ *   predict::AttendCached src/predict.rs:63-79   (attend, stage)
+ *   gpu::Gpu / VramModel  src/gpu.rs:725-1019, src/gpu.rs:2033-2149 (new, work budget, load, attend_resident,
+ *                                                                     in_context)
+ *
+ * Conventions (the reference's, src/gpu.rs:720-722, src/gpu.rs:887-889):
+ *   - every function returns an int status; 0 is success;
+ *   - TAH_E_BUDGET is the reference's io::ErrorKind::OutOfMemory (working-memory budget exceeded);
+ *   - TAH_E_DEVICE is a HIP runtime failure ("graphics card: ..."); callers answer on the CPU instead;
+ *   - TAH_E_DECLINED is the reference's Ok(None)/Ok(false): not offered for this shape, nothing was done;
+ *   - tah_last_error() gives the message of the last failure on a device handle;
+ *   - host buffers are caller-owned and borrowed for the duration of the call; functions taking host pointers
+ *     block until their results are on the host. Functions suffixed _dev take device pointers and leave the
+ *     work queued on the device handle's stream (tah_sync waits for it).
+ *   - a device handle may be shared by threads; calls on it are serialised.
+ *
+ * Matrices are row-major; weight matrices are [out][in] as PyTorch stores them. Keys and values of a fitted
+ * in-context layer stay in the reference's stored chunk layout (src/fit.rs:102-127, src/fit.rs:549-576):
+ * chunks of `chunk` training rows, the last one short; a chunk of rc rows is
+ *     f32:     [K: d][rc] f32  then [V: d][rc] f32
+ *     i16/i8:  [2d scales] f32, then [K: d][rc] ints, then [V: d][rc] ints     (value = int * scale[coordinate])
+ * and chunk ci starts at byte ci * record(d, chunk).
+ */
+#ifndef TAH_H
+#define TAH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    TAH_OK = 0,
+    TAH_E_ARG = 1,      /* invalid argument (io::ErrorKind::InvalidInput) */
+    TAH_E_BUDGET = 2,   /* over the working-memory budget (io::ErrorKind::OutOfMemory) */
+    TAH_E_DEVICE = 3,   /* HIP runtime error; answer on the CPU */
+    TAH_E_DECLINED = 4  /* not offered for this shape; nothing was done */
+};
+
+/* Stored formats of in-context keys and values: the reference's Kv codes (src/fit.rs:102-127, Kv::from_code). */
+enum { TAH_KV_F32 = 0, TAH_KV_I16 = 1, TAH_KV_I8 = 2 };
+
+/* One pre-norm attention block, x += attn(norm1 x); x += l2(gelu(l1(norm2 x))) (src/model.rs:27-98).
+ * ss_hidden is 0 for a block without the scalable softmax ("QASSMax", src/model.rs:14-24, src/nn.rs:97-152). */
+typedef struct tah_block {
+    int32_t d, heads, ff, ss_hidden;
+    const float *n1w, *n1b, *n2w, *n2b; /* [d] each; absent layer-norm biases are passed as zeros */
+    const float *in_w, *in_b;           /* [3d][d], [3d]: query, key, value projections stacked */
+    const float *out_w, *out_b;         /* [d][d], [d] */
+    const float *l1w, *l1b;             /* [ff][d], [ff] */
+    const float *l2w, *l2b;             /* [d][ff], [d] */
+    const float *b0w, *b0b;             /* scalable softmax base MLP: [ss_hidden][1], [ss_hidden] */
+    const float *b2w, *b2b;             /* [d][ss_hidden], [d] */
+    const float *q0w, *q0b;             /* query MLP shared by the heads: [ss_hidden][hd], [ss_hidden] */
+    const float *q2w, *q2b;             /* [hd][ss_hidden], [hd] */
+} tah_block;
+
+/* The whole network's weights and sizes (src/model.rs:110-143, Model::load src/model.rs:202-272). The two target
+ * tables are the reference's class_table form (src/model.rs:164-177): [max_classes][width] with the bias folded
+ * in, or for a regression model (max_classes 0) the layer as [weight][bias], 2 x width. */
+typedef struct tah_model_desc {
+    int32_t e, d, group, inds, cls, max_classes;
+    int32_t col_heads, row_heads, icl_heads;
+    int32_t col_blocks, row_blocks, icl_layers;
+    int32_t dec_hidden, outputs, rope_half;
+    const float *in_w, *in_b;       /* [e][group], [e] */
+    const tah_block *col_a1;        /* [col_blocks]: inducing points attend to cells (fitting only; may be NULL) */
+    const tah_block *col_a2;        /* [col_blocks]: cells attend to the inducing points' keys and values */
+    const float *col_ind;           /* [col_blocks][inds][e] (fitting only; may be NULL) */
+    const float *col_y;             /* [max_classes][e] or [2][e] */
+    const float *cls_tokens;        /* [cls][e] */
+    const tah_block *row;           /* [row_blocks] */
+    const float *rope_freqs;        /* [rope_half] */
+    const float *out_lnw, *out_lnb; /* [e] */
+    const tah_block *icl;           /* [icl_layers] */
+    const float *icl_y;             /* [max_classes][d] or [2][d] */
+    const float *lnw, *lnb;         /* [d] */
+    const float *dec0w, *dec0b;     /* [dec_hidden][d], [dec_hidden] */
+    const float *dec2w, *dec2b;     /* [outputs][dec_hidden], [outputs] */
+} tah_model_desc;
+
+typedef struct tah_dev tah_dev;         /* one GPU: its stream, working memory and last error (gpu::Gpu) */
+typedef struct tah_weights tah_weights; /* a model's weights on the card (gpu::GpuWeights) */
+typedef struct tah_model tah_model;     /* one fitted in-context problem held on the card (gpu::VramModel) */
+
+/* Bytes of one stored chunk of rc rows: Kv::record, src/fit.rs:123-126. */
+size_t tah_kv_record(int32_t kv_format, int32_t d, int32_t rc);
+
+/* ---- device handle: Gpu::new, set_work_budget, work_budget, working, overdrawn, release (src/gpu.rs:925-1019) */
+int tah_open(int32_t ordinal, tah_dev **out);
+void tah_close(tah_dev *dev);
+const char *tah_last_error(const tah_dev *dev);
+int tah_device_name(const tah_dev *dev, char *buf, size_t len);
+int tah_set_work_budget(tah_dev *dev, size_t bytes);
+size_t tah_work_budget(const tah_dev *dev);
+int tah_working(const tah_dev *dev, size_t *now, size_t *peak);
+size_t tah_overdrawn(const tah_dev *dev);
+int tah_release(tah_dev *dev);
+int tah_sync(tah_dev *dev);
+/* The device handle's HIP stream (a hipStream_t), for callers that time or order work around _dev calls. */
+void *tah_stream(tah_dev *dev);
+
+/* ---- weights: GpuWeights::new / bytes (src/gpu.rs:1838-2027). Copies every tensor the card uses. */
+int tah_weights_upload(tah_dev *dev, const tah_model_desc *m, tah_weights **out);
+size_t tah_weights_bytes(const tah_weights *w);
+void tah_weights_free(tah_weights *w);
+
+/* ---- fitted model on the card: VramModel::model_bytes / load (src/gpu.rs:2064-2116), but from the bundle's own
+ * chunk records as they are stored (n{j}_kv{l}), any of the three formats, no re-layout on the host.
+ * layer_records[l] points at layer l's bytes (tah_kv_record summed over its chunks); scales is n{j}_scale,
+ * [layers][d]. */
+size_t tah_model_bytes(int32_t kv_format, int32_t rows, int32_t chunk, int32_t d, int32_t layers);
+int tah_model_load(tah_dev *dev, const tah_weights *w, int32_t kv_format, int32_t rows, int32_t chunk,
+                   const uint8_t *const *layer_records, const float *scales, tah_model **out);
+void tah_model_free(tah_model *m);
+
+/* ---- prediction: AttendCached::attend (src/predict.rs:66, VramHandle src/gpu.rs:2648-2655): attention outputs
+ * [nq][d] (before the output projection) of queries q [nq][d] (already scaled) over layer `layer` of `model`. */
+int tah_attend_resident(tah_dev *dev, const tah_model *model, int32_t layer, const float *q, int32_t nq,
+                        float *out);
+int tah_attend_resident_dev(tah_dev *dev, const tah_model *model, int32_t layer, const float *q_dev, int32_t nq,
+                            float *out_dev);
+
+/* AttendCached::stage (src/predict.rs:70, Gpu::in_context src/gpu.rs:2140): the whole in-context stage of one
+ * problem, row representations h [nq][d] to the first out_n decoder outputs [nq][out_n]. */
+int tah_stage(tah_dev *dev, const tah_weights *w, const tah_model *model, const float *h, int32_t nq,
+              int32_t out_n, float *out);
+int tah_stage_dev(tah_dev *dev, const tah_weights *w, const tah_model *model, const float *h_dev, int32_t nq,
+                  int32_t out_n, float *out_dev);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TAH_H */
