@@ -110,6 +110,7 @@ void *tah_stream(tah_dev *dev);
 /* ---- weights: GpuWeights::new / bytes (src/gpu.rs:1838-2027). Copies every tensor the card uses. */
 int tah_weights_upload(tah_dev *dev, const tah_model_desc *m, tah_weights **out);
 size_t tah_weights_bytes(const tah_weights *w);
+/* Frees the weights; valid after tah_close of their device (no call may be using them). */
 void tah_weights_free(tah_weights *w);
 
 /* ---- fitted model on the card: VramModel::model_bytes / load (src/gpu.rs:2064-2116), but from the bundle's own
@@ -119,6 +120,7 @@ void tah_weights_free(tah_weights *w);
 size_t tah_model_bytes(int32_t kv_format, int32_t rows, int32_t chunk, int32_t d, int32_t layers);
 int tah_model_load(tah_dev *dev, const tah_weights *w, int32_t kv_format, int32_t rows, int32_t chunk,
                    const uint8_t *const *layer_records, const float *scales, tah_model **out);
+/* Frees the model; valid after tah_close of its device (no call may be using it). */
 void tah_model_free(tah_model *m);
 
 /* ---- prediction: AttendCached::attend (src/predict.rs:66, VramHandle src/gpu.rs:2648-2655): attention outputs

@@ -1,0 +1,501 @@
+// The C ABI (include/tah.h): device handles, working memory, weights and fitted models on the card, and the
+// in-context passes built from the kernels. Host code only; every kernel lives in the other sources.
+#include <algorithm>
+#include <cstring>
+#include <new>
+
+#include "common.hpp"
+
+using namespace tah;
+
+// ---- working memory --------------------------------------------------------------------------------------------
+namespace tah {
+
+void *Pool::take(size_t want, int device) {
+    want = (want + 255) & ~size_t(255);
+    if (want == 0) want = 256;
+    // the smallest idle buffer that is big enough (and not absurdly bigger)
+    int best = -1;
+    for (size_t i = 0; i < bufs.size(); i++)
+        if (!bufs[i].busy && bufs[i].bytes >= want && bufs[i].bytes <= 2 * want + (size_t(1) << 20) &&
+            (best < 0 || bufs[i].bytes < bufs[best].bytes))
+            best = (int)i;
+    if (best >= 0) {
+        bufs[best].busy = true;
+        return bufs[best].p;
+    }
+    if (bytes + want > budget) release_idle();
+    if (bytes + want > budget) {
+        overdrawn = std::max(overdrawn, bytes + want - budget);
+        throw BudgetError{"graphics card: working memory budget exceeded (" + std::to_string(bytes + want) + " > " +
+                          std::to_string(budget) + " bytes)"};
+    }
+    void *p = nullptr;
+    TAH_HIP(hipMalloc(&p, want));
+    bufs.push_back({p, want, true});
+    bytes += want;
+    peak = std::max(peak, bytes);
+    (void)device;
+    return p;
+}
+
+void Pool::give(void *p) {
+    for (auto &b : bufs)
+        if (b.p == p) b.busy = false;
+}
+
+void Pool::release_idle() {
+    std::vector<Buf> keep;
+    for (auto &b : bufs) {
+        if (b.busy) {
+            keep.push_back(b);
+        } else {
+            (void)hipFree(b.p);
+            bytes -= b.bytes;
+        }
+    }
+    bufs.swap(keep);
+}
+
+}  // namespace tah
+
+// Borrowed working buffers of one call, given back when it ends.
+struct Loans {
+    tah_dev *dev;
+    std::vector<void *> held;
+    explicit Loans(tah_dev *d) : dev(d) {}
+    template <class T>
+    T *take(size_t count) {
+        void *p = dev->pool.take(count * sizeof(T), dev->ordinal);
+        held.push_back(p);
+        return static_cast<T *>(p);
+    }
+    ~Loans() {
+        for (void *p : held) dev->pool.give(p);
+    }
+};
+
+template <class F>
+static int guarded(tah_dev *dev, F &&f) {
+    if (!dev) return TAH_E_ARG;
+    std::lock_guard<std::mutex> g(dev->lock);
+    try {
+        hipError_t e = hipSetDevice(dev->ordinal);
+        if (e != hipSuccess) throw DeviceError{std::string("graphics card: hipSetDevice: ") + hipGetErrorString(e)};
+        return f();
+    } catch (const DeviceError &e) {
+        dev->last_error = e.msg;
+        return TAH_E_DEVICE;
+    } catch (const ArgError &e) {
+        dev->last_error = e.msg;
+        return TAH_E_ARG;
+    } catch (const BudgetError &e) {
+        dev->last_error = e.msg;
+        return TAH_E_BUDGET;
+    } catch (const std::bad_alloc &) {
+        dev->last_error = "out of host memory";
+        return TAH_E_BUDGET;
+    }
+}
+
+extern "C" size_t tah_kv_record(int32_t kv_format, int32_t d, int32_t rc) {
+    const size_t w = kv_format == TAH_KV_F32 ? 4 : (kv_format == TAH_KV_I16 ? 2 : 1);
+    return 2 * (size_t)d * rc * w + (kv_format == TAH_KV_F32 ? 0 : 8 * (size_t)d);
+}
+
+static size_t layer_bytes(int fmt, int rows, int chunk, int d) {
+    return (size_t)(rows / chunk) * tah_kv_record(fmt, d, chunk) + (rows % chunk ? tah_kv_record(fmt, d, rows % chunk) : 0);
+}
+
+static size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+// ---- device handle ---------------------------------------------------------------------------------------------
+extern "C" int tah_open(int32_t ordinal, tah_dev **out) {
+    if (!out) return TAH_E_ARG;
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || ordinal < 0 || ordinal >= count) return TAH_E_DEVICE;
+    tah_dev *dev = new (std::nothrow) tah_dev();
+    if (!dev) return TAH_E_BUDGET;
+    dev->ordinal = ordinal;
+    int rc = guarded(dev, [&] {
+        hipDeviceProp_t prop;
+        TAH_HIP(hipGetDeviceProperties(&prop, ordinal));
+        dev->name = std::string(prop.name) + " (" + prop.gcnArchName + ")";
+        TAH_HIP(hipStreamCreateWithFlags(&dev->stream, hipStreamNonBlocking));
+        return TAH_OK;
+    });
+    if (rc != TAH_OK) {
+        delete dev;
+        return rc;
+    }
+    *out = dev;
+    return TAH_OK;
+}
+
+extern "C" void tah_close(tah_dev *dev) {
+    if (!dev) return;
+    {
+        std::lock_guard<std::mutex> g(dev->lock);
+        (void)hipSetDevice(dev->ordinal);
+        if (dev->stream) (void)hipStreamSynchronize(dev->stream);
+        for (auto &b : dev->pool.bufs) (void)hipFree(b.p);
+        dev->pool.bufs.clear();
+        if (dev->stream) (void)hipStreamDestroy(dev->stream);
+    }
+    delete dev;
+}
+
+extern "C" const char *tah_last_error(const tah_dev *dev) { return dev ? dev->last_error.c_str() : "no device"; }
+
+extern "C" int tah_device_name(const tah_dev *dev, char *buf, size_t len) {
+    if (!dev || !buf || len == 0) return TAH_E_ARG;
+    std::snprintf(buf, len, "%s", dev->name.c_str());
+    return TAH_OK;
+}
+
+extern "C" int tah_set_work_budget(tah_dev *dev, size_t bytes) {
+    return guarded(dev, [&] {
+        dev->pool.budget = bytes;
+        if (dev->pool.bytes > bytes) dev->pool.release_idle();
+        return TAH_OK;
+    });
+}
+
+extern "C" size_t tah_work_budget(const tah_dev *dev) { return dev ? dev->pool.budget : 0; }
+
+extern "C" int tah_working(const tah_dev *dev, size_t *now, size_t *peak) {
+    if (!dev) return TAH_E_ARG;
+    if (now) *now = dev->pool.bytes;
+    if (peak) *peak = dev->pool.peak;
+    return TAH_OK;
+}
+
+extern "C" size_t tah_overdrawn(const tah_dev *dev) { return dev ? dev->pool.overdrawn : 0; }
+
+extern "C" int tah_release(tah_dev *dev) {
+    return guarded(dev, [&] {
+        TAH_HIP(hipStreamSynchronize(dev->stream));
+        dev->pool.release_idle();
+        dev->pool.peak = dev->pool.bytes;
+        return TAH_OK;
+    });
+}
+
+extern "C" int tah_sync(tah_dev *dev) {
+    return guarded(dev, [&] {
+        TAH_HIP(hipStreamSynchronize(dev->stream));
+        return TAH_OK;
+    });
+}
+
+extern "C" void *tah_stream(tah_dev *dev) { return dev ? (void *)dev->stream : nullptr; }
+
+// ---- weights ---------------------------------------------------------------------------------------------------
+namespace {
+
+// Lays tensors out in one device allocation (each 256-byte aligned), then copies them in.
+struct Packer {
+    struct Item {
+        const float *src;
+        size_t n;
+        const float **dst;
+    };
+    std::vector<Item> items;
+    size_t bytes = 0;
+    void add(const float *src, size_t n, const float **dst) {
+        if (!src || n == 0) {
+            *dst = nullptr;
+            return;
+        }
+        items.push_back({src, n, dst});
+        bytes += align256(n * sizeof(float));
+    }
+};
+
+void add_block(Packer &pk, const tah_block &b, DevBlock &o) {
+    o.d = b.d;
+    o.heads = b.heads;
+    o.ff = b.ff;
+    o.ss_hidden = b.ss_hidden;
+    const size_t d = b.d, ff = b.ff, hid = b.ss_hidden, hd = b.heads ? b.d / b.heads : 0;
+    pk.add(b.n1w, d, &o.n1w);
+    pk.add(b.n1b, d, &o.n1b);
+    pk.add(b.n2w, d, &o.n2w);
+    pk.add(b.n2b, d, &o.n2b);
+    pk.add(b.in_w, 3 * d * d, &o.in_w);
+    pk.add(b.in_b, 3 * d, &o.in_b);
+    pk.add(b.out_w, d * d, &o.out_w);
+    pk.add(b.out_b, d, &o.out_b);
+    pk.add(b.l1w, ff * d, &o.l1w);
+    pk.add(b.l1b, ff, &o.l1b);
+    pk.add(b.l2w, d * ff, &o.l2w);
+    pk.add(b.l2b, d, &o.l2b);
+    if (hid) {
+        pk.add(b.b0w, hid, &o.b0w);
+        pk.add(b.b0b, hid, &o.b0b);
+        pk.add(b.b2w, d * hid, &o.b2w);
+        pk.add(b.b2b, d, &o.b2b);
+        pk.add(b.q0w, hid * hd, &o.q0w);
+        pk.add(b.q0b, hid, &o.q0b);
+        pk.add(b.q2w, hd * hid, &o.q2w);
+        pk.add(b.q2b, hd, &o.q2b);
+    } else {
+        o.b0w = o.b0b = o.b2w = o.b2b = o.q0w = o.q0b = o.q2w = o.q2b = nullptr;
+    }
+}
+
+bool block_ok(const tah_block &b) {
+    return b.d > 0 && b.heads > 0 && b.d % b.heads == 0 && b.ff > 0 && b.ss_hidden >= 0 && b.n1w && b.n1b && b.n2w &&
+           b.n2b && b.in_w && b.in_b && b.out_w && b.out_b && b.l1w && b.l1b && b.l2w && b.l2b &&
+           (b.ss_hidden == 0 || (b.b0w && b.b0b && b.b2w && b.b2b && b.q0w && b.q0b && b.q2w && b.q2b));
+}
+
+}  // namespace
+
+extern "C" int tah_weights_upload(tah_dev *dev, const tah_model_desc *m, tah_weights **out) {
+    if (!m || !out) return TAH_E_ARG;
+    *out = nullptr;
+    return guarded(dev, [&] {
+        if (m->e <= 0 || m->d <= 0 || m->icl_layers <= 0 || m->icl_heads <= 0 || m->d % m->icl_heads || !m->icl ||
+            m->dec_hidden <= 0 || m->outputs <= 0 || !m->lnw || !m->lnb || !m->dec0w || !m->dec0b || !m->dec2w || !m->dec2b)
+            throw ArgError{"weights: incomplete model description"};
+        for (int l = 0; l < m->icl_layers; l++)
+            if (!block_ok(m->icl[l]) || m->icl[l].d != m->d) throw ArgError{"weights: bad in-context block"};
+        auto *w = new tah_weights();
+        w->dev = dev;
+        w->ordinal = dev->ordinal;
+        w->e = m->e;
+        w->d = m->d;
+        w->group = m->group;
+        w->inds = m->inds;
+        w->cls = m->cls;
+        w->max_classes = m->max_classes;
+        w->col_heads = m->col_heads;
+        w->row_heads = m->row_heads;
+        w->icl_heads = m->icl_heads;
+        w->col_blocks = m->col_blocks;
+        w->row_blocks = m->row_blocks;
+        w->icl_layers = m->icl_layers;
+        w->dec_hidden = m->dec_hidden;
+        w->outputs = m->outputs;
+        w->rope_half = m->rope_half;
+        Packer pk;
+        const size_t e = m->e, d = m->d, ytab = m->max_classes > 0 ? m->max_classes : 2;
+        pk.add(m->in_w, e * m->group, &w->in_w);
+        pk.add(m->in_b, e, &w->in_b);
+        pk.add(m->col_ind, (size_t)m->col_blocks * m->inds * e, &w->col_ind);
+        pk.add(m->col_y, ytab * e, &w->col_y);
+        pk.add(m->cls_tokens, (size_t)m->cls * e, &w->cls_tokens);
+        pk.add(m->rope_freqs, m->rope_half, &w->rope_freqs);
+        pk.add(m->out_lnw, e, &w->out_lnw);
+        pk.add(m->out_lnb, e, &w->out_lnb);
+        pk.add(m->icl_y, ytab * d, &w->icl_y);
+        pk.add(m->lnw, d, &w->lnw);
+        pk.add(m->lnb, d, &w->lnb);
+        pk.add(m->dec0w, (size_t)m->dec_hidden * d, &w->dec0w);
+        pk.add(m->dec0b, m->dec_hidden, &w->dec0b);
+        pk.add(m->dec2w, (size_t)m->outputs * m->dec_hidden, &w->dec2w);
+        pk.add(m->dec2b, m->outputs, &w->dec2b);
+        w->icl.resize(m->icl_layers);
+        for (int l = 0; l < m->icl_layers; l++) add_block(pk, m->icl[l], w->icl[l]);
+        if (m->col_a2 && m->col_blocks > 0) {
+            w->col_a2.resize(m->col_blocks);
+            for (int i = 0; i < m->col_blocks; i++) add_block(pk, m->col_a2[i], w->col_a2[i]);
+        }
+        if (m->col_a1 && m->col_blocks > 0) {
+            w->col_a1.resize(m->col_blocks);
+            for (int i = 0; i < m->col_blocks; i++) add_block(pk, m->col_a1[i], w->col_a1[i]);
+        }
+        if (m->row && m->row_blocks > 0) {
+            w->row.resize(m->row_blocks);
+            for (int i = 0; i < m->row_blocks; i++) add_block(pk, m->row[i], w->row[i]);
+        }
+        try {
+            TAH_HIP(hipMalloc(&w->arena, std::max<size_t>(pk.bytes, 256)));
+            w->bytes = pk.bytes;
+            size_t at = 0;
+            for (auto &it : pk.items) {
+                float *dst = reinterpret_cast<float *>(static_cast<char *>(w->arena) + at);
+                TAH_HIP(hipMemcpy(dst, it.src, it.n * sizeof(float), hipMemcpyHostToDevice));
+                *it.dst = dst;
+                at += align256(it.n * sizeof(float));
+            }
+        } catch (...) {
+            if (w->arena) (void)hipFree(w->arena);
+            delete w;
+            throw;
+        }
+        *out = w;
+        return TAH_OK;
+    });
+}
+
+extern "C" size_t tah_weights_bytes(const tah_weights *w) { return w ? w->bytes : 0; }
+
+extern "C" void tah_weights_free(tah_weights *w) {
+    // independent of the device handle, which may already be closed; hipFree waits for work that uses the memory
+    if (!w) return;
+    (void)hipSetDevice(w->ordinal);
+    if (w->arena) (void)hipFree(w->arena);
+    delete w;
+}
+
+// ---- fitted model ----------------------------------------------------------------------------------------------
+extern "C" size_t tah_model_bytes(int32_t kv_format, int32_t rows, int32_t chunk, int32_t d, int32_t layers) {
+    if (rows <= 0 || chunk <= 0 || d <= 0 || layers <= 0 || kv_format < 0 || kv_format > 2) return 0;
+    return (size_t)layers * align256(layer_bytes(kv_format, rows, chunk, d)) + align256(sizeof(float) * layers * d);
+}
+
+extern "C" int tah_model_load(tah_dev *dev, const tah_weights *w, int32_t kv_format, int32_t rows, int32_t chunk,
+                              const uint8_t *const *layer_records, const float *scales, tah_model **out) {
+    if (!out || !w || !layer_records || !scales) return TAH_E_ARG;
+    *out = nullptr;
+    return guarded(dev, [&] {
+        if (rows <= 0 || chunk <= 0 || kv_format < 0 || kv_format > 2) throw ArgError{"model: bad rows, chunk or format"};
+        for (int l = 0; l < w->icl_layers; l++)
+            if (!layer_records[l]) throw ArgError{"model: missing layer records"};
+        auto *m = new tah_model();
+        m->dev = dev;
+        m->ordinal = dev->ordinal;
+        m->kv_format = kv_format;
+        m->rows = rows;
+        m->chunk = chunk;
+        m->d = w->d;
+        m->layers = w->icl_layers;
+        m->heads = w->icl_heads;
+        m->layer_bytes = align256(layer_bytes(kv_format, rows, chunk, w->d));
+        m->bytes = tah_model_bytes(kv_format, rows, chunk, w->d, w->icl_layers);
+        try {
+            TAH_HIP(hipMalloc(&m->records, m->bytes));
+            m->scales = reinterpret_cast<float *>(m->records + (size_t)m->layers * m->layer_bytes);
+            for (int l = 0; l < m->layers; l++)
+                TAH_HIP(hipMemcpy(m->records + (size_t)l * m->layer_bytes, layer_records[l],
+                                  layer_bytes(kv_format, rows, chunk, w->d), hipMemcpyHostToDevice));
+            TAH_HIP(hipMemcpy(m->scales, scales, sizeof(float) * m->layers * m->d, hipMemcpyHostToDevice));
+        } catch (...) {
+            if (m->records) (void)hipFree(m->records);
+            delete m;
+            throw;
+        }
+        *out = m;
+        return TAH_OK;
+    });
+}
+
+extern "C" void tah_model_free(tah_model *m) {
+    if (!m) return;
+    (void)hipSetDevice(m->ordinal);
+    if (m->records) (void)hipFree(m->records);
+    delete m;
+}
+
+// ---- prediction ------------------------------------------------------------------------------------------------
+static AttnShape shape_of(const tah_model *m, int heads, int nq) {
+    return AttnShape{nq, m->rows, m->chunk, m->d, heads, m->kv_format};
+}
+
+static const uint8_t *layer_of(const tah_model *m, int l) { return m->records + (size_t)l * m->layer_bytes; }
+
+extern "C" int tah_attend_resident_dev(tah_dev *dev, const tah_model *model, int32_t layer, const float *q_dev,
+                                       int32_t nq, float *out_dev) {
+    if (!model || !q_dev || !out_dev) return TAH_E_ARG;
+    return guarded(dev, [&] {
+        if (layer < 0 || layer >= model->layers || nq < 0) throw ArgError{"attend: bad layer or row count"};
+        Loans loans(dev);
+        const AttnShape a = shape_of(model, model->heads, nq);
+        void *work = loans.take<uint8_t>(attention_work_bytes(a));
+        attention(dev->stream, a, q_dev, layer_of(model, layer), out_dev, work);
+        return TAH_OK;
+    });
+}
+
+extern "C" int tah_attend_resident(tah_dev *dev, const tah_model *model, int32_t layer, const float *q, int32_t nq,
+                                   float *out) {
+    if (!model || !q || !out) return TAH_E_ARG;
+    return guarded(dev, [&] {
+        if (layer < 0 || layer >= model->layers || nq < 0) throw ArgError{"attend: bad layer or row count"};
+        if (nq == 0) return TAH_OK;
+        Loans loans(dev);
+        const size_t n = (size_t)nq * model->d;
+        float *qd = loans.take<float>(n), *od = loans.take<float>(n);
+        const AttnShape a = shape_of(model, model->heads, nq);
+        void *work = loans.take<uint8_t>(attention_work_bytes(a));
+        TAH_HIP(hipMemcpyAsync(qd, q, n * sizeof(float), hipMemcpyHostToDevice, dev->stream));
+        attention(dev->stream, a, qd, layer_of(model, layer), od, work);
+        TAH_HIP(hipMemcpyAsync(out, od, n * sizeof(float), hipMemcpyDeviceToHost, dev->stream));
+        TAH_HIP(hipStreamSynchronize(dev->stream));
+        return TAH_OK;
+    });
+}
+
+// The in-context stage for nq rows already on the card (src/predict.rs:413-585): h_dev is updated in place.
+static void stage_rows(tah_dev *dev, const tah_weights *w, const tah_model *model, float *h, int nq, int out_n,
+                       float *out, Loans &loans) {
+    const int d = w->d, heads = w->icl_heads;
+    int ff = 0;
+    for (auto &b : w->icl) ff = std::max(ff, b.ff);
+    const int wide = std::max(ff, w->dec_hidden);
+    hipStream_t s = dev->stream;
+    float *t = loans.take<float>((size_t)nq * d);
+    float *q = loans.take<float>((size_t)nq * d);
+    float *att = loans.take<float>((size_t)nq * d);
+    float *mid = loans.take<float>((size_t)nq * wide);
+    const AttnShape a = shape_of(model, heads, nq);
+    void *work = loans.take<uint8_t>(attention_work_bytes(a));
+    for (int l = 0; l < w->icl_layers; l++) {
+        const DevBlock &b = w->icl[l];
+        // query: q = modulate(Wq norm1(h) + bq)  (src/nn.rs:130-152)
+        layer_norm(s, nq, d, h, d, b.n1w, b.n1b, t, d);
+        gemm(s, nq, d, d, t, d, b.in_w, b.in_b, q, d, EPI_NONE, nullptr, 0);
+        query_modulate(s, nq, b, model->scales + (size_t)l * d, q);
+        // attention over the stored layer, then h += out(att)  (src/predict.rs:421-551)
+        attention(s, a, q, layer_of(model, l), att, work);
+        gemm(s, nq, d, d, att, d, b.out_w, b.out_b, h, d, EPI_RESID, h, d);
+        // h += l2(gelu(l1(norm2 h)))  (src/predict.rs:552-568)
+        layer_norm(s, nq, d, h, d, b.n2w, b.n2b, t, d);
+        gemm(s, nq, b.ff, d, t, d, b.l1w, b.l1b, mid, b.ff, EPI_GELU, nullptr, 0);
+        gemm(s, nq, d, b.ff, mid, b.ff, b.l2w, b.l2b, h, d, EPI_RESID, h, d);
+    }
+    // decoder, first out_n outputs  (src/predict.rs:570-585)
+    layer_norm(s, nq, d, h, d, w->lnw, w->lnb, t, d);
+    gemm(s, nq, w->dec_hidden, d, t, d, w->dec0w, w->dec0b, mid, w->dec_hidden, EPI_GELU, nullptr, 0);
+    gemm(s, nq, out_n, w->dec_hidden, mid, w->dec_hidden, w->dec2w, w->dec2b, out, out_n, EPI_NONE, nullptr, 0);
+}
+
+static void check_stage(const tah_weights *w, const tah_model *model, int nq, int out_n) {
+    if (!w || !model) throw ArgError{"stage: no weights or model"};
+    if (model->d != w->d || model->layers != w->icl_layers) throw ArgError{"stage: model and weights disagree"};
+    if (nq < 0 || out_n <= 0 || out_n > w->outputs) throw ArgError{"stage: bad row or output count"};
+}
+
+extern "C" int tah_stage_dev(tah_dev *dev, const tah_weights *w, const tah_model *model, const float *h_dev, int32_t nq,
+                             int32_t out_n, float *out_dev) {
+    if (!h_dev || !out_dev) return TAH_E_ARG;
+    return guarded(dev, [&] {
+        check_stage(w, model, nq, out_n);
+        if (nq == 0) return TAH_OK;
+        Loans loans(dev);
+        float *h = loans.take<float>((size_t)nq * w->d);
+        TAH_HIP(hipMemcpyAsync(h, h_dev, sizeof(float) * nq * w->d, hipMemcpyDeviceToDevice, dev->stream));
+        stage_rows(dev, w, model, h, nq, out_n, out_dev, loans);
+        return TAH_OK;
+    });
+}
+
+extern "C" int tah_stage(tah_dev *dev, const tah_weights *w, const tah_model *model, const float *h, int32_t nq,
+                         int32_t out_n, float *out) {
+    if (!h || !out) return TAH_E_ARG;
+    return guarded(dev, [&] {
+        check_stage(w, model, nq, out_n);
+        if (nq == 0) return TAH_OK;
+        Loans loans(dev);
+        float *hd = loans.take<float>((size_t)nq * w->d);
+        float *od = loans.take<float>((size_t)nq * out_n);
+        TAH_HIP(hipMemcpyAsync(hd, h, sizeof(float) * nq * w->d, hipMemcpyHostToDevice, dev->stream));
+        stage_rows(dev, w, model, hd, nq, out_n, od, loans);
+        TAH_HIP(hipMemcpyAsync(out, od, sizeof(float) * nq * out_n, hipMemcpyDeviceToHost, dev->stream));
+        TAH_HIP(hipStreamSynchronize(dev->stream));
+        return TAH_OK;
+    });
+}

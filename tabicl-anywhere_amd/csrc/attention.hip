@@ -1,0 +1,410 @@
+// In-context attention of query rows over one stored layer of training-row keys and values, read in place from
+// the bundle's chunk records (f32, or i16/i8 codes with per-chunk, per-coordinate scales dequantised in the
+// kernel). This replaces the reference's streaming loop (src/predict.rs:427-533 with Soft::update/update_int,
+// src/nn.rs:194-258) and its WGSL attend/merge shaders (src/gpu.rs:492-627).
+//
+// Keys are visited in blocks of 64 that never straddle a stored chunk. Each workgroup keeps, per query and head,
+// the running maximum m, weight sum l and weighted value sum o over its range of key blocks (the online softmax
+// of Soft); when the keys are split over several workgroups, their (m, l, o) are combined by a log-sum-exp merge
+// (Soft::merge, src/nn.rs:261-276) and divided through (Soft::finish).
+//
+// Two kernels:
+//  * k_attn_mfma64: head width 64 and at least 64 queries. 4 wavefronts x 16 queries share LDS tiles of K and V
+//    (64 coordinates x 64 keys). Scores are formed transposed, S^T = K Q^T, with v_mfma_f32_16x16x4_f32 so that
+//    each lane owns one query (lane % 16) in both products; the softmax then needs only two cross-lane steps, and
+//    O^T = V^T P^T takes each lane's own weights as its B operand with no transpose through LDS.
+//  * k_attn_decode: any head width up to 64 and few queries: one wavefront per (key range, head, 8 queries),
+//    lane = key for the scores and lane = coordinate for the weighted sum. Bandwidth-bound, as single-row
+//    prediction is.
+#include <algorithm>
+
+#include "common.hpp"
+#include "device_math.hpp"
+
+namespace tah {
+
+constexpr int KB = 64;   // keys per block
+constexpr int KP = 68;   // padded LDS row of a K or V tile
+constexpr int QG = 8;    // queries per decode workgroup
+
+struct KeyBlocks {
+    int bpc;       // key blocks per full chunk
+    int n_chunks;  // stored chunks
+    int last_rc;   // rows of the last chunk
+    int n_kb;      // key blocks in all
+};
+
+__host__ __device__ inline KeyBlocks key_blocks(int rows, int chunk) {
+    KeyBlocks k;
+    k.bpc = (chunk + KB - 1) / KB;
+    k.n_chunks = (rows + chunk - 1) / chunk;
+    k.last_rc = rows - (k.n_chunks - 1) * chunk;
+    k.n_kb = (k.n_chunks - 1) * k.bpc + (k.last_rc + KB - 1) / KB;
+    return k;
+}
+
+__host__ __device__ inline size_t record_bytes(int fmt, int d, int rc) {
+    const size_t w = fmt == TAH_KV_F32 ? 4 : (fmt == TAH_KV_I16 ? 2 : 1);
+    return 2 * (size_t)d * rc * w + (fmt == TAH_KV_F32 ? 0 : 8 * (size_t)d);
+}
+
+// Where key block kb lives: its chunk's record, the chunk's row count and the block's first row in it.
+struct Where {
+    const uint8_t *rec;
+    int rc, o, nk;
+};
+
+__device__ inline Where locate(const KeyBlocks &k, int kb, const uint8_t *records, int fmt, int d, int chunk) {
+    Where w;
+    const int ci = kb / k.bpc, j = kb % k.bpc;
+    w.rec = records + (size_t)ci * record_bytes(fmt, d, chunk);
+    w.rc = ci == k.n_chunks - 1 ? k.last_rc : chunk;
+    w.o = j * KB;
+    w.nk = min(KB, w.rc - w.o);
+    return w;
+}
+
+// Element (coordinate c of the 2d stacked K;V rows, key r) of a record, widened and scaled to f32.
+template <int FMT>
+__device__ __forceinline__ float rec_value(const uint8_t *rec, int d, int rc, int c, int r) {
+    if (FMT == TAH_KV_F32) return reinterpret_cast<const float *>(rec)[(size_t)c * rc + r];
+    const float sc = reinterpret_cast<const float *>(rec)[c];
+    const uint8_t *body = rec + 8 * (size_t)d;
+    if (FMT == TAH_KV_I16) return (float)reinterpret_cast<const int16_t *>(body)[(size_t)c * rc + r] * sc;
+    return (float)reinterpret_cast<const int8_t *>(body)[(size_t)c * rc + r] * sc;
+}
+
+// Sixteen consecutive keys (from key o16) of stacked coordinate c, widened, into dst[0..16). Fast path when the
+// row segment is whole and 16-byte aligned.
+template <int FMT>
+__device__ __forceinline__ void load16(const uint8_t *rec, int d, int rc, int c, int o16, int nk_left, bool fast,
+                                       float *dst) {
+    if (fast) {
+        if (FMT == TAH_KV_F32) {
+            const float4 *p = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(rec) + (size_t)c * rc + o16);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 v = p[i];
+                dst[4 * i] = v.x;
+                dst[4 * i + 1] = v.y;
+                dst[4 * i + 2] = v.z;
+                dst[4 * i + 3] = v.w;
+            }
+        } else {
+            const float sc = reinterpret_cast<const float *>(rec)[c];
+            const uint8_t *body = rec + 8 * (size_t)d;
+            if (FMT == TAH_KV_I16) {
+                const int16_t *p = reinterpret_cast<const int16_t *>(body) + (size_t)c * rc + o16;
+                const uint4 a = reinterpret_cast<const uint4 *>(p)[0], b = reinterpret_cast<const uint4 *>(p)[1];
+                const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    dst[2 * i] = (float)(int16_t)(w[i] & 0xffffu) * sc;
+                    dst[2 * i + 1] = (float)(int16_t)(w[i] >> 16) * sc;
+                }
+            } else {
+                const int8_t *p = reinterpret_cast<const int8_t *>(body) + (size_t)c * rc + o16;
+                const uint4 a = reinterpret_cast<const uint4 *>(p)[0];
+                const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) dst[4 * i + j] = (float)(int8_t)((w[i] >> (8 * j)) & 0xffu) * sc;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) dst[i] = i < nk_left ? rec_value<FMT>(rec, d, rc, c, o16 + i) : 0.0f;
+    }
+}
+
+// ---- MFMA kernel: head width 64 ------------------------------------------------------------------------------
+// grid (query tiles of 64, heads, splits); 256 threads.
+template <int FMT>
+__global__ __launch_bounds__(256) void k_attn_mfma64(int nq, int rows, int chunk, int d, int heads,
+                                                      const float *__restrict__ q, const uint8_t *__restrict__ records,
+                                                      int kb_per_split, float *__restrict__ part_o,
+                                                      float *__restrict__ part_ml, float *__restrict__ out) {
+    __shared__ float Ks[64][KP];
+    __shared__ float Vs[64][KP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = blockIdx.y, split = blockIdx.z, splits = gridDim.z;
+    const KeyBlocks kbs = key_blocks(rows, chunk);
+    const int kb0 = split * kb_per_split, kb1 = min(kbs.n_kb, kb0 + kb_per_split);
+    const int r16 = lane & 15, g4 = lane >> 4;
+    const int qrow = blockIdx.x * 64 + wave * 16 + r16;
+    const bool qlive = qrow < nq;
+
+    // this lane's query coordinates: c = 16 cs + 4 g4 + t for cs, t in 0..3
+    float qreg[16];
+#pragma unroll
+    for (int cs = 0; cs < 4; cs++) {
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (qlive) v = *reinterpret_cast<const float4 *>(q + (size_t)qrow * d + h * 64 + 16 * cs + 4 * g4);
+        qreg[4 * cs] = v.x;
+        qreg[4 * cs + 1] = v.y;
+        qreg[4 * cs + 2] = v.z;
+        qreg[4 * cs + 3] = v.w;
+    }
+    float m = -INFINITY, l = 0.0f;
+    floatx4 acc_o[4];
+#pragma unroll
+    for (int db = 0; db < 4; db++) acc_o[db] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int lc = tid >> 2, seg = (tid & 3) * 16;  // loader: coordinate row and 16-key segment
+    const int width = FMT == TAH_KV_F32 ? 4 : (FMT == TAH_KV_I16 ? 2 : 1);
+    for (int kb = kb0; kb < kb1; kb++) {
+        const Where w = locate(kbs, kb, records, FMT, d, chunk);
+        const bool fast = w.nk == KB && ((size_t)w.rc * width) % 16 == 0;
+        float tmp[16];
+        load16<FMT>(w.rec, d, w.rc, h * 64 + lc, w.o + seg, w.nk - seg, fast, tmp);
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) *reinterpret_cast<float4 *>(&Ks[lc][seg + i]) = make_float4(tmp[i], tmp[i + 1], tmp[i + 2], tmp[i + 3]);
+        load16<FMT>(w.rec, d, w.rc, d + h * 64 + lc, w.o + seg, w.nk - seg, fast, tmp);
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) *reinterpret_cast<float4 *>(&Vs[lc][seg + i]) = make_float4(tmp[i], tmp[i + 1], tmp[i + 2], tmp[i + 3]);
+        __syncthreads();
+
+        // S^T = K Q^T: lane holds S[q = r16][key = 16 kb4 + 4 g4 + v]
+        floatx4 sacc[4];
+#pragma unroll
+        for (int kb4 = 0; kb4 < 4; kb4++) sacc[kb4] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int cs = 0; cs < 4; cs++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int c = 16 * cs + 4 * g4 + t;
+#pragma unroll
+                for (int kb4 = 0; kb4 < 4; kb4++)
+                    sacc[kb4] = __builtin_amdgcn_mfma_f32_16x16x4f32(Ks[c][16 * kb4 + r16], qreg[4 * cs + t], sacc[kb4], 0, 0, 0);
+            }
+        // online softmax for this lane's query over the block's 64 keys (16 here, the rest on lanes ^16, ^32)
+        float mb = -INFINITY;
+#pragma unroll
+        for (int kb4 = 0; kb4 < 4; kb4++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int key = 16 * kb4 + 4 * g4 + v;
+                if (key >= w.nk) sacc[kb4][v] = -INFINITY;
+                mb = fmaxf(mb, sacc[kb4][v]);
+            }
+        mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
+        mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+        const float mnew = fmaxf(m, mb);
+        const float alpha = fast_exp(m - mnew);
+        float lb = 0.0f;
+#pragma unroll
+        for (int kb4 = 0; kb4 < 4; kb4++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const float p = fast_exp(sacc[kb4][v] - mnew);
+                sacc[kb4][v] = p;
+                lb += p;
+            }
+        lb += __shfl_xor(lb, 16, 64);
+        lb += __shfl_xor(lb, 32, 64);
+        l = l * alpha + lb;
+        m = mnew;
+#pragma unroll
+        for (int db = 0; db < 4; db++) acc_o[db] *= alpha;
+        // O^T += V^T P^T: lane holds O[q = r16][dim = 16 db + 4 g4 + v]
+#pragma unroll
+        for (int kb4 = 0; kb4 < 4; kb4++)
+#pragma unroll
+            for (int db = 0; db < 4; db++) {
+                const float4 vv = *reinterpret_cast<const float4 *>(&Vs[16 * db + r16][16 * kb4 + 4 * g4]);
+                acc_o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.x, sacc[kb4][0], acc_o[db], 0, 0, 0);
+                acc_o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.y, sacc[kb4][1], acc_o[db], 0, 0, 0);
+                acc_o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.z, sacc[kb4][2], acc_o[db], 0, 0, 0);
+                acc_o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.w, sacc[kb4][3], acc_o[db], 0, 0, 0);
+            }
+        __syncthreads();
+    }
+    if (!qlive) return;
+    if (splits == 1) {
+        const float inv = 1.0f / l;
+#pragma unroll
+        for (int db = 0; db < 4; db++) {
+            float4 o4 = make_float4(acc_o[db][0] * inv, acc_o[db][1] * inv, acc_o[db][2] * inv, acc_o[db][3] * inv);
+            *reinterpret_cast<float4 *>(out + (size_t)qrow * d + h * 64 + 16 * db + 4 * g4) = o4;
+        }
+    } else {
+        const size_t at = ((size_t)split * nq + qrow) * heads + h;
+#pragma unroll
+        for (int db = 0; db < 4; db++) {
+            float4 o4 = make_float4(acc_o[db][0], acc_o[db][1], acc_o[db][2], acc_o[db][3]);
+            *reinterpret_cast<float4 *>(part_o + at * 64 + 16 * db + 4 * g4) = o4;
+        }
+        if (g4 == 0) {
+            part_ml[at * 2] = m;
+            part_ml[at * 2 + 1] = l;
+        }
+    }
+}
+
+// ---- decode kernel: any head width <= 64, few queries --------------------------------------------------------
+// grid (splits, heads, query groups of QG); 64 threads.
+template <int FMT>
+__global__ __launch_bounds__(64) void k_attn_decode(int nq, int rows, int chunk, int d, int heads,
+                                                     const float *__restrict__ q, const uint8_t *__restrict__ records,
+                                                     int kb_per_split, float *__restrict__ part_o,
+                                                     float *__restrict__ part_ml, float *__restrict__ out) {
+    __shared__ float Qs[QG][64];
+    __shared__ float Ks[64][KB + 1];
+    __shared__ float Vs[64][KB + 1];
+    __shared__ float Ps[QG][KB];
+    const int lane = threadIdx.x;
+    const int split = blockIdx.x, h = blockIdx.y, q0 = blockIdx.z * QG;
+    const int splits = gridDim.x;
+    const int hd = d / heads;
+    const KeyBlocks kbs = key_blocks(rows, chunk);
+    const int kb0 = split * kb_per_split, kb1 = min(kbs.n_kb, kb0 + kb_per_split);
+    for (int qi = 0; qi < QG; qi++) Qs[qi][lane] = (lane < hd && q0 + qi < nq) ? q[(size_t)(q0 + qi) * d + h * hd + lane] : 0.0f;
+    float m[QG], l[QG], o[QG];
+#pragma unroll
+    for (int qi = 0; qi < QG; qi++) {
+        m[qi] = -INFINITY;
+        l[qi] = 0.0f;
+        o[qi] = 0.0f;
+    }
+    for (int kb = kb0; kb < kb1; kb++) {
+        const Where w = locate(kbs, kb, records, FMT, d, chunk);
+        __syncthreads();
+        for (int c = 0; c < hd; c++) {
+            Ks[c][lane] = lane < w.nk ? rec_value<FMT>(w.rec, d, w.rc, h * hd + c, w.o + lane) : 0.0f;
+            Vs[c][lane] = lane < w.nk ? rec_value<FMT>(w.rec, d, w.rc, d + h * hd + c, w.o + lane) : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int qi = 0; qi < QG; qi++) {
+            float s = 0.0f;
+            for (int c = 0; c < hd; c++) s += Qs[qi][c] * Ks[c][lane];
+            if (lane >= w.nk) s = -INFINITY;
+            const float mnew = fmaxf(m[qi], wave_max(s));
+            const float alpha = fast_exp(m[qi] - mnew);
+            const float p = lane < w.nk ? fast_exp(s - mnew) : 0.0f;
+            l[qi] = l[qi] * alpha + wave_sum(p);
+            m[qi] = mnew;
+            o[qi] *= alpha;
+            Ps[qi][lane] = p;
+        }
+        __syncthreads();
+        if (lane < hd) {
+#pragma unroll
+            for (int qi = 0; qi < QG; qi++) {
+                float a = 0.0f;
+                for (int k = 0; k < KB; k++) a += Ps[qi][k] * Vs[lane][k];
+                o[qi] += a;
+            }
+        }
+    }
+    if (lane >= hd) return;
+#pragma unroll
+    for (int qi = 0; qi < QG; qi++) {
+        const int qr = q0 + qi;
+        if (qr >= nq) break;
+        if (splits == 1) {
+            out[(size_t)qr * d + h * hd + lane] = o[qi] / l[qi];
+        } else {
+            const size_t at = ((size_t)split * nq + qr) * heads + h;
+            part_o[at * hd + lane] = o[qi];
+            if (lane == 0) {
+                part_ml[at * 2] = m[qi];
+                part_ml[at * 2 + 1] = l[qi];
+            }
+        }
+    }
+}
+
+// ---- split merge: Soft::merge then Soft::finish ---------------------------------------------------------------
+// grid nq * heads; 64 threads (lane = coordinate).
+__global__ __launch_bounds__(64) void k_attn_merge(int nq, int d, int heads, int splits, const float *__restrict__ part_o,
+                                                    const float *__restrict__ part_ml, float *__restrict__ out) {
+    const int item = blockIdx.x, lane = threadIdx.x;
+    const int qr = item / heads, h = item % heads, hd = d / heads;
+    float M = -INFINITY;
+    for (int s = 0; s < splits; s++) {
+        const size_t at = ((size_t)s * nq + qr) * heads + h;
+        if (part_ml[at * 2 + 1] > 0.0f) M = fmaxf(M, part_ml[at * 2]);
+    }
+    for (int c = lane; c < hd; c += 64) {
+        float L = 0.0f, O = 0.0f;
+        for (int s = 0; s < splits; s++) {
+            const size_t at = ((size_t)s * nq + qr) * heads + h;
+            const float ls = part_ml[at * 2 + 1];
+            if (ls <= 0.0f) continue;
+            const float f = fast_exp(part_ml[at * 2] - M);
+            L += ls * f;
+            O += part_o[at * hd + c] * f;
+        }
+        out[(size_t)qr * d + h * hd + c] = O / L;
+    }
+}
+
+// ---- planning and launch --------------------------------------------------------------------------------------
+struct AttnPlan {
+    bool mfma;
+    int splits, kb_per_split, groups;
+};
+
+static AttnPlan plan(const AttnShape &a) {
+    AttnPlan p;
+    const KeyBlocks k = key_blocks(a.rows, a.chunk);
+    const int hd = a.d / a.heads;
+    p.mfma = hd == 64 && a.nq >= 64;
+    p.groups = p.mfma ? (a.nq + 63) / 64 : (a.nq + QG - 1) / QG;
+    // enough workgroups to fill 256 compute units a few times over, each with at least 2 key blocks
+    const long target = 1024;
+    long want = (target + (long)p.groups * a.heads - 1) / ((long)p.groups * a.heads);
+    want = std::max(1L, std::min(want, (long)(k.n_kb + 1) / 2));
+    p.kb_per_split = (int)((k.n_kb + want - 1) / want);
+    p.splits = (k.n_kb + p.kb_per_split - 1) / p.kb_per_split;
+    return p;
+}
+
+size_t attention_work_bytes(const AttnShape &a) {
+    const AttnPlan p = plan(a);
+    if (p.splits == 1) return 0;
+    const int hd = a.d / a.heads;
+    return sizeof(float) * (size_t)p.splits * a.nq * a.heads * (hd + 2) + 256;
+}
+
+template <int FMT>
+static void launch(hipStream_t s, const AttnShape &a, const AttnPlan &p, const float *q, const uint8_t *records, float *out,
+                   float *part_o, float *part_ml) {
+    if (p.mfma) {
+        hipLaunchKernelGGL(k_attn_mfma64<FMT>, dim3(p.groups, a.heads, p.splits), dim3(256), 0, s, a.nq, a.rows, a.chunk,
+                           a.d, a.heads, q, records, p.kb_per_split, part_o, part_ml, out);
+    } else {
+        hipLaunchKernelGGL(k_attn_decode<FMT>, dim3(p.splits, a.heads, p.groups), dim3(64), 0, s, a.nq, a.rows, a.chunk,
+                           a.d, a.heads, q, records, p.kb_per_split, part_o, part_ml, out);
+    }
+    TAH_LAUNCHED();
+}
+
+void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t *records, float *out, void *work) {
+    if (a.nq <= 0) return;
+    const int hd = a.d / a.heads;
+    if (a.d % a.heads != 0 || hd > 64 || a.rows <= 0 || a.chunk <= 0)
+        throw ArgError{"attention: head width must divide d and be at most 64, rows and chunk positive"};
+    if ((size_t)a.nq > (size_t)65535 * 8) throw ArgError{"attention: too many queries for one launch"};
+    const AttnPlan p = plan(a);
+    float *part_o = nullptr, *part_ml = nullptr;
+    if (p.splits > 1) {
+        part_o = static_cast<float *>(work);
+        part_ml = part_o + (size_t)p.splits * a.nq * a.heads * hd;
+    }
+    switch (a.kv_format) {
+        case TAH_KV_F32: launch<TAH_KV_F32>(s, a, p, q, records, out, part_o, part_ml); break;
+        case TAH_KV_I16: launch<TAH_KV_I16>(s, a, p, q, records, out, part_o, part_ml); break;
+        case TAH_KV_I8: launch<TAH_KV_I8>(s, a, p, q, records, out, part_o, part_ml); break;
+        default: throw ArgError{"attention: unknown key/value format"};
+    }
+    if (p.splits > 1) {
+        hipLaunchKernelGGL(k_attn_merge, dim3(a.nq * a.heads), dim3(64), 0, s, a.nq, a.d, a.heads, p.splits, part_o,
+                           part_ml, out);
+        TAH_LAUNCHED();
+    }
+}
+
+}  // namespace tah

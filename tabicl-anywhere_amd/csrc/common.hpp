@@ -1,0 +1,121 @@
+// Internal declarations shared by the HIP sources of libtah_hip.so: the device handle, the weights and fitted
+// model as they sit on the card, working memory, and the kernel launchers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/tah.h"
+
+namespace tah {
+
+// A HIP failure inside a call: carries the message reported through tah_last_error ("graphics card: ...").
+struct DeviceError {
+    std::string msg;
+};
+struct ArgError {
+    std::string msg;
+};
+struct BudgetError {
+    std::string msg;
+};
+
+#define TAH_HIP(expr)                                                                                     \
+    do {                                                                                                  \
+        hipError_t e_ = (expr);                                                                           \
+        if (e_ != hipSuccess)                                                                             \
+            throw ::tah::DeviceError{std::string("graphics card: ") + #expr + ": " + hipGetErrorString(e_)}; \
+    } while (0)
+
+// Kernel launches: the launch itself and any error it left.
+#define TAH_LAUNCHED() TAH_HIP(hipGetLastError())
+
+// ---- working memory ----------------------------------------------------------------------------------------
+// Buffers a call borrows: kept between calls (allocating and freeing a few hundred MB per call costs more than
+// a small prediction), never more in existence than the device's work budget.
+struct Pool {
+    struct Buf {
+        void *p;
+        size_t bytes;
+        bool busy;
+    };
+    std::vector<Buf> bufs;
+    size_t budget = size_t(1536) << 20;
+    size_t bytes = 0, peak = 0, overdrawn = 0;
+
+    void *take(size_t bytes, int device);
+    void give(void *p);
+    void release_idle();
+};
+
+}  // namespace tah
+
+// One GPU.
+struct tah_dev {
+    int ordinal = 0;
+    hipStream_t stream = nullptr;
+    std::mutex lock;
+    std::string last_error;
+    std::string name;
+    tah::Pool pool;
+};
+
+// A block's tensors on the card (device pointers; nullptr where absent).
+struct DevBlock {
+    int d, heads, ff, ss_hidden;
+    const float *n1w, *n1b, *n2w, *n2b, *in_w, *in_b, *out_w, *out_b, *l1w, *l1b, *l2w, *l2b;
+    const float *b0w, *b0b, *b2w, *b2b, *q0w, *q0b, *q2w, *q2b;
+};
+
+struct tah_weights {
+    tah_dev *dev;
+    int ordinal;
+    void *arena = nullptr;
+    size_t bytes = 0;
+    int e, d, group, inds, cls, max_classes, col_heads, row_heads, icl_heads;
+    int col_blocks, row_blocks, icl_layers, dec_hidden, outputs, rope_half;
+    std::vector<DevBlock> col_a1, col_a2, row, icl;
+    const float *in_w, *in_b, *col_ind, *col_y, *cls_tokens, *rope_freqs, *out_lnw, *out_lnb;
+    const float *icl_y, *lnw, *lnb, *dec0w, *dec0b, *dec2w, *dec2b;
+};
+
+struct tah_model {
+    tah_dev *dev;
+    int ordinal;
+    int kv_format, rows, chunk, d, layers, heads;
+    size_t layer_bytes;
+    uint8_t *records = nullptr;  // layers x layer_bytes, the stored chunk records as they are
+    float *scales = nullptr;     // [layers][d]
+    size_t bytes = 0;
+};
+
+namespace tah {
+
+enum Epi { EPI_NONE = 0, EPI_GELU = 1, EPI_RESID = 2 };
+
+// Y[M][N] (leading dim ldy) = epi(X[M][K] (ldx) * W[N][K]^T + b[N]); EPI_RESID adds R (ldr, may alias Y).
+void gemm(hipStream_t s, int M, int N, int K, const float *X, int ldx, const float *W, const float *b, float *Y,
+          int ldy, Epi epi, const float *R, int ldr);
+
+// y[r] = layer_norm(x[r]) * w + b over rows of n numbers (eps 1e-5, biased variance).
+void layer_norm(hipStream_t s, int rows, int n, const float *x, int ldx, const float *w, const float *b, float *y,
+                int ldy);
+
+// In place on q [rows][d] (after the query projection): q *= scale (no scalable softmax), or per head
+// q_h *= scale_h * (1 + tanh(q2 gelu(q0 q_h + q0b) + q2b)).
+void query_modulate(hipStream_t s, int rows, const DevBlock &b, const float *scale, float *q);
+
+// The attention of nq queries q [nq][d] (scaled) over one stored in-context layer (chunk records on the card):
+// out [nq][d], normalised. work must hold attention_work_bytes(...).
+struct AttnShape {
+    int nq, rows, chunk, d, heads, kv_format;
+};
+size_t attention_work_bytes(const AttnShape &a);
+void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t *records, float *out, void *work);
+
+}  // namespace tah

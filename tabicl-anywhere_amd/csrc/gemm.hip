@@ -1,0 +1,144 @@
+// Dense layers of every block: Y = epi(X W^T + b), W [out][in] as PyTorch stores it.
+//
+// The main kernel is an fp32 MFMA GEMM for CDNA4 (v_mfma_f32_16x16x4_f32): a 256-thread workgroup computes a
+// 64 x 64 tile of Y as 2 x 2 wavefronts of 32 x 32 (2 x 2 MFMA tiles of 16 x 16 each), staging 64 x 16 slices of X
+// and W through LDS. Both operands are K-contiguous, so each lane reads four consecutive K values with one
+// 128-bit LDS load and feeds them to four MFMA steps: step t gives lane l the K index 4*(l/16) + t, the same
+// permutation on both operands, which leaves the sum unchanged. The epilogue fuses bias, GELU and the block's
+// residual add (src/nn.rs:156-164, src/predict.rs:542-568). Shapes whose K is not a multiple of 4 (the input
+// layer's 3 features) use a plain one-thread-per-output kernel.
+#include "common.hpp"
+#include "device_math.hpp"
+
+namespace tah {
+
+template <int EPI>
+__device__ __forceinline__ float epilogue(float acc, const float *b, int n, const float *R, int ldr, int m) {
+    float y = acc + (b ? b[n] : 0.0f);
+    if (EPI == EPI_GELU) y = gelu(y);
+    if (EPI == EPI_RESID) y += R[(size_t)m * ldr + n];
+    return y;
+}
+
+constexpr int GB = 64;   // tile rows and columns
+constexpr int GK = 16;   // K slice
+constexpr int GKP = 20;  // padded LDS row
+
+template <int EPI>
+__global__ __launch_bounds__(256) void k_gemm_mfma(int M, int N, int K, const float *__restrict__ X, int ldx,
+                                                    const float *__restrict__ W, const float *__restrict__ b,
+                                                    float *Y, int ldy, const float *R, int ldr) {
+    __shared__ float As[2][GB][GKP];
+    __shared__ float Bs[2][GB][GKP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * GB, n0 = blockIdx.x * GB;
+    const int lr = tid >> 2, lc = (tid & 3) * 4;
+    const int gm = m0 + lr, gn = n0 + lr;
+    floatx4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto load = [&](int k0, float4 &av, float4 &bv) {
+        const int gk = k0 + lc;
+        av = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        bv = av;
+        if (gk < K) {
+            if (gm < M) av = *reinterpret_cast<const float4 *>(X + (size_t)gm * ldx + gk);
+            if (gn < N) bv = *reinterpret_cast<const float4 *>(W + (size_t)gn * K + gk);
+        }
+    };
+    float4 av, bv;
+    load(0, av, bv);
+    int buf = 0;
+    *reinterpret_cast<float4 *>(&As[0][lr][lc]) = av;
+    *reinterpret_cast<float4 *>(&Bs[0][lr][lc]) = bv;
+    __syncthreads();
+    const int kq = (lane >> 4) * 4, r16 = lane & 15;
+    for (int k0 = 0; k0 < K; k0 += GK) {
+        const bool more = k0 + GK < K;
+        if (more) load(k0 + GK, av, bv);  // next slice in flight while this one is multiplied
+        const float4 a0 = *reinterpret_cast<const float4 *>(&As[buf][wm * 32 + r16][kq]);
+        const float4 a1 = *reinterpret_cast<const float4 *>(&As[buf][wm * 32 + 16 + r16][kq]);
+        const float4 b0 = *reinterpret_cast<const float4 *>(&Bs[buf][wn * 32 + r16][kq]);
+        const float4 b1 = *reinterpret_cast<const float4 *>(&Bs[buf][wn * 32 + 16 + r16][kq]);
+        acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0.x, b0.x, acc[0][0], 0, 0, 0);
+        acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0.x, b1.x, acc[0][1], 0, 0, 0);
+        acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1.x, b0.x, acc[1][0], 0, 0, 0);
+        acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1.x, b1.x, acc[1][1], 0, 0, 0);
+        acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0.y, b0.y, acc[0][0], 0, 0, 0);
+        acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0.y, b1.y, acc[0][1], 0, 0, 0);
+        acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1.y, b0.y, acc[1][0], 0, 0, 0);
+        acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1.y, b1.y, acc[1][1], 0, 0, 0);
+        acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0.z, b0.z, acc[0][0], 0, 0, 0);
+        acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0.z, b1.z, acc[0][1], 0, 0, 0);
+        acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1.z, b0.z, acc[1][0], 0, 0, 0);
+        acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1.z, b1.z, acc[1][1], 0, 0, 0);
+        acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0.w, b0.w, acc[0][0], 0, 0, 0);
+        acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0.w, b1.w, acc[0][1], 0, 0, 0);
+        acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1.w, b0.w, acc[1][0], 0, 0, 0);
+        acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1.w, b1.w, acc[1][1], 0, 0, 0);
+        if (more) {
+            *reinterpret_cast<float4 *>(&As[buf ^ 1][lr][lc]) = av;
+            *reinterpret_cast<float4 *>(&Bs[buf ^ 1][lr][lc]) = bv;
+        }
+        __syncthreads();
+        buf ^= 1;
+    }
+    // lane l holds D[4*(l/16) + v][l % 16] of each 16 x 16 tile
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int n = n0 + wn * 32 + j * 16 + r16;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int m = m0 + wm * 32 + i * 16 + kq + v;
+                if (m < M && n < N) Y[(size_t)m * ldy + n] = epilogue<EPI>(acc[i][j][v], b, n, R, ldr, m);
+            }
+        }
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256) void k_gemm_plain(int M, int N, int K, const float *__restrict__ X, int ldx,
+                                                     const float *__restrict__ W, const float *__restrict__ b,
+                                                     float *Y, int ldy, const float *R, int ldr) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)M * N) return;
+    const int m = (int)(i / N), n = (int)(i % N);
+    const float *xr = X + (size_t)m * ldx, *wr = W + (size_t)n * K;
+    float a = 0.0f;
+    for (int k = 0; k < K; k++) a += xr[k] * wr[k];
+    Y[(size_t)m * ldy + n] = epilogue<EPI>(a, b, n, R, ldr, m);
+}
+
+template <int EPI>
+static void launch(hipStream_t s, int M, int N, int K, const float *X, int ldx, const float *W, const float *b, float *Y,
+                   int ldy, const float *R, int ldr) {
+    const bool aligned = K % 4 == 0 && ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 &&
+                         (reinterpret_cast<uintptr_t>(W) & 15) == 0;
+    if (aligned) {
+        dim3 grid((N + GB - 1) / GB, (M + GB - 1) / GB);
+        hipLaunchKernelGGL(k_gemm_mfma<EPI>, grid, dim3(256), 0, s, M, N, K, X, ldx, W, b, Y, ldy, R, ldr);
+    } else {
+        const size_t n = (size_t)M * N;
+        hipLaunchKernelGGL(k_gemm_plain<EPI>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, M, N, K, X, ldx, W, b,
+                           Y, ldy, R, ldr);
+    }
+    TAH_LAUNCHED();
+}
+
+void gemm(hipStream_t s, int M, int N, int K, const float *X, int ldx, const float *W, const float *b, float *Y, int ldy,
+          Epi epi, const float *R, int ldr) {
+    if (M <= 0 || N <= 0) return;
+    if ((size_t)M > (size_t)65535 * GB) throw ArgError{"gemm: too many rows for one launch"};
+    switch (epi) {
+        case EPI_NONE: launch<EPI_NONE>(s, M, N, K, X, ldx, W, b, Y, ldy, R, ldr); break;
+        case EPI_GELU: launch<EPI_GELU>(s, M, N, K, X, ldx, W, b, Y, ldy, R, ldr); break;
+        case EPI_RESID: launch<EPI_RESID>(s, M, N, K, X, ldx, W, b, Y, ldy, R, ldr); break;
+    }
+}
+
+}  // namespace tah

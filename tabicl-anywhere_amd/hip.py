@@ -1,0 +1,215 @@
+"""The card handle over libtah_hip.so: the Python mirror of the reference's `gpu::Gpu` surface and its two plugin
+traits, as the `hip` feature would expose them.
+
+* `Gpu` mirrors `gpu::Gpu` (`src/gpu.rs:725-1019`): `new`, `name`, `set_work_budget`, `work_budget`, `working`,
+  `overdrawn`, `release`, `weights` (`GpuWeights::new`), `load` (`VramModel`, from the bundle's stored chunk records
+  as they are), `attend_resident` (`src/gpu.rs:2120-2134`) and `in_context` (`src/gpu.rs:2140`).
+* `CardAttend` implements `predict::AttendCached` (`src/predict.rs:63-79`): `attend` and `stage` return `None` when
+  the card does not hold the problem, and the caller streams on the CPU as usual.
+
+Errors are the reference's: `CardError` ("graphics card: ...", `io::ErrorKind::Other`), `BudgetError`
+(`io::ErrorKind::OutOfMemory`), `ValueError` for invalid arguments. Nothing here falls back to another
+implementation: without the built library every call raises `abi.LibraryMissing`.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import abi
+
+
+class CardError(RuntimeError):
+    """A failure on the card (the reference's `fail`, `src/gpu.rs:720-722`)."""
+
+
+class BudgetError(MemoryError):
+    """Over the working-memory budget (`io::ErrorKind::OutOfMemory`, `src/gpu.rs:887-889`)."""
+
+
+def _fp(a: np.ndarray):
+    return a.ctypes.data_as(abi.F32P)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class Gpu:
+    """One GPU: its stream, working-memory pool and last error."""
+
+    def __init__(self, ordinal: int = 0):
+        self._l = abi.lib()
+        h = ctypes.c_void_p()
+        rc = self._l.tah_open(int(ordinal), ctypes.byref(h))
+        if rc != abi.OK:
+            raise CardError(f"graphics card: none found at ordinal {ordinal} (status {rc})")
+        self._h = h
+        buf = ctypes.create_string_buffer(256)
+        self._l.tah_device_name(self._h, buf, 256)
+        self.name = buf.value.decode()
+        self.software = False
+
+    new = classmethod(lambda cls, ordinal=0: cls(ordinal))
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._l.tah_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc: int) -> None:
+        if rc == abi.OK:
+            return
+        msg = (self._l.tah_last_error(self._h) or b"").decode()
+        if rc == abi.E_BUDGET:
+            raise BudgetError(msg)
+        if rc == abi.E_ARG:
+            raise ValueError(msg)
+        if rc == abi.E_DECLINED:
+            raise LookupError(msg)
+        raise CardError(msg)
+
+    # ---- working memory (Gpu::set_work_budget .. release, src/gpu.rs:975-1019) --------------------------------
+    def set_work_budget(self, nbytes: int) -> None:
+        self._check(self._l.tah_set_work_budget(self._h, int(nbytes)))
+
+    def work_budget(self) -> int:
+        return int(self._l.tah_work_budget(self._h))
+
+    def working(self):
+        now, peak = ctypes.c_size_t(), ctypes.c_size_t()
+        self._check(self._l.tah_working(self._h, ctypes.byref(now), ctypes.byref(peak)))
+        return now.value, peak.value
+
+    def overdrawn(self) -> int:
+        return int(self._l.tah_overdrawn(self._h))
+
+    def release(self) -> None:
+        self._check(self._l.tah_release(self._h))
+
+    def sync(self) -> None:
+        self._check(self._l.tah_sync(self._h))
+
+    @property
+    def stream(self) -> int:
+        return int(self._l.tah_stream(self._h) or 0)
+
+    # ---- weights and fitted models -----------------------------------------------------------------------------
+    def weights(self, model) -> "GpuWeights":
+        return GpuWeights(self, model)
+
+    def load(self, weights: "GpuWeights", kv_format: int, rows: int, chunk: int, layers, scales) -> "VramModel":
+        return VramModel(self, weights, kv_format, rows, chunk, layers, scales)
+
+    def attend_resident(self, vm: "VramModel", layer: int, q) -> np.ndarray:
+        q = _f32(q)
+        nq = q.shape[0]
+        out = np.empty((nq, vm.d), np.float32)
+        self._check(self._l.tah_attend_resident(self._h, vm._h, int(layer), _fp(q), nq, _fp(out)))
+        return out
+
+    def in_context(self, weights: "GpuWeights", vm: "VramModel", h, out_n: int) -> np.ndarray:
+        """The whole in-context stage: row representations `h [n][d]` to the first `out_n` decoder outputs."""
+        h = _f32(h)
+        nq = h.shape[0]
+        out = np.empty((nq, out_n), np.float32)
+        self._check(self._l.tah_stage(self._h, weights._h, vm._h, _fp(h), nq, int(out_n), _fp(out)))
+        return out
+
+    # device-pointer forms: inputs already in HBM, work left queued on the handle's stream
+    def attend_resident_dev(self, vm: "VramModel", layer: int, q_ptr: int, nq: int, out_ptr: int) -> None:
+        self._check(self._l.tah_attend_resident_dev(self._h, vm._h, int(layer), ctypes.c_void_p(q_ptr), int(nq),
+                                                    ctypes.c_void_p(out_ptr)))
+
+    def in_context_dev(self, weights: "GpuWeights", vm: "VramModel", h_ptr: int, nq: int, out_n: int, out_ptr: int) -> None:
+        self._check(self._l.tah_stage_dev(self._h, weights._h, vm._h, ctypes.c_void_p(h_ptr), int(nq), int(out_n),
+                                          ctypes.c_void_p(out_ptr)))
+
+
+class GpuWeights:
+    """A model's weights on the card (`GpuWeights`, `src/gpu.rs:1838-2027`)."""
+
+    def __init__(self, gpu: Gpu, model):
+        self.gpu, self.model = gpu, model
+        h = ctypes.c_void_p()
+        gpu._check(gpu._l.tah_weights_upload(gpu._h, ctypes.byref(model.desc()), ctypes.byref(h)))
+        self._h = h
+
+    def bytes(self) -> int:
+        return int(self.gpu._l.tah_weights_bytes(self._h))
+
+    def free(self) -> None:
+        if getattr(self, "_h", None):
+            self.gpu._l.tah_weights_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class VramModel:
+    """One fitted in-context problem held on the card (`VramModel`, `src/gpu.rs:2033-2116`): every layer's stored
+    chunk records as they are in the bundle (`n{j}_kv{l}`), and the layers' query scales (`n{j}_scale`)."""
+
+    def __init__(self, gpu: Gpu, weights: GpuWeights, kv_format: int, rows: int, chunk: int, layers, scales):
+        self.gpu, self.weights = gpu, weights
+        self.kv_format, self.rows, self.chunk = int(kv_format), int(rows), int(chunk)
+        self.d = weights.model.d
+        want = abi.layer_bytes(self.kv_format, self.rows, self.chunk, self.d)
+        bufs = [np.ascontiguousarray(l, dtype=np.uint8).reshape(-1) for l in layers]
+        if len(bufs) != weights.model.icl_layers or any(b.nbytes != want for b in bufs):
+            raise ValueError(f"model: expected {weights.model.icl_layers} layers of {want} bytes")
+        ptrs = (abi.U8P * len(bufs))(*[b.ctypes.data_as(abi.U8P) for b in bufs])
+        scales = _f32(scales)
+        h = ctypes.c_void_p()
+        gpu._check(gpu._l.tah_model_load(gpu._h, weights._h, self.kv_format, self.rows, self.chunk, ptrs, _fp(scales),
+                                         ctypes.byref(h)))
+        self._h = h
+
+    @staticmethod
+    def model_bytes(kv_format: int, rows: int, chunk: int, d: int, layers: int) -> int:
+        return int(abi.lib().tah_model_bytes(kv_format, rows, chunk, d, layers))
+
+    def free(self) -> None:
+        if getattr(self, "_h", None):
+            self.gpu._l.tah_model_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class CardAttend:
+    """`predict::AttendCached` over problems held on the card, keyed by `(prefix, node)`."""
+
+    def __init__(self, gpu: Gpu, weights: GpuWeights):
+        self.gpu, self.weights = gpu, weights
+        self.models: dict = {}
+
+    def hold(self, prefix: str, node: int, vm: VramModel) -> None:
+        self.models[(prefix, node)] = vm
+
+    def attend(self, prefix: str, node: int, layer: int, q, d: int, heads: int):
+        vm = self.models.get((prefix, node))
+        if vm is None or d != vm.d:
+            return None
+        return self.gpu.attend_resident(vm, layer, q)
+
+    def stage(self, prefix: str, node: int, h, d: int, out_n: int):
+        vm = self.models.get((prefix, node))
+        if vm is None or d != vm.d:
+            return None
+        return self.gpu.in_context(self.weights, vm, h, out_n)

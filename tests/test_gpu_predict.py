@@ -1,0 +1,129 @@
+"""Prediction on the card against the oracle: the in-context attention over stored layers in all three formats,
+and the whole in-context stage, at the tiny model (against the reference's golden logits too) and at the full-size
+TabICL v2 architecture. Tolerances are the stated ones: attention outputs and raw scores within 5e-5."""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as orc
+from conftest import pkg
+
+abi, hip, M = pkg("abi"), pkg("hip"), pkg("model")
+pytestmark = pytest.mark.gpu
+
+SCORE_TOL = 5e-5
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    g = hip.Gpu(0)
+    say("device:", g.name)
+    yield g
+    g.close()
+
+
+@pytest.fixture(scope="module")
+def full_model():
+    return M.Model.random(M.FULL_CLASSIFIER, seed=2)
+
+
+@pytest.fixture(scope="module")
+def full_weights(gpu, full_model):
+    return gpu.weights(full_model)
+
+
+def random_layers(rng, layers, rows, chunk, d, kv_format, scale=1.0):
+    """Stored layers of random keys and values (normal, scaled), packed by the oracle's quantiser."""
+    out = []
+    for _ in range(layers):
+        parts = []
+        for c0 in range(0, rows, chunk):
+            rc = min(chunk, rows - c0)
+            c = (rng.standard_normal(2 * d * rc) * scale).astype(np.float32)
+            parts.append(orc.pack(c, d, rc, kv_format))
+        out.append(np.concatenate(parts))
+    return out
+
+
+@pytest.mark.parametrize("kv_format", [abi.KV_F32, abi.KV_I16, abi.KV_I8])
+@pytest.mark.parametrize("rows,chunk", [(10000, 256), (1000, 48), (37, 8)])
+@pytest.mark.parametrize("nq", [1, 7, 64, 130])
+def test_attention_full_width(gpu, full_model, full_weights, kv_format, rows, chunk, nq):
+    """AttendCached::attend at d = 512, 8 heads of 64: decode path below 64 queries, MFMA path above."""
+    say(f"attention d=512 fmt={kv_format} rows={rows} chunk={chunk} nq={nq}")
+    rng = np.random.default_rng(rows * 7 + nq + kv_format)
+    d, L = full_model.d, full_model.icl_layers
+    layers = random_layers(rng, 1, rows, chunk, d, kv_format, scale=0.5) * L
+    scales = np.ones((L, d), np.float32)
+    vm = gpu.load(full_weights, kv_format, rows, chunk, layers, scales)
+    q = (rng.standard_normal((nq, d)) * 0.3).astype(np.float32)
+    got = gpu.attend_resident(vm, 3, q)
+    want = orc.attend_records(q, layers[0], kv_format, rows, chunk, d, full_model.icl_heads)
+    vm.free()
+    err = np.abs(got - want).max()
+    say("  worst", err)
+    assert err < SCORE_TOL
+
+
+@pytest.mark.parametrize("kv_format", [abi.KV_F32, abi.KV_I16, abi.KV_I8])
+def test_attention_tiny_width(gpu, tiny_model, kv_format):
+    """Head width 8 (the tiny model): the decode kernel at any query count."""
+    say(f"attention tiny fmt={kv_format}")
+    w = gpu.weights(tiny_model)
+    rng = np.random.default_rng(kv_format)
+    d, L = tiny_model.d, tiny_model.icl_layers
+    for rows, chunk, nq in ((120, 48, 16), (300, 64, 70), (5, 8, 1)):
+        layers = random_layers(rng, L, rows, chunk, d, kv_format)
+        vm = gpu.load(w, kv_format, rows, chunk, layers, np.ones((L, d), np.float32))
+        q = rng.standard_normal((nq, d)).astype(np.float32)
+        got = gpu.attend_resident(vm, 1, q)
+        want = orc.attend_records(q, layers[1], kv_format, rows, chunk, d, tiny_model.icl_heads)
+        vm.free()
+        assert np.abs(got - want).max() < SCORE_TOL, (rows, chunk, nq)
+
+
+def test_stage_tiny_matches_oracle_and_reference(gpu, tiny_model, tiny_raw):
+    """AttendCached::stage on the tiny model fitted by the oracle: the raw scores agree with the oracle's and
+    with the reference's golden logits (tests/reference.rs:141-148, at TINY = 5e-5)."""
+    say("stage tiny golden")
+    x = tiny_raw.f32s("x_train").reshape(120, 7)
+    y = tiny_raw.i32s("y_train").astype(np.float32)
+    fit = orc.fit_raw(tiny_model, x, y, 3, chunk=48)
+    rep = orc.represent(tiny_model, orc.embed(tiny_model, fit, tiny_raw.f32s("x_test").reshape(16, 7)))
+    w = gpu.weights(tiny_model)
+    vm = gpu.load(w, abi.KV_F32, 120, 48, fit.layers[0], fit.scales[0])
+    got = gpu.in_context(w, vm, rep, 3)
+    want = orc.in_context(tiny_model, fit.scales[0], fit.layers[0], abi.KV_F32, 120, 48, rep, 3)
+    assert np.abs(got - want).max() < SCORE_TOL
+    assert np.abs(got - tiny_raw.f32s("logits").reshape(16, 3)).max() < SCORE_TOL
+    # through the plugin trait
+    card = hip.CardAttend(gpu, w)
+    assert card.stage("", 0, rep, tiny_model.d, 3) is None  # not held: the CPU streams instead
+    card.hold("", 0, vm)
+    assert np.array_equal(card.stage("", 0, rep, tiny_model.d, 3), got)
+
+
+@pytest.mark.parametrize("kv_format", [abi.KV_F32, abi.KV_I16, abi.KV_I8])
+@pytest.mark.parametrize("nq", [1, 64, 200])
+def test_stage_full_size(gpu, full_model, full_weights, kv_format, nq):
+    """The whole in-context stage (12 layers of 8 x 64 heads, d = 512, then the decoder) over a stored cache of
+    2,000 rows, against the oracle on the same inputs."""
+    say(f"stage full fmt={kv_format} nq={nq}")
+    rng = np.random.default_rng(100 + nq + kv_format)
+    d, L, rows, chunk = full_model.d, full_model.icl_layers, 2000, 256
+    layers = random_layers(rng, L, rows, chunk, d, kv_format)
+    scales = np.stack([orc.query_scale(b, rows) for b in full_model.icl])
+    vm = gpu.load(full_weights, kv_format, rows, chunk, layers, scales)
+    h = rng.standard_normal((nq, d)).astype(np.float32)
+    got = gpu.in_context(full_weights, vm, h, 10)
+    want = orc.in_context(full_model, scales, layers, kv_format, rows, chunk, h, 10)
+    vm.free()
+    err = np.abs(got - want).max()
+    say("  worst", err, "scale", np.abs(want).max())
+    assert err < SCORE_TOL * max(1.0, np.abs(want).max())
