@@ -13,9 +13,10 @@
 //    (64 coordinates x 64 keys). Scores are formed transposed, S^T = K Q^T, with v_mfma_f32_16x16x4_f32 so that
 //    each lane owns one query (lane % 16) in both products; the softmax then needs only two cross-lane steps, and
 //    O^T = V^T P^T takes each lane's own weights as its B operand with no transpose through LDS.
-//  * k_attn_decode: any head width up to 64 and few queries: one wavefront per (key range, head, 8 queries),
-//    lane = key for the scores and lane = coordinate for the weighted sum. Bandwidth-bound, as single-row
-//    prediction is.
+//  * k_attn_decode64: head width 64 and few queries: 256 threads per (key range, head, 8 queries), K/V tiles
+//    loaded with 128-bit loads, lane = key for the scores and lane = coordinate for the weighted sum.
+//    Bandwidth-bound, as single-row prediction is.
+//  * k_attn_decode: any other head width up to 64 (the tiny test models): the same with one wavefront.
 #include <algorithm>
 
 #include "common.hpp"
@@ -316,24 +317,110 @@ __global__ __launch_bounds__(64) void k_attn_decode(int nq, int rows, int chunk,
     }
 }
 
+// ---- decode kernel for head width 64: few queries, bandwidth-bound ------------------------------------------
+// grid (splits, heads, query groups of QG); 256 threads. The K and V tiles of each key block are loaded with the
+// same 128-bit loads as the MFMA kernel (every thread has 32 keys' worth of loads in flight); wavefront w then
+// owns queries w and w + 4 of the group: lane = key for the scores and the softmax, lane = coordinate for the
+// weighted values.
+template <int FMT>
+__global__ __launch_bounds__(256) void k_attn_decode64(int nq, int rows, int chunk, int d, int heads,
+                                                        const float *__restrict__ q, const uint8_t *__restrict__ records,
+                                                        int kb_per_split, float *__restrict__ part_o,
+                                                        float *__restrict__ part_ml, float *__restrict__ out) {
+    __shared__ float Ks[64][KP];       // [coordinate][key]
+    __shared__ float Vt[KB][KB + 1];   // [key][coordinate]
+    __shared__ float Qs[QG][64];
+    __shared__ float Ps[QG][KB];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int split = blockIdx.x, h = blockIdx.y, q0 = blockIdx.z * QG;
+    const int splits = gridDim.x;
+    const KeyBlocks kbs = key_blocks(rows, chunk);
+    const int kb0 = split * kb_per_split, kb1 = min(kbs.n_kb, kb0 + kb_per_split);
+    for (int i = tid; i < QG * 64; i += 256) {
+        const int qi = i >> 6, c = i & 63;
+        Qs[qi][c] = q0 + qi < nq ? q[(size_t)(q0 + qi) * d + h * 64 + c] : 0.0f;
+    }
+    const int qa = wave, qb = wave + 4;  // this wavefront's two queries
+    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f}, o[2] = {0.0f, 0.0f};
+    const int lc = tid >> 2, seg = (tid & 3) * 16;
+    const int width = FMT == TAH_KV_F32 ? 4 : (FMT == TAH_KV_I16 ? 2 : 1);
+    for (int kb = kb0; kb < kb1; kb++) {
+        const Where w = locate(kbs, kb, records, FMT, d, chunk);
+        const bool fast = w.nk == KB && ((size_t)w.rc * width) % 16 == 0;
+        float tk[16], tv[16];
+        load16<FMT>(w.rec, d, w.rc, h * 64 + lc, w.o + seg, w.nk - seg, fast, tk);
+        load16<FMT>(w.rec, d, w.rc, d + h * 64 + lc, w.o + seg, w.nk - seg, fast, tv);
+        __syncthreads();  // the previous block's tiles are no longer read
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) *reinterpret_cast<float4 *>(&Ks[lc][seg + i]) = make_float4(tk[i], tk[i + 1], tk[i + 2], tk[i + 3]);
+#pragma unroll
+        for (int i = 0; i < 16; i++) Vt[seg + i][lc] = tv[i];
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int qi = j ? qb : qa;
+            float sc = 0.0f;
+#pragma unroll 16
+            for (int c = 0; c < 64; c++) sc += Qs[qi][c] * Ks[c][lane];
+            if (lane >= w.nk) sc = -INFINITY;
+            const float mnew = fmaxf(m[j], wave_max(sc));
+            const float alpha = fast_exp(m[j] - mnew);
+            const float p = lane < w.nk ? fast_exp(sc - mnew) : 0.0f;
+            l[j] = l[j] * alpha + wave_sum(p);
+            m[j] = mnew;
+            o[j] *= alpha;
+            Ps[qi][lane] = p;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int qi = j ? qb : qa;
+            float a = 0.0f;
+#pragma unroll 16
+            for (int k = 0; k < KB; k++) a += Ps[qi][k] * Vt[k][lane];
+            o[j] += a;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int qr = q0 + (j ? qb : qa);
+        if (qr >= nq) continue;
+        if (splits == 1) {
+            out[(size_t)qr * d + h * 64 + lane] = o[j] / l[j];
+        } else {
+            const size_t at = ((size_t)split * nq + qr) * heads + h;
+            part_o[at * 64 + lane] = o[j];
+            if (lane == 0) {
+                part_ml[at * 2] = m[j];
+                part_ml[at * 2 + 1] = l[j];
+            }
+        }
+    }
+}
+
 // ---- split merge: Soft::merge then Soft::finish ---------------------------------------------------------------
-// grid nq * heads; 64 threads (lane = coordinate).
+// grid nq * heads; 64 threads. The largest running maximum first (lanes over splits), then one pass over the
+// splits accumulating each one's weight sum and weighted values rescaled to it; loads are independent across
+// splits, so they stream.
 __global__ __launch_bounds__(64) void k_attn_merge(int nq, int d, int heads, int splits, const float *__restrict__ part_o,
                                                     const float *__restrict__ part_ml, float *__restrict__ out) {
     const int item = blockIdx.x, lane = threadIdx.x;
     const int qr = item / heads, h = item % heads, hd = d / heads;
+    const size_t stride = (size_t)nq * heads;  // between splits, in (query, head) items
+    const size_t base = (size_t)qr * heads + h;
     float M = -INFINITY;
-    for (int s = 0; s < splits; s++) {
-        const size_t at = ((size_t)s * nq + qr) * heads + h;
+    for (int s = lane; s < splits; s += 64) {
+        const size_t at = s * stride + base;
         if (part_ml[at * 2 + 1] > 0.0f) M = fmaxf(M, part_ml[at * 2]);
     }
+    M = wave_max(M);
     for (int c = lane; c < hd; c += 64) {
         float L = 0.0f, O = 0.0f;
+#pragma unroll 8
         for (int s = 0; s < splits; s++) {
-            const size_t at = ((size_t)s * nq + qr) * heads + h;
+            const size_t at = s * stride + base;
             const float ls = part_ml[at * 2 + 1];
-            if (ls <= 0.0f) continue;
-            const float f = fast_exp(part_ml[at * 2] - M);
+            const float f = ls > 0.0f ? fast_exp(part_ml[at * 2] - M) : 0.0f;
             L += ls * f;
             O += part_o[at * hd + c] * f;
         }
@@ -375,6 +462,9 @@ static void launch(hipStream_t s, const AttnShape &a, const AttnPlan &p, const f
     if (p.mfma) {
         hipLaunchKernelGGL(k_attn_mfma64<FMT>, dim3(p.groups, a.heads, p.splits), dim3(256), 0, s, a.nq, a.rows, a.chunk,
                            a.d, a.heads, q, records, p.kb_per_split, part_o, part_ml, out);
+    } else if (a.d / a.heads == 64) {
+        hipLaunchKernelGGL(k_attn_decode64<FMT>, dim3(p.splits, a.heads, p.groups), dim3(256), 0, s, a.nq, a.rows,
+                           a.chunk, a.d, a.heads, q, records, p.kb_per_split, part_o, part_ml, out);
     } else {
         hipLaunchKernelGGL(k_attn_decode<FMT>, dim3(p.splits, a.heads, p.groups), dim3(64), 0, s, a.nq, a.rows, a.chunk,
                            a.d, a.heads, q, records, p.kb_per_split, part_o, part_ml, out);

@@ -101,6 +101,45 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(int M, int N, int K, const fl
         }
 }
 
+// Few rows (single-row and small-batch prediction): a workgroup computes one 16 x 16 tile of Y and its four
+// wavefronts split K between them, loading MFMA operands straight from global memory (each weight row is read
+// once per tile, coalesced in 64-byte runs); the four partial tiles are summed through LDS before the epilogue.
+// Many more workgroups than the 64 x 64 kernel has at small M, so the weights stream at a useful rate.
+template <int EPI>
+__global__ __launch_bounds__(256) void k_gemm_skinny(int M, int N, int K, const float *__restrict__ X, int ldx,
+                                                      const float *__restrict__ W, const float *__restrict__ b,
+                                                      float *Y, int ldy, const float *R, int ldr) {
+    __shared__ float red[4][16][17];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int m0 = blockIdx.y * 16, n0 = blockIdx.x * 16;
+    const int r16 = lane & 15, g4 = lane >> 4;
+    const int gm = m0 + r16, gn = n0 + r16;
+    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const float *xr = X + (size_t)gm * ldx, *wr = W + (size_t)gn * K;
+#pragma unroll 4
+    for (int k0 = 16 * wave; k0 < K; k0 += 64) {
+        const int gk = k0 + 4 * g4;
+        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), bb = a;
+        if (gk < K) {
+            if (gm < M) a = *reinterpret_cast<const float4 *>(xr + gk);
+            if (gn < N) bb = *reinterpret_cast<const float4 *>(wr + gk);
+        }
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, bb.x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, bb.y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, bb.z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, bb.w, acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; v++) red[wave][4 * g4 + v][r16] = acc[v];
+    __syncthreads();
+    const int i = tid >> 4, j = tid & 15;
+    const int m = m0 + i, n = n0 + j;
+    if (m < M && n < N) {
+        const float a = (red[0][i][j] + red[1][i][j]) + (red[2][i][j] + red[3][i][j]);
+        Y[(size_t)m * ldy + n] = epilogue<EPI>(a, b, n, R, ldr, m);
+    }
+}
+
 template <int EPI>
 __global__ __launch_bounds__(256) void k_gemm_plain(int M, int N, int K, const float *__restrict__ X, int ldx,
                                                      const float *__restrict__ W, const float *__restrict__ b,
@@ -119,7 +158,10 @@ static void launch(hipStream_t s, int M, int N, int K, const float *X, int ldx, 
                    int ldy, const float *R, int ldr) {
     const bool aligned = K % 4 == 0 && ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 &&
                          (reinterpret_cast<uintptr_t>(W) & 15) == 0;
-    if (aligned) {
+    if (aligned && M <= 256) {
+        dim3 grid((N + 15) / 16, (M + 15) / 16);
+        hipLaunchKernelGGL(k_gemm_skinny<EPI>, grid, dim3(256), 0, s, M, N, K, X, ldx, W, b, Y, ldy, R, ldr);
+    } else if (aligned) {
         dim3 grid((N + GB - 1) / GB, (M + GB - 1) / GB);
         hipLaunchKernelGGL(k_gemm_mfma<EPI>, grid, dim3(256), 0, s, M, N, K, X, ldx, W, b, Y, ldy, R, ldr);
     } else {
