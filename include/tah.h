@@ -41,7 +41,8 @@ enum {
     TAH_E_ARG = 1,      /* invalid argument (io::ErrorKind::InvalidInput) */
     TAH_E_BUDGET = 2,   /* over the working-memory budget (io::ErrorKind::OutOfMemory) */
     TAH_E_DEVICE = 3,   /* HIP runtime error; answer on the CPU */
-    TAH_E_DECLINED = 4  /* not offered for this shape; nothing was done */
+    TAH_E_DECLINED = 4, /* not offered for this shape; nothing was done */
+    TAH_E_SINK = 5      /* the caller's layer sink returned non-zero; the fit stopped there */
 };
 
 /* Stored formats of in-context keys and values: the reference's Kv codes (src/fit.rs:102-127, Kv::from_code). */
@@ -136,6 +137,31 @@ int tah_stage(tah_dev *dev, const tah_weights *w, const tah_model *model, const 
               int32_t out_n, float *out);
 int tah_stage_dev(tah_dev *dev, const tah_weights *w, const tah_model *model, const float *h_dev, int32_t nq,
                   int32_t out_n, float *out_dev);
+
+/* ---- fitting: the fit::Attend hooks (src/fit.rs:45-74) ---------------------------------------------------------
+ *
+ * tah_pack: one stored chunk from its f32 keys and values c ([2d][rc]: the d key rows then the d value rows) to the
+ * record of format kv_format, quantised on the card exactly as the reference's pack (src/fit.rs:549-576). */
+int tah_pack(tah_dev *dev, const float *c, int32_t d, int32_t rc, int32_t kv_format, uint8_t *out);
+
+/* Attend::attend (src/fit.rs:46, Gpu src/gpu.rs:1471-1510): every training row's attention over all training rows
+ * of one layer. q [rows][d] (already scaled), kv the layer's exact f32 keys and values in chunk layout
+ * (2 * rows * d floats), out [rows][d] before the output projection. */
+int tah_attend(tah_dev *dev, const float *q, const float *kv, int32_t rows, int32_t chunk, int32_t d, int32_t heads,
+               float *out);
+
+/* Receives layer `layer`'s stored records (tah_kv_record summed over its chunks, in host memory valid for the
+ * duration of the call) while the in-context stage is fitted; non-zero stops the fit with TAH_E_SINK. */
+typedef int (*tah_layer_sink)(void *ctx, int32_t layer, const uint8_t *records, size_t bytes);
+
+/* Attend::in_context (src/fit.rs:67-73, Gpu src/gpu.rs:1650-1714): the whole in-context stage of one problem at
+ * fit time. h [rows][d] is the row representations with the target's embedding added, scales [layers][d] what each
+ * layer multiplies its queries by (Block::query_scale(rows)). Per layer, in order: keys and values of every row
+ * (layer norm, projection), stored as chunk records of `chunk` rows in kv_format and handed to sink; then (except
+ * after the last layer, whose outputs are never used, src/fit.rs:664-666) every row attends to all rows over the
+ * exact f32 keys and values, and the output projection and feed-forward update h. */
+int tah_in_context(tah_dev *dev, const tah_weights *w, const float *h, int32_t rows, const float *scales,
+                   int32_t kv_format, int32_t chunk, tah_layer_sink sink, void *ctx);
 
 #ifdef __cplusplus
 }

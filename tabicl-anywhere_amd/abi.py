@@ -11,7 +11,7 @@ import os
 F32P = ctypes.POINTER(ctypes.c_float)
 U8P = ctypes.POINTER(ctypes.c_uint8)
 
-OK, E_ARG, E_BUDGET, E_DEVICE, E_DECLINED = 0, 1, 2, 3, 4
+OK, E_ARG, E_BUDGET, E_DEVICE, E_DECLINED, E_SINK = 0, 1, 2, 3, 4, 5
 KV_F32, KV_I16, KV_I8 = 0, 1, 2
 KV_NAMES = {"f32": KV_F32, "i16": KV_I16, "i8": KV_I8}
 
@@ -34,6 +34,10 @@ class ModelDesc(ctypes.Structure):
         ("rope_freqs", F32P), ("out_lnw", F32P), ("out_lnb", F32P), ("icl", ctypes.POINTER(Block)),
         ("icl_y", F32P), ("lnw", F32P), ("lnb", F32P), ("dec0w", F32P), ("dec0b", F32P), ("dec2w", F32P),
         ("dec2b", F32P)]
+
+
+# int (*tah_layer_sink)(void *ctx, int32_t layer, const uint8_t *records, size_t bytes)
+LAYER_SINK = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_int32, U8P, ctypes.c_size_t)
 
 
 def kv_record(kv_format: int, d: int, rc: int) -> int:
@@ -93,6 +97,11 @@ SIGNATURES = {
                                  ctypes.c_int32, F32P]),
     "tah_stage_dev": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                      ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
+    "tah_pack": (ctypes.c_int, [ctypes.c_void_p, F32P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, U8P]),
+    "tah_attend": (ctypes.c_int, [ctypes.c_void_p, F32P, F32P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                  ctypes.c_int32, F32P]),
+    "tah_in_context": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, F32P, ctypes.c_int32, F32P, ctypes.c_int32,
+                                      ctypes.c_int32, LAYER_SINK, ctypes.c_void_p]),
 }
 
 

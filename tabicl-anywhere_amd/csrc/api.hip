@@ -75,6 +75,10 @@ struct Loans {
     }
 };
 
+struct SinkError {
+    int status;
+};
+
 template <class F>
 static int guarded(tah_dev *dev, F &&f) {
     if (!dev) return TAH_E_ARG;
@@ -92,6 +96,9 @@ static int guarded(tah_dev *dev, F &&f) {
     } catch (const BudgetError &e) {
         dev->last_error = e.msg;
         return TAH_E_BUDGET;
+    } catch (const SinkError &e) {
+        dev->last_error = "layer sink returned " + std::to_string(e.status);
+        return TAH_E_SINK;
     } catch (const std::bad_alloc &) {
         dev->last_error = "out of host memory";
         return TAH_E_BUDGET;
@@ -496,6 +503,108 @@ extern "C" int tah_stage(tah_dev *dev, const tah_weights *w, const tah_model *mo
         stage_rows(dev, w, model, hd, nq, out_n, od, loans);
         TAH_HIP(hipMemcpyAsync(out, od, sizeof(float) * nq * out_n, hipMemcpyDeviceToHost, dev->stream));
         TAH_HIP(hipStreamSynchronize(dev->stream));
+        return TAH_OK;
+    });
+}
+
+// ---- fitting ---------------------------------------------------------------------------------------------------
+extern "C" int tah_pack(tah_dev *dev, const float *c, int32_t d, int32_t rc, int32_t kv_format, uint8_t *out) {
+    if (!c || !out) return TAH_E_ARG;
+    return guarded(dev, [&] {
+        if (d <= 0 || rc <= 0 || kv_format < 0 || kv_format > 2) throw ArgError{"pack: bad size or format"};
+        Loans loans(dev);
+        const size_t n = 2 * (size_t)d * rc, bytes = tah_kv_record(kv_format, d, rc);
+        float *cd = loans.take<float>(n);
+        uint8_t *od = loans.take<uint8_t>(bytes);
+        TAH_HIP(hipMemcpyAsync(cd, c, n * sizeof(float), hipMemcpyHostToDevice, dev->stream));
+        if (kv_format == TAH_KV_F32)
+            TAH_HIP(hipMemcpyAsync(od, cd, bytes, hipMemcpyDeviceToDevice, dev->stream));
+        else
+            pack(dev->stream, rc, d, rc, kv_format, cd, od);
+        TAH_HIP(hipMemcpyAsync(out, od, bytes, hipMemcpyDeviceToHost, dev->stream));
+        TAH_HIP(hipStreamSynchronize(dev->stream));
+        return TAH_OK;
+    });
+}
+
+extern "C" int tah_attend(tah_dev *dev, const float *q, const float *kv, int32_t rows, int32_t chunk, int32_t d,
+                          int32_t heads, float *out) {
+    if (!q || !kv || !out) return TAH_E_ARG;
+    return guarded(dev, [&] {
+        if (rows <= 0 || chunk <= 0 || d <= 0 || heads <= 0 || d % heads) throw ArgError{"attend: bad shape"};
+        Loans loans(dev);
+        const size_t n = (size_t)rows * d;
+        float *qd = loans.take<float>(n), *kvd = loans.take<float>(2 * n), *od = loans.take<float>(n);
+        const AttnShape a{rows, rows, chunk, d, heads, TAH_KV_F32};
+        void *work = loans.take<uint8_t>(attention_work_bytes(a));
+        TAH_HIP(hipMemcpyAsync(qd, q, n * sizeof(float), hipMemcpyHostToDevice, dev->stream));
+        TAH_HIP(hipMemcpyAsync(kvd, kv, 2 * n * sizeof(float), hipMemcpyHostToDevice, dev->stream));
+        attention(dev->stream, a, qd, reinterpret_cast<const uint8_t *>(kvd), od, work);
+        TAH_HIP(hipMemcpyAsync(out, od, n * sizeof(float), hipMemcpyDeviceToHost, dev->stream));
+        TAH_HIP(hipStreamSynchronize(dev->stream));
+        return TAH_OK;
+    });
+}
+
+// Pinned host staging for records on their way to the sink.
+struct Pinned {
+    void *p = nullptr;
+    ~Pinned() {
+        if (p) (void)hipHostFree(p);
+    }
+};
+
+extern "C" int tah_in_context(tah_dev *dev, const tah_weights *w, const float *h_host, int32_t rows, const float *scales,
+                              int32_t kv_format, int32_t chunk, tah_layer_sink sink, void *ctx) {
+    if (!w || !h_host || !scales || !sink) return TAH_E_ARG;
+    return guarded(dev, [&] {
+        if (rows <= 0 || chunk <= 0 || kv_format < 0 || kv_format > 2) throw ArgError{"in_context: bad rows, chunk or format"};
+        const int d = w->d, L = w->icl_layers;
+        int ff = 0;
+        for (auto &b : w->icl) ff = std::max(ff, b.ff);
+        const size_t n = (size_t)rows * d;
+        const size_t lbytes = layer_bytes(kv_format, rows, chunk, d);
+        hipStream_t s = dev->stream;
+        Loans loans(dev);
+        float *h = loans.take<float>(n), *t = loans.take<float>(n), *q = loans.take<float>(n);
+        float *att = loans.take<float>(n), *kv = loans.take<float>(2 * n), *rec32 = loans.take<float>(2 * n);
+        float *mid = loans.take<float>((size_t)rows * ff), *sc = loans.take<float>((size_t)L * d);
+        uint8_t *recq = kv_format == TAH_KV_F32 ? nullptr : loans.take<uint8_t>(lbytes);
+        const AttnShape a{rows, rows, chunk, d, w->icl_heads, TAH_KV_F32};
+        void *work = loans.take<uint8_t>(attention_work_bytes(a));
+        Pinned host;
+        TAH_HIP(hipHostMalloc(&host.p, lbytes, hipHostMallocDefault));
+        TAH_HIP(hipMemcpyAsync(h, h_host, n * sizeof(float), hipMemcpyHostToDevice, s));
+        TAH_HIP(hipMemcpyAsync(sc, scales, sizeof(float) * L * d, hipMemcpyHostToDevice, s));
+        for (int l = 0; l < L; l++) {
+            const DevBlock &b = w->icl[l];
+            // keys and values of every row, stored (src/fit.rs:627-663)
+            layer_norm(s, rows, d, h, d, b.n1w, b.n1b, t, d);
+            gemm(s, rows, 2 * d, d, t, d, b.in_w + (size_t)d * d, b.in_b + d, kv, 2 * d, EPI_NONE, nullptr, 0);
+            to_records(s, rows, d, chunk, kv, rec32);
+            const uint8_t *stored = reinterpret_cast<const uint8_t *>(rec32);
+            if (kv_format != TAH_KV_F32) {
+                pack(s, rows, d, chunk, kv_format, rec32, recq);
+                stored = recq;
+            }
+            TAH_HIP(hipMemcpyAsync(host.p, stored, lbytes, hipMemcpyDeviceToHost, s));
+            const bool last = l + 1 == L;
+            if (!last) {
+                // every row attends to all rows over the exact keys and values, then the rest of the block
+                // (src/fit.rs:667-744)
+                gemm(s, rows, d, d, t, d, b.in_w, b.in_b, q, d, EPI_NONE, nullptr, 0);
+                query_modulate(s, rows, b, sc + (size_t)l * d, q);
+                attention(s, a, q, reinterpret_cast<const uint8_t *>(rec32), att, work);
+                gemm(s, rows, d, d, att, d, b.out_w, b.out_b, h, d, EPI_RESID, h, d);
+                layer_norm(s, rows, d, h, d, b.n2w, b.n2b, t, d);
+                gemm(s, rows, b.ff, d, t, d, b.l1w, b.l1b, mid, b.ff, EPI_GELU, nullptr, 0);
+                gemm(s, rows, d, b.ff, mid, b.ff, b.l2w, b.l2b, h, d, EPI_RESID, h, d);
+            }
+            // the layer's records reached the host before the next layer's keys overwrite rec32
+            TAH_HIP(hipStreamSynchronize(s));
+            const int rc = sink(ctx, l, static_cast<const uint8_t *>(host.p), lbytes);
+            if (rc != 0) throw SinkError{rc};
+        }
         return TAH_OK;
     });
 }

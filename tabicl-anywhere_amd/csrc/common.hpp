@@ -116,6 +116,10 @@ struct AttnShape {
     int nq, rows, chunk, d, heads, kv_format;
 };
 size_t attention_work_bytes(const AttnShape &a);
+// Row-major keys and values kv [rows][2d] to f32 chunk records (2 * rows * d floats).
+void to_records(hipStream_t s, int rows, int d, int chunk, const float *kv, float *rec32);
+// f32 chunk records to i16/i8 records (the reference's quantiser, bit for bit).
+void pack(hipStream_t s, int rows, int d, int chunk, int fmt, const float *rec32, uint8_t *recq);
 void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t *records, float *out, void *work);
 
 }  // namespace tah

@@ -24,6 +24,10 @@ class CardError(RuntimeError):
     """A failure on the card (the reference's `fail`, `src/gpu.rs:720-722`)."""
 
 
+class SinkError(RuntimeError):
+    """The layer sink of a fit refused a layer."""
+
+
 class BudgetError(MemoryError):
     """Over the working-memory budget (`io::ErrorKind::OutOfMemory`, `src/gpu.rs:887-889`)."""
 
@@ -74,6 +78,8 @@ class Gpu:
             raise ValueError(msg)
         if rc == abi.E_DECLINED:
             raise LookupError(msg)
+        if rc == abi.E_SINK:
+            raise SinkError(msg)
         raise CardError(msg)
 
     # ---- working memory (Gpu::set_work_budget .. release, src/gpu.rs:975-1019) --------------------------------
@@ -122,6 +128,48 @@ class Gpu:
         out = np.empty((nq, out_n), np.float32)
         self._check(self._l.tah_stage(self._h, weights._h, vm._h, _fp(h), nq, int(out_n), _fp(out)))
         return out
+
+    # ---- fitting: fit::Attend (src/fit.rs:45-74) ---------------------------------------------------------------
+    def pack(self, c, d: int, rc: int, kv_format: int) -> np.ndarray:
+        """One stored chunk record from its f32 keys and values `c` ([2d][rc]), quantised on the card."""
+        c = _f32(c).reshape(-1)
+        if c.size != 2 * d * rc:
+            raise ValueError("pack: c must hold 2 * d * rc floats")
+        out = np.empty(abi.kv_record(kv_format, d, rc), np.uint8)
+        self._check(self._l.tah_pack(self._h, _fp(c), int(d), int(rc), int(kv_format), out.ctypes.data_as(abi.U8P)))
+        return out
+
+    def attend(self, q, kv, rows: int, chunk: int, d: int, heads: int) -> np.ndarray:
+        """`Attend::attend`: all rows' attention over the layer's exact f32 keys and values (chunk layout)."""
+        q, kv = _f32(q), _f32(kv).reshape(-1)
+        if q.size != rows * d or kv.size != 2 * rows * d:
+            raise ValueError("attend: q must be [rows][d] and kv 2 * rows * d floats")
+        out = np.empty((rows, d), np.float32)
+        self._check(self._l.tah_attend(self._h, _fp(q), _fp(kv), int(rows), int(chunk), int(d), int(heads), _fp(out)))
+        return out
+
+    def in_context_fit(self, weights: "GpuWeights", h, scales, kv_format: int, chunk: int, sink) -> bool:
+        """`Attend::in_context`: fits the in-context stage of one problem on the card. `sink(layer, records)` gets
+        each layer's stored records (a uint8 array, valid during the call) in order; returning a true value (or
+        raising) stops the fit. Returns True (the card always offers the stage here)."""
+        h, scales = _f32(h), _f32(scales)
+        rows = h.shape[0]
+        failure = []
+
+        def call(_ctx, layer, ptr, nbytes):
+            try:
+                view = np.ctypeslib.as_array(ptr, shape=(nbytes,))
+                return 1 if sink(int(layer), view) else 0
+            except BaseException as exc:  # surfaced after the call returns
+                failure.append(exc)
+                return 1
+
+        cb = abi.LAYER_SINK(call)
+        rc = self._l.tah_in_context(self._h, weights._h, _fp(h), rows, _fp(scales), int(kv_format), int(chunk), cb, None)
+        if failure:
+            raise failure[0]
+        self._check(rc)
+        return True
 
     # device-pointer forms: inputs already in HBM, work left queued on the handle's stream
     def attend_resident_dev(self, vm: "VramModel", layer: int, q_ptr: int, nq: int, out_ptr: int) -> None:
