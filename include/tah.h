@@ -138,6 +138,24 @@ int tah_stage(tah_dev *dev, const tah_weights *w, const tah_model *model, const 
 int tah_stage_dev(tah_dev *dev, const tah_weights *w, const tah_model *model, const float *h_dev, int32_t nq,
                   int32_t out_n, float *out_dev);
 
+/* ---- the column and row stages, and AttendCached::rows (src/predict.rs:74-78, Gpu::predict src/gpu.rs:2146) --
+ *
+ * tah_model_set_columns: gives the fitted member's column cache (col_kv, [features][digits][col_blocks][2][e][inds],
+ * src/fit.rs:6-7) to a model on the card, as VramModel holds it. */
+int tah_model_set_columns(tah_dev *dev, tah_model *model, const tah_weights *w, const float *col_kv, int32_t features,
+                          int32_t digits);
+/* The column stage at prediction (embed, src/predict.rs:282-353): x [n][features] (already normalised) to tokens
+ * [n][cls + features][e], class tokens first. */
+int tah_embed(tah_dev *dev, const tah_weights *w, const tah_model *model, const float *x, int32_t n, float *tok);
+/* The row stage (represent, src/predict.rs:356-372): tokens [n][tokens][e] to row representations [n][d]. */
+int tah_represent(tah_dev *dev, const tah_weights *w, const float *tok, int32_t n, int32_t tokens, float *rep);
+/* AttendCached::rows: all three stages, x [n][features] to the first out_n decoder outputs [n][out_n], for a member
+ * with one in-context problem. Rows are processed in sub-batches that fit the working-memory budget. */
+int tah_predict_rows(tah_dev *dev, const tah_weights *w, const tah_model *model, const float *x, int32_t n,
+                     int32_t out_n, float *out);
+int tah_predict_rows_dev(tah_dev *dev, const tah_weights *w, const tah_model *model, const float *x_dev, int32_t n,
+                         int32_t out_n, float *out_dev);
+
 /* ---- fitting: the fit::Attend hooks (src/fit.rs:45-74) ---------------------------------------------------------
  *
  * tah_pack: one stored chunk from its f32 keys and values c ([2d][rc]: the d key rows then the d value rows) to the

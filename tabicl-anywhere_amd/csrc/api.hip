@@ -304,6 +304,13 @@ extern "C" int tah_weights_upload(tah_dev *dev, const tah_model_desc *m, tah_wei
         pk.add(m->dec0b, m->dec_hidden, &w->dec0b);
         pk.add(m->dec2w, (size_t)m->outputs * m->dec_hidden, &w->dec2w);
         pk.add(m->dec2b, m->outputs, &w->dec2b);
+        std::vector<float> col_scale;
+        if (m->col_heads > 0 && m->e % m->col_heads == 0) {
+            col_scale.assign(m->e, 1.0f / sqrtf((float)(m->e / m->col_heads)));
+            pk.add(col_scale.data(), col_scale.size(), &w->col_scale);
+        } else {
+            w->col_scale = nullptr;
+        }
         w->icl.resize(m->icl_layers);
         for (int l = 0; l < m->icl_layers; l++) add_block(pk, m->icl[l], w->icl[l]);
         if (m->col_a2 && m->col_blocks > 0) {
@@ -394,6 +401,7 @@ extern "C" void tah_model_free(tah_model *m) {
     if (!m) return;
     (void)hipSetDevice(m->ordinal);
     if (m->records) (void)hipFree(m->records);
+    if (m->col_kv) (void)hipFree(m->col_kv);
     delete m;
 }
 
@@ -605,6 +613,171 @@ extern "C" int tah_in_context(tah_dev *dev, const tah_weights *w, const float *h
             const int rc = sink(ctx, l, static_cast<const uint8_t *>(host.p), lbytes);
             if (rc != 0) throw SinkError{rc};
         }
+        return TAH_OK;
+    });
+}
+
+// ---- the column and row stages, and whole prediction from feature rows ------------------------------------------
+extern "C" int tah_model_set_columns(tah_dev *dev, tah_model *model, const tah_weights *w, const float *col_kv,
+                                     int32_t features, int32_t digits) {
+    if (!model || !w || !col_kv) return TAH_E_ARG;
+    return guarded(dev, [&] {
+        if (features <= 0 || digits <= 0 || w->col_a2.empty()) throw ArgError{"columns: bad features or digits"};
+        const size_t n = (size_t)features * digits * w->col_blocks * 2 * w->e * w->inds;
+        if (model->col_kv) {
+            (void)hipFree(model->col_kv);
+            model->col_kv = nullptr;
+        }
+        TAH_HIP(hipMalloc(&model->col_kv, n * sizeof(float)));
+        TAH_HIP(hipMemcpy(model->col_kv, col_kv, n * sizeof(float), hipMemcpyHostToDevice));
+        model->features = features;
+        model->digits = digits;
+        model->bytes += align256(n * sizeof(float));
+        return TAH_OK;
+    });
+}
+
+// cos and sin of position * frequency for T positions ([T][half]), as Rope::new (src/nn.rs:304-321), on the card.
+static float *rope_tables(tah_dev *dev, const tah_weights *w, int T, Loans &loans) {
+    const int half = w->rope_half;
+    std::vector<float> freqs(half), tab(2 * (size_t)T * half);
+    TAH_HIP(hipMemcpy(freqs.data(), w->rope_freqs, sizeof(float) * half, hipMemcpyDeviceToHost));
+    for (int p = 0; p < T; p++)
+        for (int i = 0; i < half; i++) {
+            const float a = (float)p * freqs[i];
+            tab[(size_t)p * half + i] = cosf(a);
+            tab[(size_t)T * half + (size_t)p * half + i] = sinf(a);
+        }
+    float *d = loans.take<float>(tab.size());
+    TAH_HIP(hipMemcpyAsync(d, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice, dev->stream));
+    TAH_HIP(hipStreamSynchronize(dev->stream));  // tab is a local
+    return d;
+}
+
+static void check_columns(const tah_weights *w, const tah_model *model) {
+    if (!model->col_kv) throw ArgError{"the model holds no column cache (tah_model_set_columns)"};
+    if (w->col_a2.empty() || w->row.empty() || !w->col_scale) throw ArgError{"weights lack the column or row stage"};
+}
+
+// Device work for n rows x (on the card): tokens [n][T][e] after the column stage.
+static void embed_rows(tah_dev *dev, const tah_weights *w, const tah_model *model, const float *x, int n, float *tok,
+                       Loans &loans) {
+    const int features = model->features;
+    float *cells = loans.take<float>((size_t)n * features * w->e);
+    float *scratch = loans.take<float>(column_stage_floats(w, n, features, model->digits));
+    column_stage(dev->stream, w, model->col_kv, model->digits, x, n, features, cells, scratch);
+    assemble_tokens(dev->stream, w, cells, n, features, tok);
+}
+
+extern "C" int tah_embed(tah_dev *dev, const tah_weights *w, const tah_model *model, const float *x, int32_t n,
+                         float *tok) {
+    if (!w || !model || !x || !tok) return TAH_E_ARG;
+    return guarded(dev, [&] {
+        check_columns(w, model);
+        if (n <= 0) return TAH_OK;
+        const int T = w->cls + model->features;
+        Loans loans(dev);
+        float *xd = loans.take<float>((size_t)n * model->features);
+        float *td = loans.take<float>((size_t)n * T * w->e);
+        TAH_HIP(hipMemcpyAsync(xd, x, sizeof(float) * n * model->features, hipMemcpyHostToDevice, dev->stream));
+        embed_rows(dev, w, model, xd, n, td, loans);
+        TAH_HIP(hipMemcpyAsync(tok, td, sizeof(float) * n * T * w->e, hipMemcpyDeviceToHost, dev->stream));
+        TAH_HIP(hipStreamSynchronize(dev->stream));
+        return TAH_OK;
+    });
+}
+
+extern "C" int tah_represent(tah_dev *dev, const tah_weights *w, const float *tok, int32_t n, int32_t tokens,
+                             float *rep) {
+    if (!w || !tok || !rep) return TAH_E_ARG;
+    return guarded(dev, [&] {
+        if (w->row.empty()) throw ArgError{"weights lack the row stage"};
+        if (n <= 0) return TAH_OK;
+        if (tokens <= w->cls) throw ArgError{"represent: too few tokens"};
+        Loans loans(dev);
+        const size_t nt = (size_t)n * tokens * w->e;
+        float *td = loans.take<float>(nt), *rd = loans.take<float>((size_t)n * w->d);
+        float *scratch = loans.take<float>(row_stage_floats(w, n, tokens));
+        const float *tabs = rope_tables(dev, w, tokens, loans);
+        TAH_HIP(hipMemcpyAsync(td, tok, nt * sizeof(float), hipMemcpyHostToDevice, dev->stream));
+        row_stage(dev->stream, w, td, n, tokens, tabs, tabs + (size_t)tokens * w->rope_half, rd, scratch);
+        TAH_HIP(hipMemcpyAsync(rep, rd, sizeof(float) * n * w->d, hipMemcpyDeviceToHost, dev->stream));
+        TAH_HIP(hipStreamSynchronize(dev->stream));
+        return TAH_OK;
+    });
+}
+
+// Working bytes a sub-batch of k rows borrows in predict_rows (every buffer it and stage_rows take).
+static size_t predict_batch_bytes(const tah_weights *w, const tah_model *model, int k) {
+    const int T = w->cls + model->features;
+    int ff = 0;
+    for (auto &b : w->icl) ff = std::max(ff, b.ff);
+    const size_t kk = (size_t)k;
+    const size_t floats[] = {kk * T * w->e, kk * w->d, kk * model->features * w->e,
+                             column_stage_floats(w, k, model->features, model->digits), row_stage_floats(w, k, T),
+                             kk * w->d, kk * w->d, kk * w->d, kk * std::max(ff, w->dec_hidden)};
+    size_t bytes = attention_work_bytes(shape_of(model, model->heads, k)) + 256;
+    for (size_t f : floats) bytes += align256(f * sizeof(float)) + 256;
+    return bytes;
+}
+
+static size_t busy_bytes(const Pool &p) {
+    size_t b = 0;
+    for (auto &x : p.bufs)
+        if (x.busy) b += x.bytes;
+    return b;
+}
+
+// All three stages for n rows x (on the card) into out [n][out_n] (on the card), in sub-batches that fit the
+// working-memory budget (the reference's chain, src/gpu.rs:2171-2224); rows are independent.
+static void predict_rows(tah_dev *dev, const tah_weights *w, const tah_model *model, const float *x, int n, int out_n,
+                         float *out) {
+    check_columns(w, model);
+    check_stage(w, model, n, out_n);
+    const int T = w->cls + model->features;
+    Loans tabs_loan(dev);
+    const float *tabs = rope_tables(dev, w, T, tabs_loan);
+    const size_t used = busy_bytes(dev->pool);
+    const size_t room = dev->pool.budget > used ? dev->pool.budget - used : 0;
+    int batch = n;
+    while (batch > 1 && predict_batch_bytes(w, model, batch) > room) batch = (batch + 1) / 2;
+    if (predict_batch_bytes(w, model, batch) > room)
+        throw BudgetError{"graphics card: one row does not fit the working-memory budget"};
+    for (int r0 = 0; r0 < n; r0 += batch) {
+        const int k = std::min(batch, n - r0);
+        Loans loans(dev);
+        float *tok = loans.take<float>((size_t)k * T * w->e);
+        float *rep = loans.take<float>((size_t)k * w->d);
+        embed_rows(dev, w, model, x + (size_t)r0 * model->features, k, tok, loans);
+        float *scratch = loans.take<float>(row_stage_floats(w, k, T));
+        row_stage(dev->stream, w, tok, k, T, tabs, tabs + (size_t)T * w->rope_half, rep, scratch);
+        stage_rows(dev, w, model, rep, k, out_n, out + (size_t)r0 * out_n, loans);
+    }
+}
+
+extern "C" int tah_predict_rows_dev(tah_dev *dev, const tah_weights *w, const tah_model *model, const float *x_dev,
+                                    int32_t n, int32_t out_n, float *out_dev) {
+    if (!w || !model || !x_dev || !out_dev) return TAH_E_ARG;
+    return guarded(dev, [&] {
+        if (n < 0) throw ArgError{"predict: bad row count"};
+        if (n > 0) predict_rows(dev, w, model, x_dev, n, out_n, out_dev);
+        return TAH_OK;
+    });
+}
+
+extern "C" int tah_predict_rows(tah_dev *dev, const tah_weights *w, const tah_model *model, const float *x, int32_t n,
+                                int32_t out_n, float *out) {
+    if (!w || !model || !x || !out) return TAH_E_ARG;
+    return guarded(dev, [&] {
+        if (n < 0) throw ArgError{"predict: bad row count"};
+        if (n == 0) return TAH_OK;
+        check_columns(w, model);
+        Loans io(dev);
+        float *xd = io.take<float>((size_t)n * model->features), *od = io.take<float>((size_t)n * out_n);
+        TAH_HIP(hipMemcpyAsync(xd, x, sizeof(float) * n * model->features, hipMemcpyHostToDevice, dev->stream));
+        predict_rows(dev, w, model, xd, n, out_n, od);
+        TAH_HIP(hipMemcpyAsync(out, od, sizeof(float) * n * out_n, hipMemcpyDeviceToHost, dev->stream));
+        TAH_HIP(hipStreamSynchronize(dev->stream));
         return TAH_OK;
     });
 }

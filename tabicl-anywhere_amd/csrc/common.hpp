@@ -53,6 +53,16 @@ struct Pool {
     void release_idle();
 };
 
+// Column and row stages (stages.hip).
+void input_cells(hipStream_t s, const tah_weights *w, const float *x, int n, int features, float *cells);
+size_t column_stage_floats(const tah_weights *w, int n, int features, int digits);
+void column_stage(hipStream_t s, const tah_weights *w, const float *col_kv, int digits, const float *x, int n,
+                  int features, float *cells, float *scratch);
+void assemble_tokens(hipStream_t s, const tah_weights *w, const float *cells, int n, int features, float *tok);
+size_t row_stage_floats(const tah_weights *w, int n, int T);
+void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, const float *cosv, const float *sinv,
+               float *rep, float *scratch);
+
 }  // namespace tah
 
 // One GPU.
@@ -82,6 +92,7 @@ struct tah_weights {
     std::vector<DevBlock> col_a1, col_a2, row, icl;
     const float *in_w, *in_b, *col_ind, *col_y, *cls_tokens, *rope_freqs, *out_lnw, *out_lnb;
     const float *icl_y, *lnw, *lnb, *dec0w, *dec0b, *dec2w, *dec2b;
+    const float *col_scale;  // [e]: 1 / sqrt(column head width), what the column blocks' queries are multiplied by
 };
 
 struct tah_model {
@@ -92,6 +103,8 @@ struct tah_model {
     uint8_t *records = nullptr;  // layers x layer_bytes, the stored chunk records as they are
     float *scales = nullptr;     // [layers][d]
     size_t bytes = 0;
+    float *col_kv = nullptr;     // [features][digits][blocks][2][e][inds] (tah_model_set_columns)
+    int features = 0, digits = 0;
 };
 
 namespace tah {
@@ -121,5 +134,15 @@ void to_records(hipStream_t s, int rows, int d, int chunk, const float *kv, floa
 // f32 chunk records to i16/i8 records (the reference's quantiser, bit for bit).
 void pack(hipStream_t s, int rows, int d, int chunk, int fmt, const float *rec32, uint8_t *recq);
 void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t *records, float *out, void *work);
+
+// Column and row stages (stages.hip).
+void input_cells(hipStream_t s, const tah_weights *w, const float *x, int n, int features, float *cells);
+size_t column_stage_floats(const tah_weights *w, int n, int features, int digits);
+void column_stage(hipStream_t s, const tah_weights *w, const float *col_kv, int digits, const float *x, int n,
+                  int features, float *cells, float *scratch);
+void assemble_tokens(hipStream_t s, const tah_weights *w, const float *cells, int n, int features, float *tok);
+size_t row_stage_floats(const tah_weights *w, int n, int T);
+void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, const float *cosv, const float *sinv,
+               float *rep, float *scratch);
 
 }  // namespace tah

@@ -1,0 +1,437 @@
+// The column and row stages on the card: a test (or training) table's feature rows to row representations.
+//
+// Column stage (src/predict.rs:282-353, src/fit.rs:326-423): every cell is the input layer applied to three of its
+// row's features (src/nn.rs:424-429; all -100 stays -100), then per column block a whole attention block against
+// that feature group's 128 cached inducing-point keys and values (cached_block, src/nn.rs:291-301). All cells of
+// all rows go through each dense layer as one GEMM; the attention is grouped by feature group: a workgroup holds
+// one group's K and V for one head in LDS and attends 64 cells to its 128 keys with fp32 MFMA (head width 16),
+// scores transposed so that each lane owns one cell, as in the in-context kernel.
+//
+// Row stage (row_forward, src/nn.rs:357-419): per row, the class tokens and the row's cells attend to each other
+// with non-interleaved rotary positions (queries also scaled by 1/sqrt(head width)); the last block updates only
+// the class tokens, which are then normalised and laid end to end as the row's representation.
+#include <algorithm>
+
+#include "common.hpp"
+#include "device_math.hpp"
+
+namespace tah {
+
+// ---- input layer -------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_input_cells(int n, int features, int group, int e, const float *__restrict__ x,
+                                                      const float *__restrict__ in_w, const float *__restrict__ in_b,
+                                                      float *__restrict__ cells) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)n * features * e) return;
+    const int o = (int)(i % e);
+    const size_t cell = i / e;
+    const int g = (int)(cell % features);
+    const float *xr = x + (cell / features) * features;
+    float vals[8];
+    bool missing = true;
+    for (int k = 0; k < group; k++) {
+        vals[k] = xr[(g + (1 << k)) % features];
+        missing = missing && vals[k] == -100.0f;
+    }
+    if (missing) {
+        cells[i] = -100.0f;
+        return;
+    }
+    float s = 0.0f;
+    for (int k = 0; k < group; k++) s += in_w[o * group + k] * vals[k];
+    cells[i] = s + in_b[o];
+}
+
+// ---- cells against a group's inducing points: head width 16, 16 * NT keys ----------------------------------------
+// grid (tiles of 64 rows, heads, groups); 256 threads. q and out are [n * features][e] (cell (r, g) at r*features+g);
+// group g's keys and values are K = kvbase + g * gstride ([e][inds]) and V = K + e * inds.
+template <int NT>
+__global__ __launch_bounds__(256) void k_cell_attn16(int n, int features, int e, const float *__restrict__ q,
+                                                      const float *__restrict__ kvbase, size_t gstride,
+                                                      float *__restrict__ out) {
+    constexpr int INDS = 16 * NT;
+    __shared__ float Ks[16][INDS + 4];
+    __shared__ float Vs[16][INDS + 4];
+    const int h = blockIdx.y, g = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
+    const float *K = kvbase + (size_t)g * gstride, *V = K + (size_t)e * INDS;
+    for (int i = tid; i < 16 * INDS; i += 256) {
+        const int c = i / INDS, k = i % INDS;
+        Ks[c][k] = K[(size_t)(h * 16 + c) * INDS + k];
+        Vs[c][k] = V[(size_t)(h * 16 + c) * INDS + k];
+    }
+    __syncthreads();
+    const int r = blockIdx.x * 64 + wave * 16 + r16;
+    const bool live = r < n;
+    const size_t m = (size_t)r * features + g;
+    float4 qv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (live) qv = *reinterpret_cast<const float4 *>(q + m * e + h * 16 + 4 * g4);
+    const float qa[4] = {qv.x, qv.y, qv.z, qv.w};
+    floatx4 sacc[NT];
+#pragma unroll
+    for (int kt = 0; kt < NT; kt++) {
+        sacc[kt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int t = 0; t < 4; t++) sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(Ks[4 * g4 + t][16 * kt + r16], qa[t], sacc[kt], 0, 0, 0);
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < NT; kt++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) mx = fmaxf(mx, sacc[kt][v]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    float l = 0.0f;
+#pragma unroll
+    for (int kt = 0; kt < NT; kt++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            sacc[kt][v] = fast_exp(sacc[kt][v] - mx);
+            l += sacc[kt][v];
+        }
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kt = 0; kt < NT; kt++) {
+        const float4 vv = *reinterpret_cast<const float4 *>(&Vs[r16][16 * kt + 4 * g4]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.x, sacc[kt][0], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.y, sacc[kt][1], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.z, sacc[kt][2], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.w, sacc[kt][3], acc, 0, 0, 0);
+    }
+    if (live) {
+        const float inv = 1.0f / l;
+        *reinterpret_cast<float4 *>(out + m * e + h * 16 + 4 * g4) = make_float4(acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv);
+    }
+}
+
+// Any head width and key count (the tiny test models): one thread per (cell, head).
+__global__ __launch_bounds__(256) void k_cell_attn_plain(int n, int features, int e, int heads, int inds,
+                                                          const float *__restrict__ q, const float *__restrict__ kvbase,
+                                                          size_t gstride, float *__restrict__ out) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)n * features * heads) return;
+    const int h = (int)(i % heads);
+    const size_t m = i / heads;
+    const int g = (int)(m % features), hd = e / heads;
+    const float *K = kvbase + (size_t)g * gstride, *V = K + (size_t)e * inds;
+    const float *qr = q + m * e + h * hd;
+    float mx = -INFINITY;
+    for (int k = 0; k < inds; k++) {
+        float s = 0.0f;
+        for (int c = 0; c < hd; c++) s += qr[c] * K[(size_t)(h * hd + c) * inds + k];
+        mx = fmaxf(mx, s);
+    }
+    float l = 0.0f;
+    float *o = out + m * e + h * hd;
+    for (int c = 0; c < hd; c++) o[c] = 0.0f;
+    for (int k = 0; k < inds; k++) {
+        float s = 0.0f;
+        for (int c = 0; c < hd; c++) s += qr[c] * K[(size_t)(h * hd + c) * inds + k];
+        const float p = fast_exp(s - mx);
+        l += p;
+        for (int c = 0; c < hd; c++) o[c] += p * V[(size_t)(h * hd + c) * inds + k];
+    }
+    for (int c = 0; c < hd; c++) o[c] /= l;
+}
+
+// ---- rotary positions --------------------------------------------------------------------------------------
+// qkv [rows][3e] with rows = n * T token rows (position = row % T). Queries also take 1/sqrt(hd).
+__global__ __launch_bounds__(256) void k_rope(size_t rows, int T, int e, int heads, int half,
+                                               const float *__restrict__ cosv, const float *__restrict__ sinv,
+                                               float *__restrict__ qkv, float inv) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * heads * half) return;
+    const int k = (int)(i % half);
+    const int h = (int)((i / half) % heads);
+    const size_t row = i / ((size_t)half * heads);
+    const int t = (int)(row % T), hd = 2 * half;
+    const float c = cosv[t * half + k], s = sinv[t * half + k];
+    float *qh = qkv + row * 3 * e + h * hd;
+    const float a = qh[k], b = qh[k + half];
+    qh[k] = (a * c - b * s) * inv;
+    qh[k + half] = (b * c + a * s) * inv;
+    float *kh = qh + e;
+    const float ka = kh[k], kb = kh[k + half];
+    kh[k] = ka * c - kb * s;
+    kh[k + half] = kb * c + ka * s;
+}
+
+// ---- attention within each row: head width 16, up to 16 * NT tokens -------------------------------------------
+// grid (rows, heads); 256 threads. Queries are the first nq_tok tokens of each row; out is [n][nq_tok][e].
+template <int NT>
+__global__ __launch_bounds__(256) void k_row_attn16(int n, int T, int nq_tok, int e, const float *__restrict__ qkv,
+                                                     float *__restrict__ out) {
+    constexpr int KT = 16 * NT;
+    __shared__ float Ks[16][KT + 4];
+    __shared__ float Vs[16][KT + 4];
+    const int r = blockIdx.x, h = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r16 = lane & 15, g4 = lane >> 4;
+    const float *base = qkv + (size_t)r * T * 3 * e;
+    for (int i = tid; i < 16 * KT; i += 256) {
+        const int k = i >> 4, c = i & 15;
+        const bool ok = k < T;
+        Ks[c][k] = ok ? base[(size_t)k * 3 * e + e + h * 16 + c] : 0.0f;
+        Vs[c][k] = ok ? base[(size_t)k * 3 * e + 2 * e + h * 16 + c] : 0.0f;
+    }
+    __syncthreads();
+    for (int qt = wave; qt * 16 < nq_tok; qt += 4) {
+        const int t = qt * 16 + r16;
+        const bool live = t < nq_tok;
+        float4 qv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (live) qv = *reinterpret_cast<const float4 *>(base + (size_t)t * 3 * e + h * 16 + 4 * g4);
+        const float qa[4] = {qv.x, qv.y, qv.z, qv.w};
+        floatx4 sacc[NT];
+#pragma unroll
+        for (int kt = 0; kt < NT; kt++) {
+            sacc[kt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int s = 0; s < 4; s++) sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(Ks[4 * g4 + s][16 * kt + r16], qa[s], sacc[kt], 0, 0, 0);
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < NT; kt++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                if (16 * kt + 4 * g4 + v >= T) sacc[kt][v] = -INFINITY;
+                mx = fmaxf(mx, sacc[kt][v]);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        float l = 0.0f;
+#pragma unroll
+        for (int kt = 0; kt < NT; kt++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                sacc[kt][v] = fast_exp(sacc[kt][v] - mx);
+                l += sacc[kt][v];
+            }
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+        floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kt = 0; kt < NT; kt++) {
+            const float4 vv = *reinterpret_cast<const float4 *>(&Vs[r16][16 * kt + 4 * g4]);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.x, sacc[kt][0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.y, sacc[kt][1], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.z, sacc[kt][2], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.w, sacc[kt][3], acc, 0, 0, 0);
+        }
+        if (live) {
+            const float inv = 1.0f / l;
+            *reinterpret_cast<float4 *>(out + ((size_t)r * nq_tok + t) * e + h * 16 + 4 * g4) =
+                make_float4(acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv);
+        }
+    }
+}
+
+// Any head width and token count: one thread per (row, query token, head).
+__global__ __launch_bounds__(256) void k_row_attn_plain(int n, int T, int nq_tok, int e, int heads,
+                                                         const float *__restrict__ qkv, float *__restrict__ out) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)n * nq_tok * heads) return;
+    const int h = (int)(i % heads);
+    const int t = (int)((i / heads) % nq_tok);
+    const size_t r = i / ((size_t)heads * nq_tok);
+    const int hd = e / heads;
+    const float *base = qkv + r * T * 3 * e;
+    const float *qr = base + (size_t)t * 3 * e + h * hd;
+    float mx = -INFINITY;
+    for (int k = 0; k < T; k++) {
+        float s = 0.0f;
+        for (int c = 0; c < hd; c++) s += qr[c] * base[(size_t)k * 3 * e + e + h * hd + c];
+        mx = fmaxf(mx, s);
+    }
+    float l = 0.0f;
+    float *o = out + (r * nq_tok + t) * e + h * hd;
+    for (int c = 0; c < hd; c++) o[c] = 0.0f;
+    for (int k = 0; k < T; k++) {
+        float s = 0.0f;
+        for (int c = 0; c < hd; c++) s += qr[c] * base[(size_t)k * 3 * e + e + h * hd + c];
+        const float p = fast_exp(s - mx);
+        l += p;
+        for (int c = 0; c < hd; c++) o[c] += p * base[(size_t)k * 3 * e + 2 * e + h * hd + c];
+    }
+    for (int c = 0; c < hd; c++) o[c] /= l;
+}
+
+// ---- small copies ------------------------------------------------------------------------------------------
+// tok [n][T][e]: class tokens, then the row's cells (cells [n][features][e]).
+__global__ __launch_bounds__(256) void k_tokens(int n, int cls, int features, int e, const float *__restrict__ cls_tokens,
+                                                 const float *__restrict__ cells, float *__restrict__ tok) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int T = cls + features;
+    if (i >= (size_t)n * T * e) return;
+    const int o = (int)(i % e);
+    const int t = (int)((i / e) % T);
+    const size_t r = i / ((size_t)e * T);
+    tok[i] = t < cls ? cls_tokens[t * e + o] : cells[(r * features + (t - cls)) * e + o];
+}
+
+// dst [n][k][e] = the first k tokens of each row of src [n][T][e].
+__global__ __launch_bounds__(256) void k_first_tokens(int n, int T, int k, int e, const float *__restrict__ src,
+                                                       float *__restrict__ dst) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)n * k * e) return;
+    const int o = (int)(i % e);
+    const int t = (int)((i / e) % k);
+    const size_t r = i / ((size_t)e * k);
+    dst[i] = src[(r * T + t) * e + o];
+}
+
+__global__ __launch_bounds__(256) void k_accumulate(size_t count, const float *__restrict__ x, float *__restrict__ sum) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < count) sum[i] += x[i];
+}
+
+// x = sum / digits (the prediction-side average over label digits, src/predict.rs:343-345)
+__global__ __launch_bounds__(256) void k_divide(size_t count, const float *__restrict__ sum, float digits,
+                                                 float *__restrict__ x) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < count) x[i] = sum[i] / digits;
+}
+
+static dim3 blocks_for(size_t count) { return dim3((unsigned)((count + 255) / 256)); }
+
+// ---- host side ---------------------------------------------------------------------------------------------
+void input_cells(hipStream_t s, const tah_weights *w, const float *x, int n, int features, float *cells) {
+    if (w->group > 8 || w->group < 1) throw ArgError{"column stage: feature group size must be 1..8"};
+    const size_t count = (size_t)n * features * w->e;
+    hipLaunchKernelGGL(k_input_cells, blocks_for(count), dim3(256), 0, s, n, features, w->group, w->e, x, w->in_w, w->in_b,
+                       cells);
+    TAH_LAUNCHED();
+}
+
+// One column block (cached_block with a2) for all cells [n * features][e] in place: K/V of group g at
+// kvbase + g * gstride.
+void column_block(hipStream_t s, const tah_weights *w, const DevBlock &b, float *cells, int n, int features,
+                  const float *kvbase, size_t gstride, float *t, float *q, float *att, float *mid) {
+    const int e = w->e;
+    const int M = n * features;
+    layer_norm(s, M, e, cells, e, b.n1w, b.n1b, t, e);
+    gemm(s, M, e, e, t, e, b.in_w, b.in_b, q, e, EPI_NONE, nullptr, 0);
+    query_modulate(s, M, b, w->col_scale, q);
+    const int hd = e / b.heads;
+    if (hd == 16 && w->inds % 16 == 0 && w->inds <= 256) {
+        dim3 grid((n + 63) / 64, b.heads, features);
+        switch (w->inds / 16) {
+            case 8: hipLaunchKernelGGL(k_cell_attn16<8>, grid, dim3(256), 0, s, n, features, e, q, kvbase, gstride, att); break;
+            case 16: hipLaunchKernelGGL(k_cell_attn16<16>, grid, dim3(256), 0, s, n, features, e, q, kvbase, gstride, att); break;
+            default:
+                hipLaunchKernelGGL(k_cell_attn_plain, blocks_for((size_t)M * b.heads), dim3(256), 0, s, n, features, e,
+                                   b.heads, w->inds, q, kvbase, gstride, att);
+        }
+    } else {
+        hipLaunchKernelGGL(k_cell_attn_plain, blocks_for((size_t)M * b.heads), dim3(256), 0, s, n, features, e, b.heads,
+                           w->inds, q, kvbase, gstride, att);
+    }
+    TAH_LAUNCHED();
+    gemm(s, M, e, e, att, e, b.out_w, b.out_b, cells, e, EPI_RESID, cells, e);
+    layer_norm(s, M, e, cells, e, b.n2w, b.n2b, t, e);
+    gemm(s, M, b.ff, e, t, e, b.l1w, b.l1b, mid, b.ff, EPI_GELU, nullptr, 0);
+    gemm(s, M, e, b.ff, mid, b.ff, b.l2w, b.l2b, cells, e, EPI_RESID, cells, e);
+}
+
+size_t column_stage_floats(const tah_weights *w, int n, int features, int digits) {
+    int ff = 0;
+    for (auto &b : w->col_a2) ff = std::max(ff, b.ff);
+    const size_t M = (size_t)n * features;
+    return M * (4 * (size_t)w->e + ff) + (digits > 1 ? 2 * M * w->e : 0);
+}
+
+// The column stage at prediction for n rows x [n][features] (device): cells [n * features][e] after the stage.
+// col_kv [features][digits][blocks][2][e][inds] on the card. scratch holds column_stage_floats floats.
+void column_stage(hipStream_t s, const tah_weights *w, const float *col_kv, int digits, const float *x, int n,
+                  int features, float *cells, float *scratch) {
+    const int e = w->e, nb = w->col_blocks;
+    int ff = 0;
+    for (auto &b : w->col_a2) ff = std::max(ff, b.ff);
+    const size_t M = (size_t)n * features;
+    float *t = scratch, *q = t + M * e, *att = q + M * e, *mid = att + M * e;
+    float *plain = mid + M * ff, *sum = plain + M * e;
+    const size_t per = 2 * (size_t)e * w->inds, gstride = (size_t)digits * nb * per;
+    input_cells(s, w, x, n, features, cells);
+    if (digits == 1) {
+        for (int bi = 0; bi < nb; bi++) column_block(s, w, w->col_a2[bi], cells, n, features, col_kv + bi * per, gstride, t, q, att, mid);
+        return;
+    }
+    const size_t count = M * e;
+    TAH_HIP(hipMemcpyAsync(plain, cells, count * sizeof(float), hipMemcpyDeviceToDevice, s));
+    TAH_HIP(hipMemsetAsync(sum, 0, count * sizeof(float), s));
+    for (int dg = 0; dg < digits; dg++) {
+        if (dg > 0) TAH_HIP(hipMemcpyAsync(cells, plain, count * sizeof(float), hipMemcpyDeviceToDevice, s));
+        for (int bi = 0; bi < nb; bi++)
+            column_block(s, w, w->col_a2[bi], cells, n, features, col_kv + ((size_t)dg * nb + bi) * per, gstride, t, q, att, mid);
+        hipLaunchKernelGGL(k_accumulate, blocks_for(count), dim3(256), 0, s, count, cells, sum);
+        TAH_LAUNCHED();
+    }
+    hipLaunchKernelGGL(k_divide, blocks_for(count), dim3(256), 0, s, count, sum, (float)digits, cells);
+    TAH_LAUNCHED();
+}
+
+size_t row_stage_floats(const tah_weights *w, int n, int T) {
+    int ff = 0;
+    for (auto &b : w->row) ff = std::max(ff, b.ff);
+    const size_t R = (size_t)n * T;
+    return R * ((size_t)w->e * 5 + ff) + 2 * (size_t)T * w->rope_half + (size_t)n * w->cls * w->e * 2;
+}
+
+// The row stage for n rows: tok [n][T][e] (consumed) to rep [n][cls * e]. cosv/sinv [T][half] on the card.
+void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, const float *cosv, const float *sinv,
+               float *rep, float *scratch) {
+    const int e = w->e, heads = w->row_heads, cls = w->cls;
+    int ff = 0;
+    for (auto &b : w->row) ff = std::max(ff, b.ff);
+    const size_t R = (size_t)n * T;
+    float *t = scratch, *qkv = t + R * e, *att = qkv + R * 3 * e, *mid = att + R * e;
+    float *xc = mid + R * ff, *ac = xc + (size_t)n * cls * e;
+    const int hd = e / heads, half = w->rope_half;
+    if (2 * half != hd) throw ArgError{"row stage: rotary frequencies must cover half the head width"};
+    const float inv = 1.0f / sqrtf((float)hd);
+    const int last = w->row_blocks - 1;
+    const bool mfma = hd == 16 && T <= 256;
+    auto attend = [&](int nq_tok, float *dst) {
+        if (mfma && T <= 128)
+            hipLaunchKernelGGL(k_row_attn16<8>, dim3(n, heads), dim3(256), 0, s, n, T, nq_tok, e, qkv, dst);
+        else if (mfma)
+            hipLaunchKernelGGL(k_row_attn16<16>, dim3(n, heads), dim3(256), 0, s, n, T, nq_tok, e, qkv, dst);
+        else
+            hipLaunchKernelGGL(k_row_attn_plain, blocks_for((size_t)n * nq_tok * heads), dim3(256), 0, s, n, T, nq_tok, e,
+                               heads, qkv, dst);
+        TAH_LAUNCHED();
+    };
+    for (int bi = 0; bi <= last; bi++) {
+        const DevBlock &b = w->row[bi];
+        layer_norm(s, (int)R, e, tok, e, b.n1w, b.n1b, t, e);
+        gemm(s, (int)R, 3 * e, e, t, e, b.in_w, b.in_b, qkv, 3 * e, EPI_NONE, nullptr, 0);
+        hipLaunchKernelGGL(k_rope, blocks_for(R * heads * half), dim3(256), 0, s, R, T, e, heads, half, cosv, sinv, qkv, inv);
+        TAH_LAUNCHED();
+        if (bi < last) {
+            attend(T, att);
+            gemm(s, (int)R, e, e, att, e, b.out_w, b.out_b, tok, e, EPI_RESID, tok, e);
+            layer_norm(s, (int)R, e, tok, e, b.n2w, b.n2b, t, e);
+            gemm(s, (int)R, b.ff, e, t, e, b.l1w, b.l1b, mid, b.ff, EPI_GELU, nullptr, 0);
+            gemm(s, (int)R, e, b.ff, mid, b.ff, b.l2w, b.l2b, tok, e, EPI_RESID, tok, e);
+        } else {
+            // the last block: only the class tokens are queried and updated
+            const int M = n * cls;
+            attend(cls, ac);
+            hipLaunchKernelGGL(k_first_tokens, blocks_for((size_t)M * e), dim3(256), 0, s, n, T, cls, e, tok, xc);
+            TAH_LAUNCHED();
+            gemm(s, M, e, e, ac, e, b.out_w, b.out_b, xc, e, EPI_RESID, xc, e);
+            layer_norm(s, M, e, xc, e, b.n2w, b.n2b, t, e);
+            gemm(s, M, b.ff, e, t, e, b.l1w, b.l1b, mid, b.ff, EPI_GELU, nullptr, 0);
+            gemm(s, M, e, b.ff, mid, b.ff, b.l2w, b.l2b, xc, e, EPI_RESID, xc, e);
+            layer_norm(s, M, e, xc, e, w->out_lnw, w->out_lnb, rep, e);
+        }
+    }
+}
+
+void assemble_tokens(hipStream_t s, const tah_weights *w, const float *cells, int n, int features, float *tok) {
+    const size_t count = (size_t)n * (w->cls + features) * w->e;
+    hipLaunchKernelGGL(k_tokens, blocks_for(count), dim3(256), 0, s, n, w->cls, features, w->e, w->cls_tokens, cells, tok);
+    TAH_LAUNCHED();
+}
+
+}  // namespace tah

@@ -129,6 +129,36 @@ class Gpu:
         self._check(self._l.tah_stage(self._h, weights._h, vm._h, _fp(h), nq, int(out_n), _fp(out)))
         return out
 
+    # ---- the column and row stages, and all three at once (AttendCached::rows) -------------------------------
+    def embed(self, weights: "GpuWeights", vm: "VramModel", x) -> np.ndarray:
+        """The column stage: x [n][features] to tokens [n][cls + features][e] (`embed`, `src/predict.rs:282-353`)."""
+        x = _f32(x)
+        n = x.shape[0]
+        m = weights.model
+        tok = np.empty((n, m.cls + vm.features, m.e), np.float32)
+        self._check(self._l.tah_embed(self._h, weights._h, vm._h, _fp(x), n, _fp(tok)))
+        return tok
+
+    def represent(self, weights: "GpuWeights", tok) -> np.ndarray:
+        """The row stage: tokens [n][T][e] to representations [n][d] (`represent`, `src/predict.rs:356-372`)."""
+        tok = _f32(tok)
+        n, T = tok.shape[0], tok.shape[1]
+        rep = np.empty((n, weights.model.d), np.float32)
+        self._check(self._l.tah_represent(self._h, weights._h, _fp(tok), n, T, _fp(rep)))
+        return rep
+
+    def predict(self, weights: "GpuWeights", vm: "VramModel", x, out_n: int) -> np.ndarray:
+        """All three stages (`Gpu::predict`, `src/gpu.rs:2146`): x [n][features] to the first out_n outputs."""
+        x = _f32(x)
+        n = x.shape[0]
+        out = np.empty((n, out_n), np.float32)
+        self._check(self._l.tah_predict_rows(self._h, weights._h, vm._h, _fp(x), n, int(out_n), _fp(out)))
+        return out
+
+    def predict_dev(self, weights: "GpuWeights", vm: "VramModel", x_ptr: int, n: int, out_n: int, out_ptr: int) -> None:
+        self._check(self._l.tah_predict_rows_dev(self._h, weights._h, vm._h, ctypes.c_void_p(x_ptr), int(n), int(out_n),
+                                                 ctypes.c_void_p(out_ptr)))
+
     # ---- fitting: fit::Attend (src/fit.rs:45-74) ---------------------------------------------------------------
     def pack(self, c, d: int, rc: int, kv_format: int) -> np.ndarray:
         """One stored chunk record from its f32 keys and values `c` ([2d][rc]), quantised on the card."""
@@ -224,6 +254,16 @@ class VramModel:
                                          ctypes.byref(h)))
         self._h = h
 
+    def set_columns(self, col_kv, features: int, digits: int) -> None:
+        """Hold the member's column cache too (`col_kv`, [features][digits][blocks][2][e][inds])."""
+        m = self.weights.model
+        col_kv = _f32(col_kv).reshape(-1)
+        if col_kv.size != features * digits * len(m.col_a2) * 2 * m.e * m.inds:
+            raise ValueError("set_columns: col_kv has the wrong size")
+        self.gpu._check(self.gpu._l.tah_model_set_columns(self.gpu._h, self._h, self.weights._h, _fp(col_kv),
+                                                          int(features), int(digits)))
+        self.features, self.digits = int(features), int(digits)
+
     @staticmethod
     def model_bytes(kv_format: int, rows: int, chunk: int, d: int, layers: int) -> int:
         return int(abi.lib().tah_model_bytes(kv_format, rows, chunk, d, layers))
@@ -261,3 +301,9 @@ class CardAttend:
         if vm is None or d != vm.d:
             return None
         return self.gpu.in_context(self.weights, vm, h, out_n)
+
+    def rows(self, prefix: str, x, out_n: int):
+        vm = self.models.get((prefix, 0))
+        if vm is None or not getattr(vm, "features", 0) or vm.digits != 1:
+            return None
+        return self.gpu.predict(self.weights, vm, x, out_n)

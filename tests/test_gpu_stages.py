@@ -1,0 +1,145 @@
+"""The column and row stages on the card, and prediction from feature rows (AttendCached::rows), against the
+oracle and the reference's golden embeddings, representations and scores."""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as orc
+from conftest import pkg
+
+abi, hip, M = pkg("abi"), pkg("hip"), pkg("model")
+planmod = pkg("plan")
+pytestmark = pytest.mark.gpu
+TOL = 5e-5
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    g = hip.Gpu(0)
+    yield g
+    g.close()
+
+
+@pytest.fixture(scope="module")
+def full_model():
+    return M.Model.random(M.FULL_CLASSIFIER, seed=2)
+
+
+@pytest.fixture(scope="module")
+def full_weights(gpu, full_model):
+    return gpu.weights(full_model)
+
+
+def test_stages_tiny_match_reference(gpu, tiny_model, tiny_raw):
+    """embed, represent and all three stages on the card for the golden tiny table (tests/reference.rs:91-116)."""
+    say("stages tiny golden")
+    m = tiny_model
+    x = tiny_raw.f32s("x_train").reshape(120, 7)
+    y = tiny_raw.i32s("y_train").astype(np.float32)
+    fit = orc.fit_raw(m, x, y, 3, chunk=48)
+    xt = tiny_raw.f32s("x_test").reshape(16, 7)
+    w = gpu.weights(m)
+    vm = gpu.load(w, abi.KV_F32, 120, 48, fit.layers[0], fit.scales[0])
+    vm.set_columns(fit.col_kv, 7, 1)
+    tok = gpu.embed(w, vm, xt)
+    want = tiny_raw.f32s("test_emb").reshape(16, m.cls + 7, m.e)
+    assert np.abs(tok - orc.embed(m, fit, xt)).max() < TOL
+    assert np.abs(tok[:, m.cls:] - want[:, m.cls:]).max() < TOL
+    rep = gpu.represent(w, tok)
+    assert np.abs(rep - tiny_raw.f32s("test_rep").reshape(16, m.d)).max() < TOL
+    scores = gpu.predict(w, vm, xt, 3)
+    assert np.abs(scores - tiny_raw.f32s("logits").reshape(16, 3)).max() < TOL
+    card = hip.CardAttend(gpu, w)
+    card.hold("", 0, vm)
+    assert np.array_equal(card.rows("", xt, 3), scores)
+
+
+def test_embed_with_label_digits_and_missing_cells(gpu, tiny_model):
+    """Several label digits (averaged, src/predict.rs:326-345) and all--100 cells (src/predict.rs:314-316)."""
+    m = tiny_model
+    rng = np.random.default_rng(5)
+    features, digits, n = 6, 2, 40
+    col_kv = rng.standard_normal((features, digits, len(m.col_a2), 2, m.e, m.inds)).astype(np.float32)
+    x = rng.standard_normal((n, features)).astype(np.float32)
+    x[3, :] = -100.0
+    x[5, 1:4] = -100.0
+    w = gpu.weights(m)
+    dummy = [np.zeros(abi.layer_bytes(abi.KV_F32, 8, 8, m.d), np.uint8) for _ in range(m.icl_layers)]
+    vm = gpu.load(w, abi.KV_F32, 8, 8, dummy, np.ones((m.icl_layers, m.d), np.float32))
+    vm.set_columns(col_kv, features, digits)
+    fitted = orc.Fitted(8, features, 3, 8, abi.KV_F32, planmod.Plan([4, 4], []), col_kv, [], [])
+    fitted.digits = digits
+    got = gpu.embed(w, vm, x)
+    want = orc.embed(m, fitted, x)
+    assert np.abs(got - want).max() < TOL
+
+
+@pytest.mark.parametrize("features", [100, 150])
+def test_stages_full_size(gpu, full_model, full_weights, features):
+    """Full-size column stage (3 blocks, 8 x 16 heads, 128 inducing points per group) and row stage (104 or 154
+    tokens, RoPE) against the oracle, then all three stages with a stored in-context cache."""
+    say(f"stages full features={features}")
+    m = full_model
+    rng = np.random.default_rng(features)
+    n = 24
+    col_kv = (rng.standard_normal((features, 1, len(m.col_a2), 2, m.e, m.inds)) * 0.5).astype(np.float32)
+    rows, chunk = 600, 256
+    layers = []
+    for _ in range(m.icl_layers):
+        parts = [orc.pack((rng.standard_normal(2 * m.d * min(chunk, rows - c0)) * 0.5).astype(np.float32), m.d,
+                          min(chunk, rows - c0), abi.KV_F32) for c0 in range(0, rows, chunk)]
+        layers.append(np.concatenate(parts))
+    scales = np.stack([orc.query_scale(b, rows) for b in m.icl])
+    vm = gpu.load(full_weights, abi.KV_F32, rows, chunk, layers, scales)
+    vm.set_columns(col_kv, features, 1)
+    x = rng.standard_normal((n, features)).astype(np.float32)
+    x[2, :] = -100.0
+    fitted = orc.Fitted(rows, features, 10, chunk, abi.KV_F32, planmod.Plan([10], [planmod.Node(None, [], 10, True, list(range(10)))]),
+                        col_kv, [scales], [layers])
+    tok = gpu.embed(full_weights, vm, x)
+    want_tok = orc.embed(m, fitted, x)
+    err = np.abs(tok - want_tok).max()
+    say("  embed worst", err, "scale", np.abs(want_tok).max())
+    assert err < TOL * max(1.0, np.abs(want_tok).max())
+    rep = gpu.represent(full_weights, want_tok)
+    want_rep = orc.represent(m, want_tok)
+    err = np.abs(rep - want_rep).max()
+    say("  represent worst", err)
+    assert err < TOL
+    scores = gpu.predict(full_weights, vm, x, 10)
+    want = orc.predict_raw(m, fitted, x)
+    err = np.abs(scores - want).max()
+    say("  predict worst", err, "scale", np.abs(want).max())
+    assert err < TOL * max(1.0, np.abs(want).max())
+
+
+def test_sub_batches_give_the_same_answers(gpu, tiny_model, tiny_raw):
+    """A working-memory budget that forces sub-batches of rows changes no answer beyond rounding
+    (tests/card.rs:237-274), and a budget too small for one row is an OutOfMemory error."""
+    m = tiny_model
+    x = tiny_raw.f32s("x_train").reshape(120, 7)
+    y = tiny_raw.i32s("y_train").astype(np.float32)
+    fit = orc.fit_raw(m, x, y, 3, chunk=48)
+    xt = np.concatenate([tiny_raw.f32s("x_test").reshape(16, 7)] * 8)
+    w = gpu.weights(m)
+    vm = gpu.load(w, abi.KV_F32, 120, 48, fit.layers[0], fit.scales[0])
+    vm.set_columns(fit.col_kv, 7, 1)
+    whole = gpu.predict(w, vm, xt, 3)
+    old = gpu.work_budget()
+    try:
+        gpu.release()
+        gpu.set_work_budget(64 << 10)
+        part = gpu.predict(w, vm, xt, 3)
+        assert np.abs(part - whole).max() < 1e-5
+        assert gpu.working()[1] <= 64 << 10
+        gpu.set_work_budget(4 << 10)
+        with pytest.raises(hip.BudgetError):
+            gpu.predict(w, vm, xt, 3)
+    finally:
+        gpu.set_work_budget(old)
