@@ -1,11 +1,13 @@
-"""Benchmark: predicted rows/s of the in-context stage on one MI355X.
+"""Benchmark: predicted rows/s on one MI355X against a 10,000-row x 100-feature fitted cache.
 
-Workload: the full-size TabICL v2 classifier architecture (d = 512, 12 in-context layers of 8 heads x 64, decoder
-1024 -> 10), random-init weights from seed 2, against a stored f32 cache of 10,000 training rows (chunks of 256,
-the last of 16). A step is one in-context pass (12 layers + decoder) of a batch of 2,048 test rows, inputs already
-resident in HBM. Also reported: rows/s at batches of 1, 64 and 256; the attention kernel's share of the MFMA
-roofline (measured with HIP events on the library's stream); and the oracle (the C restatement of the reference's
-CPU path) timed on this host's cores on a bounded sample of the same workload.
+Workload: the full-size TabICL v2 classifier architecture (e = 128, 3 column blocks of 8 x 16 heads over 128
+inducing points, 3 row blocks, d = 512, 12 in-context layers of 8 heads x 64, decoder 1024 -> 10), random-init
+weights from seed 2, a stored f32 cache of 10,000 training rows (chunks of 256, the last of 16) and its column cache
+for 100 features. A step is one prediction pass of a batch of 2,048 test rows of 100 features through all three
+stages (column, row, in-context + decoder), inputs already resident in HBM. Also reported: rows/s at batches of 1,
+64 and 256, the in-context stage alone, the attention kernel's share of the fp32 MFMA roofline (measured with HIP
+events on the library's stream), and the oracle (the C restatement of the reference's CPU path) timed on this
+host's cores on a bounded sample of the same workload.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 """
@@ -21,7 +23,7 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-ROWS, CHUNK, BATCH, CLASSES = 10000, 256, 2048, 10
+ROWS, FEATURES, CHUNK, BATCH, CLASSES = 10000, 100, 256, 2048, 10
 PEAK_F32_MFMA = 157.3e12  # MI355X dense fp32 matrix FLOP/s
 PEAK_HBM = 8.0e12
 
@@ -63,13 +65,17 @@ def main():
     log("device:", gpu.name)
     w = gpu.weights(model)
     vm = gpu.load(w, abi.KV_F32, ROWS, CHUNK, layers, scales)
+    col_kv = (rng.standard_normal((FEATURES, 1, len(model.col_a2), 2, model.e, model.inds)) * 0.5).astype(np.float32)
+    vm.set_columns(col_kv, FEATURES, 1)
+    x_host = rng.standard_normal((BATCH, FEATURES)).astype(np.float32)
+    x_dev = dm.DeviceBuffer.of(x_host)
     h_host = rng.standard_normal((BATCH, d)).astype(np.float32)
     h_dev = dm.DeviceBuffer.of(h_host)
     out_dev = dm.DeviceBuffer(BATCH * CLASSES * 4)
     timer = dm.EventTimer(gpu.stream)
 
     def run(n):
-        gpu.in_context_dev(w, vm, h_dev.ptr, n, CLASSES, out_dev.ptr)
+        gpu.predict_dev(w, vm, x_dev.ptr, n, CLASSES, out_dev.ptr)
 
     # ---- the headline: batches of 2,048 rows --------------------------------------------------------------
     for _ in range(args.warmup):
@@ -85,7 +91,7 @@ def main():
     wall_ms = (time.perf_counter() - t0) * 1e3
     ms_step = max(ev_ms, wall_ms) / args.steps
     rows_s = BATCH / (ms_step / 1e3)
-    log(f"in-context stage, {BATCH} rows: {ms_step:.3f} ms/step, {rows_s:,.0f} rows/s")
+    log(f"prediction, {BATCH} rows: {ms_step:.3f} ms/step, {rows_s:,.0f} rows/s")
 
     # ---- other batch sizes -------------------------------------------------------------------------------
     per_batch = {}
@@ -99,8 +105,18 @@ def main():
             run(n)
         ms = timer.stop() / reps
         per_batch[str(n)] = round(n / (ms / 1e3), 1)
-        log(f"in-context stage, {n} rows: {ms:.3f} ms, {per_batch[str(n)]:,.0f} rows/s")
+        log(f"prediction, {n} rows: {ms:.3f} ms, {per_batch[str(n)]:,.0f} rows/s")
     per_batch[str(BATCH)] = round(rows_s, 1)
+
+    # ---- the in-context stage alone (row representations in, scores out) --------------------------------------
+    for _ in range(2):
+        gpu.in_context_dev(w, vm, h_dev.ptr, BATCH, CLASSES, out_dev.ptr)
+    gpu.sync()
+    timer.start()
+    for _ in range(args.steps):
+        gpu.in_context_dev(w, vm, h_dev.ptr, BATCH, CLASSES, out_dev.ptr)
+    icl_ms = timer.stop() / args.steps
+    log(f"in-context stage alone, {BATCH} rows: {icl_ms:.3f} ms")
 
     # ---- the dominant kernel: attention over one stored layer, 2,048 queries ---------------------------------
     q_dev = dm.DeviceBuffer.of((rng.standard_normal((BATCH, d)) * 0.1).astype(np.float32))
@@ -125,12 +141,16 @@ def main():
 
         threads = min(16, os.cpu_count() or 1)
         orc.set_threads(threads)
-        sample = 1024
+        sample = 512
+        planmod = importlib.import_module("tabicl-anywhere_amd.plan")
+        fitted = orc.Fitted(ROWS, FEATURES, CLASSES, CHUNK, abi.KV_F32,
+                            planmod.Plan([CLASSES], [planmod.Node(None, [], CLASSES, True, list(range(CLASSES)))]),
+                            col_kv, [scales], [layers])
         t0 = time.perf_counter()
-        orc.in_context(model, scales, layers, abi.KV_F32, ROWS, CHUNK, h_host[:sample], CLASSES)
+        orc.predict_raw(model, fitted, x_host[:sample])
         secs = time.perf_counter() - t0
         cpu = {"value": round(sample / secs, 2), "unit": "rows/s", "cores": threads, "kind": "port",
-               "sample": f"{sample} test rows through the in-context stage over the same 10,000-row f32 cache "
+               "sample": f"{sample} test rows through all three stages against the same caches "
                          f"(C restatement of the reference CPU path, {threads} OpenMP threads, {secs:.1f} s)"}
         log(f"cpu baseline: {cpu['value']} rows/s on {threads} threads")
 
@@ -146,12 +166,14 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic: random-init full-size TabICL v2 classifier weights (seed 2), random row representations "
-                "and a random stored f32 cache of the 10,000-row shape",
-        "config": {"workload": "in-context stage (12 layers + decoder) of 2,048 test rows over a 10,000-row f32 "
-                               "key/value cache, d=512, 8x64 heads, 10 classes",
-                   "train_rows": ROWS, "chunk": CHUNK, "test_rows": BATCH, "classes": CLASSES, "kv": "f32"},
+        "data": "synthetic: random-init full-size TabICL v2 classifier weights (seed 2), N(0,1) test rows, and random "
+                "stored f32 caches of the 10,000-row x 100-feature shape",
+        "config": {"workload": "predict 2,048 test rows x 100 features through the column, row and in-context stages "
+                               "against a 10,000-row f32 cache (d=512, 12 layers of 8x64 heads, 10 classes)",
+                   "train_rows": ROWS, "features": FEATURES, "chunk": CHUNK, "test_rows": BATCH, "classes": CLASSES,
+                   "kv": "f32"},
         "rows_per_s_by_batch": per_batch,
+        "in_context_stage_ms": round(icl_ms, 4),
         "fit_s": None,
         "roofline": {"bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": PEAK_F32_MFMA / 1e12,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_F32_MFMA, 4), "traffic": None,
@@ -159,7 +181,7 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
-    for b in (q_dev, att_dev, h_dev, out_dev):
+    for b in (q_dev, att_dev, h_dev, out_dev, x_dev):
         b.free()
     vm.free()
     w.free()

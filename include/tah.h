@@ -99,6 +99,8 @@ int tah_open(int32_t ordinal, tah_dev **out);
 void tah_close(tah_dev *dev);
 const char *tah_last_error(const tah_dev *dev);
 int tah_device_name(const tah_dev *dev, char *buf, size_t len);
+/* The working-memory budget (default 16 GiB): calls size their batches to it, and fail with TAH_E_BUDGET when
+ * even one row or one feature group would not fit. */
 int tah_set_work_budget(tah_dev *dev, size_t bytes);
 size_t tah_work_budget(const tah_dev *dev);
 int tah_working(const tah_dev *dev, size_t *now, size_t *peak);
@@ -167,6 +169,17 @@ int tah_pack(tah_dev *dev, const float *c, int32_t d, int32_t rc, int32_t kv_for
  * (2 * rows * d floats), out [rows][d] before the output projection. */
 int tah_attend(tah_dev *dev, const float *q, const float *kv, int32_t rows, int32_t chunk, int32_t d, int32_t heads,
                float *out);
+
+/* The column and row stages of a fit (Attend::columns and Attend::rows, src/fit.rs:54-65, the CPU loops at
+ * src/fit.rs:326-423 and 486-540), with the cells kept on the card between them. x [rows][features] (numeric,
+ * normalised), y [rows] (class index as a float, or the standardised target of a regression model), bases [digits]
+ * the label digits' bases (one digit: {classes}), ind_scales [col_blocks][e] each block's
+ * Block::query_scale(rows) for the inducing points' queries. Writes col_kv_out
+ * [features][digits][col_blocks][2][e][inds] and reps_out [rows][d]. Feature groups and rows go in batches that
+ * fit the working-memory budget. */
+int tah_fit_represent(tah_dev *dev, const tah_weights *w, const float *x, const float *y, int32_t rows,
+                      int32_t features, const int32_t *bases, int32_t digits, const float *ind_scales,
+                      float *col_kv_out, float *reps_out);
 
 /* Receives layer `layer`'s stored records (tah_kv_record summed over its chunks, in host memory valid for the
  * duration of the call) while the in-context stage is fitted; non-zero stops the fit with TAH_E_SINK. */

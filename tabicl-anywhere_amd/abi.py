@@ -105,6 +105,8 @@ SIGNATURES = {
                                         ctypes.c_int32, F32P]),
     "tah_predict_rows_dev": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                             ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
+    "tah_fit_represent": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, F32P, F32P, ctypes.c_int32, ctypes.c_int32,
+                                         ctypes.POINTER(ctypes.c_int32), ctypes.c_int32, F32P, F32P, F32P]),
     "tah_pack": (ctypes.c_int, [ctypes.c_void_p, F32P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, U8P]),
     "tah_attend": (ctypes.c_int, [ctypes.c_void_p, F32P, F32P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                   ctypes.c_int32, F32P]),

@@ -638,7 +638,7 @@ extern "C" int tah_model_set_columns(tah_dev *dev, tah_model *model, const tah_w
 }
 
 // cos and sin of position * frequency for T positions ([T][half]), as Rope::new (src/nn.rs:304-321), on the card.
-static float *rope_tables(tah_dev *dev, const tah_weights *w, int T, Loans &loans) {
+static const float *rope_tables(tah_dev *dev, const tah_weights *w, int T, Loans &loans) {
     const int half = w->rope_half;
     std::vector<float> freqs(half), tab(2 * (size_t)T * half);
     TAH_HIP(hipMemcpy(freqs.data(), w->rope_freqs, sizeof(float) * half, hipMemcpyDeviceToHost));
@@ -778,6 +778,130 @@ extern "C" int tah_predict_rows(tah_dev *dev, const tah_weights *w, const tah_mo
         predict_rows(dev, w, model, xd, n, out_n, od);
         TAH_HIP(hipMemcpyAsync(out, od, sizeof(float) * n * out_n, hipMemcpyDeviceToHost, dev->stream));
         TAH_HIP(hipStreamSynchronize(dev->stream));
+        return TAH_OK;
+    });
+}
+
+// ---- the column and row stages of a fit (Attend::columns + Attend::rows, cells kept on the card) -----------------
+extern "C" int tah_fit_represent(tah_dev *dev, const tah_weights *w, const float *x, const float *y, int32_t rows,
+                                 int32_t features, const int32_t *bases, int32_t digits, const float *ind_scales,
+                                 float *col_kv_out, float *reps_out) {
+    if (!w || !x || !y || !bases || !ind_scales || !col_kv_out || !reps_out) return TAH_E_ARG;
+    return guarded(dev, [&] {
+        if (rows <= 0 || features <= 0 || digits <= 0) throw ArgError{"fit: bad rows, features or digits"};
+        if (w->col_a1.empty() || w->col_a2.empty() || w->row.empty() || !w->col_ind || !w->col_scale)
+            throw ArgError{"fit: the weights lack the column or row stage (upload them with the fitting blocks)"};
+        for (int i = 0; i < digits; i++)
+            if (bases[i] <= 0) throw ArgError{"fit: label digit bases must be positive"};
+        const int e = w->e, inds = w->inds, nb = w->col_blocks, d = w->d;
+        const int T = w->cls + features;
+        const size_t per = 2 * (size_t)e * inds, gstride = (size_t)digits * nb * per;
+        hipStream_t s = dev->stream;
+        int ff = 0;
+        for (auto &b : w->col_a1) ff = std::max(ff, b.ff);
+        for (auto &b : w->col_a2) ff = std::max(ff, b.ff);
+        Loans keep(dev);
+        float *xd = keep.take<float>((size_t)rows * features), *yd = keep.take<float>(rows);
+        float *sc = keep.take<float>((size_t)nb * e), *indq = keep.take<float>((size_t)nb * inds * e);
+        float *it = keep.take<float>((size_t)inds * e);
+        float *col_kv = keep.take<float>((size_t)features * gstride);
+        float *emb = keep.take<float>((size_t)features * rows * e);
+        float *reps = keep.take<float>((size_t)rows * d);
+        TAH_HIP(hipMemcpyAsync(xd, x, sizeof(float) * rows * features, hipMemcpyHostToDevice, s));
+        TAH_HIP(hipMemcpyAsync(yd, y, sizeof(float) * rows, hipMemcpyHostToDevice, s));
+        TAH_HIP(hipMemcpyAsync(sc, ind_scales, sizeof(float) * nb * e, hipMemcpyHostToDevice, s));
+        // the inducing points' queries, once per block, scaled for all rows (src/fit.rs:300-313)
+        for (int bi = 0; bi < nb; bi++) {
+            const DevBlock &a1 = w->col_a1[bi];
+            float *qb = indq + (size_t)bi * inds * e;
+            layer_norm(s, inds, e, w->col_ind + (size_t)bi * inds * e, e, a1.n1w, a1.n1b, it, e);
+            gemm(s, inds, e, e, it, e, a1.in_w, a1.in_b, qb, e, EPI_NONE, nullptr, 0);
+            query_modulate(s, inds, a1, sc + (size_t)bi * e, qb);
+        }
+        // feature groups in batches that fit the working memory
+        auto group_bytes = [&](int gb) {
+            const size_t M = (size_t)gb * rows, I = (size_t)gb * inds;
+            const size_t f[] = {M * e, M * e, M * e, M * std::max<size_t>(ff, 2 * e), digits > 1 ? M * e : 0,
+                                digits > 1 ? M * e : 0, I * e, I * e, I * e, I * ff, I * 2 * e};
+            size_t b = ind_attention_work_bytes(w, rows, gb) + 256;
+            for (size_t v : f) b += align256(v * sizeof(float)) + 256;
+            return b;
+        };
+        size_t used = 0;
+        for (auto &b : dev->pool.bufs)
+            if (b.busy) used += b.bytes;
+        const size_t room = dev->pool.budget > used ? dev->pool.budget - used : 0;
+        int gb = features;
+        while (gb > 1 && group_bytes(gb) > room) gb = (gb + 1) / 2;
+        if (group_bytes(gb) > room) throw BudgetError{"graphics card: one feature group does not fit the working-memory budget"};
+        for (int g0 = 0; g0 < features; g0 += gb) {
+            const int g = std::min(gb, features - g0);
+            const size_t M = (size_t)g * rows, I = (size_t)g * inds;
+            Loans loans(dev);
+            float *cells = emb + (size_t)g0 * rows * e;
+            float *t = loans.take<float>(M * e), *q = loans.take<float>(M * e), *att = loans.take<float>(M * e);
+            float *mid = loans.take<float>(M * std::max<size_t>(ff, 2 * e));
+            float *plain = digits > 1 ? loans.take<float>(M * e) : nullptr;
+            float *sum = digits > 1 ? loans.take<float>(M * e) : nullptr;
+            float *acc = loans.take<float>(I * e), *hid = loans.take<float>(I * e), *ht = loans.take<float>(I * e);
+            float *hmid = loans.take<float>(I * ff), *kv2 = loans.take<float>(I * 2 * e);
+            void *work = loans.take<uint8_t>(ind_attention_work_bytes(w, rows, g));
+            fit_cells(s, w, xd, rows, features, g0, g, cells);
+            if (digits > 1) {
+                TAH_HIP(hipMemcpyAsync(plain, cells, M * e * sizeof(float), hipMemcpyDeviceToDevice, s));
+                TAH_HIP(hipMemsetAsync(sum, 0, M * e * sizeof(float), s));
+            }
+            for (int dg = 0; dg < digits; dg++) {
+                if (dg > 0) TAH_HIP(hipMemcpyAsync(cells, plain, M * e * sizeof(float), hipMemcpyDeviceToDevice, s));
+                int divisor = 1;
+                for (int k = dg + 1; k < digits; k++) divisor *= bases[k];
+                add_y_cells(s, w, yd, rows, g, digits, divisor, bases[dg], cells);
+                for (int bi = 0; bi < nb; bi++) {
+                    const DevBlock &a1 = w->col_a1[bi], &a2 = w->col_a2[bi];
+                    // the inducing points look at this batch's cells (src/fit.rs:366-392)
+                    layer_norm(s, (int)M, e, cells, e, a1.n1w, a1.n1b, t, e);
+                    gemm(s, (int)M, 2 * e, e, t, e, a1.in_w + (size_t)e * e, a1.in_b + e, mid, 2 * e, EPI_NONE, nullptr, 0);
+                    ind_attention(s, w, rows, g, indq + (size_t)bi * inds * e, mid, acc, work);
+                    gemm(s, (int)I, e, e, acc, e, a1.out_w, a1.out_b, hid, e, EPI_NONE, nullptr, 0);
+                    add_ind(s, I * e, inds, e, w->col_ind + (size_t)bi * inds * e, hid);
+                    layer_norm(s, (int)I, e, hid, e, a1.n2w, a1.n2b, ht, e);
+                    gemm(s, (int)I, a1.ff, e, ht, e, a1.l1w, a1.l1b, hmid, a1.ff, EPI_GELU, nullptr, 0);
+                    gemm(s, (int)I, e, a1.ff, hmid, a1.ff, a1.l2w, a1.l2b, hid, e, EPI_RESID, hid, e);
+                    // their keys and values for the second attention: what prediction reuses (src/fit.rs:393-403)
+                    layer_norm(s, (int)I, e, hid, e, a2.n1w, a2.n1b, ht, e);
+                    gemm(s, (int)I, 2 * e, e, ht, e, a2.in_w + (size_t)e * e, a2.in_b + e, kv2, 2 * e, EPI_NONE, nullptr, 0);
+                    const size_t off = ((size_t)dg * nb + bi) * per;
+                    col_records(s, g, inds, e, kv2, col_kv, gstride, off, g0);
+                    // every cell against them (src/fit.rs:404-406)
+                    column_block(s, w, a2, cells, rows, g, 1, rows, col_kv + (size_t)g0 * gstride + off, gstride, t, q, att, mid);
+                }
+                if (digits > 1) add_to(s, M * e, cells, sum);
+            }
+            if (digits > 1) scale_by(s, M * e, sum, 1.0f / (float)digits, cells);
+        }
+        // the row stage in batches of rows (src/fit.rs:516-539)
+        const float *tabs = rope_tables(dev, w, T, keep);
+        size_t used2 = 0;
+        for (auto &b : dev->pool.bufs)
+            if (b.busy) used2 += b.bytes;
+        const size_t room2 = dev->pool.budget > used2 ? dev->pool.budget - used2 : 0;
+        auto row_bytes = [&](int rb) {
+            return align256(sizeof(float) * (size_t)rb * T * e) + align256(sizeof(float) * row_stage_floats(w, rb, T)) + 512;
+        };
+        int rb = rows;
+        while (rb > 1 && row_bytes(rb) > room2) rb = (rb + 1) / 2;
+        if (row_bytes(rb) > room2) throw BudgetError{"graphics card: one row does not fit the working-memory budget"};
+        for (int r0 = 0; r0 < rows; r0 += rb) {
+            const int k = std::min(rb, rows - r0);
+            Loans loans(dev);
+            float *tok = loans.take<float>((size_t)k * T * e);
+            float *scratch = loans.take<float>(row_stage_floats(w, k, T));
+            tokens_gmajor(s, w, k, r0, rows, features, emb, tok);
+            row_stage(s, w, tok, k, T, tabs, tabs + (size_t)T * w->rope_half, reps + (size_t)r0 * d, scratch);
+        }
+        TAH_HIP(hipMemcpyAsync(col_kv_out, col_kv, sizeof(float) * features * gstride, hipMemcpyDeviceToHost, s));
+        TAH_HIP(hipMemcpyAsync(reps_out, reps, sizeof(float) * rows * d, hipMemcpyDeviceToHost, s));
+        TAH_HIP(hipStreamSynchronize(s));
         return TAH_OK;
     });
 }

@@ -428,6 +428,12 @@ __global__ __launch_bounds__(64) void k_attn_merge(int nq, int d, int heads, int
     }
 }
 
+void merge_splits(hipStream_t s, int nq, int d, int heads, int splits, const float *part_o, const float *part_ml,
+                  float *out) {
+    hipLaunchKernelGGL(k_attn_merge, dim3(nq * heads), dim3(64), 0, s, nq, d, heads, splits, part_o, part_ml, out);
+    TAH_LAUNCHED();
+}
+
 // ---- planning and launch --------------------------------------------------------------------------------------
 struct AttnPlan {
     bool mfma;

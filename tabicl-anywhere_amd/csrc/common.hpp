@@ -45,23 +45,13 @@ struct Pool {
         bool busy;
     };
     std::vector<Buf> bufs;
-    size_t budget = size_t(1536) << 20;
+    size_t budget = size_t(16) << 30;  // MI355X holds 288 GB of HBM; the reference's 1.5 GB suits 24 GB cards
     size_t bytes = 0, peak = 0, overdrawn = 0;
 
     void *take(size_t bytes, int device);
     void give(void *p);
     void release_idle();
 };
-
-// Column and row stages (stages.hip).
-void input_cells(hipStream_t s, const tah_weights *w, const float *x, int n, int features, float *cells);
-size_t column_stage_floats(const tah_weights *w, int n, int features, int digits);
-void column_stage(hipStream_t s, const tah_weights *w, const float *col_kv, int digits, const float *x, int n,
-                  int features, float *cells, float *scratch);
-void assemble_tokens(hipStream_t s, const tah_weights *w, const float *cells, int n, int features, float *tok);
-size_t row_stage_floats(const tah_weights *w, int n, int T);
-void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, const float *cosv, const float *sinv,
-               float *rep, float *scratch);
 
 }  // namespace tah
 
@@ -144,5 +134,20 @@ void assemble_tokens(hipStream_t s, const tah_weights *w, const float *cells, in
 size_t row_stage_floats(const tah_weights *w, int n, int T);
 void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, const float *cosv, const float *sinv,
                float *rep, float *scratch);
+void column_block(hipStream_t s, const tah_weights *w, const DevBlock &b, float *cells, int n, int groups, size_t sr,
+                  size_t sg, const float *kvbase, size_t gstride, float *t, float *q, float *att, float *mid);
+
+// The column stage of a fit (fit_stages.hip).
+void fit_cells(hipStream_t s, const tah_weights *w, const float *x, int rows, int features, int g0, int gb, float *cells);
+void add_y_cells(hipStream_t s, const tah_weights *w, const float *y, int rows, int gb, int digits, int divisor, int base,
+                 float *cells);
+void scale_by(hipStream_t s, size_t count, const float *src, float f, float *dst);
+void add_to(hipStream_t s, size_t count, const float *x, float *sum);
+void add_ind(hipStream_t s, size_t count, int inds, int e, const float *ind, float *hid);
+void col_records(hipStream_t s, int gb, int inds, int e, const float *kv2, float *col_kv, size_t gstride, size_t off, int g0);
+void tokens_gmajor(hipStream_t s, const tah_weights *w, int rb, int r0, int rows, int features, const float *emb, float *tok);
+size_t ind_attention_work_bytes(const tah_weights *w, int rows, int gb);
+void ind_attention(hipStream_t s, const tah_weights *w, int rows, int gb, const float *indq, const float *kv, float *out,
+                   void *work);
 
 }  // namespace tah

@@ -43,10 +43,11 @@ __global__ __launch_bounds__(256) void k_input_cells(int n, int features, int gr
 }
 
 // ---- cells against a group's inducing points: head width 16, 16 * NT keys ----------------------------------------
-// grid (tiles of 64 rows, heads, groups); 256 threads. q and out are [n * features][e] (cell (r, g) at r*features+g);
-// group g's keys and values are K = kvbase + g * gstride ([e][inds]) and V = K + e * inds.
+// grid (tiles of 64 rows, heads, groups); 256 threads. q and out hold cell (r, g) at row r * sr + g * sg of e
+// numbers ([n][features][e] at prediction, [groups][rows][e] at fit); group g's keys and values are
+// K = kvbase + g * gstride ([e][inds]) and V = K + e * inds.
 template <int NT>
-__global__ __launch_bounds__(256) void k_cell_attn16(int n, int features, int e, const float *__restrict__ q,
+__global__ __launch_bounds__(256) void k_cell_attn16(int n, size_t sr, size_t sg, int e, const float *__restrict__ q,
                                                       const float *__restrict__ kvbase, size_t gstride,
                                                       float *__restrict__ out) {
     constexpr int INDS = 16 * NT;
@@ -63,7 +64,7 @@ __global__ __launch_bounds__(256) void k_cell_attn16(int n, int features, int e,
     __syncthreads();
     const int r = blockIdx.x * 64 + wave * 16 + r16;
     const bool live = r < n;
-    const size_t m = (size_t)r * features + g;
+    const size_t m = (size_t)r * sr + (size_t)g * sg;
     float4 qv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (live) qv = *reinterpret_cast<const float4 *>(q + m * e + h * 16 + 4 * g4);
     const float qa[4] = {qv.x, qv.y, qv.z, qv.w};
@@ -107,14 +108,16 @@ __global__ __launch_bounds__(256) void k_cell_attn16(int n, int features, int e,
 }
 
 // Any head width and key count (the tiny test models): one thread per (cell, head).
-__global__ __launch_bounds__(256) void k_cell_attn_plain(int n, int features, int e, int heads, int inds,
-                                                          const float *__restrict__ q, const float *__restrict__ kvbase,
-                                                          size_t gstride, float *__restrict__ out) {
+__global__ __launch_bounds__(256) void k_cell_attn_plain(int n, int groups, size_t sr, size_t sg, int e, int heads,
+                                                          int inds, const float *__restrict__ q,
+                                                          const float *__restrict__ kvbase, size_t gstride,
+                                                          float *__restrict__ out) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (size_t)n * features * heads) return;
+    if (i >= (size_t)n * groups * heads) return;
     const int h = (int)(i % heads);
-    const size_t m = i / heads;
-    const int g = (int)(m % features), hd = e / heads;
+    const size_t cell = i / heads;
+    const int g = (int)(cell % groups), hd = e / heads;
+    const size_t m = (cell / groups) * sr + (size_t)g * sg;
     const float *K = kvbase + (size_t)g * gstride, *V = K + (size_t)e * inds;
     const float *qr = q + m * e + h * hd;
     float mx = -INFINITY;
@@ -303,29 +306,24 @@ void input_cells(hipStream_t s, const tah_weights *w, const float *x, int n, int
     TAH_LAUNCHED();
 }
 
-// One column block (cached_block with a2) for all cells [n * features][e] in place: K/V of group g at
-// kvbase + g * gstride.
-void column_block(hipStream_t s, const tah_weights *w, const DevBlock &b, float *cells, int n, int features,
-                  const float *kvbase, size_t gstride, float *t, float *q, float *att, float *mid) {
+// One column block (cached_block with a2) for all cells in place: n rows x groups, cell (r, g) at row r * sr + g * sg
+// of cells; K/V of group g at kvbase + g * gstride.
+void column_block(hipStream_t s, const tah_weights *w, const DevBlock &b, float *cells, int n, int groups, size_t sr,
+                  size_t sg, const float *kvbase, size_t gstride, float *t, float *q, float *att, float *mid) {
     const int e = w->e;
-    const int M = n * features;
+    const int M = n * groups;
     layer_norm(s, M, e, cells, e, b.n1w, b.n1b, t, e);
     gemm(s, M, e, e, t, e, b.in_w, b.in_b, q, e, EPI_NONE, nullptr, 0);
     query_modulate(s, M, b, w->col_scale, q);
     const int hd = e / b.heads;
-    if (hd == 16 && w->inds % 16 == 0 && w->inds <= 256) {
-        dim3 grid((n + 63) / 64, b.heads, features);
-        switch (w->inds / 16) {
-            case 8: hipLaunchKernelGGL(k_cell_attn16<8>, grid, dim3(256), 0, s, n, features, e, q, kvbase, gstride, att); break;
-            case 16: hipLaunchKernelGGL(k_cell_attn16<16>, grid, dim3(256), 0, s, n, features, e, q, kvbase, gstride, att); break;
-            default:
-                hipLaunchKernelGGL(k_cell_attn_plain, blocks_for((size_t)M * b.heads), dim3(256), 0, s, n, features, e,
-                                   b.heads, w->inds, q, kvbase, gstride, att);
-        }
-    } else {
-        hipLaunchKernelGGL(k_cell_attn_plain, blocks_for((size_t)M * b.heads), dim3(256), 0, s, n, features, e, b.heads,
-                           w->inds, q, kvbase, gstride, att);
-    }
+    const dim3 grid((n + 63) / 64, b.heads, groups);
+    if (hd == 16 && w->inds == 128)
+        hipLaunchKernelGGL(k_cell_attn16<8>, grid, dim3(256), 0, s, n, sr, sg, e, q, kvbase, gstride, att);
+    else if (hd == 16 && w->inds == 256)
+        hipLaunchKernelGGL(k_cell_attn16<16>, grid, dim3(256), 0, s, n, sr, sg, e, q, kvbase, gstride, att);
+    else
+        hipLaunchKernelGGL(k_cell_attn_plain, blocks_for((size_t)M * b.heads), dim3(256), 0, s, n, groups, sr, sg, e,
+                           b.heads, w->inds, q, kvbase, gstride, att);
     TAH_LAUNCHED();
     gemm(s, M, e, e, att, e, b.out_w, b.out_b, cells, e, EPI_RESID, cells, e);
     layer_norm(s, M, e, cells, e, b.n2w, b.n2b, t, e);
@@ -353,7 +351,8 @@ void column_stage(hipStream_t s, const tah_weights *w, const float *col_kv, int 
     const size_t per = 2 * (size_t)e * w->inds, gstride = (size_t)digits * nb * per;
     input_cells(s, w, x, n, features, cells);
     if (digits == 1) {
-        for (int bi = 0; bi < nb; bi++) column_block(s, w, w->col_a2[bi], cells, n, features, col_kv + bi * per, gstride, t, q, att, mid);
+        for (int bi = 0; bi < nb; bi++)
+            column_block(s, w, w->col_a2[bi], cells, n, features, features, 1, col_kv + bi * per, gstride, t, q, att, mid);
         return;
     }
     const size_t count = M * e;
@@ -362,7 +361,8 @@ void column_stage(hipStream_t s, const tah_weights *w, const float *col_kv, int 
     for (int dg = 0; dg < digits; dg++) {
         if (dg > 0) TAH_HIP(hipMemcpyAsync(cells, plain, count * sizeof(float), hipMemcpyDeviceToDevice, s));
         for (int bi = 0; bi < nb; bi++)
-            column_block(s, w, w->col_a2[bi], cells, n, features, col_kv + ((size_t)dg * nb + bi) * per, gstride, t, q, att, mid);
+            column_block(s, w, w->col_a2[bi], cells, n, features, features, 1, col_kv + ((size_t)dg * nb + bi) * per, gstride,
+                         t, q, att, mid);
         hipLaunchKernelGGL(k_accumulate, blocks_for(count), dim3(256), 0, s, count, cells, sum);
         TAH_LAUNCHED();
     }

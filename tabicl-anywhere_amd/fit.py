@@ -1,0 +1,129 @@
+"""Fitting on the card: the reference's `fit_raw_async` (`src/fit.rs:285-752`) with every stage handed to the
+accelerator, as its `fit::Attend` hooks allow (`columns`, `rows`, `in_context`).
+
+The host keeps the reference's host-side work: the label-digit plan and class tree (`Plan`, `src/fit.rs:159-215`),
+each block's query scale (`Block::query_scale`, `src/nn.rs:97-107`, restated here in float32 with the reference's
+own exp and erf polynomials, `src/kern.rs:185-253`), gathering each in-context problem's rows and adding the
+target's embedding (`src/fit.rs:577-585`). The card does the column and row stages (`tah_fit_represent`) and each
+problem's in-context stage (`tah_in_context`), which hands back every layer's stored chunk records.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import abi
+from .plan import Plan, parse_tree
+
+F = np.float32
+
+
+def exp1(x: np.ndarray) -> np.ndarray:
+    """`kern::exp1` (`src/kern.rs:185-206`) in float32."""
+    x = np.clip(np.asarray(x, F), F(-87.0), F(88.0))
+    n = np.floor(x * F(1.44269504088896340736) + F(0.5))
+    r = (x - n * F(0.6933594)) - n * F(-2.1219444e-4)
+    p = F(1.0) / F(5040.0)
+    for c in (F(1.0) / F(720.0), F(1.0) / F(120.0), F(1.0) / F(24.0), F(1.0) / F(6.0), F(0.5), F(1.0), F(1.0)):
+        p = p * r + c
+    two = ((n.astype(np.int32) + 127) << 23).astype(np.int32).view(F)
+    return (p * two).astype(F)
+
+
+def erf1(x: np.ndarray) -> np.ndarray:
+    """`kern::erf1` (`src/kern.rs:227-253`): Abramowitz and Stegun 7.1.26 away from zero, a series near it."""
+    x = np.asarray(x, F)
+    a = np.abs(x)
+    t = F(1.0) / (F(1.0) + F(0.3275911) * a)
+    p = F(1.0614054)
+    for c in (F(-1.4531521), F(1.4214138), F(-0.28449674), F(0.2548296)):
+        p = p * t + c
+    far = np.copysign(F(1.0) - p * t * exp1(-a * a), x)
+    x2 = x * x
+    q = F(-1.0) / F(1320.0)
+    for c in (F(1.0) / F(216.0), F(-1.0) / F(42.0), F(0.1), F(-1.0) / F(3.0), F(1.0)):
+        q = q * x2 + c
+    near = q * x * F(1.12837916709551257390)
+    return np.where(a < F(0.5), near, far).astype(F)
+
+
+def gelu(x: np.ndarray) -> np.ndarray:
+    x = np.asarray(x, F)
+    return (F(0.5) * x * (F(1.0) + erf1(x * F(0.70710678118654752440)))).astype(F)
+
+
+def query_scale(block, n: int) -> np.ndarray:
+    """`Block::query_scale` (`src/nn.rs:97-107`): what every query of the block is multiplied by with n keys."""
+    inv = F(1.0) / np.sqrt(F(block.hd))
+    if block.ss_hidden == 0:
+        return np.full(block.d, inv, F)
+    logn = np.log(F(max(n, 1)))
+    hid = gelu(block.t["b0w"] * logn + block.t["b0b"])
+    w2 = block.t["b2w"].reshape(block.d, block.ss_hidden)
+    out = np.empty(block.d, F)
+    for o in range(block.d):  # sequential sums, as the reference's matvec rows
+        s = F(0.0)
+        for j in range(block.ss_hidden):
+            s = F(s + w2[o, j] * hid[j])
+        out[o] = s + block.t["b2b"][o]
+    return (out * inv).astype(F)
+
+
+@dataclass
+class Fitted:
+    """One fitted member, as `raw_entries` (`src/fit.rs:224-241`) names its tensors: `meta`, `tree`, `col_kv`,
+    and per in-context problem `n{j}_scale` and `n{j}_kv{l}`."""
+    rows: int
+    features: int
+    classes: int
+    chunk: int
+    kv_format: int
+    plan: Plan
+    col_kv: np.ndarray
+    scales: list = field(default_factory=list)
+    layers: list = field(default_factory=list)
+
+    @property
+    def digits(self) -> int:
+        return len(self.plan.bases)
+
+    @property
+    def nodes(self):
+        return parse_tree(self.plan.tree(self.rows), len(self.plan.nodes))
+
+    def meta(self) -> np.ndarray:
+        return np.array([self.rows, self.features, self.classes, self.chunk, self.kv_format, self.digits,
+                         len(self.plan.nodes)], np.int32)
+
+
+def fit_raw(gpu, weights, x, y, classes: int, chunk: int = 256, kv_format: int = abi.KV_F32) -> Fitted:
+    """Fit one table that is already numeric and normalised (`x [rows][features]`, `y` class indices or
+    standardised targets) with every stage on the card."""
+    m = weights.model
+    x = np.ascontiguousarray(x, F)
+    y = np.ascontiguousarray(y, F)
+    rows, features = x.shape
+    chunk = max(int(chunk), 8)
+    plan = Plan.new(m.max_classes, y, classes)
+    digits = len(plan.bases)
+    ind_scales = np.stack([query_scale(b, rows) for b in m.col_a1]).astype(F)
+    col_kv = np.empty((features, digits, len(m.col_a2), 2, m.e, m.inds), F)
+    reps = np.empty((rows, m.d), F)
+    bases = (ctypes.c_int32 * digits)(*plan.bases)
+    gpu._check(gpu._l.tah_fit_represent(gpu._h, weights._h, x.ctypes.data_as(abi.F32P), y.ctypes.data_as(abi.F32P),
+                                        rows, features, bases, digits, ind_scales.ctypes.data_as(abi.F32P),
+                                        col_kv.ctypes.data_as(abi.F32P), reps.ctypes.data_as(abi.F32P)))
+    fitted = Fitted(rows, features, classes, chunk, kv_format, plan, col_kv)
+    for node in plan.nodes:
+        n_rows = rows if node.rows is None else len(node.rows)
+        h = reps if node.rows is None else reps[np.asarray(node.rows, np.int64)]
+        h = np.array(h, F, copy=True)
+        m.add_y(m.t["icl_y"], np.asarray(node.y, F), h)
+        scales = np.stack([query_scale(b, n_rows) for b in m.icl]).astype(F)
+        layers = []
+        gpu.in_context_fit(weights, h, scales, kv_format, chunk, lambda l, rec: layers.append(rec.copy()))
+        fitted.scales.append(scales)
+        fitted.layers.append(layers)
+    return fitted
