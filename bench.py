@@ -1,13 +1,18 @@
-"""Benchmark: predicted rows/s on one MI355X against a 10,000-row x 100-feature fitted cache.
+"""Benchmark: fit a 10,000-row x 100-feature table on one MI355X, then predict rows/s against its cache.
 
-Workload: the full-size TabICL v2 classifier architecture (e = 128, 3 column blocks of 8 x 16 heads over 128
-inducing points, 3 row blocks, d = 512, 12 in-context layers of 8 heads x 64, decoder 1024 -> 10), random-init
-weights from seed 2, a stored f32 cache of 10,000 training rows (chunks of 256, the last of 16) and its column cache
-for 100 features. A step is one prediction pass of a batch of 2,048 test rows of 100 features through all three
-stages (column, row, in-context + decoder), inputs already resident in HBM. Also reported: rows/s at batches of 1,
-64 and 256, the in-context stage alone, the attention kernel's share of the fp32 MFMA roofline (measured with HIP
-events on the library's stream), and the oracle (the C restatement of the reference's CPU path) timed on this
-host's cores on a bounded sample of the same workload.
+Workload (the full-size TabICL v2 classifier architecture with random-init weights from seed 2: e = 128, 3 column
+blocks of 8 x 16 heads over 128 inducing points, 3 row blocks, d = 512, 12 in-context layers of 8 x 64 heads,
+decoder 1024 -> 10). Synthetic table: X ~ N(0, 1) of 10,000 training + 2,048 test rows x 100 features (seed 3);
+10 classes, y = argmax(X W + Gumbel noise) with W ~ N(0, 1) (seed 4). One member, f32 cache, chunks of 256 rows.
+
+* fit_s: the whole fit on the card (column, row and in-context stages; every layer's stored records back on the
+  host), wall clock, after one warm-up fit.
+* value: a step is one prediction pass of 2,048 test rows through all three stages against the fitted caches,
+  inputs already resident in HBM; rows/s. Also batches of 1, 64 and 256 rows and the in-context stage alone.
+* roofline: the dominant kernel, the in-context attention (2,048 queries over 10,000 keys, 8 heads of 64), timed
+  with HIP events on the library's stream, against the fp32 MFMA peak.
+* cpu_baseline: the oracle (the C restatement of the reference's CPU path) on this host's cores, predicting a
+  bounded sample of the same test rows against the same caches; and a bounded fit sample timed on both.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 """
@@ -25,18 +30,20 @@ sys.path.insert(0, ROOT)
 
 ROWS, FEATURES, CHUNK, BATCH, CLASSES = 10000, 100, 256, 2048, 10
 PEAK_F32_MFMA = 157.3e12  # MI355X dense fp32 matrix FLOP/s
-PEAK_HBM = 8.0e12
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def synthetic_cache(rng, layers, d):
-    """Stored f32 layers of the exact shape a 10,000-row fit writes (values N(0, 0.5^2))."""
-    nbytes = (ROWS // CHUNK) * 8 * d * CHUNK + (8 * d * (ROWS % CHUNK) if ROWS % CHUNK else 0)
-    one = (rng.standard_normal(nbytes // 4) * 0.5).astype(np.float32).view(np.uint8)
-    return [one.copy() for _ in range(layers)]
+def table(rows, features, classes, seed_x=3, seed_w=4):
+    rx = np.random.default_rng(seed_x)
+    x = rx.standard_normal((rows, features)).astype(np.float32)
+    rw = np.random.default_rng(seed_w)
+    w = rw.standard_normal((features, classes))
+    g = rw.gumbel(size=(rows, classes))
+    y = np.argmax(x.astype(np.float64) @ w + g, axis=1).astype(np.float32)
+    return x, y
 
 
 def main():
@@ -55,22 +62,26 @@ def main():
     M = importlib.import_module("tabicl-anywhere_amd.model")
     hip = importlib.import_module("tabicl-anywhere_amd.hip")
     dm = importlib.import_module("tabicl-anywhere_amd.devmem")
+    fitmod = importlib.import_module("tabicl-anywhere_amd.fit")
 
-    rng = np.random.default_rng(3)
     model = M.Model.random(M.FULL_CLASSIFIER, seed=2)
     d, L, heads = model.d, model.icl_layers, model.icl_heads
-    layers = synthetic_cache(rng, L, d)
-    scales = np.full((L, d), 1.0 / 8.0, np.float32)
+    x_all, y_all = table(ROWS + BATCH, FEATURES, CLASSES)
+    x_train, y_train, x_test = x_all[:ROWS], y_all[:ROWS], x_all[ROWS:]
     gpu = hip.Gpu(0)
     log("device:", gpu.name)
     w = gpu.weights(model)
-    vm = gpu.load(w, abi.KV_F32, ROWS, CHUNK, layers, scales)
-    col_kv = (rng.standard_normal((FEATURES, 1, len(model.col_a2), 2, model.e, model.inds)) * 0.5).astype(np.float32)
-    vm.set_columns(col_kv, FEATURES, 1)
-    x_host = rng.standard_normal((BATCH, FEATURES)).astype(np.float32)
-    x_dev = dm.DeviceBuffer.of(x_host)
-    h_host = rng.standard_normal((BATCH, d)).astype(np.float32)
-    h_dev = dm.DeviceBuffer.of(h_host)
+
+    # ---- fit on the card ------------------------------------------------------------------------------------
+    fitmod.fit_raw(gpu, w, x_train[:1000], y_train[:1000], CLASSES, CHUNK)  # warm-up (kernels loaded, pool grown)
+    t0 = time.perf_counter()
+    fitted = fitmod.fit_raw(gpu, w, x_train, y_train, CLASSES, CHUNK, abi.KV_F32)
+    fit_s = time.perf_counter() - t0
+    log(f"fit {ROWS} x {FEATURES} on the card: {fit_s:.3f} s")
+
+    vm = gpu.load(w, abi.KV_F32, ROWS, CHUNK, fitted.layers[0], fitted.scales[0])
+    vm.set_columns(fitted.col_kv, FEATURES, 1)
+    x_dev = dm.DeviceBuffer.of(x_test)
     out_dev = dm.DeviceBuffer(BATCH * CLASSES * 4)
     timer = dm.EventTimer(gpu.stream)
 
@@ -108,7 +119,9 @@ def main():
         log(f"prediction, {n} rows: {ms:.3f} ms, {per_batch[str(n)]:,.0f} rows/s")
     per_batch[str(BATCH)] = round(rows_s, 1)
 
-    # ---- the in-context stage alone (row representations in, scores out) --------------------------------------
+    # ---- the in-context stage alone and its attention kernel ---------------------------------------------------
+    rng = np.random.default_rng(5)
+    h_dev = dm.DeviceBuffer.of(rng.standard_normal((BATCH, d)).astype(np.float32))
     for _ in range(2):
         gpu.in_context_dev(w, vm, h_dev.ptr, BATCH, CLASSES, out_dev.ptr)
     gpu.sync()
@@ -117,8 +130,6 @@ def main():
         gpu.in_context_dev(w, vm, h_dev.ptr, BATCH, CLASSES, out_dev.ptr)
     icl_ms = timer.stop() / args.steps
     log(f"in-context stage alone, {BATCH} rows: {icl_ms:.3f} ms")
-
-    # ---- the dominant kernel: attention over one stored layer, 2,048 queries ---------------------------------
     q_dev = dm.DeviceBuffer.of((rng.standard_normal((BATCH, d)) * 0.1).astype(np.float32))
     att_dev = dm.DeviceBuffer(BATCH * d * 4)
     for l in range(2):
@@ -133,26 +144,42 @@ def main():
     achieved = flops / (att_ms / 1e3)
     log(f"attention, {BATCH} queries x {ROWS} keys x {heads} heads: {att_ms:.3f} ms, {achieved / 1e12:.1f} TFLOP/s")
 
-    # ---- CPU baseline: the oracle on a bounded sample of the same workload -----------------------------------
-    cpu = None
+    # a plain 256 MiB device-to-device copy: the known-size reference that the memory counters of a profile of
+    # this run are scaled by (profiles/README.md)
+    cal_a, cal_b = dm.DeviceBuffer(256 << 20), dm.DeviceBuffer(256 << 20)
+    dm.copy(cal_b, cal_a, 256 << 20)
+    dm.synchronize()
+    cal_a.free()
+    cal_b.free()
+
+    # ---- CPU baseline: the oracle on bounded samples of the same workload ------------------------------------
+    cpu, fit_sample = None, None
     if not args.no_cpu:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import oracle as orc
 
         threads = min(16, os.cpu_count() or 1)
         orc.set_threads(threads)
-        sample = 512
-        planmod = importlib.import_module("tabicl-anywhere_amd.plan")
-        fitted = orc.Fitted(ROWS, FEATURES, CLASSES, CHUNK, abi.KV_F32,
-                            planmod.Plan([CLASSES], [planmod.Node(None, [], CLASSES, True, list(range(CLASSES)))]),
-                            col_kv, [scales], [layers])
+        sample = 256
         t0 = time.perf_counter()
-        orc.predict_raw(model, fitted, x_host[:sample])
+        want = orc.predict_raw(model, fitted, x_test[:sample])
         secs = time.perf_counter() - t0
+        got = gpu.predict(w, vm, x_test[:sample], CLASSES)
         cpu = {"value": round(sample / secs, 2), "unit": "rows/s", "cores": threads, "kind": "port",
-               "sample": f"{sample} test rows through all three stages against the same caches "
-                         f"(C restatement of the reference CPU path, {threads} OpenMP threads, {secs:.1f} s)"}
+               "sample": f"{sample} of the test rows through all three stages against the card-fitted caches (C "
+                         f"restatement of the reference CPU path, {threads} OpenMP threads, {secs:.1f} s; largest "
+                         f"score difference to the card {np.abs(got - want).max():.1e})"}
         log(f"cpu baseline: {cpu['value']} rows/s on {threads} threads")
+        fr = 1000
+        t0 = time.perf_counter()
+        orc.fit_raw(model, x_train[:fr], y_train[:fr], CLASSES, CHUNK)
+        cpu_fit = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        fitmod.fit_raw(gpu, w, x_train[:fr], y_train[:fr], CLASSES, CHUNK)
+        gpu_fit = time.perf_counter() - t0
+        fit_sample = {"rows": fr, "features": FEATURES, "cpu_s": round(cpu_fit, 3), "gpu_s": round(gpu_fit, 4),
+                      "cores": threads, "kind": "port"}
+        log(f"fit sample {fr} x {FEATURES}: cpu {cpu_fit:.2f} s, card {gpu_fit:.3f} s")
 
     line = {
         "metric": "predicted rows/s at 10k x 100 cache (1/64/2048 rows); % roofline; fit s",
@@ -166,19 +193,21 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic: random-init full-size TabICL v2 classifier weights (seed 2), N(0,1) test rows, and random "
-                "stored f32 caches of the 10,000-row x 100-feature shape",
-        "config": {"workload": "predict 2,048 test rows x 100 features through the column, row and in-context stages "
-                               "against a 10,000-row f32 cache (d=512, 12 layers of 8x64 heads, 10 classes)",
+        "data": "synthetic: N(0,1) table of 10,000 + 2,048 rows x 100 features, 10 classes from argmax of a random "
+                "projection plus Gumbel noise; random-init full-size TabICL v2 classifier weights (seed 2); the "
+                "caches predicted against are those the card fitted",
+        "config": {"workload": "fit 10,000 x 100 on the card, then predict 2,048 test rows through the column, row "
+                               "and in-context stages (f32 cache, d=512, 12 layers of 8x64 heads, 10 classes)",
                    "train_rows": ROWS, "features": FEATURES, "chunk": CHUNK, "test_rows": BATCH, "classes": CLASSES,
-                   "kv": "f32"},
+                   "kv": "f32", "members": 1},
         "rows_per_s_by_batch": per_batch,
         "in_context_stage_ms": round(icl_ms, 4),
-        "fit_s": None,
+        "fit_s": round(fit_s, 4),
         "roofline": {"bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": PEAK_F32_MFMA / 1e12,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_F32_MFMA, 4), "traffic": None,
                      "kernel": "k_attn_mfma64 (+ split merge)", "ms_per_launch": round(att_ms, 4)},
         "cpu_baseline": cpu,
+        "fit_sample": fit_sample,
     }
     print(json.dumps(line), flush=True)
     for b in (q_dev, att_dev, h_dev, out_dev, x_dev):

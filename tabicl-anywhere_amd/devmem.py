@@ -100,5 +100,11 @@ class EventTimer:
         return float(ms.value)
 
 
+def copy(dst: DeviceBuffer, src: DeviceBuffer, nbytes: int) -> None:
+    """Device-to-device copy of nbytes (hipMemcpy, kind device-to-device)."""
+    assert nbytes <= dst.nbytes and nbytes <= src.nbytes
+    _ok(rt().hipMemcpy(ctypes.c_void_p(dst.ptr), ctypes.c_void_p(src.ptr), nbytes, 3), "hipMemcpy")
+
+
 def synchronize() -> None:
     _ok(rt().hipDeviceSynchronize(), "hipDeviceSynchronize")
