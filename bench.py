@@ -30,6 +30,9 @@ sys.path.insert(0, ROOT)
 
 ROWS, FEATURES, CHUNK, BATCH, CLASSES = 10000, 100, 256, 2048, 10
 PEAK_F32_MFMA = 157.3e12  # MI355X dense fp32 matrix FLOP/s
+# HBM bytes per launch of the roofline kernel, from rocprofv3 FETCH_SIZE and WRITE_SIZE runs of this bench scaled by
+# the counters' reading on its own 256 MiB copy (profiles/attention_f32_2048x10000_memory.md)
+TRAFFIC_BYTES = 358.2e6
 
 
 def log(*a):
@@ -204,7 +207,7 @@ def main():
         "in_context_stage_ms": round(icl_ms, 4),
         "fit_s": round(fit_s, 4),
         "roofline": {"bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": PEAK_F32_MFMA / 1e12,
-                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_F32_MFMA, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_F32_MFMA, 4), "traffic": TRAFFIC_BYTES,
                      "kernel": "k_attn_mfma64 (+ split merge)", "ms_per_launch": round(att_ms, 4)},
         "cpu_baseline": cpu,
         "fit_sample": fit_sample,
