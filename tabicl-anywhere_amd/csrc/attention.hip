@@ -9,7 +9,7 @@
 // (Soft::merge, src/nn.rs:261-276) and divided through (Soft::finish).
 //
 // Two kernels:
-//  * k_attn_mfma64: head width 64 and at least 64 queries. 4 wavefronts x 16 queries share LDS tiles of K and V
+//  * k_attn_mfma64: head width 64 and at least 32 queries. 4 wavefronts x 32 queries share LDS tiles of K and V
 //    (64 coordinates x 64 keys). Scores are formed transposed, S^T = K Q^T, with v_mfma_f32_16x16x4_f32 so that
 //    each lane owns one query (lane % 16) in both products; the softmax then needs only two cross-lane steps, and
 //    O^T = V^T P^T takes each lane's own weights as its B operand with no transpose through LDS.
@@ -120,125 +120,175 @@ __device__ __forceinline__ void load16(const uint8_t *rec, int d, int rc, int c,
 }
 
 // ---- MFMA kernel: head width 64 ------------------------------------------------------------------------------
-// grid (query tiles of 64, heads, splits); 256 threads.
+// A flat grid of qtiles x heads x splits workgroups of 256 threads; each workgroup attends 128 queries (4 wavefronts
+// x 2 groups of 16) of one head to one key range. Each wavefront owns two query groups so that every K or V value
+// it reads from LDS feeds two MFMAs (LDS bandwidth, not the matrix cores, bounded the one-group form). The flat
+// index is remapped so that the query tiles sharing a (head, key range) run on the same XCD: workgroup i is
+// dispatched to XCD i % 8, and the tiles of one (head, range) then read the same K/V tiles through one L2.
+constexpr int QW = 2;  // query groups of 16 per wavefront
+
 template <int FMT>
 __global__ __launch_bounds__(256) void k_attn_mfma64(int nq, int rows, int chunk, int d, int heads,
                                                       const float *__restrict__ q, const uint8_t *__restrict__ records,
-                                                      int kb_per_split, float *__restrict__ part_o,
-                                                      float *__restrict__ part_ml, float *__restrict__ out) {
+                                                      int kb_per_split, int qtiles, int splits,
+                                                      float *__restrict__ part_o, float *__restrict__ part_ml,
+                                                      float *__restrict__ out) {
     __shared__ float Ks[64][KP];
     __shared__ float Vs[64][KP];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int h = blockIdx.y, split = blockIdx.z, splits = gridDim.z;
+    const int total = qtiles * heads * splits;
+    int flat = blockIdx.x;
+    if (total % 8 == 0) flat = (flat % 8) * (total / 8) + flat / 8;
+    const int qt = flat % qtiles, pair = flat / qtiles;
+    const int h = pair % heads, split = pair / heads;
     const KeyBlocks kbs = key_blocks(rows, chunk);
     const int kb0 = split * kb_per_split, kb1 = min(kbs.n_kb, kb0 + kb_per_split);
     const int r16 = lane & 15, g4 = lane >> 4;
-    const int qrow = blockIdx.x * 64 + wave * 16 + r16;
-    const bool qlive = qrow < nq;
-
+    int qrow[QW];
+    bool qlive[QW];
     // this lane's query coordinates: c = 16 cs + 4 g4 + t for cs, t in 0..3
-    float qreg[16];
+    float qreg[QW][16];
 #pragma unroll
-    for (int cs = 0; cs < 4; cs++) {
-        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (qlive) v = *reinterpret_cast<const float4 *>(q + (size_t)qrow * d + h * 64 + 16 * cs + 4 * g4);
-        qreg[4 * cs] = v.x;
-        qreg[4 * cs + 1] = v.y;
-        qreg[4 * cs + 2] = v.z;
-        qreg[4 * cs + 3] = v.w;
+    for (int j = 0; j < QW; j++) {
+        qrow[j] = qt * 64 * QW + wave * 16 * QW + j * 16 + r16;
+        qlive[j] = qrow[j] < nq;
+#pragma unroll
+        for (int cs = 0; cs < 4; cs++) {
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (qlive[j]) v = *reinterpret_cast<const float4 *>(q + (size_t)qrow[j] * d + h * 64 + 16 * cs + 4 * g4);
+            qreg[j][4 * cs] = v.x;
+            qreg[j][4 * cs + 1] = v.y;
+            qreg[j][4 * cs + 2] = v.z;
+            qreg[j][4 * cs + 3] = v.w;
+        }
     }
-    float m = -INFINITY, l = 0.0f;
-    floatx4 acc_o[4];
+    float m[QW], l[QW];
+    floatx4 acc_o[QW][4];
 #pragma unroll
-    for (int db = 0; db < 4; db++) acc_o[db] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < QW; j++) {
+        m[j] = -INFINITY;
+        l[j] = 0.0f;
+#pragma unroll
+        for (int db = 0; db < 4; db++) acc_o[j][db] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
 
     const int lc = tid >> 2, seg = (tid & 3) * 16;  // loader: coordinate row and 16-key segment
     const int width = FMT == TAH_KV_F32 ? 4 : (FMT == TAH_KV_I16 ? 2 : 1);
+    // the next key block's K and V, loaded into registers while the current block is multiplied
+    float tk[16], tv[16];
+    if (kb0 < kb1) {
+        const Where w0 = locate(kbs, kb0, records, FMT, d, chunk);
+        const bool fast0 = w0.nk == KB && ((size_t)w0.rc * width) % 16 == 0;
+        load16<FMT>(w0.rec, d, w0.rc, h * 64 + lc, w0.o + seg, w0.nk - seg, fast0, tk);
+        load16<FMT>(w0.rec, d, w0.rc, d + h * 64 + lc, w0.o + seg, w0.nk - seg, fast0, tv);
+    }
     for (int kb = kb0; kb < kb1; kb++) {
         const Where w = locate(kbs, kb, records, FMT, d, chunk);
-        const bool fast = w.nk == KB && ((size_t)w.rc * width) % 16 == 0;
-        float tmp[16];
-        load16<FMT>(w.rec, d, w.rc, h * 64 + lc, w.o + seg, w.nk - seg, fast, tmp);
+        __syncthreads();  // the previous block's tiles are no longer read
 #pragma unroll
-        for (int i = 0; i < 16; i += 4) *reinterpret_cast<float4 *>(&Ks[lc][seg + i]) = make_float4(tmp[i], tmp[i + 1], tmp[i + 2], tmp[i + 3]);
-        load16<FMT>(w.rec, d, w.rc, d + h * 64 + lc, w.o + seg, w.nk - seg, fast, tmp);
-#pragma unroll
-        for (int i = 0; i < 16; i += 4) *reinterpret_cast<float4 *>(&Vs[lc][seg + i]) = make_float4(tmp[i], tmp[i + 1], tmp[i + 2], tmp[i + 3]);
+        for (int i = 0; i < 16; i += 4) {
+            *reinterpret_cast<float4 *>(&Ks[lc][seg + i]) = make_float4(tk[i], tk[i + 1], tk[i + 2], tk[i + 3]);
+            *reinterpret_cast<float4 *>(&Vs[lc][seg + i]) = make_float4(tv[i], tv[i + 1], tv[i + 2], tv[i + 3]);
+        }
+        if (kb + 1 < kb1) {
+            const Where wn = locate(kbs, kb + 1, records, FMT, d, chunk);
+            const bool fastn = wn.nk == KB && ((size_t)wn.rc * width) % 16 == 0;
+            load16<FMT>(wn.rec, d, wn.rc, h * 64 + lc, wn.o + seg, wn.nk - seg, fastn, tk);
+            load16<FMT>(wn.rec, d, wn.rc, d + h * 64 + lc, wn.o + seg, wn.nk - seg, fastn, tv);
+        }
         __syncthreads();
 
-        // S^T = K Q^T: lane holds S[q = r16][key = 16 kb4 + 4 g4 + v]
-        floatx4 sacc[4];
+        // S^T = K Q^T: lane holds S[q = r16 of group j][key = 16 kb4 + 4 g4 + v]
+        floatx4 sacc[QW][4];
 #pragma unroll
-        for (int kb4 = 0; kb4 < 4; kb4++) sacc[kb4] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < QW; j++)
+#pragma unroll
+            for (int kb4 = 0; kb4 < 4; kb4++) sacc[j][kb4] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int cs = 0; cs < 4; cs++)
 #pragma unroll
             for (int t = 0; t < 4; t++) {
                 const int c = 16 * cs + 4 * g4 + t;
 #pragma unroll
-                for (int kb4 = 0; kb4 < 4; kb4++)
-                    sacc[kb4] = __builtin_amdgcn_mfma_f32_16x16x4f32(Ks[c][16 * kb4 + r16], qreg[4 * cs + t], sacc[kb4], 0, 0, 0);
+                for (int kb4 = 0; kb4 < 4; kb4++) {
+                    const float a = Ks[c][16 * kb4 + r16];
+#pragma unroll
+                    for (int j = 0; j < QW; j++)
+                        sacc[j][kb4] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, qreg[j][4 * cs + t], sacc[j][kb4], 0, 0, 0);
+                }
             }
-        // online softmax for this lane's query over the block's 64 keys (16 here, the rest on lanes ^16, ^32)
-        float mb = -INFINITY;
+        // online softmax per query over the block's 64 keys (16 on this lane, the rest on lanes ^16, ^32)
 #pragma unroll
-        for (int kb4 = 0; kb4 < 4; kb4++)
+        for (int j = 0; j < QW; j++) {
+            float mb = -INFINITY;
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int key = 16 * kb4 + 4 * g4 + v;
-                if (key >= w.nk) sacc[kb4][v] = -INFINITY;
-                mb = fmaxf(mb, sacc[kb4][v]);
-            }
-        mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
-        mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
-        const float mnew = fmaxf(m, mb);
-        const float alpha = fast_exp(m - mnew);
-        float lb = 0.0f;
+            for (int kb4 = 0; kb4 < 4; kb4++)
 #pragma unroll
-        for (int kb4 = 0; kb4 < 4; kb4++)
+                for (int v = 0; v < 4; v++) {
+                    if (16 * kb4 + 4 * g4 + v >= w.nk) sacc[j][kb4][v] = -INFINITY;
+                    mb = fmaxf(mb, sacc[j][kb4][v]);
+                }
+            mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
+            mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+            const float mnew = fmaxf(m[j], mb);
+            const float alpha = fast_exp(m[j] - mnew);
+            float lb = 0.0f;
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const float p = fast_exp(sacc[kb4][v] - mnew);
-                sacc[kb4][v] = p;
-                lb += p;
-            }
-        lb += __shfl_xor(lb, 16, 64);
-        lb += __shfl_xor(lb, 32, 64);
-        l = l * alpha + lb;
-        m = mnew;
+            for (int kb4 = 0; kb4 < 4; kb4++)
 #pragma unroll
-        for (int db = 0; db < 4; db++) acc_o[db] *= alpha;
-        // O^T += V^T P^T: lane holds O[q = r16][dim = 16 db + 4 g4 + v]
+                for (int v = 0; v < 4; v++) {
+                    const float p = fast_exp(sacc[j][kb4][v] - mnew);
+                    sacc[j][kb4][v] = p;
+                    lb += p;
+                }
+            lb += __shfl_xor(lb, 16, 64);
+            lb += __shfl_xor(lb, 32, 64);
+            l[j] = l[j] * alpha + lb;
+            m[j] = mnew;
 #pragma unroll
-        for (int kb4 = 0; kb4 < 4; kb4++)
+            for (int db = 0; db < 4; db++) acc_o[j][db] *= alpha;
+        }
+        // O^T += V^T P^T: lane holds O[q = r16 of group j][dim = 16 db + 4 g4 + v]
+#pragma unroll
+        for (int kb4 = 0; kb4 < 4; kb4++) {
+            float vv[4][4];
 #pragma unroll
             for (int db = 0; db < 4; db++) {
-                const float4 vv = *reinterpret_cast<const float4 *>(&Vs[16 * db + r16][16 * kb4 + 4 * g4]);
-                acc_o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.x, sacc[kb4][0], acc_o[db], 0, 0, 0);
-                acc_o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.y, sacc[kb4][1], acc_o[db], 0, 0, 0);
-                acc_o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.z, sacc[kb4][2], acc_o[db], 0, 0, 0);
-                acc_o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv.w, sacc[kb4][3], acc_o[db], 0, 0, 0);
+                const float4 v4 = *reinterpret_cast<const float4 *>(&Vs[16 * db + r16][16 * kb4 + 4 * g4]);
+                vv[db][0] = v4.x;
+                vv[db][1] = v4.y;
+                vv[db][2] = v4.z;
+                vv[db][3] = v4.w;
             }
-        __syncthreads();
+            // consecutive MFMAs go to different accumulators
+#pragma unroll
+            for (int v = 0; v < 4; v++)
+#pragma unroll
+                for (int db = 0; db < 4; db++)
+#pragma unroll
+                    for (int j = 0; j < QW; j++)
+                        acc_o[j][db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[db][v], sacc[j][kb4][v], acc_o[j][db], 0, 0, 0);
+        }
     }
-    if (!qlive) return;
-    if (splits == 1) {
-        const float inv = 1.0f / l;
 #pragma unroll
-        for (int db = 0; db < 4; db++) {
-            float4 o4 = make_float4(acc_o[db][0] * inv, acc_o[db][1] * inv, acc_o[db][2] * inv, acc_o[db][3] * inv);
-            *reinterpret_cast<float4 *>(out + (size_t)qrow * d + h * 64 + 16 * db + 4 * g4) = o4;
-        }
-    } else {
-        const size_t at = ((size_t)split * nq + qrow) * heads + h;
+    for (int j = 0; j < QW; j++) {
+        if (!qlive[j]) continue;
+        if (splits == 1) {
+            const float inv = 1.0f / l[j];
 #pragma unroll
-        for (int db = 0; db < 4; db++) {
-            float4 o4 = make_float4(acc_o[db][0], acc_o[db][1], acc_o[db][2], acc_o[db][3]);
-            *reinterpret_cast<float4 *>(part_o + at * 64 + 16 * db + 4 * g4) = o4;
-        }
-        if (g4 == 0) {
-            part_ml[at * 2] = m;
-            part_ml[at * 2 + 1] = l;
+            for (int db = 0; db < 4; db++)
+                *reinterpret_cast<float4 *>(out + (size_t)qrow[j] * d + h * 64 + 16 * db + 4 * g4) =
+                    make_float4(acc_o[j][db][0] * inv, acc_o[j][db][1] * inv, acc_o[j][db][2] * inv, acc_o[j][db][3] * inv);
+        } else {
+            const size_t at = ((size_t)split * nq + qrow[j]) * heads + h;
+#pragma unroll
+            for (int db = 0; db < 4; db++)
+                *reinterpret_cast<float4 *>(part_o + at * 64 + 16 * db + 4 * g4) =
+                    make_float4(acc_o[j][db][0], acc_o[j][db][1], acc_o[j][db][2], acc_o[j][db][3]);
+            if (g4 == 0) {
+                part_ml[at * 2] = m[j];
+                part_ml[at * 2 + 1] = l[j];
+            }
         }
     }
 }
@@ -444,8 +494,8 @@ static AttnPlan plan(const AttnShape &a) {
     AttnPlan p;
     const KeyBlocks k = key_blocks(a.rows, a.chunk);
     const int hd = a.d / a.heads;
-    p.mfma = hd == 64 && a.nq >= 64;
-    p.groups = p.mfma ? (a.nq + 63) / 64 : (a.nq + QG - 1) / QG;
+    p.mfma = hd == 64 && a.nq >= 32;
+    p.groups = p.mfma ? (a.nq + 64 * QW - 1) / (64 * QW) : (a.nq + QG - 1) / QG;
     // enough workgroups to fill 256 compute units a few times over, each with at least 2 key blocks
     const long target = 1024;
     long want = (target + (long)p.groups * a.heads - 1) / ((long)p.groups * a.heads);
@@ -466,8 +516,8 @@ template <int FMT>
 static void launch(hipStream_t s, const AttnShape &a, const AttnPlan &p, const float *q, const uint8_t *records, float *out,
                    float *part_o, float *part_ml) {
     if (p.mfma) {
-        hipLaunchKernelGGL(k_attn_mfma64<FMT>, dim3(p.groups, a.heads, p.splits), dim3(256), 0, s, a.nq, a.rows, a.chunk,
-                           a.d, a.heads, q, records, p.kb_per_split, part_o, part_ml, out);
+        hipLaunchKernelGGL(k_attn_mfma64<FMT>, dim3(p.groups * a.heads * p.splits), dim3(256), 0, s, a.nq, a.rows,
+                           a.chunk, a.d, a.heads, q, records, p.kb_per_split, p.groups, p.splits, part_o, part_ml, out);
     } else if (a.d / a.heads == 64) {
         hipLaunchKernelGGL(k_attn_decode64<FMT>, dim3(p.splits, a.heads, p.groups), dim3(256), 0, s, a.nq, a.rows,
                            a.chunk, a.d, a.heads, q, records, p.kb_per_split, part_o, part_ml, out);
