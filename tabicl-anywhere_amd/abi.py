@@ -86,7 +86,7 @@ SIGNATURES = {
     "tah_weights_upload": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ModelDesc), ctypes.POINTER(ctypes.c_void_p)]),
     "tah_weights_bytes": (ctypes.c_size_t, [ctypes.c_void_p]),
     "tah_weights_free": (None, [ctypes.c_void_p]),
-    "tah_model_bytes": (ctypes.c_size_t, [ctypes.c_int32] * 5),
+    "tah_model_bytes": (ctypes.c_size_t, [ctypes.c_void_p] + [ctypes.c_int32] * 3),
     "tah_model_load": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                       ctypes.POINTER(U8P), F32P, ctypes.POINTER(ctypes.c_void_p)]),
     "tah_model_free": (None, [ctypes.c_void_p]),

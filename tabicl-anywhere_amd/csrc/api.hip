@@ -356,9 +356,39 @@ extern "C" void tah_weights_free(tah_weights *w) {
 }
 
 // ---- fitted model ----------------------------------------------------------------------------------------------
-extern "C" size_t tah_model_bytes(int32_t kv_format, int32_t rows, int32_t chunk, int32_t d, int32_t layers) {
-    if (rows <= 0 || chunk <= 0 || d <= 0 || layers <= 0 || kv_format < 0 || kv_format > 2) return 0;
-    return (size_t)layers * align256(layer_bytes(kv_format, rows, chunk, d)) + align256(sizeof(float) * layers * d);
+static AttnShape shape_of(const tah_model *m, int heads, int nq) {
+    return AttnShape{nq, m->rows, m->chunk, m->d, heads, m->kv_format};
+}
+
+static const uint8_t *layer_of(const tah_model *m, int l) { return m->records + (size_t)l * m->layer_bytes; }
+
+// Layer l's tile images (they follow its records), or none.
+static KvImages images_of(const tah_model *m, int l) {
+    if (!m->images) return KvImages{};
+    uint8_t *base = m->records + (size_t)l * m->layer_bytes + align256(layer_bytes(m->kv_format, m->rows, m->chunk, m->d));
+    return kv_images_at(base, m->rows, m->chunk, m->heads);
+}
+
+// The images of f32 records rec32 in a loaned buffer when the split-fp16 kernel applies to a's queries, else none.
+static const KvImages *loan_images(hipStream_t s, Loans &loans, const AttnShape &a, const uint8_t *rec32, KvImages &img) {
+    if (a.nq < 32 || !kv_images_apply(a.kv_format, a.d, a.heads)) return nullptr;
+    img = kv_images_at(loans.take<uint8_t>(kv_images_bytes(a.rows, a.chunk, a.heads)), a.rows, a.chunk, a.heads);
+    kv_images(s, a.rows, a.chunk, a.d, a.heads, rec32, img);
+    return &img;
+}
+
+// Per layer: the records as they are, then (f32, head width 64) the layer's split-fp16 tile images.
+static size_t model_layer_bytes(int kv_format, int rows, int chunk, int d, int heads) {
+    size_t b = align256(layer_bytes(kv_format, rows, chunk, d));
+    if (kv_images_apply(kv_format, d, heads)) b += align256(kv_images_bytes(rows, chunk, heads));
+    return b;
+}
+
+extern "C" size_t tah_model_bytes(const tah_weights *w, int32_t kv_format, int32_t rows, int32_t chunk) {
+    if (!w || rows <= 0 || chunk <= 0 || kv_format < 0 || kv_format > 2) return 0;
+    const int d = w->d, layers = w->icl_layers;
+    return (size_t)layers * model_layer_bytes(kv_format, rows, chunk, d, w->icl_heads) +
+           align256(sizeof(float) * layers * d);
 }
 
 extern "C" int tah_model_load(tah_dev *dev, const tah_weights *w, int32_t kv_format, int32_t rows, int32_t chunk,
@@ -378,8 +408,9 @@ extern "C" int tah_model_load(tah_dev *dev, const tah_weights *w, int32_t kv_for
         m->d = w->d;
         m->layers = w->icl_layers;
         m->heads = w->icl_heads;
-        m->layer_bytes = align256(layer_bytes(kv_format, rows, chunk, w->d));
-        m->bytes = tah_model_bytes(kv_format, rows, chunk, w->d, w->icl_layers);
+        m->layer_bytes = model_layer_bytes(kv_format, rows, chunk, w->d, w->icl_heads);
+        m->images = kv_images_apply(kv_format, w->d, w->icl_heads);
+        m->bytes = tah_model_bytes(w, kv_format, rows, chunk);
         try {
             TAH_HIP(hipMalloc(&m->records, m->bytes));
             m->scales = reinterpret_cast<float *>(m->records + (size_t)m->layers * m->layer_bytes);
@@ -387,6 +418,11 @@ extern "C" int tah_model_load(tah_dev *dev, const tah_weights *w, int32_t kv_for
                 TAH_HIP(hipMemcpy(m->records + (size_t)l * m->layer_bytes, layer_records[l],
                                   layer_bytes(kv_format, rows, chunk, w->d), hipMemcpyHostToDevice));
             TAH_HIP(hipMemcpy(m->scales, scales, sizeof(float) * m->layers * m->d, hipMemcpyHostToDevice));
+            if (m->images) {
+                for (int l = 0; l < m->layers; l++)
+                    kv_images(dev->stream, rows, chunk, m->d, m->heads, layer_of(m, l), images_of(m, l));
+                TAH_HIP(hipStreamSynchronize(dev->stream));
+            }
         } catch (...) {
             if (m->records) (void)hipFree(m->records);
             delete m;
@@ -406,11 +442,6 @@ extern "C" void tah_model_free(tah_model *m) {
 }
 
 // ---- prediction ------------------------------------------------------------------------------------------------
-static AttnShape shape_of(const tah_model *m, int heads, int nq) {
-    return AttnShape{nq, m->rows, m->chunk, m->d, heads, m->kv_format};
-}
-
-static const uint8_t *layer_of(const tah_model *m, int l) { return m->records + (size_t)l * m->layer_bytes; }
 
 extern "C" int tah_attend_resident_dev(tah_dev *dev, const tah_model *model, int32_t layer, const float *q_dev,
                                        int32_t nq, float *out_dev) {
@@ -420,7 +451,8 @@ extern "C" int tah_attend_resident_dev(tah_dev *dev, const tah_model *model, int
         Loans loans(dev);
         const AttnShape a = shape_of(model, model->heads, nq);
         void *work = loans.take<uint8_t>(attention_work_bytes(a));
-        attention(dev->stream, a, q_dev, layer_of(model, layer), out_dev, work);
+        const KvImages img = images_of(model, layer);
+        attention(dev->stream, a, q_dev, layer_of(model, layer), out_dev, work, &img);
         return TAH_OK;
     });
 }
@@ -437,7 +469,8 @@ extern "C" int tah_attend_resident(tah_dev *dev, const tah_model *model, int32_t
         const AttnShape a = shape_of(model, model->heads, nq);
         void *work = loans.take<uint8_t>(attention_work_bytes(a));
         TAH_HIP(hipMemcpyAsync(qd, q, n * sizeof(float), hipMemcpyHostToDevice, dev->stream));
-        attention(dev->stream, a, qd, layer_of(model, layer), od, work);
+        const KvImages img = images_of(model, layer);
+        attention(dev->stream, a, qd, layer_of(model, layer), od, work, &img);
         TAH_HIP(hipMemcpyAsync(out, od, n * sizeof(float), hipMemcpyDeviceToHost, dev->stream));
         TAH_HIP(hipStreamSynchronize(dev->stream));
         return TAH_OK;
@@ -448,9 +481,7 @@ extern "C" int tah_attend_resident(tah_dev *dev, const tah_model *model, int32_t
 static void stage_rows(tah_dev *dev, const tah_weights *w, const tah_model *model, float *h, int nq, int out_n,
                        float *out, Loans &loans) {
     const int d = w->d, heads = w->icl_heads;
-    int ff = 0;
-    for (auto &b : w->icl) ff = std::max(ff, b.ff);
-    const int wide = std::max(ff, w->dec_hidden);
+    const int wide = std::max(icl_mid(w), w->dec_hidden);
     hipStream_t s = dev->stream;
     float *t = loans.take<float>((size_t)nq * d);
     float *q = loans.take<float>((size_t)nq * d);
@@ -463,9 +494,10 @@ static void stage_rows(tah_dev *dev, const tah_weights *w, const tah_model *mode
         // query: q = modulate(Wq norm1(h) + bq)  (src/nn.rs:130-152)
         layer_norm(s, nq, d, h, d, b.n1w, b.n1b, t, d);
         gemm(s, nq, d, d, t, d, b.in_w, b.in_b, q, d, EPI_NONE, nullptr, 0);
-        query_modulate(s, nq, b, model->scales + (size_t)l * d, q);
+        query_modulate(s, nq, b, model->scales + (size_t)l * d, q, mid);
         // attention over the stored layer, then h += out(att)  (src/predict.rs:421-551)
-        attention(s, a, q, layer_of(model, l), att, work);
+        const KvImages img = images_of(model, l);
+        attention(s, a, q, layer_of(model, l), att, work, &img);
         gemm(s, nq, d, d, att, d, b.out_w, b.out_b, h, d, EPI_RESID, h, d);
         // h += l2(gelu(l1(norm2 h)))  (src/predict.rs:552-568)
         layer_norm(s, nq, d, h, d, b.n2w, b.n2b, t, d);
@@ -547,7 +579,9 @@ extern "C" int tah_attend(tah_dev *dev, const float *q, const float *kv, int32_t
         void *work = loans.take<uint8_t>(attention_work_bytes(a));
         TAH_HIP(hipMemcpyAsync(qd, q, n * sizeof(float), hipMemcpyHostToDevice, dev->stream));
         TAH_HIP(hipMemcpyAsync(kvd, kv, 2 * n * sizeof(float), hipMemcpyHostToDevice, dev->stream));
-        attention(dev->stream, a, qd, reinterpret_cast<const uint8_t *>(kvd), od, work);
+        KvImages img;
+        const KvImages *imgp = loan_images(dev->stream, loans, a, reinterpret_cast<const uint8_t *>(kvd), img);
+        attention(dev->stream, a, qd, reinterpret_cast<const uint8_t *>(kvd), od, work, imgp);
         TAH_HIP(hipMemcpyAsync(out, od, n * sizeof(float), hipMemcpyDeviceToHost, dev->stream));
         TAH_HIP(hipStreamSynchronize(dev->stream));
         return TAH_OK;
@@ -568,8 +602,7 @@ extern "C" int tah_in_context(tah_dev *dev, const tah_weights *w, const float *h
     return guarded(dev, [&] {
         if (rows <= 0 || chunk <= 0 || kv_format < 0 || kv_format > 2) throw ArgError{"in_context: bad rows, chunk or format"};
         const int d = w->d, L = w->icl_layers;
-        int ff = 0;
-        for (auto &b : w->icl) ff = std::max(ff, b.ff);
+        const int ff = icl_mid(w);
         const size_t n = (size_t)rows * d;
         const size_t lbytes = layer_bytes(kv_format, rows, chunk, d);
         hipStream_t s = dev->stream;
@@ -580,6 +613,10 @@ extern "C" int tah_in_context(tah_dev *dev, const tah_weights *w, const float *h
         uint8_t *recq = kv_format == TAH_KV_F32 ? nullptr : loans.take<uint8_t>(lbytes);
         const AttnShape a{rows, rows, chunk, d, w->icl_heads, TAH_KV_F32};
         void *work = loans.take<uint8_t>(attention_work_bytes(a));
+        KvImages img;
+        const bool use_img = rows >= 32 && kv_images_apply(TAH_KV_F32, d, w->icl_heads);
+        if (use_img)
+            img = kv_images_at(loans.take<uint8_t>(kv_images_bytes(rows, chunk, w->icl_heads)), rows, chunk, w->icl_heads);
         Pinned host;
         TAH_HIP(hipHostMalloc(&host.p, lbytes, hipHostMallocDefault));
         TAH_HIP(hipMemcpyAsync(h, h_host, n * sizeof(float), hipMemcpyHostToDevice, s));
@@ -601,8 +638,9 @@ extern "C" int tah_in_context(tah_dev *dev, const tah_weights *w, const float *h
                 // every row attends to all rows over the exact keys and values, then the rest of the block
                 // (src/fit.rs:667-744)
                 gemm(s, rows, d, d, t, d, b.in_w, b.in_b, q, d, EPI_NONE, nullptr, 0);
-                query_modulate(s, rows, b, sc + (size_t)l * d, q);
-                attention(s, a, q, reinterpret_cast<const uint8_t *>(rec32), att, work);
+                query_modulate(s, rows, b, sc + (size_t)l * d, q, mid);
+                if (use_img) kv_images(s, rows, chunk, d, w->icl_heads, reinterpret_cast<const uint8_t *>(rec32), img);
+                attention(s, a, q, reinterpret_cast<const uint8_t *>(rec32), att, work, use_img ? &img : nullptr);
                 gemm(s, rows, d, d, att, d, b.out_w, b.out_b, h, d, EPI_RESID, h, d);
                 layer_norm(s, rows, d, h, d, b.n2w, b.n2b, t, d);
                 gemm(s, rows, b.ff, d, t, d, b.l1w, b.l1b, mid, b.ff, EPI_GELU, nullptr, 0);
@@ -710,12 +748,10 @@ extern "C" int tah_represent(tah_dev *dev, const tah_weights *w, const float *to
 // Working bytes a sub-batch of k rows borrows in predict_rows (every buffer it and stage_rows take).
 static size_t predict_batch_bytes(const tah_weights *w, const tah_model *model, int k) {
     const int T = w->cls + model->features;
-    int ff = 0;
-    for (auto &b : w->icl) ff = std::max(ff, b.ff);
     const size_t kk = (size_t)k;
     const size_t floats[] = {kk * T * w->e, kk * w->d, kk * model->features * w->e,
                              column_stage_floats(w, k, model->features, model->digits), row_stage_floats(w, k, T),
-                             kk * w->d, kk * w->d, kk * w->d, kk * std::max(ff, w->dec_hidden)};
+                             kk * w->d, kk * w->d, kk * w->d, kk * std::max(icl_mid(w), w->dec_hidden)};
     size_t bytes = attention_work_bytes(shape_of(model, model->heads, k)) + 256;
     for (size_t f : floats) bytes += align256(f * sizeof(float)) + 256;
     return bytes;
@@ -811,12 +847,16 @@ extern "C" int tah_fit_represent(tah_dev *dev, const tah_weights *w, const float
         TAH_HIP(hipMemcpyAsync(yd, y, sizeof(float) * rows, hipMemcpyHostToDevice, s));
         TAH_HIP(hipMemcpyAsync(sc, ind_scales, sizeof(float) * nb * e, hipMemcpyHostToDevice, s));
         // the inducing points' queries, once per block, scaled for all rows (src/fit.rs:300-313)
+        size_t qfloats = 0;
+        for (auto &b : w->col_a1) qfloats = std::max(qfloats, query_scratch_floats(inds, b));
+        Loans qloan(dev);
+        float *qscr = qloan.take<float>(std::max<size_t>(qfloats, 1));
         for (int bi = 0; bi < nb; bi++) {
             const DevBlock &a1 = w->col_a1[bi];
             float *qb = indq + (size_t)bi * inds * e;
             layer_norm(s, inds, e, w->col_ind + (size_t)bi * inds * e, e, a1.n1w, a1.n1b, it, e);
             gemm(s, inds, e, e, it, e, a1.in_w, a1.in_b, qb, e, EPI_NONE, nullptr, 0);
-            query_modulate(s, inds, a1, sc + (size_t)bi * e, qb);
+            query_modulate(s, inds, a1, sc + (size_t)bi * e, qb, qscr);
         }
         // feature groups in batches that fit the working memory
         auto group_bytes = [&](int gb) {

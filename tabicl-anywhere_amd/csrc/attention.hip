@@ -8,7 +8,16 @@
 // of Soft); when the keys are split over several workgroups, their (m, l, o) are combined by a log-sum-exp merge
 // (Soft::merge, src/nn.rs:261-276) and divided through (Soft::finish).
 //
-// Two kernels:
+// The kernels:
+//  * k_attn_split64: head width 64, at least 32 queries, f32 keys and values prepared as tile images (below).
+//    Every f32 product runs on the fp16 matrix cores as three products of fp16 halves (hi*hi + hi*lo + lo*hi,
+//    x = hi + lo with hi = fp16(x), lo = fp16(x - hi); the splitting of Ootomo & Yokota, "Recovering single
+//    precision accuracy from Tensor Cores while surpassing the FP32 theoretical peak performance", IJHPCA 2022),
+//    accumulated in f32: the error is that of an f32 dot product (2^-22 of sum |x y| measured on gfx950), at
+//    v_mfma_f32_32x32x16_f16's rate (2 PFLOP/s sustained, 16x that of the f32 matrix instructions).
+//    Operands are scaled by powers of two first (exact): each query to a maximum near 2^14, each head's keys and
+//    values by the layer's maximum, and the softmax weights to at most 2^12, so that no half overflows and the
+//    low halves stay normal for all but negligible elements.
 //  * k_attn_mfma64: head width 64 and at least 32 queries. 4 wavefronts x 32 queries share LDS tiles of K and V
 //    (64 coordinates x 64 keys). Scores are formed transposed, S^T = K Q^T, with v_mfma_f32_16x16x4_f32 so that
 //    each lane owns one query (lane % 16) in both products; the softmax then needs only two cross-lane steps, and
@@ -17,6 +26,7 @@
 //    loaded with 128-bit loads, lane = key for the scores and lane = coordinate for the weighted sum.
 //    Bandwidth-bound, as single-row prediction is.
 //  * k_attn_decode: any other head width up to 64 (the tiny test models): the same with one wavefront.
+// All of them leave the running maximum in log2 units (score * log2 e) for the split merge.
 #include <algorithm>
 
 #include "common.hpp"
@@ -286,7 +296,7 @@ __global__ __launch_bounds__(256) void k_attn_mfma64(int nq, int rows, int chunk
                 *reinterpret_cast<float4 *>(part_o + at * 64 + 16 * db + 4 * g4) =
                     make_float4(acc_o[j][db][0], acc_o[j][db][1], acc_o[j][db][2], acc_o[j][db][3]);
             if (g4 == 0) {
-                part_ml[at * 2] = m[j];
+                part_ml[at * 2] = m[j] * LOG2E;
                 part_ml[at * 2 + 1] = l[j];
             }
         }
@@ -360,7 +370,7 @@ __global__ __launch_bounds__(64) void k_attn_decode(int nq, int rows, int chunk,
             const size_t at = ((size_t)split * nq + qr) * heads + h;
             part_o[at * hd + lane] = o[qi];
             if (lane == 0) {
-                part_ml[at * 2] = m[qi];
+                part_ml[at * 2] = m[qi] * LOG2E;
                 part_ml[at * 2 + 1] = l[qi];
             }
         }
@@ -441,9 +451,292 @@ __global__ __launch_bounds__(256) void k_attn_decode64(int nq, int rows, int chu
             const size_t at = ((size_t)split * nq + qr) * heads + h;
             part_o[at * 64 + lane] = o[j];
             if (lane == 0) {
-                part_ml[at * 2] = m[j];
+                part_ml[at * 2] = m[j] * LOG2E;
                 part_ml[at * 2 + 1] = l[j];
             }
+        }
+    }
+}
+
+// ---- tile images: f32 keys and values split into fp16 halves, laid out as the split kernel's LDS image -------
+// One image per (key block, head), 32 KB: K hi, K lo as [64 keys][64 coordinates] and V hi, V lo as
+// [64 coordinates][64 keys], fp16, each 128-byte row split in eight 16-byte chunks stored XOR-swizzled by row (the
+// lanes of one LDS read then hit eight different chunks). Keys past the end of a short block are zeros. Each head's
+// keys are scaled by 2^sk and values by 2^sv, the powers of two that bring the layer's largest magnitude of that
+// head below 2^14; kvmax holds those maxima (f32 bits) per head, [heads][2].
+typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
+constexpr int IMG = 32768;
+
+__host__ __device__ inline size_t image_bytes_of(int rows, int chunk, int heads) {
+    return (size_t)key_blocks(rows, chunk).n_kb * heads * IMG;
+}
+
+__device__ __forceinline__ int kswz(int r, int c) { return c ^ ((r & 3) | (((r >> 3) & 1) << 2)); }
+__device__ __forceinline__ int vswz(int r, int c) { return c ^ (r & 7); }
+
+// 14 - e for max = m 2^e, m in [0.5, 1): scaling by 2^(14 - e) leaves every magnitude below 2^14.
+__device__ __forceinline__ int shift_for(uint32_t max_bits) {
+    int e = 0;
+    (void)frexpf(__uint_as_float(max_bits), &e);
+    return 14 - e;
+}
+
+__global__ __launch_bounds__(64) void k_zero_u32(int n, uint32_t *__restrict__ p) {
+    const int i = blockIdx.x * 64 + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+// grid (key blocks, heads); 256 threads: the largest |K| and |V| of each head, by integer max on the f32 bits
+// (non-negative floats order as their bit patterns).
+__global__ __launch_bounds__(256) void k_kv_absmax(int rows, int chunk, int d, int heads, const uint8_t *__restrict__ records,
+                                                    uint32_t *__restrict__ kvmax) {
+    __shared__ float red[2][4];
+    const int kb = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    const KeyBlocks kbs = key_blocks(rows, chunk);
+    const Where w = locate(kbs, kb, records, TAH_KV_F32, d, chunk);
+    const int lc = tid >> 2, seg = (tid & 3) * 16;
+    const bool fast = w.nk == KB && ((size_t)w.rc * 4) % 16 == 0;
+    float tk[16], tv[16];
+    load16<TAH_KV_F32>(w.rec, d, w.rc, h * 64 + lc, w.o + seg, w.nk - seg, fast, tk);
+    load16<TAH_KV_F32>(w.rec, d, w.rc, d + h * 64 + lc, w.o + seg, w.nk - seg, fast, tv);
+    float mk = 0.0f, mv = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        mk = fmaxf(mk, fabsf(tk[i]));
+        mv = fmaxf(mv, fabsf(tv[i]));
+    }
+    mk = wave_max(mk);
+    mv = wave_max(mv);
+    if ((tid & 63) == 0) {
+        red[0][tid >> 6] = mk;
+        red[1][tid >> 6] = mv;
+    }
+    __syncthreads();
+    if (tid < 2) {
+        const float m = fmaxf(fmaxf(red[tid][0], red[tid][1]), fmaxf(red[tid][2], red[tid][3]));
+        atomicMax(kvmax + h * 2 + tid, __float_as_uint(m));
+    }
+}
+
+// grid (key blocks, heads); 256 threads: one tile image.
+__global__ __launch_bounds__(256) void k_kv_images(int rows, int chunk, int d, int heads,
+                                                    const uint8_t *__restrict__ records,
+                                                    const uint32_t *__restrict__ kvmax, uint8_t *__restrict__ images) {
+    __shared__ float Ks[64][KB + 1];  // [coordinate][key]
+    __shared__ float Vs[64][KB + 1];
+    const int kb = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    const KeyBlocks kbs = key_blocks(rows, chunk);
+    const Where w = locate(kbs, kb, records, TAH_KV_F32, d, chunk);
+    const int lc = tid >> 2, seg = (tid & 3) * 16;
+    const bool fast = w.nk == KB && ((size_t)w.rc * 4) % 16 == 0;
+    float tk[16], tv[16];
+    load16<TAH_KV_F32>(w.rec, d, w.rc, h * 64 + lc, w.o + seg, w.nk - seg, fast, tk);
+    load16<TAH_KV_F32>(w.rec, d, w.rc, d + h * 64 + lc, w.o + seg, w.nk - seg, fast, tv);
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        Ks[lc][seg + i] = tk[i];
+        Vs[lc][seg + i] = tv[i];
+    }
+    __syncthreads();
+    const float fk = ldexpf(1.0f, shift_for(kvmax[h * 2])), fv = ldexpf(1.0f, shift_for(kvmax[h * 2 + 1]));
+    uint8_t *img = images + ((size_t)kb * heads + h) * IMG;
+    for (int u = tid; u < 512; u += 256) {
+        const int r = u >> 3, c = u & 7;
+        halfx8 kh, kl, vh, vl;
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const float x = Ks[8 * c + t][r] * fk;  // key r, coordinate 8c + t
+            const _Float16 xh = (_Float16)x;
+            kh[t] = xh;
+            kl[t] = (_Float16)(x - (float)xh);
+            const float y = Vs[r][8 * c + t] * fv;  // coordinate r, key 8c + t
+            const _Float16 yh = (_Float16)y;
+            vh[t] = yh;
+            vl[t] = (_Float16)(y - (float)yh);
+        }
+        *reinterpret_cast<halfx8 *>(img + r * 128 + kswz(r, c) * 16) = kh;
+        *reinterpret_cast<halfx8 *>(img + 8192 + r * 128 + kswz(r, c) * 16) = kl;
+        *reinterpret_cast<halfx8 *>(img + 16384 + r * 128 + vswz(r, c) * 16) = vh;
+        *reinterpret_cast<halfx8 *>(img + 24576 + r * 128 + vswz(r, c) * 16) = vl;
+    }
+}
+
+// ---- split-fp16 MFMA kernel: head width 64 over tile images --------------------------------------------------
+// A flat grid of qtiles x heads x splits workgroups (remapped XCD by XCD as in k_attn_mfma64) of 4 wavefronts x 32
+// queries. Per key block of 64, the block's 32 KB image is copied into LDS (the next one already in registers),
+// then each wavefront forms S^T = K Q^T for two halves of 32 keys with v_mfma_f32_32x32x16_f16: lane l owns query
+// l % 32 and holds 16 of the half's keys. The A operand's row i takes key sigma(i) (bits 3 and 2 of i swapped),
+// which puts eight consecutive keys (16 (v / 8) + 8 (l / 32) + v % 8) in each lane's accumulators v = 8 hh..8 hh + 7:
+// exactly the B operand that O^T = V^T P^T needs for a reduction over 16 keys, so the weights never leave the lane.
+__device__ __forceinline__ floatx16 mfma16(halfx8 a, halfx8 b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(256) void k_attn_split64(int nq, int rows, int chunk, int d, int heads,
+                                                       const float *__restrict__ q, const uint8_t *__restrict__ images,
+                                                       const uint32_t *__restrict__ kvmax, int kb_per_split,
+                                                       int qtiles, int splits, float *__restrict__ part_o,
+                                                       float *__restrict__ part_ml, float *__restrict__ out) {
+    __shared__ __align__(16) uint8_t tile[IMG];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int total = qtiles * heads * splits;
+    int flat = blockIdx.x;
+    if (total % 8 == 0) flat = (flat % 8) * (total / 8) + flat / 8;
+    const int qt = flat % qtiles, pair = flat / qtiles;
+    const int h = pair % heads, split = pair / heads;
+    const KeyBlocks kbs = key_blocks(rows, chunk);
+    const int kb0 = split * kb_per_split, kb1 = min(kbs.n_kb, kb0 + kb_per_split);
+    const int r32 = lane & 31, g = lane >> 5;
+    const int qrow = qt * 128 + wave * 32 + r32;
+    const bool qlive = qrow < nq;
+
+    // this lane's query coordinates 16 dc + 8 g + t, scaled to a maximum magnitude near 2^14 and split
+    float qv[4][8];
+#pragma unroll
+    for (int dc = 0; dc < 4; dc++) {
+        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), b = a;
+        if (qlive) {
+            const float *src = q + (size_t)qrow * d + h * 64 + 16 * dc + 8 * g;
+            a = *reinterpret_cast<const float4 *>(src);
+            b = *reinterpret_cast<const float4 *>(src + 4);
+        }
+        qv[dc][0] = a.x; qv[dc][1] = a.y; qv[dc][2] = a.z; qv[dc][3] = a.w;
+        qv[dc][4] = b.x; qv[dc][5] = b.y; qv[dc][6] = b.z; qv[dc][7] = b.w;
+    }
+    float qmax = 0.0f;
+#pragma unroll
+    for (int dc = 0; dc < 4; dc++)
+#pragma unroll
+        for (int t = 0; t < 8; t++) qmax = fmaxf(qmax, fabsf(qv[dc][t]));
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
+    const int eq = shift_for(__float_as_uint(qmax));
+    halfx8 qh[4], ql[4];
+#pragma unroll
+    for (int dc = 0; dc < 4; dc++)
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const float x = ldexpf(qv[dc][t], eq);
+            const _Float16 xh = (_Float16)x;
+            qh[dc][t] = xh;
+            ql[dc][t] = (_Float16)(x - (float)xh);
+        }
+    const int sk = shift_for(kvmax[h * 2]), sv = shift_for(kvmax[h * 2 + 1]);
+    const float to_log2 = ldexpf(LOG2E, -(sk + eq));  // raw score -> score * log2 e
+
+    // A-operand row of this lane in a 32-key half: key sigma(r32)
+    const int krow = (r32 & 16) | ((r32 & 4) << 1) | ((r32 & 8) >> 1) | (r32 & 3);
+    float m = -INFINITY, l = 0.0f;
+    floatx16 acc_o[2];
+#pragma unroll
+    for (int db = 0; db < 2; db++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc_o[db][v] = 0.0f;
+
+    uint4 pre[8];
+    auto fetch = [&](int kb) {
+        const uint4 *src = reinterpret_cast<const uint4 *>(images + ((size_t)kb * heads + h) * IMG);
+#pragma unroll
+        for (int i = 0; i < 8; i++) pre[i] = src[tid + 256 * i];
+    };
+    if (kb0 < kb1) fetch(kb0);
+    for (int kb = kb0; kb < kb1; kb++) {
+        const int ci = kb / kbs.bpc;
+        const int nk = min(KB, (ci == kbs.n_chunks - 1 ? kbs.last_rc : chunk) - (kb % kbs.bpc) * KB);
+        __syncthreads();  // the previous image is no longer read
+#pragma unroll
+        for (int i = 0; i < 8; i++) reinterpret_cast<uint4 *>(tile)[tid + 256 * i] = pre[i];
+        if (kb + 1 < kb1) fetch(kb + 1);
+        __syncthreads();
+        // S^T for keys 32 kh + sigma(i)
+        floatx16 sc[2];
+#pragma unroll
+        for (int kh = 0; kh < 2; kh++) {
+#pragma unroll
+            for (int v = 0; v < 16; v++) sc[kh][v] = 0.0f;
+            const int r = 32 * kh + krow;
+#pragma unroll
+            for (int dc = 0; dc < 4; dc++) {
+                const int off = r * 128 + kswz(r, 2 * dc + g) * 16;
+                const halfx8 khi = *reinterpret_cast<const halfx8 *>(tile + off);
+                const halfx8 klo = *reinterpret_cast<const halfx8 *>(tile + 8192 + off);
+                sc[kh] = mfma16(khi, qh[dc], sc[kh]);
+                sc[kh] = mfma16(khi, ql[dc], sc[kh]);
+                sc[kh] = mfma16(klo, qh[dc], sc[kh]);
+            }
+        }
+        // online softmax in log2 units; accumulator v of half kh holds key 32 kh + 16 (v / 8) + 8 g + v % 8
+        float mb = -INFINITY;
+#pragma unroll
+        for (int kh = 0; kh < 2; kh++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int key = 32 * kh + 16 * (v >> 3) + 8 * g + (v & 7);
+                const float t = key < nk ? sc[kh][v] * to_log2 : -INFINITY;
+                sc[kh][v] = t;
+                mb = fmaxf(mb, t);
+            }
+        mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+        const float mnew = fmaxf(m, mb);
+        const float alpha = exp2f(m - mnew);
+        const float moff = mnew - 12.0f;  // weights scaled by 2^12: at most 4096
+        float lb = 0.0f;
+        halfx8 ph[2][2], pl[2][2];
+#pragma unroll
+        for (int kh = 0; kh < 2; kh++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const float p = exp2f(sc[kh][v] - moff);
+                lb += p;
+                const _Float16 hi = (_Float16)p;
+                ph[kh][v >> 3][v & 7] = hi;
+                pl[kh][v >> 3][v & 7] = (_Float16)(p - (float)hi);
+            }
+        l = l * alpha + lb;  // this lane's half of the keys; the halves are added at the end
+        m = mnew;
+#pragma unroll
+        for (int db = 0; db < 2; db++) acc_o[db] *= alpha;
+        // O^T += V^T P^T over four 16-key steps
+#pragma unroll
+        for (int db = 0; db < 2; db++) {
+            const int r = 32 * db + r32;
+#pragma unroll
+            for (int kh = 0; kh < 2; kh++)
+#pragma unroll
+                for (int hh = 0; hh < 2; hh++) {
+                    const int off = r * 128 + vswz(r, 4 * kh + 2 * hh + g) * 16;
+                    const halfx8 vhi = *reinterpret_cast<const halfx8 *>(tile + 16384 + off);
+                    const halfx8 vlo = *reinterpret_cast<const halfx8 *>(tile + 24576 + off);
+                    acc_o[db] = mfma16(vhi, ph[kh][hh], acc_o[db]);
+                    acc_o[db] = mfma16(vhi, pl[kh][hh], acc_o[db]);
+                    acc_o[db] = mfma16(vlo, ph[kh][hh], acc_o[db]);
+                }
+        }
+    }
+    l += __shfl_xor(l, 32, 64);
+    if (!qlive) return;
+    // accumulator v of dim block db holds coordinate 32 db + 8 (v / 4) + 4 g + v % 4
+    const float unscale = ldexpf(1.0f, -sv);
+    if (splits == 1) {
+        const float f = unscale / l;
+#pragma unroll
+        for (int db = 0; db < 2; db++)
+#pragma unroll
+            for (int v4 = 0; v4 < 4; v4++)
+                *reinterpret_cast<float4 *>(out + (size_t)qrow * d + h * 64 + 32 * db + 8 * v4 + 4 * g) =
+                    make_float4(acc_o[db][4 * v4] * f, acc_o[db][4 * v4 + 1] * f, acc_o[db][4 * v4 + 2] * f,
+                                acc_o[db][4 * v4 + 3] * f);
+    } else {
+        const size_t at = ((size_t)split * nq + qrow) * heads + h;
+#pragma unroll
+        for (int db = 0; db < 2; db++)
+#pragma unroll
+            for (int v4 = 0; v4 < 4; v4++)
+                *reinterpret_cast<float4 *>(part_o + at * 64 + 32 * db + 8 * v4 + 4 * g) =
+                    make_float4(acc_o[db][4 * v4] * unscale, acc_o[db][4 * v4 + 1] * unscale,
+                                acc_o[db][4 * v4 + 2] * unscale, acc_o[db][4 * v4 + 3] * unscale);
+        if (g == 0) {
+            part_ml[at * 2] = m;
+            part_ml[at * 2 + 1] = l;
         }
     }
 }
@@ -451,8 +744,9 @@ __global__ __launch_bounds__(256) void k_attn_decode64(int nq, int rows, int chu
 // ---- split merge: Soft::merge then Soft::finish ---------------------------------------------------------------
 // grid nq * heads; 64 threads. The largest running maximum first (lanes over splits), then one pass over the
 // splits accumulating each one's weight sum and weighted values rescaled to it; loads are independent across
-// splits, so they stream.
-__global__ __launch_bounds__(64) void k_attn_merge(int nq, int d, int heads, int splits, const float *__restrict__ part_o,
+// splits, so they stream. Maxima are in log2 units when log2_units is set, natural units otherwise.
+__global__ __launch_bounds__(64) void k_attn_merge(int nq, int d, int heads, int splits, int log2_units,
+                                                    const float *__restrict__ part_o,
                                                     const float *__restrict__ part_ml, float *__restrict__ out) {
     const int item = blockIdx.x, lane = threadIdx.x;
     const int qr = item / heads, h = item % heads, hd = d / heads;
@@ -470,7 +764,8 @@ __global__ __launch_bounds__(64) void k_attn_merge(int nq, int d, int heads, int
         for (int s = 0; s < splits; s++) {
             const size_t at = s * stride + base;
             const float ls = part_ml[at * 2 + 1];
-            const float f = ls > 0.0f ? fast_exp(part_ml[at * 2] - M) : 0.0f;
+            const float dm = part_ml[at * 2] - M;
+            const float f = ls > 0.0f ? (log2_units ? exp2f(dm) : fast_exp(dm)) : 0.0f;
             L += ls * f;
             O += part_o[at * hd + c] * f;
         }
@@ -480,21 +775,49 @@ __global__ __launch_bounds__(64) void k_attn_merge(int nq, int d, int heads, int
 
 void merge_splits(hipStream_t s, int nq, int d, int heads, int splits, const float *part_o, const float *part_ml,
                   float *out) {
-    hipLaunchKernelGGL(k_attn_merge, dim3(nq * heads), dim3(64), 0, s, nq, d, heads, splits, part_o, part_ml, out);
+    hipLaunchKernelGGL(k_attn_merge, dim3(nq * heads), dim3(64), 0, s, nq, d, heads, splits, 0, part_o, part_ml, out);
     TAH_LAUNCHED();
 }
 
 // ---- planning and launch --------------------------------------------------------------------------------------
 struct AttnPlan {
-    bool mfma;
+    bool mfma, split16;
     int splits, kb_per_split, groups;
 };
 
-static AttnPlan plan(const AttnShape &a) {
+bool kv_images_apply(int kv_format, int d, int heads) {
+    return kv_format == TAH_KV_F32 && heads > 0 && d == 64 * heads;
+}
+
+size_t kv_images_bytes(int rows, int chunk, int heads) {
+    return ((image_bytes_of(rows, chunk, heads) + 255) / 256) * 256 + 256 + sizeof(uint32_t) * 2 * (size_t)heads;
+}
+
+void kv_images(hipStream_t s, int rows, int chunk, int d, int heads, const uint8_t *rec32, KvImages img) {
+    if (!kv_images_apply(TAH_KV_F32, d, heads)) throw ArgError{"key/value images need head width 64"};
+    const KeyBlocks k = key_blocks(rows, chunk);
+    hipLaunchKernelGGL(k_zero_u32, dim3((2 * heads + 63) / 64), dim3(64), 0, s, 2 * heads, img.kvmax);
+    TAH_LAUNCHED();
+    hipLaunchKernelGGL(k_kv_absmax, dim3(k.n_kb, heads), dim3(256), 0, s, rows, chunk, d, heads, rec32, img.kvmax);
+    TAH_LAUNCHED();
+    hipLaunchKernelGGL(k_kv_images, dim3(k.n_kb, heads), dim3(256), 0, s, rows, chunk, d, heads, rec32, img.kvmax,
+                       img.images);
+    TAH_LAUNCHED();
+}
+
+KvImages kv_images_at(uint8_t *base, int rows, int chunk, int heads) {
+    KvImages img;
+    img.images = base;
+    img.kvmax = reinterpret_cast<uint32_t *>(base + ((image_bytes_of(rows, chunk, heads) + 255) / 256) * 256);
+    return img;
+}
+
+static AttnPlan plan(const AttnShape &a, bool images) {
     AttnPlan p;
     const KeyBlocks k = key_blocks(a.rows, a.chunk);
     const int hd = a.d / a.heads;
     p.mfma = hd == 64 && a.nq >= 32;
+    p.split16 = p.mfma && images && kv_images_apply(a.kv_format, a.d, a.heads);
     p.groups = p.mfma ? (a.nq + 64 * QW - 1) / (64 * QW) : (a.nq + QG - 1) / QG;
     // enough workgroups to fill 256 compute units a few times over, each with at least 2 key blocks
     const long target = 1024;
@@ -506,7 +829,7 @@ static AttnPlan plan(const AttnShape &a) {
 }
 
 size_t attention_work_bytes(const AttnShape &a) {
-    const AttnPlan p = plan(a);
+    const AttnPlan p = plan(a, false);  // the split count does not depend on the kernel
     if (p.splits == 1) return 0;
     const int hd = a.d / a.heads;
     return sizeof(float) * (size_t)p.splits * a.nq * a.heads * (hd + 2) + 256;
@@ -528,26 +851,32 @@ static void launch(hipStream_t s, const AttnShape &a, const AttnPlan &p, const f
     TAH_LAUNCHED();
 }
 
-void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t *records, float *out, void *work) {
+void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t *records, float *out, void *work,
+               const KvImages *img) {
     if (a.nq <= 0) return;
     const int hd = a.d / a.heads;
     if (a.d % a.heads != 0 || hd > 64 || a.rows <= 0 || a.chunk <= 0)
         throw ArgError{"attention: head width must divide d and be at most 64, rows and chunk positive"};
     if ((size_t)a.nq > (size_t)65535 * 8) throw ArgError{"attention: too many queries for one launch"};
-    const AttnPlan p = plan(a);
+    const AttnPlan p = plan(a, img != nullptr && img->images != nullptr);
     float *part_o = nullptr, *part_ml = nullptr;
     if (p.splits > 1) {
         part_o = static_cast<float *>(work);
         part_ml = part_o + (size_t)p.splits * a.nq * a.heads * hd;
     }
-    switch (a.kv_format) {
+    if (p.split16) {
+        hipLaunchKernelGGL(k_attn_split64, dim3(p.groups * a.heads * p.splits), dim3(256), 0, s, a.nq, a.rows, a.chunk,
+                           a.d, a.heads, q, img->images, img->kvmax, p.kb_per_split, p.groups, p.splits, part_o, part_ml,
+                           out);
+        TAH_LAUNCHED();
+    } else switch (a.kv_format) {
         case TAH_KV_F32: launch<TAH_KV_F32>(s, a, p, q, records, out, part_o, part_ml); break;
         case TAH_KV_I16: launch<TAH_KV_I16>(s, a, p, q, records, out, part_o, part_ml); break;
         case TAH_KV_I8: launch<TAH_KV_I8>(s, a, p, q, records, out, part_o, part_ml); break;
         default: throw ArgError{"attention: unknown key/value format"};
     }
     if (p.splits > 1) {
-        hipLaunchKernelGGL(k_attn_merge, dim3(a.nq * a.heads), dim3(64), 0, s, a.nq, a.d, a.heads, p.splits, part_o,
+        hipLaunchKernelGGL(k_attn_merge, dim3(a.nq * a.heads), dim3(64), 0, s, a.nq, a.d, a.heads, p.splits, 1, part_o,
                            part_ml, out);
         TAH_LAUNCHED();
     }

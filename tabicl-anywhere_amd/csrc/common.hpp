@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstddef>
 #include <cstdint>
 #include <mutex>
@@ -90,7 +91,8 @@ struct tah_model {
     int ordinal;
     int kv_format, rows, chunk, d, layers, heads;
     size_t layer_bytes;
-    uint8_t *records = nullptr;  // layers x layer_bytes, the stored chunk records as they are
+    uint8_t *records = nullptr;  // layers x layer_bytes: the stored chunk records as they are, then their images
+    bool images = false;         // f32 records of head width 64: tile images follow each layer's records
     float *scales = nullptr;     // [layers][d]
     size_t bytes = 0;
     float *col_kv = nullptr;     // [features][digits][blocks][2][e][inds] (tah_model_set_columns)
@@ -99,19 +101,31 @@ struct tah_model {
 
 namespace tah {
 
-enum Epi { EPI_NONE = 0, EPI_GELU = 1, EPI_RESID = 2 };
+enum Epi { EPI_NONE = 0, EPI_GELU = 1, EPI_RESID = 2, EPI_QMOD = 3 };
 
 // Y[M][N] (leading dim ldy) = epi(X[M][K] (ldx) * W[N][K]^T + b[N]); EPI_RESID adds R (ldr, may alias Y).
 void gemm(hipStream_t s, int M, int N, int K, const float *X, int ldx, const float *W, const float *b, float *Y,
           int ldy, Epi epi, const float *R, int ldr);
+
+// q [M][N] (in place) = q * scale[(m % heads) * N + n] * (1 + tanh(X W^T + b)): the query MLP's modulation.
+void gemm_qmod(hipStream_t s, int M, int N, int K, const float *X, int ldx, const float *W, const float *b, float *q,
+               const float *scale, int heads);
 
 // y[r] = layer_norm(x[r]) * w + b over rows of n numbers (eps 1e-5, biased variance).
 void layer_norm(hipStream_t s, int rows, int n, const float *x, int ldx, const float *w, const float *b, float *y,
                 int ldy);
 
 // In place on q [rows][d] (after the query projection): q *= scale (no scalable softmax), or per head
-// q_h *= scale_h * (1 + tanh(q2 gelu(q0 q_h + q0b) + q2b)).
-void query_modulate(hipStream_t s, int rows, const DevBlock &b, const float *scale, float *q);
+// q_h *= scale_h * (1 + tanh(q2 gelu(q0 q_h + q0b) + q2b)). scratch holds rows * heads * ss_hidden floats.
+void query_modulate(hipStream_t s, int rows, const DevBlock &b, const float *scale, float *q, float *scratch);
+size_t query_scratch_floats(int rows, const DevBlock &b);
+
+// Widest per-row scratch of an in-context block: its feed-forward hidden layer or its query MLP's hidden layers.
+inline int icl_mid(const tah_weights *w) {
+    int m = 0;
+    for (auto &b : w->icl) m = std::max(m, std::max(b.ff, b.heads * b.ss_hidden));
+    return m;
+}
 
 // The attention of nq queries q [nq][d] (scaled) over one stored in-context layer (chunk records on the card):
 // out [nq][d], normalised. work must hold attention_work_bytes(...).
@@ -123,7 +137,19 @@ size_t attention_work_bytes(const AttnShape &a);
 void to_records(hipStream_t s, int rows, int d, int chunk, const float *kv, float *rec32);
 // f32 chunk records to i16/i8 records (the reference's quantiser, bit for bit).
 void pack(hipStream_t s, int rows, int d, int chunk, int fmt, const float *rec32, uint8_t *recq);
-void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t *records, float *out, void *work);
+// f32 keys and values of one layer as fp16 hi/lo tile images (head width 64 only), with each head's largest
+// magnitudes: the split-fp16 attention kernel's input, built once per stored layer.
+struct KvImages {
+    uint8_t *images = nullptr;
+    uint32_t *kvmax = nullptr;
+};
+bool kv_images_apply(int kv_format, int d, int heads);
+size_t kv_images_bytes(int rows, int chunk, int heads);
+KvImages kv_images_at(uint8_t *base, int rows, int chunk, int heads);
+void kv_images(hipStream_t s, int rows, int chunk, int d, int heads, const uint8_t *rec32, KvImages img);
+// img (optional): the layer's images, used for 32 queries or more.
+void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t *records, float *out, void *work,
+               const KvImages *img = nullptr);
 
 // Column and row stages (stages.hip).
 void input_cells(hipStream_t s, const tah_weights *w, const float *x, int n, int features, float *cells);

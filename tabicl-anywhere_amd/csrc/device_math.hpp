@@ -6,6 +6,7 @@
 namespace tah {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -22,6 +23,8 @@ __device__ __forceinline__ float wave_max(float v) {
 // GELU as PyTorch defines it by default, x * (1 + erf(x / sqrt 2)) / 2 (src/kern.rs:255-261), with the device
 // library's erff.
 __device__ __forceinline__ float gelu(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f)); }
+
+constexpr float LOG2E = 1.44269504088896340736f;
 
 // e^x for the softmax weights: exp2 of x * log2(e) on the hardware's exp2 unit. Arguments are <= 0 here.
 __device__ __forceinline__ float fast_exp(float x) { return exp2f(x * 1.44269504088896340736f); }

@@ -12,11 +12,22 @@
 
 namespace tah {
 
+// Epilogues: bias, then GELU, or the block's residual add, or the scalable softmax's query modulation
+// (EPI_QMOD: the output is R * scale * (1 + tanh(acc + b)), src/nn.rs:145-149, with R the query projection viewed
+// as [rows * heads][hd] and scale[(m % heads) * hd + n]).
+struct EpiArgs {
+    const float *R;
+    int ldr;
+    const float *scale;
+    int heads;
+};
+
 template <int EPI>
-__device__ __forceinline__ float epilogue(float acc, const float *b, int n, const float *R, int ldr, int m) {
+__device__ __forceinline__ float epilogue(float acc, const float *b, int n, const EpiArgs &e, int m, int N) {
     float y = acc + (b ? b[n] : 0.0f);
     if (EPI == EPI_GELU) y = gelu(y);
-    if (EPI == EPI_RESID) y += R[(size_t)m * ldr + n];
+    if (EPI == EPI_RESID) y += e.R[(size_t)m * e.ldr + n];
+    if (EPI == EPI_QMOD) y = e.R[(size_t)m * e.ldr + n] * (e.scale[(m % e.heads) * N + n] * (1.0f + tanhf(y)));
     return y;
 }
 
@@ -27,7 +38,7 @@ constexpr int GKP = 20;  // padded LDS row
 template <int EPI>
 __global__ __launch_bounds__(256) void k_gemm_mfma(int M, int N, int K, const float *__restrict__ X, int ldx,
                                                     const float *__restrict__ W, const float *__restrict__ b,
-                                                    float *Y, int ldy, const float *R, int ldr) {
+                                                    float *Y, int ldy, EpiArgs ea) {
     __shared__ float As[2][GB][GKP];
     __shared__ float Bs[2][GB][GKP];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -96,7 +107,7 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(int M, int N, int K, const fl
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const int m = m0 + wm * 32 + i * 16 + kq + v;
-                if (m < M && n < N) Y[(size_t)m * ldy + n] = epilogue<EPI>(acc[i][j][v], b, n, R, ldr, m);
+                if (m < M && n < N) Y[(size_t)m * ldy + n] = epilogue<EPI>(acc[i][j][v], b, n, ea, m, N);
             }
         }
 }
@@ -108,7 +119,7 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(int M, int N, int K, const fl
 template <int EPI>
 __global__ __launch_bounds__(256) void k_gemm_skinny(int M, int N, int K, const float *__restrict__ X, int ldx,
                                                       const float *__restrict__ W, const float *__restrict__ b,
-                                                      float *Y, int ldy, const float *R, int ldr) {
+                                                      float *Y, int ldy, EpiArgs ea) {
     __shared__ float red[4][16][17];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int m0 = blockIdx.y * 16, n0 = blockIdx.x * 16;
@@ -136,38 +147,38 @@ __global__ __launch_bounds__(256) void k_gemm_skinny(int M, int N, int K, const 
     const int m = m0 + i, n = n0 + j;
     if (m < M && n < N) {
         const float a = (red[0][i][j] + red[1][i][j]) + (red[2][i][j] + red[3][i][j]);
-        Y[(size_t)m * ldy + n] = epilogue<EPI>(a, b, n, R, ldr, m);
+        Y[(size_t)m * ldy + n] = epilogue<EPI>(a, b, n, ea, m, N);
     }
 }
 
 template <int EPI>
 __global__ __launch_bounds__(256) void k_gemm_plain(int M, int N, int K, const float *__restrict__ X, int ldx,
                                                      const float *__restrict__ W, const float *__restrict__ b,
-                                                     float *Y, int ldy, const float *R, int ldr) {
+                                                     float *Y, int ldy, EpiArgs ea) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (size_t)M * N) return;
     const int m = (int)(i / N), n = (int)(i % N);
     const float *xr = X + (size_t)m * ldx, *wr = W + (size_t)n * K;
     float a = 0.0f;
     for (int k = 0; k < K; k++) a += xr[k] * wr[k];
-    Y[(size_t)m * ldy + n] = epilogue<EPI>(a, b, n, R, ldr, m);
+    Y[(size_t)m * ldy + n] = epilogue<EPI>(a, b, n, ea, m, N);
 }
 
 template <int EPI>
 static void launch(hipStream_t s, int M, int N, int K, const float *X, int ldx, const float *W, const float *b, float *Y,
-                   int ldy, const float *R, int ldr) {
+                   int ldy, EpiArgs ea) {
     const bool aligned = K % 4 == 0 && ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 &&
                          (reinterpret_cast<uintptr_t>(W) & 15) == 0;
     if (aligned && M <= 256) {
         dim3 grid((N + 15) / 16, (M + 15) / 16);
-        hipLaunchKernelGGL(k_gemm_skinny<EPI>, grid, dim3(256), 0, s, M, N, K, X, ldx, W, b, Y, ldy, R, ldr);
+        hipLaunchKernelGGL(k_gemm_skinny<EPI>, grid, dim3(256), 0, s, M, N, K, X, ldx, W, b, Y, ldy, ea);
     } else if (aligned) {
         dim3 grid((N + GB - 1) / GB, (M + GB - 1) / GB);
-        hipLaunchKernelGGL(k_gemm_mfma<EPI>, grid, dim3(256), 0, s, M, N, K, X, ldx, W, b, Y, ldy, R, ldr);
+        hipLaunchKernelGGL(k_gemm_mfma<EPI>, grid, dim3(256), 0, s, M, N, K, X, ldx, W, b, Y, ldy, ea);
     } else {
         const size_t n = (size_t)M * N;
         hipLaunchKernelGGL(k_gemm_plain<EPI>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, M, N, K, X, ldx, W, b,
-                           Y, ldy, R, ldr);
+                           Y, ldy, ea);
     }
     TAH_LAUNCHED();
 }
@@ -175,12 +186,21 @@ static void launch(hipStream_t s, int M, int N, int K, const float *X, int ldx, 
 void gemm(hipStream_t s, int M, int N, int K, const float *X, int ldx, const float *W, const float *b, float *Y, int ldy,
           Epi epi, const float *R, int ldr) {
     if (M <= 0 || N <= 0) return;
-    if ((size_t)M > (size_t)65535 * GB) throw ArgError{"gemm: too many rows for one launch"};
+    if ((size_t)M > (size_t)65535 * 16) throw ArgError{"gemm: too many rows for one launch"};
+    const EpiArgs ea{R, ldr, nullptr, 1};
     switch (epi) {
-        case EPI_NONE: launch<EPI_NONE>(s, M, N, K, X, ldx, W, b, Y, ldy, R, ldr); break;
-        case EPI_GELU: launch<EPI_GELU>(s, M, N, K, X, ldx, W, b, Y, ldy, R, ldr); break;
-        case EPI_RESID: launch<EPI_RESID>(s, M, N, K, X, ldx, W, b, Y, ldy, R, ldr); break;
+        case EPI_NONE: launch<EPI_NONE>(s, M, N, K, X, ldx, W, b, Y, ldy, ea); break;
+        case EPI_GELU: launch<EPI_GELU>(s, M, N, K, X, ldx, W, b, Y, ldy, ea); break;
+        case EPI_RESID: launch<EPI_RESID>(s, M, N, K, X, ldx, W, b, Y, ldy, ea); break;
+        default: throw ArgError{"gemm: unknown epilogue"};
     }
+}
+
+void gemm_qmod(hipStream_t s, int M, int N, int K, const float *X, int ldx, const float *W, const float *b, float *q,
+               const float *scale, int heads) {
+    if (M <= 0 || N <= 0) return;
+    if ((size_t)M > (size_t)65535 * 16) throw ArgError{"gemm: too many rows for one launch"};
+    launch<EPI_QMOD>(s, M, N, K, X, ldx, W, b, q, N, EpiArgs{q, N, scale, heads});
 }
 
 }  // namespace tah

@@ -314,7 +314,8 @@ void column_block(hipStream_t s, const tah_weights *w, const DevBlock &b, float 
     const int M = n * groups;
     layer_norm(s, M, e, cells, e, b.n1w, b.n1b, t, e);
     gemm(s, M, e, e, t, e, b.in_w, b.in_b, q, e, EPI_NONE, nullptr, 0);
-    query_modulate(s, M, b, w->col_scale, q);
+    if ((size_t)b.heads * b.ss_hidden > (size_t)b.ff) throw ArgError{"column stage: query MLP wider than the feed-forward"};
+    query_modulate(s, M, b, w->col_scale, q, mid);
     const int hd = e / b.heads;
     const dim3 grid((n + 63) / 64, b.heads, groups);
     if (hd == 16 && w->inds == 128)

@@ -265,8 +265,10 @@ class VramModel:
         self.features, self.digits = int(features), int(digits)
 
     @staticmethod
-    def model_bytes(kv_format: int, rows: int, chunk: int, d: int, layers: int) -> int:
-        return int(abi.lib().tah_model_bytes(kv_format, rows, chunk, d, layers))
+    def model_bytes(weights: "GpuWeights", kv_format: int, rows: int, chunk: int) -> int:
+        """Card bytes a problem of `rows` stored rows takes once loaded (`Gpu::model_bytes`, src/gpu.rs:2064-2068):
+        the records as stored, plus for f32 records of head width 64 their split-fp16 tile images."""
+        return int(abi.lib().tah_model_bytes(weights._h, kv_format, rows, chunk))
 
     def free(self) -> None:
         if getattr(self, "_h", None):

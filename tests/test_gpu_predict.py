@@ -71,6 +71,48 @@ def test_attention_full_width(gpu, full_model, full_weights, kv_format, rows, ch
     assert err < SCORE_TOL
 
 
+@pytest.mark.parametrize("kv_scale,q_scale", [(2000.0, 1e-4), (1e-3, 300.0), (1.0, 1.0)])
+def test_attention_magnitudes(gpu, full_model, full_weights, kv_scale, q_scale):
+    """Keys, values and queries far from unit size, and heads of different sizes (each head's coordinates scaled by
+    4^h): the split-fp16 path's power-of-two scaling keeps f32 accuracy, relative to the outputs' size."""
+    say(f"attention magnitudes kv={kv_scale} q={q_scale}")
+    rng = np.random.default_rng(int(kv_scale * 10) + 3)
+    d, L, heads = full_model.d, full_model.icl_layers, full_model.icl_heads
+    rows, chunk, nq = 3000, 256, 96
+    per_dim = np.repeat(4.0 ** (np.arange(heads) - heads // 2), d // heads).astype(np.float32)
+    parts = []
+    for c0 in range(0, rows, chunk):
+        rc = min(chunk, rows - c0)
+        kv = rng.standard_normal((2, d, rc)).astype(np.float32) * np.float32(kv_scale)
+        kv[0] *= per_dim[:, None]
+        kv[1] *= per_dim[:, None]
+        parts.append(orc.pack(kv.reshape(-1), d, rc, abi.KV_F32))
+    layers = [np.concatenate(parts)] * L
+    vm = gpu.load(full_weights, abi.KV_F32, rows, chunk, layers, np.ones((L, d), np.float32))
+    q = (rng.standard_normal((nq, d)) * q_scale / per_dim).astype(np.float32)  # scores stay of moderate size
+    got = gpu.attend_resident(vm, 0, q)
+    want = orc.attend_records(q, layers[0], abi.KV_F32, rows, chunk, d, heads)
+    vm.free()
+    for h in range(heads):
+        sl = slice(h * 64, (h + 1) * 64)
+        size = np.abs(want[:, sl]).max()
+        err = np.abs(got[:, sl] - want[:, sl]).max()
+        say(f"  head {h}: worst {err:.3g} of {size:.3g}")
+        assert err <= 2e-5 * size, h
+
+
+def test_model_bytes(gpu, full_weights):
+    """Gpu::model_bytes: stored records per layer (the published sizes at 10,000 rows, chunk 256), plus the
+    split-fp16 tile images of f32 layers (157 key blocks x 8 heads x 32 KB each), plus the query scales."""
+    f32 = hip.VramModel.model_bytes(full_weights, abi.KV_F32, 10000, 256)
+    i16 = hip.VramModel.model_bytes(full_weights, abi.KV_I16, 10000, 256)
+    images = 157 * 8 * 32768
+    assert f32 >= 12 * (40_960_000 + images)
+    assert f32 < 12 * (40_960_000 + images + 4096) + 4 * 12 * 512 + 256
+    assert 12 * 20_643_840 <= i16 < 12 * (20_643_840 + 256) + 4 * 12 * 512 + 256
+    assert hip.VramModel.model_bytes(full_weights, abi.KV_F32, 0, 256) == 0
+
+
 @pytest.mark.parametrize("kv_format", [abi.KV_F32, abi.KV_I16, abi.KV_I8])
 def test_attention_tiny_width(gpu, tiny_model, kv_format):
     """Head width 8 (the tiny model): the decode kernel at any query count."""

@@ -119,6 +119,34 @@ def test_stages_full_size(gpu, full_model, full_weights, features):
     assert err < TOL * max(1.0, np.abs(want).max())
 
 
+def test_stages_many_cells(gpu, full_model, full_weights):
+    """Many cells (72,000) and tokens (168,000): the column and row stages' dense layers and attention over grids of
+    thousands of workgroups, embed and represent against the oracle."""
+    say("stages many cells")
+    m = full_model
+    rng = np.random.default_rng(77)
+    features, n = 3, 24000
+    col_kv = (rng.standard_normal((features, 1, len(m.col_a2), 2, m.e, m.inds)) * 0.5).astype(np.float32)
+    scales = np.stack([orc.query_scale(b, 64) for b in m.icl])
+    layers = [orc.pack((rng.standard_normal(2 * m.d * 64) * 0.5).astype(np.float32), m.d, 64, abi.KV_F32)
+              for _ in range(m.icl_layers)]
+    vm = gpu.load(full_weights, abi.KV_F32, 64, 64, layers, scales)
+    vm.set_columns(col_kv, features, 1)
+    x = rng.standard_normal((n, features)).astype(np.float32)
+    fitted = orc.Fitted(64, features, 10, 64, abi.KV_F32, planmod.Plan([10], [planmod.Node(None, [], 10, True, list(range(10)))]),
+                        col_kv, [scales], [layers])
+    tok = gpu.embed(full_weights, vm, x)
+    want_tok = orc.embed(m, fitted, x)
+    err = np.abs(tok - want_tok).max()
+    say("  embed worst", err, "scale", np.abs(want_tok).max())
+    assert err < TOL * max(1.0, np.abs(want_tok).max())
+    rep = gpu.represent(full_weights, want_tok)
+    want_rep = orc.represent(m, want_tok)
+    err = np.abs(rep - want_rep).max()
+    say("  represent worst", err)
+    assert err < TOL
+
+
 def test_sub_batches_give_the_same_answers(gpu, tiny_model, tiny_raw):
     """A working-memory budget that forces sub-batches of rows changes no answer beyond rounding
     (tests/card.rs:237-274), and a budget too small for one row is an OutOfMemory error."""
