@@ -460,8 +460,9 @@ __global__ __launch_bounds__(256) void k_attn_decode64(int nq, int rows, int chu
 
 // ---- tile images: f32 keys and values split into fp16 halves, laid out as the split kernel's LDS image -------
 // One image per (key block, head), 32 KB: K hi, K lo as [64 keys][64 coordinates] and V hi, V lo as
-// [64 coordinates][64 keys], fp16, each 128-byte row split in eight 16-byte chunks stored XOR-swizzled by row (the
-// lanes of one LDS read then hit eight different chunks). Keys past the end of a short block are zeros. Each head's
+// [64 coordinates][64 keys], fp16, each 128-byte row split in eight 16-byte chunks stored XOR-swizzled by row: the
+// 64-bank LDS serves a 128-bit read 16 lanes at a time, and the 16 rows one such group reads (at one logical chunk)
+// then fall on 16 different 16-byte bank groups. Keys past the end of a short block are zeros. Each head's
 // keys are scaled by 2^sk and values by 2^sv, the powers of two that bring the layer's largest magnitude of that
 // head below 2^14; kvmax holds those maxima (f32 bits) per head, [heads][2].
 typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
@@ -471,8 +472,9 @@ __host__ __device__ inline size_t image_bytes_of(int rows, int chunk, int heads)
     return (size_t)key_blocks(rows, chunk).n_kb * heads * IMG;
 }
 
-__device__ __forceinline__ int kswz(int r, int c) { return c ^ ((r & 3) | (((r >> 3) & 1) << 2)); }
-__device__ __forceinline__ int vswz(int r, int c) { return c ^ (r & 7); }
+// rows r and r + 1 already sit in different bank halves (128-byte rows); rows of one parity among 16 consecutive ones
+// get eight different chunks
+__device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 7); }
 
 // 14 - e for max = m 2^e, m in [0.5, 1): scaling by 2^(14 - e) leaves every magnitude below 2^14.
 __device__ __forceinline__ int shift_for(uint32_t max_bits) {
@@ -554,30 +556,65 @@ __global__ __launch_bounds__(256) void k_kv_images(int rows, int chunk, int d, i
             vh[t] = yh;
             vl[t] = (_Float16)(y - (float)yh);
         }
-        *reinterpret_cast<halfx8 *>(img + r * 128 + kswz(r, c) * 16) = kh;
-        *reinterpret_cast<halfx8 *>(img + 8192 + r * 128 + kswz(r, c) * 16) = kl;
-        *reinterpret_cast<halfx8 *>(img + 16384 + r * 128 + vswz(r, c) * 16) = vh;
-        *reinterpret_cast<halfx8 *>(img + 24576 + r * 128 + vswz(r, c) * 16) = vl;
+        *reinterpret_cast<halfx8 *>(img + r * 128 + swz(r, c) * 16) = kh;
+        *reinterpret_cast<halfx8 *>(img + 8192 + r * 128 + swz(r, c) * 16) = kl;
+        *reinterpret_cast<halfx8 *>(img + 16384 + r * 128 + swz(r, c) * 16) = vh;
+        *reinterpret_cast<halfx8 *>(img + 24576 + r * 128 + swz(r, c) * 16) = vl;
     }
 }
 
 // ---- split-fp16 MFMA kernel: head width 64 over tile images --------------------------------------------------
-// A flat grid of qtiles x heads x splits workgroups (remapped XCD by XCD as in k_attn_mfma64) of 4 wavefronts x 32
-// queries. Per key block of 64, the block's 32 KB image is copied into LDS (the next one already in registers),
-// then each wavefront forms S^T = K Q^T for two halves of 32 keys with v_mfma_f32_32x32x16_f16: lane l owns query
-// l % 32 and holds 16 of the half's keys. The A operand's row i takes key sigma(i) (bits 3 and 2 of i swapped),
-// which puts eight consecutive keys (16 (v / 8) + 8 (l / 32) + v % 8) in each lane's accumulators v = 8 hh..8 hh + 7:
-// exactly the B operand that O^T = V^T P^T needs for a reduction over 16 keys, so the weights never leave the lane.
+// A flat grid of qtiles x heads x splits workgroups (remapped XCD by XCD as in k_attn_mfma64) of SPLIT_WAVES
+// wavefronts x 32 queries (two workgroups a compute unit: their two 32 KB buffers each fill 128 of the 160 KB LDS;
+// six wavefronts, at three a SIMD, measured slower). Key blocks of 64 stream through two LDS buffers: the next block's 32 KB image is copied global -> LDS
+// directly (global_load_lds_dwordx4) while the current one is multiplied, one barrier per block. Each wavefront
+// forms S^T = K Q^T for two halves of 32 keys with v_mfma_f32_32x32x16_f16: lane l owns query l % 32 and holds 16 of
+// the half's keys. The A operand's row i takes key sigma(i) (bits 3 and 2 of i swapped), which puts eight
+// consecutive keys (16 (v / 8) + 8 (l / 32) + v % 8) in each lane's accumulators v = 8 hh..8 hh + 7: exactly the B
+// operand that O^T = V^T P^T needs for a reduction over 16 keys, so the weights never leave the lane.
+//
+// The softmax runs in log2 units against a reference maximum that is raised only when a block's maximum passes it by
+// more than 3 (then the sums are rescaled): weights exp2(t - ref + 12) stay below 2^15, inside fp16, and most blocks
+// skip the rescaling.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ floatx16 mfma16(halfx8 a, halfx8 b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-__global__ __launch_bounds__(256) void k_attn_split64(int nq, int rows, int chunk, int d, int heads,
-                                                       const float *__restrict__ q, const uint8_t *__restrict__ images,
-                                                       const uint32_t *__restrict__ kvmax, int kb_per_split,
-                                                       int qtiles, int splits, float *__restrict__ part_o,
-                                                       float *__restrict__ part_ml, float *__restrict__ out) {
-    __shared__ __align__(16) uint8_t tile[IMG];
+__device__ __forceinline__ uint32_t bits(fp16x2 h) { return __builtin_bit_cast(uint32_t, h); }
+
+// hi/lo fp16 halves of two floats, hi rounded toward zero (the residual x - hi is exact in f32)
+__device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t &lo) {
+    const fp16x2 h = __builtin_amdgcn_cvt_pkrtz(a, b);
+    hi = bits(h);
+    lo = bits(__builtin_amdgcn_cvt_pkrtz(a - (float)h.x, b - (float)h.y));
+}
+
+// One key block's 32 KB image into an LDS buffer, 16 bytes a lane: in copy i, wavefront w fills the 1 KB at chunk
+// 64 (WAVES i + w) (a wavefront-uniform LDS base; the lanes' offsets are implicit).
+template <int WAVES>
+__device__ __forceinline__ void image_to_lds(const uint8_t *src, uint8_t *dst, int tid) {
+    constexpr int T = 64 * WAVES, CHUNKS = IMG / 16;
+    const int w = tid >> 6;
+#pragma unroll
+    for (int i = 0; i < (CHUNKS + T - 1) / T; i++) {
+        const int base = i * T + 64 * w;
+        if (CHUNKS % T == 0 || base < CHUNKS)
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4 *>(src) + base + (tid & 63), dst + 16 * base, 16,
+                                             0, 0);
+    }
+}
+
+template <int WAVES>
+__global__ __launch_bounds__(64 * WAVES, (WAVES * 2 + 3) / 4) void k_attn_split64(int nq, int rows, int chunk, int d, int heads,
+                                                          const float *__restrict__ q,
+                                                          const uint8_t *__restrict__ images,
+                                                          const uint32_t *__restrict__ kvmax, int kb_per_split,
+                                                          int qtiles, int splits, float *__restrict__ part_o,
+                                                          float *__restrict__ part_ml, float *__restrict__ out) {
+    __shared__ __align__(16) uint8_t tiles[2][IMG];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int total = qtiles * heads * splits;
     int flat = blockIdx.x;
@@ -587,8 +624,11 @@ __global__ __launch_bounds__(256) void k_attn_split64(int nq, int rows, int chun
     const KeyBlocks kbs = key_blocks(rows, chunk);
     const int kb0 = split * kb_per_split, kb1 = min(kbs.n_kb, kb0 + kb_per_split);
     const int r32 = lane & 31, g = lane >> 5;
-    const int qrow = qt * 128 + wave * 32 + r32;
+    const int qrow = qt * 32 * WAVES + wave * 32 + r32;
     const bool qlive = qrow < nq;
+    const uint8_t *head_images = images + (size_t)h * IMG;
+    const size_t kb_stride = (size_t)heads * IMG;
+    if (kb0 < kb1) image_to_lds<WAVES>(head_images + kb0 * kb_stride, tiles[0], tid);
 
     // this lane's query coordinates 16 dc + 8 g + t, scaled to a maximum magnitude near 2^14 and split
     float qv[4][8];
@@ -612,89 +652,99 @@ __global__ __launch_bounds__(256) void k_attn_split64(int nq, int rows, int chun
     const int eq = shift_for(__float_as_uint(qmax));
     halfx8 qh[4], ql[4];
 #pragma unroll
-    for (int dc = 0; dc < 4; dc++)
+    for (int dc = 0; dc < 4; dc++) {
+        u32x4 hw, lw;
 #pragma unroll
-        for (int t = 0; t < 8; t++) {
-            const float x = ldexpf(qv[dc][t], eq);
-            const _Float16 xh = (_Float16)x;
-            qh[dc][t] = xh;
-            ql[dc][t] = (_Float16)(x - (float)xh);
+        for (int t = 0; t < 4; t++) {
+            uint32_t hi, lo;
+            split2(ldexpf(qv[dc][2 * t], eq), ldexpf(qv[dc][2 * t + 1], eq), hi, lo);
+            hw[t] = hi;
+            lw[t] = lo;
         }
+        qh[dc] = __builtin_bit_cast(halfx8, hw);
+        ql[dc] = __builtin_bit_cast(halfx8, lw);
+    }
     const int sk = shift_for(kvmax[h * 2]), sv = shift_for(kvmax[h * 2 + 1]);
     const float to_log2 = ldexpf(LOG2E, -(sk + eq));  // raw score -> score * log2 e
 
     // A-operand row of this lane in a 32-key half: key sigma(r32)
     const int krow = (r32 & 16) | ((r32 & 4) << 1) | ((r32 & 8) >> 1) | (r32 & 3);
-    float m = -INFINITY, l = 0.0f;
+    float ref = -INFINITY, l = 0.0f;
     floatx16 acc_o[2];
 #pragma unroll
     for (int db = 0; db < 2; db++)
 #pragma unroll
         for (int v = 0; v < 16; v++) acc_o[db][v] = 0.0f;
-
-    uint4 pre[8];
-    auto fetch = [&](int kb) {
-        const uint4 *src = reinterpret_cast<const uint4 *>(images + ((size_t)kb * heads + h) * IMG);
+    floatx16 zero;
 #pragma unroll
-        for (int i = 0; i < 8; i++) pre[i] = src[tid + 256 * i];
-    };
-    if (kb0 < kb1) fetch(kb0);
-    for (int kb = kb0; kb < kb1; kb++) {
+    for (int v = 0; v < 16; v++) zero[v] = 0.0f;
+
+    int buf = 0;
+    for (int kb = kb0; kb < kb1; kb++, buf ^= 1) {
         const int ci = kb / kbs.bpc;
         const int nk = min(KB, (ci == kbs.n_chunks - 1 ? kbs.last_rc : chunk) - (kb % kbs.bpc) * KB);
-        __syncthreads();  // the previous image is no longer read
-#pragma unroll
-        for (int i = 0; i < 8; i++) reinterpret_cast<uint4 *>(tile)[tid + 256 * i] = pre[i];
-        if (kb + 1 < kb1) fetch(kb + 1);
-        __syncthreads();
+        __builtin_amdgcn_s_waitcnt(0);  // this wavefront's copies of block kb have landed
+        __syncthreads();                // everyone's have, and block kb - 1's buffer is no longer read
+        if (kb + 1 < kb1) image_to_lds<WAVES>(head_images + (kb + 1) * kb_stride, tiles[buf ^ 1], tid);
+        const uint8_t *tile = tiles[buf];
         // S^T for keys 32 kh + sigma(i)
         floatx16 sc[2];
 #pragma unroll
         for (int kh = 0; kh < 2; kh++) {
-#pragma unroll
-            for (int v = 0; v < 16; v++) sc[kh][v] = 0.0f;
             const int r = 32 * kh + krow;
 #pragma unroll
             for (int dc = 0; dc < 4; dc++) {
-                const int off = r * 128 + kswz(r, 2 * dc + g) * 16;
+                const int off = r * 128 + swz(r, 2 * dc + g) * 16;
                 const halfx8 khi = *reinterpret_cast<const halfx8 *>(tile + off);
                 const halfx8 klo = *reinterpret_cast<const halfx8 *>(tile + 8192 + off);
-                sc[kh] = mfma16(khi, qh[dc], sc[kh]);
+                sc[kh] = mfma16(khi, qh[dc], dc == 0 ? zero : sc[kh]);
                 sc[kh] = mfma16(khi, ql[dc], sc[kh]);
                 sc[kh] = mfma16(klo, qh[dc], sc[kh]);
             }
         }
-        // online softmax in log2 units; accumulator v of half kh holds key 32 kh + 16 (v / 8) + 8 g + v % 8
+        // accumulator v of half kh holds key 32 kh + 16 (v / 8) + 8 g + v % 8; raw scores order as scores
         float mb = -INFINITY;
+        if (nk < KB) {
+#pragma unroll
+            for (int kh = 0; kh < 2; kh++)
+#pragma unroll
+                for (int v = 0; v < 16; v++)
+                    if (32 * kh + 16 * (v >> 3) + 8 * g + (v & 7) >= nk) sc[kh][v] = -INFINITY;
+        }
 #pragma unroll
         for (int kh = 0; kh < 2; kh++)
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int key = 32 * kh + 16 * (v >> 3) + 8 * g + (v & 7);
-                const float t = key < nk ? sc[kh][v] * to_log2 : -INFINITY;
-                sc[kh][v] = t;
-                mb = fmaxf(mb, t);
-            }
-        mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
-        const float mnew = fmaxf(m, mb);
-        const float alpha = exp2f(m - mnew);
-        const float moff = mnew - 12.0f;  // weights scaled by 2^12: at most 4096
-        float lb = 0.0f;
+            for (int v = 0; v < 16; v++) mb = fmaxf(mb, sc[kh][v]);
+        mb = fmaxf(mb, __shfl_xor(mb, 32, 64)) * to_log2;
+        const bool grow = mb > ref + 3.0f;
+        if (__any(grow)) {
+            const float nref = grow ? mb : ref;
+            const float alpha = exp2_hw(ref - nref);
+            l *= alpha;
+#pragma unroll
+            for (int db = 0; db < 2; db++) acc_o[db] *= alpha;
+            ref = nref;
+        }
+        const float off = 12.0f - ref;
         halfx8 ph[2][2], pl[2][2];
 #pragma unroll
         for (int kh = 0; kh < 2; kh++)
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const float p = exp2f(sc[kh][v] - moff);
-                lb += p;
-                const _Float16 hi = (_Float16)p;
-                ph[kh][v >> 3][v & 7] = hi;
-                pl[kh][v >> 3][v & 7] = (_Float16)(p - (float)hi);
-            }
-        l = l * alpha + lb;  // this lane's half of the keys; the halves are added at the end
-        m = mnew;
+            for (int hh = 0; hh < 2; hh++) {
+                u32x4 hw, lw;
 #pragma unroll
-        for (int db = 0; db < 2; db++) acc_o[db] *= alpha;
+                for (int t = 0; t < 4; t++) {
+                    const float p0 = exp2_hw(fmaf(sc[kh][8 * hh + 2 * t], to_log2, off));
+                    const float p1 = exp2_hw(fmaf(sc[kh][8 * hh + 2 * t + 1], to_log2, off));
+                    l += p0 + p1;
+                    uint32_t hi, lo;
+                    split2(p0, p1, hi, lo);
+                    hw[t] = hi;
+                    lw[t] = lo;
+                }
+                ph[kh][hh] = __builtin_bit_cast(halfx8, hw);
+                pl[kh][hh] = __builtin_bit_cast(halfx8, lw);
+            }
         // O^T += V^T P^T over four 16-key steps
 #pragma unroll
         for (int db = 0; db < 2; db++) {
@@ -703,7 +753,7 @@ __global__ __launch_bounds__(256) void k_attn_split64(int nq, int rows, int chun
             for (int kh = 0; kh < 2; kh++)
 #pragma unroll
                 for (int hh = 0; hh < 2; hh++) {
-                    const int off = r * 128 + vswz(r, 4 * kh + 2 * hh + g) * 16;
+                    const int off = r * 128 + swz(r, 4 * kh + 2 * hh + g) * 16;
                     const halfx8 vhi = *reinterpret_cast<const halfx8 *>(tile + 16384 + off);
                     const halfx8 vlo = *reinterpret_cast<const halfx8 *>(tile + 24576 + off);
                     acc_o[db] = mfma16(vhi, ph[kh][hh], acc_o[db]);
@@ -735,7 +785,7 @@ __global__ __launch_bounds__(256) void k_attn_split64(int nq, int rows, int chun
                     make_float4(acc_o[db][4 * v4] * unscale, acc_o[db][4 * v4 + 1] * unscale,
                                 acc_o[db][4 * v4 + 2] * unscale, acc_o[db][4 * v4 + 3] * unscale);
         if (g == 0) {
-            part_ml[at * 2] = m;
+            part_ml[at * 2] = ref;
             part_ml[at * 2 + 1] = l;
         }
     }
@@ -765,7 +815,7 @@ __global__ __launch_bounds__(64) void k_attn_merge(int nq, int d, int heads, int
             const size_t at = s * stride + base;
             const float ls = part_ml[at * 2 + 1];
             const float dm = part_ml[at * 2] - M;
-            const float f = ls > 0.0f ? (log2_units ? exp2f(dm) : fast_exp(dm)) : 0.0f;
+            const float f = ls > 0.0f ? (log2_units ? exp2_hw(dm) : fast_exp(dm)) : 0.0f;
             L += ls * f;
             O += part_o[at * hd + c] * f;
         }
@@ -812,13 +862,16 @@ KvImages kv_images_at(uint8_t *base, int rows, int chunk, int heads) {
     return img;
 }
 
+constexpr int SPLIT_WAVES = 4;
+
 static AttnPlan plan(const AttnShape &a, bool images) {
     AttnPlan p;
     const KeyBlocks k = key_blocks(a.rows, a.chunk);
     const int hd = a.d / a.heads;
     p.mfma = hd == 64 && a.nq >= 32;
     p.split16 = p.mfma && images && kv_images_apply(a.kv_format, a.d, a.heads);
-    p.groups = p.mfma ? (a.nq + 64 * QW - 1) / (64 * QW) : (a.nq + QG - 1) / QG;
+    const int per_group = p.split16 ? 32 * SPLIT_WAVES : (p.mfma ? 64 * QW : QG);
+    p.groups = (a.nq + per_group - 1) / per_group;
     // enough workgroups to fill 256 compute units a few times over, each with at least 2 key blocks
     const long target = 1024;
     long want = (target + (long)p.groups * a.heads - 1) / ((long)p.groups * a.heads);
@@ -829,7 +882,8 @@ static AttnPlan plan(const AttnShape &a, bool images) {
 }
 
 size_t attention_work_bytes(const AttnShape &a) {
-    const AttnPlan p = plan(a, false);  // the split count does not depend on the kernel
+    const AttnPlan p0 = plan(a, false), p1 = plan(a, true);  // either kernel may run
+    const AttnPlan &p = p0.splits > p1.splits ? p0 : p1;
     if (p.splits == 1) return 0;
     const int hd = a.d / a.heads;
     return sizeof(float) * (size_t)p.splits * a.nq * a.heads * (hd + 2) + 256;
@@ -865,7 +919,8 @@ void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t 
         part_ml = part_o + (size_t)p.splits * a.nq * a.heads * hd;
     }
     if (p.split16) {
-        hipLaunchKernelGGL(k_attn_split64, dim3(p.groups * a.heads * p.splits), dim3(256), 0, s, a.nq, a.rows, a.chunk,
+        hipLaunchKernelGGL(k_attn_split64<SPLIT_WAVES>, dim3(p.groups * a.heads * p.splits), dim3(64 * SPLIT_WAVES), 0, s,
+                           a.nq, a.rows, a.chunk,
                            a.d, a.heads, q, img->images, img->kvmax, p.kb_per_split, p.groups, p.splits, part_o, part_ml,
                            out);
         TAH_LAUNCHED();

@@ -26,7 +26,11 @@ __device__ __forceinline__ float gelu(float x) { return 0.5f * x * (1.0f + erff(
 
 constexpr float LOG2E = 1.44269504088896340736f;
 
+// 2^x straight from v_exp_f32 (1 ulp): results below 2^-126, which only ever weight a softmax term, flush to 0
+// instead of taking exp2f's denormal rescaling path.
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // e^x for the softmax weights: exp2 of x * log2(e) on the hardware's exp2 unit. Arguments are <= 0 here.
-__device__ __forceinline__ float fast_exp(float x) { return exp2f(x * 1.44269504088896340736f); }
+__device__ __forceinline__ float fast_exp(float x) { return exp2_hw(x * LOG2E); }
 
 }  // namespace tah
