@@ -1,7 +1,9 @@
 // The C ABI (include/tah.h): device handles, working memory, weights and fitted models on the card, and the
 // in-context passes built from the kernels. Host code only; every kernel lives in the other sources.
 #include <algorithm>
+#include <cmath>
 #include <cstring>
+#include <memory>
 #include <new>
 
 #include "common.hpp"
@@ -204,21 +206,52 @@ namespace {
 // Lays tensors out in one device allocation (each 256-byte aligned), then copies them in.
 struct Packer {
     struct Item {
-        const float *src;
-        size_t n;
-        const float **dst;
+        const void *src;
+        size_t bytes;
+        const void **dst;
     };
     std::vector<Item> items;
+    std::vector<std::unique_ptr<std::vector<uint8_t>>> owned;  // buffers made here (weight images)
     size_t bytes = 0;
     void add(const float *src, size_t n, const float **dst) {
         if (!src || n == 0) {
             *dst = nullptr;
             return;
         }
-        items.push_back({src, n, dst});
+        items.push_back({src, n * sizeof(float), reinterpret_cast<const void **>(dst)});
         bytes += align256(n * sizeof(float));
     }
+    void add_bytes(std::vector<uint8_t> &&buf, const uint8_t **dst) {
+        owned.push_back(std::make_unique<std::vector<uint8_t>>(std::move(buf)));
+        items.push_back({owned.back()->data(), owned.back()->size(), reinterpret_cast<const void **>(dst)});
+        bytes += align256(owned.back()->size());
+    }
 };
+
+// W [N][K] (N a multiple of 128, K of 16) scaled by 2^shift (its largest magnitude below 2^14) and split into fp16
+// hi/lo, in the order the fused blocks stream it through LDS: per block of 128 rows rb, per 16 columns ks,
+// [hi, lo][k half g][row n of the block][8 halves of W[128 rb + n][16 ks + 8 g + t]] (8 KB a step).
+static std::vector<uint8_t> weight_image(const float *W, int N, int K, int &shift) {
+    float mx = 0.0f;
+    for (size_t i = 0; i < (size_t)N * K; i++) mx = std::max(mx, std::fabs(W[i]));
+    int e = 0;
+    (void)std::frexp(mx, &e);
+    shift = 14 - e;
+    const float f = std::ldexp(1.0f, shift);
+    std::vector<uint8_t> out((size_t)N * K * 4);
+    _Float16 *o = reinterpret_cast<_Float16 *>(out.data());
+    for (int rb = 0; rb < N / 128; rb++)
+        for (int ks = 0; ks < K / 16; ks++)
+            for (int part = 0; part < 2; part++)
+                for (int g = 0; g < 2; g++)
+                    for (int n = 128 * rb; n < 128 * rb + 128; n++)
+                        for (int t = 0; t < 8; t++) {
+                            const float x = W[(size_t)n * K + 16 * ks + 8 * g + t] * f;
+                            const _Float16 hi = (_Float16)x;
+                            *o++ = part == 0 ? hi : (_Float16)(x - (float)hi);
+                        }
+    return out;
+}
 
 void add_block(Packer &pk, const tah_block &b, DevBlock &o) {
     o.d = b.d;
@@ -249,6 +282,11 @@ void add_block(Packer &pk, const tah_block &b, DevBlock &o) {
         pk.add(b.q2b, hd, &o.q2b);
     } else {
         o.b0w = o.b0b = o.b2w = o.b2b = o.q0w = o.q0b = o.q2w = o.q2b = nullptr;
+    }
+    o.l1img = o.l2img = nullptr;
+    if (ff_fused_shape(b.d, b.ff) && b.l1w && b.l2w) {
+        pk.add_bytes(weight_image(b.l1w, b.ff, b.d, o.l1s), &o.l1img);
+        pk.add_bytes(weight_image(b.l2w, b.d, b.ff, o.l2s), &o.l2img);
     }
 }
 
@@ -330,10 +368,10 @@ extern "C" int tah_weights_upload(tah_dev *dev, const tah_model_desc *m, tah_wei
             w->bytes = pk.bytes;
             size_t at = 0;
             for (auto &it : pk.items) {
-                float *dst = reinterpret_cast<float *>(static_cast<char *>(w->arena) + at);
-                TAH_HIP(hipMemcpy(dst, it.src, it.n * sizeof(float), hipMemcpyHostToDevice));
+                void *dst = static_cast<char *>(w->arena) + at;
+                TAH_HIP(hipMemcpy(dst, it.src, it.bytes, hipMemcpyHostToDevice));
                 *it.dst = dst;
-                at += align256(it.n * sizeof(float));
+                at += align256(it.bytes);
             }
         } catch (...) {
             if (w->arena) (void)hipFree(w->arena);

@@ -465,7 +465,6 @@ __global__ __launch_bounds__(256) void k_attn_decode64(int nq, int rows, int chu
 // then fall on 16 different 16-byte bank groups. Keys past the end of a short block are zeros. Each head's
 // keys are scaled by 2^sk and values by 2^sv, the powers of two that bring the layer's largest magnitude of that
 // head below 2^14; kvmax holds those maxima (f32 bits) per head, [heads][2].
-typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
 constexpr int IMG = 32768;
 
 __host__ __device__ inline size_t image_bytes_of(int rows, int chunk, int heads) {
@@ -475,13 +474,6 @@ __host__ __device__ inline size_t image_bytes_of(int rows, int chunk, int heads)
 // rows r and r + 1 already sit in different bank halves (128-byte rows); rows of one parity among 16 consecutive ones
 // get eight different chunks
 __device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 7); }
-
-// 14 - e for max = m 2^e, m in [0.5, 1): scaling by 2^(14 - e) leaves every magnitude below 2^14.
-__device__ __forceinline__ int shift_for(uint32_t max_bits) {
-    int e = 0;
-    (void)frexpf(__uint_as_float(max_bits), &e);
-    return 14 - e;
-}
 
 __global__ __launch_bounds__(64) void k_zero_u32(int n, uint32_t *__restrict__ p) {
     const int i = blockIdx.x * 64 + threadIdx.x;
@@ -576,22 +568,6 @@ __global__ __launch_bounds__(256) void k_kv_images(int rows, int chunk, int d, i
 // The softmax runs in log2 units against a reference maximum that is raised only when a block's maximum passes it by
 // more than 3 (then the sums are rescaled): weights exp2(t - ref + 12) stay below 2^15, inside fp16, and most blocks
 // skip the rescaling.
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ floatx16 mfma16(halfx8 a, halfx8 b, floatx16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ uint32_t bits(fp16x2 h) { return __builtin_bit_cast(uint32_t, h); }
-
-// hi/lo fp16 halves of two floats, hi rounded toward zero (the residual x - hi is exact in f32)
-__device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t &lo) {
-    const fp16x2 h = __builtin_amdgcn_cvt_pkrtz(a, b);
-    hi = bits(h);
-    lo = bits(__builtin_amdgcn_cvt_pkrtz(a - (float)h.x, b - (float)h.y));
-}
-
 // One key block's 32 KB image into an LDS buffer, 16 bytes a lane: in copy i, wavefront w fills the 1 KB at chunk
 // 64 (WAVES i + w) (a wavefront-uniform LDS base; the lanes' offsets are implicit).
 template <int WAVES>
@@ -668,7 +644,7 @@ __global__ __launch_bounds__(64 * WAVES, (WAVES * 2 + 3) / 4) void k_attn_split6
     const float to_log2 = ldexpf(LOG2E, -(sk + eq));  // raw score -> score * log2 e
 
     // A-operand row of this lane in a 32-key half: key sigma(r32)
-    const int krow = (r32 & 16) | ((r32 & 4) << 1) | ((r32 & 8) >> 1) | (r32 & 3);
+    const int krow = sigma32(r32);
     float ref = -INFINITY, l = 0.0f;
     floatx16 acc_o[2];
 #pragma unroll

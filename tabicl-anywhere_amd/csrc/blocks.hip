@@ -1,0 +1,219 @@
+// Fused transformer sub-blocks for the column and row stages, on the fp16 matrix cores with split f32 operands.
+//
+// The feed-forward sub-block x += l2(gelu(l1(layer_norm2(x)))) (src/nn.rs:154-170 after the attention; the
+// reference runs it as kern::layer_norm, two kern::linear and kern::gelu passes, src/predict.rs:233-246) runs as one
+// kernel for width 128 and hidden width 256, the shape of the full-size column and row blocks:
+//
+//  * each wavefront owns 32 rows and keeps them in registers from start to end; the products are formed transposed,
+//    H^T = W1 X^T and Y^T = W2 H^T, with the rows as the B operand (lane l holds row l % 32, eight consecutive
+//    columns 8 (l / 32) + 0..7 of each 16-column step);
+//  * the A operands, the weights, are read with their rows in sigma32 order, which leaves each lane's accumulators
+//    holding eight consecutive hidden units: exactly the B operand of the second product, so the hidden layer
+//    never leaves the registers;
+//  * the weights stream through two 16 KB LDS buffers, one slice per step, copied global -> LDS by DMA
+//    (global_load_lds_dwordx4) and shared by the workgroup's four wavefronts. They are stored pre-split at upload
+//    in exactly the order of those slices (weight_image in the C ABI: blocks of 128 rows, then 16-column steps);
+//  * the first product runs in two halves of 128 hidden units, each finished (bias, GELU, split) before the next,
+//    so that at most 64 accumulators and half the hidden layer are live at once;
+//  * layer normalisation needs each row's sums: a row's 128 values sit on lanes l and l + 32, so one cross-lane step;
+//  * each row is scaled by its own power of two before splitting (its largest magnitude below 2^14; each half of
+//    the hidden layer by its own), the weights by one per matrix; the products are unscaled in the epilogues.
+#include "common.hpp"
+#include "device_math.hpp"
+
+namespace tah {
+
+constexpr int SLAB = 16384;  // one weight slice in LDS
+
+// bytes (a multiple of 4 KB) from global to LDS by 256 threads, 16 bytes a lane; wavefront w's 64 lanes fill the
+// 1 KB at 4096 i + 1024 w of copy i (a wavefront-uniform LDS base, the lanes' offsets implicit)
+__device__ __forceinline__ void dma_to_lds(const uint8_t *src, uint8_t *dst, int bytes, int tid) {
+    for (int o = 0; o < bytes; o += 4096)
+        __builtin_amdgcn_global_load_lds(src + o + 16 * tid, dst + o + 1024 * (tid >> 6), 16, 0, 0);
+}
+
+// grid ceil(M / 128); 256 threads. x [M][128] in place.
+__global__ __launch_bounds__(256, 2) void k_ff128(int M, float *__restrict__ x, const float *__restrict__ lnw,
+                                                   const float *__restrict__ lnb, const uint8_t *__restrict__ w1img,
+                                                   const float *__restrict__ b1, int s1,
+                                                   const uint8_t *__restrict__ w2img, const float *__restrict__ b2,
+                                                   int s2) {
+    constexpr int E = 128;
+    __shared__ __align__(16) uint8_t slab[2][SLAB];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r32 = lane & 31, g = lane >> 5;
+    const int m = blockIdx.x * 128 + wave * 32 + r32;
+    const bool live = m < M;
+    dma_to_lds(w1img, slab[0], SLAB, tid);
+
+    // this lane's half of row m: columns 16 ks + 8 g + t
+    float xv[8][8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) {
+        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), b = a;
+        if (live) {
+            const float *src = x + (size_t)m * E + 16 * ks + 8 * g;
+            a = *reinterpret_cast<const float4 *>(src);
+            b = *reinterpret_cast<const float4 *>(src + 4);
+        }
+        xv[ks][0] = a.x; xv[ks][1] = a.y; xv[ks][2] = a.z; xv[ks][3] = a.w;
+        xv[ks][4] = b.x; xv[ks][5] = b.y; xv[ks][6] = b.z; xv[ks][7] = b.w;
+    }
+    // layer normalisation (two passes, biased variance, eps 1e-5)
+    float sum = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+        for (int t = 0; t < 8; t++) sum += xv[ks][t];
+    sum += __shfl_xor(sum, 32, 64);
+    const float mean = sum / (float)E;
+    float sq = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const float dv = xv[ks][t] - mean;
+            sq += dv * dv;
+        }
+    sq += __shfl_xor(sq, 32, 64);
+    const float inv = 1.0f / sqrtf(sq / (float)E + 1e-5f);
+    float xmax = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) {
+        const float4 wa = *reinterpret_cast<const float4 *>(lnw + 16 * ks + 8 * g);
+        const float4 wb = *reinterpret_cast<const float4 *>(lnw + 16 * ks + 8 * g + 4);
+        const float4 ba = *reinterpret_cast<const float4 *>(lnb + 16 * ks + 8 * g);
+        const float4 bb = *reinterpret_cast<const float4 *>(lnb + 16 * ks + 8 * g + 4);
+        const float wv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+        const float bv[8] = {ba.x, ba.y, ba.z, ba.w, bb.x, bb.y, bb.z, bb.w};
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            xv[ks][t] = (xv[ks][t] - mean) * inv * wv[t] + bv[t];
+            xmax = fmaxf(xmax, fabsf(xv[ks][t]));
+        }
+    }
+    xmax = fmaxf(xmax, __shfl_xor(xmax, 32, 64));
+    const int sx = shift_for_max(xmax);
+    halfx8 xh[8], xl[8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) split8(xv[ks], ldexpf(1.0f, sx), xh[ks], xl[ks]);
+
+    // H^T = W1 X^T in two halves of 128 hidden units (4 tiles of 32 each); the weights stream as 16 slices of
+    // 16 KB, W1's eight (half-major, two 16-column steps each) then W2's eight, slice j into buffer j % 2
+    const int arow = sigma32(r32);
+    auto slice = [&](int j) { return j < 8 ? w1img + (size_t)j * SLAB : w2img + (size_t)(j - 8) * SLAB; };
+    halfx8 hh8[16], hl8[16];  // the hidden layer, split: 16-unit step k = 2 T + hh of half 0, then of half 1
+    int shd[2];
+#pragma unroll
+    for (int half = 0; half < 2; half++) {
+        floatx16 acc[4];
+#pragma unroll
+        for (int T = 0; T < 4; T++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[T][v] = 0.0f;
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            const int j = 4 * half + st;
+            __builtin_amdgcn_s_waitcnt(0);  // this wavefront's copies of slice j have landed
+            __syncthreads();                // everyone's have; slice j - 1's buffer is free
+            dma_to_lds(slice(j + 1), slab[(j + 1) & 1], SLAB, tid);
+            const uint8_t *sl = slab[j & 1];
+#pragma unroll
+            for (int c = 0; c < 2; c++)
+#pragma unroll
+                for (int T = 0; T < 4; T++) {
+                    const int n = 32 * T + arow;
+                    const halfx8 ah = *reinterpret_cast<const halfx8 *>(sl + c * 8192 + (g * 128 + n) * 16);
+                    const halfx8 al = *reinterpret_cast<const halfx8 *>(sl + c * 8192 + ((2 + g) * 128 + n) * 16);
+                    acc[T] = mfma16x3(ah, al, xh[2 * st + c], xl[2 * st + c], acc[T]);
+                }
+        }
+        // hidden unit of accumulator v of tile T: 128 half + 32 T + 16 (v / 8) + 8 g + v % 8
+        const float u1 = ldexpf(1.0f, -(sx + s1));
+        float hmax = 0.0f;
+#pragma unroll
+        for (int T = 0; T < 4; T++)
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                const float *bp = b1 + 128 * half + 32 * T + 16 * hh + 8 * g;
+                const float4 ba = *reinterpret_cast<const float4 *>(bp), bb = *reinterpret_cast<const float4 *>(bp + 4);
+                const float bv[8] = {ba.x, ba.y, ba.z, ba.w, bb.x, bb.y, bb.z, bb.w};
+#pragma unroll
+                for (int t = 0; t < 8; t++) {
+                    const float hv = gelu(acc[T][8 * hh + t] * u1 + bv[t]);
+                    acc[T][8 * hh + t] = hv;
+                    hmax = fmaxf(hmax, fabsf(hv));
+                }
+            }
+        hmax = fmaxf(hmax, __shfl_xor(hmax, 32, 64));
+        shd[half] = shift_for_max(hmax);
+#pragma unroll
+        for (int T = 0; T < 4; T++)
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                float hv[8];
+#pragma unroll
+                for (int t = 0; t < 8; t++) hv[t] = acc[T][8 * hh + t];
+                split8(hv, ldexpf(1.0f, shd[half]), hh8[8 * half + 2 * T + hh], hl8[8 * half + 2 * T + hh]);
+            }
+    }
+
+    // Y^T = W2 H^T: 4 tiles of 32 outputs; slice 8 + st = hidden units 32 st..32 st + 31, two 8 KB steps. The two
+    // halves of the hidden layer carry their own scales: between them the sums are rescaled (exactly) to the second.
+    floatx16 y[4];
+#pragma unroll
+    for (int T = 0; T < 4; T++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) y[T][v] = 0.0f;
+#pragma unroll
+    for (int st = 0; st < 8; st++) {
+        const int j = 8 + st;
+        if (st == 4) {
+            const float r = ldexpf(1.0f, shd[1] - shd[0]);
+#pragma unroll
+            for (int T = 0; T < 4; T++) y[T] *= r;
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (j + 1 < 16) dma_to_lds(slice(j + 1), slab[(j + 1) & 1], SLAB, tid);
+        const uint8_t *sl = slab[j & 1];
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int T = 0; T < 4; T++) {
+                const int n = 32 * T + arow;
+                const halfx8 ah = *reinterpret_cast<const halfx8 *>(sl + c * 8192 + (g * E + n) * 16);
+                const halfx8 al = *reinterpret_cast<const halfx8 *>(sl + c * 8192 + ((2 + g) * E + n) * 16);
+                y[T] = mfma16x3(ah, al, hh8[2 * st + c], hl8[2 * st + c], y[T]);
+            }
+    }
+    if (!live) return;
+    // output column of accumulator v of tile T: 32 T + 16 (v / 8) + 8 g + v % 8; x += y + b2
+    const float u2 = ldexpf(1.0f, -(shd[1] + s2));
+#pragma unroll
+    for (int T = 0; T < 4; T++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const int c0 = 32 * T + 16 * hh + 8 * g;
+            float *dst = x + (size_t)m * E + c0;
+            const float4 ra = *reinterpret_cast<const float4 *>(dst), rb = *reinterpret_cast<const float4 *>(dst + 4);
+            const float4 ba = *reinterpret_cast<const float4 *>(b2 + c0), bb = *reinterpret_cast<const float4 *>(b2 + c0 + 4);
+            float yv[8];
+#pragma unroll
+            for (int t = 0; t < 8; t++) yv[t] = y[T][8 * hh + t];
+            *reinterpret_cast<float4 *>(dst) = make_float4(yv[0] * u2 + ba.x + ra.x, yv[1] * u2 + ba.y + ra.y,
+                                                           yv[2] * u2 + ba.z + ra.z, yv[3] * u2 + ba.w + ra.w);
+            *reinterpret_cast<float4 *>(dst + 4) = make_float4(yv[4] * u2 + bb.x + rb.x, yv[5] * u2 + bb.y + rb.y,
+                                                               yv[6] * u2 + bb.z + rb.z, yv[7] * u2 + bb.w + rb.w);
+        }
+}
+
+void ff_block(hipStream_t s, int M, float *x, const DevBlock &b) {
+    if (M <= 0) return;
+    if (!ff_fused_shape(b.d, b.ff) || !b.l1img || !b.l2img) throw ArgError{"ff_block: no fused weights for this shape"};
+    hipLaunchKernelGGL(k_ff128, dim3((M + 127) / 128), dim3(256), 0, s, M, x, b.n2w, b.n2b, b.l1img, b.l1b, b.l1s,
+                       b.l2img, b.l2b, b.l2s);
+    TAH_LAUNCHED();
+}
+
+}  // namespace tah

@@ -71,6 +71,10 @@ struct DevBlock {
     int d, heads, ff, ss_hidden;
     const float *n1w, *n1b, *n2w, *n2b, *in_w, *in_b, *out_w, *out_b, *l1w, *l1b, *l2w, *l2b;
     const float *b0w, *b0b, *b2w, *b2b, *q0w, *q0b, *q2w, *q2b;
+    // feed-forward weights as split-fp16 images for the fused feed-forward kernel (width 128, hidden 256), else null;
+    // l1s / l2s: the powers of two they were scaled by
+    const uint8_t *l1img, *l2img;
+    int l1s, l2s;
 };
 
 struct tah_weights {
@@ -119,6 +123,12 @@ void layer_norm(hipStream_t s, int rows, int n, const float *x, int ldx, const f
 // q_h *= scale_h * (1 + tanh(q2 gelu(q0 q_h + q0b) + q2b)). scratch holds rows * heads * ss_hidden floats.
 void query_modulate(hipStream_t s, int rows, const DevBlock &b, const float *scale, float *q, float *scratch);
 size_t query_scratch_floats(int rows, const DevBlock &b);
+
+// Fused feed-forward sub-block (blocks.hip): x [M][128] += l2(gelu(l1(layer_norm2(x)))) in one kernel, the hidden
+// layer kept in registers; for blocks of width 128 and hidden width 256 (ff_fused_shape), else the caller runs
+// layer_norm and two GEMMs.
+inline bool ff_fused_shape(int d, int ff) { return d == 128 && ff == 256; }
+void ff_block(hipStream_t s, int M, float *x, const DevBlock &b);
 
 // Widest per-row scratch of an in-context block: its feed-forward hidden layer or its query MLP's hidden layers.
 inline int icl_mid(const tah_weights *w) {

@@ -27,7 +27,7 @@ __device__ __forceinline__ float epilogue(float acc, const float *b, int n, cons
     float y = acc + (b ? b[n] : 0.0f);
     if (EPI == EPI_GELU) y = gelu(y);
     if (EPI == EPI_RESID) y += e.R[(size_t)m * e.ldr + n];
-    if (EPI == EPI_QMOD) y = e.R[(size_t)m * e.ldr + n] * (e.scale[(m % e.heads) * N + n] * (1.0f + tanhf(y)));
+    if (EPI == EPI_QMOD) y = e.R[(size_t)m * e.ldr + n] * (e.scale[(m % e.heads) * N + n] * (1.0f + tanh1(y)));
     return y;
 }
 

@@ -306,6 +306,19 @@ void input_cells(hipStream_t s, const tah_weights *w, const float *x, int n, int
     TAH_LAUNCHED();
 }
 
+// x [M][e] += l2(gelu(l1(norm2 x))): the fused kernel where the block's shape has one, else layer_norm and two GEMMs
+// (t [M][e] and mid [M][ff] scratch).
+static void feed_forward(hipStream_t s, int M, float *x, const DevBlock &b, float *t, float *mid) {
+    if (b.l1img) {
+        ff_block(s, M, x, b);
+        return;
+    }
+    const int e = b.d;
+    layer_norm(s, M, e, x, e, b.n2w, b.n2b, t, e);
+    gemm(s, M, b.ff, e, t, e, b.l1w, b.l1b, mid, b.ff, EPI_GELU, nullptr, 0);
+    gemm(s, M, e, b.ff, mid, b.ff, b.l2w, b.l2b, x, e, EPI_RESID, x, e);
+}
+
 // One column block (cached_block with a2) for all cells in place: n rows x groups, cell (r, g) at row r * sr + g * sg
 // of cells; K/V of group g at kvbase + g * gstride.
 void column_block(hipStream_t s, const tah_weights *w, const DevBlock &b, float *cells, int n, int groups, size_t sr,
@@ -327,9 +340,7 @@ void column_block(hipStream_t s, const tah_weights *w, const DevBlock &b, float 
                            b.heads, w->inds, q, kvbase, gstride, att);
     TAH_LAUNCHED();
     gemm(s, M, e, e, att, e, b.out_w, b.out_b, cells, e, EPI_RESID, cells, e);
-    layer_norm(s, M, e, cells, e, b.n2w, b.n2b, t, e);
-    gemm(s, M, b.ff, e, t, e, b.l1w, b.l1b, mid, b.ff, EPI_GELU, nullptr, 0);
-    gemm(s, M, e, b.ff, mid, b.ff, b.l2w, b.l2b, cells, e, EPI_RESID, cells, e);
+    feed_forward(s, M, cells, b, t, mid);
 }
 
 size_t column_stage_floats(const tah_weights *w, int n, int features, int digits) {
@@ -411,9 +422,7 @@ void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, co
         if (bi < last) {
             attend(T, att);
             gemm(s, (int)R, e, e, att, e, b.out_w, b.out_b, tok, e, EPI_RESID, tok, e);
-            layer_norm(s, (int)R, e, tok, e, b.n2w, b.n2b, t, e);
-            gemm(s, (int)R, b.ff, e, t, e, b.l1w, b.l1b, mid, b.ff, EPI_GELU, nullptr, 0);
-            gemm(s, (int)R, e, b.ff, mid, b.ff, b.l2w, b.l2b, tok, e, EPI_RESID, tok, e);
+            feed_forward(s, (int)R, tok, b, t, mid);
         } else {
             // the last block: only the class tokens are queried and updated
             const int M = n * cls;
@@ -421,9 +430,7 @@ void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, co
             hipLaunchKernelGGL(k_first_tokens, blocks_for((size_t)M * e), dim3(256), 0, s, n, T, cls, e, tok, xc);
             TAH_LAUNCHED();
             gemm(s, M, e, e, ac, e, b.out_w, b.out_b, xc, e, EPI_RESID, xc, e);
-            layer_norm(s, M, e, xc, e, b.n2w, b.n2b, t, e);
-            gemm(s, M, b.ff, e, t, e, b.l1w, b.l1b, mid, b.ff, EPI_GELU, nullptr, 0);
-            gemm(s, M, e, b.ff, mid, b.ff, b.l2w, b.l2b, xc, e, EPI_RESID, xc, e);
+            feed_forward(s, M, xc, b, t, mid);
             layer_norm(s, M, e, xc, e, w->out_lnw, w->out_lnb, rep, e);
         }
     }
