@@ -231,12 +231,49 @@ struct Packer {
 // W [N][K] (N a multiple of 128, K of 16) scaled by 2^shift (its largest magnitude below 2^14) and split into fp16
 // hi/lo, in the order the fused blocks stream it through LDS: per block of 128 rows rb, per 16 columns ks,
 // [hi, lo][k half g][row n of the block][8 halves of W[128 rb + n][16 ks + 8 g + t]] (8 KB a step).
-static std::vector<uint8_t> weight_image(const float *W, int N, int K, int &shift) {
+static int weight_shift(const float *W, size_t n) {
     float mx = 0.0f;
-    for (size_t i = 0; i < (size_t)N * K; i++) mx = std::max(mx, std::fabs(W[i]));
+    for (size_t i = 0; i < n; i++) mx = std::max(mx, std::fabs(W[i]));
     int e = 0;
     (void)std::frexp(mx, &e);
-    shift = 14 - e;
+    return 14 - e;
+}
+
+static inline void split_half(float x, _Float16 &hi, _Float16 &lo) {
+    hi = (_Float16)x;
+    lo = (_Float16)(x - (float)hi);
+}
+
+// W [N][K] as a gemm_split image (SplitW): 32-row tiles, rows sigma32-ordered within a tile, 16-column steps of
+// [hi, lo][k half g][32 rows][8 halves].
+static void add_split(Packer &pk, const float *W, int N, int K, SplitW &o) {
+    o = SplitW{};
+    if (!W || N <= 0 || N % 32 || K <= 0 || K % 16) return;
+    o.shift = weight_shift(W, (size_t)N * K);
+    o.N = N;
+    o.K = K;
+    const float f = std::ldexp(1.0f, o.shift);
+    std::vector<uint8_t> out((size_t)N * K * 4);
+    _Float16 *img = reinterpret_cast<_Float16 *>(out.data());
+    for (int tile = 0; tile < N / 32; tile++)
+        for (int ks = 0; ks < K / 16; ks++) {
+            _Float16 *step = img + ((size_t)tile * (K / 16) + ks) * 1024;  // 2 KB = 1024 halves
+            for (int g = 0; g < 2; g++)
+                for (int slot = 0; slot < 32; slot++) {
+                    const int row = 32 * tile + ((slot & 16) | ((slot & 4) << 1) | ((slot & 8) >> 1) | (slot & 3));
+                    for (int t = 0; t < 8; t++) {
+                        _Float16 hi, lo;
+                        split_half(W[(size_t)row * K + 16 * ks + 8 * g + t] * f, hi, lo);
+                        step[(g * 32 + slot) * 8 + t] = hi;
+                        step[((2 + g) * 32 + slot) * 8 + t] = lo;
+                    }
+                }
+        }
+    pk.add_bytes(std::move(out), &o.img);
+}
+
+static std::vector<uint8_t> weight_image(const float *W, int N, int K, int &shift) {
+    shift = weight_shift(W, (size_t)N * K);
     const float f = std::ldexp(1.0f, shift);
     std::vector<uint8_t> out((size_t)N * K * 4);
     _Float16 *o = reinterpret_cast<_Float16 *>(out.data());
@@ -246,9 +283,9 @@ static std::vector<uint8_t> weight_image(const float *W, int N, int K, int &shif
                 for (int g = 0; g < 2; g++)
                     for (int n = 128 * rb; n < 128 * rb + 128; n++)
                         for (int t = 0; t < 8; t++) {
-                            const float x = W[(size_t)n * K + 16 * ks + 8 * g + t] * f;
-                            const _Float16 hi = (_Float16)x;
-                            *o++ = part == 0 ? hi : (_Float16)(x - (float)hi);
+                            _Float16 hi, lo;
+                            split_half(W[(size_t)n * K + 16 * ks + 8 * g + t] * f, hi, lo);
+                            *o++ = part == 0 ? hi : lo;
                         }
     return out;
 }
@@ -283,10 +320,26 @@ void add_block(Packer &pk, const tah_block &b, DevBlock &o) {
     } else {
         o.b0w = o.b0b = o.b2w = o.b2b = o.q0w = o.q0b = o.q2w = o.q2b = nullptr;
     }
-    o.l1img = o.l2img = nullptr;
+    o.l1img = o.l2img = o.inimg = o.outimg = nullptr;
+    o.in_s = o.out_s = o.l1_s = o.l2_s = o.q0_s = o.q2_s = SplitW{};
+    if (b.d == 128) {
+        // the column and row stages' shape: the fused kernels of blocks.hip
+        if (b.in_w) pk.add_bytes(weight_image(b.in_w, 3 * b.d, b.d, o.ins), &o.inimg);
+        if (b.out_w) pk.add_bytes(weight_image(b.out_w, b.d, b.d, o.outs), &o.outimg);
+    } else {
+        add_split(pk, b.in_w, 3 * b.d, b.d, o.in_s);
+        add_split(pk, b.out_w, b.d, b.d, o.out_s);
+    }
     if (ff_fused_shape(b.d, b.ff) && b.l1w && b.l2w) {
         pk.add_bytes(weight_image(b.l1w, b.ff, b.d, o.l1s), &o.l1img);
         pk.add_bytes(weight_image(b.l2w, b.d, b.ff, o.l2s), &o.l2img);
+    } else {
+        add_split(pk, b.l1w, b.ff, b.d, o.l1_s);
+        add_split(pk, b.l2w, b.d, b.ff, o.l2_s);
+    }
+    if (hid) {
+        add_split(pk, b.q0w, b.ss_hidden, (int)hd, o.q0_s);
+        add_split(pk, b.q2w, (int)hd, b.ss_hidden, o.q2_s);
     }
 }
 
@@ -340,6 +393,7 @@ extern "C" int tah_weights_upload(tah_dev *dev, const tah_model_desc *m, tah_wei
         pk.add(m->lnb, d, &w->lnb);
         pk.add(m->dec0w, (size_t)m->dec_hidden * d, &w->dec0w);
         pk.add(m->dec0b, m->dec_hidden, &w->dec0b);
+        add_split(pk, m->dec0w, m->dec_hidden, (int)d, w->dec0_s);
         pk.add(m->dec2w, (size_t)m->outputs * m->dec_hidden, &w->dec2w);
         pk.add(m->dec2b, m->outputs, &w->dec2b);
         std::vector<float> col_scale;
@@ -531,20 +585,20 @@ static void stage_rows(tah_dev *dev, const tah_weights *w, const tah_model *mode
         const DevBlock &b = w->icl[l];
         // query: q = modulate(Wq norm1(h) + bq)  (src/nn.rs:130-152)
         layer_norm(s, nq, d, h, d, b.n1w, b.n1b, t, d);
-        gemm(s, nq, d, d, t, d, b.in_w, b.in_b, q, d, EPI_NONE, nullptr, 0);
+        dense(s, nq, d, d, t, d, b.in_w, b.in_s.rows(0), b.in_b, q, d, EPI_NONE, nullptr, 0);
         query_modulate(s, nq, b, model->scales + (size_t)l * d, q, mid);
         // attention over the stored layer, then h += out(att)  (src/predict.rs:421-551)
         const KvImages img = images_of(model, l);
         attention(s, a, q, layer_of(model, l), att, work, &img);
-        gemm(s, nq, d, d, att, d, b.out_w, b.out_b, h, d, EPI_RESID, h, d);
+        dense(s, nq, d, d, att, d, b.out_w, b.out_s, b.out_b, h, d, EPI_RESID, h, d);
         // h += l2(gelu(l1(norm2 h)))  (src/predict.rs:552-568)
         layer_norm(s, nq, d, h, d, b.n2w, b.n2b, t, d);
-        gemm(s, nq, b.ff, d, t, d, b.l1w, b.l1b, mid, b.ff, EPI_GELU, nullptr, 0);
-        gemm(s, nq, d, b.ff, mid, b.ff, b.l2w, b.l2b, h, d, EPI_RESID, h, d);
+        dense(s, nq, b.ff, d, t, d, b.l1w, b.l1_s, b.l1b, mid, b.ff, EPI_GELU, nullptr, 0);
+        dense(s, nq, d, b.ff, mid, b.ff, b.l2w, b.l2_s, b.l2b, h, d, EPI_RESID, h, d);
     }
     // decoder, first out_n outputs  (src/predict.rs:570-585)
     layer_norm(s, nq, d, h, d, w->lnw, w->lnb, t, d);
-    gemm(s, nq, w->dec_hidden, d, t, d, w->dec0w, w->dec0b, mid, w->dec_hidden, EPI_GELU, nullptr, 0);
+    dense(s, nq, w->dec_hidden, d, t, d, w->dec0w, w->dec0_s, w->dec0b, mid, w->dec_hidden, EPI_GELU, nullptr, 0);
     gemm(s, nq, out_n, w->dec_hidden, mid, w->dec_hidden, w->dec2w, w->dec2b, out, out_n, EPI_NONE, nullptr, 0);
 }
 
@@ -663,7 +717,8 @@ extern "C" int tah_in_context(tah_dev *dev, const tah_weights *w, const float *h
             const DevBlock &b = w->icl[l];
             // keys and values of every row, stored (src/fit.rs:627-663)
             layer_norm(s, rows, d, h, d, b.n1w, b.n1b, t, d);
-            gemm(s, rows, 2 * d, d, t, d, b.in_w + (size_t)d * d, b.in_b + d, kv, 2 * d, EPI_NONE, nullptr, 0);
+            dense(s, rows, 2 * d, d, t, d, b.in_w + (size_t)d * d, b.in_s.rows(d), b.in_b + d, kv, 2 * d, EPI_NONE,
+                  nullptr, 0);
             to_records(s, rows, d, chunk, kv, rec32);
             const uint8_t *stored = reinterpret_cast<const uint8_t *>(rec32);
             if (kv_format != TAH_KV_F32) {
@@ -675,14 +730,14 @@ extern "C" int tah_in_context(tah_dev *dev, const tah_weights *w, const float *h
             if (!last) {
                 // every row attends to all rows over the exact keys and values, then the rest of the block
                 // (src/fit.rs:667-744)
-                gemm(s, rows, d, d, t, d, b.in_w, b.in_b, q, d, EPI_NONE, nullptr, 0);
+                dense(s, rows, d, d, t, d, b.in_w, b.in_s.rows(0), b.in_b, q, d, EPI_NONE, nullptr, 0);
                 query_modulate(s, rows, b, sc + (size_t)l * d, q, mid);
                 if (use_img) kv_images(s, rows, chunk, d, w->icl_heads, reinterpret_cast<const uint8_t *>(rec32), img);
                 attention(s, a, q, reinterpret_cast<const uint8_t *>(rec32), att, work, use_img ? &img : nullptr);
-                gemm(s, rows, d, d, att, d, b.out_w, b.out_b, h, d, EPI_RESID, h, d);
+                dense(s, rows, d, d, att, d, b.out_w, b.out_s, b.out_b, h, d, EPI_RESID, h, d);
                 layer_norm(s, rows, d, h, d, b.n2w, b.n2b, t, d);
-                gemm(s, rows, b.ff, d, t, d, b.l1w, b.l1b, mid, b.ff, EPI_GELU, nullptr, 0);
-                gemm(s, rows, d, b.ff, mid, b.ff, b.l2w, b.l2b, h, d, EPI_RESID, h, d);
+                dense(s, rows, b.ff, d, t, d, b.l1w, b.l1_s, b.l1b, mid, b.ff, EPI_GELU, nullptr, 0);
+                dense(s, rows, d, b.ff, mid, b.ff, b.l2w, b.l2_s, b.l2b, h, d, EPI_RESID, h, d);
             }
             // the layer's records reached the host before the next layer's keys overwrite rec32
             TAH_HIP(hipStreamSynchronize(s));

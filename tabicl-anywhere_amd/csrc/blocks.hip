@@ -216,4 +216,159 @@ void ff_block(hipStream_t s, int M, float *x, const DevBlock &b) {
     TAH_LAUNCHED();
 }
 
+// ---- projections of width 128 over many rows ----------------------------------------------------------------------
+// Y [M][N] = epi(X' W^T + b), K = 128: the column stage's query projection (with norm1 and the query scale folded
+// in), the row stage's query/key/value projection (with norm1) and both stages' output projections (with the
+// residual add). Each wavefront owns 32 rows of X, split once (per-row power of two) and kept in registers as the B
+// operand; the weights, one block of 128 output columns at a time (64 KB: the same image as the feed-forward's,
+// 128-row blocks of 16-column steps), are copied global -> LDS by DMA and shared by the four wavefronts, and each
+// block's four 32-column tiles are formed with sigma32-ordered rows so that the epilogue writes eight consecutive
+// columns per lane. Two workgroups share a compute unit (2 x 64 KB of LDS).
+template <int EPI, bool LN>
+__global__ __launch_bounds__(256, 2) void k_rows128(int M, int N, const float *__restrict__ X, int ldx,
+                                                     const uint8_t *__restrict__ wimg, int wshift,
+                                                     const float *__restrict__ b, float *Y, int ldy,
+                                                     const float *R, int ldr, const float *__restrict__ scale,
+                                                     const float *__restrict__ lnw, const float *__restrict__ lnb) {
+    constexpr int BLK = 65536;  // one block of 128 output columns: 8 steps of 8 KB
+    __shared__ __align__(16) uint8_t wl[BLK];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r32 = lane & 31, g = lane >> 5;
+    const int m = blockIdx.x * 128 + wave * 32 + r32;
+    const bool live = m < M;
+    dma_to_lds(wimg, wl, BLK, tid);
+
+    float xv[8][8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) {
+        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), c = a;
+        if (live) {
+            const float *src = X + (size_t)m * ldx + 16 * ks + 8 * g;
+            a = *reinterpret_cast<const float4 *>(src);
+            c = *reinterpret_cast<const float4 *>(src + 4);
+        }
+        xv[ks][0] = a.x; xv[ks][1] = a.y; xv[ks][2] = a.z; xv[ks][3] = a.w;
+        xv[ks][4] = c.x; xv[ks][5] = c.y; xv[ks][6] = c.z; xv[ks][7] = c.w;
+    }
+    if (LN) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+            for (int t = 0; t < 8; t++) sum += xv[ks][t];
+        sum += __shfl_xor(sum, 32, 64);
+        const float mean = sum / 128.0f;
+        float sq = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const float dv = xv[ks][t] - mean;
+                sq += dv * dv;
+            }
+        sq += __shfl_xor(sq, 32, 64);
+        const float inv = 1.0f / sqrtf(sq / 128.0f + 1e-5f);
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            const float4 wa = *reinterpret_cast<const float4 *>(lnw + 16 * ks + 8 * g);
+            const float4 wb = *reinterpret_cast<const float4 *>(lnw + 16 * ks + 8 * g + 4);
+            const float4 ba = *reinterpret_cast<const float4 *>(lnb + 16 * ks + 8 * g);
+            const float4 bb = *reinterpret_cast<const float4 *>(lnb + 16 * ks + 8 * g + 4);
+            const float wv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+            const float bv[8] = {ba.x, ba.y, ba.z, ba.w, bb.x, bb.y, bb.z, bb.w};
+#pragma unroll
+            for (int t = 0; t < 8; t++) xv[ks][t] = (xv[ks][t] - mean) * inv * wv[t] + bv[t];
+        }
+    }
+    float xmax = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+        for (int t = 0; t < 8; t++) xmax = fmaxf(xmax, fabsf(xv[ks][t]));
+    xmax = fmaxf(xmax, __shfl_xor(xmax, 32, 64));
+    const int sx = shift_for_max(xmax);
+    halfx8 xh[8], xl[8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) split8(xv[ks], ldexpf(1.0f, sx), xh[ks], xl[ks]);
+    const float u = ldexpf(1.0f, -(sx + wshift));
+    const int arow = sigma32(r32);
+
+    for (int cb = 0; cb < N / 128; cb++) {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();  // block cb of the weights is in LDS
+        floatx16 acc[4];
+#pragma unroll
+        for (int T = 0; T < 4; T++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[T][v] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+            for (int T = 0; T < 4; T++) {
+                const int n = 32 * T + arow;
+                const halfx8 ah = *reinterpret_cast<const halfx8 *>(wl + ks * 8192 + (g * 128 + n) * 16);
+                const halfx8 al = *reinterpret_cast<const halfx8 *>(wl + ks * 8192 + ((2 + g) * 128 + n) * 16);
+                acc[T] = mfma16x3(ah, al, xh[ks], xl[ks], acc[T]);
+            }
+        __syncthreads();  // everyone is done with block cb
+        if (cb + 1 < N / 128) dma_to_lds(wimg + (size_t)(cb + 1) * BLK, wl, BLK, tid);
+        if (!live) continue;
+        // column of accumulator v of tile T: 128 cb + 32 T + 16 (v / 8) + 8 g + v % 8
+#pragma unroll
+        for (int T = 0; T < 4; T++)
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                const int n0 = 128 * cb + 32 * T + 16 * hh + 8 * g;
+                const float4 ba = *reinterpret_cast<const float4 *>(b + n0);
+                const float4 bb = *reinterpret_cast<const float4 *>(b + n0 + 4);
+                const float bv[8] = {ba.x, ba.y, ba.z, ba.w, bb.x, bb.y, bb.z, bb.w};
+                float yv[8];
+#pragma unroll
+                for (int t = 0; t < 8; t++) yv[t] = acc[T][8 * hh + t] * u + bv[t];
+                if (EPI == EPI_SCALE) {
+                    const float4 sa = *reinterpret_cast<const float4 *>(scale + n0);
+                    const float4 sb = *reinterpret_cast<const float4 *>(scale + n0 + 4);
+                    yv[0] *= sa.x; yv[1] *= sa.y; yv[2] *= sa.z; yv[3] *= sa.w;
+                    yv[4] *= sb.x; yv[5] *= sb.y; yv[6] *= sb.z; yv[7] *= sb.w;
+                }
+                if (EPI == EPI_RESID) {
+                    const float *rp = R + (size_t)m * ldr + n0;
+                    const float4 ra = *reinterpret_cast<const float4 *>(rp);
+                    const float4 rb = *reinterpret_cast<const float4 *>(rp + 4);
+                    yv[0] += ra.x; yv[1] += ra.y; yv[2] += ra.z; yv[3] += ra.w;
+                    yv[4] += rb.x; yv[5] += rb.y; yv[6] += rb.z; yv[7] += rb.w;
+                }
+                float *dst = Y + (size_t)m * ldy + n0;
+                *reinterpret_cast<float4 *>(dst) = make_float4(yv[0], yv[1], yv[2], yv[3]);
+                *reinterpret_cast<float4 *>(dst + 4) = make_float4(yv[4], yv[5], yv[6], yv[7]);
+            }
+    }
+}
+
+void rows128(hipStream_t s, int M, int N, const float *X, int ldx, const uint8_t *wimg, int wshift, const float *b,
+             float *Y, int ldy, Epi epi, const float *R, int ldr, const float *scale, const float *lnw,
+             const float *lnb) {
+    if (M <= 0) return;
+    if (!wimg || N <= 0 || N % 128 || ldx % 4 || ldy % 4 || (reinterpret_cast<uintptr_t>(X) & 15) ||
+        (reinterpret_cast<uintptr_t>(Y) & 15))
+        throw ArgError{"rows128: needs a weight image, output width a multiple of 128 and 16-byte aligned rows"};
+    const dim3 grid((M + 127) / 128);
+    const bool ln = lnw != nullptr;
+    if (epi == EPI_NONE && ln)
+        hipLaunchKernelGGL((k_rows128<EPI_NONE, true>), grid, dim3(256), 0, s, M, N, X, ldx, wimg, wshift, b, Y, ldy, R,
+                           ldr, scale, lnw, lnb);
+    else if (epi == EPI_NONE)
+        hipLaunchKernelGGL((k_rows128<EPI_NONE, false>), grid, dim3(256), 0, s, M, N, X, ldx, wimg, wshift, b, Y, ldy, R,
+                           ldr, scale, lnw, lnb);
+    else if (epi == EPI_SCALE && ln)
+        hipLaunchKernelGGL((k_rows128<EPI_SCALE, true>), grid, dim3(256), 0, s, M, N, X, ldx, wimg, wshift, b, Y, ldy, R,
+                           ldr, scale, lnw, lnb);
+    else if (epi == EPI_RESID && !ln)
+        hipLaunchKernelGGL((k_rows128<EPI_RESID, false>), grid, dim3(256), 0, s, M, N, X, ldx, wimg, wshift, b, Y, ldy,
+                           R, ldr, scale, lnw, lnb);
+    else
+        throw ArgError{"rows128: unsupported epilogue"};
+    TAH_LAUNCHED();
+}
+
 }  // namespace tah

@@ -67,6 +67,19 @@ struct tah_dev {
 };
 
 // A block's tensors on the card (device pointers; nullptr where absent).
+// A weight matrix W [N][K] uploaded as a split-fp16 image for gemm_split: 32-row tiles (rows in sigma32 order within
+// a tile), then 16-column steps, each [hi, lo][k half][32 rows][8 halves] (2 KB); W scaled by 2^shift first. row0
+// selects rows row0.. of it (a multiple of 32).
+struct SplitW {
+    const uint8_t *img = nullptr;
+    int shift = 0, N = 0, K = 0, row0 = 0;
+    SplitW rows(int r0) const {
+        SplitW o = *this;
+        o.row0 = r0;
+        return o;
+    }
+};
+
 struct DevBlock {
     int d, heads, ff, ss_hidden;
     const float *n1w, *n1b, *n2w, *n2b, *in_w, *in_b, *out_w, *out_b, *l1w, *l1b, *l2w, *l2b;
@@ -75,6 +88,12 @@ struct DevBlock {
     // l1s / l2s: the powers of two they were scaled by
     const uint8_t *l1img, *l2img;
     int l1s, l2s;
+    // width 128: in_w [384][128] and out_w [128][128] as the same images, for k_rows128 (rows128)
+    const uint8_t *inimg, *outimg;
+    int ins, outs;
+    // the dense layers as gemm_split images (empty where the shape does not fit): in_w [3d][d], out_w, l1w, l2w and
+    // the query MLP's q0w, q2w
+    SplitW in_s, out_s, l1_s, l2_s, q0_s, q2_s;
 };
 
 struct tah_weights {
@@ -87,6 +106,7 @@ struct tah_weights {
     std::vector<DevBlock> col_a1, col_a2, row, icl;
     const float *in_w, *in_b, *col_ind, *col_y, *cls_tokens, *rope_freqs, *out_lnw, *out_lnb;
     const float *icl_y, *lnw, *lnb, *dec0w, *dec0b, *dec2w, *dec2b;
+    SplitW dec0_s;  // the decoder's first layer as a gemm_split image
     const float *col_scale;  // [e]: 1 / sqrt(column head width), what the column blocks' queries are multiplied by
 };
 
@@ -105,7 +125,7 @@ struct tah_model {
 
 namespace tah {
 
-enum Epi { EPI_NONE = 0, EPI_GELU = 1, EPI_RESID = 2, EPI_QMOD = 3 };
+enum Epi { EPI_NONE = 0, EPI_GELU = 1, EPI_RESID = 2, EPI_QMOD = 3, EPI_SCALE = 4 };
 
 // Y[M][N] (leading dim ldy) = epi(X[M][K] (ldx) * W[N][K]^T + b[N]); EPI_RESID adds R (ldr, may alias Y).
 void gemm(hipStream_t s, int M, int N, int K, const float *X, int ldx, const float *W, const float *b, float *Y,
@@ -114,6 +134,15 @@ void gemm(hipStream_t s, int M, int N, int K, const float *X, int ldx, const flo
 // q [M][N] (in place) = q * scale[(m % heads) * N + n] * (1 + tanh(X W^T + b)): the query MLP's modulation.
 void gemm_qmod(hipStream_t s, int M, int N, int K, const float *X, int ldx, const float *W, const float *b, float *q,
                const float *scale, int heads);
+
+// The same on split-fp16 MFMA from a weight image (gemm_split.hip); EPI_SCALE multiplies by scale [N], EPI_QMOD as
+// gemm_qmod with scale [heads][N].
+bool gemm_split_fits(int N, int K);
+void gemm_split(hipStream_t s, int M, int N, int K, const float *X, int ldx, const SplitW &w, const float *b, float *Y,
+                int ldy, Epi epi, const float *R, int ldr, const float *scale, int heads);
+// gemm_split where the image fits and there are 32 rows or more, else gemm on the f32 weights.
+void dense(hipStream_t s, int M, int N, int K, const float *X, int ldx, const float *W, const SplitW &w, const float *b,
+           float *Y, int ldy, Epi epi, const float *R, int ldr);
 
 // y[r] = layer_norm(x[r]) * w + b over rows of n numbers (eps 1e-5, biased variance).
 void layer_norm(hipStream_t s, int rows, int n, const float *x, int ldx, const float *w, const float *b, float *y,
@@ -129,6 +158,11 @@ size_t query_scratch_floats(int rows, const DevBlock &b);
 // layer_norm and two GEMMs.
 inline bool ff_fused_shape(int d, int ff) { return d == 128 && ff == 256; }
 void ff_block(hipStream_t s, int M, float *x, const DevBlock &b);
+// Y [M][N] = epi(X' W^T + b) for K = 128 and N a multiple of 128, W as such an image (scaled by 2^shift), X' = X or
+// layer_norm(X) with lnw/lnb; EPI_NONE, EPI_SCALE (by scale [N]) or EPI_RESID (adds R, may alias Y).
+void rows128(hipStream_t s, int M, int N, const float *X, int ldx, const uint8_t *wimg, int wshift, const float *b,
+             float *Y, int ldy, Epi epi, const float *R, int ldr, const float *scale, const float *lnw,
+             const float *lnb);
 
 // Widest per-row scratch of an in-context block: its feed-forward hidden layer or its query MLP's hidden layers.
 inline int icl_mid(const tah_weights *w) {

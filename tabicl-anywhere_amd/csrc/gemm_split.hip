@@ -1,0 +1,311 @@
+// Dense layers on the fp16 matrix cores with split f32 operands: Y = epi(X W^T + b) for weights uploaded as split
+// images (SplitW), the products formed as in device_math.hpp (three v_mfma_f32_32x32x16_f16 per f32 product).
+//
+// The product is formed transposed, Y^T = W X^T: each wavefront owns 32 rows of X, one per lane pair (lane l holds
+// row l % 32 and, of every 16 columns, the eight 8 (l / 32) + 0..7) -- the B operand -- and 32 TN output columns.
+// The weights are the A operand, read straight from their image (32-row tiles with the rows in sigma32 order, then
+// 16-column steps: one coalesced 512-byte read per lane half), which puts eight consecutive output columns in each
+// lane's accumulators v = 8 hh .. 8 hh + 7, stored as two 128-bit writes. No LDS: the four wavefronts of a
+// workgroup take four row groups of one column tile, so the weight tile they all read is shared through the caches.
+//
+// X is scaled per row and per chunk of 128 columns by a power of two (the chunk's largest magnitude below 2^14)
+// before splitting; the accumulators are rescaled (exactly) from one chunk's power to the next and unscaled in the
+// epilogue. (Products with K = 128 over many rows, the column and row stages', use k_rows128 in blocks.hip, which
+// keeps the weights in LDS and can fold a layer normalisation in front.)
+#include "common.hpp"
+#include "device_math.hpp"
+
+namespace tah {
+
+struct SplitEpi {
+    const float *R;      // EPI_RESID: added; EPI_QMOD: the query being modulated (may alias Y)
+    int ldr;
+    const float *scale;  // EPI_SCALE: [N]; EPI_QMOD: [heads][N]
+    int heads;
+};
+
+template <int EPI, int TN>
+__global__ __launch_bounds__(256, 3) void k_gemm_split(int M, int N, int K, const float *__restrict__ X, int ldx,
+                                                        const uint8_t *__restrict__ wimg, int wshift,
+                                                        const float *__restrict__ b, float *Y, int ldy, SplitEpi ea) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r32 = lane & 31, g = lane >> 5;
+    const int m = (blockIdx.y * 4 + wave) * 32 + r32;
+    const bool live = m < M;
+    const int tile0 = blockIdx.x * TN;  // first 32-column tile of this wavefront
+    const int KS = K / 16;
+    const float *xrow = X + (size_t)(live ? m : 0) * ldx;
+
+    floatx16 acc[TN];
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[j][v] = 0.0f;
+    int eprev = 0;
+    for (int k0 = 0; k0 < K; k0 += 128) {
+        const int nks = min(8, (K - k0) / 16);
+        float xv[8][8];
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), c = a;
+            if (live && ks < nks) {
+                const float *src = xrow + k0 + 16 * ks + 8 * g;
+                a = *reinterpret_cast<const float4 *>(src);
+                c = *reinterpret_cast<const float4 *>(src + 4);
+            }
+            xv[ks][0] = a.x; xv[ks][1] = a.y; xv[ks][2] = a.z; xv[ks][3] = a.w;
+            xv[ks][4] = c.x; xv[ks][5] = c.y; xv[ks][6] = c.z; xv[ks][7] = c.w;
+        }
+        float xmax = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+            for (int t = 0; t < 8; t++) xmax = fmaxf(xmax, fabsf(xv[ks][t]));
+        xmax = fmaxf(xmax, __shfl_xor(xmax, 32, 64));
+        const int e = shift_for_max(xmax);
+        if (k0 > 0) {
+            const float r = ldexpf(1.0f, e - eprev);
+#pragma unroll
+            for (int j = 0; j < TN; j++) acc[j] *= r;
+        }
+        eprev = e;
+        const float f = ldexpf(1.0f, e);
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            if (ks >= nks) break;
+            halfx8 xh, xl;
+            split8(xv[ks], f, xh, xl);
+            const int kk = k0 / 16 + ks;
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const uint8_t *w = wimg + ((size_t)(tile0 + j) * KS + kk) * 2048 + (g * 32 + r32) * 16;
+                const halfx8 ah = *reinterpret_cast<const halfx8 *>(w);
+                const halfx8 al = *reinterpret_cast<const halfx8 *>(w + 1024);
+                acc[j] = mfma16x3(ah, al, xh, xl, acc[j]);
+            }
+        }
+    }
+    if (!live) return;
+    // column of accumulator v of tile j: 32 (tile0 + j) + 16 (v / 8) + 8 g + v % 8
+    const float u = ldexpf(1.0f, -(wshift + eprev));
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const int n0 = 32 * (tile0 + j) + 16 * hh + 8 * g;
+            float yv[8];
+#pragma unroll
+            for (int t = 0; t < 8; t++) yv[t] = acc[j][8 * hh + t] * u;
+            if (b) {
+                const float4 ba = *reinterpret_cast<const float4 *>(b + n0);
+                const float4 bb = *reinterpret_cast<const float4 *>(b + n0 + 4);
+                yv[0] += ba.x; yv[1] += ba.y; yv[2] += ba.z; yv[3] += ba.w;
+                yv[4] += bb.x; yv[5] += bb.y; yv[6] += bb.z; yv[7] += bb.w;
+            }
+            if (EPI == EPI_GELU) {
+#pragma unroll
+                for (int t = 0; t < 8; t++) yv[t] = gelu(yv[t]);
+            }
+            if (EPI == EPI_SCALE) {
+                const float4 sa = *reinterpret_cast<const float4 *>(ea.scale + n0);
+                const float4 sb = *reinterpret_cast<const float4 *>(ea.scale + n0 + 4);
+                yv[0] *= sa.x; yv[1] *= sa.y; yv[2] *= sa.z; yv[3] *= sa.w;
+                yv[4] *= sb.x; yv[5] *= sb.y; yv[6] *= sb.z; yv[7] *= sb.w;
+            }
+            if (EPI == EPI_RESID || EPI == EPI_QMOD) {
+                const float *rp = ea.R + (size_t)m * ea.ldr + n0;
+                const float4 ra = *reinterpret_cast<const float4 *>(rp);
+                const float4 rb = *reinterpret_cast<const float4 *>(rp + 4);
+                const float rv[8] = {ra.x, ra.y, ra.z, ra.w, rb.x, rb.y, rb.z, rb.w};
+                if (EPI == EPI_RESID) {
+#pragma unroll
+                    for (int t = 0; t < 8; t++) yv[t] += rv[t];
+                } else {
+                    const float *sp = ea.scale + (size_t)(m % ea.heads) * N + n0;
+#pragma unroll
+                    for (int t = 0; t < 8; t++) yv[t] = rv[t] * (sp[t] * (1.0f + tanh1(yv[t])));
+                }
+            }
+            float *dst = Y + (size_t)m * ldy + n0;
+            *reinterpret_cast<float4 *>(dst) = make_float4(yv[0], yv[1], yv[2], yv[3]);
+            *reinterpret_cast<float4 *>(dst + 4) = make_float4(yv[4], yv[5], yv[6], yv[7]);
+        }
+}
+
+// Few rows and long rows (the in-context stage: 2,048 queries, K = 512 or 1024): one workgroup per 32 rows x 128
+// columns, its four wavefronts splitting K four ways (each a quarter, in chunks of 128 with their own per-row
+// powers of two), then summing their partial products -- unscaled to f32 -- through LDS; wavefront w finishes
+// tile w. Four times the wavefronts of k_gemm_split on the same grid of outputs, each with a quarter of the
+// dependent chain.
+template <int EPI>
+__global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, const float *__restrict__ X, int ldx,
+                                                          const uint8_t *__restrict__ wimg, int wshift,
+                                                          const float *__restrict__ b, float *Y, int ldy, SplitEpi ea) {
+    __shared__ float red[4][4][16][64];  // [wavefront][tile][accumulator][lane]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r32 = lane & 31, g = lane >> 5;
+    const int m = blockIdx.y * 32 + r32;
+    const bool live = m < M;
+    const int nt0 = blockIdx.x * 4;
+    const int KS = K / 16, kq = K / 4, kend = (wave + 1) * kq;
+    const float *xrow = X + (size_t)(live ? m : 0) * ldx;
+    floatx16 acc[4];
+#pragma unroll
+    for (int T = 0; T < 4; T++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[T][v] = 0.0f;
+    int eprev = 0;
+    for (int k0 = wave * kq; k0 < kend; k0 += 128) {
+        const int nks = min(8, (kend - k0) / 16);
+        float xv[8][8];
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), c = a;
+            if (live && ks < nks) {
+                const float *src = xrow + k0 + 16 * ks + 8 * g;
+                a = *reinterpret_cast<const float4 *>(src);
+                c = *reinterpret_cast<const float4 *>(src + 4);
+            }
+            xv[ks][0] = a.x; xv[ks][1] = a.y; xv[ks][2] = a.z; xv[ks][3] = a.w;
+            xv[ks][4] = c.x; xv[ks][5] = c.y; xv[ks][6] = c.z; xv[ks][7] = c.w;
+        }
+        float xmax = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+            for (int t = 0; t < 8; t++) xmax = fmaxf(xmax, fabsf(xv[ks][t]));
+        xmax = fmaxf(xmax, __shfl_xor(xmax, 32, 64));
+        const int e = shift_for_max(xmax);
+        if (k0 > wave * kq) {
+            const float r = ldexpf(1.0f, e - eprev);
+#pragma unroll
+            for (int T = 0; T < 4; T++) acc[T] *= r;
+        }
+        eprev = e;
+        const float f = ldexpf(1.0f, e);
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            if (ks >= nks) break;
+            halfx8 xh, xl;
+            split8(xv[ks], f, xh, xl);
+            const int kk = k0 / 16 + ks;
+#pragma unroll
+            for (int T = 0; T < 4; T++) {
+                const uint8_t *w = wimg + ((size_t)(nt0 + T) * KS + kk) * 2048 + (g * 32 + r32) * 16;
+                const halfx8 ah = *reinterpret_cast<const halfx8 *>(w);
+                const halfx8 al = *reinterpret_cast<const halfx8 *>(w + 1024);
+                acc[T] = mfma16x3(ah, al, xh, xl, acc[T]);
+            }
+        }
+    }
+    const float u = ldexpf(1.0f, -(wshift + eprev));
+#pragma unroll
+    for (int T = 0; T < 4; T++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) red[wave][T][v][lane] = acc[T][v] * u;
+    __syncthreads();
+    if (!live) return;
+    const int T = wave;
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+        const int n0 = 32 * (nt0 + T) + 16 * hh + 8 * g;
+        float yv[8];
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const int v = 8 * hh + t;
+            yv[t] = ((red[0][T][v][lane] + red[1][T][v][lane]) + red[2][T][v][lane]) + red[3][T][v][lane];
+        }
+        if (b) {
+            const float4 ba = *reinterpret_cast<const float4 *>(b + n0);
+            const float4 bb = *reinterpret_cast<const float4 *>(b + n0 + 4);
+            yv[0] += ba.x; yv[1] += ba.y; yv[2] += ba.z; yv[3] += ba.w;
+            yv[4] += bb.x; yv[5] += bb.y; yv[6] += bb.z; yv[7] += bb.w;
+        }
+        if (EPI == EPI_GELU) {
+#pragma unroll
+            for (int t = 0; t < 8; t++) yv[t] = gelu(yv[t]);
+        }
+        if (EPI == EPI_RESID) {
+            const float *rp = ea.R + (size_t)m * ea.ldr + n0;
+            const float4 ra = *reinterpret_cast<const float4 *>(rp);
+            const float4 rb = *reinterpret_cast<const float4 *>(rp + 4);
+            yv[0] += ra.x; yv[1] += ra.y; yv[2] += ra.z; yv[3] += ra.w;
+            yv[4] += rb.x; yv[5] += rb.y; yv[6] += rb.z; yv[7] += rb.w;
+        }
+        float *dst = Y + (size_t)m * ldy + n0;
+        *reinterpret_cast<float4 *>(dst) = make_float4(yv[0], yv[1], yv[2], yv[3]);
+        *reinterpret_cast<float4 *>(dst + 4) = make_float4(yv[4], yv[5], yv[6], yv[7]);
+    }
+}
+
+bool gemm_split_fits(int N, int K) { return N > 0 && N % 32 == 0 && K > 0 && K % 16 == 0; }
+
+template <int EPI>
+static void launch_split(hipStream_t s, int M, int N, int K, const float *X, int ldx, const SplitW &w, const float *b,
+                         float *Y, int ldy, const SplitEpi &ea) {
+    const int row_groups = (M + 127) / 128;
+    // two column tiles a wavefront halves the reads of X, when there are waves enough to fill the chip without
+    const bool wide = N % 64 == 0 && (long)row_groups * 4 * (N / 64) >= 2048;
+    if (wide)
+        hipLaunchKernelGGL((k_gemm_split<EPI, 2>), dim3(N / 64, row_groups), dim3(256), 0, s, M, N, K, X, ldx, w.img,
+                           w.shift, b, Y, ldy, ea);
+    else
+        hipLaunchKernelGGL((k_gemm_split<EPI, 1>), dim3(N / 32, row_groups), dim3(256), 0, s, M, N, K, X, ldx, w.img,
+                           w.shift, b, Y, ldy, ea);
+    TAH_LAUNCHED();
+}
+
+void gemm_split(hipStream_t s, int M, int N, int K, const float *X, int ldx, const SplitW &w, const float *b, float *Y,
+                int ldy, Epi epi, const float *R, int ldr, const float *scale, int heads) {
+    if (M <= 0) return;
+    if (!w.img || !gemm_split_fits(N, K) || K != w.K || w.row0 % 32 || N + w.row0 > w.N)
+        throw ArgError{"gemm_split: the weight image does not fit the product"};
+    if ((size_t)(M + 127) / 128 > 65535) throw ArgError{"gemm_split: too many rows for one launch"};
+    if ((ldx % 4) || (ldy % 4) || (reinterpret_cast<uintptr_t>(X) & 15) || (reinterpret_cast<uintptr_t>(Y) & 15))
+        throw ArgError{"gemm_split: rows must be 16-byte aligned"};
+    const SplitEpi ea{R, ldr, scale, heads > 0 ? heads : 1};
+    SplitW sub = w;
+    sub.img = w.img + (size_t)(w.row0 / 32) * (w.K / 16) * 2048;
+    switch (epi) {
+        case EPI_NONE: launch_split<EPI_NONE>(s, M, N, K, X, ldx, sub, b, Y, ldy, ea); break;
+        case EPI_GELU: launch_split<EPI_GELU>(s, M, N, K, X, ldx, sub, b, Y, ldy, ea); break;
+        case EPI_RESID: launch_split<EPI_RESID>(s, M, N, K, X, ldx, sub, b, Y, ldy, ea); break;
+        case EPI_QMOD: launch_split<EPI_QMOD>(s, M, N, K, X, ldx, sub, b, Y, ldy, ea); break;
+        case EPI_SCALE: launch_split<EPI_SCALE>(s, M, N, K, X, ldx, sub, b, Y, ldy, ea); break;
+        default: throw ArgError{"gemm_split: unknown epilogue"};
+    }
+}
+
+void dense(hipStream_t s, int M, int N, int K, const float *X, int ldx, const float *W, const SplitW &w, const float *b,
+           float *Y, int ldy, Epi epi, const float *R, int ldr) {
+    const bool img = w.img && gemm_split_fits(N, K) && K == w.K && w.row0 % 32 == 0 && N + w.row0 <= w.N &&
+                     ldx % 4 == 0 && ldy % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 &&
+                     (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
+    // below a few hundred rows the f32 kernels' weight streaming wins (measured at 64 and 256 rows)
+    if (!img || M < 512 || (epi != EPI_NONE && epi != EPI_GELU && epi != EPI_RESID)) {
+        gemm(s, M, N, K, X, ldx, W, b, Y, ldy, epi, R, ldr);
+        return;
+    }
+    if (N % 128 == 0 && K % 64 == 0 && K >= 256) {
+        if ((size_t)(M + 31) / 32 > 65535) throw ArgError{"dense: too many rows for one launch"};
+        const SplitEpi ea{R, ldr, nullptr, 1};
+        const uint8_t *sub = w.img + (size_t)(w.row0 / 32) * (w.K / 16) * 2048;
+        const dim3 grid(N / 128, (M + 31) / 32);
+        switch (epi) {
+            case EPI_NONE:
+                hipLaunchKernelGGL(k_gemm_splitk4<EPI_NONE>, grid, dim3(256), 0, s, M, N, K, X, ldx, sub, w.shift, b, Y, ldy, ea);
+                break;
+            case EPI_GELU:
+                hipLaunchKernelGGL(k_gemm_splitk4<EPI_GELU>, grid, dim3(256), 0, s, M, N, K, X, ldx, sub, w.shift, b, Y, ldy, ea);
+                break;
+            default:
+                hipLaunchKernelGGL(k_gemm_splitk4<EPI_RESID>, grid, dim3(256), 0, s, M, N, K, X, ldx, sub, w.shift, b, Y, ldy, ea);
+                break;
+        }
+        TAH_LAUNCHED();
+        return;
+    }
+    gemm_split(s, M, N, K, X, ldx, w, b, Y, ldy, epi, R, ldr, nullptr, 1);
+}
+
+}  // namespace tah

@@ -319,16 +319,31 @@ static void feed_forward(hipStream_t s, int M, float *x, const DevBlock &b, floa
     gemm(s, M, e, b.ff, mid, b.ff, b.l2w, b.l2b, x, e, EPI_RESID, x, e);
 }
 
+// x [M][e] += out(att): the block's output projection and residual add
+static void out_projection(hipStream_t s, int M, const float *att, const DevBlock &b, float *x) {
+    const int e = b.d;
+    if (b.outimg)
+        rows128(s, M, e, att, e, b.outimg, b.outs, b.out_b, x, e, EPI_RESID, x, e, nullptr, nullptr, nullptr);
+    else
+        dense(s, M, e, e, att, e, b.out_w, b.out_s, b.out_b, x, e, EPI_RESID, x, e);
+}
+
 // One column block (cached_block with a2) for all cells in place: n rows x groups, cell (r, g) at row r * sr + g * sg
 // of cells; K/V of group g at kvbase + g * gstride.
 void column_block(hipStream_t s, const tah_weights *w, const DevBlock &b, float *cells, int n, int groups, size_t sr,
                   size_t sg, const float *kvbase, size_t gstride, float *t, float *q, float *att, float *mid) {
     const int e = w->e;
     const int M = n * groups;
-    layer_norm(s, M, e, cells, e, b.n1w, b.n1b, t, e);
-    gemm(s, M, e, e, t, e, b.in_w, b.in_b, q, e, EPI_NONE, nullptr, 0);
-    if ((size_t)b.heads * b.ss_hidden > (size_t)b.ff) throw ArgError{"column stage: query MLP wider than the feed-forward"};
-    query_modulate(s, M, b, w->col_scale, q, mid);
+    if (b.inimg && b.ss_hidden == 0) {
+        // norm1, the query projection and its scale in one pass
+        rows128(s, M, e, cells, e, b.inimg, b.ins, b.in_b, q, e, EPI_SCALE, nullptr, 0, w->col_scale, b.n1w, b.n1b);
+    } else {
+        layer_norm(s, M, e, cells, e, b.n1w, b.n1b, t, e);
+        gemm(s, M, e, e, t, e, b.in_w, b.in_b, q, e, EPI_NONE, nullptr, 0);
+        if ((size_t)b.heads * b.ss_hidden > (size_t)b.ff)
+            throw ArgError{"column stage: query MLP wider than the feed-forward"};
+        query_modulate(s, M, b, w->col_scale, q, mid);
+    }
     const int hd = e / b.heads;
     const dim3 grid((n + 63) / 64, b.heads, groups);
     if (hd == 16 && w->inds == 128)
@@ -339,7 +354,7 @@ void column_block(hipStream_t s, const tah_weights *w, const DevBlock &b, float 
         hipLaunchKernelGGL(k_cell_attn_plain, blocks_for((size_t)M * b.heads), dim3(256), 0, s, n, groups, sr, sg, e,
                            b.heads, w->inds, q, kvbase, gstride, att);
     TAH_LAUNCHED();
-    gemm(s, M, e, e, att, e, b.out_w, b.out_b, cells, e, EPI_RESID, cells, e);
+    out_projection(s, M, att, b, cells);
     feed_forward(s, M, cells, b, t, mid);
 }
 
@@ -415,13 +430,18 @@ void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, co
     };
     for (int bi = 0; bi <= last; bi++) {
         const DevBlock &b = w->row[bi];
-        layer_norm(s, (int)R, e, tok, e, b.n1w, b.n1b, t, e);
-        gemm(s, (int)R, 3 * e, e, t, e, b.in_w, b.in_b, qkv, 3 * e, EPI_NONE, nullptr, 0);
+        if (b.inimg) {
+            rows128(s, (int)R, 3 * e, tok, e, b.inimg, b.ins, b.in_b, qkv, 3 * e, EPI_NONE, nullptr, 0, nullptr, b.n1w,
+                    b.n1b);
+        } else {
+            layer_norm(s, (int)R, e, tok, e, b.n1w, b.n1b, t, e);
+            gemm(s, (int)R, 3 * e, e, t, e, b.in_w, b.in_b, qkv, 3 * e, EPI_NONE, nullptr, 0);
+        }
         hipLaunchKernelGGL(k_rope, blocks_for(R * heads * half), dim3(256), 0, s, R, T, e, heads, half, cosv, sinv, qkv, inv);
         TAH_LAUNCHED();
         if (bi < last) {
             attend(T, att);
-            gemm(s, (int)R, e, e, att, e, b.out_w, b.out_b, tok, e, EPI_RESID, tok, e);
+            out_projection(s, (int)R, att, b, tok);
             feed_forward(s, (int)R, tok, b, t, mid);
         } else {
             // the last block: only the class tokens are queried and updated
@@ -429,7 +449,7 @@ void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, co
             attend(cls, ac);
             hipLaunchKernelGGL(k_first_tokens, blocks_for((size_t)M * e), dim3(256), 0, s, n, T, cls, e, tok, xc);
             TAH_LAUNCHED();
-            gemm(s, M, e, e, ac, e, b.out_w, b.out_b, xc, e, EPI_RESID, xc, e);
+            out_projection(s, M, ac, b, xc);
             feed_forward(s, M, xc, b, t, mid);
             layer_norm(s, M, e, xc, e, w->out_lnw, w->out_lnb, rep, e);
         }
