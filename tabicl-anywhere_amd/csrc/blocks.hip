@@ -10,7 +10,7 @@
 //  * the A operands, the weights, are read with their rows in sigma32 order, which leaves each lane's accumulators
 //    holding eight consecutive hidden units: exactly the B operand of the second product, so the hidden layer
 //    never leaves the registers;
-//  * the weights stream through two 16 KB LDS buffers, one slice per step, copied global -> LDS by DMA
+//  * the weights stream through two 32 KB LDS buffers, one slice per step, copied global -> LDS by DMA
 //    (global_load_lds_dwordx4) and shared by the workgroup's four wavefronts. They are stored pre-split at upload
 //    in exactly the order of those slices (weight_image in the C ABI: blocks of 128 rows, then 16-column steps);
 //  * the first product runs in two halves of 128 hidden units, each finished (bias, GELU, split) before the next,
@@ -23,7 +23,9 @@
 
 namespace tah {
 
-constexpr int SLAB = 16384;  // one weight slice in LDS
+constexpr int CPS = 4;              // 16-column steps (8 KB of a 128-row weight block) per weight slice
+constexpr int SLAB = CPS * 8192;    // one weight slice in LDS
+constexpr int NSL = 8 * 8192 / SLAB;  // slices per 128 x 128 weight block
 
 // bytes (a multiple of 4 KB) from global to LDS by 256 threads, 16 bytes a lane; wavefront w's 64 lanes fill the
 // 1 KB at 4096 i + 1024 w of copy i (a wavefront-uniform LDS base, the lanes' offsets implicit)
@@ -98,10 +100,13 @@ __global__ __launch_bounds__(256, 2) void k_ff128(int M, float *__restrict__ x, 
 #pragma unroll
     for (int ks = 0; ks < 8; ks++) split8(xv[ks], ldexpf(1.0f, sx), xh[ks], xl[ks]);
 
-    // H^T = W1 X^T in two halves of 128 hidden units (4 tiles of 32 each); the weights stream as 16 slices of
-    // 16 KB, W1's eight (half-major, two 16-column steps each) then W2's eight, slice j into buffer j % 2
+    // H^T = W1 X^T in two halves of 128 hidden units (4 tiles of 32 each); the weights stream as slices of CPS
+    // 16-column steps, W1's (half-major) then W2's, slice j into buffer j % 2
     const int arow = sigma32(r32);
-    auto slice = [&](int j) { return j < 8 ? w1img + (size_t)j * SLAB : w2img + (size_t)(j - 8) * SLAB; };
+    // slices 0 .. 2 NSL - 1: W1 (two 128-row blocks), then 2 NSL .. 4 NSL - 1: W2 (128 rows, 256 columns)
+    auto slice = [&](int j) {
+        return j < 2 * NSL ? w1img + (size_t)j * SLAB : w2img + (size_t)(j - 2 * NSL) * SLAB;
+    };
     halfx8 hh8[16], hl8[16];  // the hidden layer, split: 16-unit step k = 2 T + hh of half 0, then of half 1
     int shd[2];
 #pragma unroll
@@ -112,20 +117,20 @@ __global__ __launch_bounds__(256, 2) void k_ff128(int M, float *__restrict__ x, 
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[T][v] = 0.0f;
 #pragma unroll
-        for (int st = 0; st < 4; st++) {
-            const int j = 4 * half + st;
+        for (int st = 0; st < NSL; st++) {
+            const int j = NSL * half + st;
             __builtin_amdgcn_s_waitcnt(0);  // this wavefront's copies of slice j have landed
             __syncthreads();                // everyone's have; slice j - 1's buffer is free
             dma_to_lds(slice(j + 1), slab[(j + 1) & 1], SLAB, tid);
             const uint8_t *sl = slab[j & 1];
 #pragma unroll
-            for (int c = 0; c < 2; c++)
+            for (int c = 0; c < CPS; c++)
 #pragma unroll
                 for (int T = 0; T < 4; T++) {
                     const int n = 32 * T + arow;
                     const halfx8 ah = *reinterpret_cast<const halfx8 *>(sl + c * 8192 + (g * 128 + n) * 16);
                     const halfx8 al = *reinterpret_cast<const halfx8 *>(sl + c * 8192 + ((2 + g) * 128 + n) * 16);
-                    acc[T] = mfma16x3(ah, al, xh[2 * st + c], xl[2 * st + c], acc[T]);
+                    acc[T] = mfma16x3(ah, al, xh[CPS * st + c], xl[CPS * st + c], acc[T]);
                 }
         }
         // hidden unit of accumulator v of tile T: 128 half + 32 T + 16 (v / 8) + 8 g + v % 8
@@ -158,7 +163,7 @@ __global__ __launch_bounds__(256, 2) void k_ff128(int M, float *__restrict__ x, 
             }
     }
 
-    // Y^T = W2 H^T: 4 tiles of 32 outputs; slice 8 + st = hidden units 32 st..32 st + 31, two 8 KB steps. The two
+    // Y^T = W2 H^T: 4 tiles of 32 outputs; slice 2 NSL + st = hidden units 16 CPS st .. 16 CPS (st + 1) - 1. The two
     // halves of the hidden layer carry their own scales: between them the sums are rescaled (exactly) to the second.
     floatx16 y[4];
 #pragma unroll
@@ -166,25 +171,25 @@ __global__ __launch_bounds__(256, 2) void k_ff128(int M, float *__restrict__ x, 
 #pragma unroll
         for (int v = 0; v < 16; v++) y[T][v] = 0.0f;
 #pragma unroll
-    for (int st = 0; st < 8; st++) {
-        const int j = 8 + st;
-        if (st == 4) {
+    for (int st = 0; st < 2 * NSL; st++) {
+        const int j = 2 * NSL + st;
+        if (st == NSL) {
             const float r = ldexpf(1.0f, shd[1] - shd[0]);
 #pragma unroll
             for (int T = 0; T < 4; T++) y[T] *= r;
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        if (j + 1 < 16) dma_to_lds(slice(j + 1), slab[(j + 1) & 1], SLAB, tid);
+        if (j + 1 < 4 * NSL) dma_to_lds(slice(j + 1), slab[(j + 1) & 1], SLAB, tid);
         const uint8_t *sl = slab[j & 1];
 #pragma unroll
-        for (int c = 0; c < 2; c++)
+        for (int c = 0; c < CPS; c++)
 #pragma unroll
             for (int T = 0; T < 4; T++) {
                 const int n = 32 * T + arow;
                 const halfx8 ah = *reinterpret_cast<const halfx8 *>(sl + c * 8192 + (g * E + n) * 16);
                 const halfx8 al = *reinterpret_cast<const halfx8 *>(sl + c * 8192 + ((2 + g) * E + n) * 16);
-                y[T] = mfma16x3(ah, al, hh8[2 * st + c], hl8[2 * st + c], y[T]);
+                y[T] = mfma16x3(ah, al, hh8[CPS * st + c], hl8[CPS * st + c], y[T]);
             }
     }
     if (!live) return;

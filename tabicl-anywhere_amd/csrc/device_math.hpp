@@ -26,7 +26,8 @@ constexpr float LOG2E = 1.44269504088896340736f;
 // e^x by range reduction and a degree-7 polynomial, clamped to [-87, 88] (exp1, src/kern.rs:191-206); erf by
 // Abramowitz & Stegun 7.1.26 away from zero and its power series below |x| = 0.5 (erf1, src/kern.rs:230-255);
 // tanh through one exponential (tanh1, src/kern.rs:263-268); GELU as x (1 + erf(x / sqrt 2)) / 2
-// (src/kern.rs:257-261). The reciprocal in erf1 is v_rcp_f32's (1 ulp).
+// (src/kern.rs:257-261). In erf1 the reciprocal is v_rcp_f32's and e^(-a^2) the hardware exp2's (1 ulp each, against
+// exp1's own few ulp; the term they form is below 0.3).
 __device__ __forceinline__ float exp1(float x) {
     x = fminf(fmaxf(x, -87.0f), 88.0f);
     const float n = floorf(x * LOG2E + 0.5f);
@@ -50,7 +51,7 @@ __device__ __forceinline__ float erf1(float x) {
     p = p * t + 1.4214138f;
     p = p * t - 0.28449674f;
     p = p * t + 0.2548296f;
-    const float far = copysignf(1.0f - p * t * exp1(-a * a), x);
+    const float far = copysignf(1.0f - p * t * __builtin_amdgcn_exp2f(-a * a * LOG2E), x);
     const float x2 = x * x;
     float q = -1.0f / 1320.0f;
     q = q * x2 + 1.0f / 216.0f;
