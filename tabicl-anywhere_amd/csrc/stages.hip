@@ -229,6 +229,188 @@ __global__ __launch_bounds__(256) void k_row_attn16(int n, int T, int nq_tok, in
     }
 }
 
+__device__ __forceinline__ void load8(const float *p, float *v) {
+    const float4 a = *reinterpret_cast<const float4 *>(p), b = *reinterpret_cast<const float4 *>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+// ---- attention within each row on split-fp16 MFMA, rotary positions folded in: head width 16, T <= 128 ---------
+// grid (rows, heads); 256 threads. The row's keys and values of head h are loaded once per workgroup (one thread per
+// token), the keys rotated (RoPE, the k_rope formula), both scaled by the power of two that brings the head's
+// largest magnitude below 2^14 and split into fp16 hi/lo in LDS: K as [k half][key][8], V^T as
+// [16-key step][k half][coordinate][8] (every 16-lane read contiguous; coordinates XOR-swizzled by block so the
+// scattered writes spread over the banks). Wavefront w then takes query tokens
+// 32 w .. 32 w + 31 (lane = query, its two halves of the head's 16 coordinates on lanes l and l + 32, rotated
+// with one cross-lane exchange and multiplied by 1 / sqrt(16)): S^T = K Q^T for four 32-key tiles (K in sigma32
+// order), a plain softmax over the row's tokens (weights at most 2^12), and O^T = V^T P^T with the weights straight
+// from the accumulators as the B operand; V^T fills 16 of the 32 A-operand rows (the rest are zeros).
+__global__ __launch_bounds__(256) void k_row_attn_x3(int n, int T, int nq_tok, int e, const float *__restrict__ qkv,
+                                                      const float *__restrict__ cosv, const float *__restrict__ sinv,
+                                                      float *__restrict__ out) {
+    __shared__ __align__(16) _Float16 Kh[2][128][8], Kl[2][128][8];
+    __shared__ __align__(16) _Float16 Vh[8][2][16][8], Vl[8][2][16][8];
+    __shared__ float red[2][4];
+    const int r = blockIdx.x, h = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float *base = qkv + (size_t)r * T * 3 * e;
+    // keys and values, one token a thread
+    float kv[16], vv[16];
+    const bool tok_live = tid < T;
+    if (tok_live) {
+        const float *kp = base + (size_t)tid * 3 * e + e + h * 16;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 a = *reinterpret_cast<const float4 *>(kp + 4 * i);
+            const float4 b = *reinterpret_cast<const float4 *>(kp + e + 4 * i);
+            kv[4 * i] = a.x; kv[4 * i + 1] = a.y; kv[4 * i + 2] = a.z; kv[4 * i + 3] = a.w;
+            vv[4 * i] = b.x; vv[4 * i + 1] = b.y; vv[4 * i + 2] = b.z; vv[4 * i + 3] = b.w;
+        }
+        float cs[8], sn[8];
+        load8(cosv + tid * 8, cs);
+        load8(sinv + tid * 8, sn);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float a = kv[k], b = kv[k + 8];
+            kv[k] = a * cs[k] - b * sn[k];
+            kv[k + 8] = b * cs[k] + a * sn[k];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) kv[i] = vv[i] = 0.0f;
+    }
+    float mk = 0.0f, mv = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        mk = fmaxf(mk, fabsf(kv[i]));
+        mv = fmaxf(mv, fabsf(vv[i]));
+    }
+    mk = wave_max(mk);
+    mv = wave_max(mv);
+    if (lane == 0) {
+        red[0][wave] = mk;
+        red[1][wave] = mv;
+    }
+    __syncthreads();
+    const int sk = shift_for_max(fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3])));
+    const int sv = shift_for_max(fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3])));
+    if (tid < 128) {
+        halfx8 h0, l0, h1, l1;
+        split8(kv, ldexpf(1.0f, sk), h0, l0);
+        split8(kv + 8, ldexpf(1.0f, sk), h1, l1);
+        *reinterpret_cast<halfx8 *>(&Kh[0][tid][0]) = h0;
+        *reinterpret_cast<halfx8 *>(&Kl[0][tid][0]) = l0;
+        *reinterpret_cast<halfx8 *>(&Kh[1][tid][0]) = h1;
+        *reinterpret_cast<halfx8 *>(&Kl[1][tid][0]) = l1;
+        const int st = tid >> 4, kg = (tid >> 3) & 1, t8 = tid & 7;
+        const int sw = (2 * st + kg) & 15;  // coordinate c of block (st, kg) sits at row c ^ sw: one write's 8
+                                            // blocks then hit different banks
+        const float fv = ldexpf(1.0f, sv);
+#pragma unroll
+        for (int c = 0; c < 16; c++) {
+            const float x = vv[c] * fv;
+            const _Float16 hi = (_Float16)x;
+            Vh[st][kg][c ^ sw][t8] = hi;
+            Vl[st][kg][c ^ sw][t8] = (_Float16)(x - (float)hi);
+        }
+    }
+    __syncthreads();
+    const int r32 = lane & 31, g = lane >> 5;
+    const int qt = wave * 32 + r32;  // query token
+    if (wave * 32 >= nq_tok) return;
+    const bool live = qt < nq_tok;
+    // this lane's half of the query's coordinates (8 g .. 8 g + 7), rotated with the other half from lane l ^ 32
+    float qv[8];
+    {
+        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), b = a;
+        if (live) {
+            const float *qp = base + (size_t)qt * 3 * e + h * 16 + 8 * g;
+            a = *reinterpret_cast<const float4 *>(qp);
+            b = *reinterpret_cast<const float4 *>(qp + 4);
+        }
+        qv[0] = a.x; qv[1] = a.y; qv[2] = a.z; qv[3] = a.w; qv[4] = b.x; qv[5] = b.y; qv[6] = b.z; qv[7] = b.w;
+        const float sgn = g == 0 ? -1.0f : 1.0f;
+        float cs[8] = {1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f}, sn[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        if (live) {
+            load8(cosv + qt * 8, cs);
+            load8(sinv + qt * 8, sn);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float other = __shfl_xor(qv[k], 32, 64);
+            qv[k] = (qv[k] * cs[k] + sgn * other * sn[k]) * 0.25f;  // (a c - b s) or (b c + a s), times 1 / sqrt(16)
+        }
+    }
+    float qmax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) qmax = fmaxf(qmax, fabsf(qv[k]));
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
+    const int sq = shift_for_max(qmax);
+    halfx8 qh, ql;
+    split8(qv, ldexpf(1.0f, sq), qh, ql);
+    const float to_log2 = ldexpf(LOG2E, -(sk + sq));  // raw score -> score * log2 e (positive)
+    // S^T: key tiles of 32, rows in sigma32 order; accumulator v of tile kt holds key 32 kt + 16 (v / 8) + 8 g + v % 8
+    const int krow = sigma32(r32);
+    floatx16 sc[4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) sc[kt][v] = 0.0f;
+        const int key = 32 * kt + krow;  // keys past T are zero rows, masked below
+        const halfx8 ah = *reinterpret_cast<const halfx8 *>(&Kh[g][key][0]);
+        const halfx8 al = *reinterpret_cast<const halfx8 *>(&Kl[g][key][0]);
+        sc[kt] = mfma16x3(ah, al, qh, ql, sc[kt]);
+        if (32 * kt + 32 > T) {
+#pragma unroll
+            for (int v = 0; v < 16; v++)
+                if (32 * kt + 16 * (v >> 3) + 8 * g + (v & 7) >= T) sc[kt][v] = -INFINITY;
+        }
+#pragma unroll
+        for (int v = 0; v < 16; v++) mx = fmaxf(mx, sc[kt][v]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float off = 12.0f - mx * to_log2;
+    float l = 0.0f;
+    halfx8 ph[8], pl[8];  // 16-key step s = 2 kt + hh
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            float p[8];
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                p[t] = exp2_hw(fmaf(sc[kt][8 * hh + t], to_log2, off));
+                l += p[t];
+            }
+            split8(p, 1.0f, ph[2 * kt + hh], pl[2 * kt + hh]);
+        }
+    l += __shfl_xor(l, 32, 64);
+    // O^T = V^T P^T: A rows 0..15 the coordinates, 16..31 zero
+    floatx16 o;
+#pragma unroll
+    for (int v = 0; v < 16; v++) o[v] = 0.0f;
+    halfx8 zero8;
+#pragma unroll
+    for (int t = 0; t < 8; t++) zero8[t] = (_Float16)0.0f;
+#pragma unroll
+    for (int st = 0; st < 8; st++) {
+        if (16 * st >= T) break;
+        halfx8 ah = zero8, al = zero8;
+        if (r32 < 16) {
+            const int row = r32 ^ ((2 * st + g) & 15);
+            ah = *reinterpret_cast<const halfx8 *>(&Vh[st][g][row][0]);
+            al = *reinterpret_cast<const halfx8 *>(&Vl[st][g][row][0]);
+        }
+        o = mfma16x3(ah, al, ph[st], pl[st], o);
+    }
+    if (!live) return;
+    // accumulator v < 8 holds coordinate 8 (v / 4) + 4 g + v % 4 of this lane's query
+    const float f = ldexpf(1.0f, -sv) / l;
+    float *dst = out + ((size_t)r * nq_tok + qt) * e + h * 16;
+    *reinterpret_cast<float4 *>(dst + 4 * g) = make_float4(o[0] * f, o[1] * f, o[2] * f, o[3] * f);
+    *reinterpret_cast<float4 *>(dst + 8 + 4 * g) = make_float4(o[4] * f, o[5] * f, o[6] * f, o[7] * f);
+}
+
 // Any head width and token count: one thread per (row, query token, head).
 __global__ __launch_bounds__(256) void k_row_attn_plain(int n, int T, int nq_tok, int e, int heads,
                                                          const float *__restrict__ qkv, float *__restrict__ out) {
@@ -418,8 +600,11 @@ void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, co
     const float inv = 1.0f / sqrtf((float)hd);
     const int last = w->row_blocks - 1;
     const bool mfma = hd == 16 && T <= 256;
+    const bool fused = hd == 16 && half == 8 && T <= 128;  // rotary positions applied inside k_row_attn_x3
     auto attend = [&](int nq_tok, float *dst) {
-        if (mfma && T <= 128)
+        if (fused)
+            hipLaunchKernelGGL(k_row_attn_x3, dim3(n, heads), dim3(256), 0, s, n, T, nq_tok, e, qkv, cosv, sinv, dst);
+        else if (mfma && T <= 128)
             hipLaunchKernelGGL(k_row_attn16<8>, dim3(n, heads), dim3(256), 0, s, n, T, nq_tok, e, qkv, dst);
         else if (mfma)
             hipLaunchKernelGGL(k_row_attn16<16>, dim3(n, heads), dim3(256), 0, s, n, T, nq_tok, e, qkv, dst);
@@ -437,8 +622,11 @@ void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, co
             layer_norm(s, (int)R, e, tok, e, b.n1w, b.n1b, t, e);
             gemm(s, (int)R, 3 * e, e, t, e, b.in_w, b.in_b, qkv, 3 * e, EPI_NONE, nullptr, 0);
         }
-        hipLaunchKernelGGL(k_rope, blocks_for(R * heads * half), dim3(256), 0, s, R, T, e, heads, half, cosv, sinv, qkv, inv);
-        TAH_LAUNCHED();
+        if (!fused) {
+            hipLaunchKernelGGL(k_rope, blocks_for(R * heads * half), dim3(256), 0, s, R, T, e, heads, half, cosv, sinv,
+                               qkv, inv);
+            TAH_LAUNCHED();
+        }
         if (bi < last) {
             attend(T, att);
             out_projection(s, (int)R, att, b, tok);
