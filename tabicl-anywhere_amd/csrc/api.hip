@@ -584,21 +584,19 @@ static void stage_rows(tah_dev *dev, const tah_weights *w, const tah_model *mode
     for (int l = 0; l < w->icl_layers; l++) {
         const DevBlock &b = w->icl[l];
         // query: q = modulate(Wq norm1(h) + bq)  (src/nn.rs:130-152)
-        layer_norm(s, nq, d, h, d, b.n1w, b.n1b, t, d);
-        dense(s, nq, d, d, t, d, b.in_w, b.in_s.rows(0), b.in_b, q, d, EPI_NONE, nullptr, 0);
+        dense(s, nq, d, d, h, d, b.in_w, b.in_s.rows(0), b.in_b, q, d, EPI_NONE, nullptr, 0, b.n1w, b.n1b, t);
         query_modulate(s, nq, b, model->scales + (size_t)l * d, q, mid);
         // attention over the stored layer, then h += out(att)  (src/predict.rs:421-551)
         const KvImages img = images_of(model, l);
         attention(s, a, q, layer_of(model, l), att, work, &img);
         dense(s, nq, d, d, att, d, b.out_w, b.out_s, b.out_b, h, d, EPI_RESID, h, d);
         // h += l2(gelu(l1(norm2 h)))  (src/predict.rs:552-568)
-        layer_norm(s, nq, d, h, d, b.n2w, b.n2b, t, d);
-        dense(s, nq, b.ff, d, t, d, b.l1w, b.l1_s, b.l1b, mid, b.ff, EPI_GELU, nullptr, 0);
+        dense(s, nq, b.ff, d, h, d, b.l1w, b.l1_s, b.l1b, mid, b.ff, EPI_GELU, nullptr, 0, b.n2w, b.n2b, t);
         dense(s, nq, d, b.ff, mid, b.ff, b.l2w, b.l2_s, b.l2b, h, d, EPI_RESID, h, d);
     }
     // decoder, first out_n outputs  (src/predict.rs:570-585)
-    layer_norm(s, nq, d, h, d, w->lnw, w->lnb, t, d);
-    dense(s, nq, w->dec_hidden, d, t, d, w->dec0w, w->dec0_s, w->dec0b, mid, w->dec_hidden, EPI_GELU, nullptr, 0);
+    dense(s, nq, w->dec_hidden, d, h, d, w->dec0w, w->dec0_s, w->dec0b, mid, w->dec_hidden, EPI_GELU, nullptr, 0, w->lnw,
+          w->lnb, t);
     gemm(s, nq, out_n, w->dec_hidden, mid, w->dec_hidden, w->dec2w, w->dec2b, out, out_n, EPI_NONE, nullptr, 0);
 }
 

@@ -140,9 +140,11 @@ void gemm_qmod(hipStream_t s, int M, int N, int K, const float *X, int ldx, cons
 bool gemm_split_fits(int N, int K);
 void gemm_split(hipStream_t s, int M, int N, int K, const float *X, int ldx, const SplitW &w, const float *b, float *Y,
                 int ldy, Epi epi, const float *R, int ldr, const float *scale, int heads);
-// gemm_split where the image fits and there are 32 rows or more, else gemm on the f32 weights.
+// The split-fp16 kernels where the image fits and there are 512 rows or more, else gemm on the f32 weights. With
+// lnw/lnb the rows of X are layer-normalised first: inside the kernel for K = 512, else through t [M][K].
 void dense(hipStream_t s, int M, int N, int K, const float *X, int ldx, const float *W, const SplitW &w, const float *b,
-           float *Y, int ldy, Epi epi, const float *R, int ldr);
+           float *Y, int ldy, Epi epi, const float *R, int ldr, const float *lnw = nullptr, const float *lnb = nullptr,
+           float *t = nullptr);
 
 // y[r] = layer_norm(x[r]) * w + b over rows of n numbers (eps 1e-5, biased variance).
 void layer_norm(hipStream_t s, int rows, int n, const float *x, int ldx, const float *w, const float *b, float *y,
@@ -152,6 +154,9 @@ void layer_norm(hipStream_t s, int rows, int n, const float *x, int ldx, const f
 // q_h *= scale_h * (1 + tanh(q2 gelu(q0 q_h + q0b) + q2b)). scratch holds rows * heads * ss_hidden floats.
 void query_modulate(hipStream_t s, int rows, const DevBlock &b, const float *scale, float *q, float *scratch);
 size_t query_scratch_floats(int rows, const DevBlock &b);
+// The whole query MLP in one kernel (gemm_split.hip), for head width 64 and hidden width 64 with images.
+bool qmlp_fused(const DevBlock &b);
+void qmlp(hipStream_t s, int rows, const DevBlock &b, const float *scale, float *q);
 
 // Fused feed-forward sub-block (blocks.hip): x [M][128] += l2(gelu(l1(layer_norm2(x)))) in one kernel, the hidden
 // layer kept in registers; for blocks of width 128 and hidden width 256 (ff_fused_shape), else the caller runs

@@ -137,11 +137,13 @@ __global__ __launch_bounds__(256, 3) void k_gemm_split(int M, int N, int K, cons
 // powers of two), then summing their partial products -- unscaled to f32 -- through LDS; wavefront w finishes
 // tile w. Four times the wavefronts of k_gemm_split on the same grid of outputs, each with a quarter of the
 // dependent chain.
-template <int EPI>
+template <int EPI, bool LN>
 __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, const float *__restrict__ X, int ldx,
                                                           const uint8_t *__restrict__ wimg, int wshift,
-                                                          const float *__restrict__ b, float *Y, int ldy, SplitEpi ea) {
+                                                          const float *__restrict__ b, float *Y, int ldy, SplitEpi ea,
+                                                          const float *__restrict__ lnw, const float *__restrict__ lnb) {
     __shared__ float red[4][4][16][64];  // [wavefront][tile][accumulator][lane]
+    __shared__ float rsum[4][32];        // LN: per-wavefront partial row sums
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r32 = lane & 31, g = lane >> 5;
     const int m = blockIdx.y * 32 + r32;
@@ -168,6 +170,45 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
             }
             xv[ks][0] = a.x; xv[ks][1] = a.y; xv[ks][2] = a.z; xv[ks][3] = a.w;
             xv[ks][4] = c.x; xv[ks][5] = c.y; xv[ks][6] = c.z; xv[ks][7] = c.w;
+        }
+        if (LN) {
+            // K = 512: this wavefront holds columns 128 w .. 128 w + 127 of its 32 rows; the row's sums go
+            // through LDS (two passes: mean, then biased variance; eps 1e-5)
+            float sum = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+                for (int t = 0; t < 8; t++) sum += xv[ks][t];
+            sum += __shfl_xor(sum, 32, 64);
+            if (g == 0) rsum[wave][r32] = sum;
+            __syncthreads();
+            const float mean = (((rsum[0][r32] + rsum[1][r32]) + rsum[2][r32]) + rsum[3][r32]) / (float)K;
+            float sq = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+                for (int t = 0; t < 8; t++) {
+                    const float dv = xv[ks][t] - mean;
+                    sq += dv * dv;
+                }
+            sq += __shfl_xor(sq, 32, 64);
+            __syncthreads();
+            if (g == 0) rsum[wave][r32] = sq;
+            __syncthreads();
+            const float inv = 1.0f / sqrtf((((rsum[0][r32] + rsum[1][r32]) + rsum[2][r32]) + rsum[3][r32]) / (float)K +
+                                           1e-5f);
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++) {
+                float wv[8], bv[8];
+                const int c0 = k0 + 16 * ks + 8 * g;
+#pragma unroll
+                for (int t = 0; t < 8; t++) {
+                    wv[t] = lnw[c0 + t];
+                    bv[t] = lnb[c0 + t];
+                }
+#pragma unroll
+                for (int t = 0; t < 8; t++) xv[ks][t] = (xv[ks][t] - mean) * inv * wv[t] + bv[t];
+            }
         }
         float xmax = 0.0f;
 #pragma unroll
@@ -238,6 +279,123 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
     }
 }
 
+// ---- the query MLP of the scalable softmax, whole, for head width 64 and hidden width 64 ------------------------
+// q [rows * heads][64] in place: q *= scale[h] * (1 + tanh1(W2 gelu(W0 q + b0) + b2)) (src/nn.rs:130-152). Each
+// wavefront owns 32 query-heads (lane = query-head, its 64 coordinates on lanes l and l + 32), split once; H^T =
+// W0 X^T with W0's rows in sigma32 order leaves the hidden layer in registers as the B operand of Y^T = W2 H^T, and
+// the lane's output columns are exactly the input columns it holds, so the modulation needs no second read of q.
+// W0 and W2 are read from their gemm_split images.
+__global__ __launch_bounds__(256) void k_qmlp64(int M, int heads, float *__restrict__ q, const uint8_t *__restrict__ w0,
+                                                int s0, const float *__restrict__ b0, const uint8_t *__restrict__ w2,
+                                                int s2, const float *__restrict__ b2, const float *__restrict__ scale) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r32 = lane & 31, g = lane >> 5;
+    const int m = (blockIdx.x * 4 + wave) * 32 + r32;
+    const bool live = m < M;
+    float *qr = q + (size_t)(live ? m : 0) * 64;
+    float xv[4][8];
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), c = a;
+        if (live) {
+            a = *reinterpret_cast<const float4 *>(qr + 16 * ks + 8 * g);
+            c = *reinterpret_cast<const float4 *>(qr + 16 * ks + 8 * g + 4);
+        }
+        xv[ks][0] = a.x; xv[ks][1] = a.y; xv[ks][2] = a.z; xv[ks][3] = a.w;
+        xv[ks][4] = c.x; xv[ks][5] = c.y; xv[ks][6] = c.z; xv[ks][7] = c.w;
+    }
+    float xmax = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+        for (int t = 0; t < 8; t++) xmax = fmaxf(xmax, fabsf(xv[ks][t]));
+    xmax = fmaxf(xmax, __shfl_xor(xmax, 32, 64));
+    const int sx = shift_for_max(xmax);
+    halfx8 xh[4], xl[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) split8(xv[ks], ldexpf(1.0f, sx), xh[ks], xl[ks]);
+    // hidden = gelu(W0 x + b0): 2 tiles of 32, 4 steps of 16 (image: (tile * 4 + step) * 2 KB)
+    floatx16 hacc[2];
+#pragma unroll
+    for (int T = 0; T < 2; T++) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) hacc[T][v] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const uint8_t *w = w0 + ((size_t)T * 4 + ks) * 2048 + (g * 32 + r32) * 16;
+            hacc[T] = mfma16x3(*reinterpret_cast<const halfx8 *>(w), *reinterpret_cast<const halfx8 *>(w + 1024),
+                               xh[ks], xl[ks], hacc[T]);
+        }
+    }
+    const float u0 = ldexpf(1.0f, -(sx + s0));
+    float hmax = 0.0f;
+#pragma unroll
+    for (int T = 0; T < 2; T++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const float *bp = b0 + 32 * T + 16 * hh + 8 * g;
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const float hv = gelu(hacc[T][8 * hh + t] * u0 + bp[t]);
+                hacc[T][8 * hh + t] = hv;
+                hmax = fmaxf(hmax, fabsf(hv));
+            }
+        }
+    hmax = fmaxf(hmax, __shfl_xor(hmax, 32, 64));
+    const int sh = shift_for_max(hmax);
+    halfx8 hh8[4], hl8[4];
+#pragma unroll
+    for (int T = 0; T < 2; T++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            float hv[8];
+#pragma unroll
+            for (int t = 0; t < 8; t++) hv[t] = hacc[T][8 * hh + t];
+            split8(hv, ldexpf(1.0f, sh), hh8[2 * T + hh], hl8[2 * T + hh]);
+        }
+    // y = W2 hidden + b2; q *= scale (1 + tanh1(y)); output column 32 T + 16 hh + 8 g + t is input step 2 T + hh
+    floatx16 yacc[2];
+#pragma unroll
+    for (int T = 0; T < 2; T++) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) yacc[T][v] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const uint8_t *w = w2 + ((size_t)T * 4 + ks) * 2048 + (g * 32 + r32) * 16;
+            yacc[T] = mfma16x3(*reinterpret_cast<const halfx8 *>(w), *reinterpret_cast<const halfx8 *>(w + 1024),
+                               hh8[ks], hl8[ks], yacc[T]);
+        }
+    }
+    if (!live) return;
+    const float u2 = ldexpf(1.0f, -(sh + s2));
+    const float *sc = scale + (size_t)(m % heads) * 64;
+#pragma unroll
+    for (int T = 0; T < 2; T++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const int n0 = 32 * T + 16 * hh + 8 * g;
+            float out[8];
+#pragma unroll
+            for (int t = 0; t < 8; t++)
+                out[t] = xv[2 * T + hh][t] * (sc[n0 + t] * (1.0f + tanh1(yacc[T][8 * hh + t] * u2 + b2[n0 + t])));
+            *reinterpret_cast<float4 *>(qr + n0) = make_float4(out[0], out[1], out[2], out[3]);
+            *reinterpret_cast<float4 *>(qr + n0 + 4) = make_float4(out[4], out[5], out[6], out[7]);
+        }
+}
+
+bool qmlp_fused(const DevBlock &b) {
+    return b.heads > 0 && b.d == 64 * b.heads && b.ss_hidden == 64 && b.q0_s.img && b.q2_s.img && b.q0_s.K == 64 &&
+           b.q2_s.K == 64 && b.q0_s.N == 64 && b.q2_s.N == 64;
+}
+
+void qmlp(hipStream_t s, int rows, const DevBlock &b, const float *scale, float *q) {
+    const int M = rows * b.heads;
+    if (M <= 0) return;
+    hipLaunchKernelGGL(k_qmlp64, dim3((M + 127) / 128), dim3(256), 0, s, M, b.heads, q, b.q0_s.img, b.q0_s.shift, b.q0b,
+                       b.q2_s.img, b.q2_s.shift, b.q2b, scale);
+    TAH_LAUNCHED();
+}
+
 bool gemm_split_fits(int N, int K) { return N > 0 && N % 32 == 0 && K > 0 && K % 16 == 0; }
 
 template <int EPI>
@@ -276,33 +434,56 @@ void gemm_split(hipStream_t s, int M, int N, int K, const float *X, int ldx, con
     }
 }
 
+template <bool LN>
+static void launch_splitk4(hipStream_t s, int M, int N, int K, const float *X, int ldx, const uint8_t *img, int shift,
+                           const float *b, float *Y, int ldy, Epi epi, const SplitEpi &ea, const float *lnw,
+                           const float *lnb) {
+    const dim3 grid(N / 128, (M + 31) / 32);
+    switch (epi) {
+        case EPI_NONE:
+            hipLaunchKernelGGL((k_gemm_splitk4<EPI_NONE, LN>), grid, dim3(256), 0, s, M, N, K, X, ldx, img, shift, b, Y,
+                               ldy, ea, lnw, lnb);
+            break;
+        case EPI_GELU:
+            hipLaunchKernelGGL((k_gemm_splitk4<EPI_GELU, LN>), grid, dim3(256), 0, s, M, N, K, X, ldx, img, shift, b, Y,
+                               ldy, ea, lnw, lnb);
+            break;
+        default:
+            hipLaunchKernelGGL((k_gemm_splitk4<EPI_RESID, LN>), grid, dim3(256), 0, s, M, N, K, X, ldx, img, shift, b, Y,
+                               ldy, ea, lnw, lnb);
+            break;
+    }
+    TAH_LAUNCHED();
+}
+
 void dense(hipStream_t s, int M, int N, int K, const float *X, int ldx, const float *W, const SplitW &w, const float *b,
-           float *Y, int ldy, Epi epi, const float *R, int ldr) {
+           float *Y, int ldy, Epi epi, const float *R, int ldr, const float *lnw, const float *lnb, float *t) {
     const bool img = w.img && gemm_split_fits(N, K) && K == w.K && w.row0 % 32 == 0 && N + w.row0 <= w.N &&
                      ldx % 4 == 0 && ldy % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 &&
                      (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
     // below a few hundred rows the f32 kernels' weight streaming wins (measured at 64 and 256 rows)
-    if (!img || M < 512 || (epi != EPI_NONE && epi != EPI_GELU && epi != EPI_RESID)) {
+    const bool split = img && M >= 512 && (epi == EPI_NONE || epi == EPI_GELU || epi == EPI_RESID);
+    const bool k4 = split && N % 128 == 0 && K % 64 == 0 && K >= 256;
+    if (lnw && !(k4 && K == 512)) {
+        // layer normalisation first, into t
+        if (!t) throw ArgError{"dense: layer normalisation needs a scratch buffer"};
+        layer_norm(s, M, K, X, ldx, lnw, lnb, t, K);
+        X = t;
+        ldx = K;
+        lnw = lnb = nullptr;
+    }
+    if (!split) {
         gemm(s, M, N, K, X, ldx, W, b, Y, ldy, epi, R, ldr);
         return;
     }
-    if (N % 128 == 0 && K % 64 == 0 && K >= 256) {
+    if (k4) {
         if ((size_t)(M + 31) / 32 > 65535) throw ArgError{"dense: too many rows for one launch"};
         const SplitEpi ea{R, ldr, nullptr, 1};
         const uint8_t *sub = w.img + (size_t)(w.row0 / 32) * (w.K / 16) * 2048;
-        const dim3 grid(N / 128, (M + 31) / 32);
-        switch (epi) {
-            case EPI_NONE:
-                hipLaunchKernelGGL(k_gemm_splitk4<EPI_NONE>, grid, dim3(256), 0, s, M, N, K, X, ldx, sub, w.shift, b, Y, ldy, ea);
-                break;
-            case EPI_GELU:
-                hipLaunchKernelGGL(k_gemm_splitk4<EPI_GELU>, grid, dim3(256), 0, s, M, N, K, X, ldx, sub, w.shift, b, Y, ldy, ea);
-                break;
-            default:
-                hipLaunchKernelGGL(k_gemm_splitk4<EPI_RESID>, grid, dim3(256), 0, s, M, N, K, X, ldx, sub, w.shift, b, Y, ldy, ea);
-                break;
-        }
-        TAH_LAUNCHED();
+        if (lnw)
+            launch_splitk4<true>(s, M, N, K, X, ldx, sub, w.shift, b, Y, ldy, epi, ea, lnw, lnb);
+        else
+            launch_splitk4<false>(s, M, N, K, X, ldx, sub, w.shift, b, Y, ldy, epi, ea, nullptr, nullptr);
         return;
     }
     gemm_split(s, M, N, K, X, ldx, w, b, Y, ldy, epi, R, ldr, nullptr, 1);

@@ -55,6 +55,10 @@ void query_modulate(hipStream_t s, int rows, const DevBlock &b, const float *sca
         return;
     }
     const int hd = b.d / b.heads, M = rows * b.heads;
+    if (M >= 32 && qmlp_fused(b)) {
+        qmlp(s, rows, b, scale, q);
+        return;
+    }
     dense(s, M, b.ss_hidden, hd, q, hd, b.q0w, b.q0_s, b.q0b, scratch, b.ss_hidden, EPI_GELU, nullptr, 0);
     if (M >= 32 && b.q2_s.img && gemm_split_fits(hd, b.ss_hidden) && b.ss_hidden % 4 == 0)
         gemm_split(s, M, hd, b.ss_hidden, scratch, b.ss_hidden, b.q2_s, b.q2b, q, hd, EPI_QMOD, q, hd, scale, b.heads);

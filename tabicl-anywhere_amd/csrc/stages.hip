@@ -17,6 +17,11 @@
 
 namespace tah {
 
+__device__ __forceinline__ void load8(const float *p, float *v) {
+    const float4 a = *reinterpret_cast<const float4 *>(p), b = *reinterpret_cast<const float4 *>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
 // ---- input layer -------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_input_cells(int n, int features, int group, int e, const float *__restrict__ x,
                                                       const float *__restrict__ in_w, const float *__restrict__ in_b,
@@ -105,6 +110,136 @@ __global__ __launch_bounds__(256) void k_cell_attn16(int n, size_t sr, size_t sg
         const float inv = 1.0f / l;
         *reinterpret_cast<float4 *>(out + m * e + h * 16 + 4 * g4) = make_float4(acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv);
     }
+}
+
+// ---- cells against their group's inducing keys on split-fp16 MFMA: head width 16, 128 keys ----------------------
+// grid (ceil(n / 128), heads, groups); 256 threads. The group's keys and values of head h (the column cache,
+// [coordinate][key] f32) are split into fp16 hi/lo in LDS by the workgroup (one key a thread, the head's largest
+// magnitude scaled below 2^14), laid out as in k_row_attn_x3; wavefront w takes cells of rows 128 x + 32 w + 0..31.
+// S^T = K Q^T over four 32-key tiles, a plain softmax over the 128 keys, O^T = V^T P^T.
+__global__ __launch_bounds__(256) void k_cell_attn_x3(int n, size_t sr, size_t sg, int e, const float *__restrict__ q,
+                                                       const float *__restrict__ kvbase, size_t gstride,
+                                                       float *__restrict__ out) {
+    constexpr int INDS = 128;
+    __shared__ __align__(16) _Float16 Kh[2][128][8], Kl[2][128][8];
+    __shared__ __align__(16) _Float16 Vh[8][2][16][8], Vl[8][2][16][8];
+    __shared__ float red[2][4];
+    const int h = blockIdx.y, grp = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float *K = kvbase + (size_t)grp * gstride, *V = K + (size_t)e * INDS;
+    float kv[16], vv[16];
+    if (tid < INDS) {
+#pragma unroll
+        for (int c = 0; c < 16; c++) {
+            kv[c] = K[(size_t)(h * 16 + c) * INDS + tid];
+            vv[c] = V[(size_t)(h * 16 + c) * INDS + tid];
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < 16; c++) kv[c] = vv[c] = 0.0f;
+    }
+    float mk = 0.0f, mv = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        mk = fmaxf(mk, fabsf(kv[i]));
+        mv = fmaxf(mv, fabsf(vv[i]));
+    }
+    mk = wave_max(mk);
+    mv = wave_max(mv);
+    if (lane == 0) {
+        red[0][wave] = mk;
+        red[1][wave] = mv;
+    }
+    __syncthreads();
+    const int sk = shift_for_max(fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3])));
+    const int sv = shift_for_max(fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3])));
+    if (tid < INDS) {
+        halfx8 h0, l0, h1, l1;
+        split8(kv, ldexpf(1.0f, sk), h0, l0);
+        split8(kv + 8, ldexpf(1.0f, sk), h1, l1);
+        *reinterpret_cast<halfx8 *>(&Kh[0][tid][0]) = h0;
+        *reinterpret_cast<halfx8 *>(&Kl[0][tid][0]) = l0;
+        *reinterpret_cast<halfx8 *>(&Kh[1][tid][0]) = h1;
+        *reinterpret_cast<halfx8 *>(&Kl[1][tid][0]) = l1;
+        const int st = tid >> 4, kg = (tid >> 3) & 1, t8 = tid & 7;
+        const int sw = (2 * st + kg) & 15;
+        const float fv = ldexpf(1.0f, sv);
+#pragma unroll
+        for (int c = 0; c < 16; c++) {
+            const float x = vv[c] * fv;
+            const _Float16 hi = (_Float16)x;
+            Vh[st][kg][c ^ sw][t8] = hi;
+            Vl[st][kg][c ^ sw][t8] = (_Float16)(x - (float)hi);
+        }
+    }
+    __syncthreads();
+    const int r32 = lane & 31, g = lane >> 5;
+    const int r = blockIdx.x * 128 + wave * 32 + r32;
+    if (blockIdx.x * 128 + wave * 32 >= n) return;
+    const bool live = r < n;
+    const size_t m = (size_t)(live ? r : 0) * sr + (size_t)grp * sg;
+    float qv[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    if (live) load8(q + m * e + h * 16 + 8 * g, qv);
+    float qmax = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) qmax = fmaxf(qmax, fabsf(qv[k]));
+    qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
+    const int sq = shift_for_max(qmax);
+    halfx8 qh, ql;
+    split8(qv, ldexpf(1.0f, sq), qh, ql);
+    const float to_log2 = ldexpf(LOG2E, -(sk + sq));
+    const int krow = sigma32(r32);
+    floatx16 sc[4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) sc[kt][v] = 0.0f;
+        const int key = 32 * kt + krow;
+        const halfx8 ah = *reinterpret_cast<const halfx8 *>(&Kh[g][key][0]);
+        const halfx8 al = *reinterpret_cast<const halfx8 *>(&Kl[g][key][0]);
+        sc[kt] = mfma16x3(ah, al, qh, ql, sc[kt]);
+#pragma unroll
+        for (int v = 0; v < 16; v++) mx = fmaxf(mx, sc[kt][v]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float off = 12.0f - mx * to_log2;
+    float l = 0.0f;
+    halfx8 ph[8], pl[8];
+#pragma unroll
+    for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            float p[8];
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                p[t] = exp2_hw(fmaf(sc[kt][8 * hh + t], to_log2, off));
+                l += p[t];
+            }
+            split8(p, 1.0f, ph[2 * kt + hh], pl[2 * kt + hh]);
+        }
+    l += __shfl_xor(l, 32, 64);
+    floatx16 o;
+#pragma unroll
+    for (int v = 0; v < 16; v++) o[v] = 0.0f;
+    halfx8 zero8;
+#pragma unroll
+    for (int t = 0; t < 8; t++) zero8[t] = (_Float16)0.0f;
+#pragma unroll
+    for (int st = 0; st < 8; st++) {
+        halfx8 ah = zero8, al = zero8;
+        if (r32 < 16) {
+            const int row = r32 ^ ((2 * st + g) & 15);
+            ah = *reinterpret_cast<const halfx8 *>(&Vh[st][g][row][0]);
+            al = *reinterpret_cast<const halfx8 *>(&Vl[st][g][row][0]);
+        }
+        o = mfma16x3(ah, al, ph[st], pl[st], o);
+    }
+    if (!live) return;
+    const float f = ldexpf(1.0f, -sv) / l;
+    float *dst = out + m * e + h * 16;
+    *reinterpret_cast<float4 *>(dst + 4 * g) = make_float4(o[0] * f, o[1] * f, o[2] * f, o[3] * f);
+    *reinterpret_cast<float4 *>(dst + 8 + 4 * g) = make_float4(o[4] * f, o[5] * f, o[6] * f, o[7] * f);
 }
 
 // Any head width and key count (the tiny test models): one thread per (cell, head).
@@ -227,11 +362,6 @@ __global__ __launch_bounds__(256) void k_row_attn16(int n, int T, int nq_tok, in
                 make_float4(acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv);
         }
     }
-}
-
-__device__ __forceinline__ void load8(const float *p, float *v) {
-    const float4 a = *reinterpret_cast<const float4 *>(p), b = *reinterpret_cast<const float4 *>(p + 4);
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
 // ---- attention within each row on split-fp16 MFMA, rotary positions folded in: head width 16, T <= 128 ---------
@@ -529,7 +659,8 @@ void column_block(hipStream_t s, const tah_weights *w, const DevBlock &b, float 
     const int hd = e / b.heads;
     const dim3 grid((n + 63) / 64, b.heads, groups);
     if (hd == 16 && w->inds == 128)
-        hipLaunchKernelGGL(k_cell_attn16<8>, grid, dim3(256), 0, s, n, sr, sg, e, q, kvbase, gstride, att);
+        hipLaunchKernelGGL(k_cell_attn_x3, dim3((n + 127) / 128, b.heads, groups), dim3(256), 0, s, n, sr, sg, e, q,
+                           kvbase, gstride, att);
     else if (hd == 16 && w->inds == 256)
         hipLaunchKernelGGL(k_cell_attn16<16>, grid, dim3(256), 0, s, n, sr, sg, e, q, kvbase, gstride, att);
     else
