@@ -27,15 +27,18 @@ constexpr int CPS = 4;              // 16-column steps (8 KB of a 128-row weight
 constexpr int SLAB = CPS * 8192;    // one weight slice in LDS
 constexpr int NSL = 8 * 8192 / SLAB;  // slices per 128 x 128 weight block
 
-// bytes (a multiple of 4 KB) from global to LDS by 256 threads, 16 bytes a lane; wavefront w's 64 lanes fill the
-// 1 KB at 4096 i + 1024 w of copy i (a wavefront-uniform LDS base, the lanes' offsets implicit)
+// bytes (a multiple of 16 * THREADS) from global to LDS by THREADS threads, 16 bytes a lane; in copy i wavefront w's
+// 64 lanes fill the 1 KB at 16 THREADS i + 1024 w (a wavefront-uniform LDS base, the lanes' offsets implicit)
+template <int THREADS = 256>
 __device__ __forceinline__ void dma_to_lds(const uint8_t *src, uint8_t *dst, int bytes, int tid) {
-    for (int o = 0; o < bytes; o += 4096)
+    for (int o = 0; o < bytes; o += 16 * THREADS)
         __builtin_amdgcn_global_load_lds(src + o + 16 * tid, dst + o + 1024 * (tid >> 6), 16, 0, 0);
 }
 
-// grid ceil(M / 128); 256 threads. x [M][128] in place.
-__global__ __launch_bounds__(256, 2) void k_ff128(int M, float *__restrict__ x, const float *__restrict__ lnw,
+constexpr int FFW = 4;  // wavefronts (of 32 rows each) per k_ff128 workgroup (eight, one workgroup a CU, measured slower)
+
+// grid ceil(M / (32 FFW)); 64 FFW threads. x [M][128] in place.
+__global__ __launch_bounds__(64 * FFW, 2) void k_ff128(int M, float *__restrict__ x, const float *__restrict__ lnw,
                                                    const float *__restrict__ lnb, const uint8_t *__restrict__ w1img,
                                                    const float *__restrict__ b1, int s1,
                                                    const uint8_t *__restrict__ w2img, const float *__restrict__ b2,
@@ -44,9 +47,9 @@ __global__ __launch_bounds__(256, 2) void k_ff128(int M, float *__restrict__ x, 
     __shared__ __align__(16) uint8_t slab[2][SLAB];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r32 = lane & 31, g = lane >> 5;
-    const int m = blockIdx.x * 128 + wave * 32 + r32;
+    const int m = blockIdx.x * 32 * FFW + wave * 32 + r32;
     const bool live = m < M;
-    dma_to_lds(w1img, slab[0], SLAB, tid);
+    dma_to_lds<64 * FFW>(w1img, slab[0], SLAB, tid);
 
     // this lane's half of row m: columns 16 ks + 8 g + t
     float xv[8][8];
@@ -121,7 +124,7 @@ __global__ __launch_bounds__(256, 2) void k_ff128(int M, float *__restrict__ x, 
             const int j = NSL * half + st;
             __builtin_amdgcn_s_waitcnt(0);  // this wavefront's copies of slice j have landed
             __syncthreads();                // everyone's have; slice j - 1's buffer is free
-            dma_to_lds(slice(j + 1), slab[(j + 1) & 1], SLAB, tid);
+            dma_to_lds<64 * FFW>(slice(j + 1), slab[(j + 1) & 1], SLAB, tid);
             const uint8_t *sl = slab[j & 1];
 #pragma unroll
             for (int c = 0; c < CPS; c++)
@@ -180,7 +183,7 @@ __global__ __launch_bounds__(256, 2) void k_ff128(int M, float *__restrict__ x, 
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        if (j + 1 < 4 * NSL) dma_to_lds(slice(j + 1), slab[(j + 1) & 1], SLAB, tid);
+        if (j + 1 < 4 * NSL) dma_to_lds<64 * FFW>(slice(j + 1), slab[(j + 1) & 1], SLAB, tid);
         const uint8_t *sl = slab[j & 1];
 #pragma unroll
         for (int c = 0; c < CPS; c++)
@@ -216,7 +219,7 @@ __global__ __launch_bounds__(256, 2) void k_ff128(int M, float *__restrict__ x, 
 void ff_block(hipStream_t s, int M, float *x, const DevBlock &b) {
     if (M <= 0) return;
     if (!ff_fused_shape(b.d, b.ff) || !b.l1img || !b.l2img) throw ArgError{"ff_block: no fused weights for this shape"};
-    hipLaunchKernelGGL(k_ff128, dim3((M + 127) / 128), dim3(256), 0, s, M, x, b.n2w, b.n2b, b.l1img, b.l1b, b.l1s,
+    hipLaunchKernelGGL(k_ff128, dim3((M + 32 * FFW - 1) / (32 * FFW)), dim3(64 * FFW), 0, s, M, x, b.n2w, b.n2b, b.l1img, b.l1b, b.l1s,
                        b.l2img, b.l2b, b.l2s);
     TAH_LAUNCHED();
 }

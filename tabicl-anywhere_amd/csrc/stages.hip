@@ -23,28 +23,43 @@ __device__ __forceinline__ void load8(const float *p, float *v) {
 }
 
 // ---- input layer -------------------------------------------------------------------------------------------
+// 32 threads per cell, four outputs a thread (e a multiple of 4); 32-bit index arithmetic throughout.
 __global__ __launch_bounds__(256) void k_input_cells(int n, int features, int group, int e, const float *__restrict__ x,
                                                       const float *__restrict__ in_w, const float *__restrict__ in_b,
                                                       float *__restrict__ cells) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (size_t)n * features * e) return;
-    const int o = (int)(i % e);
-    const size_t cell = i / e;
-    const int g = (int)(cell % features);
-    const float *xr = x + (cell / features) * features;
+    const int cell = blockIdx.x * 8 + (threadIdx.x >> 5), q = threadIdx.x & 31;
+    if (cell >= n * features) return;
+    const int r = cell / features, g = cell - r * features;
+    const float *xr = x + (size_t)r * features;
     float vals[8];
     bool missing = true;
     for (int k = 0; k < group; k++) {
-        vals[k] = xr[(g + (1 << k)) % features];
+        int j = g + (1 << k);
+        while (j >= features) j -= features;
+        vals[k] = xr[j];
         missing = missing && vals[k] == -100.0f;
     }
-    if (missing) {
-        cells[i] = -100.0f;
-        return;
+    float *dst = cells + (size_t)cell * e;
+    for (int o = 4 * q; o < e; o += 128) {
+        float4 v = make_float4(-100.0f, -100.0f, -100.0f, -100.0f);
+        if (!missing) {
+            // in_w rows o .. o + 3 are 4 * group consecutive floats (16-byte aligned: o is a multiple of 4)
+            float wv[32];
+            const float4 *wp = reinterpret_cast<const float4 *>(in_w + (size_t)o * group);
+            for (int i = 0; i < group; i++) {
+                const float4 t = wp[i];
+                wv[4 * i] = t.x; wv[4 * i + 1] = t.y; wv[4 * i + 2] = t.z; wv[4 * i + 3] = t.w;
+            }
+            const float4 bb = *reinterpret_cast<const float4 *>(in_b + o);
+            float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int k = 0; k < group; k++) {
+#pragma unroll
+                for (int u = 0; u < 4; u++) acc[u] += wv[u * group + k] * vals[k];
+            }
+            v = make_float4(acc[0] + bb.x, acc[1] + bb.y, acc[2] + bb.z, acc[3] + bb.w);
+        }
+        *reinterpret_cast<float4 *>(dst + o) = v;
     }
-    float s = 0.0f;
-    for (int k = 0; k < group; k++) s += in_w[o * group + k] * vals[k];
-    cells[i] = s + in_b[o];
 }
 
 // ---- cells against a group's inducing points: head width 16, 16 * NT keys ----------------------------------------
@@ -612,9 +627,10 @@ static dim3 blocks_for(size_t count) { return dim3((unsigned)((count + 255) / 25
 // ---- host side ---------------------------------------------------------------------------------------------
 void input_cells(hipStream_t s, const tah_weights *w, const float *x, int n, int features, float *cells) {
     if (w->group > 8 || w->group < 1) throw ArgError{"column stage: feature group size must be 1..8"};
-    const size_t count = (size_t)n * features * w->e;
-    hipLaunchKernelGGL(k_input_cells, blocks_for(count), dim3(256), 0, s, n, features, w->group, w->e, x, w->in_w, w->in_b,
-                       cells);
+    if (w->e % 4) throw ArgError{"column stage: embedding width must be a multiple of 4"};
+    if ((size_t)n * features > (size_t)INT32_MAX) throw ArgError{"column stage: too many cells"};
+    hipLaunchKernelGGL(k_input_cells, dim3((unsigned)(((size_t)n * features + 7) / 8)), dim3(256), 0, s, n, features,
+                       w->group, w->e, x, w->in_w, w->in_b, cells);
     TAH_LAUNCHED();
 }
 
