@@ -120,7 +120,7 @@ void tah_weights_free(tah_weights *w);
  * chunk records as they are stored (n{j}_kv{l}), any of the three formats, no re-layout on the host.
  * layer_records[l] points at layer l's bytes (tah_kv_record summed over its chunks); scales is n{j}_scale,
  * [layers][d]. tah_model_bytes (like Gpu::model_bytes, from the weights' shape) counts the records, the split-fp16
- * tile images the card builds from f32 records of head width 64, and the scales; 0 without weights. */
+ * tile images the card builds from them (head width 64), and the scales; 0 without weights. */
 size_t tah_model_bytes(const tah_weights *w, int32_t kv_format, int32_t rows, int32_t chunk);
 int tah_model_load(tah_dev *dev, const tah_weights *w, int32_t kv_format, int32_t rows, int32_t chunk,
                    const uint8_t *const *layer_records, const float *scales, tah_model **out);

@@ -465,7 +465,7 @@ static KvImages images_of(const tah_model *m, int l) {
 static const KvImages *loan_images(hipStream_t s, Loans &loans, const AttnShape &a, const uint8_t *rec32, KvImages &img) {
     if (a.nq < 32 || !kv_images_apply(a.kv_format, a.d, a.heads)) return nullptr;
     img = kv_images_at(loans.take<uint8_t>(kv_images_bytes(a.rows, a.chunk, a.heads)), a.rows, a.chunk, a.heads);
-    kv_images(s, a.rows, a.chunk, a.d, a.heads, rec32, img);
+    kv_images(s, a.rows, a.chunk, a.d, a.heads, a.kv_format, rec32, img);
     return &img;
 }
 
@@ -512,7 +512,7 @@ extern "C" int tah_model_load(tah_dev *dev, const tah_weights *w, int32_t kv_for
             TAH_HIP(hipMemcpy(m->scales, scales, sizeof(float) * m->layers * m->d, hipMemcpyHostToDevice));
             if (m->images) {
                 for (int l = 0; l < m->layers; l++)
-                    kv_images(dev->stream, rows, chunk, m->d, m->heads, layer_of(m, l), images_of(m, l));
+                    kv_images(dev->stream, rows, chunk, m->d, m->heads, kv_format, layer_of(m, l), images_of(m, l));
                 TAH_HIP(hipStreamSynchronize(dev->stream));
             }
         } catch (...) {
@@ -730,7 +730,8 @@ extern "C" int tah_in_context(tah_dev *dev, const tah_weights *w, const float *h
                 // (src/fit.rs:667-744)
                 dense(s, rows, d, d, t, d, b.in_w, b.in_s.rows(0), b.in_b, q, d, EPI_NONE, nullptr, 0);
                 query_modulate(s, rows, b, sc + (size_t)l * d, q, mid);
-                if (use_img) kv_images(s, rows, chunk, d, w->icl_heads, reinterpret_cast<const uint8_t *>(rec32), img);
+                if (use_img)
+                    kv_images(s, rows, chunk, d, w->icl_heads, TAH_KV_F32, reinterpret_cast<const uint8_t *>(rec32), img);
                 attention(s, a, q, reinterpret_cast<const uint8_t *>(rec32), att, work, use_img ? &img : nullptr);
                 dense(s, rows, d, d, att, d, b.out_w, b.out_s, b.out_b, h, d, EPI_RESID, h, d);
                 layer_norm(s, rows, d, h, d, b.n2w, b.n2b, t, d);

@@ -458,7 +458,8 @@ __global__ __launch_bounds__(256) void k_attn_decode64(int nq, int rows, int chu
     }
 }
 
-// ---- tile images: f32 keys and values split into fp16 halves, laid out as the split kernel's LDS image -------
+// ---- tile images: keys and values (f32, or i16/i8 codes dequantised with their chunk's per-coordinate scales) split
+// into fp16 halves, laid out as the split kernel's LDS image -----------------------------------------------------
 // One image per (key block, head), 32 KB: K hi, K lo as [64 keys][64 coordinates] and V hi, V lo as
 // [64 coordinates][64 keys], fp16, each 128-byte row split in eight 16-byte chunks stored XOR-swizzled by row: the
 // 64-bank LDS serves a 128-bit read 16 lanes at a time, and the 16 rows one such group reads (at one logical chunk)
@@ -482,17 +483,19 @@ __global__ __launch_bounds__(64) void k_zero_u32(int n, uint32_t *__restrict__ p
 
 // grid (key blocks, heads); 256 threads: the largest |K| and |V| of each head, by integer max on the f32 bits
 // (non-negative floats order as their bit patterns).
+template <int FMT>
 __global__ __launch_bounds__(256) void k_kv_absmax(int rows, int chunk, int d, int heads, const uint8_t *__restrict__ records,
                                                     uint32_t *__restrict__ kvmax) {
     __shared__ float red[2][4];
     const int kb = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
     const KeyBlocks kbs = key_blocks(rows, chunk);
-    const Where w = locate(kbs, kb, records, TAH_KV_F32, d, chunk);
+    const Where w = locate(kbs, kb, records, FMT, d, chunk);
     const int lc = tid >> 2, seg = (tid & 3) * 16;
-    const bool fast = w.nk == KB && ((size_t)w.rc * 4) % 16 == 0;
+    const int width = FMT == TAH_KV_F32 ? 4 : (FMT == TAH_KV_I16 ? 2 : 1);
+    const bool fast = w.nk == KB && ((size_t)w.rc * width) % 16 == 0;
     float tk[16], tv[16];
-    load16<TAH_KV_F32>(w.rec, d, w.rc, h * 64 + lc, w.o + seg, w.nk - seg, fast, tk);
-    load16<TAH_KV_F32>(w.rec, d, w.rc, d + h * 64 + lc, w.o + seg, w.nk - seg, fast, tv);
+    load16<FMT>(w.rec, d, w.rc, h * 64 + lc, w.o + seg, w.nk - seg, fast, tk);
+    load16<FMT>(w.rec, d, w.rc, d + h * 64 + lc, w.o + seg, w.nk - seg, fast, tv);
     float mk = 0.0f, mv = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; i++) {
@@ -513,6 +516,7 @@ __global__ __launch_bounds__(256) void k_kv_absmax(int rows, int chunk, int d, i
 }
 
 // grid (key blocks, heads); 256 threads: one tile image.
+template <int FMT>
 __global__ __launch_bounds__(256) void k_kv_images(int rows, int chunk, int d, int heads,
                                                     const uint8_t *__restrict__ records,
                                                     const uint32_t *__restrict__ kvmax, uint8_t *__restrict__ images) {
@@ -520,12 +524,13 @@ __global__ __launch_bounds__(256) void k_kv_images(int rows, int chunk, int d, i
     __shared__ float Vs[64][KB + 1];
     const int kb = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
     const KeyBlocks kbs = key_blocks(rows, chunk);
-    const Where w = locate(kbs, kb, records, TAH_KV_F32, d, chunk);
+    const Where w = locate(kbs, kb, records, FMT, d, chunk);
     const int lc = tid >> 2, seg = (tid & 3) * 16;
-    const bool fast = w.nk == KB && ((size_t)w.rc * 4) % 16 == 0;
+    const int width = FMT == TAH_KV_F32 ? 4 : (FMT == TAH_KV_I16 ? 2 : 1);
+    const bool fast = w.nk == KB && ((size_t)w.rc * width) % 16 == 0;
     float tk[16], tv[16];
-    load16<TAH_KV_F32>(w.rec, d, w.rc, h * 64 + lc, w.o + seg, w.nk - seg, fast, tk);
-    load16<TAH_KV_F32>(w.rec, d, w.rc, d + h * 64 + lc, w.o + seg, w.nk - seg, fast, tv);
+    load16<FMT>(w.rec, d, w.rc, h * 64 + lc, w.o + seg, w.nk - seg, fast, tk);
+    load16<FMT>(w.rec, d, w.rc, d + h * 64 + lc, w.o + seg, w.nk - seg, fast, tv);
 #pragma unroll
     for (int i = 0; i < 16; i++) {
         Ks[lc][seg + i] = tk[i];
@@ -812,23 +817,33 @@ struct AttnPlan {
 };
 
 bool kv_images_apply(int kv_format, int d, int heads) {
-    return kv_format == TAH_KV_F32 && heads > 0 && d == 64 * heads;
+    return kv_format >= TAH_KV_F32 && kv_format <= TAH_KV_I8 && heads > 0 && d == 64 * heads;
 }
 
 size_t kv_images_bytes(int rows, int chunk, int heads) {
     return ((image_bytes_of(rows, chunk, heads) + 255) / 256) * 256 + 256 + sizeof(uint32_t) * 2 * (size_t)heads;
 }
 
-void kv_images(hipStream_t s, int rows, int chunk, int d, int heads, const uint8_t *rec32, KvImages img) {
-    if (!kv_images_apply(TAH_KV_F32, d, heads)) throw ArgError{"key/value images need head width 64"};
+template <int FMT>
+static void launch_images(hipStream_t s, int rows, int chunk, int d, int heads, const uint8_t *records, KvImages img) {
     const KeyBlocks k = key_blocks(rows, chunk);
     hipLaunchKernelGGL(k_zero_u32, dim3((2 * heads + 63) / 64), dim3(64), 0, s, 2 * heads, img.kvmax);
     TAH_LAUNCHED();
-    hipLaunchKernelGGL(k_kv_absmax, dim3(k.n_kb, heads), dim3(256), 0, s, rows, chunk, d, heads, rec32, img.kvmax);
+    hipLaunchKernelGGL(k_kv_absmax<FMT>, dim3(k.n_kb, heads), dim3(256), 0, s, rows, chunk, d, heads, records, img.kvmax);
     TAH_LAUNCHED();
-    hipLaunchKernelGGL(k_kv_images, dim3(k.n_kb, heads), dim3(256), 0, s, rows, chunk, d, heads, rec32, img.kvmax,
+    hipLaunchKernelGGL(k_kv_images<FMT>, dim3(k.n_kb, heads), dim3(256), 0, s, rows, chunk, d, heads, records, img.kvmax,
                        img.images);
     TAH_LAUNCHED();
+}
+
+void kv_images(hipStream_t s, int rows, int chunk, int d, int heads, int kv_format, const uint8_t *records,
+               KvImages img) {
+    if (!kv_images_apply(kv_format, d, heads)) throw ArgError{"key/value images need head width 64"};
+    switch (kv_format) {
+        case TAH_KV_F32: launch_images<TAH_KV_F32>(s, rows, chunk, d, heads, records, img); break;
+        case TAH_KV_I16: launch_images<TAH_KV_I16>(s, rows, chunk, d, heads, records, img); break;
+        default: launch_images<TAH_KV_I8>(s, rows, chunk, d, heads, records, img); break;
+    }
 }
 
 KvImages kv_images_at(uint8_t *base, int rows, int chunk, int heads) {

@@ -116,7 +116,7 @@ struct tah_model {
     int kv_format, rows, chunk, d, layers, heads;
     size_t layer_bytes;
     uint8_t *records = nullptr;  // layers x layer_bytes: the stored chunk records as they are, then their images
-    bool images = false;         // f32 records of head width 64: tile images follow each layer's records
+    bool images = false;         // head width 64: tile images follow each layer's records
     float *scales = nullptr;     // [layers][d]
     size_t bytes = 0;
     float *col_kv = nullptr;     // [features][digits][blocks][2][e][inds] (tah_model_set_columns)
@@ -186,8 +186,8 @@ size_t attention_work_bytes(const AttnShape &a);
 void to_records(hipStream_t s, int rows, int d, int chunk, const float *kv, float *rec32);
 // f32 chunk records to i16/i8 records (the reference's quantiser, bit for bit).
 void pack(hipStream_t s, int rows, int d, int chunk, int fmt, const float *rec32, uint8_t *recq);
-// f32 keys and values of one layer as fp16 hi/lo tile images (head width 64 only), with each head's largest
-// magnitudes: the split-fp16 attention kernel's input, built once per stored layer.
+// Keys and values of one layer (any format, dequantised) as fp16 hi/lo tile images (head width 64 only), with each
+// head's largest magnitudes: the split-fp16 attention kernel's input, built once per stored layer.
 struct KvImages {
     uint8_t *images = nullptr;
     uint32_t *kvmax = nullptr;
@@ -195,7 +195,8 @@ struct KvImages {
 bool kv_images_apply(int kv_format, int d, int heads);
 size_t kv_images_bytes(int rows, int chunk, int heads);
 KvImages kv_images_at(uint8_t *base, int rows, int chunk, int heads);
-void kv_images(hipStream_t s, int rows, int chunk, int d, int heads, const uint8_t *rec32, KvImages img);
+void kv_images(hipStream_t s, int rows, int chunk, int d, int heads, int kv_format, const uint8_t *records,
+               KvImages img);
 // img (optional): the layer's images, used for 32 queries or more.
 void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t *records, float *out, void *work,
                const KvImages *img = nullptr);

@@ -267,7 +267,7 @@ class VramModel:
     @staticmethod
     def model_bytes(weights: "GpuWeights", kv_format: int, rows: int, chunk: int) -> int:
         """Card bytes a problem of `rows` stored rows takes once loaded (`Gpu::model_bytes`, src/gpu.rs:2064-2068):
-        the records as stored, plus for f32 records of head width 64 their split-fp16 tile images."""
+        the records as stored, plus for head width 64 the split-fp16 tile images the card makes of them."""
         return int(abi.lib().tah_model_bytes(weights._h, kv_format, rows, chunk))
 
     def free(self) -> None:

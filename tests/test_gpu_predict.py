@@ -103,13 +103,13 @@ def test_attention_magnitudes(gpu, full_model, full_weights, kv_scale, q_scale):
 
 def test_model_bytes(gpu, full_weights):
     """Gpu::model_bytes: stored records per layer (the published sizes at 10,000 rows, chunk 256), plus the
-    split-fp16 tile images of f32 layers (157 key blocks x 8 heads x 32 KB each), plus the query scales."""
+    split-fp16 tile images of every layer (157 key blocks x 8 heads x 32 KB each), plus the query scales."""
     f32 = hip.VramModel.model_bytes(full_weights, abi.KV_F32, 10000, 256)
     i16 = hip.VramModel.model_bytes(full_weights, abi.KV_I16, 10000, 256)
     images = 157 * 8 * 32768
     assert f32 >= 12 * (40_960_000 + images)
     assert f32 < 12 * (40_960_000 + images + 4096) + 4 * 12 * 512 + 256
-    assert 12 * 20_643_840 <= i16 < 12 * (20_643_840 + 256) + 4 * 12 * 512 + 256
+    assert 12 * (20_643_840 + images) <= i16 < 12 * (20_643_840 + images + 4096) + 4 * 12 * 512 + 256
     assert hip.VramModel.model_bytes(full_weights, abi.KV_F32, 0, 256) == 0
 
 
