@@ -8,7 +8,8 @@ decoder 1024 -> 10). Synthetic table: X ~ N(0, 1) of 10,000 training + 2,048 tes
 * fit_s: the whole fit on the card (column, row and in-context stages; every layer's stored records back on the
   host), wall clock, after one warm-up fit.
 * value: a step is one prediction pass of 2,048 test rows through all three stages against the fitted caches,
-  inputs already resident in HBM; rows/s. Also batches of 1, 64 and 256 rows and the in-context stage alone.
+  inputs already resident in HBM; rows/s. Also batches of 1, 64 and 256 rows, the in-context stage alone, and
+  2,048 rows against the same table's cache quantised to i16 and to i8 (fitted again in that format).
 * roofline: the dominant kernel, the in-context attention (2,048 queries over 10,000 keys, 8 heads of 64), timed
   with HIP events on the library's stream. Its f32 products run on the fp16 matrix cores as three fp16 products
   each, so its ceiling is the dense fp16 MFMA peak (2.5 PFLOP/s) over three: 833 TFLOP/s of f32 work.
@@ -124,6 +125,23 @@ def main():
         log(f"prediction, {n} rows: {ms:.3f} ms, {per_batch[str(n)]:,.0f} rows/s")
     per_batch[str(BATCH)] = round(rows_s, 1)
 
+    # ---- the same table with the cache quantised to i16 and to i8 (dequantised inside the kernels) -----------------
+    per_cache = {"f32": round(rows_s, 1)}
+    for name, fmt in (("i16", abi.KV_I16), ("i8", abi.KV_I8)):
+        fq = fitmod.fit_raw(gpu, w, x_train, y_train, CLASSES, CHUNK, fmt)
+        vq = gpu.load(w, fmt, ROWS, CHUNK, fq.layers[0], fq.scales[0])
+        vq.set_columns(fq.col_kv, FEATURES, 1)
+        for _ in range(2):
+            gpu.predict_dev(w, vq, x_dev.ptr, BATCH, CLASSES, out_dev.ptr)
+        gpu.sync()
+        timer.start()
+        for _ in range(args.steps):
+            gpu.predict_dev(w, vq, x_dev.ptr, BATCH, CLASSES, out_dev.ptr)
+        ms = timer.stop() / args.steps
+        per_cache[name] = round(BATCH / (ms / 1e3), 1)
+        log(f"prediction, {BATCH} rows, {name} cache: {ms:.3f} ms, {per_cache[name]:,.0f} rows/s")
+        vq.free()
+
     # ---- the in-context stage alone and its attention kernel ---------------------------------------------------
     rng = np.random.default_rng(5)
     h_dev = dm.DeviceBuffer.of(rng.standard_normal((BATCH, d)).astype(np.float32))
@@ -206,6 +224,7 @@ def main():
                    "train_rows": ROWS, "features": FEATURES, "chunk": CHUNK, "test_rows": BATCH, "classes": CLASSES,
                    "kv": "f32", "members": 1},
         "rows_per_s_by_batch": per_batch,
+        "rows_per_s_by_cache": per_cache,
         "in_context_stage_ms": round(icl_ms, 4),
         "fit_s": round(fit_s, 4),
         "roofline": {"bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": round(PEAK_SPLIT_F32 / 1e12, 1),
