@@ -52,7 +52,7 @@ def random_layers(rng, layers, rows, chunk, d, kv_format, scale=1.0):
 
 
 @pytest.mark.parametrize("kv_format", [abi.KV_F32, abi.KV_I16, abi.KV_I8])
-@pytest.mark.parametrize("rows,chunk", [(10000, 256), (1000, 48), (37, 8)])
+@pytest.mark.parametrize("rows,chunk", [(10000, 256), (1000, 48), (37, 8), (50, 64)])
 @pytest.mark.parametrize("nq", [1, 7, 64, 130])
 def test_attention_full_width(gpu, full_model, full_weights, kv_format, rows, chunk, nq):
     """AttendCached::attend at d = 512, 8 heads of 64: decode path below 64 queries, MFMA path above."""
@@ -64,6 +64,25 @@ def test_attention_full_width(gpu, full_model, full_weights, kv_format, rows, ch
     vm = gpu.load(full_weights, kv_format, rows, chunk, layers, scales)
     q = (rng.standard_normal((nq, d)) * 0.3).astype(np.float32)
     got = gpu.attend_resident(vm, 3, q)
+    want = orc.attend_records(q, layers[0], kv_format, rows, chunk, d, full_model.icl_heads)
+    vm.free()
+    err = np.abs(got - want).max()
+    say("  worst", err)
+    assert err < SCORE_TOL
+
+
+@pytest.mark.parametrize("kv_format", [abi.KV_F32, abi.KV_I8])
+def test_attention_many_queries(gpu, full_model, full_weights, kv_format):
+    """2,048 queries (16 tiles of 128 x 8 heads x 8 key ranges): the batched path and its four-coordinate split merge,
+    against the oracle."""
+    say(f"attention 2048 queries fmt={kv_format}")
+    rng = np.random.default_rng(2048 + kv_format)
+    d, L = full_model.d, full_model.icl_layers
+    rows, chunk, nq = 3000, 256, 2048
+    layers = random_layers(rng, 1, rows, chunk, d, kv_format, scale=0.5) * L
+    vm = gpu.load(full_weights, kv_format, rows, chunk, layers, np.ones((L, d), np.float32))
+    q = (rng.standard_normal((nq, d)) * 0.3).astype(np.float32)
+    got = gpu.attend_resident(vm, 5, q)
     want = orc.attend_records(q, layers[0], kv_format, rows, chunk, d, full_model.icl_heads)
     vm.free()
     err = np.abs(got - want).max()
