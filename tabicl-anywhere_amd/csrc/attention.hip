@@ -1,6 +1,6 @@
-// In-context attention of query rows over one stored layer of training-row keys and values, read in place from
-// the bundle's chunk records (f32, or i16/i8 codes with per-chunk, per-coordinate scales dequantised in the
-// kernel). This replaces the reference's streaming loop (src/predict.rs:427-533 with Soft::update/update_int,
+// In-context attention of query rows over one stored layer of training-row keys and values: the bundle's chunk
+// records (f32, or i16/i8 codes with per-chunk, per-coordinate scales, dequantised on the card), or the tile images
+// made of them. This replaces the reference's streaming loop (src/predict.rs:427-533 with Soft::update/update_int,
 // src/nn.rs:194-258) and its WGSL attend/merge shaders (src/gpu.rs:492-627).
 //
 // Keys are visited in blocks of 64 that never straddle a stored chunk. Each workgroup keeps, per query and head,
@@ -9,24 +9,23 @@
 // (Soft::merge, src/nn.rs:261-276) and divided through (Soft::finish).
 //
 // The kernels:
-//  * k_attn_split64: head width 64, at least 32 queries, f32 keys and values prepared as tile images (below).
-//    Every f32 product runs on the fp16 matrix cores as three products of fp16 halves (hi*hi + hi*lo + lo*hi,
-//    x = hi + lo with hi = fp16(x), lo = fp16(x - hi); the splitting of Ootomo & Yokota, "Recovering single
-//    precision accuracy from Tensor Cores while surpassing the FP32 theoretical peak performance", IJHPCA 2022),
-//    accumulated in f32: the error is that of an f32 dot product (2^-22 of sum |x y| measured on gfx950), at
-//    v_mfma_f32_32x32x16_f16's rate (2 PFLOP/s sustained, 16x that of the f32 matrix instructions).
-//    Operands are scaled by powers of two first (exact): each query to a maximum near 2^14, each head's keys and
-//    values by the layer's maximum, and the softmax weights to at most 2^12, so that no half overflows and the
-//    low halves stay normal for all but negligible elements.
-//  * k_attn_mfma64: head width 64 and at least 32 queries. 4 wavefronts x 32 queries share LDS tiles of K and V
-//    (64 coordinates x 64 keys). Scores are formed transposed, S^T = K Q^T, with v_mfma_f32_16x16x4_f32 so that
-//    each lane owns one query (lane % 16) in both products; the softmax then needs only two cross-lane steps, and
-//    O^T = V^T P^T takes each lane's own weights as its B operand with no transpose through LDS.
-//  * k_attn_decode64: head width 64 and few queries: 256 threads per (key range, head, 8 queries), K/V tiles
-//    loaded with 128-bit loads, lane = key for the scores and lane = coordinate for the weighted sum.
-//    Bandwidth-bound, as single-row prediction is.
+//  * k_attn_split64: head width 64, at least 32 queries, over tile images (below; any cache format). Every f32
+//    product runs on the fp16 matrix cores as three products of fp16 halves (device_math.hpp): the error is that
+//    of an f32 dot product, at v_mfma_f32_32x32x16_f16's rate (2 PFLOP/s sustained, 16x that of the f32 matrix
+//    instructions). Operands are scaled by powers of two first (exact): each query to a maximum near 2^14, each
+//    head's keys and values by the layer's maximum, and the softmax weights to at most 2^15, so that no half
+//    overflows and the low halves stay normal for all but negligible elements.
+//  * k_attn_mfma64: head width 64 and at least 32 queries, on v_mfma_f32_16x16x4_f32 straight from the records
+//    (used where no images were made). 4 wavefronts x 32 queries share LDS tiles of K and V (64 coordinates x 64
+//    keys). Scores are formed transposed, S^T = K Q^T, so that each lane owns one query (lane % 16) in both
+//    products; the softmax then needs only two cross-lane steps, and O^T = V^T P^T takes each lane's own weights as
+//    its B operand with no transpose through LDS.
+//  * k_attn_decode64: head width 64 and few queries, from the records: 256 threads per (key range, head, 8
+//    queries), K/V tiles loaded with 128-bit loads, lane = key for the scores and lane = coordinate for the
+//    weighted sum. Bandwidth-bound, as single-row prediction is.
 //  * k_attn_decode: any other head width up to 64 (the tiny test models): the same with one wavefront.
-// All of them leave the running maximum in log2 units (score * log2 e) for the split merge.
+// All of them leave the running maximum in log2 units (score * log2 e) for the split merge (k_attn_merge64 for
+// head width 64 and few key ranges, k_attn_merge otherwise).
 #include <algorithm>
 
 #include "common.hpp"
