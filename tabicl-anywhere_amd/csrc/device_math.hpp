@@ -109,11 +109,15 @@ __device__ __forceinline__ floatx16 mfma16x3(halfx8 ah, halfx8 al, halfx8 bh, ha
 
 __device__ __forceinline__ uint32_t bits(fp16x2 h) { return __builtin_bit_cast(uint32_t, h); }
 
-// hi/lo fp16 halves of two floats, hi rounded toward zero (the residual x - hi is exact in f32)
+// hi/lo fp16 halves of two floats, hi rounded toward zero (the residual x - hi is exact in f32). The residuals come
+// from v_fma_mix_f32 reading each fp16 half of hi directly (x + (-1) hi, one instruction each, where a conversion
+// back to f32 and a subtraction would take two).
 __device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t &lo) {
-    const fp16x2 h = __builtin_amdgcn_cvt_pkrtz(a, b);
-    hi = bits(h);
-    lo = bits(__builtin_amdgcn_cvt_pkrtz(a - (float)h.x, b - (float)h.y));
+    hi = bits(__builtin_amdgcn_cvt_pkrtz(a, b));
+    float ra, rb;
+    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(ra) : "v"(hi), "v"(a));
+    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(rb) : "v"(hi), "v"(b));
+    lo = bits(__builtin_amdgcn_cvt_pkrtz(ra, rb));
 }
 
 // eight floats times f (a power of two) as hi/lo halves
