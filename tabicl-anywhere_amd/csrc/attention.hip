@@ -667,6 +667,9 @@ __global__ __launch_bounds__(64 * WAVES, (WAVES * 2 + 3) / 4) void k_attn_split6
         __syncthreads();                // everyone's have, and block kb - 1's buffer is no longer read
         if (kb + 1 < kb1) image_to_lds<WAVES>(head_images + (kb + 1) * kb_stride, tiles[buf ^ 1], tid);
         const uint8_t *tile = tiles[buf];
+        // the matrix phases run at raised wave priority, so that a SIMD's other wavefront fills the softmax's VALU
+        // work in around them rather than the other way round (measured 3% faster)
+        __builtin_amdgcn_s_setprio(1);
         // S^T for keys 32 kh + sigma(i)
         floatx16 sc[2];
 #pragma unroll
@@ -682,6 +685,7 @@ __global__ __launch_bounds__(64 * WAVES, (WAVES * 2 + 3) / 4) void k_attn_split6
                 sc[kh] = mfma16(klo, qh[dc], sc[kh]);
             }
         }
+        __builtin_amdgcn_s_setprio(0);
         // accumulator v of half kh holds key 32 kh + 16 (v / 8) + 8 g + v % 8; raw scores order as scores
         float mb = -INFINITY;
         if (nk < KB) {
@@ -726,6 +730,7 @@ __global__ __launch_bounds__(64 * WAVES, (WAVES * 2 + 3) / 4) void k_attn_split6
                 pl[kh][hh] = __builtin_bit_cast(halfx8, lw);
             }
         // O^T += V^T P^T over four 16-key steps
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int db = 0; db < 2; db++) {
             const int r = 32 * db + r32;
@@ -741,6 +746,7 @@ __global__ __launch_bounds__(64 * WAVES, (WAVES * 2 + 3) / 4) void k_attn_split6
                     acc_o[db] = mfma16(vlo, ph[kh][hh], acc_o[db]);
                 }
         }
+        __builtin_amdgcn_s_setprio(0);
     }
     l += __shfl_xor(l, 32, 64);
     if (!qlive) return;
