@@ -560,23 +560,32 @@ __global__ __launch_bounds__(256) void k_kv_images(int rows, int chunk, int d, i
 }
 
 // ---- split-fp16 MFMA kernel: head width 64 over tile images --------------------------------------------------
-// A flat grid of qtiles x heads x splits workgroups (remapped XCD by XCD as in k_attn_mfma64) of SPLIT_WAVES
-// wavefronts x 32 queries (two workgroups a compute unit: their two 32 KB buffers each fill 128 of the 160 KB LDS;
-// six wavefronts, at three a SIMD, measured slower). Key blocks of 64 stream through two LDS buffers: the next block's 32 KB image is copied global -> LDS
-// directly (global_load_lds_dwordx4) while the current one is multiplied, one barrier per block. Each wavefront
-// forms S^T = K Q^T for two halves of 32 keys with v_mfma_f32_32x32x16_f16: lane l owns query l % 32 and holds 16 of
-// the half's keys. The A operand's row i takes key sigma(i) (bits 3 and 2 of i swapped), which puts eight
-// consecutive keys (16 (v / 8) + 8 (l / 32) + v % 8) in each lane's accumulators v = 8 hh..8 hh + 7: exactly the B
-// operand that O^T = V^T P^T needs for a reduction over 16 keys, so the weights never leave the lane.
+// A flat grid of qtiles x heads x splits workgroups (remapped XCD by XCD as in k_attn_mfma64) of WAVES wavefronts x
+// 32 queries, two wavefronts a SIMD: 8 wavefronts (256 queries, one workgroup a compute unit) for many queries, 4 (two
+// workgroups a compute unit) otherwise. Key blocks of 64 stream through LDS in two rings of two 16 KB buffers, one
+// for the blocks' key halves (K hi, K lo) and one for their value halves (V hi, V lo), copied global -> LDS directly
+// (global_load_lds_dwordx4); one barrier per block.
+//
+// Each wavefront forms S^T = K Q^T for two halves of 32 keys with v_mfma_f32_32x32x16_f16: lane l owns query l % 32
+// and holds 16 of the half's keys. The A operand's row i takes key sigma(i) (bits 3 and 2 of i swapped), which puts
+// eight consecutive keys (16 (v / 8) + 8 (l / 32) + v % 8) in each lane's accumulators v = 8 hh..8 hh + 7: exactly
+// the B operand that O^T = V^T P^T needs for a reduction over 16 keys, so the weights never leave the lane.
+//
+// The loop is software-pipelined one block deep: while block kb's softmax weights are formed on the VALU, the
+// matrix cores compute block kb + 1's scores, then block kb's weighted values; one scheduling region per block
+// interleaves the three (sched_group_barrier), so that each wavefront keeps its own matrix work queued under its
+// vector work. Block kb's keys are thus read one block ahead of its values: in step kb the buffers hold keys kb + 1
+// and values kb, and the copies bring in keys kb + 2 and values kb + 1.
 //
 // The softmax runs in log2 units against a reference maximum that is raised only when a block's maximum passes it by
 // more than 3 (then the sums are rescaled): weights exp2(t - ref + 12) stay below 2^15, inside fp16, and most blocks
 // skip the rescaling.
-// One key block's 32 KB image into an LDS buffer, 16 bytes a lane: in copy i, wavefront w fills the 1 KB at chunk
-// 64 (WAVES i + w) (a wavefront-uniform LDS base; the lanes' offsets are implicit).
+
+// Half an image (its keys or its values, 16 KB) into an LDS buffer, 16 bytes a lane: in copy i, wavefront w fills
+// the 1 KB at chunk 64 (WAVES i + w) (a wavefront-uniform LDS base; the lanes' offsets are implicit).
 template <int WAVES>
-__device__ __forceinline__ void image_to_lds(const uint8_t *src, uint8_t *dst, int tid) {
-    constexpr int T = 64 * WAVES, CHUNKS = IMG / 16;
+__device__ __forceinline__ void half_image_to_lds(const uint8_t *src, uint8_t *dst, int tid) {
+    constexpr int T = 64 * WAVES, CHUNKS = IMG / 32;
     const int w = tid >> 6;
 #pragma unroll
     for (int i = 0; i < (CHUNKS + T - 1) / T; i++) {
@@ -587,14 +596,19 @@ __device__ __forceinline__ void image_to_lds(const uint8_t *src, uint8_t *dst, i
     }
 }
 
+template <bool B>
+struct Flag {
+    static constexpr bool value = B;
+};
+
 template <int WAVES>
-__global__ __launch_bounds__(64 * WAVES, (WAVES * 2 + 3) / 4) void k_attn_split64(int nq, int rows, int chunk, int d, int heads,
-                                                          const float *__restrict__ q,
-                                                          const uint8_t *__restrict__ images,
-                                                          const uint32_t *__restrict__ kvmax, int kb_per_split,
-                                                          int qtiles, int splits, float *__restrict__ part_o,
-                                                          float *__restrict__ part_ml, float *__restrict__ out) {
-    __shared__ __align__(16) uint8_t tiles[2][IMG];
+__global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows, int chunk, int d, int heads,
+                                                               const float *__restrict__ q,
+                                                               const uint8_t *__restrict__ images,
+                                                               const uint32_t *__restrict__ kvmax, int kb_per_split,
+                                                               int qtiles, int splits, float *__restrict__ part_o,
+                                                               float *__restrict__ part_ml, float *__restrict__ out) {
+    __shared__ __align__(16) uint8_t kt[2][IMG / 2], vt[2][IMG / 2];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int total = qtiles * heads * splits;
     int flat = blockIdx.x;
@@ -608,7 +622,11 @@ __global__ __launch_bounds__(64 * WAVES, (WAVES * 2 + 3) / 4) void k_attn_split6
     const bool qlive = qrow < nq;
     const uint8_t *head_images = images + (size_t)h * IMG;
     const size_t kb_stride = (size_t)heads * IMG;
-    if (kb0 < kb1) image_to_lds<WAVES>(head_images + kb0 * kb_stride, tiles[0], tid);
+    if (kb0 < kb1) {
+        half_image_to_lds<WAVES>(head_images + kb0 * kb_stride, kt[0], tid);
+        half_image_to_lds<WAVES>(head_images + kb0 * kb_stride + IMG / 2, vt[0], tid);
+        if (kb0 + 1 < kb1) half_image_to_lds<WAVES>(head_images + (kb0 + 1) * kb_stride, kt[1], tid);
+    }
 
     // this lane's query coordinates 16 dc + 8 g + t, scaled to a maximum magnitude near 2^14 and split
     float qv[4][8];
@@ -659,47 +677,57 @@ __global__ __launch_bounds__(64 * WAVES, (WAVES * 2 + 3) / 4) void k_attn_split6
 #pragma unroll
     for (int v = 0; v < 16; v++) zero[v] = 0.0f;
 
-    int buf = 0;
-    for (int kb = kb0; kb < kb1; kb++, buf ^= 1) {
+    // block kb's raw scores: keys past the block's end set to -inf, then the maximum over the query's 64 keys (both
+    // halves of the wavefront) in log2 units
+    auto mask_and_max = [&](floatx16 (&sc)[2], int kb) {
         const int ci = kb / kbs.bpc;
         const int nk = min(KB, (ci == kbs.n_chunks - 1 ? kbs.last_rc : chunk) - (kb % kbs.bpc) * KB);
-        __builtin_amdgcn_s_waitcnt(0);  // this wavefront's copies of block kb have landed
-        __syncthreads();                // everyone's have, and block kb - 1's buffer is no longer read
-        if (kb + 1 < kb1) image_to_lds<WAVES>(head_images + (kb + 1) * kb_stride, tiles[buf ^ 1], tid);
-        const uint8_t *tile = tiles[buf];
-        // the matrix phases run at raised wave priority, so that a SIMD's other wavefront fills the softmax's VALU
-        // work in around them rather than the other way round (measured 3% faster)
-        __builtin_amdgcn_s_setprio(1);
-        // S^T for keys 32 kh + sigma(i)
-        floatx16 sc[2];
-#pragma unroll
-        for (int kh = 0; kh < 2; kh++) {
-            const int r = 32 * kh + krow;
-#pragma unroll
-            for (int dc = 0; dc < 4; dc++) {
-                const int off = r * 128 + swz(r, 2 * dc + g) * 16;
-                const halfx8 khi = *reinterpret_cast<const halfx8 *>(tile + off);
-                const halfx8 klo = *reinterpret_cast<const halfx8 *>(tile + 8192 + off);
-                sc[kh] = mfma16(khi, qh[dc], dc == 0 ? zero : sc[kh]);
-                sc[kh] = mfma16(khi, ql[dc], sc[kh]);
-                sc[kh] = mfma16(klo, qh[dc], sc[kh]);
-            }
-        }
-        __builtin_amdgcn_s_setprio(0);
-        // accumulator v of half kh holds key 32 kh + 16 (v / 8) + 8 g + v % 8; raw scores order as scores
-        float mb = -INFINITY;
         if (nk < KB) {
+            const int lim = nk - 8 * g;  // accumulator v of half kh is a key while 32 kh + 16 (v / 8) + v % 8 < lim
 #pragma unroll
             for (int kh = 0; kh < 2; kh++)
 #pragma unroll
                 for (int v = 0; v < 16; v++)
-                    if (32 * kh + 16 * (v >> 3) + 8 * g + (v & 7) >= nk) sc[kh][v] = -INFINITY;
+                    if (32 * kh + 16 * (v >> 3) + (v & 7) >= lim) sc[kh][v] = -INFINITY;
         }
+        float mb = -INFINITY;
 #pragma unroll
         for (int kh = 0; kh < 2; kh++)
 #pragma unroll
             for (int v = 0; v < 16; v++) mb = fmaxf(mb, sc[kh][v]);
-        mb = fmaxf(mb, __shfl_xor(mb, 32, 64)) * to_log2;
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mb), __float_as_uint(mb), false, false);
+        return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * to_log2;
+    };
+    // S^T of a block from its key half in LDS, products in the order the operands are read (coordinate step outer)
+    auto scores = [&](const uint8_t *tile, floatx16 (&sc)[2]) {
+        halfx8 khi[4][2], klo[4][2];
+#pragma unroll
+        for (int dc = 0; dc < 4; dc++)
+#pragma unroll
+            for (int kh = 0; kh < 2; kh++) {
+                const int r = 32 * kh + krow;
+                const int off = r * 128 + swz(r, 2 * dc + g) * 16;
+                khi[dc][kh] = *reinterpret_cast<const halfx8 *>(tile + off);
+                klo[dc][kh] = *reinterpret_cast<const halfx8 *>(tile + 8192 + off);
+            }
+#pragma unroll
+        for (int dc = 0; dc < 4; dc++)
+#pragma unroll
+            for (int kh = 0; kh < 2; kh++) {
+                sc[kh] = mfma16(khi[dc][kh], qh[dc], dc == 0 ? zero : sc[kh]);
+                sc[kh] = mfma16(khi[dc][kh], ql[dc], sc[kh]);
+                sc[kh] = mfma16(klo[dc][kh], qh[dc], sc[kh]);
+            }
+    };
+    // step kb: cur holds block kb's scores; with NEXT, block kb + 1's go into nxt
+    auto step = [&](auto next_flag, floatx16 (&cur)[2], floatx16 (&nxt)[2], int kb) {
+        constexpr bool NEXT = decltype(next_flag)::value;
+        const int sl = (kb - kb0) & 1;
+        __builtin_amdgcn_s_waitcnt(0);  // this wavefront's copies of keys kb + 1 and values kb have landed
+        __syncthreads();                // everyone's have, and step kb - 1's buffers are no longer read
+        if (kb + 2 < kb1) half_image_to_lds<WAVES>(head_images + (kb + 2) * kb_stride, kt[sl], tid);
+        if (kb + 1 < kb1) half_image_to_lds<WAVES>(head_images + (kb + 1) * kb_stride + IMG / 2, vt[sl ^ 1], tid);
+        const float mb = mask_and_max(cur, kb);
         const bool grow = mb > ref + 3.0f;
         if (__any(grow)) {
             const float nref = grow ? mb : ref;
@@ -710,7 +738,10 @@ __global__ __launch_bounds__(64 * WAVES, (WAVES * 2 + 3) / 4) void k_attn_split6
             ref = nref;
         }
         const float off = 12.0f - ref;
+        if constexpr (NEXT) scores(kt[sl ^ 1], nxt);
+        // block kb's weights, split into fp16 halves for the products
         halfx8 ph[2][2], pl[2][2];
+        float ps = 0.0f;
 #pragma unroll
         for (int kh = 0; kh < 2; kh++)
 #pragma unroll
@@ -718,9 +749,9 @@ __global__ __launch_bounds__(64 * WAVES, (WAVES * 2 + 3) / 4) void k_attn_split6
                 u32x4 hw, lw;
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
-                    const float p0 = exp2_hw(fmaf(sc[kh][8 * hh + 2 * t], to_log2, off));
-                    const float p1 = exp2_hw(fmaf(sc[kh][8 * hh + 2 * t + 1], to_log2, off));
-                    l += p0 + p1;
+                    const float p0 = exp2_hw(fmaf(cur[kh][8 * hh + 2 * t], to_log2, off));
+                    const float p1 = exp2_hw(fmaf(cur[kh][8 * hh + 2 * t + 1], to_log2, off));
+                    ps += p0 + p1;
                     uint32_t hi, lo;
                     split2(p0, p1, hi, lo);
                     hw[t] = hi;
@@ -729,24 +760,65 @@ __global__ __launch_bounds__(64 * WAVES, (WAVES * 2 + 3) / 4) void k_attn_split6
                 ph[kh][hh] = __builtin_bit_cast(halfx8, hw);
                 pl[kh][hh] = __builtin_bit_cast(halfx8, lw);
             }
-        // O^T += V^T P^T over four 16-key steps
-        __builtin_amdgcn_s_setprio(1);
+        // O^T += V^T P^T over four 16-key steps, in the order the weights are formed
+        const uint8_t *vtile = vt[sl];
 #pragma unroll
-        for (int db = 0; db < 2; db++) {
-            const int r = 32 * db + r32;
+        for (int kh = 0; kh < 2; kh++)
 #pragma unroll
-            for (int kh = 0; kh < 2; kh++)
+            for (int hh = 0; hh < 2; hh++)
 #pragma unroll
-                for (int hh = 0; hh < 2; hh++) {
-                    const int off = r * 128 + swz(r, 4 * kh + 2 * hh + g) * 16;
-                    const halfx8 vhi = *reinterpret_cast<const halfx8 *>(tile + 16384 + off);
-                    const halfx8 vlo = *reinterpret_cast<const halfx8 *>(tile + 24576 + off);
+                for (int db = 0; db < 2; db++) {
+                    const int r = 32 * db + r32;
+                    const int voff = r * 128 + swz(r, 4 * kh + 2 * hh + g) * 16;
+                    const halfx8 vhi = *reinterpret_cast<const halfx8 *>(vtile + voff);
+                    const halfx8 vlo = *reinterpret_cast<const halfx8 *>(vtile + 8192 + voff);
                     acc_o[db] = mfma16(vhi, ph[kh][hh], acc_o[db]);
                     acc_o[db] = mfma16(vhi, pl[kh][hh], acc_o[db]);
                     acc_o[db] = mfma16(vlo, ph[kh][hh], acc_o[db]);
                 }
+        l += ps;
+        if constexpr (NEXT) {
+            // one region: 16 key and 16 value operand reads, 24 + 24 products and 160 VALU operations (the weights
+            // and their sum), dealt out as 4 VALU operations a product while the scores run and 2 after
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 24; i++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+                if (i < 12) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
         }
-        __builtin_amdgcn_s_setprio(0);
+    };
+    if (kb0 < kb1) {
+        floatx16 sa[2], sb[2];
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        scores(kt[0], sa);
+        // two steps an iteration, so that the score registers swap roles without copies
+        for (int kb = kb0;; kb += 2) {
+            if (kb + 1 >= kb1) {
+                step(Flag<false>{}, sa, sb, kb);
+                break;
+            }
+            step(Flag<true>{}, sa, sb, kb);
+            if (kb + 2 >= kb1) {
+                step(Flag<false>{}, sb, sa, kb + 1);
+                break;
+            }
+            step(Flag<true>{}, sb, sa, kb + 1);
+        }
     }
     l += __shfl_xor(l, 32, 64);
     if (!qlive) return;
@@ -847,7 +919,7 @@ void merge_splits(hipStream_t s, int nq, int d, int heads, int splits, const flo
 // ---- planning and launch --------------------------------------------------------------------------------------
 struct AttnPlan {
     bool mfma, split16;
-    int splits, kb_per_split, groups;
+    int splits, kb_per_split, groups, waves;
 };
 
 bool kv_images_apply(int kv_format, int d, int heads) {
@@ -887,7 +959,6 @@ KvImages kv_images_at(uint8_t *base, int rows, int chunk, int heads) {
     return img;
 }
 
-constexpr int SPLIT_WAVES = 4;
 
 static AttnPlan plan(const AttnShape &a, bool images) {
     AttnPlan p;
@@ -895,10 +966,14 @@ static AttnPlan plan(const AttnShape &a, bool images) {
     const int hd = a.d / a.heads;
     p.mfma = hd == 64 && a.nq >= 32;
     p.split16 = p.mfma && images && kv_images_apply(a.kv_format, a.d, a.heads);
-    const int per_group = p.split16 ? 32 * SPLIT_WAVES : (p.mfma ? 64 * QW : QG);
+    // k_attn_split64: 256 queries a workgroup (one a compute unit, one wave of them) from 512 queries on, else 128
+    // (two a compute unit, two waves of them)
+    p.waves = p.split16 && a.nq >= 512 ? 8 : 4;
+    const int per_group = p.split16 ? 32 * p.waves : (p.mfma ? 64 * QW : QG);
     p.groups = (a.nq + per_group - 1) / per_group;
-    // enough workgroups to fill 256 compute units a few times over, each with at least 2 key blocks
-    const long target = 1024;
+    // enough workgroups to fill 256 compute units (a few times over, for the smaller workgroups), each with at least
+    // 2 key blocks
+    const long target = p.waves == 8 ? 256 : 1024;
     long want = (target + (long)p.groups * a.heads - 1) / ((long)p.groups * a.heads);
     want = std::max(1L, std::min(want, (long)(k.n_kb + 1) / 2));
     p.kb_per_split = (int)((k.n_kb + want - 1) / want);
@@ -944,10 +1019,14 @@ void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t 
         part_ml = part_o + (size_t)p.splits * a.nq * a.heads * hd;
     }
     if (p.split16) {
-        hipLaunchKernelGGL(k_attn_split64<SPLIT_WAVES>, dim3(p.groups * a.heads * p.splits), dim3(64 * SPLIT_WAVES), 0, s,
-                           a.nq, a.rows, a.chunk,
-                           a.d, a.heads, q, img->images, img->kvmax, p.kb_per_split, p.groups, p.splits, part_o, part_ml,
-                           out);
+        if (p.waves == 8)
+            hipLaunchKernelGGL(k_attn_split64<8>, dim3(p.groups * a.heads * p.splits), dim3(512), 0, s, a.nq, a.rows,
+                               a.chunk, a.d, a.heads, q, img->images, img->kvmax, p.kb_per_split, p.groups, p.splits,
+                               part_o, part_ml, out);
+        else
+            hipLaunchKernelGGL(k_attn_split64<4>, dim3(p.groups * a.heads * p.splits), dim3(256), 0, s, a.nq, a.rows,
+                               a.chunk, a.d, a.heads, q, img->images, img->kvmax, p.kb_per_split, p.groups, p.splits,
+                               part_o, part_ml, out);
         TAH_LAUNCHED();
     } else switch (a.kv_format) {
         case TAH_KV_F32: launch<TAH_KV_F32>(s, a, p, q, records, out, part_o, part_ml); break;

@@ -87,6 +87,8 @@ __device__ __forceinline__ float fast_exp(float x) { return exp2_hw(x * LOG2E); 
 typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
+// Reinterpret whole vectors only: this compiler turns __builtin_bit_cast(T, v[i]) of a vector element into element 0
+// for every i (copy the element into a scalar first).
 
 // 14 - e for max = m 2^e, m in [0.5, 1): scaling by 2^(14 - e) leaves every magnitude below 2^14.
 __device__ __forceinline__ int shift_for(uint32_t max_bits) {
