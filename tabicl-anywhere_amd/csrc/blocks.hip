@@ -353,6 +353,348 @@ __global__ __launch_bounds__(256, 2) void k_rows128(int M, int N, const float *_
     }
 }
 
+// ---- fused column block, attention half ---------------------------------------------------------------------------
+// x += out(attend(scale * (Wq layer_norm1(x) + bq), K_g, V_g)) + bo for the cells of one group against the group's
+// cached inducing keys and values (src/nn.rs:291-301 with src/nn.rs:130-152), for e = 128, 8 heads of 16 and 128
+// inducing points, in one pass: the queries and the attention's output never leave the registers.
+//
+// The group's keys and values are first made into one 16 KB image per (group, head), in the LDS layout the attention
+// reads (k_cell_images): keys [dims half][key][8] and V^T [16-key step][8-key half][row][8], hi halves then lo
+// halves, scaled by the head's power of two (its largest magnitude below 2^14; the two shifts beside the images).
+// V^T's rows are the coordinates with bits 2 and 3 swapped, xor the step's swizzle: O^T's accumulators 0..7 then
+// hold coordinates 8 (l / 32) + 0..7 of lane l's cell, the B operand of the output projection's step for the head.
+constexpr int CIMG = 16384;  // bytes of one (group, head) image
+
+// grid (groups, 8); 256 threads: thread t takes key t % 128, coordinates 8 (t / 128) + 0..7 of head blockIdx.y.
+__global__ __launch_bounds__(256) void k_cell_images(const float *__restrict__ kvbase, size_t gstride,
+                                                      uint8_t *__restrict__ images, int *__restrict__ shifts) {
+    constexpr int E = 128, INDS = 128;
+    __shared__ float red[2][4];
+    const int grp = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int key = tid & 127, half = tid >> 7;
+    const float *K = kvbase + (size_t)grp * gstride, *V = K + (size_t)E * INDS;
+    float kv[8], vv[8];
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        kv[c] = K[(size_t)(16 * h + 8 * half + c) * INDS + key];
+        vv[c] = V[(size_t)(16 * h + 8 * half + c) * INDS + key];
+    }
+    float mk = 0.0f, mv = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        mk = fmaxf(mk, fabsf(kv[c]));
+        mv = fmaxf(mv, fabsf(vv[c]));
+    }
+    mk = wave_max(mk);
+    mv = wave_max(mv);
+    if (lane == 0) {
+        red[0][wave] = mk;
+        red[1][wave] = mv;
+    }
+    __syncthreads();
+    const int sk = shift_for_max(fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3])));
+    const int sv = shift_for_max(fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3])));
+    uint8_t *img = images + ((size_t)grp * 8 + h) * CIMG;
+    _Float16 *Kh = reinterpret_cast<_Float16 *>(img), *Kl = Kh + 2 * 128 * 8;
+    _Float16 *Vh = Kl + 2 * 128 * 8, *Vl = Vh + 8 * 2 * 16 * 8;
+    halfx8 h0, l0;
+    split8(kv, ldexpf(1.0f, sk), h0, l0);
+    *reinterpret_cast<halfx8 *>(Kh + (half * 128 + key) * 8) = h0;
+    *reinterpret_cast<halfx8 *>(Kl + (half * 128 + key) * 8) = l0;
+    const int st = key >> 4, kg = (key >> 3) & 1, t8 = key & 7;
+    const int sw = (2 * st + kg) & 15;
+    const float fv = ldexpf(1.0f, sv);
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        const int cd = 8 * half + c;
+        const int row = ((cd & 3) | ((cd & 4) << 1) | ((cd & 8) >> 1)) ^ sw;
+        const float x = vv[c] * fv;
+        const _Float16 hi = (_Float16)x;
+        Vh[((st * 2 + kg) * 16 + row) * 8 + t8] = hi;
+        Vl[((st * 2 + kg) * 16 + row) * 8 + t8] = (_Float16)(x - (float)hi);
+    }
+    if (tid == 0) {
+        shifts[(grp * 8 + h) * 2] = sk;
+        shifts[(grp * 8 + h) * 2 + 1] = sv;
+    }
+}
+
+// grid (ceil(n / 128), groups); 256 threads; wavefront w owns cells of rows 128 x + 32 w + 0..31 of group blockIdx.y
+// (cell (r, g) at row r sr + g sg of cells), lane l cell l % 32, as the B operand of every product:
+//  * query projection H^T = Wq X^T as in k_rows128 (its accumulators hold, for each head, eight consecutive query
+//    coordinates 8 (l / 32) + 0..7: the B operand of the head's S^T = K Q^T);
+//  * per head, S^T = K Q^T, a softmax over the 128 keys in two halves and O^T = V^T P^T (V^T fills 16 of the 32 A
+//    rows; the other lanes read a zero block), then the head's step of the output projection;
+//  * LDS (64 KB, two workgroups a compute unit): the query weights (64 KB) first; then the output projection's
+//    16-column steps (8 KB each) in four slots, refilled three heads ahead, and two head images, the next one copied
+//    in (global_load_lds) while the current one is used: one barrier per head.
+// The output projection's input is scaled by one power of two for all heads, lowered (and the sums rescaled) when a
+// head's values are larger than all before: every head's output is at most its values' largest magnitude.
+__global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t sg, float *cells,
+                                                        const float *__restrict__ n1w, const float *__restrict__ n1b,
+                                                        const uint8_t *__restrict__ qimg, int qshift,
+                                                        const float *__restrict__ qb, const float *__restrict__ qscale,
+                                                        const uint8_t *__restrict__ images, const int *__restrict__ shifts,
+                                                        const uint8_t *__restrict__ oimg, int oshift,
+                                                        const float *__restrict__ ob) {
+    constexpr int E = 128;
+    __shared__ __align__(16) uint8_t lds[65536];
+    __shared__ __align__(16) uint8_t zero[32];
+    uint8_t *const wo = lds;           // output projection steps, four slots of 8 KB
+    uint8_t *const kvl = lds + 32768;  // two head images
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r32 = lane & 31, g = lane >> 5;
+    const int grp = blockIdx.y;
+    const int r = blockIdx.x * 128 + wave * 32 + r32;
+    const bool live = r < n;
+    const size_t m = (size_t)(live ? r : 0) * sr + (size_t)grp * sg;
+    const uint8_t *gimg = images + (size_t)grp * 8 * CIMG;
+    const int *gsh = shifts + grp * 16;
+    dma_to_lds(qimg, lds, 65536, tid);
+    if (tid < 8) reinterpret_cast<float *>(zero)[tid] = 0.0f;
+
+    // this wavefront's cells: layer norm, then split as the B operand (coordinates 16 ks + 8 g + t)
+    float xv[8][8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) {
+        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), c = a;
+        if (live) {
+            const float *src = cells + m * E + 16 * ks + 8 * g;
+            a = *reinterpret_cast<const float4 *>(src);
+            c = *reinterpret_cast<const float4 *>(src + 4);
+        }
+        xv[ks][0] = a.x; xv[ks][1] = a.y; xv[ks][2] = a.z; xv[ks][3] = a.w;
+        xv[ks][4] = c.x; xv[ks][5] = c.y; xv[ks][6] = c.z; xv[ks][7] = c.w;
+    }
+    {
+        float sum = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+            for (int t = 0; t < 8; t++) sum += xv[ks][t];
+        sum += __shfl_xor(sum, 32, 64);
+        const float mean = sum / 128.0f;
+        float sq = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const float dv = xv[ks][t] - mean;
+                sq += dv * dv;
+            }
+        sq += __shfl_xor(sq, 32, 64);
+        const float inv = 1.0f / sqrtf(sq / 128.0f + 1e-5f);
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            float wv[8], bv[8];
+            load8(n1w + 16 * ks + 8 * g, wv);
+            load8(n1b + 16 * ks + 8 * g, bv);
+#pragma unroll
+            for (int t = 0; t < 8; t++) xv[ks][t] = (xv[ks][t] - mean) * inv * wv[t] + bv[t];
+        }
+    }
+    float xmax = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+        for (int t = 0; t < 8; t++) xmax = fmaxf(xmax, fabsf(xv[ks][t]));
+    xmax = fmaxf(xmax, __shfl_xor(xmax, 32, 64));
+    const int sx = shift_for_max(xmax);
+    const int arow = sigma32(r32);
+
+    // query projection: accumulator v of tile T holds column 32 T + 16 (v / 8) + 8 g + v % 8, i.e. head 2 T + v / 8,
+    // coordinate 8 g + v % 8
+    floatx16 qa[4];
+    {
+        halfx8 xh[8], xl[8];
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) split8(xv[ks], ldexpf(1.0f, sx), xh[ks], xl[ks]);
+#pragma unroll
+        for (int T = 0; T < 4; T++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) qa[T][v] = 0.0f;
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();  // the query weights are in LDS
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+            for (int T = 0; T < 4; T++) {
+                const int nn = 32 * T + arow;
+                const halfx8 ah = *reinterpret_cast<const halfx8 *>(lds + ks * 8192 + (g * 128 + nn) * 16);
+                const halfx8 al = *reinterpret_cast<const halfx8 *>(lds + ks * 8192 + ((2 + g) * 128 + nn) * 16);
+                qa[T] = mfma16x3(ah, al, xh[ks], xl[ks], qa[T]);
+            }
+        const float u = ldexpf(1.0f, -(sx + qshift));
+#pragma unroll
+        for (int T = 0; T < 4; T++)
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                const int n0 = 32 * T + 16 * hh + 8 * g;
+                float bv[8], cv[8];
+                load8(qb + n0, bv);
+                load8(qscale + n0, cv);
+#pragma unroll
+                for (int t = 0; t < 8; t++) qa[T][8 * hh + t] = (qa[T][8 * hh + t] * u + bv[t]) * cv[t];
+            }
+    }
+    __syncthreads();  // everyone is done with the query weights
+    dma_to_lds(oimg, wo, 32768, tid);  // output projection steps 0..3 (heads 0..3)
+    dma_to_lds(gimg, kvl, CIMG, tid);  // head 0
+
+    floatx16 acc[4];
+#pragma unroll
+    for (int T = 0; T < 4; T++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[T][v] = 0.0f;
+    int so = 1 << 30;  // the output projection's input scale (log2), lowered as heads need
+    const int krow = sigma32(r32);
+#pragma unroll
+    for (int h = 0; h < 8; h++) {
+        const int par = h & 1;
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();  // head h's image and step h of the output weights have landed; head h - 1 is done
+        if (h + 1 < 8) dma_to_lds(gimg + (size_t)(h + 1) * CIMG, kvl + (par ^ 1) * CIMG, CIMG, tid);
+        if (h >= 1 && h + 3 < 8) dma_to_lds(oimg + (size_t)(h + 3) * 8192, wo + ((h + 3) & 3) * 8192, 8192, tid);
+        const int sk = gsh[2 * h], sv = gsh[2 * h + 1];
+        const _Float16 *Kh = reinterpret_cast<const _Float16 *>(kvl + par * CIMG), *Kl = Kh + 2 * 128 * 8;
+        const _Float16 *Vh = Kl + 2 * 128 * 8, *Vl = Vh + 8 * 2 * 16 * 8;
+        // this head's query coordinates 8 g + t
+        float qv[8];
+#pragma unroll
+        for (int t = 0; t < 8; t++) qv[t] = qa[h >> 1][8 * (h & 1) + t];
+        float qmax = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 8; t++) qmax = fmaxf(qmax, fabsf(qv[t]));
+        qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
+        const int sq = shift_for_max(qmax);
+        halfx8 qh, ql;
+        split8(qv, ldexpf(1.0f, sq), qh, ql);
+        const float to_log2 = ldexpf(LOG2E, -(sk + sq));
+        // two halves of 64 keys, the softmax against a reference maximum raised only when a half passes it by more
+        // than 3 (weights exp2(t - ref + 12) below 2^15)
+        float ref = -INFINITY, l = 0.0f;
+        floatx16 o;
+#pragma unroll
+        for (int v = 0; v < 16; v++) o[v] = 0.0f;
+#pragma unroll
+        for (int k2 = 0; k2 < 2; k2++) {
+            floatx16 sc[2];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+#pragma unroll
+                for (int v = 0; v < 16; v++) sc[j][v] = 0.0f;
+                const int key = 64 * k2 + 32 * j + krow;
+                const halfx8 ah = *reinterpret_cast<const halfx8 *>(Kh + (g * 128 + key) * 8);
+                const halfx8 al = *reinterpret_cast<const halfx8 *>(Kl + (g * 128 + key) * 8);
+                sc[j] = mfma16x3(ah, al, qh, ql, sc[j]);
+#pragma unroll
+                for (int v = 0; v < 16; v++) mx = fmaxf(mx, sc[j][v]);
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * to_log2;
+            const bool grow = mx > ref + 3.0f;
+            if (__any(grow)) {
+                const float nref = grow ? mx : ref;
+                const float alpha = exp2_hw(ref - nref);
+                l *= alpha;
+                o *= alpha;
+                ref = nref;
+            }
+            const float off = 12.0f - ref;
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int hh = 0; hh < 2; hh++) {
+                    float p[8];
+#pragma unroll
+                    for (int t = 0; t < 8; t++) {
+                        p[t] = exp2_hw(fmaf(sc[j][8 * hh + t], to_log2, off));
+                        l += p[t];
+                    }
+                    halfx8 ph, pl;
+                    split8(p, 1.0f, ph, pl);
+                    // 16-key step st (keys 16 st + 8 g + 0..7 of this lane's weights); A rows 16..31 read zeros
+                    const int st = 4 * k2 + 2 * j + hh;
+                    const int row = r32 ^ ((2 * st + g) & 15);
+                    const _Float16 *vh = r32 < 16 ? Vh + ((st * 2 + g) * 16 + row) * 8
+                                                   : reinterpret_cast<const _Float16 *>(zero);
+                    const _Float16 *vl = r32 < 16 ? Vl + ((st * 2 + g) * 16 + row) * 8
+                                                   : reinterpret_cast<const _Float16 *>(zero + 16);
+                    o = mfma16x3(*reinterpret_cast<const halfx8 *>(vh), *reinterpret_cast<const halfx8 *>(vl), ph, pl,
+                                 o);
+                }
+        }
+        l += __shfl_xor(l, 32, 64);
+        // accumulators 0..7: this cell's coordinates 8 g + 0..7 of the head, in units of 2^sv; |o / l| < 2^(14 - sv)
+        if (sv < so) {
+            if (so != (1 << 30)) {
+                const float rs = ldexpf(1.0f, sv - so);
+#pragma unroll
+                for (int T = 0; T < 4; T++) acc[T] *= rs;
+            }
+            so = sv;
+        }
+        float ov[8];
+        const float f = ldexpf(1.0f, so - sv) / l;
+#pragma unroll
+        for (int t = 0; t < 8; t++) ov[t] = o[t] * f;
+        halfx8 oh, ol;
+        split8(ov, 1.0f, oh, ol);
+        const uint8_t *ws = wo + (h & 3) * 8192;
+#pragma unroll
+        for (int T = 0; T < 4; T++) {
+            const int nn = 32 * T + arow;
+            const halfx8 ah = *reinterpret_cast<const halfx8 *>(ws + (g * 128 + nn) * 16);
+            const halfx8 al = *reinterpret_cast<const halfx8 *>(ws + ((2 + g) * 128 + nn) * 16);
+            acc[T] = mfma16x3(ah, al, oh, ol, acc[T]);
+        }
+    }
+    if (!live) return;
+    // column of accumulator v of tile T: 32 T + 16 (v / 8) + 8 g + v % 8
+    const float u = ldexpf(1.0f, -(so + oshift));
+    float *xrow = cells + m * E;
+#pragma unroll
+    for (int T = 0; T < 4; T++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const int n0 = 32 * T + 16 * hh + 8 * g;
+            float bv[8], xr[8];
+            load8(ob + n0, bv);
+            load8(xrow + n0, xr);
+            float4 y0, y1;
+            y0.x = xr[0] + acc[T][8 * hh + 0] * u + bv[0];
+            y0.y = xr[1] + acc[T][8 * hh + 1] * u + bv[1];
+            y0.z = xr[2] + acc[T][8 * hh + 2] * u + bv[2];
+            y0.w = xr[3] + acc[T][8 * hh + 3] * u + bv[3];
+            y1.x = xr[4] + acc[T][8 * hh + 4] * u + bv[4];
+            y1.y = xr[5] + acc[T][8 * hh + 5] * u + bv[5];
+            y1.z = xr[6] + acc[T][8 * hh + 6] * u + bv[6];
+            y1.w = xr[7] + acc[T][8 * hh + 7] * u + bv[7];
+            *reinterpret_cast<float4 *>(xrow + n0) = y0;
+            *reinterpret_cast<float4 *>(xrow + n0 + 4) = y1;
+        }
+}
+
+bool cell_block_fits(const DevBlock &b) {
+    return b.d == 128 && b.heads == 8 && b.ss_hidden == 0 && b.inimg && b.outimg;
+}
+
+size_t cell_block_work_bytes(int groups) { return (size_t)groups * 8 * (CIMG + 2 * sizeof(int)); }
+
+void cell_block(hipStream_t s, int n, int groups, size_t sr, size_t sg, float *cells, const DevBlock &b,
+                const float *qscale, const float *kvbase, size_t gstride, void *work) {
+    if (n <= 0 || groups <= 0) return;
+    if (!cell_block_fits(b) || (reinterpret_cast<uintptr_t>(cells) & 15) || (reinterpret_cast<uintptr_t>(work) & 15))
+        throw ArgError{"cell_block: needs e = 128, 8 heads, weight images and 16-byte aligned cells and work"};
+    uint8_t *images = static_cast<uint8_t *>(work);
+    int *shifts = reinterpret_cast<int *>(images + (size_t)groups * 8 * CIMG);
+    hipLaunchKernelGGL(k_cell_images, dim3(groups, 8), dim3(256), 0, s, kvbase, gstride, images, shifts);
+    TAH_LAUNCHED();
+    hipLaunchKernelGGL(k_cell_block, dim3((n + 127) / 128, groups), dim3(256), 0, s, n, sr, sg, cells, b.n1w, b.n1b,
+                       b.inimg, b.ins, b.in_b, qscale, images, shifts, b.outimg, b.outs, b.out_b);
+    TAH_LAUNCHED();
+}
+
 void rows128(hipStream_t s, int M, int N, const float *X, int ldx, const uint8_t *wimg, int wshift, const float *b,
              float *Y, int ldy, Epi epi, const float *R, int ldr, const float *scale, const float *lnw,
              const float *lnb) {

@@ -163,6 +163,14 @@ void qmlp(hipStream_t s, int rows, const DevBlock &b, const float *scale, float 
 // layer_norm and two GEMMs.
 inline bool ff_fused_shape(int d, int ff) { return d == 128 && ff == 256; }
 void ff_block(hipStream_t s, int M, float *x, const DevBlock &b);
+// The attention half of a column block (norm1, query, attention to the cached inducing keys, output projection and
+// residual) in one kernel, in place on cells (n rows x groups; cell (r, g) at row r * sr + g * sg); e = 128, 8 heads
+// of 16, 128 inducing points (cell_block_fits).
+// work: cell_block_work_bytes(groups) bytes, 16-byte aligned (the groups' key/value images).
+bool cell_block_fits(const DevBlock &b);
+size_t cell_block_work_bytes(int groups);
+void cell_block(hipStream_t s, int n, int groups, size_t sr, size_t sg, float *cells, const DevBlock &b,
+                const float *qscale, const float *kvbase, size_t gstride, void *work);
 // Y [M][N] = epi(X' W^T + b) for K = 128 and N a multiple of 128, W as such an image (scaled by 2^shift), X' = X or
 // layer_norm(X) with lnw/lnb; EPI_NONE, EPI_SCALE (by scale [N]) or EPI_RESID (adds R, may alias Y).
 void rows128(hipStream_t s, int M, int N, const float *X, int ldx, const uint8_t *wimg, int wshift, const float *b,

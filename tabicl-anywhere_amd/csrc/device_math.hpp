@@ -90,6 +90,12 @@ typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
 // Reinterpret whole vectors only: this compiler turns __builtin_bit_cast(T, v[i]) of a vector element into element 0
 // for every i (copy the element into a scalar first).
 
+// eight consecutive floats (16-byte aligned) into v
+__device__ __forceinline__ void load8(const float *p, float *v) {
+    const float4 a = *reinterpret_cast<const float4 *>(p), b = *reinterpret_cast<const float4 *>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
 // 14 - e for max = m 2^e, m in [0.5, 1): scaling by 2^(14 - e) leaves every magnitude below 2^14.
 __device__ __forceinline__ int shift_for(uint32_t max_bits) {
     int e = 0;

@@ -17,11 +17,6 @@
 
 namespace tah {
 
-__device__ __forceinline__ void load8(const float *p, float *v) {
-    const float4 a = *reinterpret_cast<const float4 *>(p), b = *reinterpret_cast<const float4 *>(p + 4);
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-}
-
 // ---- input layer -------------------------------------------------------------------------------------------
 // 32 threads per cell, four outputs a thread (e a multiple of 4); 32-bit index arithmetic throughout.
 __global__ __launch_bounds__(256) void k_input_cells(int n, int features, int group, int e, const float *__restrict__ x,
@@ -662,6 +657,12 @@ void column_block(hipStream_t s, const tah_weights *w, const DevBlock &b, float 
                   size_t sg, const float *kvbase, size_t gstride, float *t, float *q, float *att, float *mid) {
     const int e = w->e;
     const int M = n * groups;
+    if (cell_block_fits(b) && w->inds == 128 && cell_block_work_bytes(groups) <= (size_t)M * e * sizeof(float)) {
+        // the attention half in one kernel; the query and attention buffers are not needed, att holds the images
+        cell_block(s, n, groups, sr, sg, cells, b, w->col_scale, kvbase, gstride, att);
+        feed_forward(s, M, cells, b, t, mid);
+        return;
+    }
     if (b.inimg && b.ss_hidden == 0) {
         // norm1, the query projection and its scale in one pass
         rows128(s, M, e, cells, e, b.inimg, b.ins, b.in_b, q, e, EPI_SCALE, nullptr, 0, w->col_scale, b.n1w, b.n1b);
