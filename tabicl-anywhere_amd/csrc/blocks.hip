@@ -440,6 +440,7 @@ __global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t 
     constexpr int E = 128;
     __shared__ __align__(16) uint8_t lds[65536];
     __shared__ __align__(16) uint8_t zero[32];
+    __shared__ __align__(16) float qbs[2][128];  // the query bias and scale
     uint8_t *const wo = lds;           // output projection steps, four slots of 8 KB
     uint8_t *const kvl = lds + 32768;  // two head images
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -452,6 +453,9 @@ __global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t 
     const int *gsh = shifts + grp * 16;
     dma_to_lds(qimg, lds, 65536, tid);
     if (tid < 8) reinterpret_cast<float *>(zero)[tid] = 0.0f;
+    if (tid < 64)
+        reinterpret_cast<float4 *>(&qbs[0][0])[tid] =
+            *reinterpret_cast<const float4 *>(tid < 32 ? qb + 4 * tid : qscale + 4 * (tid - 32));
 
     // this wavefront's cells: layer norm, then split as the B operand (coordinates 16 ks + 8 g + t)
     float xv[8][8];
@@ -524,6 +528,7 @@ __global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t 
                 const halfx8 al = *reinterpret_cast<const halfx8 *>(lds + ks * 8192 + ((2 + g) * 128 + nn) * 16);
                 qa[T] = mfma16x3(ah, al, xh[ks], xl[ks], qa[T]);
             }
+        __builtin_amdgcn_sched_barrier(0);  // the epilogue's loads stay after the products (registers)
         const float u = ldexpf(1.0f, -(sx + qshift));
 #pragma unroll
         for (int T = 0; T < 4; T++)
@@ -531,11 +536,13 @@ __global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t 
             for (int hh = 0; hh < 2; hh++) {
                 const int n0 = 32 * T + 16 * hh + 8 * g;
                 float bv[8], cv[8];
-                load8(qb + n0, bv);
-                load8(qscale + n0, cv);
+                load8(&qbs[0][n0], bv);
+                load8(&qbs[1][n0], cv);
 #pragma unroll
                 for (int t = 0; t < 8; t++) qa[T][8 * hh + t] = (qa[T][8 * hh + t] * u + bv[t]) * cv[t];
             }
+#pragma unroll
+        for (int T = 0; T < 4; T++) asm volatile("" : "+v"(qa[T]));  // finished here, not at each head's first use
     }
     __syncthreads();  // everyone is done with the query weights
     dma_to_lds(oimg, wo, 32768, tid);  // output projection steps 0..3 (heads 0..3)
@@ -547,10 +554,14 @@ __global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t 
 #pragma unroll
         for (int v = 0; v < 16; v++) acc[T][v] = 0.0f;
     int so = 1 << 30;  // the output projection's input scale (log2), lowered as heads need
-    const int krow = sigma32(r32);
 #pragma unroll
     for (int h = 0; h < 8; h++) {
         const int par = h & 1;
+        // lane-dependent offsets recomputed per head (an opaque copy of the lane index): kept live across all eight
+        // heads they would take the registers the products need
+        int hl = lane;
+        asm volatile("" : "+v"(hl));
+        const int r32 = hl & 31, g = hl >> 5, krow = sigma32(r32), arow = krow;
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();  // head h's image and step h of the output weights have landed; head h - 1 is done
         if (h + 1 < 8) dma_to_lds(gimg + (size_t)(h + 1) * CIMG, kvl + (par ^ 1) * CIMG, CIMG, tid);
