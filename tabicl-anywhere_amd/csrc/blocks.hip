@@ -439,7 +439,7 @@ __global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t 
                                                         const float *__restrict__ ob) {
     constexpr int E = 128;
     __shared__ __align__(16) uint8_t lds[65536];
-    __shared__ __align__(16) uint8_t zero[32];
+    __shared__ __align__(16) uint8_t zero[16], ones[16];  // eight fp16 zeros, eight fp16 ones
     __shared__ __align__(16) float qbs[2][128];  // the query bias and scale
     uint8_t *const wo = lds;           // output projection steps, four slots of 8 KB
     uint8_t *const kvl = lds + 32768;  // two head images
@@ -452,7 +452,8 @@ __global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t 
     const uint8_t *gimg = images + (size_t)grp * 8 * CIMG;
     const int *gsh = shifts + grp * 16;
     dma_to_lds(qimg, lds, 65536, tid);
-    if (tid < 8) reinterpret_cast<float *>(zero)[tid] = 0.0f;
+    if (tid < 4) reinterpret_cast<uint32_t *>(zero)[tid] = 0u;
+    else if (tid < 8) reinterpret_cast<uint32_t *>(ones)[tid - 4] = 0x3c003c00u;
     if (tid < 64)
         reinterpret_cast<float4 *>(&qbs[0][0])[tid] =
             *reinterpret_cast<const float4 *>(tid < 32 ? qb + 4 * tid : qscale + 4 * (tid - 32));
@@ -583,7 +584,7 @@ __global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t 
         const float to_log2 = ldexpf(LOG2E, -(sk + sq));
         // two halves of 64 keys, the softmax against a reference maximum raised only when a half passes it by more
         // than 3 (weights exp2(t - ref + 12) below 2^15)
-        float ref = -INFINITY, l = 0.0f;
+        float ref = -INFINITY;
         floatx16 o;
 #pragma unroll
         for (int v = 0; v < 16; v++) o[v] = 0.0f;
@@ -607,7 +608,6 @@ __global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t 
             if (__any(grow)) {
                 const float nref = grow ? mx : ref;
                 const float alpha = exp2_hw(ref - nref);
-                l *= alpha;
                 o *= alpha;
                 ref = nref;
             }
@@ -618,24 +618,23 @@ __global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t 
                 for (int hh = 0; hh < 2; hh++) {
                     float p[8];
 #pragma unroll
-                    for (int t = 0; t < 8; t++) {
-                        p[t] = exp2_hw(fmaf(sc[j][8 * hh + t], to_log2, off));
-                        l += p[t];
-                    }
+                    for (int t = 0; t < 8; t++) p[t] = exp2_hw(fmaf(sc[j][8 * hh + t], to_log2, off));
                     halfx8 ph, pl;
                     split8(p, 1.0f, ph, pl);
-                    // 16-key step st (keys 16 st + 8 g + 0..7 of this lane's weights); A rows 16..31 read zeros
+                    // 16-key step st (keys 16 st + 8 g + 0..7 of this lane's weights). A rows 16 and 20 are ones (hi)
+                    // and zeros (lo), the other rows past 15 zeros: accumulator 8 of every lane sums the weights
                     const int st = 4 * k2 + 2 * j + hh;
                     const int row = r32 ^ ((2 * st + g) & 15);
+                    const uint8_t *pad = (r32 & 11) == 0 ? ones : zero;
                     const _Float16 *vh = r32 < 16 ? Vh + ((st * 2 + g) * 16 + row) * 8
-                                                   : reinterpret_cast<const _Float16 *>(zero);
+                                                   : reinterpret_cast<const _Float16 *>(pad);
                     const _Float16 *vl = r32 < 16 ? Vl + ((st * 2 + g) * 16 + row) * 8
-                                                   : reinterpret_cast<const _Float16 *>(zero + 16);
+                                                   : reinterpret_cast<const _Float16 *>(zero);
                     o = mfma16x3(*reinterpret_cast<const halfx8 *>(vh), *reinterpret_cast<const halfx8 *>(vl), ph, pl,
                                  o);
                 }
         }
-        l += __shfl_xor(l, 32, 64);
+        const float l = o[8];  // the weights' sum (row 16 + 4 g of O^T)
         // accumulators 0..7: this cell's coordinates 8 g + 0..7 of the head, in units of 2^sv; |o / l| < 2^(14 - sv)
         if (sv < so) {
             if (so != (1 << 30)) {

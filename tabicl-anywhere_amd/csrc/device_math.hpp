@@ -119,7 +119,9 @@ __device__ __forceinline__ uint32_t bits(fp16x2 h) { return __builtin_bit_cast(u
 
 // hi/lo fp16 halves of two floats, hi rounded toward zero (the residual x - hi is exact in f32). The residuals come
 // from v_fma_mix_f32 reading each fp16 half of hi directly (x + (-1) hi, one instruction each, where a conversion
-// back to f32 and a subtraction would take two).
+// back to f32 and a subtraction would take two). The last writer of lo stays an ordinary instruction (the packing
+// conversion): the compiler inserts the wait states a matrix instruction needs after it, which it cannot do after
+// inline assembly (v_fma_mix{lo,hi}_f16 writing lo directly gave wrong products).
 __device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t &lo) {
     hi = bits(__builtin_amdgcn_cvt_pkrtz(a, b));
     float ra, rb;
