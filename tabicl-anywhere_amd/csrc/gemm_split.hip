@@ -137,27 +137,47 @@ __global__ __launch_bounds__(256, 3) void k_gemm_split(int M, int N, int K, cons
 // powers of two), then summing their partial products -- unscaled to f32 -- through LDS; wavefront w finishes
 // tile w. Four times the wavefronts of k_gemm_split on the same grid of outputs, each with a quarter of the
 // dependent chain.
-template <int EPI, bool LN>
+constexpr int SPLITK_MAX_KQ = 512;  // each wavefront's share of K at most (K at most 2048)
+
+template <int EPI, bool LN, int TN>
 __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, const float *__restrict__ X, int ldx,
                                                           const uint8_t *__restrict__ wimg, int wshift,
                                                           const float *__restrict__ b, float *Y, int ldy, SplitEpi ea,
                                                           const float *__restrict__ lnw, const float *__restrict__ lnb) {
-    __shared__ float red[4][4][16][64];  // [wavefront][tile][accumulator][lane]
+    __shared__ float red[4][TN][16][64];  // [wavefront][tile][accumulator][lane]
     __shared__ float rsum[4][32];        // LN: per-wavefront partial row sums
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r32 = lane & 31, g = lane >> 5;
     const int m = blockIdx.y * 32 + r32;
     const bool live = m < M;
-    const int nt0 = blockIdx.x * 4;
+    const int nt0 = blockIdx.x * TN;
     const int KS = K / 16, kq = K / 4, kend = (wave + 1) * kq;
     const float *xrow = X + (size_t)(live ? m : 0) * ldx;
-    floatx16 acc[4];
+    floatx16 acc[TN];
 #pragma unroll
-    for (int T = 0; T < 4; T++)
+    for (int T = 0; T < TN; T++)
 #pragma unroll
         for (int v = 0; v < 16; v++) acc[T][v] = 0.0f;
     int eprev = 0;
-    for (int k0 = wave * kq; k0 < kend; k0 += 128) {
+    // weight operands of this wavefront's 16-column steps j, two steps ahead of the products; the first two are
+    // issued before the rows are read, so that their latency overlaps the rows' and the layer norm's
+    const uint8_t *wl = wimg + ((size_t)nt0 * KS + wave * kq / 16) * 2048 + (g * 32 + r32) * 16;
+    const int nsteps = kq / 16;
+    auto wload = [&](int j, halfx8 (&w)[TN][2]) {
+#pragma unroll
+        for (int T = 0; T < TN; T++) {
+            const uint8_t *src = wl + ((size_t)T * KS + j) * 2048;
+            w[T][0] = *reinterpret_cast<const halfx8 *>(src);
+            w[T][1] = *reinterpret_cast<const halfx8 *>(src + 1024);
+        }
+    };
+    halfx8 wb[3][TN][2];
+    wload(0, wb[0]);
+    if (nsteps > 1) wload(1, wb[1]);
+#pragma unroll
+    for (int it = 0; it < (LN ? 1 : SPLITK_MAX_KQ / 128); it++) {  // with the layer norm, K = 512
+        const int k0 = wave * kq + 128 * it;
+        if (k0 >= kend) break;
         const int nks = min(8, (kend - k0) / 16);
         float xv[8][8];
 #pragma unroll
@@ -220,35 +240,33 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
         if (k0 > wave * kq) {
             const float r = ldexpf(1.0f, e - eprev);
 #pragma unroll
-            for (int T = 0; T < 4; T++) acc[T] *= r;
+            for (int T = 0; T < TN; T++) acc[T] *= r;
         }
         eprev = e;
         const float f = ldexpf(1.0f, e);
 #pragma unroll
         for (int ks = 0; ks < 8; ks++) {
             if (ks >= nks) break;
+            const int j = 8 * it + ks;
+            if (j + 2 < nsteps) wload(j + 2, wb[(j + 2) % 3]);
             halfx8 xh, xl;
             split8(xv[ks], f, xh, xl);
-            const int kk = k0 / 16 + ks;
 #pragma unroll
-            for (int T = 0; T < 4; T++) {
-                const uint8_t *w = wimg + ((size_t)(nt0 + T) * KS + kk) * 2048 + (g * 32 + r32) * 16;
-                const halfx8 ah = *reinterpret_cast<const halfx8 *>(w);
-                const halfx8 al = *reinterpret_cast<const halfx8 *>(w + 1024);
-                acc[T] = mfma16x3(ah, al, xh, xl, acc[T]);
-            }
+            for (int T = 0; T < TN; T++) acc[T] = mfma16x3(wb[j % 3][T][0], wb[j % 3][T][1], xh, xl, acc[T]);
         }
     }
     const float u = ldexpf(1.0f, -(wshift + eprev));
 #pragma unroll
-    for (int T = 0; T < 4; T++)
+    for (int T = 0; T < TN; T++)
 #pragma unroll
         for (int v = 0; v < 16; v++) red[wave][T][v][lane] = acc[T][v] * u;
     __syncthreads();
     if (!live) return;
-    const int T = wave;
+    // wavefront w sums tile w (both halves) of four, or half w % 2 of tile w / 2 of two
+    const int T = TN == 4 ? wave : wave >> 1;
 #pragma unroll
     for (int hh = 0; hh < 2; hh++) {
+        if (TN == 2 && hh != (wave & 1)) continue;
         const int n0 = 32 * (nt0 + T) + 16 * hh + 8 * g;
         float yv[8];
 #pragma unroll
@@ -438,19 +456,20 @@ template <bool LN>
 static void launch_splitk4(hipStream_t s, int M, int N, int K, const float *X, int ldx, const uint8_t *img, int shift,
                            const float *b, float *Y, int ldy, Epi epi, const SplitEpi &ea, const float *lnw,
                            const float *lnb) {
-    const dim3 grid(N / 128, (M + 31) / 32);
+    constexpr int TN = 4;  // two tiles a wavefront (twice the workgroups) measured slower
+    const dim3 grid(N / (32 * TN), (M + 31) / 32);
     switch (epi) {
         case EPI_NONE:
-            hipLaunchKernelGGL((k_gemm_splitk4<EPI_NONE, LN>), grid, dim3(256), 0, s, M, N, K, X, ldx, img, shift, b, Y,
-                               ldy, ea, lnw, lnb);
+            hipLaunchKernelGGL((k_gemm_splitk4<EPI_NONE, LN, TN>), grid, dim3(256), 0, s, M, N, K, X, ldx, img, shift, b,
+                               Y, ldy, ea, lnw, lnb);
             break;
         case EPI_GELU:
-            hipLaunchKernelGGL((k_gemm_splitk4<EPI_GELU, LN>), grid, dim3(256), 0, s, M, N, K, X, ldx, img, shift, b, Y,
-                               ldy, ea, lnw, lnb);
+            hipLaunchKernelGGL((k_gemm_splitk4<EPI_GELU, LN, TN>), grid, dim3(256), 0, s, M, N, K, X, ldx, img, shift, b,
+                               Y, ldy, ea, lnw, lnb);
             break;
         default:
-            hipLaunchKernelGGL((k_gemm_splitk4<EPI_RESID, LN>), grid, dim3(256), 0, s, M, N, K, X, ldx, img, shift, b, Y,
-                               ldy, ea, lnw, lnb);
+            hipLaunchKernelGGL((k_gemm_splitk4<EPI_RESID, LN, TN>), grid, dim3(256), 0, s, M, N, K, X, ldx, img, shift, b,
+                               Y, ldy, ea, lnw, lnb);
             break;
     }
     TAH_LAUNCHED();
@@ -463,7 +482,7 @@ void dense(hipStream_t s, int M, int N, int K, const float *X, int ldx, const fl
                      (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
     // below a few hundred rows the f32 kernels' weight streaming wins (measured at 64 and 256 rows)
     const bool split = img && M >= 512 && (epi == EPI_NONE || epi == EPI_GELU || epi == EPI_RESID);
-    const bool k4 = split && N % 128 == 0 && K % 64 == 0 && K >= 256;
+    const bool k4 = split && N % 128 == 0 && K % 64 == 0 && K >= 256 && K <= 4 * SPLITK_MAX_KQ;
     if (lnw && !(k4 && K == 512)) {
         // layer normalisation first, into t
         if (!t) throw ArgError{"dense: layer normalisation needs a scratch buffer"};
