@@ -68,7 +68,20 @@ __device__ __forceinline__ float tanh1(float x) {
     return (e - 1.0f) / (e + 1.0f);
 }
 
-__device__ __forceinline__ float gelu(float x) { return 0.5f * x * (1.0f + erf1(x * 0.70710678118654752440f)); }
+// GELU takes erf from A&S 7.1.26 at every argument: below |x| = 0.5 the reference's power series differs from it by
+// at most 1.5e-7 (the formula's absolute error bound), which moves x (1 + erf) / 2 by under 1e-7 there, and the
+// series and its selection cost as much as the formula itself (GELU is most of the feed-forward kernels' vector work).
+__device__ __forceinline__ float gelu(float x) {
+    const float z = x * 0.70710678118654752440f, a = fabsf(z);
+    const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * a);
+    float p = 1.0614054f;
+    p = p * t - 1.4531521f;
+    p = p * t + 1.4214138f;
+    p = p * t - 0.28449674f;
+    p = p * t + 0.2548296f;
+    const float erf = copysignf(1.0f - p * t * __builtin_amdgcn_exp2f(-a * a * LOG2E), z);
+    return 0.5f * x * (1.0f + erf);
+}
 
 // 2^x straight from v_exp_f32 (1 ulp): results below 2^-126, which only ever weight a softmax term, flush to 0
 // instead of taking exp2f's denormal rescaling path.
