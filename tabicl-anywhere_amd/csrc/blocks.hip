@@ -685,6 +685,368 @@ __global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t 
         }
 }
 
+// ---- fused row block, attention half ------------------------------------------------------------------------------
+// x += out(attend(rope(Wq layer_norm1(x) + bq) / 4, rope(K), V)) + bo for every token of one row over all the row's
+// tokens (src/nn.rs:357-419, Rope src/nn.rs:304-321), for e = 128, 8 heads of 16 and T <= 128 tokens; the keys and
+// values [T][2 e] (k then v per token, without rotation) come from a projection before it.
+// grid n rows; 256 threads; wavefront w owns tokens 32 w + 0..31 of row blockIdx.x, lane l token l % 32, as the B
+// operand of every product (as in k_cell_block):
+//  * the query projection as in k_cell_block, its accumulators rotated in registers (a coordinate's partner for the
+//    rotation sits on lane l ^ 32) and scaled by 1 / sqrt(16);
+//  * per head the workgroup stages the row's keys (rotated) and values into LDS split into fp16 halves, scaled by the
+//    head's power of two (one wavefront-pair's maximum each, across wavefronts through LDS): threads 0..127 a key
+//    each, threads 128..255 a value each, for the next head while the current one is attended (two barriers a head);
+//  * keys past T are masked; the attention and the output projection then run as in k_cell_block.
+__global__ __launch_bounds__(256, 2) void k_row_block(int T, float *tok, const float *__restrict__ kv,
+                                                       const float *__restrict__ cosv, const float *__restrict__ sinv,
+                                                       const float *__restrict__ n1w, const float *__restrict__ n1b,
+                                                       const uint8_t *__restrict__ qimg, int qshift,
+                                                       const float *__restrict__ qb, const uint8_t *__restrict__ oimg,
+                                                       int oshift, const float *__restrict__ ob) {
+    constexpr int E = 128;
+    __shared__ __align__(16) uint8_t lds[65536];
+    __shared__ __align__(16) uint8_t zero[16], ones[16];
+    __shared__ __align__(16) float qbs[128];
+    __shared__ __align__(16) float cst[2][128][8];  // cos, sin of token t, pair k
+    __shared__ float red[2][2][2];                  // [head parity][keys, values][wavefront of the pair]
+    uint8_t *const wo = lds;
+    uint8_t *const kvl = lds + 32768;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r32 = lane & 31, g = lane >> 5;
+    const int row = blockIdx.x;
+    const int tk = wave * 32 + r32;  // this lane's token
+    const bool live = tk < T;
+    float *xrow = tok + ((size_t)row * T + (live ? tk : 0)) * E;
+    const float *kvrow = kv + (size_t)row * T * 2 * E;
+    dma_to_lds(qimg, lds, 65536, tid);
+    if (tid < 4) reinterpret_cast<uint32_t *>(zero)[tid] = 0u;
+    else if (tid < 8) reinterpret_cast<uint32_t *>(ones)[tid - 4] = 0x3c003c00u;
+    if (tid < 32) reinterpret_cast<float4 *>(qbs)[tid] = *reinterpret_cast<const float4 *>(qb + 4 * tid);
+    if (tid < T) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            cst[0][tid][k] = cosv[tid * 8 + k];
+            cst[1][tid][k] = sinv[tid * 8 + k];
+        }
+    }
+
+    // staging of head h: thread t < 128 takes key t (16 coordinates, rotated), thread 128 + t value t
+    const int st_tok = tid & 127;
+    const bool st_key = tid < 128, st_live = st_tok < T;
+    float stv[16];
+    auto stage_load = [&](int h, int par) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (st_live) a = *reinterpret_cast<const float4 *>(kvrow + (size_t)st_tok * 2 * E + (st_key ? 0 : E) + 16 * h + 4 * i);
+            stv[4 * i] = a.x; stv[4 * i + 1] = a.y; stv[4 * i + 2] = a.z; stv[4 * i + 3] = a.w;
+        }
+        float mx = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 16; c++) mx = fmaxf(mx, fabsf(stv[c]));
+        mx = wave_max(mx);
+        if (lane == 0) red[par][wave >> 1][wave & 1] = mx;
+    };
+    auto stage_store = [&](int par) {
+        // the keys' maximum is over the unrotated values: rotation keeps each pair's norm, so the rotated values stay
+        // within sqrt(2) of it, and the split's scale (a maximum below 2^14) leaves that room
+        const int s = shift_for_max(fmaxf(red[par][st_key ? 0 : 1][0], red[par][st_key ? 0 : 1][1]) * 1.5f);
+        const float f = ldexpf(1.0f, s);
+        _Float16 *Kh = reinterpret_cast<_Float16 *>(kvl + par * 16384), *Kl = Kh + 2 * 128 * 8;
+        _Float16 *Vh = Kl + 2 * 128 * 8, *Vl = Vh + 8 * 2 * 16 * 8;
+        if (st_key) {
+            float rk[16];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const float c = cst[0][st_tok][k], sn = cst[1][st_tok][k];
+                rk[k] = stv[k] * c - stv[k + 8] * sn;
+                rk[k + 8] = stv[k + 8] * c + stv[k] * sn;
+            }
+            halfx8 h0, l0, h1, l1;
+            split8(rk, f, h0, l0);
+            split8(rk + 8, f, h1, l1);
+            *reinterpret_cast<halfx8 *>(Kh + st_tok * 8) = h0;
+            *reinterpret_cast<halfx8 *>(Kl + st_tok * 8) = l0;
+            *reinterpret_cast<halfx8 *>(Kh + (128 + st_tok) * 8) = h1;
+            *reinterpret_cast<halfx8 *>(Kl + (128 + st_tok) * 8) = l1;
+        } else {
+            const int st = st_tok >> 4, kg = (st_tok >> 3) & 1, t8 = st_tok & 7;
+            const int sw = (2 * st + kg) & 15;
+#pragma unroll
+            for (int cd = 0; cd < 16; cd++) {
+                const int rw = ((cd & 3) | ((cd & 4) << 1) | ((cd & 8) >> 1)) ^ sw;
+                const float x = stv[cd] * f;
+                const _Float16 hi = (_Float16)x;
+                Vh[((st * 2 + kg) * 16 + rw) * 8 + t8] = hi;
+                Vl[((st * 2 + kg) * 16 + rw) * 8 + t8] = (_Float16)(x - (float)hi);
+            }
+        }
+        return s;
+    };
+    stage_load(0, 0);
+
+    // this wavefront's tokens: layer norm, then split as the B operand (coordinates 16 ks + 8 g + t)
+    float xv[8][8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) {
+        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), c = a;
+        if (live) {
+            a = *reinterpret_cast<const float4 *>(xrow + 16 * ks + 8 * g);
+            c = *reinterpret_cast<const float4 *>(xrow + 16 * ks + 8 * g + 4);
+        }
+        xv[ks][0] = a.x; xv[ks][1] = a.y; xv[ks][2] = a.z; xv[ks][3] = a.w;
+        xv[ks][4] = c.x; xv[ks][5] = c.y; xv[ks][6] = c.z; xv[ks][7] = c.w;
+    }
+    {
+        float sum = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+            for (int t = 0; t < 8; t++) sum += xv[ks][t];
+        sum += __shfl_xor(sum, 32, 64);
+        const float mean = sum / 128.0f;
+        float sq = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const float dv = xv[ks][t] - mean;
+                sq += dv * dv;
+            }
+        sq += __shfl_xor(sq, 32, 64);
+        const float inv = 1.0f / sqrtf(sq / 128.0f + 1e-5f);
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            float wv[8], bv[8];
+            load8(n1w + 16 * ks + 8 * g, wv);
+            load8(n1b + 16 * ks + 8 * g, bv);
+#pragma unroll
+            for (int t = 0; t < 8; t++) xv[ks][t] = (xv[ks][t] - mean) * inv * wv[t] + bv[t];
+        }
+    }
+    float xmax = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+        for (int t = 0; t < 8; t++) xmax = fmaxf(xmax, fabsf(xv[ks][t]));
+    xmax = fmaxf(xmax, __shfl_xor(xmax, 32, 64));
+    const int sx = shift_for_max(xmax);
+
+    // query projection (accumulator v of tile T: head 2 T + v / 8, coordinate 8 g + v % 8), bias, rotation, 1 / 4
+    floatx16 qa[4];
+    {
+        const int arow = sigma32(r32);
+        halfx8 xh[8], xl[8];
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) split8(xv[ks], ldexpf(1.0f, sx), xh[ks], xl[ks]);
+#pragma unroll
+        for (int T4 = 0; T4 < 4; T4++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) qa[T4][v] = 0.0f;
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();  // the query weights, bias and rotation tables are in LDS; the first head's maxima in red
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+            for (int T4 = 0; T4 < 4; T4++) {
+                const int nn = 32 * T4 + arow;
+                const halfx8 ah = *reinterpret_cast<const halfx8 *>(lds + ks * 8192 + (g * 128 + nn) * 16);
+                const halfx8 al = *reinterpret_cast<const halfx8 *>(lds + ks * 8192 + ((2 + g) * 128 + nn) * 16);
+                qa[T4] = mfma16x3(ah, al, xh[ks], xl[ks], qa[T4]);
+            }
+        __builtin_amdgcn_sched_barrier(0);
+        const float u = ldexpf(1.0f, -(sx + qshift));
+        const int ct = live ? tk : 0;
+        float cs[8], sn[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            cs[k] = cst[0][ct][k];
+            sn[k] = cst[1][ct][k];
+        }
+        const float sgn = g == 0 ? -1.0f : 1.0f;
+#pragma unroll
+        for (int T4 = 0; T4 < 4; T4++)
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                float bv[8];
+                load8(qbs + 32 * T4 + 16 * hh + 8 * g, bv);
+#pragma unroll
+                for (int t = 0; t < 8; t++) {
+                    const float qv = qa[T4][8 * hh + t] * u + bv[t];
+                    const auto sw2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(qv), __float_as_uint(qv), false, false);
+                    const float other = __uint_as_float(g ? sw2[0] : sw2[1]);  // the coordinate 8 away, lane l ^ 32
+                    qa[T4][8 * hh + t] = (qv * cs[t] + sgn * other * sn[t]) * 0.25f;
+                }
+            }
+#pragma unroll
+        for (int T4 = 0; T4 < 4; T4++) asm volatile("" : "+v"(qa[T4]));
+    }
+    __syncthreads();  // everyone is done with the query weights
+    dma_to_lds(oimg, wo, 32768, tid);
+    int sk = stage_store(0);
+    int sv = sk;
+
+    floatx16 acc[4];
+#pragma unroll
+    for (int T4 = 0; T4 < 4; T4++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[T4][v] = 0.0f;
+    int so = 1 << 30;
+#pragma unroll
+    for (int h = 0; h < 8; h++) {
+        const int par = h & 1;
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();  // head h's keys and values are staged; step h of the output weights has landed
+        if (h >= 1 && h + 3 < 8) dma_to_lds(oimg + (size_t)(h + 3) * 8192, wo + ((h + 3) & 3) * 8192, 8192, tid);
+        if (h + 1 < 8) stage_load(h + 1, par ^ 1);
+        const int skh = shift_for_max(fmaxf(red[par][0][0], red[par][0][1]) * 1.5f);
+        const int svh = shift_for_max(fmaxf(red[par][1][0], red[par][1][1]) * 1.5f);
+        int hl = lane;
+        asm volatile("" : "+v"(hl));
+        const int r32h = hl & 31, gh = hl >> 5, krow = sigma32(r32h), arow = krow;
+        const _Float16 *Kh = reinterpret_cast<const _Float16 *>(kvl + par * 16384), *Kl = Kh + 2 * 128 * 8;
+        const _Float16 *Vh = Kl + 2 * 128 * 8, *Vl = Vh + 8 * 2 * 16 * 8;
+        // this head's query coordinates: tile 0 holds heads h and h + 1 of an even h (the tiles shift down by one
+        // after every second head, so that no register is indexed by the head)
+        float qv[8];
+#pragma unroll
+        for (int t = 0; t < 8; t++) qv[t] = par ? qa[0][8 + t] : qa[0][t];
+        float qmax = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 8; t++) qmax = fmaxf(qmax, fabsf(qv[t]));
+        qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
+        const int sq = shift_for_max(qmax);
+        halfx8 qh, ql;
+        split8(qv, ldexpf(1.0f, sq), qh, ql);
+        const float to_log2 = ldexpf(LOG2E, -(skh + sq));
+        float ref = -INFINITY;
+        floatx16 o;
+#pragma unroll
+        for (int v = 0; v < 16; v++) o[v] = 0.0f;
+#pragma unroll
+        for (int k2 = 0; k2 < 2; k2++) {  // (a half past T is all masked and adds nothing)
+            floatx16 sc[2];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+#pragma unroll
+                for (int v = 0; v < 16; v++) sc[j][v] = 0.0f;
+                const int key = 64 * k2 + 32 * j + krow;
+                const halfx8 ah = *reinterpret_cast<const halfx8 *>(Kh + (gh * 128 + key) * 8);
+                const halfx8 al = *reinterpret_cast<const halfx8 *>(Kl + (gh * 128 + key) * 8);
+                sc[j] = mfma16x3(ah, al, qh, ql, sc[j]);
+                // accumulator v holds key 64 k2 + 32 j + 16 (v / 8) + 8 g + v % 8
+                const int lim = T - (64 * k2 + 32 * j) - 8 * gh;
+                if (lim < 32) {
+#pragma unroll
+                    for (int v = 0; v < 16; v++)
+                        if (16 * (v >> 3) + (v & 7) >= lim) sc[j][v] = -INFINITY;
+                }
+#pragma unroll
+                for (int v = 0; v < 16; v++) mx = fmaxf(mx, sc[j][v]);
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * to_log2;
+            const bool grow = mx > ref + 3.0f;
+            if (__any(grow)) {
+                const float nref = grow ? mx : ref;
+                const float alpha = exp2_hw(ref - nref);
+                o *= alpha;
+                ref = nref;
+            }
+            const float off = 12.0f - ref;
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int hh = 0; hh < 2; hh++) {
+                    float p[8];
+#pragma unroll
+                    for (int t = 0; t < 8; t++) p[t] = exp2_hw(fmaf(sc[j][8 * hh + t], to_log2, off));
+                    halfx8 ph, pl;
+                    split8(p, 1.0f, ph, pl);
+                    const int st = 4 * k2 + 2 * j + hh;
+                    const int rw = r32h ^ ((2 * st + gh) & 15);
+                    const uint8_t *pad = (r32h & 11) == 0 ? ones : zero;
+                    const _Float16 *vh = r32h < 16 ? Vh + ((st * 2 + gh) * 16 + rw) * 8
+                                                    : reinterpret_cast<const _Float16 *>(pad);
+                    const _Float16 *vl = r32h < 16 ? Vl + ((st * 2 + gh) * 16 + rw) * 8
+                                                    : reinterpret_cast<const _Float16 *>(zero);
+                    o = mfma16x3(*reinterpret_cast<const halfx8 *>(vh), *reinterpret_cast<const halfx8 *>(vl), ph, pl,
+                                 o);
+                }
+        }
+        const float l = o[8];
+        if (svh < so) {
+            if (so != (1 << 30)) {
+                const float rs = ldexpf(1.0f, svh - so);
+#pragma unroll
+                for (int T4 = 0; T4 < 4; T4++) acc[T4] *= rs;
+            }
+            so = svh;
+        }
+        float ov[8];
+        const float f = ldexpf(1.0f, so - svh) / l;
+#pragma unroll
+        for (int t = 0; t < 8; t++) ov[t] = o[t] * f;
+        halfx8 oh, ol;
+        split8(ov, 1.0f, oh, ol);
+        const uint8_t *ws = wo + (h & 3) * 8192;
+#pragma unroll
+        for (int T4 = 0; T4 < 4; T4++) {
+            const int nn = 32 * T4 + arow;
+            const halfx8 ah = *reinterpret_cast<const halfx8 *>(ws + (gh * 128 + nn) * 16);
+            const halfx8 al = *reinterpret_cast<const halfx8 *>(ws + ((2 + gh) * 128 + nn) * 16);
+            acc[T4] = mfma16x3(ah, al, oh, ol, acc[T4]);
+        }
+        if (par) {
+            qa[0] = qa[1];
+            qa[1] = qa[2];
+            qa[2] = qa[3];
+        }
+        if (h + 1 < 8) {
+            __syncthreads();  // head h + 1's maxima are in red; everyone is done with buffer par ^ 1 since head h - 1
+            stage_store(par ^ 1);
+        }
+    }
+    (void)sk;
+    (void)sv;
+    if (!live) return;
+    const float u = ldexpf(1.0f, -(so + oshift));
+#pragma unroll
+    for (int T4 = 0; T4 < 4; T4++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const int n0 = 32 * T4 + 16 * hh + 8 * g;
+            float bv[8], xr[8];
+            load8(ob + n0, bv);
+            load8(xrow + n0, xr);
+            float4 y0, y1;
+            y0.x = xr[0] + acc[T4][8 * hh + 0] * u + bv[0];
+            y0.y = xr[1] + acc[T4][8 * hh + 1] * u + bv[1];
+            y0.z = xr[2] + acc[T4][8 * hh + 2] * u + bv[2];
+            y0.w = xr[3] + acc[T4][8 * hh + 3] * u + bv[3];
+            y1.x = xr[4] + acc[T4][8 * hh + 4] * u + bv[4];
+            y1.y = xr[5] + acc[T4][8 * hh + 5] * u + bv[5];
+            y1.z = xr[6] + acc[T4][8 * hh + 6] * u + bv[6];
+            y1.w = xr[7] + acc[T4][8 * hh + 7] * u + bv[7];
+            *reinterpret_cast<float4 *>(xrow + n0) = y0;
+            *reinterpret_cast<float4 *>(xrow + n0 + 4) = y1;
+        }
+}
+
+bool row_block_fits(const DevBlock &b, int T) {
+    return b.d == 128 && b.heads == 8 && b.inimg && b.outimg && T >= 1 && T <= 128;
+}
+
+void row_block(hipStream_t s, int n, int T, float *tok, const float *kv, const float *cosv, const float *sinv,
+               const DevBlock &b) {
+    if (n <= 0) return;
+    if (!row_block_fits(b, T) || (reinterpret_cast<uintptr_t>(tok) & 15) || (reinterpret_cast<uintptr_t>(kv) & 15))
+        throw ArgError{"row_block: needs e = 128, 8 heads, weight images, at most 128 tokens and aligned rows"};
+    hipLaunchKernelGGL(k_row_block, dim3(n), dim3(256), 0, s, T, tok, kv, cosv, sinv, b.n1w, b.n1b, b.inimg, b.ins,
+                       b.in_b, b.outimg, b.outs, b.out_b);
+    TAH_LAUNCHED();
+}
+
 bool cell_block_fits(const DevBlock &b) {
     return b.d == 128 && b.heads == 8 && b.ss_hidden == 0 && b.inimg && b.outimg;
 }

@@ -168,6 +168,11 @@ void ff_block(hipStream_t s, int M, float *x, const DevBlock &b);
 // of 16, 128 inducing points (cell_block_fits).
 // work: cell_block_work_bytes(groups) bytes, 16-byte aligned (the groups' key/value images).
 bool cell_block_fits(const DevBlock &b);
+// The attention half of a row block for every token of n rows of T tokens (tok [n][T][e] in place), from the keys
+// and values kv [n][T][2 e] the projection made (unrotated); e = 128, 8 heads of 16, T <= 128 (row_block_fits).
+bool row_block_fits(const DevBlock &b, int T);
+void row_block(hipStream_t s, int n, int T, float *tok, const float *kv, const float *cosv, const float *sinv,
+               const DevBlock &b);
 size_t cell_block_work_bytes(int groups);
 void cell_block(hipStream_t s, int n, int groups, size_t sr, size_t sg, float *cells, const DevBlock &b,
                 const float *qscale, const float *kvbase, size_t gstride, void *work);

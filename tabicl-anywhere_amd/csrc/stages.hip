@@ -763,6 +763,15 @@ void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, co
     };
     for (int bi = 0; bi <= last; bi++) {
         const DevBlock &b = w->row[bi];
+        if (bi < last && fused && row_block_fits(b, T)) {
+            // keys and values by the projection (its second and third 128-row blocks), then the attention half of
+            // the block in one kernel; qkv holds [R][2 e]
+            rows128(s, (int)R, 2 * e, tok, e, b.inimg + (size_t)128 * e * 4, b.ins, b.in_b + e, qkv, 2 * e, EPI_NONE,
+                    nullptr, 0, nullptr, b.n1w, b.n1b);
+            row_block(s, n, T, tok, qkv, cosv, sinv, b);
+            feed_forward(s, (int)R, tok, b, t, mid);
+            continue;
+        }
         if (b.inimg) {
             rows128(s, (int)R, 3 * e, tok, e, b.inimg, b.ins, b.in_b, qkv, 3 * e, EPI_NONE, nullptr, 0, nullptr, b.n1w,
                     b.n1b);
