@@ -709,6 +709,7 @@ __global__ __launch_bounds__(256, 2) void k_row_block(int T, float *tok, const f
     __shared__ __align__(16) float qbs[128];
     __shared__ __align__(16) float cst[2][128][8];  // cos, sin of token t, pair k
     __shared__ float red[2][2][2];                  // [head parity][keys, values][wavefront of the pair]
+    __shared__ int shs[2][2];                       // [buffer][keys, values]: the staged head's scales
     uint8_t *const wo = lds;
     uint8_t *const kvl = lds + 32768;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -752,6 +753,7 @@ __global__ __launch_bounds__(256, 2) void k_row_block(int T, float *tok, const f
         // within sqrt(2) of it, and the split's scale (a maximum below 2^14) leaves that room
         const int s = shift_for_max(fmaxf(red[par][st_key ? 0 : 1][0], red[par][st_key ? 0 : 1][1]) * 1.5f);
         const float f = ldexpf(1.0f, s);
+        if (st_tok == 0) shs[par][st_key ? 0 : 1] = s;
         _Float16 *Kh = reinterpret_cast<_Float16 *>(kvl + par * 16384), *Kl = Kh + 2 * 128 * 8;
         _Float16 *Vh = Kl + 2 * 128 * 8, *Vl = Vh + 8 * 2 * 16 * 8;
         if (st_key) {
@@ -883,8 +885,8 @@ __global__ __launch_bounds__(256, 2) void k_row_block(int T, float *tok, const f
     }
     __syncthreads();  // everyone is done with the query weights
     dma_to_lds(oimg, wo, 32768, tid);
-    int sk = stage_store(0);
-    int sv = sk;
+    stage_store(0);
+    stage_load(1, 1);
 
     floatx16 acc[4];
 #pragma unroll
@@ -896,11 +898,13 @@ __global__ __launch_bounds__(256, 2) void k_row_block(int T, float *tok, const f
     for (int h = 0; h < 8; h++) {
         const int par = h & 1;
         __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();  // head h's keys and values are staged; step h of the output weights has landed
+        __syncthreads();  // head h's keys and values are staged, head h + 1's maxima are in red; step h of the output
+                          // weights has landed; everyone is done with head h - 1 and its buffer
         if (h >= 1 && h + 3 < 8) dma_to_lds(oimg + (size_t)(h + 3) * 8192, wo + ((h + 3) & 3) * 8192, 8192, tid);
-        if (h + 1 < 8) stage_load(h + 1, par ^ 1);
-        const int skh = shift_for_max(fmaxf(red[par][0][0], red[par][0][1]) * 1.5f);
-        const int svh = shift_for_max(fmaxf(red[par][1][0], red[par][1][1]) * 1.5f);
+        // one head ahead: head h + 1 into the buffer head h - 1 used, then head h + 2's values into registers
+        if (h + 1 < 8) stage_store(par ^ 1);
+        if (h + 2 < 8) stage_load(h + 2, par);
+        const int skh = shs[par][0], svh = shs[par][1];
         int hl = lane;
         asm volatile("" : "+v"(hl));
         const int r32h = hl & 31, gh = hl >> 5, krow = sigma32(r32h), arow = krow;
@@ -1002,13 +1006,7 @@ __global__ __launch_bounds__(256, 2) void k_row_block(int T, float *tok, const f
             qa[1] = qa[2];
             qa[2] = qa[3];
         }
-        if (h + 1 < 8) {
-            __syncthreads();  // head h + 1's maxima are in red; everyone is done with buffer par ^ 1 since head h - 1
-            stage_store(par ^ 1);
-        }
     }
-    (void)sk;
-    (void)sv;
     if (!live) return;
     const float u = ldexpf(1.0f, -(so + oshift));
 #pragma unroll
