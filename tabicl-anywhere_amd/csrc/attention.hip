@@ -971,9 +971,10 @@ static AttnPlan plan(const AttnShape &a, bool images) {
     p.waves = p.split16 && a.nq >= 512 ? 8 : 4;
     const int per_group = p.split16 ? 32 * p.waves : (p.mfma ? 64 * QW : QG);
     p.groups = (a.nq + per_group - 1) / per_group;
-    // enough workgroups to fill 256 compute units (a few times over, for the smaller workgroups), each with at least
-    // 2 key blocks
-    const long target = p.waves == 8 ? 256 : 1024;
+    // enough workgroups to fill the 256 compute units about once (twice for the smaller workgroups of two or more
+    // query tiles), each with at least 2 key blocks: more, shorter key ranges measured slower at every batch (the
+    // merge and each workgroup's fixed costs grow with them; 64 queries: 22 us at 256 workgroups against 36 at 632)
+    const long target = p.waves == 8 ? 256 : (p.groups == 1 ? 256 : 512);
     long want = (target + (long)p.groups * a.heads - 1) / ((long)p.groups * a.heads);
     want = std::max(1L, std::min(want, (long)(k.n_kb + 1) / 2));
     p.kb_per_split = (int)((k.n_kb + want - 1) / want);
