@@ -128,8 +128,10 @@ namespace tah {
 enum Epi { EPI_NONE = 0, EPI_GELU = 1, EPI_RESID = 2, EPI_QMOD = 3, EPI_SCALE = 4 };
 
 // Y[M][N] (leading dim ldy) = epi(X[M][K] (ldx) * W[N][K]^T + b[N]); EPI_RESID adds R (ldr, may alias Y).
+// With lnw/lnb, X's rows are layer-normalised first inside the kernel (only where gemm_ln_fits).
 void gemm(hipStream_t s, int M, int N, int K, const float *X, int ldx, const float *W, const float *b, float *Y,
-          int ldy, Epi epi, const float *R, int ldr);
+          int ldy, Epi epi, const float *R, int ldr, const float *lnw = nullptr, const float *lnb = nullptr);
+bool gemm_ln_fits(int M, int K, const float *X, int ldx, const float *W);
 
 // q [M][N] (in place) = q * scale[(m % heads) * N + n] * (1 + tanh(X W^T + b)): the query MLP's modulation.
 void gemm_qmod(hipStream_t s, int M, int N, int K, const float *X, int ldx, const float *W, const float *b, float *q,

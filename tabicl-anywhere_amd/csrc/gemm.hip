@@ -116,23 +116,63 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(int M, int N, int K, const fl
 // wavefronts split K between them, loading MFMA operands straight from global memory (each weight row is read
 // once per tile, coalesced in 64-byte runs); the four partial tiles are summed through LDS before the epilogue.
 // Many more workgroups than the 64 x 64 kernel has at small M, so the weights stream at a useful rate.
-template <int EPI>
+// With LN, the workgroup first normalises its 16 rows into LDS (two passes, biased variance, eps 1e-5, as
+// k_layer_norm; 16 threads a row), and the products read them from there: the separate layer-norm launch, which at
+// these sizes costs as much as the product, goes away.
+constexpr int SKINNY_LN_K = 1024;  // widest rows the fused layer norm takes
+template <int EPI, bool LN>
 __global__ __launch_bounds__(256) void k_gemm_skinny(int M, int N, int K, const float *__restrict__ X, int ldx,
                                                       const float *__restrict__ W, const float *__restrict__ b,
-                                                      float *Y, int ldy, EpiArgs ea) {
+                                                      float *Y, int ldy, EpiArgs ea, const float *__restrict__ lnw,
+                                                      const float *__restrict__ lnb) {
     __shared__ float red[4][16][17];
+    __shared__ __align__(16) float xs[LN ? 16 * (SKINNY_LN_K + 4) : 4];  // rows padded by 4: no bank conflicts
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int m0 = blockIdx.y * 16, n0 = blockIdx.x * 16;
     const int r16 = lane & 15, g4 = lane >> 4;
     const int gm = m0 + r16, gn = n0 + r16;
+    const int xstride = K + 4;
+    if (LN) {
+        const int rr = tid >> 4, cc = tid & 15, gmr = m0 + rr;
+        float *xw = xs + rr * xstride;
+        float sum = 0.0f;
+        for (int k = 4 * cc; k < K; k += 64) {
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (gmr < M) v = *reinterpret_cast<const float4 *>(X + (size_t)gmr * ldx + k);
+            *reinterpret_cast<float4 *>(xw + k) = v;
+            sum += (v.x + v.y) + (v.z + v.w);
+        }
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o, 64);
+        const float mean = sum / (float)K;
+        float sq = 0.0f;
+        for (int k = 4 * cc; k < K; k += 64) {
+            const float4 v = *reinterpret_cast<const float4 *>(xw + k);
+            const float d0 = v.x - mean, d1 = v.y - mean, d2 = v.z - mean, d3 = v.w - mean;
+            sq += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+        }
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) sq += __shfl_xor(sq, o, 64);
+        const float inv = 1.0f / sqrtf(sq / (float)K + 1e-5f);
+        for (int k = 4 * cc; k < K; k += 64) {
+            const float4 v = *reinterpret_cast<const float4 *>(xw + k);
+            const float4 w4 = *reinterpret_cast<const float4 *>(lnw + k), b4 = *reinterpret_cast<const float4 *>(lnb + k);
+            *reinterpret_cast<float4 *>(xw + k) =
+                make_float4((v.x - mean) * inv * w4.x + b4.x, (v.y - mean) * inv * w4.y + b4.y,
+                            (v.z - mean) * inv * w4.z + b4.z, (v.w - mean) * inv * w4.w + b4.w);
+        }
+        __syncthreads();
+    }
     floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     const float *xr = X + (size_t)gm * ldx, *wr = W + (size_t)gn * K;
+    const float *xl = xs + r16 * xstride;
 #pragma unroll 4
     for (int k0 = 16 * wave; k0 < K; k0 += 64) {
         const int gk = k0 + 4 * g4;
         float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), bb = a;
         if (gk < K) {
-            if (gm < M) a = *reinterpret_cast<const float4 *>(xr + gk);
+            if (LN) a = *reinterpret_cast<const float4 *>(xl + gk);
+            else if (gm < M) a = *reinterpret_cast<const float4 *>(xr + gk);
             if (gn < N) bb = *reinterpret_cast<const float4 *>(wr + gk);
         }
         acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, bb.x, acc, 0, 0, 0);
@@ -166,12 +206,18 @@ __global__ __launch_bounds__(256) void k_gemm_plain(int M, int N, int K, const f
 
 template <int EPI>
 static void launch(hipStream_t s, int M, int N, int K, const float *X, int ldx, const float *W, const float *b, float *Y,
-                   int ldy, EpiArgs ea) {
+                   int ldy, EpiArgs ea, const float *lnw = nullptr, const float *lnb = nullptr) {
     const bool aligned = K % 4 == 0 && ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 &&
                          (reinterpret_cast<uintptr_t>(W) & 15) == 0;
-    if (aligned && M <= 256) {
+    if (lnw) {
+        if (!(aligned && M <= 256 && K <= SKINNY_LN_K)) throw ArgError{"gemm: fused layer norm needs the few-rows kernel"};
         dim3 grid((N + 15) / 16, (M + 15) / 16);
-        hipLaunchKernelGGL(k_gemm_skinny<EPI>, grid, dim3(256), 0, s, M, N, K, X, ldx, W, b, Y, ldy, ea);
+        hipLaunchKernelGGL((k_gemm_skinny<EPI, true>), grid, dim3(256), 0, s, M, N, K, X, ldx, W, b, Y, ldy, ea, lnw,
+                           lnb);
+    } else if (aligned && M <= 256) {
+        dim3 grid((N + 15) / 16, (M + 15) / 16);
+        hipLaunchKernelGGL((k_gemm_skinny<EPI, false>), grid, dim3(256), 0, s, M, N, K, X, ldx, W, b, Y, ldy, ea,
+                           nullptr, nullptr);
     } else if (aligned) {
         dim3 grid((N + GB - 1) / GB, (M + GB - 1) / GB);
         hipLaunchKernelGGL(k_gemm_mfma<EPI>, grid, dim3(256), 0, s, M, N, K, X, ldx, W, b, Y, ldy, ea);
@@ -184,16 +230,21 @@ static void launch(hipStream_t s, int M, int N, int K, const float *X, int ldx, 
 }
 
 void gemm(hipStream_t s, int M, int N, int K, const float *X, int ldx, const float *W, const float *b, float *Y, int ldy,
-          Epi epi, const float *R, int ldr) {
+          Epi epi, const float *R, int ldr, const float *lnw, const float *lnb) {
     if (M <= 0 || N <= 0) return;
     if ((size_t)M > (size_t)65535 * 16) throw ArgError{"gemm: too many rows for one launch"};
     const EpiArgs ea{R, ldr, nullptr, 1};
     switch (epi) {
-        case EPI_NONE: launch<EPI_NONE>(s, M, N, K, X, ldx, W, b, Y, ldy, ea); break;
-        case EPI_GELU: launch<EPI_GELU>(s, M, N, K, X, ldx, W, b, Y, ldy, ea); break;
-        case EPI_RESID: launch<EPI_RESID>(s, M, N, K, X, ldx, W, b, Y, ldy, ea); break;
+        case EPI_NONE: launch<EPI_NONE>(s, M, N, K, X, ldx, W, b, Y, ldy, ea, lnw, lnb); break;
+        case EPI_GELU: launch<EPI_GELU>(s, M, N, K, X, ldx, W, b, Y, ldy, ea, lnw, lnb); break;
+        case EPI_RESID: launch<EPI_RESID>(s, M, N, K, X, ldx, W, b, Y, ldy, ea, lnw, lnb); break;
         default: throw ArgError{"gemm: unknown epilogue"};
     }
+}
+
+bool gemm_ln_fits(int M, int K, const float *X, int ldx, const float *W) {
+    return M <= 256 && K <= SKINNY_LN_K && K % 4 == 0 && ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(W) & 15) == 0;
 }
 
 void gemm_qmod(hipStream_t s, int M, int N, int K, const float *X, int ldx, const float *W, const float *b, float *q,

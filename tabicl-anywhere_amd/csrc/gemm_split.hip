@@ -483,6 +483,11 @@ void dense(hipStream_t s, int M, int N, int K, const float *X, int ldx, const fl
     // below a few hundred rows the f32 kernels' weight streaming wins (measured at 64 and 256 rows)
     const bool split = img && M >= 512 && (epi == EPI_NONE || epi == EPI_GELU || epi == EPI_RESID);
     const bool k4 = split && N % 128 == 0 && K % 64 == 0 && K >= 256 && K <= 4 * SPLITK_MAX_KQ;
+    if (lnw && !split && W && gemm_ln_fits(M, K, X, ldx, W)) {
+        // few rows: the layer norm inside the product's kernel
+        gemm(s, M, N, K, X, ldx, W, b, Y, ldy, epi, R, ldr, lnw, lnb);
+        return;
+    }
     if (lnw && !(k4 && K == 512)) {
         // layer normalisation first, into t
         if (!t) throw ArgError{"dense: layer normalisation needs a scratch buffer"};
