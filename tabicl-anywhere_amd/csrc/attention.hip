@@ -403,17 +403,23 @@ __global__ __launch_bounds__(256) void k_attn_decode64(int nq, int rows, int chu
     float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f}, o[2] = {0.0f, 0.0f};
     const int lc = tid >> 2, seg = (tid & 3) * 16;
     const int width = FMT == TAH_KV_F32 ? 4 : (FMT == TAH_KV_I16 ? 2 : 1);
-    for (int kb = kb0; kb < kb1; kb++) {
+    // the next block's tiles are read into registers while the current one is used
+    auto tiles = [&](int kb, float (&tk)[16], float (&tv)[16]) {
         const Where w = locate(kbs, kb, records, FMT, d, chunk);
         const bool fast = w.nk == KB && ((size_t)w.rc * width) % 16 == 0;
-        float tk[16], tv[16];
         load16<FMT>(w.rec, d, w.rc, h * 64 + lc, w.o + seg, w.nk - seg, fast, tk);
         load16<FMT>(w.rec, d, w.rc, d + h * 64 + lc, w.o + seg, w.nk - seg, fast, tv);
+    };
+    float tk[16], tv[16];
+    if (kb0 < kb1) tiles(kb0, tk, tv);
+    for (int kb = kb0; kb < kb1; kb++) {
+        const Where w = locate(kbs, kb, records, FMT, d, chunk);
         __syncthreads();  // the previous block's tiles are no longer read
 #pragma unroll
         for (int i = 0; i < 16; i += 4) *reinterpret_cast<float4 *>(&Ks[lc][seg + i]) = make_float4(tk[i], tk[i + 1], tk[i + 2], tk[i + 3]);
 #pragma unroll
         for (int i = 0; i < 16; i++) Vt[seg + i][lc] = tv[i];
+        if (kb + 1 < kb1) tiles(kb + 1, tk, tv);
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < 2; j++) {
