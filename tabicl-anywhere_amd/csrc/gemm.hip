@@ -191,6 +191,68 @@ __global__ __launch_bounds__(256) void k_gemm_skinny(int M, int N, int K, const 
     }
 }
 
+// At most 8 rows (single-row prediction, the query MLP of one query): one wavefront per output column, its lanes
+// over K (four consecutive columns a lane per 256), the rows held in LDS (normalised there first with LN, 32
+// threads a row), the rows' dot products summed across the wavefront. Every compute unit gets a few columns' weight
+// streams, where the 16 x 16 tile kernel would occupy N / 16 of them.
+constexpr int GEMV_ROWS = 8;
+template <int EPI, bool LN>
+__global__ __launch_bounds__(256) void k_gemv(int M, int N, int K, const float *__restrict__ X, int ldx,
+                                               const float *__restrict__ W, const float *__restrict__ b, float *Y,
+                                               int ldy, EpiArgs ea, const float *__restrict__ lnw,
+                                               const float *__restrict__ lnb) {
+    __shared__ __align__(16) float xs[GEMV_ROWS][SKINNY_LN_K];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = blockIdx.x * 4 + wave;
+    for (int i = 4 * tid; i < M * K; i += 1024) {
+        const int r = i / K, k = i - r * K;
+        *reinterpret_cast<float4 *>(&xs[r][k]) = *reinterpret_cast<const float4 *>(X + (size_t)r * ldx + k);
+    }
+    __syncthreads();
+    if (LN) {
+        const int r = tid >> 5, c = tid & 31;  // 32 threads a row (lanes 32 (r % 2) .. + 31 of a wavefront)
+        float sum = 0.0f;
+        if (r < M)
+            for (int k = c; k < K; k += 32) sum += xs[r][k];
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) sum += __shfl_xor(sum, o, 64);
+        const float mean = sum / (float)K;
+        float sq = 0.0f;
+        if (r < M)
+            for (int k = c; k < K; k += 32) {
+                const float dv = xs[r][k] - mean;
+                sq += dv * dv;
+            }
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) sq += __shfl_xor(sq, o, 64);
+        const float inv = 1.0f / sqrtf(sq / (float)K + 1e-5f);
+        __syncthreads();
+        if (r < M)
+            for (int k = c; k < K; k += 32) xs[r][k] = (xs[r][k] - mean) * inv * lnw[k] + lnb[k];
+        __syncthreads();
+    }
+    if (n >= N) return;
+    float acc[GEMV_ROWS];
+#pragma unroll
+    for (int r = 0; r < GEMV_ROWS; r++) acc[r] = 0.0f;
+    const float *wr = W + (size_t)n * K;
+    for (int k = 4 * lane; k < K; k += 256) {
+        const float4 w4 = *reinterpret_cast<const float4 *>(wr + k);
+#pragma unroll
+        for (int r = 0; r < GEMV_ROWS; r++) {
+            if (r >= M) break;
+            const float4 x4 = *reinterpret_cast<const float4 *>(&xs[r][k]);
+            acc[r] += (w4.x * x4.x + w4.y * x4.y) + (w4.z * x4.z + w4.w * x4.w);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < GEMV_ROWS; r++) {
+        if (r >= M) break;
+        const float a = wave_sum(acc[r]);
+        if (lane == 0) Y[(size_t)r * ldy + n] = epilogue<EPI>(a, b, n, ea, r, N);
+    }
+}
+
 template <int EPI>
 __global__ __launch_bounds__(256) void k_gemm_plain(int M, int N, int K, const float *__restrict__ X, int ldx,
                                                      const float *__restrict__ W, const float *__restrict__ b,
@@ -209,7 +271,15 @@ static void launch(hipStream_t s, int M, int N, int K, const float *X, int ldx, 
                    int ldy, EpiArgs ea, const float *lnw = nullptr, const float *lnb = nullptr) {
     const bool aligned = K % 4 == 0 && ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 &&
                          (reinterpret_cast<uintptr_t>(W) & 15) == 0;
-    if (lnw) {
+    const bool wq = (reinterpret_cast<uintptr_t>(W) & 15) == 0 && K % 4 == 0;
+    if (aligned && wq && M <= GEMV_ROWS && K <= SKINNY_LN_K) {
+        if (lnw)
+            hipLaunchKernelGGL((k_gemv<EPI, true>), dim3((N + 3) / 4), dim3(256), 0, s, M, N, K, X, ldx, W, b, Y, ldy,
+                               ea, lnw, lnb);
+        else
+            hipLaunchKernelGGL((k_gemv<EPI, false>), dim3((N + 3) / 4), dim3(256), 0, s, M, N, K, X, ldx, W, b, Y, ldy,
+                               ea, nullptr, nullptr);
+    } else if (lnw) {
         if (!(aligned && M <= 256 && K <= SKINNY_LN_K)) throw ArgError{"gemm: fused layer norm needs the few-rows kernel"};
         dim3 grid((N + 15) / 16, (M + 15) / 16);
         hipLaunchKernelGGL((k_gemm_skinny<EPI, true>), grid, dim3(256), 0, s, M, N, K, X, ldx, W, b, Y, ldy, ea, lnw,
