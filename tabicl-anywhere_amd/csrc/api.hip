@@ -135,6 +135,7 @@ extern "C" int tah_open(int32_t ordinal, tah_dev **out) {
         return TAH_OK;
     });
     if (rc != TAH_OK) {
+        if (dev->stream) (void)hipStreamDestroy(dev->stream);
         delete dev;
         return rc;
     }
@@ -584,8 +585,13 @@ static void stage_rows(tah_dev *dev, const tah_weights *w, const tah_model *mode
     for (int l = 0; l < w->icl_layers; l++) {
         const DevBlock &b = w->icl[l];
         // query: q = modulate(Wq norm1(h) + bq)  (src/nn.rs:130-152)
-        dense(s, nq, d, d, h, d, b.in_w, b.in_s.rows(0), b.in_b, q, d, EPI_NONE, nullptr, 0, b.n1w, b.n1b, t);
-        query_modulate(s, nq, b, model->scales + (size_t)l * d, q, mid);
+        const float *scale = model->scales + (size_t)l * d;
+        if (query_few_fits(b, nq, h, d)) {
+            query_few(s, nq, h, d, b, scale, q);
+        } else {
+            dense(s, nq, d, d, h, d, b.in_w, b.in_s.rows(0), b.in_b, q, d, EPI_NONE, nullptr, 0, b.n1w, b.n1b, t);
+            query_modulate(s, nq, b, scale, q, mid);
+        }
         // attention over the stored layer, then h += out(att)  (src/predict.rs:421-551)
         const KvImages img = images_of(model, l);
         attention(s, a, q, layer_of(model, l), att, work, &img);

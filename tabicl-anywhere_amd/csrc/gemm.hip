@@ -191,66 +191,105 @@ __global__ __launch_bounds__(256) void k_gemm_skinny(int M, int N, int K, const 
     }
 }
 
-// At most 8 rows (single-row prediction, the query MLP of one query): one wavefront per output column, its lanes
-// over K (four consecutive columns a lane per 256), the rows held in LDS (normalised there first with LN, 32
-// threads a row), the rows' dot products summed across the wavefront. Every compute unit gets a few columns' weight
-// streams, where the 16 x 16 tile kernel would occupy N / 16 of them.
+// At most 8 rows (single-row prediction): one wavefront per output column, its lanes over K (four consecutive
+// columns a lane per 256), the rows held in LDS, the rows' dot products summed across the wavefront. Every global
+// read is issued first -- the column's weights, with LN the norm's weights at the same K positions, the rows, and
+// the bias and residual of the epilogue (lane r holds row r's) -- so that one memory latency precedes the sums
+// rather than a chain of them; with LN each row's mean and inverse deviation go through LDS and the normalisation
+// is applied inside the dot products. Every compute unit gets a few columns' weight streams, where the 16 x 16 tile
+// kernel would occupy N / 16 of them.
 constexpr int GEMV_ROWS = 8;
 template <int EPI, bool LN>
 __global__ __launch_bounds__(256) void k_gemv(int M, int N, int K, const float *__restrict__ X, int ldx,
                                                const float *__restrict__ W, const float *__restrict__ b, float *Y,
                                                int ldy, EpiArgs ea, const float *__restrict__ lnw,
                                                const float *__restrict__ lnb) {
+    constexpr int KJ = SKINNY_LN_K / 256;
     __shared__ __align__(16) float xs[GEMV_ROWS][SKINNY_LN_K];
+    __shared__ float stat[GEMV_ROWS][2];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = blockIdx.x * 4 + wave;
+    const bool col = n < N;
+    // (slots past the row's end, or of a column past N, read clamped in-range addresses and are never used)
+    float4 w4[KJ], g4[KJ], c4[KJ];
+    const float *wr = W + (size_t)min(n, N - 1) * K;
+#pragma unroll
+    for (int j = 0; j < KJ; j++) {
+        const int k = min(4 * lane + 256 * j, K - 4);
+        w4[j] = *reinterpret_cast<const float4 *>(wr + k);
+        if (LN) {
+            g4[j] = *reinterpret_cast<const float4 *>(lnw + k);
+            c4[j] = *reinterpret_cast<const float4 *>(lnb + k);
+        }
+    }
+    float bias = 0.0f, res = 0.0f;
+    if (col && lane < M) {
+        if (b) bias = b[n];
+        if (EPI == EPI_RESID) res = ea.R[(size_t)lane * ea.ldr + n];
+    }
     for (int i = 4 * tid; i < M * K; i += 1024) {
         const int r = i / K, k = i - r * K;
         *reinterpret_cast<float4 *>(&xs[r][k]) = *reinterpret_cast<const float4 *>(X + (size_t)r * ldx + k);
     }
     __syncthreads();
     if (LN) {
-        const int r = tid >> 5, c = tid & 31;  // 32 threads a row (lanes 32 (r % 2) .. + 31 of a wavefront)
-        float sum = 0.0f;
-        if (r < M)
-            for (int k = c; k < K; k += 32) sum += xs[r][k];
-#pragma unroll
-        for (int o = 1; o < 32; o <<= 1) sum += __shfl_xor(sum, o, 64);
-        const float mean = sum / (float)K;
-        float sq = 0.0f;
-        if (r < M)
-            for (int k = c; k < K; k += 32) {
+        // wavefront w takes rows w and w + 4 (two passes: mean, then biased variance; eps 1e-5)
+        for (int r = wave; r < M; r += 4) {
+            float sum = 0.0f;
+            for (int k = lane; k < K; k += 64) sum += xs[r][k];
+            const float mean = wave_sum(sum) / (float)K;
+            float sq = 0.0f;
+            for (int k = lane; k < K; k += 64) {
                 const float dv = xs[r][k] - mean;
                 sq += dv * dv;
             }
-#pragma unroll
-        for (int o = 1; o < 32; o <<= 1) sq += __shfl_xor(sq, o, 64);
-        const float inv = 1.0f / sqrtf(sq / (float)K + 1e-5f);
-        __syncthreads();
-        if (r < M)
-            for (int k = c; k < K; k += 32) xs[r][k] = (xs[r][k] - mean) * inv * lnw[k] + lnb[k];
+            const float inv = 1.0f / sqrtf(wave_sum(sq) / (float)K + 1e-5f);
+            if (lane == 0) {
+                stat[r][0] = mean;
+                stat[r][1] = inv;
+            }
+        }
         __syncthreads();
     }
-    if (n >= N) return;
+    if (!col) return;
     float acc[GEMV_ROWS];
 #pragma unroll
     for (int r = 0; r < GEMV_ROWS; r++) acc[r] = 0.0f;
-    const float *wr = W + (size_t)n * K;
-    for (int k = 4 * lane; k < K; k += 256) {
-        const float4 w4 = *reinterpret_cast<const float4 *>(wr + k);
+#pragma unroll
+    for (int j = 0; j < KJ; j++) {
+        const int k = 4 * lane + 256 * j;
+        if (k >= K) break;
 #pragma unroll
         for (int r = 0; r < GEMV_ROWS; r++) {
             if (r >= M) break;
-            const float4 x4 = *reinterpret_cast<const float4 *>(&xs[r][k]);
-            acc[r] += (w4.x * x4.x + w4.y * x4.y) + (w4.z * x4.z + w4.w * x4.w);
+            float4 x4 = *reinterpret_cast<const float4 *>(&xs[r][k]);
+            if (LN) {
+                const float mean = stat[r][0], inv = stat[r][1];
+                x4.x = (x4.x - mean) * inv * g4[j].x + c4[j].x;
+                x4.y = (x4.y - mean) * inv * g4[j].y + c4[j].y;
+                x4.z = (x4.z - mean) * inv * g4[j].z + c4[j].z;
+                x4.w = (x4.w - mean) * inv * g4[j].w + c4[j].w;
+            }
+            acc[r] += (w4[j].x * x4.x + w4[j].y * x4.y) + (w4[j].z * x4.z + w4[j].w * x4.w);
         }
     }
+    float mine = 0.0f;  // lane r: row r's sum
 #pragma unroll
     for (int r = 0; r < GEMV_ROWS; r++) {
         if (r >= M) break;
         const float a = wave_sum(acc[r]);
-        if (lane == 0) Y[(size_t)r * ldy + n] = epilogue<EPI>(a, b, n, ea, r, N);
+        if (lane == r) mine = a;
     }
+    if (lane >= M) return;
+    float y;
+    if (EPI == EPI_QMOD) {
+        y = epilogue<EPI>(mine, b, n, ea, lane, N);
+    } else {
+        y = mine + bias;
+        if (EPI == EPI_GELU) y = gelu(y);
+        if (EPI == EPI_RESID) y += res;
+    }
+    Y[(size_t)lane * ldy + n] = y;
 }
 
 template <int EPI>
