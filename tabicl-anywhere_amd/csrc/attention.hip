@@ -22,10 +22,10 @@
 //    its B operand with no transpose through LDS.
 //  * k_attn_decode64: head width 64 and few queries, from the records: 256 threads per (key range, head, 8
 //    queries), K/V tiles loaded with 128-bit loads, lane = key for the scores and lane = coordinate for the
-//    weighted sum. Bandwidth-bound, as single-row prediction is.
+//    weighted sum; wavefronts whose query slots are empty skip the arithmetic (one query: wavefront 0 alone).
 //  * k_attn_decode: any other head width up to 64 (the tiny test models): the same with one wavefront.
-// All of them leave the running maximum in log2 units (score * log2 e) for the split merge (k_attn_merge64 for
-// head width 64 and few key ranges, k_attn_merge otherwise).
+// All of them leave the running maximum in log2 units (score * log2 e) for the split merge (head width 64:
+// k_attn_merge64 for few key ranges, k_attn_merge_many for many; k_attn_merge otherwise).
 #include <algorithm>
 
 #include "common.hpp"
@@ -424,6 +424,7 @@ __global__ __launch_bounds__(256) void k_attn_decode64(int nq, int rows, int chu
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const int qi = j ? qb : qa;
+            if (q0 + qi >= nq) continue;  // (wavefront-uniform) no query in this slot
             float sc = 0.0f;
 #pragma unroll 16
             for (int c = 0; c < 64; c++) sc += Qs[qi][c] * Ks[c][lane];
@@ -440,6 +441,7 @@ __global__ __launch_bounds__(256) void k_attn_decode64(int nq, int rows, int chu
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const int qi = j ? qb : qa;
+            if (q0 + qi >= nq) continue;
             float a = 0.0f;
 #pragma unroll 16
             for (int k = 0; k < KB; k++) a += Ps[qi][k] * Vt[k][lane];
@@ -916,6 +918,68 @@ __global__ __launch_bounds__(256) void k_attn_merge64(int items, int heads, int 
     *reinterpret_cast<float4 *>(out + ((size_t)qr * heads + h) * 64 + c4) = make_float4(O.x / L, O.y / L, O.z / L, O.w / L);
 }
 
+// Head width 64, maxima in log2 units, many splits (the few-query kernel's short key ranges): one workgroup of
+// 1024 threads per (query, head), lane = coordinate. Wavefront w takes splits w, w + 16, ..., MW_PER of them a pass
+// with every load issued before any is used, and sums them against its own running maximum; the 16 wavefronts'
+// sums are then rescaled to the largest maximum through LDS. One memory latency per pass rather than one per split.
+constexpr int MW_WAVES = 16, MW_PER = 16;
+__global__ __launch_bounds__(1024) void k_attn_merge_many(int items, int splits, const float *__restrict__ part_o,
+                                                          const float *__restrict__ part_ml, float *__restrict__ out) {
+    __shared__ float wo[MW_WAVES][64], wml[MW_WAVES][2];
+    const int i = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const size_t stride = (size_t)items;  // between splits, in (query, head) items
+    float M = -INFINITY, L = 0.0f, O = 0.0f;
+    for (int s0 = wave; s0 < splits; s0 += MW_WAVES * MW_PER) {
+        float2 ml[MW_PER];
+        float po[MW_PER];
+#pragma unroll
+        for (int u = 0; u < MW_PER; u++) {
+            const int sp = s0 + u * MW_WAVES;
+            if (sp < splits) {
+                const size_t at = sp * stride + i;
+                ml[u] = *reinterpret_cast<const float2 *>(part_ml + at * 2);
+                po[u] = part_o[at * 64 + lane];
+            } else {
+                ml[u] = make_float2(-INFINITY, 0.0f);
+                po[u] = 0.0f;
+            }
+        }
+        float cm = M;
+#pragma unroll
+        for (int u = 0; u < MW_PER; u++)
+            if (ml[u].y > 0.0f) cm = fmaxf(cm, ml[u].x);
+        const float r = M == -INFINITY ? 0.0f : exp2_hw(M - cm);
+        L *= r;
+        O *= r;
+        M = cm;
+#pragma unroll
+        for (int u = 0; u < MW_PER; u++) {
+            const float f = ml[u].y > 0.0f ? exp2_hw(ml[u].x - M) : 0.0f;
+            L += ml[u].y * f;
+            O += po[u] * f;
+        }
+    }
+    wo[wave][lane] = O;
+    if (lane == 0) {
+        wml[wave][0] = M;
+        wml[wave][1] = L;
+    }
+    __syncthreads();
+    if (wave) return;
+    float GM = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < MW_WAVES; w++)
+        if (wml[w][1] > 0.0f) GM = fmaxf(GM, wml[w][0]);
+    float GL = 0.0f, GO = 0.0f;
+#pragma unroll
+    for (int w = 0; w < MW_WAVES; w++) {
+        const float f = wml[w][1] > 0.0f ? exp2_hw(wml[w][0] - GM) : 0.0f;
+        GL += wml[w][1] * f;
+        GO += wo[w][lane] * f;
+    }
+    out[(size_t)i * 64 + lane] = GO / GL;
+}
+
 void merge_splits(hipStream_t s, int nq, int d, int heads, int splits, const float *part_o, const float *part_ml,
                   float *out) {
     hipLaunchKernelGGL(k_attn_merge, dim3(nq * heads), dim3(64), 0, s, nq, d, heads, splits, 0, part_o, part_ml, out);
@@ -1045,6 +1109,9 @@ void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t 
         if (a.d == 64 * a.heads && p.splits <= 16)  // many queries, few splits (else lanes over splits win)
             hipLaunchKernelGGL(k_attn_merge64, dim3((a.nq * a.heads + 15) / 16), dim3(256), 0, s, a.nq * a.heads,
                                a.heads, p.splits, part_o, part_ml, out);
+        else if (a.d == 64 * a.heads && (long)a.nq * a.heads <= 512)  // few items: a workgroup each
+            hipLaunchKernelGGL(k_attn_merge_many, dim3(a.nq * a.heads), dim3(1024), 0, s, a.nq * a.heads, p.splits,
+                               part_o, part_ml, out);
         else
             hipLaunchKernelGGL(k_attn_merge, dim3(a.nq * a.heads), dim3(64), 0, s, a.nq, a.d, a.heads, p.splits, 1,
                                part_o, part_ml, out);
