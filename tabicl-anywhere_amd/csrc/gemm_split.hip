@@ -20,8 +20,12 @@ namespace tah {
 struct SplitEpi {
     const float *R;      // EPI_RESID: added; EPI_QMOD: the query being modulated (may alias Y)
     int ldr;
-    const float *scale;  // EPI_SCALE: [N]; EPI_QMOD: [heads][N]
+    const float *scale;  // EPI_SCALE: [N]; EPI_QMOD: [heads][N]; the fused query MLP: [N] (head h at 64 h)
     int heads;
+    // the fused query MLP (k_gemm_splitk4 with QM): W0 and W2 as gemm_split images, their shifts and biases
+    const uint8_t *w0 = nullptr, *w2 = nullptr;
+    int s0 = 0, s2 = 0;
+    const float *b0 = nullptr, *b2 = nullptr;
 };
 
 template <int EPI, int TN>
@@ -132,14 +136,104 @@ __global__ __launch_bounds__(256, 3) void k_gemm_split(int M, int N, int K, cons
         }
 }
 
+// ---- the query MLP of the scalable softmax, whole, for head width 64 and hidden width 64 ------------------------
+// q *= scale[h] * (1 + tanh1(W2 gelu(W0 q + b0) + b2)) (src/nn.rs:130-152) for the 32 query-heads of a wavefront:
+// lane l holds query-head l % 32, its 64 coordinates 16 ks + 8 (l / 32) + t in xv[ks][t] (split once here); H^T =
+// W0 X^T with W0's rows in sigma32 order leaves the hidden layer in registers as the B operand of Y^T = W2 H^T, and
+// the lane's output columns are exactly the input columns it holds, so the modulation needs no second read of q.
+// W0 and W2 are read from their gemm_split images; sc = the head's 64 scales; the result goes to dst (the
+// query-head's 64 values), nowhere where dst is null.
+__device__ __forceinline__ void qmlp64_lane(const float (&xv)[4][8], int r32, int g, const uint8_t *__restrict__ w0,
+                                            int s0, const float *__restrict__ b0, const uint8_t *__restrict__ w2,
+                                            int s2, const float *__restrict__ b2, const float *__restrict__ sc,
+                                            float *dst) {
+    float xmax = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+        for (int t = 0; t < 8; t++) xmax = fmaxf(xmax, fabsf(xv[ks][t]));
+    xmax = fmaxf(xmax, __shfl_xor(xmax, 32, 64));
+    const int sx = shift_for_max(xmax);
+    halfx8 xh[4], xl[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) split8(xv[ks], ldexpf(1.0f, sx), xh[ks], xl[ks]);
+    // hidden = gelu(W0 x + b0): 2 tiles of 32, 4 steps of 16 (image: (tile * 4 + step) * 2 KB)
+    floatx16 hacc[2];
+#pragma unroll
+    for (int T = 0; T < 2; T++) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) hacc[T][v] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const uint8_t *w = w0 + ((size_t)T * 4 + ks) * 2048 + (g * 32 + r32) * 16;
+            hacc[T] = mfma16x3(*reinterpret_cast<const halfx8 *>(w), *reinterpret_cast<const halfx8 *>(w + 1024),
+                               xh[ks], xl[ks], hacc[T]);
+        }
+    }
+    const float u0 = ldexpf(1.0f, -(sx + s0));
+    float hmax = 0.0f;
+#pragma unroll
+    for (int T = 0; T < 2; T++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const float *bp = b0 + 32 * T + 16 * hh + 8 * g;
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const float hv = gelu(hacc[T][8 * hh + t] * u0 + bp[t]);
+                hacc[T][8 * hh + t] = hv;
+                hmax = fmaxf(hmax, fabsf(hv));
+            }
+        }
+    hmax = fmaxf(hmax, __shfl_xor(hmax, 32, 64));
+    const int sh = shift_for_max(hmax);
+    halfx8 hh8[4], hl8[4];
+#pragma unroll
+    for (int T = 0; T < 2; T++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            float hv[8];
+#pragma unroll
+            for (int t = 0; t < 8; t++) hv[t] = hacc[T][8 * hh + t];
+            split8(hv, ldexpf(1.0f, sh), hh8[2 * T + hh], hl8[2 * T + hh]);
+        }
+    // y = W2 hidden + b2; q *= scale (1 + tanh1(y)); output column 32 T + 16 hh + 8 g + t is input step 2 T + hh
+    floatx16 yacc[2];
+#pragma unroll
+    for (int T = 0; T < 2; T++) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) yacc[T][v] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const uint8_t *w = w2 + ((size_t)T * 4 + ks) * 2048 + (g * 32 + r32) * 16;
+            yacc[T] = mfma16x3(*reinterpret_cast<const halfx8 *>(w), *reinterpret_cast<const halfx8 *>(w + 1024),
+                               hh8[ks], hl8[ks], yacc[T]);
+        }
+    }
+    if (!dst) return;
+    const float u2 = ldexpf(1.0f, -(sh + s2));
+#pragma unroll
+    for (int T = 0; T < 2; T++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const int n0 = 32 * T + 16 * hh + 8 * g;
+            float out[8];
+#pragma unroll
+            for (int t = 0; t < 8; t++)
+                out[t] = xv[2 * T + hh][t] * (sc[n0 + t] * (1.0f + tanh1(yacc[T][8 * hh + t] * u2 + b2[n0 + t])));
+            *reinterpret_cast<float4 *>(dst + n0) = make_float4(out[0], out[1], out[2], out[3]);
+            *reinterpret_cast<float4 *>(dst + n0 + 4) = make_float4(out[4], out[5], out[6], out[7]);
+        }
+}
+
 // Few rows and long rows (the in-context stage: 2,048 queries, K = 512 or 1024): one workgroup per 32 rows x 128
 // columns, its four wavefronts splitting K four ways (each a quarter, in chunks of 128 with their own per-row
 // powers of two), then summing their partial products -- unscaled to f32 -- through LDS; wavefront w finishes
 // tile w. Four times the wavefronts of k_gemm_split on the same grid of outputs, each with a quarter of the
-// dependent chain.
+// dependent chain. With QM (the query projection, 128 columns = two heads of 64), the finished tile goes through LDS
+// and wavefronts 0 and 1 run the query MLP on one head each (qmlp64_lane): no separate launch for it.
 constexpr int SPLITK_MAX_KQ = 512;  // each wavefront's share of K at most (K at most 2048)
 
-template <int EPI, bool LN, int TN>
+template <int EPI, bool LN, int TN, bool QM = false>
 __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, const float *__restrict__ X, int ldx,
                                                           const uint8_t *__restrict__ wimg, int wshift,
                                                           const float *__restrict__ b, float *Y, int ldy, SplitEpi ea,
@@ -261,6 +355,38 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
 #pragma unroll
         for (int v = 0; v < 16; v++) red[wave][T][v][lane] = acc[T][v] * u;
     __syncthreads();
+    if (QM) {
+        static_assert(TN == 4, "the fused query MLP takes two whole heads per workgroup");
+        // wavefront w: tile w (rows r32, columns 32 w + 16 hh + 8 g + t of the workgroup's 128), bias added
+        float yq[2][8];
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const int n0 = 32 * (nt0 + wave) + 16 * hh + 8 * g;
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const int v = 8 * hh + t;
+                yq[hh][t] = (((red[0][wave][v][lane] + red[1][wave][v][lane]) + red[2][wave][v][lane]) +
+                             red[3][wave][v][lane]) + b[n0 + t];
+            }
+        }
+        __syncthreads();  // the partial sums are all read: their LDS holds the tile next, [32 rows][132]
+        float *qt = &red[0][0][0][0];
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+            for (int t = 0; t < 8; t++) qt[r32 * 132 + 32 * wave + 16 * hh + 8 * g + t] = yq[hh][t];
+        __syncthreads();
+        if (wave >= 2) return;
+        float xv[4][8];
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+            for (int t = 0; t < 8; t++) xv[ks][t] = qt[r32 * 132 + 64 * wave + 16 * ks + 8 * g + t];
+        const int head = 2 * blockIdx.x + wave;
+        qmlp64_lane(xv, r32, g, ea.w0, ea.s0, ea.b0, ea.w2, ea.s2, ea.b2, ea.scale + 64 * head,
+                    live ? Y + (size_t)m * ldy + 64 * head : nullptr);
+        return;
+    }
     if (!live) return;
     // wavefront w sums tile w (both halves) of four, or half w % 2 of tile w / 2 of two
     const int T = TN == 4 ? wave : wave >> 1;
@@ -297,12 +423,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
     }
 }
 
-// ---- the query MLP of the scalable softmax, whole, for head width 64 and hidden width 64 ------------------------
-// q [rows * heads][64] in place: q *= scale[h] * (1 + tanh1(W2 gelu(W0 q + b0) + b2)) (src/nn.rs:130-152). Each
-// wavefront owns 32 query-heads (lane = query-head, its 64 coordinates on lanes l and l + 32), split once; H^T =
-// W0 X^T with W0's rows in sigma32 order leaves the hidden layer in registers as the B operand of Y^T = W2 H^T, and
-// the lane's output columns are exactly the input columns it holds, so the modulation needs no second read of q.
-// W0 and W2 are read from their gemm_split images.
+// grid ceil(M / 128); 256 threads: q [rows * heads][64] in place, wavefront w the query-heads of rows 32 (4 x + w) +
+// 0..31 of that view.
 __global__ __launch_bounds__(256) void k_qmlp64(int M, int heads, float *__restrict__ q, const uint8_t *__restrict__ w0,
                                                 int s0, const float *__restrict__ b0, const uint8_t *__restrict__ w2,
                                                 int s2, const float *__restrict__ b2, const float *__restrict__ scale) {
@@ -322,83 +444,7 @@ __global__ __launch_bounds__(256) void k_qmlp64(int M, int heads, float *__restr
         xv[ks][0] = a.x; xv[ks][1] = a.y; xv[ks][2] = a.z; xv[ks][3] = a.w;
         xv[ks][4] = c.x; xv[ks][5] = c.y; xv[ks][6] = c.z; xv[ks][7] = c.w;
     }
-    float xmax = 0.0f;
-#pragma unroll
-    for (int ks = 0; ks < 4; ks++)
-#pragma unroll
-        for (int t = 0; t < 8; t++) xmax = fmaxf(xmax, fabsf(xv[ks][t]));
-    xmax = fmaxf(xmax, __shfl_xor(xmax, 32, 64));
-    const int sx = shift_for_max(xmax);
-    halfx8 xh[4], xl[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ks++) split8(xv[ks], ldexpf(1.0f, sx), xh[ks], xl[ks]);
-    // hidden = gelu(W0 x + b0): 2 tiles of 32, 4 steps of 16 (image: (tile * 4 + step) * 2 KB)
-    floatx16 hacc[2];
-#pragma unroll
-    for (int T = 0; T < 2; T++) {
-#pragma unroll
-        for (int v = 0; v < 16; v++) hacc[T][v] = 0.0f;
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            const uint8_t *w = w0 + ((size_t)T * 4 + ks) * 2048 + (g * 32 + r32) * 16;
-            hacc[T] = mfma16x3(*reinterpret_cast<const halfx8 *>(w), *reinterpret_cast<const halfx8 *>(w + 1024),
-                               xh[ks], xl[ks], hacc[T]);
-        }
-    }
-    const float u0 = ldexpf(1.0f, -(sx + s0));
-    float hmax = 0.0f;
-#pragma unroll
-    for (int T = 0; T < 2; T++)
-#pragma unroll
-        for (int hh = 0; hh < 2; hh++) {
-            const float *bp = b0 + 32 * T + 16 * hh + 8 * g;
-#pragma unroll
-            for (int t = 0; t < 8; t++) {
-                const float hv = gelu(hacc[T][8 * hh + t] * u0 + bp[t]);
-                hacc[T][8 * hh + t] = hv;
-                hmax = fmaxf(hmax, fabsf(hv));
-            }
-        }
-    hmax = fmaxf(hmax, __shfl_xor(hmax, 32, 64));
-    const int sh = shift_for_max(hmax);
-    halfx8 hh8[4], hl8[4];
-#pragma unroll
-    for (int T = 0; T < 2; T++)
-#pragma unroll
-        for (int hh = 0; hh < 2; hh++) {
-            float hv[8];
-#pragma unroll
-            for (int t = 0; t < 8; t++) hv[t] = hacc[T][8 * hh + t];
-            split8(hv, ldexpf(1.0f, sh), hh8[2 * T + hh], hl8[2 * T + hh]);
-        }
-    // y = W2 hidden + b2; q *= scale (1 + tanh1(y)); output column 32 T + 16 hh + 8 g + t is input step 2 T + hh
-    floatx16 yacc[2];
-#pragma unroll
-    for (int T = 0; T < 2; T++) {
-#pragma unroll
-        for (int v = 0; v < 16; v++) yacc[T][v] = 0.0f;
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            const uint8_t *w = w2 + ((size_t)T * 4 + ks) * 2048 + (g * 32 + r32) * 16;
-            yacc[T] = mfma16x3(*reinterpret_cast<const halfx8 *>(w), *reinterpret_cast<const halfx8 *>(w + 1024),
-                               hh8[ks], hl8[ks], yacc[T]);
-        }
-    }
-    if (!live) return;
-    const float u2 = ldexpf(1.0f, -(sh + s2));
-    const float *sc = scale + (size_t)(m % heads) * 64;
-#pragma unroll
-    for (int T = 0; T < 2; T++)
-#pragma unroll
-        for (int hh = 0; hh < 2; hh++) {
-            const int n0 = 32 * T + 16 * hh + 8 * g;
-            float out[8];
-#pragma unroll
-            for (int t = 0; t < 8; t++)
-                out[t] = xv[2 * T + hh][t] * (sc[n0 + t] * (1.0f + tanh1(yacc[T][8 * hh + t] * u2 + b2[n0 + t])));
-            *reinterpret_cast<float4 *>(qr + n0) = make_float4(out[0], out[1], out[2], out[3]);
-            *reinterpret_cast<float4 *>(qr + n0 + 4) = make_float4(out[4], out[5], out[6], out[7]);
-        }
+    qmlp64_lane(xv, r32, g, w0, s0, b0, w2, s2, b2, scale + (size_t)(m % heads) * 64, live ? qr : nullptr);
 }
 
 bool qmlp_fused(const DevBlock &b) {
@@ -472,6 +518,29 @@ static void launch_splitk4(hipStream_t s, int M, int N, int K, const float *X, i
                                Y, ldy, ea, lnw, lnb);
             break;
     }
+    TAH_LAUNCHED();
+}
+
+bool query_split_fits(const DevBlock &b, int M, const float *X, int ldx, const float *Y) {
+    const SplitW &w = b.in_s;
+    return M >= 512 && w.img && w.row0 == 0 && w.K == b.d && b.d == 512 && b.d % 128 == 0 && b.heads > 0 &&
+           b.d == 64 * b.heads && qmlp_fused(b) && b.n1w && b.n1b && ldx % 4 == 0 &&
+           (reinterpret_cast<uintptr_t>(X) & 15) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0 &&
+           (size_t)(M + 31) / 32 <= 65535;
+}
+
+void query_split(hipStream_t s, int M, const float *X, int ldx, const DevBlock &b, const float *scale, float *q) {
+    if (!query_split_fits(b, M, X, ldx, q)) throw ArgError{"query_split: shape not supported"};
+    SplitEpi ea{nullptr, 0, scale, b.heads};
+    ea.w0 = b.q0_s.img;
+    ea.s0 = b.q0_s.shift;
+    ea.b0 = b.q0b;
+    ea.w2 = b.q2_s.img;
+    ea.s2 = b.q2_s.shift;
+    ea.b2 = b.q2b;
+    const int d = b.d;
+    hipLaunchKernelGGL((k_gemm_splitk4<EPI_NONE, true, 4, true>), dim3(d / 128, (M + 31) / 32), dim3(256), 0, s, M, d,
+                       d, X, ldx, b.in_s.img, b.in_s.shift, b.in_b, q, d, ea, b.n1w, b.n1b);
     TAH_LAUNCHED();
 }
 
