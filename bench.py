@@ -35,7 +35,7 @@ PEAK_F16_MFMA = 2.5e15  # MI355X dense fp16 matrix FLOP/s
 PEAK_SPLIT_F32 = PEAK_F16_MFMA / 3  # f32 work at three fp16 products per f32 product
 # HBM bytes per launch of the roofline kernel, from rocprofv3 FETCH_SIZE and WRITE_SIZE runs of this bench scaled by
 # the counters' reading on its own 256 MiB copy (profiles/attention_f32_2048x10000_memory.md)
-TRAFFIC_BYTES = 74.0e6
+TRAFFIC_BYTES = 75.6e6
 
 
 def log(*a):
