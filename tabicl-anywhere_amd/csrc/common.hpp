@@ -162,7 +162,8 @@ size_t query_scratch_floats(int rows, const DevBlock &b);
 // The whole query MLP in one kernel (gemm_split.hip), for head width 64 and hidden width 64 with images.
 bool qmlp_fused(const DevBlock &b);
 // q = modulate(Wq norm1(X) + bq) for many rows in one launch: the split-K projection with the query MLP in its
-// epilogue (d = 512, head width and query-MLP width 64, at least 512 rows)
+// epilogue (d = 512, head width and query-MLP width 64; measured faster than the f32 projection and a separate
+// query MLP from 64 rows up, and the few-row kernel takes up to eight)
 bool query_split_fits(const DevBlock &b, int M, const float *X, int ldx, const float *Y);
 void query_split(hipStream_t s, int M, const float *X, int ldx, const DevBlock &b, const float *scale, float *q);
 void qmlp(hipStream_t s, int rows, const DevBlock &b, const float *scale, float *q);

@@ -523,7 +523,7 @@ static void launch_splitk4(hipStream_t s, int M, int N, int K, const float *X, i
 
 bool query_split_fits(const DevBlock &b, int M, const float *X, int ldx, const float *Y) {
     const SplitW &w = b.in_s;
-    return M >= 512 && w.img && w.row0 == 0 && w.K == b.d && b.d == 512 && b.d % 128 == 0 && b.heads > 0 &&
+    return M > 8 && w.img && w.row0 == 0 && w.K == b.d && b.d == 512 && b.d % 128 == 0 && b.heads > 0 &&
            b.d == 64 * b.heads && qmlp_fused(b) && b.n1w && b.n1b && ldx % 4 == 0 &&
            (reinterpret_cast<uintptr_t>(X) & 15) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0 &&
            (size_t)(M + 31) / 32 <= 65535;
