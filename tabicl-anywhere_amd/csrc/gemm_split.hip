@@ -549,8 +549,9 @@ void dense(hipStream_t s, int M, int N, int K, const float *X, int ldx, const fl
     const bool img = w.img && gemm_split_fits(N, K) && K == w.K && w.row0 % 32 == 0 && N + w.row0 <= w.N &&
                      ldx % 4 == 0 && ldy % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 &&
                      (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
-    // below a few hundred rows the f32 kernels' weight streaming wins (measured at 64 and 256 rows)
-    const bool split = img && M >= 512 && (epi == EPI_NONE || epi == EPI_GELU || epi == EPI_RESID);
+    // at 64 rows the f32 kernels' weight streaming wins (1.41 against 1.48 ms a prediction), at 256 the split
+    // kernels (1.66 against 1.72 ms)
+    const bool split = img && M >= 256 && (epi == EPI_NONE || epi == EPI_GELU || epi == EPI_RESID);
     const bool k4 = split && N % 128 == 0 && K % 64 == 0 && K >= 256 && K <= 4 * SPLITK_MAX_KQ;
     if (lnw && !split && W && gemm_ln_fits(M, K, X, ldx, W)) {
         // few rows: the layer norm inside the product's kernel
