@@ -1013,7 +1013,8 @@ extern "C" int tah_fit_represent(tah_dev *dev, const tah_weights *w, const float
                     const size_t off = ((size_t)dg * nb + bi) * per;
                     col_records(s, g, inds, e, kv2, col_kv, gstride, off, g0);
                     // every cell against them (src/fit.rs:404-406)
-                    column_block(s, w, a2, cells, rows, g, 1, rows, col_kv + (size_t)g0 * gstride + off, gstride, t, q, att, mid);
+                    column_block(s, w, a2, cells, rows, g, 1, rows, col_kv + (size_t)g0 * gstride + off, gstride, t, q, att,
+                                 M * e * sizeof(float), mid);
                 }
                 if (digits > 1) add_to(s, M * e, cells, sum);
             }

@@ -130,7 +130,8 @@ enum Epi { EPI_NONE = 0, EPI_GELU = 1, EPI_RESID = 2, EPI_QMOD = 3, EPI_SCALE = 
 // Y[M][N] (leading dim ldy) = epi(X[M][K] (ldx) * W[N][K]^T + b[N]); EPI_RESID adds R (ldr, may alias Y).
 // With lnw/lnb, X's rows are layer-normalised first inside the kernel (only where gemm_ln_fits).
 void gemm(hipStream_t s, int M, int N, int K, const float *X, int ldx, const float *W, const float *b, float *Y,
-          int ldy, Epi epi, const float *R, int ldr, const float *lnw = nullptr, const float *lnb = nullptr);
+          int ldy, Epi epi, const float *R, int ldr, const float *lnw = nullptr, const float *lnb = nullptr,
+          const float *scale = nullptr);
 bool gemm_ln_fits(int M, int K, const float *X, int ldx, const float *W);
 
 // q [M][N] (in place) = q * scale[(m % heads) * N + n] * (1 + tanh(X W^T + b)): the query MLP's modulation.
@@ -233,8 +234,10 @@ void assemble_tokens(hipStream_t s, const tah_weights *w, const float *cells, in
 size_t row_stage_floats(const tah_weights *w, int n, int T);
 void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, const float *cosv, const float *sinv,
                float *rep, float *scratch);
+// att: att_bytes of scratch (the fused kernel needs cell_block_work_bytes(groups) of it, else M e floats)
 void column_block(hipStream_t s, const tah_weights *w, const DevBlock &b, float *cells, int n, int groups, size_t sr,
-                  size_t sg, const float *kvbase, size_t gstride, float *t, float *q, float *att, float *mid);
+                  size_t sg, const float *kvbase, size_t gstride, float *t, float *q, float *att, size_t att_bytes,
+                  float *mid);
 
 // The column stage of a fit (fit_stages.hip).
 void fit_cells(hipStream_t s, const tah_weights *w, const float *x, int rows, int features, int g0, int gb, float *cells);

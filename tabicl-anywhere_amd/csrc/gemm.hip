@@ -28,6 +28,7 @@ __device__ __forceinline__ float epilogue(float acc, const float *b, int n, cons
     if (EPI == EPI_GELU) y = gelu(y);
     if (EPI == EPI_RESID) y += e.R[(size_t)m * e.ldr + n];
     if (EPI == EPI_QMOD) y = e.R[(size_t)m * e.ldr + n] * (e.scale[(m % e.heads) * N + n] * (1.0f + tanh1(y)));
+    if (EPI == EPI_SCALE) y *= e.scale[n];
     return y;
 }
 
@@ -282,7 +283,7 @@ __global__ __launch_bounds__(256) void k_gemv(int M, int N, int K, const float *
     }
     if (lane >= M) return;
     float y;
-    if (EPI == EPI_QMOD) {
+    if (EPI == EPI_QMOD || EPI == EPI_SCALE) {
         y = epilogue<EPI>(mine, b, n, ea, lane, N);
     } else {
         y = mine + bias;
@@ -339,14 +340,16 @@ static void launch(hipStream_t s, int M, int N, int K, const float *X, int ldx, 
 }
 
 void gemm(hipStream_t s, int M, int N, int K, const float *X, int ldx, const float *W, const float *b, float *Y, int ldy,
-          Epi epi, const float *R, int ldr, const float *lnw, const float *lnb) {
+          Epi epi, const float *R, int ldr, const float *lnw, const float *lnb, const float *scale) {
     if (M <= 0 || N <= 0) return;
     if ((size_t)M > (size_t)65535 * 16) throw ArgError{"gemm: too many rows for one launch"};
-    const EpiArgs ea{R, ldr, nullptr, 1};
+    if (epi == EPI_SCALE && !scale) throw ArgError{"gemm: the scale epilogue needs its scales"};
+    const EpiArgs ea{R, ldr, scale, 1};
     switch (epi) {
         case EPI_NONE: launch<EPI_NONE>(s, M, N, K, X, ldx, W, b, Y, ldy, ea, lnw, lnb); break;
         case EPI_GELU: launch<EPI_GELU>(s, M, N, K, X, ldx, W, b, Y, ldy, ea, lnw, lnb); break;
         case EPI_RESID: launch<EPI_RESID>(s, M, N, K, X, ldx, W, b, Y, ldy, ea, lnw, lnb); break;
+        case EPI_SCALE: launch<EPI_SCALE>(s, M, N, K, X, ldx, W, b, Y, ldy, ea, lnw, lnb); break;
         default: throw ArgError{"gemm: unknown epilogue"};
     }
 }

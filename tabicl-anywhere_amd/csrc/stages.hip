@@ -629,14 +629,29 @@ void input_cells(hipStream_t s, const tah_weights *w, const float *x, int n, int
     TAH_LAUNCHED();
 }
 
-// x [M][e] += l2(gelu(l1(norm2 x))): the fused kernel where the block's shape has one, else layer_norm and two GEMMs
-// (t [M][e] and mid [M][ff] scratch).
+// At most this many rows (one 128-row tile: the cells or tokens of a single table row), the width-128 projections
+// and feed-forward run on the f32 kernels, whose grids spread the weights over many compute units, rather than on
+// the fused tile kernels, which stream every weight through the one workgroup of the tile.
+constexpr int SMALL_ROWS = 128;
+// The row block's fused kernel (k_row_block, a workgroup per table row) from this many table rows up; below, the
+// projections, the attention (a workgroup per row and head) and the output projection separately (measured: one
+// row 0.84 -> 0.76 ms a prediction, 64 rows 1.43 -> 1.40 ms).
+constexpr int ROW_BLOCK_MIN = 128;
+
+// x [M][e] += l2(gelu(l1(norm2 x))): the fused kernel where the block's shape has one (above SMALL_ROWS rows), else
+// two GEMMs with the norm folded into the first where it fits, else layer_norm and two GEMMs (t [M][e] and mid [M][ff]
+// scratch).
 static void feed_forward(hipStream_t s, int M, float *x, const DevBlock &b, float *t, float *mid) {
-    if (b.l1img) {
+    if (b.l1img && M > SMALL_ROWS) {
         ff_block(s, M, x, b);
         return;
     }
     const int e = b.d;
+    if (gemm_ln_fits(M, e, x, e, b.l1w)) {
+        gemm(s, M, b.ff, e, x, e, b.l1w, b.l1b, mid, b.ff, EPI_GELU, nullptr, 0, b.n2w, b.n2b);
+        gemm(s, M, e, b.ff, mid, b.ff, b.l2w, b.l2b, x, e, EPI_RESID, x, e);
+        return;
+    }
     layer_norm(s, M, e, x, e, b.n2w, b.n2b, t, e);
     gemm(s, M, b.ff, e, t, e, b.l1w, b.l1b, mid, b.ff, EPI_GELU, nullptr, 0);
     gemm(s, M, e, b.ff, mid, b.ff, b.l2w, b.l2b, x, e, EPI_RESID, x, e);
@@ -645,7 +660,7 @@ static void feed_forward(hipStream_t s, int M, float *x, const DevBlock &b, floa
 // x [M][e] += out(att): the block's output projection and residual add
 static void out_projection(hipStream_t s, int M, const float *att, const DevBlock &b, float *x) {
     const int e = b.d;
-    if (b.outimg)
+    if (b.outimg && M > SMALL_ROWS)
         rows128(s, M, e, att, e, b.outimg, b.outs, b.out_b, x, e, EPI_RESID, x, e, nullptr, nullptr, nullptr);
     else
         dense(s, M, e, e, att, e, b.out_w, b.out_s, b.out_b, x, e, EPI_RESID, x, e);
@@ -654,18 +669,21 @@ static void out_projection(hipStream_t s, int M, const float *att, const DevBloc
 // One column block (cached_block with a2) for all cells in place: n rows x groups, cell (r, g) at row r * sr + g * sg
 // of cells; K/V of group g at kvbase + g * gstride.
 void column_block(hipStream_t s, const tah_weights *w, const DevBlock &b, float *cells, int n, int groups, size_t sr,
-                  size_t sg, const float *kvbase, size_t gstride, float *t, float *q, float *att, float *mid) {
+                  size_t sg, const float *kvbase, size_t gstride, float *t, float *q, float *att, size_t att_bytes,
+                  float *mid) {
     const int e = w->e;
     const int M = n * groups;
-    if (cell_block_fits(b) && w->inds == 128 && cell_block_work_bytes(groups) <= (size_t)M * e * sizeof(float)) {
+    if (cell_block_fits(b) && w->inds == 128 && cell_block_work_bytes(groups) <= att_bytes) {
         // the attention half in one kernel; the query and attention buffers are not needed, att holds the images
         cell_block(s, n, groups, sr, sg, cells, b, w->col_scale, kvbase, gstride, att);
         feed_forward(s, M, cells, b, t, mid);
         return;
     }
-    if (b.inimg && b.ss_hidden == 0) {
+    if (b.inimg && b.ss_hidden == 0 && M > SMALL_ROWS) {
         // norm1, the query projection and its scale in one pass
         rows128(s, M, e, cells, e, b.inimg, b.ins, b.in_b, q, e, EPI_SCALE, nullptr, 0, w->col_scale, b.n1w, b.n1b);
+    } else if (b.ss_hidden == 0 && gemm_ln_fits(M, e, cells, e, b.in_w)) {
+        gemm(s, M, e, e, cells, e, b.in_w, b.in_b, q, e, EPI_SCALE, nullptr, 0, b.n1w, b.n1b, w->col_scale);
     } else {
         layer_norm(s, M, e, cells, e, b.n1w, b.n1b, t, e);
         gemm(s, M, e, e, t, e, b.in_w, b.in_b, q, e, EPI_NONE, nullptr, 0);
@@ -688,11 +706,22 @@ void column_block(hipStream_t s, const tah_weights *w, const DevBlock &b, float 
     feed_forward(s, M, cells, b, t, mid);
 }
 
+// The attention buffer of the column stage: the cells' attention outputs, or, for a single table row's cells where a
+// block takes the fused column block (k_cell_block: a workgroup per feature group, rather than one per 128 cells of
+// the separate kernels), its key/value images if larger. From 250 rows on the images fit anyway; in between the
+// separate kernels measured faster (64 rows).
+static size_t column_att_floats(const tah_weights *w, size_t M, int features) {
+    bool fused = false;
+    for (auto &b : w->col_a2) fused = fused || (cell_block_fits(b) && w->inds == 128);
+    if (!fused || M > (size_t)SMALL_ROWS) return M * w->e;
+    return std::max(M * w->e, (cell_block_work_bytes(features) + 255) / 256 * 64);
+}
+
 size_t column_stage_floats(const tah_weights *w, int n, int features, int digits) {
     int ff = 0;
     for (auto &b : w->col_a2) ff = std::max(ff, b.ff);
     const size_t M = (size_t)n * features;
-    return M * (4 * (size_t)w->e + ff) + (digits > 1 ? 2 * M * w->e : 0);
+    return M * (3 * (size_t)w->e + ff) + column_att_floats(w, M, features) + (digits > 1 ? 2 * M * w->e : 0);
 }
 
 // The column stage at prediction for n rows x [n][features] (device): cells [n * features][e] after the stage.
@@ -703,13 +732,15 @@ void column_stage(hipStream_t s, const tah_weights *w, const float *col_kv, int 
     int ff = 0;
     for (auto &b : w->col_a2) ff = std::max(ff, b.ff);
     const size_t M = (size_t)n * features;
-    float *t = scratch, *q = t + M * e, *att = q + M * e, *mid = att + M * e;
+    const size_t natt = column_att_floats(w, M, features);
+    float *t = scratch, *q = t + M * e, *att = q + M * e, *mid = att + natt;
     float *plain = mid + M * ff, *sum = plain + M * e;
     const size_t per = 2 * (size_t)e * w->inds, gstride = (size_t)digits * nb * per;
     input_cells(s, w, x, n, features, cells);
     if (digits == 1) {
         for (int bi = 0; bi < nb; bi++)
-            column_block(s, w, w->col_a2[bi], cells, n, features, features, 1, col_kv + bi * per, gstride, t, q, att, mid);
+            column_block(s, w, w->col_a2[bi], cells, n, features, features, 1, col_kv + bi * per, gstride, t, q, att,
+                         natt * sizeof(float), mid);
         return;
     }
     const size_t count = M * e;
@@ -719,7 +750,7 @@ void column_stage(hipStream_t s, const tah_weights *w, const float *col_kv, int 
         if (dg > 0) TAH_HIP(hipMemcpyAsync(cells, plain, count * sizeof(float), hipMemcpyDeviceToDevice, s));
         for (int bi = 0; bi < nb; bi++)
             column_block(s, w, w->col_a2[bi], cells, n, features, features, 1, col_kv + ((size_t)dg * nb + bi) * per, gstride,
-                         t, q, att, mid);
+                         t, q, att, natt * sizeof(float), mid);
         hipLaunchKernelGGL(k_accumulate, blocks_for(count), dim3(256), 0, s, count, cells, sum);
         TAH_LAUNCHED();
     }
@@ -763,7 +794,7 @@ void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, co
     };
     for (int bi = 0; bi <= last; bi++) {
         const DevBlock &b = w->row[bi];
-        if (bi < last && fused && row_block_fits(b, T)) {
+        if (bi < last && fused && row_block_fits(b, T) && n >= ROW_BLOCK_MIN) {
             // keys and values by the projection (its second and third 128-row blocks), then the attention half of
             // the block in one kernel; qkv holds [R][2 e]
             rows128(s, (int)R, 2 * e, tok, e, b.inimg + (size_t)128 * e * 4, b.ins, b.in_b + e, qkv, 2 * e, EPI_NONE,
@@ -772,9 +803,11 @@ void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, co
             feed_forward(s, (int)R, tok, b, t, mid);
             continue;
         }
-        if (b.inimg) {
+        if (b.inimg && R > SMALL_ROWS) {
             rows128(s, (int)R, 3 * e, tok, e, b.inimg, b.ins, b.in_b, qkv, 3 * e, EPI_NONE, nullptr, 0, nullptr, b.n1w,
                     b.n1b);
+        } else if (gemm_ln_fits((int)R, e, tok, e, b.in_w)) {
+            gemm(s, (int)R, 3 * e, e, tok, e, b.in_w, b.in_b, qkv, 3 * e, EPI_NONE, nullptr, 0, b.n1w, b.n1b);
         } else {
             layer_norm(s, (int)R, e, tok, e, b.n1w, b.n1b, t, e);
             gemm(s, (int)R, 3 * e, e, t, e, b.in_w, b.in_b, qkv, 3 * e, EPI_NONE, nullptr, 0);

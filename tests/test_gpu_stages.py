@@ -80,14 +80,15 @@ def test_embed_with_label_digits_and_missing_cells(gpu, tiny_model):
     assert np.abs(got - want).max() < TOL
 
 
-@pytest.mark.parametrize("features", [100, 150])
-def test_stages_full_size(gpu, full_model, full_weights, features):
+@pytest.mark.parametrize("features,n", [(100, 24), (150, 24), (100, 1), (100, 130)])
+def test_stages_full_size(gpu, full_model, full_weights, features, n):
     """Full-size column stage (3 blocks, 8 x 16 heads, 128 inducing points per group) and row stage (104 or 154
-    tokens, RoPE) against the oracle, then all three stages with a stored in-context cache."""
-    say(f"stages full features={features}")
+    tokens, RoPE) against the oracle, then all three stages with a stored in-context cache. One row takes the
+    single-row routes (the fused column block over its key/value images, the f32 projections and feed-forward);
+    130 rows the fused row block."""
+    say(f"stages full features={features} n={n}")
     m = full_model
-    rng = np.random.default_rng(features)
-    n = 24
+    rng = np.random.default_rng(features + n)
     col_kv = (rng.standard_normal((features, 1, len(m.col_a2), 2, m.e, m.inds)) * 0.5).astype(np.float32)
     rows, chunk = 600, 256
     layers = []
@@ -99,7 +100,8 @@ def test_stages_full_size(gpu, full_model, full_weights, features):
     vm = gpu.load(full_weights, abi.KV_F32, rows, chunk, layers, scales)
     vm.set_columns(col_kv, features, 1)
     x = rng.standard_normal((n, features)).astype(np.float32)
-    x[2, :] = -100.0
+    if n > 2:
+        x[2, :] = -100.0
     fitted = orc.Fitted(rows, features, 10, chunk, abi.KV_F32, planmod.Plan([10], [planmod.Node(None, [], 10, True, list(range(10)))]),
                         col_kv, [scales], [layers])
     tok = gpu.embed(full_weights, vm, x)
