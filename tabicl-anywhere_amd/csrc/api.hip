@@ -586,9 +586,7 @@ static void stage_rows(tah_dev *dev, const tah_weights *w, const tah_model *mode
         const DevBlock &b = w->icl[l];
         // query: q = modulate(Wq norm1(h) + bq)  (src/nn.rs:130-152)
         const float *scale = model->scales + (size_t)l * d;
-        if (query_few_fits(b, nq, h, d)) {
-            query_few(s, nq, h, d, b, scale, q);
-        } else if (query_split_fits(b, nq, h, d, q)) {
+        if (query_split_fits(b, nq, h, d, q)) {
             query_split(s, nq, h, d, b, scale, q);
         } else {
             dense(s, nq, d, d, h, d, b.in_w, b.in_s.rows(0), b.in_b, q, d, EPI_NONE, nullptr, 0, b.n1w, b.n1b, t);

@@ -156,9 +156,6 @@ void layer_norm(hipStream_t s, int rows, int n, const float *x, int ldx, const f
 // In place on q [rows][d] (after the query projection): q *= scale (no scalable softmax), or per head
 // q_h *= scale_h * (1 + tanh(q2 gelu(q0 q_h + q0b) + q2b)). scratch holds rows * heads * ss_hidden floats.
 void query_modulate(hipStream_t s, int rows, const DevBlock &b, const float *scale, float *q, float *scratch);
-// q = modulate(Wq norm1(h) + bq) in one launch for at most eight rows (head width 64, query-MLP width 64)
-bool query_few_fits(const DevBlock &b, int rows, const float *h, int ldh);
-void query_few(hipStream_t s, int rows, const float *h, int ldh, const DevBlock &b, const float *scale, float *q);
 size_t query_scratch_floats(int rows, const DevBlock &b);
 // The whole query MLP in one kernel (gemm_split.hip), for head width 64 and hidden width 64 with images.
 bool qmlp_fused(const DevBlock &b);

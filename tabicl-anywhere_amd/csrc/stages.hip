@@ -706,22 +706,11 @@ void column_block(hipStream_t s, const tah_weights *w, const DevBlock &b, float 
     feed_forward(s, M, cells, b, t, mid);
 }
 
-// The attention buffer of the column stage: the cells' attention outputs, or, for a single table row's cells where a
-// block takes the fused column block (k_cell_block: a workgroup per feature group, rather than one per 128 cells of
-// the separate kernels), its key/value images if larger. From 250 rows on the images fit anyway; in between the
-// separate kernels measured faster (64 rows).
-static size_t column_att_floats(const tah_weights *w, size_t M, int features) {
-    bool fused = false;
-    for (auto &b : w->col_a2) fused = fused || (cell_block_fits(b) && w->inds == 128);
-    if (!fused || M > (size_t)SMALL_ROWS) return M * w->e;
-    return std::max(M * w->e, (cell_block_work_bytes(features) + 255) / 256 * 64);
-}
-
 size_t column_stage_floats(const tah_weights *w, int n, int features, int digits) {
     int ff = 0;
     for (auto &b : w->col_a2) ff = std::max(ff, b.ff);
     const size_t M = (size_t)n * features;
-    return M * (3 * (size_t)w->e + ff) + column_att_floats(w, M, features) + (digits > 1 ? 2 * M * w->e : 0);
+    return M * (4 * (size_t)w->e + ff) + (digits > 1 ? 2 * M * w->e : 0);
 }
 
 // The column stage at prediction for n rows x [n][features] (device): cells [n * features][e] after the stage.
@@ -732,7 +721,7 @@ void column_stage(hipStream_t s, const tah_weights *w, const float *col_kv, int 
     int ff = 0;
     for (auto &b : w->col_a2) ff = std::max(ff, b.ff);
     const size_t M = (size_t)n * features;
-    const size_t natt = column_att_floats(w, M, features);
+    const size_t natt = M * e;
     float *t = scratch, *q = t + M * e, *att = q + M * e, *mid = att + natt;
     float *plain = mid + M * ff, *sum = plain + M * e;
     const size_t per = 2 * (size_t)e * w->inds, gstride = (size_t)digits * nb * per;
