@@ -15,6 +15,8 @@ decoder 1024 -> 10). Synthetic table: X ~ N(0, 1) of 10,000 training + 2,048 tes
   each, so its ceiling is the dense fp16 MFMA peak (2.5 PFLOP/s) over three: 833 TFLOP/s of f32 work.
 * cpu_baseline: the oracle (the C restatement of the reference's CPU path) on this host's cores, predicting a
   bounded sample of the same test rows against the same caches; and a bounded fit sample timed on both.
+* regression_head: 2,048 rows x 8 members of 999 predicted quantiles read as distributions on the card (mean,
+  variance, median and six quantiles a row, tah_quantile_stats), and a sample of rows through the host statement.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 """
@@ -167,6 +169,24 @@ def main():
     achieved = flops / (att_ms / 1e3)
     log(f"attention, {BATCH} queries x {ROWS} keys x {heads} heads: {att_ms:.3f} ms, {achieved / 1e12:.1f} TFLOP/s")
 
+    # ---- the regression head: 2,048 rows x 8 members of 999 predicted quantiles read as distributions --------------
+    alphas = np.array([0.025, 0.1, 0.25, 0.75, 0.9, 0.975], np.float32)
+    rq, nqv = 8 * BATCH, 999
+    q_host = (rng.standard_normal((rq, nqv)) * 3.0 + 1.0).astype(np.float32)
+    qq_dev = dm.DeviceBuffer.of(q_host)
+    st_dev = dm.DeviceBuffer(rq * (3 + alphas.size) * 4)
+    gpu.quantile_stats_dev(qq_dev.ptr, rq, nqv, alphas, st_dev.ptr)
+    gpu.sync()
+    timer.start()
+    for _ in range(3):
+        gpu.quantile_stats_dev(qq_dev.ptr, rq, nqv, alphas, st_dev.ptr)
+    qs_ms = timer.stop() / 3
+    regression = {"rows": rq, "quantiles": nqv, "levels": int(alphas.size), "ms": round(qs_ms, 4),
+                  "rows_per_s": round(rq / (qs_ms / 1e3), 1)}
+    log(f"regression head, {rq} rows x {nqv} quantiles: {qs_ms:.3f} ms, {regression['rows_per_s']:,.0f} rows/s")
+    qq_dev.free()
+    st_dev.free()
+
     # a plain 256 MiB device-to-device copy: the known-size reference that the memory counters of a profile of
     # this run are scaled by (profiles/README.md)
     cal_a, cal_b = dm.DeviceBuffer(256 << 20), dm.DeviceBuffer(256 << 20)
@@ -203,6 +223,16 @@ def main():
         fit_sample = {"rows": fr, "features": FEATURES, "cpu_s": round(cpu_fit, 3), "gpu_s": round(gpu_fit, 4),
                       "cores": threads, "kind": "port"}
         log(f"fit sample {fr} x {FEATURES}: cpu {cpu_fit:.2f} s, card {gpu_fit:.3f} s")
+        tab = importlib.import_module("tabicl-anywhere_amd.table")
+        hs = 512
+        t0 = time.perf_counter()
+        for row in q_host[:hs]:
+            dd = tab.QuantileDist(row)
+            dd.mean(), dd.variance(), dd.icdf(0.5), [dd.icdf(a) for a in alphas]
+        host_s = time.perf_counter() - t0
+        regression["host_rows_per_s"] = round(hs / host_s, 1)
+        regression["host_sample"] = f"{hs} rows through the host statement (table.QuantileDist, numpy, one thread)"
+        log(f"regression head on the host: {regression['host_rows_per_s']:,.0f} rows/s")
 
     line = {
         "metric": "predicted rows/s at 10k x 100 cache (1/64/2048 rows); % roofline; fit s",
@@ -227,6 +257,7 @@ def main():
         "rows_per_s_by_cache": per_cache,
         "in_context_stage_ms": round(icl_ms, 4),
         "fit_s": round(fit_s, 4),
+        "regression_head": regression,
         "roofline": {"bound": "mfma", "achieved": round(achieved / 1e12, 2), "peak": round(PEAK_SPLIT_F32 / 1e12, 1),
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_SPLIT_F32, 4), "traffic": TRAFFIC_BYTES,
                      "kernel": "k_attn_split64 (+ split merge)", "ms_per_launch": round(att_ms, 4),

@@ -195,6 +195,20 @@ typedef int (*tah_layer_sink)(void *ctx, int32_t layer, const uint8_t *records, 
 int tah_in_context(tah_dev *dev, const tah_weights *w, const float *h, int32_t rows, const float *scales,
                    int32_t kv_format, int32_t chunk, tah_layer_sink sink, void *ctx);
 
+/* ---- the regression head: QuantileDist (src/table.rs:292-346) ---------------------------------------------------
+ *
+ * A regression member's output rows read as distributions, as the reference reads each row on the host
+ * (QuantileDist::new, mean, variance and icdf, applied per row at src/table.rs:479-486): q [rows][n] predicted
+ * quantiles (n from 2 to 1024: the model's 999), alphas [n_alphas] (at most 64) the requested levels; writes
+ * stats [rows][3 + n_alphas]: mean, sample variance, median (icdf at 0.5), then the icdf at each alpha, in f32,
+ * summed in the reference's order (the tails beyond the first and last level through the device's logf). The
+ * member average in f64 and the mapping back to the target's units stay with the caller (src/table.rs:481-494). */
+int tah_quantile_stats(tah_dev *dev, const float *q, int32_t rows, int32_t n, const float *alphas,
+                       int32_t n_alphas, float *stats);
+/* The same with q and stats in device memory (alphas on the host); ordered on the library's stream. */
+int tah_quantile_stats_dev(tah_dev *dev, const float *q_dev, int32_t rows, int32_t n, const float *alphas,
+                           int32_t n_alphas, float *stats_dev);
+
 #ifdef __cplusplus
 }
 #endif

@@ -112,6 +112,10 @@ SIGNATURES = {
                                   ctypes.c_int32, F32P]),
     "tah_in_context": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, F32P, ctypes.c_int32, F32P, ctypes.c_int32,
                                       ctypes.c_int32, LAYER_SINK, ctypes.c_void_p]),
+    "tah_quantile_stats": (ctypes.c_int, [ctypes.c_void_p, F32P, ctypes.c_int32, ctypes.c_int32, F32P,
+                                          ctypes.c_int32, F32P]),
+    "tah_quantile_stats_dev": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, F32P,
+                                              ctypes.c_int32, ctypes.c_void_p]),
 }
 
 

@@ -684,6 +684,48 @@ extern "C" int tah_attend(tah_dev *dev, const float *q, const float *kv, int32_t
     });
 }
 
+// ---- the regression head --------------------------------------------------------------------------------------
+static void check_quantiles(int rows, int n, const float *alphas, int na) {
+    if (rows < 0 || n < 2 || n > 1024 || na < 0 || na > 64 || (na > 0 && !alphas))
+        throw ArgError{"quantile_stats: 2 to 1024 quantiles a row and at most 64 levels"};
+}
+
+extern "C" int tah_quantile_stats_dev(tah_dev *dev, const float *q_dev, int32_t rows, int32_t n, const float *alphas,
+                                      int32_t n_alphas, float *stats_dev) {
+    if (!q_dev || !stats_dev) return TAH_E_ARG;
+    return guarded(dev, [&] {
+        check_quantiles(rows, n, alphas, n_alphas);
+        if (rows == 0) return TAH_OK;
+        Loans loans(dev);
+        float *ad = loans.take<float>(std::max(n_alphas, 1));
+        if (n_alphas)
+            TAH_HIP(hipMemcpyAsync(ad, alphas, sizeof(float) * n_alphas, hipMemcpyHostToDevice, dev->stream));
+        quantile_stats(dev->stream, rows, n, q_dev, n_alphas, ad, stats_dev);
+        // the alphas' staging buffer goes back to the pool only once the copy from the caller's memory is done
+        TAH_HIP(hipStreamSynchronize(dev->stream));
+        return TAH_OK;
+    });
+}
+
+extern "C" int tah_quantile_stats(tah_dev *dev, const float *q, int32_t rows, int32_t n, const float *alphas,
+                                  int32_t n_alphas, float *stats) {
+    if (!q || !stats) return TAH_E_ARG;
+    return guarded(dev, [&] {
+        check_quantiles(rows, n, alphas, n_alphas);
+        if (rows == 0) return TAH_OK;
+        Loans loans(dev);
+        const size_t nin = (size_t)rows * n, nout = (size_t)rows * (3 + n_alphas);
+        float *qd = loans.take<float>(nin), *sd = loans.take<float>(nout), *ad = loans.take<float>(std::max(n_alphas, 1));
+        TAH_HIP(hipMemcpyAsync(qd, q, sizeof(float) * nin, hipMemcpyHostToDevice, dev->stream));
+        if (n_alphas)
+            TAH_HIP(hipMemcpyAsync(ad, alphas, sizeof(float) * n_alphas, hipMemcpyHostToDevice, dev->stream));
+        quantile_stats(dev->stream, rows, n, qd, n_alphas, ad, sd);
+        TAH_HIP(hipMemcpyAsync(stats, sd, sizeof(float) * nout, hipMemcpyDeviceToHost, dev->stream));
+        TAH_HIP(hipStreamSynchronize(dev->stream));
+        return TAH_OK;
+    });
+}
+
 // Pinned host staging for records on their way to the sink.
 struct Pinned {
     void *p = nullptr;

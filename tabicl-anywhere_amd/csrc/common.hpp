@@ -222,6 +222,10 @@ void kv_images(hipStream_t s, int rows, int chunk, int d, int heads, int kv_form
 void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t *records, float *out, void *work,
                const KvImages *img = nullptr);
 
+// The regression head (quantiles.hip): per row of q [rows][n], mean, variance, median and icdf at alphas [na]
+// (device) into stats [rows][3 + na].
+void quantile_stats(hipStream_t s, int rows, int n, const float *q, int na, const float *alphas, float *stats);
+
 // Column and row stages (stages.hip).
 void input_cells(hipStream_t s, const tah_weights *w, const float *x, int n, int features, float *cells);
 size_t column_stage_floats(const tah_weights *w, int n, int features, int digits);

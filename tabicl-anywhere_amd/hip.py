@@ -160,6 +160,25 @@ class Gpu:
                                                  ctypes.c_void_p(out_ptr)))
 
     # ---- fitting: fit::Attend (src/fit.rs:45-74) ---------------------------------------------------------------
+    def quantile_stats(self, q, alphas) -> np.ndarray:
+        """Per row of a regression member's outputs `q` ([rows][n] predicted quantiles), the row read as a
+        distribution (`QuantileDist`, `src/table.rs:292-346`): [rows][3 + len(alphas)] float32 holding the mean, the
+        sample variance, the median and the quantiles at `alphas`."""
+        q = _f32(q)
+        if q.ndim != 2:
+            raise ValueError("quantile_stats: q must be [rows][n]")
+        a = _f32(np.asarray(alphas, np.float32).reshape(-1))
+        out = np.empty((q.shape[0], 3 + a.size), np.float32)
+        self._check(self._l.tah_quantile_stats(self._h, _fp(q), int(q.shape[0]), int(q.shape[1]), _fp(a), int(a.size),
+                                               _fp(out)))
+        return out
+
+    def quantile_stats_dev(self, q_ptr: int, rows: int, n: int, alphas, out_ptr: int) -> None:
+        """`quantile_stats` with q ([rows][n]) and the output ([rows][3 + len(alphas)]) in device memory."""
+        a = _f32(np.asarray(alphas, np.float32).reshape(-1))
+        self._check(self._l.tah_quantile_stats_dev(self._h, ctypes.c_void_p(q_ptr), int(rows), int(n), _fp(a),
+                                                   int(a.size), ctypes.c_void_p(out_ptr)))
+
     def pack(self, c, d: int, rc: int, kv_format: int) -> np.ndarray:
         """One stored chunk record from its f32 keys and values `c` ([2d][rc]), quantised on the card."""
         c = _f32(c).reshape(-1)

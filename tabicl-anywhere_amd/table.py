@@ -44,23 +44,38 @@ def finish_proba(sums: np.ndarray, members: int, temperature: float) -> np.ndarr
     return out / out.sum(axis=1, keepdims=True)
 
 
+def _seq_sum(a) -> np.float32:
+    """A float32 sum left to right, the order of Rust's `iter().sum::<f32>()`."""
+    a = np.asarray(a, np.float32)
+    return np.add.accumulate(a, dtype=np.float32)[-1] if a.size else np.float32(0.0)
+
+
+def _total_sort(q) -> np.ndarray:
+    """Sorted by the total order of float32 (`f32::total_cmp`: -0 before +0, NaNs by sign at the ends)."""
+    q = np.asarray(q, np.float32)
+    u = q.view(np.uint32)
+    key = u ^ np.where(u >> 31 != 0, np.uint32(0xFFFFFFFF), np.uint32(0x80000000))
+    return q[np.argsort(key, kind="stable")]
+
+
 class QuantileDist:
     """`src/table.rs:292-346`: sorted quantiles at levels i/(n+1), linear between them, exponential tails fitted by
-    least squares to the first and last k = clamp(n/4, 1, 20) points, all in float32."""
+    least squares to the first and last k = clamp(n/4, 1, 20) points, all in float32 with the reference's left-to-right
+    sums."""
 
     def __init__(self, q):
         f = np.float32
-        q = np.sort(np.asarray(q, f))
+        q = _total_sort(q)
         n = q.size
         self.q = q
         self.levels = (np.arange(1, n + 1, dtype=f) / f(n + 1)).astype(f)
         k = max(min(20, n // 4), 1)
 
         def slope(xs, ys):
-            mx = f(np.sum(xs, dtype=f) / f(k))
-            my = f(np.sum(ys, dtype=f) / f(k))
-            cov = f(np.sum((xs - mx) * (ys - my), dtype=f) / f(k))
-            var = f(np.sum((xs - mx) * (xs - mx), dtype=f) / f(k))
+            mx = f(_seq_sum(xs) / f(k))
+            my = f(_seq_sum(ys) / f(k))
+            cov = f(_seq_sum((xs - mx) * (ys - my)) / f(k))
+            var = f(_seq_sum((xs - mx) * (xs - mx)) / f(k))
             return f(min(max(abs(cov / max(var, f(1e-6))), f(0.01)), f(100.0)))
 
         ln_l = np.log(np.maximum(self.levels[:k], f(1e-6))).astype(f)
@@ -70,11 +85,11 @@ class QuantileDist:
         self.tail_r = (f(-br), f(q[n - 1] + br * np.log(f(1.0) - min(self.levels[n - 1], f(1.0 - 1e-6)))))
 
     def mean(self) -> np.float32:
-        return np.float32(np.sum(self.q, dtype=np.float32) / np.float32(self.q.size))
+        return np.float32(_seq_sum(self.q) / np.float32(self.q.size))
 
     def variance(self) -> np.float32:
         m = self.mean()
-        return np.float32(np.sum((self.q - m) * (self.q - m), dtype=np.float32) / np.float32(self.q.size - 1))
+        return np.float32(_seq_sum((self.q - m) * (self.q - m)) / np.float32(self.q.size - 1))
 
     def icdf(self, alpha) -> np.float32:
         f = np.float32
@@ -93,9 +108,18 @@ class QuantileDist:
         return f(self.q[i] + t * (self.q[i + 1] - self.q[i]))
 
 
-def add_regression(out: dict, outputs: np.ndarray, alphas, target_mean: float, target_scale: float) -> None:
+def add_regression(out: dict, outputs: np.ndarray, alphas, target_mean: float, target_scale: float,
+                   gpu=None) -> None:
     """One member's contribution to `Regression` (`src/table.rs:472-490`): per row, the quantile distribution's
-    mean, variance, median and quantiles at `alphas`, mapped back to the target's units, added in float64."""
+    mean, variance, median and quantiles at `alphas`, mapped back to the target's units, added in float64. With a
+    card (`hip.Gpu`), the rows are read as distributions there (`tah_quantile_stats`), all at once."""
+    if gpu is not None:
+        st = gpu.quantile_stats(outputs, alphas).astype(np.float64) * target_scale + target_mean
+        out["mean"] += st[:, 0]
+        out["variance"] += st[:, 1]
+        out["median"] += st[:, 2]
+        out["quantiles"] += st[:, 3:]
+        return
     back = lambda v: float(v) * target_scale + target_mean
     for r, row in enumerate(np.asarray(outputs, np.float32)):
         d = QuantileDist(row)
