@@ -324,7 +324,7 @@ static void launch(hipStream_t s, int M, int N, int K, const float *X, int ldx, 
         dim3 grid((N + 15) / 16, (M + 15) / 16);
         hipLaunchKernelGGL((k_gemm_skinny<EPI, true>), grid, dim3(256), 0, s, M, N, K, X, ldx, W, b, Y, ldy, ea, lnw,
                            lnb);
-    } else if (aligned && M <= 256) {
+    } else if (aligned && (M <= 256 || N <= 32)) {  // few rows, or few columns (the decoder's last layer)
         dim3 grid((N + 15) / 16, (M + 15) / 16);
         hipLaunchKernelGGL((k_gemm_skinny<EPI, false>), grid, dim3(256), 0, s, M, N, K, X, ldx, W, b, Y, ldy, ea,
                            nullptr, nullptr);
