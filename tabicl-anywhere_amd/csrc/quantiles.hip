@@ -27,6 +27,11 @@ __device__ __forceinline__ float from_total_order_key(uint32_t k) {
     return __uint_as_float((k >> 31) ? (k ^ 0x80000000u) : ~k);
 }
 
+// f32::clamp: NaN stays NaN (fminf/fmaxf alone would return a bound)
+__device__ __forceinline__ float clamp_keep_nan(float x, float lo, float hi) {
+    return x != x ? x : fminf(fmaxf(x, lo), hi);
+}
+
 // (a, b) least-squares slope of ys on xs over k points, |.| clamped to [0.01, 100] (src/table.rs:305-310)
 __device__ float tail_slope(const float *xs, const float *ys, int k) {
 #pragma clang fp contract(off)
@@ -38,7 +43,7 @@ __device__ float tail_slope(const float *xs, const float *ys, int k) {
     for (int i = 0; i < k; i++) c += (xs[i] - mx) * (ys[i] - my);
     for (int i = 0; i < k; i++) v += (xs[i] - mx) * (xs[i] - mx);
     const float cov = c / (float)k, var = v / (float)k;
-    return fminf(fmaxf(fabsf(cov / fmaxf(var, 1e-6f)), 0.01f), 100.0f);
+    return clamp_keep_nan(fabsf(cov / fmaxf(var, 1e-6f)), 0.01f, 100.0f);
 }
 
 __device__ __forceinline__ float level(int i, int n) { return (float)(i + 1) / (float)(n + 1); }
@@ -112,7 +117,7 @@ __global__ __launch_bounds__(256) void k_quantile_stats(int n, const float *__re
             else hi = mid;
         }
         const int i = min(max(lo - 1, 0), n - 2);
-        const float t = fminf(fmaxf((alpha - level(i, n)) / fmaxf(level(i + 1, n) - level(i, n), 1e-6f), 0.0f), 1.0f);
+        const float t = clamp_keep_nan((alpha - level(i, n)) / fmaxf(level(i + 1, n) - level(i, n), 1e-6f), 0.0f, 1.0f);
         y = qs[i] + t * (qs[i + 1] - qs[i]);
     }
     out[2 + tid] = y;

@@ -51,6 +51,9 @@ def rows_of(rng, rows, n):
     q[2, 1::3] = -0.0                               # signed zeros, ordered -0 before +0
     q[3] *= np.float32(1e6)                         # large magnitudes
     q[4] = np.sort(q[4])[::-1]                      # reversed
+    if rows > 6:
+        q[5, 7] = np.nan                            # a NaN: sorted last by total_cmp, the moments NaN
+        q[6, : max(1, n // 4)] = -np.inf            # infinities in the left tail
     return q
 
 
@@ -63,10 +66,13 @@ def test_quantile_stats_match_host(gpu, n, rows):
     want = host_stats(q, ALPHAS)
     lo, hi = np.float32(1) / np.float32(n + 1), np.float32(n) / np.float32(n + 1)
     inner = np.concatenate([[True, True, True], (ALPHAS >= lo) & (ALPHAS <= hi)])
-    assert np.array_equal(got[:, inner], want[:, inner]), np.abs(got[:, inner] - want[:, inner]).max()
+    assert np.array_equal(got[:, inner], want[:, inner], equal_nan=True)
     tail = ~inner
     if tail.any():
-        err = np.abs(got[:, tail] - want[:, tail]) / np.maximum(np.abs(want[:, tail]), 1.0)
+        gt, wt = got[:, tail], want[:, tail]
+        assert np.array_equal(np.isnan(gt), np.isnan(wt)) and np.array_equal(np.isinf(gt), np.isinf(wt))
+        ok = np.isfinite(wt)
+        err = np.abs(gt[ok] - wt[ok]) / np.maximum(np.abs(wt[ok]), 1.0)
         say("  tails worst relative", err.max())
         assert err.max() < 5e-5
 
@@ -98,5 +104,5 @@ def test_add_regression_card_matches_host(gpu):
     T.add_regression(a, q, ALPHAS, 2.5, 0.75, gpu=gpu)
     T.add_regression(b, q, ALPHAS, 2.5, 0.75)
     for k in ("mean", "variance", "median"):
-        assert np.array_equal(a[k], b[k])
-    assert np.allclose(a["quantiles"], b["quantiles"], rtol=5e-5, atol=5e-5)
+        assert np.array_equal(a[k], b[k], equal_nan=True)
+    assert np.allclose(a["quantiles"], b["quantiles"], rtol=5e-5, atol=5e-5, equal_nan=True)
