@@ -151,6 +151,10 @@ extern "C" void tah_close(tah_dev *dev) {
         if (dev->stream) (void)hipStreamSynchronize(dev->stream);
         for (auto &b : dev->pool.bufs) (void)hipFree(b.p);
         dev->pool.bufs.clear();
+        for (int i = 0; i < 2; i++) {
+            if (dev->pinned[i]) (void)hipHostFree(dev->pinned[i]);
+            if (dev->copied[i]) (void)hipEventDestroy(dev->copied[i]);
+        }
         if (dev->stream) (void)hipStreamDestroy(dev->stream);
     }
     delete dev;
@@ -726,13 +730,19 @@ extern "C" int tah_quantile_stats(tah_dev *dev, const float *q, int32_t rows, in
     });
 }
 
-// Pinned host staging for records on their way to the sink.
-struct Pinned {
-    void *p = nullptr;
-    ~Pinned() {
-        if (p) (void)hipHostFree(p);
+// The device's two pinned staging buffers for records on their way to a sink, at least `bytes` each.
+static void staging(tah_dev *dev, size_t bytes) {
+    for (int i = 0; i < 2; i++)
+        if (!dev->copied[i]) TAH_HIP(hipEventCreateWithFlags(&dev->copied[i], hipEventDisableTiming));
+    if (dev->pinned_bytes >= bytes) return;
+    for (int i = 0; i < 2; i++) {
+        if (dev->pinned[i]) TAH_HIP(hipHostFree(dev->pinned[i]));
+        dev->pinned[i] = nullptr;
     }
-};
+    dev->pinned_bytes = 0;
+    for (int i = 0; i < 2; i++) TAH_HIP(hipHostMalloc(&dev->pinned[i], bytes, hipHostMallocDefault));
+    dev->pinned_bytes = bytes;
+}
 
 extern "C" int tah_in_context(tah_dev *dev, const tah_weights *w, const float *h_host, int32_t rows, const float *scales,
                               int32_t kv_format, int32_t chunk, tah_layer_sink sink, void *ctx) {
@@ -755,8 +765,7 @@ extern "C" int tah_in_context(tah_dev *dev, const tah_weights *w, const float *h
         const bool use_img = rows >= 32 && kv_images_apply(TAH_KV_F32, d, w->icl_heads);
         if (use_img)
             img = kv_images_at(loans.take<uint8_t>(kv_images_bytes(rows, chunk, w->icl_heads)), rows, chunk, w->icl_heads);
-        Pinned host;
-        TAH_HIP(hipHostMalloc(&host.p, lbytes, hipHostMallocDefault));
+        staging(dev, lbytes);
         TAH_HIP(hipMemcpyAsync(h, h_host, n * sizeof(float), hipMemcpyHostToDevice, s));
         TAH_HIP(hipMemcpyAsync(sc, scales, sizeof(float) * L * d, hipMemcpyHostToDevice, s));
         for (int l = 0; l < L; l++) {
@@ -771,7 +780,9 @@ extern "C" int tah_in_context(tah_dev *dev, const tah_weights *w, const float *h
                 pack(s, rows, d, chunk, kv_format, rec32, recq);
                 stored = recq;
             }
-            TAH_HIP(hipMemcpyAsync(host.p, stored, lbytes, hipMemcpyDeviceToHost, s));
+            // layer l's records into staging buffer l % 2 (the sink read layer l - 2's there before this was queued)
+            TAH_HIP(hipMemcpyAsync(dev->pinned[l & 1], stored, lbytes, hipMemcpyDeviceToHost, s));
+            TAH_HIP(hipEventRecord(dev->copied[l & 1], s));
             const bool last = l + 1 == L;
             if (!last) {
                 // every row attends to all rows over the exact keys and values, then the rest of the block
@@ -786,11 +797,21 @@ extern "C" int tah_in_context(tah_dev *dev, const tah_weights *w, const float *h
                 dense(s, rows, b.ff, d, t, d, b.l1w, b.l1_s, b.l1b, mid, b.ff, EPI_GELU, nullptr, 0);
                 dense(s, rows, d, b.ff, mid, b.ff, b.l2w, b.l2_s, b.l2b, h, d, EPI_RESID, h, d);
             }
-            // the layer's records reached the host before the next layer's keys overwrite rec32
-            TAH_HIP(hipStreamSynchronize(s));
-            const int rc = sink(ctx, l, static_cast<const uint8_t *>(host.p), lbytes);
-            if (rc != 0) throw SinkError{rc};
+            // the card works on layer l (queued above) while the sink takes layer l - 1's records; on the stream the
+            // copy of layer l's records runs before layer l + 1's keys overwrite rec32
+            if (l > 0) {
+                TAH_HIP(hipEventSynchronize(dev->copied[(l - 1) & 1]));
+                const int rc = sink(ctx, l - 1, static_cast<const uint8_t *>(dev->pinned[(l - 1) & 1]), lbytes);
+                if (rc != 0) {
+                    TAH_HIP(hipStreamSynchronize(s));  // nothing queued is left touching the staging buffers
+                    throw SinkError{rc};
+                }
+            }
         }
+        TAH_HIP(hipEventSynchronize(dev->copied[(L - 1) & 1]));
+        const int rc = sink(ctx, L - 1, static_cast<const uint8_t *>(dev->pinned[(L - 1) & 1]), lbytes);
+        TAH_HIP(hipStreamSynchronize(s));
+        if (rc != 0) throw SinkError{rc};
         return TAH_OK;
     });
 }

@@ -60,6 +60,11 @@ struct Pool {
 struct tah_dev {
     int ordinal = 0;
     hipStream_t stream = nullptr;
+    // pinned host staging for records on their way to a layer sink: two buffers (one being filled by the card while
+    // the sink reads the other), kept between calls and grown as needed; two events marking their copies done
+    void *pinned[2] = {nullptr, nullptr};
+    size_t pinned_bytes = 0;
+    hipEvent_t copied[2] = {nullptr, nullptr};
     std::mutex lock;
     std::string last_error;
     std::string name;
