@@ -62,12 +62,9 @@ def query_scale(block, n: int) -> np.ndarray:
     logn = np.log(F(max(n, 1)))
     hid = gelu(block.t["b0w"] * logn + block.t["b0b"])
     w2 = block.t["b2w"].reshape(block.d, block.ss_hidden)
-    out = np.empty(block.d, F)
-    for o in range(block.d):  # sequential sums, as the reference's matvec rows
-        s = F(0.0)
-        for j in range(block.ss_hidden):
-            s = F(s + w2[o, j] * hid[j])
-        out[o] = s + block.t["b2b"][o]
+    # each row's sum left to right in float32, as the reference's matvec rows (accumulate is sequential)
+    s = np.add.accumulate((w2 * hid[None, :]).astype(F), axis=1, dtype=F)[:, -1]
+    out = (s + block.t["b2b"]).astype(F)
     return (out * inv).astype(F)
 
 
