@@ -115,8 +115,12 @@ def fit_raw(gpu, weights, x, y, classes: int, chunk: int = 256, kv_format: int =
     fitted = Fitted(rows, features, classes, chunk, kv_format, plan, col_kv)
     for node in plan.nodes:
         n_rows = rows if node.rows is None else len(node.rows)
-        h = reps if node.rows is None else reps[np.asarray(node.rows, np.int64)]
-        h = np.array(h, F, copy=True)
+        if node.rows is not None:
+            h = reps[np.asarray(node.rows, np.int64)]  # a copy
+        elif len(plan.nodes) == 1:
+            h = reps  # no other problem reads the representations
+        else:
+            h = reps.copy()
         m.add_y(m.t["icl_y"], np.asarray(node.y, F), h)
         scales = np.stack([query_scale(b, n_rows) for b in m.icl]).astype(F)
         layers = []

@@ -251,8 +251,13 @@ class Model:
     def add_y(self, table: np.ndarray, y: np.ndarray, cells: np.ndarray) -> None:
         """`Model::add_y` (`src/model.rs:188-200`) for many rows: `cells [rows][w] += embedding(y)`."""
         w = cells.shape[-1]
+        # in blocks of rows, so that the gathered embeddings stay small and cached instead of a fresh array as
+        # large as the cells
         if self.max_classes > 0:
-            cells += table.reshape(-1, w)[y.astype(np.int64)]
+            tw, idx = table.reshape(-1, w), y.reshape(-1).astype(np.intp)
+            for i in range(0, len(cells), 512):
+                cells[i:i + 512] += tw[idx[i:i + 512]]
         else:
-            tw = table.reshape(2, w)
-            cells += tw[0][None, :] * y.astype(np.float32)[:, None] + tw[1][None, :]
+            tw, yv = table.reshape(2, w), y.reshape(-1).astype(np.float32)
+            for i in range(0, len(cells), 512):
+                cells[i:i + 512] += tw[0][None, :] * yv[i:i + 512, None] + tw[1][None, :]
