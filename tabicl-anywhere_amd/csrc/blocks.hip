@@ -13,8 +13,11 @@
 //  * the weights stream through two 32 KB LDS buffers, one slice per step, copied global -> LDS by DMA
 //    (global_load_lds_dwordx4) and shared by the workgroup's four wavefronts. They are stored pre-split at upload
 //    in exactly the order of those slices (weight_image in the C ABI: blocks of 128 rows, then 16-column steps);
-//  * the first product runs in two halves of 128 hidden units, each finished (bias, GELU, split) before the next,
-//    so that at most 64 accumulators and half the hidden layer are live at once;
+//  * the first product runs in two halves of 128 hidden units, and each product's matrix work overlaps the vector
+//    work of the half before it: half 1's products under half 0's bias, GELU and split, then the second product's
+//    sums over half 0 under half 1's (the vector work is as long as the matrix work here; run one after the other,
+//    the matrix cores idle through it);
+//  * the first layer's bias is staged in LDS, so that the reads next to the GELU wait for LDS, not for the caches;
 //  * layer normalisation needs each row's sums: a row's 128 values sit on lanes l and l + 32, so one cross-lane step;
 //  * each row is scaled by its own power of two before splitting (its largest magnitude below 2^14; each half of
 //    the hidden layer by its own), the weights by one per matrix; the products are unscaled in the epilogues.
@@ -45,11 +48,13 @@ __global__ __launch_bounds__(64 * FFW, 2) void k_ff128(int M, float *__restrict_
                                                    int s2) {
     constexpr int E = 128;
     __shared__ __align__(16) uint8_t slab[2][SLAB];
+    __shared__ __align__(16) float bias1[256];  // b1, read next to the GELU it feeds (an LDS read's short wait)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r32 = lane & 31, g = lane >> 5;
     const int m = blockIdx.x * 32 * FFW + wave * 32 + r32;
     const bool live = m < M;
     dma_to_lds<64 * FFW>(w1img, slab[0], SLAB, tid);
+    if (tid < 64) reinterpret_cast<float4 *>(bias1)[tid] = reinterpret_cast<const float4 *>(b1)[tid];
 
     // this lane's half of row m: columns 16 ks + 8 g + t
     float xv[8][8];
@@ -111,93 +116,101 @@ __global__ __launch_bounds__(64 * FFW, 2) void k_ff128(int M, float *__restrict_
         return j < 2 * NSL ? w1img + (size_t)j * SLAB : w2img + (size_t)(j - 2 * NSL) * SLAB;
     };
     halfx8 hh8[16], hl8[16];  // the hidden layer, split: 16-unit step k = 2 T + hh of half 0, then of half 1
-    int shd[2];
+    static_assert(NSL == 2, "two slices a 128-row weight block: two tiles of the other half activated a slice");
+
+    // wait for slice j (and free slice j - 1's buffer), start slice j + 1's copy; slice j in LDS
+    auto next = [&](int j) {
+        __builtin_amdgcn_s_waitcnt(0);  // this wavefront's copies of slice j have landed
+        __syncthreads();                // everyone's have; slice j - 1's buffer is free
+        if (j + 1 < 4 * NSL) dma_to_lds<64 * FFW>(slice(j + 1), slab[(j + 1) & 1], SLAB, tid);
+        return static_cast<const uint8_t *>(slab[j & 1]);
+    };
+    // acc[T] += (rows 32 T .. 32 T + 31 of the slice's weights) B over the slice's CPS 16-column steps
+    auto mma = [&](floatx16 (&acc)[4], const uint8_t *sl, const halfx8 *bh, const halfx8 *bl, int rows) {
 #pragma unroll
-    for (int half = 0; half < 2; half++) {
-        floatx16 acc[4];
+        for (int c = 0; c < CPS; c++)
 #pragma unroll
-        for (int T = 0; T < 4; T++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) acc[T][v] = 0.0f;
-#pragma unroll
-        for (int st = 0; st < NSL; st++) {
-            const int j = NSL * half + st;
-            __builtin_amdgcn_s_waitcnt(0);  // this wavefront's copies of slice j have landed
-            __syncthreads();                // everyone's have; slice j - 1's buffer is free
-            dma_to_lds<64 * FFW>(slice(j + 1), slab[(j + 1) & 1], SLAB, tid);
-            const uint8_t *sl = slab[j & 1];
-#pragma unroll
-            for (int c = 0; c < CPS; c++)
-#pragma unroll
-                for (int T = 0; T < 4; T++) {
-                    const int n = 32 * T + arow;
-                    const halfx8 ah = *reinterpret_cast<const halfx8 *>(sl + c * 8192 + (g * 128 + n) * 16);
-                    const halfx8 al = *reinterpret_cast<const halfx8 *>(sl + c * 8192 + ((2 + g) * 128 + n) * 16);
-                    acc[T] = mfma16x3(ah, al, xh[CPS * st + c], xl[CPS * st + c], acc[T]);
-                }
-        }
-        // hidden unit of accumulator v of tile T: 128 half + 32 T + 16 (v / 8) + 8 g + v % 8
-        const float u1 = ldexpf(1.0f, -(sx + s1));
-        float hmax = 0.0f;
-#pragma unroll
-        for (int T = 0; T < 4; T++)
-#pragma unroll
-            for (int hh = 0; hh < 2; hh++) {
-                const float *bp = b1 + 128 * half + 32 * T + 16 * hh + 8 * g;
-                const float4 ba = *reinterpret_cast<const float4 *>(bp), bb = *reinterpret_cast<const float4 *>(bp + 4);
-                const float bv[8] = {ba.x, ba.y, ba.z, ba.w, bb.x, bb.y, bb.z, bb.w};
-#pragma unroll
-                for (int t = 0; t < 8; t++) {
-                    const float hv = gelu(acc[T][8 * hh + t] * u1 + bv[t]);
-                    acc[T][8 * hh + t] = hv;
-                    hmax = fmaxf(hmax, fabsf(hv));
-                }
+            for (int T = 0; T < 4; T++) {
+                const int n = 32 * T + arow;
+                const halfx8 ah = *reinterpret_cast<const halfx8 *>(sl + c * 8192 + (g * rows + n) * 16);
+                const halfx8 al = *reinterpret_cast<const halfx8 *>(sl + c * 8192 + ((2 + g) * rows + n) * 16);
+                acc[T] = mfma16x3(ah, al, bh[c], bl[c], acc[T]);
             }
-        hmax = fmaxf(hmax, __shfl_xor(hmax, 32, 64));
-        shd[half] = shift_for_max(hmax);
+    };
+    // hidden unit of accumulator v of tile T of half h: 128 h + 32 T + 16 (v / 8) + 8 g + v % 8; bias and GELU in
+    // place, the running largest magnitude in mx
+    const float u1 = ldexpf(1.0f, -(sx + s1));
+    auto act = [&](floatx16 &a, int half, int T, float &mx) {
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const float *bp = bias1 + 128 * half + 32 * T + 16 * hh + 8 * g;
+            const float4 ba = *reinterpret_cast<const float4 *>(bp), bb = *reinterpret_cast<const float4 *>(bp + 4);
+            const float bv[8] = {ba.x, ba.y, ba.z, ba.w, bb.x, bb.y, bb.z, bb.w};
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const float hv = gelu(a[8 * hh + t] * u1 + bv[t]);
+                a[8 * hh + t] = hv;
+                mx = fmaxf(mx, fabsf(hv));
+            }
+        }
+    };
+    // a half of the hidden layer, activated, scaled by its own power of two and split into hh8 / hl8
+    auto split_half = [&](floatx16 (&a)[4], float mx, int half) {
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const int sh = shift_for_max(mx);
 #pragma unroll
         for (int T = 0; T < 4; T++)
 #pragma unroll
             for (int hh = 0; hh < 2; hh++) {
                 float hv[8];
 #pragma unroll
-                for (int t = 0; t < 8; t++) hv[t] = acc[T][8 * hh + t];
-                split8(hv, ldexpf(1.0f, shd[half]), hh8[8 * half + 2 * T + hh], hl8[8 * half + 2 * T + hh]);
+                for (int t = 0; t < 8; t++) hv[t] = a[T][8 * hh + t];
+                split8(hv, ldexpf(1.0f, sh), hh8[8 * half + 2 * T + hh], hl8[8 * half + 2 * T + hh]);
             }
-    }
+        return sh;
+    };
 
-    // Y^T = W2 H^T: 4 tiles of 32 outputs; slice 2 NSL + st = hidden units 16 CPS st .. 16 CPS (st + 1) - 1. The two
-    // halves of the hidden layer carry their own scales: between them the sums are rescaled (exactly) to the second.
-    floatx16 y[4];
+    // The four products run in slice order (W1's two halves, then W2's two halves of hidden units); each one's
+    // matrix work overlaps the vector work of the half before it: H^T half 1 = W1 X^T under GELU of half 0, and
+    // Y^T = W2 H^T over half 0 under GELU of half 1. Y's sums over the two halves carry the halves' own scales: between
+    // them they are rescaled (exactly) to the second's.
+    floatx16 acc0[4], acc1[4], y[4];
 #pragma unroll
     for (int T = 0; T < 4; T++)
 #pragma unroll
-        for (int v = 0; v < 16; v++) y[T][v] = 0.0f;
-#pragma unroll
-    for (int st = 0; st < 2 * NSL; st++) {
-        const int j = 2 * NSL + st;
-        if (st == NSL) {
-            const float r = ldexpf(1.0f, shd[1] - shd[0]);
-#pragma unroll
-            for (int T = 0; T < 4; T++) y[T] *= r;
+        for (int v = 0; v < 16; v++) {
+            acc0[T][v] = 0.0f;
+            acc1[T][v] = 0.0f;
+            y[T][v] = 0.0f;
         }
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (j + 1 < 4 * NSL) dma_to_lds<64 * FFW>(slice(j + 1), slab[(j + 1) & 1], SLAB, tid);
-        const uint8_t *sl = slab[j & 1];
 #pragma unroll
-        for (int c = 0; c < CPS; c++)
+    for (int st = 0; st < NSL; st++) mma(acc0, next(st), xh + CPS * st, xl + CPS * st, 128);
+    float m0 = 0.0f;
 #pragma unroll
-            for (int T = 0; T < 4; T++) {
-                const int n = 32 * T + arow;
-                const halfx8 ah = *reinterpret_cast<const halfx8 *>(sl + c * 8192 + (g * E + n) * 16);
-                const halfx8 al = *reinterpret_cast<const halfx8 *>(sl + c * 8192 + ((2 + g) * E + n) * 16);
-                y[T] = mfma16x3(ah, al, hh8[CPS * st + c], hl8[CPS * st + c], y[T]);
-            }
+    for (int st = 0; st < NSL; st++) {
+        mma(acc1, next(NSL + st), xh + CPS * st, xl + CPS * st, 128);
+        act(acc0[2 * st], 0, 2 * st, m0);
+        act(acc0[2 * st + 1], 0, 2 * st + 1, m0);
     }
+    const int sh0 = split_half(acc0, m0, 0);
+    float m1 = 0.0f;
+#pragma unroll
+    for (int st = 0; st < NSL; st++) {
+        mma(y, next(2 * NSL + st), hh8 + CPS * st, hl8 + CPS * st, E);
+        act(acc1[2 * st], 1, 2 * st, m1);
+        act(acc1[2 * st + 1], 1, 2 * st + 1, m1);
+    }
+    const int sh1 = split_half(acc1, m1, 1);
+    {
+        const float r = ldexpf(1.0f, sh1 - sh0);
+#pragma unroll
+        for (int T = 0; T < 4; T++) y[T] *= r;
+    }
+#pragma unroll
+    for (int st = 0; st < NSL; st++) mma(y, next(3 * NSL + st), hh8 + 8 + CPS * st, hl8 + 8 + CPS * st, E);
     if (!live) return;
     // output column of accumulator v of tile T: 32 T + 16 (v / 8) + 8 g + v % 8; x += y + b2
-    const float u2 = ldexpf(1.0f, -(shd[1] + s2));
+    const float u2 = ldexpf(1.0f, -(sh1 + s2));
 #pragma unroll
     for (int T = 0; T < 4; T++)
 #pragma unroll
