@@ -941,7 +941,7 @@ __global__ __launch_bounds__(256, 2) void k_row_block(int T, float *tok, const f
 #pragma unroll
         for (int v = 0; v < 16; v++) o[v] = 0.0f;
 #pragma unroll
-        for (int k2 = 0; k2 < 2; k2++) {  // (a half past T is all masked and adds nothing)
+        for (int k2 = 0; k2 < 2; k2++) {
             floatx16 sc[2];
             float mx = -INFINITY;
 #pragma unroll
@@ -975,12 +975,13 @@ __global__ __launch_bounds__(256, 2) void k_row_block(int T, float *tok, const f
             for (int j = 0; j < 2; j++)
 #pragma unroll
                 for (int hh = 0; hh < 2; hh++) {
+                    const int st = 4 * k2 + 2 * j + hh;
+                    if (16 * st >= T) continue;  // keys 16 st .. 16 st + 15 all past the row's tokens: weights 0
                     float p[8];
 #pragma unroll
                     for (int t = 0; t < 8; t++) p[t] = exp2_hw(fmaf(sc[j][8 * hh + t], to_log2, off));
                     halfx8 ph, pl;
                     split8(p, 1.0f, ph, pl);
-                    const int st = 4 * k2 + 2 * j + hh;
                     const int rw = r32h ^ ((2 * st + gh) & 15);
                     const uint8_t *pad = (r32h & 11) == 0 ? ones : zero;
                     const _Float16 *vh = r32h < 16 ? Vh + ((st * 2 + gh) * 16 + rw) * 8
