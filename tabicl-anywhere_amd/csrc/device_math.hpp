@@ -71,16 +71,19 @@ __device__ __forceinline__ float tanh1(float x) {
 // GELU takes erf from A&S 7.1.26 at every argument: below |x| = 0.5 the reference's power series differs from it by
 // at most 1.5e-7 (the formula's absolute error bound), which moves x (1 + erf) / 2 by under 1e-7 there, and the
 // series and its selection cost as much as the formula itself (GELU is most of the feed-forward kernels' vector work).
+// With erf(z) = sign(z) (1 - q(|z|)), q = p(t) t e^(-z^2), the product x (1 + erf(x / sqrt 2)) / 2 is
+// max(x, 0) - |x| q / 2 for either sign of x: one fused multiply-add, with p's coefficients halved. |x| is taken of
+// min(x, FLT_MAX), so that +inf gives +inf (q is 0 there) while -inf and NaN give NaN, as the product form does.
 __device__ __forceinline__ float gelu(float x) {
-    const float z = x * 0.70710678118654752440f, a = fabsf(z);
-    const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * a);
-    float p = 1.0614054f;
-    p = p * t - 1.4531521f;
-    p = p * t + 1.4214138f;
-    p = p * t - 0.28449674f;
-    p = p * t + 0.2548296f;
-    const float erf = copysignf(1.0f - p * t * __builtin_amdgcn_exp2f(-a * a * LOG2E), z);
-    return 0.5f * x * (1.0f + erf);
+    const float a = fabsf(x);
+    const float t = __builtin_amdgcn_rcpf(fmaf(a, 0.3275911f * 0.70710678118654752440f, 1.0f));
+    float p = 0.5f * 1.0614054f;
+    p = p * t - 0.5f * 1.4531521f;
+    p = p * t + 0.5f * 1.4214138f;
+    p = p * t - 0.5f * 0.28449674f;
+    p = p * t + 0.5f * 0.2548296f;
+    const float q = p * t * __builtin_amdgcn_exp2f(x * x * (-0.5f * LOG2E));
+    return fmaf(-fabsf(fminf(x, 3.40282347e38f)), q, fmaxf(x, 0.0f));
 }
 
 // 2^x straight from v_exp_f32 (1 ulp): results below 2^-126, which only ever weight a softmax term, flush to 0
