@@ -735,6 +735,8 @@ static void staging(tah_dev *dev, size_t bytes) {
     for (int i = 0; i < 2; i++)
         if (!dev->copied[i]) TAH_HIP(hipEventCreateWithFlags(&dev->copied[i], hipEventDisableTiming));
     if (dev->pinned_bytes >= bytes) return;
+    // a call that failed part-way may have left copies into them queued
+    TAH_HIP(hipStreamSynchronize(dev->stream));
     for (int i = 0; i < 2; i++) {
         if (dev->pinned[i]) TAH_HIP(hipHostFree(dev->pinned[i]));
         dev->pinned[i] = nullptr;
