@@ -356,33 +356,39 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
         for (int v = 0; v < 16; v++) red[wave][T][v][lane] = acc[T][v] * u;
     __syncthreads();
     if (QM) {
-        static_assert(TN == 4, "the fused query MLP takes two whole heads per workgroup");
-        // wavefront w: tile w (rows r32, columns 32 w + 16 hh + 8 g + t of the workgroup's 128), bias added
+        static_assert(TN == 4 || TN == 2, "the fused query MLP takes whole heads (64 columns) per workgroup");
+        constexpr int LD = 32 * TN + 4;  // the tile's row pitch in LDS
+        // wavefront w: tile w of four (rows r32, columns 32 w + 16 hh + 8 g + t of the workgroup's), or half w % 2 of
+        // tile w / 2 of two; bias added
+        const int T = TN == 4 ? wave : wave >> 1;
         float yq[2][8];
 #pragma unroll
         for (int hh = 0; hh < 2; hh++) {
-            const int n0 = 32 * (nt0 + wave) + 16 * hh + 8 * g;
+            if (TN == 2 && hh != (wave & 1)) continue;
+            const int n0 = 32 * (nt0 + T) + 16 * hh + 8 * g;
 #pragma unroll
             for (int t = 0; t < 8; t++) {
                 const int v = 8 * hh + t;
-                yq[hh][t] = (((red[0][wave][v][lane] + red[1][wave][v][lane]) + red[2][wave][v][lane]) +
-                             red[3][wave][v][lane]) + b[n0 + t];
+                yq[hh][t] = (((red[0][T][v][lane] + red[1][T][v][lane]) + red[2][T][v][lane]) + red[3][T][v][lane]) +
+                            b[n0 + t];
             }
         }
-        __syncthreads();  // the partial sums are all read: their LDS holds the tile next, [32 rows][132]
+        __syncthreads();  // the partial sums are all read: their LDS holds the tile next, [32 rows][LD]
         float *qt = &red[0][0][0][0];
 #pragma unroll
-        for (int hh = 0; hh < 2; hh++)
+        for (int hh = 0; hh < 2; hh++) {
+            if (TN == 2 && hh != (wave & 1)) continue;
 #pragma unroll
-            for (int t = 0; t < 8; t++) qt[r32 * 132 + 32 * wave + 16 * hh + 8 * g + t] = yq[hh][t];
+            for (int t = 0; t < 8; t++) qt[r32 * LD + 32 * T + 16 * hh + 8 * g + t] = yq[hh][t];
+        }
         __syncthreads();
-        if (wave >= 2) return;
+        if (wave >= TN / 2) return;
         float xv[4][8];
 #pragma unroll
         for (int ks = 0; ks < 4; ks++)
 #pragma unroll
-            for (int t = 0; t < 8; t++) xv[ks][t] = qt[r32 * 132 + 64 * wave + 16 * ks + 8 * g + t];
-        const int head = 2 * blockIdx.x + wave;
+            for (int t = 0; t < 8; t++) xv[ks][t] = qt[r32 * LD + 64 * wave + 16 * ks + 8 * g + t];
+        const int head = TN / 2 * blockIdx.x + wave;
         qmlp64_lane(xv, r32, g, ea.w0, ea.s0, ea.b0, ea.w2, ea.s2, ea.b2, ea.scale + 64 * head,
                     live ? Y + (size_t)m * ldy + 64 * head : nullptr);
         return;
@@ -529,6 +535,8 @@ bool query_split_fits(const DevBlock &b, int M, const float *X, int ldx, const f
            (size_t)(M + 31) / 32 <= 65535;
 }
 
+constexpr int QUERY_HEAD_TILES_ROWS = 512;
+
 void query_split(hipStream_t s, int M, const float *X, int ldx, const DevBlock &b, const float *scale, float *q) {
     if (!query_split_fits(b, M, X, ldx, q)) throw ArgError{"query_split: shape not supported"};
     SplitEpi ea{nullptr, 0, scale, b.heads};
@@ -539,8 +547,14 @@ void query_split(hipStream_t s, int M, const float *X, int ldx, const DevBlock &
     ea.s2 = b.q2_s.shift;
     ea.b2 = b.q2b;
     const int d = b.d;
-    hipLaunchKernelGGL((k_gemm_splitk4<EPI_NONE, true, 4, true>), dim3(d / 128, (M + 31) / 32), dim3(256), 0, s, M, d,
-                       d, X, ldx, b.in_s.img, b.in_s.shift, b.in_b, q, d, ea, b.n1w, b.n1b);
+    // up to QUERY_HEAD_TILES_ROWS rows a workgroup per head (twice the workgroups, each with half the weights to
+    // stream), above it per two heads
+    if (M <= QUERY_HEAD_TILES_ROWS)
+        hipLaunchKernelGGL((k_gemm_splitk4<EPI_NONE, true, 2, true>), dim3(d / 64, (M + 31) / 32), dim3(256), 0, s, M,
+                           d, d, X, ldx, b.in_s.img, b.in_s.shift, b.in_b, q, d, ea, b.n1w, b.n1b);
+    else
+        hipLaunchKernelGGL((k_gemm_splitk4<EPI_NONE, true, 4, true>), dim3(d / 128, (M + 31) / 32), dim3(256), 0, s,
+                           M, d, d, X, ldx, b.in_s.img, b.in_s.shift, b.in_b, q, d, ea, b.n1w, b.n1b);
     TAH_LAUNCHED();
 }
 
