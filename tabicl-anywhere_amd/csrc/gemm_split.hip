@@ -504,11 +504,10 @@ void gemm_split(hipStream_t s, int M, int N, int K, const float *X, int ldx, con
     }
 }
 
-template <bool LN>
-static void launch_splitk4(hipStream_t s, int M, int N, int K, const float *X, int ldx, const uint8_t *img, int shift,
-                           const float *b, float *Y, int ldy, Epi epi, const SplitEpi &ea, const float *lnw,
-                           const float *lnb) {
-    constexpr int TN = 4;  // two tiles a wavefront (twice the workgroups) measured slower
+template <bool LN, int TN>
+static void launch_splitk4_tiles(hipStream_t s, int M, int N, int K, const float *X, int ldx, const uint8_t *img,
+                                 int shift, const float *b, float *Y, int ldy, Epi epi, const SplitEpi &ea,
+                                 const float *lnw, const float *lnb) {
     const dim3 grid(N / (32 * TN), (M + 31) / 32);
     switch (epi) {
         case EPI_NONE:
@@ -525,6 +524,20 @@ static void launch_splitk4(hipStream_t s, int M, int N, int K, const float *X, i
             break;
     }
     TAH_LAUNCHED();
+}
+
+// Four tiles a workgroup from 2,048 rows (two, with twice the workgroups, measured slower there); two below 512 rows,
+// where the few workgroups each stream half the weights
+constexpr int SPLITK_TWO_TILES_ROWS = 512;
+
+template <bool LN>
+static void launch_splitk4(hipStream_t s, int M, int N, int K, const float *X, int ldx, const uint8_t *img, int shift,
+                           const float *b, float *Y, int ldy, Epi epi, const SplitEpi &ea, const float *lnw,
+                           const float *lnb) {
+    if (M <= SPLITK_TWO_TILES_ROWS && N % 64 == 0)
+        launch_splitk4_tiles<LN, 2>(s, M, N, K, X, ldx, img, shift, b, Y, ldy, epi, ea, lnw, lnb);
+    else
+        launch_splitk4_tiles<LN, 4>(s, M, N, K, X, ldx, img, shift, b, Y, ldy, epi, ea, lnw, lnb);
 }
 
 bool query_split_fits(const DevBlock &b, int M, const float *X, int ldx, const float *Y) {
@@ -563,9 +576,9 @@ void dense(hipStream_t s, int M, int N, int K, const float *X, int ldx, const fl
     const bool img = w.img && gemm_split_fits(N, K) && K == w.K && w.row0 % 32 == 0 && N + w.row0 <= w.N &&
                      ldx % 4 == 0 && ldy % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 &&
                      (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
-    // at 64 rows the f32 kernels' weight streaming wins (1.41 against 1.48 ms a prediction), at 256 the split
-    // kernels (1.66 against 1.72 ms)
-    const bool split = img && M >= 256 && (epi == EPI_NONE || epi == EPI_GELU || epi == EPI_RESID);
+    // from 64 rows the split kernels win (two tiles a workgroup below 512 rows: a 64-row prediction 1.285 against
+    // 1.316 ms on the f32 kernels, 256 rows 1.52 against 1.61 ms with four tiles)
+    const bool split = img && M >= 64 && (epi == EPI_NONE || epi == EPI_GELU || epi == EPI_RESID);
     const bool k4 = split && N % 128 == 0 && K % 64 == 0 && K >= 256 && K <= 4 * SPLITK_MAX_KQ;
     if (lnw && !split && W && gemm_ln_fits(M, K, X, ldx, W)) {
         // few rows: the layer norm inside the product's kernel
