@@ -104,6 +104,13 @@ static int guarded(tah_dev *dev, F &&f) {
     } catch (const std::bad_alloc &) {
         dev->last_error = "out of host memory";
         return TAH_E_BUDGET;
+    } catch (const std::exception &e) {
+        // nothing may unwind through extern "C": any other failure is the card's, and the caller answers on the CPU
+        dev->last_error = std::string("graphics card: ") + e.what();
+        return TAH_E_DEVICE;
+    } catch (...) {
+        dev->last_error = "graphics card: unexpected failure";
+        return TAH_E_DEVICE;
     }
 }
 
@@ -391,6 +398,7 @@ extern "C" int tah_weights_upload(tah_dev *dev, const tah_model_desc *m, tah_wei
         pk.add(m->col_y, ytab * e, &w->col_y);
         pk.add(m->cls_tokens, (size_t)m->cls * e, &w->cls_tokens);
         pk.add(m->rope_freqs, m->rope_half, &w->rope_freqs);
+        if (m->rope_freqs && m->rope_half > 0) w->rope_host.assign(m->rope_freqs, m->rope_freqs + m->rope_half);
         pk.add(m->out_lnw, e, &w->out_lnw);
         pk.add(m->out_lnb, e, &w->out_lnb);
         pk.add(m->icl_y, ytab * d, &w->icl_y);
@@ -448,6 +456,7 @@ extern "C" void tah_weights_free(tah_weights *w) {
     // independent of the device handle, which may already be closed; hipFree waits for work that uses the memory
     if (!w) return;
     (void)hipSetDevice(w->ordinal);
+    for (auto &r : w->rope) (void)hipFree(r.second);
     if (w->arena) (void)hipFree(w->arena);
     delete w;
 }
@@ -574,18 +583,32 @@ extern "C" int tah_attend_resident(tah_dev *dev, const tah_model *model, int32_t
     });
 }
 
-// The in-context stage for nq rows already on the card (src/predict.rs:413-585): h_dev is updated in place.
-static void stage_rows(tah_dev *dev, const tah_weights *w, const tah_model *model, float *h, int nq, int out_n,
-                       float *out, Loans &loans) {
+// Working buffers of the in-context stage for nq rows: t, q, att [nq][d], mid [nq][wide], the attention's split
+// partials.
+struct StageBufs {
+    float *t, *q, *att, *mid;
+    void *work;
+};
+
+static size_t stage_floats_wide(const tah_weights *w) { return (size_t)std::max(icl_mid(w), w->dec_hidden); }
+
+static StageBufs stage_bufs(const tah_weights *w, const tah_model *model, int nq, Loans &loans) {
+    StageBufs b;
+    b.t = loans.take<float>((size_t)nq * w->d);
+    b.q = loans.take<float>((size_t)nq * w->d);
+    b.att = loans.take<float>((size_t)nq * w->d);
+    b.mid = loans.take<float>((size_t)nq * stage_floats_wide(w));
+    b.work = loans.take<uint8_t>(attention_work_bytes(shape_of(model, w->icl_heads, nq)));
+    return b;
+}
+
+// The in-context stage for nq rows already on the card (src/predict.rs:413-585): h is updated in place.
+static void stage_rows_with(tah_dev *dev, const tah_weights *w, const tah_model *model, float *h, int nq, int out_n,
+                            float *out, const StageBufs &bb) {
     const int d = w->d, heads = w->icl_heads;
-    const int wide = std::max(icl_mid(w), w->dec_hidden);
     hipStream_t s = dev->stream;
-    float *t = loans.take<float>((size_t)nq * d);
-    float *q = loans.take<float>((size_t)nq * d);
-    float *att = loans.take<float>((size_t)nq * d);
-    float *mid = loans.take<float>((size_t)nq * wide);
+    float *t = bb.t, *q = bb.q, *att = bb.att, *mid = bb.mid;
     const AttnShape a = shape_of(model, heads, nq);
-    void *work = loans.take<uint8_t>(attention_work_bytes(a));
     for (int l = 0; l < w->icl_layers; l++) {
         const DevBlock &b = w->icl[l];
         // query: q = modulate(Wq norm1(h) + bq)  (src/nn.rs:130-152)
@@ -598,7 +621,7 @@ static void stage_rows(tah_dev *dev, const tah_weights *w, const tah_model *mode
         }
         // attention over the stored layer, then h += out(att)  (src/predict.rs:421-551)
         const KvImages img = images_of(model, l);
-        attention(s, a, q, layer_of(model, l), att, work, &img);
+        attention(s, a, q, layer_of(model, l), att, bb.work, &img);
         dense(s, nq, d, d, att, d, b.out_w, b.out_s, b.out_b, h, d, EPI_RESID, h, d);
         // h += l2(gelu(l1(norm2 h)))  (src/predict.rs:552-568)
         dense(s, nq, b.ff, d, h, d, b.l1w, b.l1_s, b.l1b, mid, b.ff, EPI_GELU, nullptr, 0, b.n2w, b.n2b, t);
@@ -608,6 +631,11 @@ static void stage_rows(tah_dev *dev, const tah_weights *w, const tah_model *mode
     dense(s, nq, w->dec_hidden, d, h, d, w->dec0w, w->dec0_s, w->dec0b, mid, w->dec_hidden, EPI_GELU, nullptr, 0, w->lnw,
           w->lnb, t);
     gemm(s, nq, out_n, w->dec_hidden, mid, w->dec_hidden, w->dec2w, w->dec2b, out, out_n, EPI_NONE, nullptr, 0);
+}
+
+static void stage_rows(tah_dev *dev, const tah_weights *w, const tah_model *model, float *h, int nq, int out_n,
+                       float *out, Loans &loans) {
+    stage_rows_with(dev, w, model, h, nq, out_n, out, stage_bufs(w, model, nq, loans));
 }
 
 static void check_stage(const tah_weights *w, const tah_model *model, int nq, int out_n) {
@@ -838,20 +866,25 @@ extern "C" int tah_model_set_columns(tah_dev *dev, tah_model *model, const tah_w
     });
 }
 
-// cos and sin of position * frequency for T positions ([T][half]), as Rope::new (src/nn.rs:304-321), on the card.
-static const float *rope_tables(tah_dev *dev, const tah_weights *w, int T, Loans &loans) {
+// cos and sin of position * frequency for T positions ([T][half] each), as Rope::new (src/nn.rs:304-321): made on
+// the host the first time a token count is seen and kept on the card with the weights, so prediction never waits
+// for the host here again.
+static const float *rope_tables(const tah_weights *w_, int T) {
+    auto *w = const_cast<tah_weights *>(w_);  // the cache is not part of the weights' value
+    for (auto &r : w->rope)
+        if (r.first == T) return r.second;
     const int half = w->rope_half;
-    std::vector<float> freqs(half), tab(2 * (size_t)T * half);
-    TAH_HIP(hipMemcpy(freqs.data(), w->rope_freqs, sizeof(float) * half, hipMemcpyDeviceToHost));
+    std::vector<float> tab(2 * (size_t)T * half);
     for (int p = 0; p < T; p++)
         for (int i = 0; i < half; i++) {
-            const float a = (float)p * freqs[i];
+            const float a = (float)p * w->rope_host[i];
             tab[(size_t)p * half + i] = cosf(a);
             tab[(size_t)T * half + (size_t)p * half + i] = sinf(a);
         }
-    float *d = loans.take<float>(tab.size());
-    TAH_HIP(hipMemcpyAsync(d, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice, dev->stream));
-    TAH_HIP(hipStreamSynchronize(dev->stream));  // tab is a local
+    float *d = nullptr;
+    TAH_HIP(hipMalloc(&d, std::max<size_t>(tab.size(), 1) * sizeof(float)));
+    w->rope.push_back({T, d});
+    TAH_HIP(hipMemcpy(d, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice));
     return d;
 }
 
@@ -899,7 +932,7 @@ extern "C" int tah_represent(tah_dev *dev, const tah_weights *w, const float *to
         const size_t nt = (size_t)n * tokens * w->e;
         float *td = loans.take<float>(nt), *rd = loans.take<float>((size_t)n * w->d);
         float *scratch = loans.take<float>(row_stage_floats(w, n, tokens));
-        const float *tabs = rope_tables(dev, w, tokens, loans);
+        const float *tabs = rope_tables(w, tokens);
         TAH_HIP(hipMemcpyAsync(td, tok, nt * sizeof(float), hipMemcpyHostToDevice, dev->stream));
         row_stage(dev->stream, w, td, n, tokens, tabs, tabs + (size_t)tokens * w->rope_half, rd, scratch);
         TAH_HIP(hipMemcpyAsync(rep, rd, sizeof(float) * n * w->d, hipMemcpyDeviceToHost, dev->stream));
@@ -934,8 +967,7 @@ static void predict_rows(tah_dev *dev, const tah_weights *w, const tah_model *mo
     check_columns(w, model);
     check_stage(w, model, n, out_n);
     const int T = w->cls + model->features;
-    Loans tabs_loan(dev);
-    const float *tabs = rope_tables(dev, w, T, tabs_loan);
+    const float *tabs = rope_tables(w, T);
     const size_t used = busy_bytes(dev->pool);
     const size_t room = dev->pool.budget > used ? dev->pool.budget - used : 0;
     int batch = n;
@@ -1084,7 +1116,7 @@ extern "C" int tah_fit_represent(tah_dev *dev, const tah_weights *w, const float
             if (digits > 1) scale_by(s, M * e, sum, 1.0f / (float)digits, cells);
         }
         // the row stage in batches of rows (src/fit.rs:516-539)
-        const float *tabs = rope_tables(dev, w, T, keep);
+        const float *tabs = rope_tables(w, T);
         size_t used2 = 0;
         for (auto &b : dev->pool.bufs)
             if (b.busy) used2 += b.bytes;

@@ -113,6 +113,10 @@ struct tah_weights {
     const float *icl_y, *lnw, *lnb, *dec0w, *dec0b, *dec2w, *dec2b;
     SplitW dec0_s;  // the decoder's first layer as a gemm_split image
     const float *col_scale;  // [e]: 1 / sqrt(column head width), what the column blocks' queries are multiplied by
+    // the row stage's rotary tables, made once per token count T and kept with the weights: cos then sin of
+    // position * frequency, [2][T][rope_half] on the card; rope_host is the frequencies as uploaded
+    std::vector<float> rope_host;
+    std::vector<std::pair<int, float *>> rope;
 };
 
 struct tah_model {

@@ -339,18 +339,26 @@ static void launch(hipStream_t s, int M, int N, int K, const float *X, int ldx, 
     TAH_LAUNCHED();
 }
 
+// Rows per launch: the tile kernel's grid covers 64 rows a workgroup in its second dimension (at most 65,535), so
+// taller matrices (a fit's column stage: feature groups x training rows) go in slabs of rows, which are independent.
+constexpr size_t SLAB_ROWS = (size_t)65535 * GB;
+
 void gemm(hipStream_t s, int M, int N, int K, const float *X, int ldx, const float *W, const float *b, float *Y, int ldy,
           Epi epi, const float *R, int ldr, const float *lnw, const float *lnb, const float *scale) {
     if (M <= 0 || N <= 0) return;
-    if ((size_t)M > (size_t)65535 * 16) throw ArgError{"gemm: too many rows for one launch"};
     if (epi == EPI_SCALE && !scale) throw ArgError{"gemm: the scale epilogue needs its scales"};
-    const EpiArgs ea{R, ldr, scale, 1};
-    switch (epi) {
-        case EPI_NONE: launch<EPI_NONE>(s, M, N, K, X, ldx, W, b, Y, ldy, ea, lnw, lnb); break;
-        case EPI_GELU: launch<EPI_GELU>(s, M, N, K, X, ldx, W, b, Y, ldy, ea, lnw, lnb); break;
-        case EPI_RESID: launch<EPI_RESID>(s, M, N, K, X, ldx, W, b, Y, ldy, ea, lnw, lnb); break;
-        case EPI_SCALE: launch<EPI_SCALE>(s, M, N, K, X, ldx, W, b, Y, ldy, ea, lnw, lnb); break;
-        default: throw ArgError{"gemm: unknown epilogue"};
+    for (size_t r0 = 0; r0 < (size_t)M; r0 += SLAB_ROWS) {
+        const int m = (int)std::min(SLAB_ROWS, (size_t)M - r0);
+        const float *Xs = X + r0 * ldx;
+        float *Ys = Y + r0 * ldy;
+        const EpiArgs ea{R ? R + r0 * ldr : nullptr, ldr, scale, 1};
+        switch (epi) {
+            case EPI_NONE: launch<EPI_NONE>(s, m, N, K, Xs, ldx, W, b, Ys, ldy, ea, lnw, lnb); break;
+            case EPI_GELU: launch<EPI_GELU>(s, m, N, K, Xs, ldx, W, b, Ys, ldy, ea, lnw, lnb); break;
+            case EPI_RESID: launch<EPI_RESID>(s, m, N, K, Xs, ldx, W, b, Ys, ldy, ea, lnw, lnb); break;
+            case EPI_SCALE: launch<EPI_SCALE>(s, m, N, K, Xs, ldx, W, b, Ys, ldy, ea, lnw, lnb); break;
+            default: throw ArgError{"gemm: unknown epilogue"};
+        }
     }
 }
 
@@ -362,8 +370,13 @@ bool gemm_ln_fits(int M, int K, const float *X, int ldx, const float *W) {
 void gemm_qmod(hipStream_t s, int M, int N, int K, const float *X, int ldx, const float *W, const float *b, float *q,
                const float *scale, int heads) {
     if (M <= 0 || N <= 0) return;
-    if ((size_t)M > (size_t)65535 * 16) throw ArgError{"gemm: too many rows for one launch"};
-    launch<EPI_QMOD>(s, M, N, K, X, ldx, W, b, q, N, EpiArgs{q, N, scale, heads});
+    if (heads <= 0) throw ArgError{"gemm: the query modulation needs its head count"};
+    // slabs of whole rows of heads, so that row m of a slab is still head m % heads
+    const size_t slab = SLAB_ROWS / heads * heads;
+    for (size_t r0 = 0; r0 < (size_t)M; r0 += slab) {
+        const int m = (int)std::min(slab, (size_t)M - r0);
+        launch<EPI_QMOD>(s, m, N, K, X + r0 * ldx, ldx, W, b, q + r0 * N, N, EpiArgs{q + r0 * N, N, scale, heads});
+    }
 }
 
 }  // namespace tah

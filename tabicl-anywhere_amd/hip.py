@@ -40,6 +40,21 @@ def _f32(a) -> np.ndarray:
     return np.ascontiguousarray(a, dtype=np.float32)
 
 
+def _rows_of(a, width: int, what: str) -> np.ndarray:
+    """`a` as a contiguous float32 [rows][width] array; anything else is refused before the card reads past it."""
+    a = _f32(a)
+    if a.ndim != 2 or a.shape[1] != width:
+        raise ValueError(f"{what}: expected [rows][{width}] values, got shape {a.shape}")
+    return a
+
+
+def _features_of(vm) -> int:
+    f = getattr(vm, "features", 0)
+    if not f:
+        raise ValueError("the model holds no column cache (VramModel.set_columns)")
+    return f
+
+
 class Gpu:
     """One GPU: its stream, working-memory pool and last error."""
 
@@ -115,7 +130,7 @@ class Gpu:
         return VramModel(self, weights, kv_format, rows, chunk, layers, scales)
 
     def attend_resident(self, vm: "VramModel", layer: int, q) -> np.ndarray:
-        q = _f32(q)
+        q = _rows_of(q, vm.d, "attend_resident")
         nq = q.shape[0]
         out = np.empty((nq, vm.d), np.float32)
         self._check(self._l.tah_attend_resident(self._h, vm._h, int(layer), _fp(q), nq, _fp(out)))
@@ -123,7 +138,7 @@ class Gpu:
 
     def in_context(self, weights: "GpuWeights", vm: "VramModel", h, out_n: int) -> np.ndarray:
         """The whole in-context stage: row representations `h [n][d]` to the first `out_n` decoder outputs."""
-        h = _f32(h)
+        h = _rows_of(h, vm.d, "in_context")
         nq = h.shape[0]
         out = np.empty((nq, out_n), np.float32)
         self._check(self._l.tah_stage(self._h, weights._h, vm._h, _fp(h), nq, int(out_n), _fp(out)))
@@ -132,7 +147,7 @@ class Gpu:
     # ---- the column and row stages, and all three at once (AttendCached::rows) -------------------------------
     def embed(self, weights: "GpuWeights", vm: "VramModel", x) -> np.ndarray:
         """The column stage: x [n][features] to tokens [n][cls + features][e] (`embed`, `src/predict.rs:282-353`)."""
-        x = _f32(x)
+        x = _rows_of(x, _features_of(vm), "embed")
         n = x.shape[0]
         m = weights.model
         tok = np.empty((n, m.cls + vm.features, m.e), np.float32)
@@ -142,6 +157,8 @@ class Gpu:
     def represent(self, weights: "GpuWeights", tok) -> np.ndarray:
         """The row stage: tokens [n][T][e] to representations [n][d] (`represent`, `src/predict.rs:356-372`)."""
         tok = _f32(tok)
+        if tok.ndim != 3 or tok.shape[2] != weights.model.e:
+            raise ValueError(f"represent: expected tokens [n][T][{weights.model.e}], got shape {tok.shape}")
         n, T = tok.shape[0], tok.shape[1]
         rep = np.empty((n, weights.model.d), np.float32)
         self._check(self._l.tah_represent(self._h, weights._h, _fp(tok), n, T, _fp(rep)))
@@ -149,7 +166,7 @@ class Gpu:
 
     def predict(self, weights: "GpuWeights", vm: "VramModel", x, out_n: int) -> np.ndarray:
         """All three stages (`Gpu::predict`, `src/gpu.rs:2146`): x [n][features] to the first out_n outputs."""
-        x = _f32(x)
+        x = _rows_of(x, _features_of(vm), "predict")
         n = x.shape[0]
         out = np.empty((n, out_n), np.float32)
         self._check(self._l.tah_predict_rows(self._h, weights._h, vm._h, _fp(x), n, int(out_n), _fp(out)))
@@ -201,7 +218,10 @@ class Gpu:
         """`Attend::in_context`: fits the in-context stage of one problem on the card. `sink(layer, records)` gets
         each layer's stored records (a uint8 array, valid during the call) in order; returning a true value (or
         raising) stops the fit. Returns True (the card always offers the stage here)."""
-        h, scales = _f32(h), _f32(scales)
+        m = weights.model
+        h, scales = _rows_of(h, m.d, "in_context_fit"), _f32(scales)
+        if scales.size != m.icl_layers * m.d:
+            raise ValueError(f"in_context_fit: scales must be [{m.icl_layers}][{m.d}]")
         rows = h.shape[0]
         failure = []
 
