@@ -134,6 +134,31 @@ class Bundle:
         return self.raw(name).tobytes()
 
 
+def join_parts(manifest_path) -> "Bundle":
+    """A bundle stored as numbered parts beside a JSON manifest (`{"bytes": total, "parts": [{"file", "bytes"}]}`),
+    joined in order, as the reference ships its 16-bit weights (`store::join_parts`, `src/store.rs:269-280`). Every
+    part must have exactly its listed size, and the parts must add up to the total."""
+    import json
+    import os
+
+    with open(manifest_path) as f:
+        man = json.load(f)
+    here = os.path.dirname(os.path.abspath(manifest_path))
+    out = bytearray()
+    for part in man["parts"]:
+        name = part["file"]
+        if os.path.basename(name) != name:
+            raise BundleError(f"part {name}: parts must sit beside their manifest")
+        with open(os.path.join(here, name), "rb") as f:
+            data = f.read()
+        if len(data) != int(part["bytes"]):
+            raise BundleError(f"{name} is {len(data)} bytes, the parts list says {part['bytes']}")
+        out += data
+    if len(out) != int(man["bytes"]):
+        raise BundleError(f"the parts hold {len(out)} bytes, the manifest says {man['bytes']}")
+    return Bundle(bytes(out))
+
+
 def _line(name: str, dtype: str, off: int, nb: int, dims) -> str:
     return " ".join([name, dtype, str(off), str(nb)] + [str(v) for v in dims]) + "\n"
 

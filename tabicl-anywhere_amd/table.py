@@ -24,6 +24,14 @@ class Member:
     classes: list    # class relabelling: member sees class c as classes[c]
 
 
+def encode_labels(labels):
+    """Arbitrary integer labels to class indices `0..classes` in increasing label order, and the sorted distinct
+    labels that map them back (`encode_labels`, `src/table.rs:42-48`)."""
+    labels = np.asarray(labels, np.int64).reshape(-1)
+    classes = np.unique(labels)
+    return np.searchsorted(classes, labels).astype(np.int64), classes
+
+
 def member_inputs(table: np.ndarray, m: Member, y=None):
     """`xs[r][j] = table[r][features[j]]` as float32, and `ys[r] = classes[y[r]]` (`src/table.rs:136-147`)."""
     xs = np.ascontiguousarray(np.asarray(table, np.float64)[:, m.features].astype(np.float32))

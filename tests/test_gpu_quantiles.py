@@ -106,3 +106,22 @@ def test_add_regression_card_matches_host(gpu):
     for k in ("mean", "variance", "median"):
         assert np.array_equal(a[k], b[k], equal_nan=True)
     assert np.allclose(a["quantiles"], b["quantiles"], rtol=5e-5, atol=5e-5, equal_nan=True)
+
+
+def test_quantile_stats_planted_tails(gpu):
+    """The card's tail fits on quantiles planted on known lines (the same closed forms the host statement is pinned
+    by in test_table_golden.py): icdf far out in either tail follows the least-squares slope of exactly the k end
+    points from the end quantile."""
+    from test_table_golden import TAIL_CASES, planted_tails
+
+    for n, a, b, c, d in TAIL_CASES:
+        q, (sl, sr) = planted_tails(n, a, b, c, d)
+        lv0, lvn = 1.0 / (n + 1), n / (n + 1)
+        lo = np.array([1e-5, 1e-4, 0.3 * lv0], np.float32)
+        hi = np.array([1 - 1e-5, 1 - 1e-4, 1 - 0.3 * (1 - lvn)], np.float32)
+        st = gpu.quantile_stats(q[None, :], np.concatenate([lo, hi]))[0, 3:]
+        want = np.concatenate([q[0] + sl * (np.log(lo.astype(np.float64)) - np.log(lv0)),
+                               q[-1] - sr * (np.log(1 - hi.astype(np.float64)) - np.log(1 - lvn))])
+        err = np.abs(st - want) / np.maximum(1.0, np.abs(want))
+        say(f"planted tails n={n}: worst relative {err.max():.2e}")
+        assert err.max() < 2e-4

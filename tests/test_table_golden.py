@@ -31,8 +31,8 @@ def tables(fx, which):
 
 
 def ensemble_proba(fx, fit_predict):
-    y = fx.i32s("y_train")
-    classes = int(y.max()) + 1
+    y, labels = T.encode_labels(fx.i32s("y_train"))
+    classes = len(labels)
     train, test = tables(fx, "train"), tables(fx, "test")
     ms = members(fx)
     nt = next(iter(test.values())).shape[0]
@@ -92,3 +92,58 @@ def test_quantile_dist_closed_forms():
     xs = [d.icdf(a) for a in np.linspace(0.001, 0.999, 200)]
     assert all(b >= a - 1e-6 for a, b in zip(xs, xs[1:]))
     assert d.icdf(0.001) < d.q[0] and d.icdf(0.999) > d.q[-1]
+
+
+def planted_tails(n: int, a: float, b: float, c: float, d: float):
+    """Quantiles at levels i/(n+1) whose first k and last k values (k = clamp(n/4, 1, 20)) lie on a ln(level) + b and
+    -c ln(1 - level) + d, except that the k-th from either end is moved off its line; the middle is monotone. Returns
+    the quantiles and the least-squares slopes of exactly the k end points on each side (np.polyfit in float64): a
+    window one point shorter or longer gives another slope."""
+    lv = np.arange(1, n + 1, dtype=np.float64) / (n + 1)
+    k = max(min(20, n // 4), 1)
+    q = np.linspace(a * np.log(lv[k - 1]) + b, -c * np.log(1 - lv[n - k]) + d, n)
+    q[:k] = a * np.log(lv[:k]) + b
+    q[n - k:] = -c * np.log(1 - lv[n - k:]) + d
+    if k > 2:
+        q[k - 1] += 0.25 * (q[k - 1] - q[k - 2])
+        q[n - k] -= 0.25 * (q[n - k + 1] - q[n - k])
+    q = q.astype(np.float32)
+    ql = q.astype(np.float64)
+    lv32 = (np.arange(1, n + 1, dtype=np.float32) / np.float32(n + 1)).astype(np.float64)
+    sl = abs(np.polyfit(np.log(lv32[:k]), ql[:k], 1)[0])
+    sr = abs(np.polyfit(np.log(1 - lv32[n - k:]), ql[n - k:], 1)[0])
+    return q, (min(max(sl, 0.01), 100.0), min(max(sr, 0.01), 100.0))
+
+
+TAIL_CASES = [  # n, a, b, c, d
+    (999, 2.0, 1.0, 3.0, 40.0),     # k = 20
+    (99, 0.5, -3.0, 1.25, 7.0),     # k = 20
+    (40, 1.5, 0.0, 0.75, 2.0),      # k = 10: n / 4
+    (999, 500.0, 0.0, 1e-4, 0.0),   # slopes clamped to [0.01, 100]
+]
+
+
+@pytest.mark.parametrize("n,a,b,c,d", TAIL_CASES)
+def test_quantile_dist_planted_tails(n, a, b, c, d):
+    """The exponential tails beyond the first and last level are least-squares lines through exactly the first and
+    last k points, pinned at the end quantiles (`src/table.rs:300-316`): icdf far out in either tail follows
+    slope * ln(level) from the end point. A wrong window, sign or intercept moves these by far more than the bound."""
+    q, (sl, sr) = planted_tails(n, a, b, c, d)
+    dist = T.QuantileDist(q)
+    lv0, lvn = 1.0 / (n + 1), n / (n + 1)
+    for alpha in (1e-5, 1e-4, 0.3 * lv0):
+        want = float(q[0]) + sl * (np.log(alpha) - np.log(lv0))
+        assert abs(float(dist.icdf(alpha)) - want) < 2e-4 * max(1.0, abs(want)), (alpha, dist.icdf(alpha), want)
+    for alpha in (1 - 1e-5, 1 - 1e-4, 1 - 0.3 * (1 - lvn)):
+        want = float(q[-1]) - sr * (np.log(1 - alpha) - np.log(1 - lvn))
+        assert abs(float(dist.icdf(alpha)) - want) < 2e-4 * max(1.0, abs(want)), (alpha, dist.icdf(alpha), want)
+
+
+def test_quantile_dist_one_point_tails():
+    """Below 8 quantiles k is 1: one point has no spread, the slope falls to its floor 0.01, and the tails leave
+    the end quantiles at that slope."""
+    q = np.array([1.0, 2.0, 4.0, 8.0, 9.0], np.float32)
+    dist = T.QuantileDist(q)
+    lv0, lvn = 1.0 / 6.0, 5.0 / 6.0
+    assert abs(float(dist.icdf(1e-3)) - (1.0 + 0.01 * (np.log(1e-3) - np.log(lv0)))) < 1e-5
+    assert abs(float(dist.icdf(1 - 1e-3)) - (9.0 - 0.01 * (np.log(1e-3) - np.log(1 - lvn)))) < 1e-5
