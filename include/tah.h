@@ -141,6 +141,16 @@ int tah_stage(tah_dev *dev, const tah_weights *w, const tah_model *model, const 
 int tah_stage_dev(tah_dev *dev, const tah_weights *w, const tah_model *model, const float *h_dev, int32_t nq,
                   int32_t out_n, float *out_dev);
 
+/* The same without allocating: for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). It has no counterpart in the reference. Its working buffers come
+ * from a static device array of TAH_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends); nq is at most
+ * TAH_NOALLOC_MAX_ROWS, and a model whose buffers would not fit there is refused with TAH_E_ARG. Calls on one GPU
+ * share the array: calls that overlap on one GPU (through two device handles) race. */
+#define TAH_NOALLOC_MAX_ROWS 256
+#define TAH_NOALLOC_SCRATCH_BYTES ((size_t)24 << 20)
+int tah_stage_dev_noalloc(tah_dev *dev, const tah_weights *w, const tah_model *model, const float *h_dev, int32_t nq,
+                          int32_t out_n, float *out_dev);
+
 /* ---- the column and row stages, and AttendCached::rows (src/predict.rs:74-78, Gpu::predict src/gpu.rs:2146) --
  *
  * tah_model_set_columns: gives the fitted member's column cache (col_kv, [features][digits][col_blocks][2][e][inds],

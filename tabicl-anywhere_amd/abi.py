@@ -97,6 +97,8 @@ SIGNATURES = {
                                  ctypes.c_int32, F32P]),
     "tah_stage_dev": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                      ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
+    "tah_stage_dev_noalloc": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                             ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
     "tah_model_set_columns": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, F32P, ctypes.c_int32,
                                              ctypes.c_int32]),
     "tah_embed": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, F32P, ctypes.c_int32, F32P]),

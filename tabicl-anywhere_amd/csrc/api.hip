@@ -125,6 +125,10 @@ static size_t layer_bytes(int fmt, int rows, int chunk, int d) {
 
 static size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
+// Device memory for tah_stage_dev_noalloc, one copy per GPU for the life of the process. Host code never uses this
+// name as an address: tah_open looks up each device's copy with hipGetSymbolAddress and keeps it in tah_dev.
+static __device__ __align__(256) uint8_t scratch[TAH_NOALLOC_SCRATCH_BYTES];
+
 // ---- device handle ---------------------------------------------------------------------------------------------
 extern "C" int tah_open(int32_t ordinal, tah_dev **out) {
     if (!out) return TAH_E_ARG;
@@ -139,6 +143,9 @@ extern "C" int tah_open(int32_t ordinal, tah_dev **out) {
         TAH_HIP(hipGetDeviceProperties(&prop, ordinal));
         dev->name = std::string(prop.name) + " (" + prop.gcnArchName + ")";
         TAH_HIP(hipStreamCreateWithFlags(&dev->stream, hipStreamNonBlocking));
+        void *p = nullptr;
+        TAH_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        dev->noalloc = static_cast<uint8_t *>(p);
         return TAH_OK;
     });
     if (rc != TAH_OK) {
@@ -671,6 +678,49 @@ extern "C" int tah_stage(tah_dev *dev, const tah_weights *w, const tah_model *mo
         stage_rows(dev, w, model, hd, nq, out_n, od, loans);
         TAH_HIP(hipMemcpyAsync(out, od, sizeof(float) * nq * out_n, hipMemcpyDeviceToHost, dev->stream));
         TAH_HIP(hipStreamSynchronize(dev->stream));
+        return TAH_OK;
+    });
+}
+
+// The in-context stage without allocating: every working buffer is carved from this device's static scratch array.
+// No hipMalloc, hipFree or pool call happens, so callers that cannot allocate (graph capture, serving loops) can use
+// it. Calls on one GPU share the array: two calls that overlap on one GPU (from two device handles, whose streams
+// are not ordered with each other) race.
+extern "C" int tah_stage_dev_noalloc(tah_dev *dev, const tah_weights *w, const tah_model *model, const float *h_dev,
+                                     int32_t nq, int32_t out_n, float *out_dev) {
+    if (!h_dev || !out_dev) return TAH_E_ARG;
+    return guarded(dev, [&] {
+        check_stage(w, model, nq, out_n);
+        if (nq > TAH_NOALLOC_MAX_ROWS)
+            throw ArgError{"stage_noalloc: at most " + std::to_string(TAH_NOALLOC_MAX_ROWS) + " rows a call"};
+        if (nq == 0) return TAH_OK;
+        if (!dev->noalloc) throw DeviceError{"graphics card: the scratch array was not resolved"};
+        const size_t wide = stage_floats_wide(w), rows_d = (size_t)nq * w->d;
+        const size_t sizes[] = {rows_d * 4, rows_d * 4, rows_d * 4, rows_d * 4, (size_t)nq * wide * 4,
+                                attention_work_bytes(shape_of(model, w->icl_heads, nq))};
+        size_t need = 0;
+        for (size_t b : sizes) need += align256(b);
+        if (need > TAH_NOALLOC_SCRATCH_BYTES)
+            throw ArgError{"stage_noalloc: this model needs " + std::to_string(need) + " bytes of scratch for " +
+                           std::to_string(nq) + " rows, more than the " + std::to_string(TAH_NOALLOC_SCRATCH_BYTES) +
+                           " the library holds"};
+        uint8_t *at = dev->noalloc;
+        auto carve = [&](size_t bytes) {
+            uint8_t *p = at;
+            at += align256(bytes);
+            return p;
+        };
+        float *h = reinterpret_cast<float *>(carve(sizes[0]));
+        StageBufs bb;
+        bb.t = reinterpret_cast<float *>(carve(sizes[1]));
+        bb.q = reinterpret_cast<float *>(carve(sizes[2]));
+        bb.att = reinterpret_cast<float *>(carve(sizes[3]));
+        bb.mid = reinterpret_cast<float *>(carve(sizes[4]));
+        bb.work = carve(sizes[5]);
+        // every buffer is written before it is read (the partials by the attention's key ranges before their merge),
+        // so nothing left by an earlier call needs clearing
+        TAH_HIP(hipMemcpyAsync(h, h_dev, rows_d * sizeof(float), hipMemcpyDeviceToDevice, dev->stream));
+        stage_rows_with(dev, w, model, h, nq, out_n, out_dev, bb);
         return TAH_OK;
     });
 }

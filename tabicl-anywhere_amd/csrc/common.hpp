@@ -69,6 +69,9 @@ struct tah_dev {
     std::string last_error;
     std::string name;
     tah::Pool pool;
+    // this device's copy of the library's static scratch array (tah_stage_dev_noalloc), resolved at tah_open with
+    // the device current: a device address, unlike the array's name in host code
+    uint8_t *noalloc = nullptr;
 };
 
 // A block's tensors on the card (device pointers; nullptr where absent).
