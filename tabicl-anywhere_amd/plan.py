@@ -19,11 +19,15 @@ import numpy as np
 
 @dataclass
 class Node:
-    rows: list | None  # training rows this node uses (None: all, in order)
-    y: list            # targets as this node sees them
-    k: int             # outputs read from the decoder at this node
+    """An in-context problem of the plan. `rows` indexes the training table (None stands for the whole table in its
+    own order); `y` holds one target per row in this problem's numbering (a group number at an inner node, a
+    within-leaf class number at a leaf); `k` is how many decoder outputs the problem's prediction keeps; `map` sends
+    output j to a class (leaf) or to the index of the child problem for group j (inner)."""
+    rows: list | None
+    y: list
+    k: int
     leaf: bool
-    map: list = field(default_factory=list)  # leaf: class per output; inner: child node per group
+    map: list = field(default_factory=list)
 
 
 @dataclass

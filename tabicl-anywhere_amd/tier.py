@@ -1,303 +1,277 @@
-"""Graphics memory shared by many tenants: the VRAM tier (`VramTier`, `src/gpu.rs:2485-2701`), with the bookkeeping of
-the in-memory tier's ledger (`warm::Ledger`, `src/warm.rs:28-118`).
+"""Fitted problems of many tenants sharing one card's memory, with the CPU answering whatever the card cannot.
 
-Every resident problem belongs to one tenant and one model; each tenant has a byte budget within the overall one;
-the least recently used ready entry makes room (the tenant's own while it would be over its share, anyone's
-otherwise); an entry in use is not released until the prediction using it has finished. The budgets are hard
-limits on what is really on the card: a load starts only when the bytes of everything loaded and not yet released,
-evicted or not, leave room for it; otherwise that prediction (and only that one) is answered by the CPU (`None`
-from the handle). A problem larger than its tenant's budget is never loaded. A card that fails a prediction does
-not fail it either: the CPU answers, and the tier counts it (`fallbacks`) and keeps the reason (`last_error`).
+This plays the part of the reference's `VramTier` (`src/gpu.rs:2485-2701`) and follows its observable rules:
 
-What the card holds at worst: `budget` of fitted problems, plus the card's working-memory budget
-(`Gpu.set_work_budget`), plus each set of weights in use.
+* each problem belongs to a tenant; the card holds at most `budget` bytes of problems in all and `tenant_budget`
+  of one tenant's;
+* making room removes the problems used longest ago: the tenant's own while the newcomer would put it over its
+  share, anyone's otherwise; a problem still being uploaded is never removed;
+* a problem that a prediction is using stays on the card until that prediction ends, even once removed, and its
+  bytes still count, so the budgets bound what is really on the card at every moment;
+* a problem larger than its tenant's budget is never uploaded;
+* a prediction the card cannot serve (not resident yet, no room, or the card failed) is left to the CPU: the
+  handle returns None; card failures are counted (`fallbacks`) and the last one is kept (`last_error`).
+
+The design is this module's own. One ordered map holds every listed problem, most recently used last. Two ledgers
+count bytes: `listed` (what the map holds: uploads in flight and ready problems) decides what to remove, and
+`resident` (listed plus removed-but-still-in-use) is the hard cap a new upload must fit under. Predictions take a
+lease on a problem; the lease's end frees a removed problem.
 """
 from __future__ import annotations
 
 import threading
+from collections import OrderedDict
+from contextlib import contextmanager
 
 from . import hip
 
-LOADING, TOO_BIG = "loading", "too big"
+UPLOADING, READY, REFUSED = "uploading", "ready", "refused"
 
 
-class Ledger:
-    """`warm::Ledger`: entries by key (tenant, model, prefix, node) with their bytes and a use clock."""
+class Residency:
+    """One problem's presence on the card."""
+
+    __slots__ = ("tenant", "nbytes", "state", "vm", "leases", "listed")
+
+    def __init__(self, tenant: str, nbytes: int, state: str):
+        self.tenant, self.nbytes, self.state = tenant, nbytes, state
+        self.vm = None
+        self.leases = 0      # predictions using it now
+        self.listed = True   # still in the tier's map (a removed one lives on while leased)
+
+
+class _Bytes:
+    """Bytes counted overall and per tenant."""
 
     def __init__(self):
-        self.entries: dict = {}  # key -> [value, bytes, clock]
-        self.bytes = 0
-        self.by_tenant: dict = {}
-        self.clock = 0
+        self.total = 0
+        self.of: dict = {}
 
-    def get(self, key):
-        """The entry's value, marked as just used (`src/warm.rs:43-50`)."""
-        self.clock += 1
-        e = self.entries.get(key)
-        if e is None:
-            return None
-        e[2] = self.clock
-        return e[0]
+    def add(self, tenant: str, n: int) -> None:
+        self.total += n
+        self.of[tenant] = self.of.get(tenant, 0) + n
 
-    def set(self, key, value) -> None:
-        self.entries[key][0] = value
-
-    def remove(self, key):
-        e = self.entries.pop(key, None)
-        if e is None:
-            return None
-        self.bytes -= e[1]
-        self.by_tenant[key[0]] = self.by_tenant.get(key[0], 0) - e[1]
-        return e[0]
-
-    def admit(self, key, nbytes: int, value, budget: int, tenant_budget: int, may_go):
-        """Hold `value` under `key`, first making room within both budgets (`src/warm.rs:61-89`): while the tenant
-        would be over its share its own least recently used entry goes, otherwise the least recently used of
-        anyone's; only entries `may_go` allows are removed. Returns (admitted, removed values)."""
-        out = []
-        if nbytes > min(tenant_budget, budget):
-            return False, out
-        while True:
-            mine = self.by_tenant.get(key[0], 0)
-            over_tenant = mine + nbytes > tenant_budget
-            if not over_tenant and self.bytes + nbytes <= budget:
-                break
-            victims = [(e[2], k) for k, e in self.entries.items() if (not over_tenant or k[0] == key[0]) and may_go(e[0])]
-            if not victims:
-                return False, out
-            out.append(self.remove(min(victims)[1]))
-        self.clock += 1
-        self.bytes += nbytes
-        self.by_tenant[key[0]] = self.by_tenant.get(key[0], 0) + nbytes
-        if key in self.entries:
-            out.append(self.remove(key))
-        self.entries[key] = [value, nbytes, self.clock]
-        return True, out
-
-    def contains(self, key) -> bool:
-        return key in self.entries
-
-    def evict(self, tenant: str, model=None) -> list:
-        keys = [k for k in self.entries if k[0] == tenant and (model is None or k[1] == model)]
-        return [self.remove(k) for k in keys]
-
-    def items(self):
-        return [(k, e[0], e[1]) for k, e in self.entries.items()]
-
-    def held(self, tenant: str):
-        return self.bytes, self.by_tenant.get(tenant, 0)
-
-
-class _Resident:
-    """A loaded problem: freed on the card once it has been released by the tier and no prediction uses it."""
-
-    def __init__(self, tier: "VramTier", tenant: str, nbytes: int, vm):
-        self.tier, self.tenant, self.nbytes, self.vm = tier, tenant, nbytes, vm
-        self.uses = 0
-        self.released = False
-
-    def release(self) -> None:  # called with the tier's lock held
-        self.released = True
-        self._maybe_free()
-
-    def _maybe_free(self) -> None:
-        if self.released and self.uses == 0 and self.vm is not None:
-            self.vm.free()
-            self.vm = None
-            self.tier._live_give(self.tenant, self.nbytes)
+    def tenant(self, tenant: str) -> int:
+        return self.of.get(tenant, 0)
 
 
 class VramTier:
-    """`VramTier` (`src/gpu.rs:2496-2611`) over `hip.Gpu`."""
+    """Problems of many tenants on one `hip.Gpu`, within an overall and a per-tenant byte budget."""
 
     def __init__(self, gpu: hip.Gpu, budget: int, tenant_budget: int):
         self.gpu = gpu
         self.budget = int(budget)
         self.tenant_budget = min(int(tenant_budget), self.budget)
-        self._state = Ledger()
-        self._live_bytes = 0
-        self._live_by_tenant: dict = {}
-        self._lock = threading.RLock()
+        self._map: "OrderedDict[tuple, Residency]" = OrderedDict()  # (tenant, model, prefix, node) -> residency
+        self._listed = _Bytes()
+        self._resident = _Bytes()
+        self._mu = threading.RLock()
         self.fallbacks = 0
-        self._last_error = None
+        self._failure = None
 
     # ---- what is held ------------------------------------------------------------------------------------------
     def held(self, tenant: str):
-        """Bytes of graphics memory the tier holds now, in all and by `tenant` (problems being loaded included)."""
-        with self._lock:
-            return self._state.held(tenant)
+        """Bytes the tier lists now (uploads in flight included), overall and of `tenant`."""
+        with self._mu:
+            return self._listed.total, self._listed.tenant(tenant)
 
     def ready(self, tenant: str) -> int:
-        """Bytes of `tenant`'s problems that are loaded and ready."""
-        with self._lock:
-            return sum(n for k, v, n in self._state.items() if k[0] == tenant and isinstance(v, _Resident))
+        """Bytes of `tenant`'s problems that are uploaded and usable."""
+        with self._mu:
+            return sum(r.nbytes for k, r in self._map.items() if k[0] == tenant and r.state == READY)
 
     def on_card(self, tenant: str):
-        """Bytes of fitted problems really on the card now, in all and of `tenant`: what the tier holds plus
-        anything evicted that a prediction is still using. Never more than the budgets."""
-        with self._lock:
-            return self._live_bytes, self._live_by_tenant.get(tenant, 0)
+        """Bytes of problems physically on the card, overall and of `tenant`: everything listed plus removed
+        problems a prediction still uses. Never above the budgets."""
+        with self._mu:
+            return self._resident.total, self._resident.tenant(tenant)
 
     def last_error(self):
-        """Why the card last failed a prediction (which the CPU then answered), if it ever did."""
-        return self._last_error
+        """The message of the card's most recent failure (that prediction went to the CPU), or None."""
+        return self._failure
+
+    # ---- removing ----------------------------------------------------------------------------------------------
+    def _unlist(self, key) -> None:
+        """Take a problem out of the map (lock held); free it now unless a prediction holds a lease on it."""
+        r = self._map.pop(key)
+        r.listed = False
+        if r.state == REFUSED:
+            return
+        self._listed.add(r.tenant, -r.nbytes)
+        self._free_if_idle(r)
+
+    def _free_if_idle(self, r: Residency) -> None:
+        if r.listed or r.leases or r.state == UPLOADING:
+            return  # an upload in flight is freed by the uploader when it sees the problem was removed
+        if r.vm is not None:
+            r.vm.free()
+            r.vm = None
+        self._resident.add(r.tenant, -r.nbytes)
+        r.nbytes = 0
 
     def evict(self, tenant: str, model=None) -> None:
-        """Release everything `tenant` holds (for `model` only, if given); problems in use by a prediction are
-        freed when it finishes."""
-        with self._lock:
-            for v in self._state.evict(tenant, model):
-                if isinstance(v, _Resident):
-                    v.release()
+        """Remove everything `tenant` holds (of `model` only, if given). Problems in use are freed when their
+        predictions end; uploads in flight when they finish."""
+        with self._mu:
+            for key in [k for k in self._map if k[0] == tenant and (model is None or k[1] == model)]:
+                self._unlist(key)
 
-    def handle(self, tenant: str, model: str, members: dict, weights: hip.GpuWeights) -> "TierAttend":
-        """One tenant's use of the tier for one fitted model (`members`: prefix -> `fit.Fitted`), to answer
-        predictions in place of the CPU where it can."""
-        return TierAttend(self, tenant, model, members, weights)
-
-    def preload(self, tenant: str, model: str, members: dict, weights: hip.GpuWeights, prefix: str, node: int) -> bool:
-        """Load problem `node` of member `prefix` now. True if it is resident afterwards; False if the budgets do
-        not allow it (now, or ever)."""
-        key = (tenant, model, prefix, int(node))
-        with self._lock:
-            if isinstance(self._state.get(key), _Resident):
-                return True
-        nbytes = self._claim(key, members[prefix], weights, node)
-        if nbytes is None:
-            return False
-        return self._finish(key, nbytes, members[prefix], weights, node)
-
-    # ---- loading -----------------------------------------------------------------------------------------------
+    # ---- admitting ---------------------------------------------------------------------------------------------
     @staticmethod
     def problem_bytes(f, weights: hip.GpuWeights, node: int) -> int:
-        """Card bytes of problem `node` of the fitted member `f` once loaded: its records and their images, plus
-        the column cache for a member with one problem and one label digit (`Gpu::model_bytes`,
-        `src/gpu.rs:2063-2068`)."""
-        rows = f.nodes[node].rows
-        n = hip.VramModel.model_bytes(weights, f.kv_format, rows, f.chunk)
+        """Card bytes of problem `node` of the fitted member `f` once loaded (`Gpu::model_bytes`,
+        `src/gpu.rs:2063-2068`): its records and their images, plus the column cache when the member is one problem
+        of one label digit (then prediction runs all three stages on the card)."""
+        n = hip.VramModel.model_bytes(weights, f.kv_format, f.nodes[node].rows, f.chunk)
         if len(f.nodes) == 1 and f.digits == 1:
             n += f.col_kv.size * 4
         return n
 
-    def _claim(self, key, f, weights, node):
-        """Take a place for a problem and count its bytes before anything is uploaded (`src/gpu.rs:2553-2585`).
-        None if there is no room within the budgets."""
-        nbytes = self.problem_bytes(f, weights, node)
-        with self._lock:
-            s = self._state
-            if s.contains(key):
-                return None
-            ok, gone = s.admit(key, nbytes, LOADING, self.budget, self.tenant_budget,
-                               lambda v: isinstance(v, _Resident))
-            for v in gone:
-                if isinstance(v, _Resident):
-                    v.release()
-            if not ok:
-                if nbytes > self.tenant_budget:
-                    s.admit(key, 0, TOO_BIG, self.budget, self.tenant_budget, lambda v: False)
-                return None
-            mine = self._live_by_tenant.get(key[0], 0)
-            if self._live_bytes + nbytes > self.budget or mine + nbytes > self.tenant_budget:
-                # the room is promised to problems still in use: not this time
-                s.remove(key)
-                return None
-            self._live_bytes += nbytes
-            self._live_by_tenant[key[0]] = mine + nbytes
-            return nbytes
+    def _room_for(self, tenant: str, nbytes: int) -> bool:
+        """Remove ready problems, least recently used first, until `nbytes` more of `tenant` fit the listed budgets
+        (lock held). False, with nothing removed past what was needed, if no removable problem is left."""
+        while True:
+            over_share = self._listed.tenant(tenant) + nbytes > self.tenant_budget
+            if not over_share and self._listed.total + nbytes <= self.budget:
+                return True
+            victim = next((k for k, r in self._map.items()
+                           if r.state == READY and (not over_share or k[0] == tenant)), None)
+            if victim is None:
+                return False
+            self._unlist(victim)
 
-    def _live_give(self, tenant: str, nbytes: int) -> None:
-        self._live_bytes -= nbytes
-        self._live_by_tenant[tenant] = self._live_by_tenant.get(tenant, 0) - nbytes
+    def _reserve(self, key, nbytes: int) -> Residency | None:
+        """List a problem as uploading, its bytes counted in both ledgers, or say why not by returning None (lock
+        held): already listed (uploading, ready or refused), too big for its tenant, or no room."""
+        tenant = key[0]
+        if key in self._map:
+            return None
+        if nbytes > self.tenant_budget:
+            self._map[key] = Residency(tenant, nbytes, REFUSED)  # remembered: never tried again
+            return None
+        if not self._room_for(tenant, nbytes):
+            return None
+        if (self._resident.total + nbytes > self.budget
+                or self._resident.tenant(tenant) + nbytes > self.tenant_budget):
+            return None  # removed problems still in use hold the room
+        r = Residency(tenant, nbytes, UPLOADING)
+        self._map[key] = r
+        self._listed.add(tenant, nbytes)
+        self._resident.add(tenant, nbytes)
+        return r
 
-    def _finish(self, key, nbytes, f, weights, node) -> bool:
-        """Upload a claimed problem and make it ready, unless it was evicted meanwhile (`src/gpu.rs:2588-2611`)."""
+    def _upload(self, key, r: Residency, f, weights, node) -> None:
+        """Put a reserved problem on the card; a failure gives its bytes back and is remembered."""
+        vm = None
         try:
             vm = self.gpu.load(weights, f.kv_format, f.nodes[node].rows, f.chunk, f.layers[node], f.scales[node])
             if len(f.nodes) == 1 and f.digits == 1:
                 vm.set_columns(f.col_kv, f.features, f.digits)
-        except Exception as e:  # noqa: BLE001 -- the card's failure is recorded and the CPU answers
-            with self._lock:
-                if self._state.get(key) == LOADING:
-                    self._state.remove(key)
-                self._live_give(key[0], nbytes)
-                self._last_error = str(e)
+            failure = None
+        except Exception as e:  # noqa: BLE001 -- the card's failure: the CPU answers
+            failure = e
+            if vm is not None:
+                vm.free()
+                vm = None
+        with self._mu:
+            r.vm = vm
+            r.state = READY
+            if failure is not None:
+                self._failure = str(failure)
+                if r.listed:
+                    self._map.pop(key)
+                    r.listed = False
+                    self._listed.add(r.tenant, -r.nbytes)
+            self._free_if_idle(r)  # removed while uploading (or failed): freed now
+
+    def preload(self, tenant: str, model: str, members: dict, weights: hip.GpuWeights, prefix: str, node: int) -> bool:
+        """Upload problem `node` of member `prefix` now, on this thread. True if it is resident afterwards."""
+        key = (tenant, model, prefix, int(node))
+        f = members[prefix]
+        with self._mu:
+            r = self._map.get(key)
+            if r is not None:
+                self._map.move_to_end(key)
+                return r.state == READY
+            r = self._reserve(key, self.problem_bytes(f, weights, node))
+        if r is None:
             return False
-        with self._lock:
-            res = _Resident(self, key[0], nbytes, vm)
-            v = self._state.get(key)
-            if v == LOADING:
-                self._state.set(key, res)
-                return True
-            res.release()  # evicted while loading
-            return isinstance(v, _Resident)
+        self._upload(key, r, f, weights, node)
+        with self._mu:
+            return r.listed and r.state == READY and r.vm is not None
 
-    def _resident(self, key, f, weights, node, wait: bool):
-        """The problem if it is resident (its use counted); otherwise start loading it (once) and say no for now.
-        The load runs on a thread of its own (on the calling thread with `wait`)."""
-        with self._lock:
-            v = self._state.get(key)
-            if isinstance(v, _Resident):
-                v.uses += 1
-                return v
-            if v is not None:
-                return None
-        nbytes = self._claim(key, f, weights, node)
-        if nbytes is None:
-            return None
-        if wait:
-            self._finish(key, nbytes, f, weights, node)
-            with self._lock:
-                v = self._state.get(key)
-                if isinstance(v, _Resident):
-                    v.uses += 1
-                    return v
-            return None
-        threading.Thread(target=self._finish, args=(key, nbytes, f, weights, node), daemon=True).start()
-        return None
+    @contextmanager
+    def _lease(self, key, f, weights, node, wait: bool):
+        """The problem's card model for the duration of a prediction, or None (then the CPU answers): a problem not
+        yet listed is reserved and uploaded, on this thread with `wait`, else on a thread of its own."""
+        mine = None  # a reservation this call made and uploads itself
+        with self._mu:
+            r = self._map.get(key)
+            if r is not None:
+                self._map.move_to_end(key)
+            else:
+                r = self._reserve(key, self.problem_bytes(f, weights, node))
+                if r is not None and wait:
+                    mine = r
+                elif r is not None:
+                    threading.Thread(target=self._upload, args=(key, r, f, weights, node), daemon=True).start()
+        if mine is not None:
+            self._upload(key, mine, f, weights, node)
+        with self._mu:
+            usable = r is not None and r.listed and r.state == READY and r.vm is not None
+            if usable:
+                r.leases += 1
+        if not usable:
+            yield None
+            return
+        try:
+            yield r.vm
+        finally:
+            with self._mu:
+                r.leases -= 1
+                self._free_if_idle(r)
 
-    def _done(self, res: _Resident) -> None:
-        with self._lock:
-            res.uses -= 1
-            res._maybe_free()
+    def handle(self, tenant: str, model: str, members: dict, weights: hip.GpuWeights) -> "TierAttend":
+        """One tenant's use of the tier for one fitted model (`members`: prefix -> `fit.Fitted`)."""
+        return TierAttend(self, tenant, model, members, weights)
 
 
 class TierAttend:
-    """`predict::AttendCached` over the tier (`VramHandle`, `src/gpu.rs:2614-2701`): `attend`, `stage` and `rows`
-    answer on the card when the problem is resident, else return None (the CPU answers) after starting its
-    load. `wait` loads on the calling thread instead, so the first prediction already uses the card."""
+    """`predict::AttendCached` over the tier: `attend`, `stage` and `rows` answer on the card when the problem is
+    resident, and otherwise return None (the CPU answers) after starting its upload. With `wait` the upload runs on
+    the calling thread, so the first prediction already uses the card."""
 
     def __init__(self, tier: VramTier, tenant: str, model: str, members: dict, weights: hip.GpuWeights,
                  wait: bool = False):
         self.tier, self.tenant, self.model, self.members, self.weights = tier, tenant, model, members, weights
         self.wait = wait
 
-    def _use(self, prefix: str, node: int, run):
+    def _on_card(self, prefix: str, node: int, work):
         f = self.members.get(prefix)
         if f is None or node >= len(f.nodes):
             return None
-        res = self.tier._resident((self.tenant, self.model, prefix, int(node)), f, self.weights, node, self.wait)
-        if res is None:
-            return None
-        try:
-            return run(res.vm, f)
-        except (hip.CardError, hip.BudgetError) as e:
-            with self.tier._lock:
-                self.tier.fallbacks += 1
-                self.tier._last_error = str(e)
-            return None
-        finally:
-            self.tier._done(res)
+        key = (self.tenant, self.model, prefix, int(node))
+        with self.tier._lease(key, f, self.weights, node, self.wait) as vm:
+            if vm is None:
+                return None
+            try:
+                return work(vm)
+            except Exception as e:  # noqa: BLE001 -- any failure on the card: counted, and the CPU answers
+                with self.tier._mu:
+                    self.tier.fallbacks += 1
+                    self.tier._failure = str(e)
+                return None
 
     def attend(self, prefix: str, node: int, layer: int, q, d: int, heads: int):
-        return self._use(prefix, node, lambda vm, f: self.tier.gpu.attend_resident(vm, layer, q) if d == vm.d else None)
+        return self._on_card(prefix, node, lambda vm: self.tier.gpu.attend_resident(vm, layer, q) if d == vm.d else None)
 
     def stage(self, prefix: str, node: int, h, d: int, out_n: int):
-        return self._use(prefix, node, lambda vm, f: self.tier.gpu.in_context(self.weights, vm, h, out_n)
-                         if d == vm.d else None)
+        return self._on_card(prefix, node, lambda vm: self.tier.gpu.in_context(self.weights, vm, h, out_n)
+                             if d == vm.d else None)
 
     def rows(self, prefix: str, x, out_n: int):
-        def run(vm, f):
+        def work(vm):
             if not getattr(vm, "features", 0) or vm.digits != 1:
                 return None
             return self.tier.gpu.predict(self.weights, vm, x, out_n)
-        return self._use(prefix, 0, run)
+        return self._on_card(prefix, 0, work)

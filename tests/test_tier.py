@@ -1,7 +1,7 @@
-"""The VRAM tier's bookkeeping (`tier.py`: `VramTier`, `src/gpu.rs:2485-2701`, over `warm::Ledger`,
-`src/warm.rs:28-118`) on the host, with a stand-in card: least-recently-used admission within the overall and the
-tenants' budgets, problems in use outliving their eviction, a problem too big for its tenant never loaded, loads
-on a thread of their own, and card failures answered by the CPU and counted. (tests/card.rs:237-346 runs the same
+"""The VRAM tier's rules (`tier.py`, the part of the reference's `VramTier`, `src/gpu.rs:2485-2701`) on the host, with
+a stand-in card: least-recently-used removal within the overall and the tenants' budgets, problems in use outliving
+their removal, uploads in flight never removed, a problem too big for its tenant never uploaded, uploads on a thread
+of their own, and card failures (of any kind) answered by the CPU and counted. (tests/card.rs:237-346 runs the same
 rules against a card; tests/test_gpu_tier.py does here.)"""
 import threading
 import time
@@ -12,26 +12,6 @@ import pytest
 from conftest import pkg
 
 hip, tier = pkg("hip"), pkg("tier")
-
-
-def test_ledger_lru_within_budgets():
-    L = tier.Ledger()
-    ready = lambda v: v != "busy"
-    assert L.admit(("a", "m", "p", 0), 40, "a0", 100, 60, ready) == (True, [])
-    assert L.admit(("b", "m", "p", 0), 40, "b0", 100, 60, ready) == (True, [])
-    L.get(("a", "m", "p", 0))  # a0 used last: b0 is now the oldest
-    # over the overall budget: the least recently used of anyone's goes
-    assert L.admit(("c", "m", "p", 0), 30, "c0", 100, 60, ready) == (True, ["b0"])
-    # over the tenant's share: a's own oldest goes, not c's
-    assert L.admit(("a", "m", "p", 1), 30, "a1", 100, 60, ready) == (True, ["a0"])
-    assert L.held("a") == (60, 30)
-    # larger than a tenant's budget: refused, nothing removed
-    assert L.admit(("d", "m", "p", 0), 61, "d0", 100, 60, ready) == (False, [])
-    # nothing may go: refused
-    L.set(("c", "m", "p", 0), "busy")
-    L.set(("a", "m", "p", 1), "busy")
-    assert L.admit(("e", "m", "p", 0), 50, "e0", 100, 60, ready) == (False, [])
-    assert sorted(L.evict("a")) == ["busy"] and L.held("a") == (30, 0)
 
 
 class FakeVM:
@@ -146,3 +126,55 @@ def test_card_failure_is_answered_by_the_cpu():
     h.wait = True
     assert h.rows("m0/", np.zeros((1, 3)), 2) is None
     assert t.fallbacks == 1 and "lost" in t.last_error()
+
+
+def test_least_recently_used_within_budgets():
+    card = FakeCard()
+    t = FakeTier(card, 100, 60)
+    m = lambda n: {"m0/": Member(n)}
+    assert t.preload("a", "x", m(40), None, "m0/", 0) and t.preload("b", "x", m(40), None, "m0/", 0)
+    assert t.preload("a", "x", m(40), None, "m0/", 0)  # a used last: b is now the oldest
+    # over the overall budget: the oldest of anyone's goes
+    assert t.preload("c", "x", m(30), None, "m0/", 0)
+    assert t.held("b") == (70, 0) and card.freed == 1
+    # over the tenant's share (40 + 30 > 60): a's own oldest goes, not c's
+    assert t.preload("a", "y", m(30), None, "m0/", 0)
+    assert t.held("a") == (60, 30) and t.held("c") == (60, 30) and card.freed == 2
+    # larger than a tenant's budget: refused for good, nothing removed
+    assert not t.preload("d", "x", m(61), None, "m0/", 0)
+    assert not t.preload("d", "x", m(61), None, "m0/", 0)
+    assert t.held("d") == (60, 0) and card.freed == 2
+    # removing one model of a tenant leaves its others
+    assert t.preload("a", "z", m(20), None, "m0/", 0)
+    t.evict("a", "y")
+    assert t.held("a") == (50, 20) and t.ready("a") == 20
+
+
+def test_upload_in_flight_is_never_removed():
+    card = FakeCard(delay=0.3)
+    t = FakeTier(card, 100, 100)
+    h = t.handle("a", "x", {"m0/": Member(70)}, None)
+    assert h.rows("m0/", np.zeros((1, 3)), 2) is None  # its upload starts on a thread of its own
+    # 70 listed and uploading: a newcomer of 40 finds nothing it may remove
+    assert not t.preload("b", "x", {"m0/": Member(40)}, None, "m0/", 0)
+    t.evict("a")  # removed while uploading: freed as soon as the upload ends
+    assert t.held("a") == (0, 0) and t.on_card("a") == (70, 70)
+    for _ in range(100):
+        if card.freed:
+            break
+        time.sleep(0.01)
+    assert card.loaded == card.freed == 1 and t.on_card("a") == (0, 0)
+
+
+def test_any_card_error_goes_to_the_cpu():
+    card = FakeCard()
+    t = FakeTier(card, 100, 100)
+    h = t.handle("a", "x", {"m0/": Member(30)}, None)
+    h.wait = True
+
+    def refuse(weights, vm, x, out_n):
+        raise ValueError("attention: too many queries for one launch")
+
+    card.predict = refuse
+    assert h.rows("m0/", np.zeros((1, 3)), 2) is None
+    assert t.fallbacks == 1 and "too many" in t.last_error()
