@@ -622,8 +622,12 @@ static void col_one(const tah_model_desc *m, const float *x, const float *y, int
     free(hidden);
 }
 
-void orc_fit_columns(const tah_model_desc *m, const float *x, const float *y, int rows, int features,
-                     const int *bases, int digits, int chunk, float *col_kv, float *emb) {
+/* The column stage of a fit for the feature groups listed in groups [ngroups] (all of them when groups is NULL):
+ * col_kv [ngroups][digits][blocks][2][e][inds] and emb [ngroups][rows][e], each group as src/fit.rs:326-423 fits
+ * it (groups are independent: a group's cache depends on its own cells over all rows). */
+void orc_fit_columns_of(const tah_model_desc *m, const float *x, const float *y, int rows, int features,
+                        const int *groups, int ngroups, const int *bases, int digits, int chunk, float *col_kv,
+                        float *emb) {
     int e = m->e, inds = m->inds, nb = m->col_blocks;
     /* the inducing points' queries, once per block (src/fit.rs:300-313), scaled for all `rows` */
     float *ind_q = xcalloc((size_t)nb * inds * e, sizeof(float));
@@ -636,12 +640,62 @@ void orc_fit_columns(const tah_model_desc *m, const float *x, const float *y, in
     float *a2_scale = xcalloc(e, sizeof(float));
     for (int i = 0; i < e; i++) a2_scale[i] = 1.0f / sqrtf((float)hd_of(&m->col_a2[0]));
     size_t rec_len = (size_t)digits * nb * 2 * e * inds;
+    int count = groups ? ngroups : features;
 #pragma omp parallel for schedule(dynamic, 1)
-    for (int g = 0; g < features; g++)
-        col_one(m, x, y, rows, features, g, bases, digits, chunk, ind_q, a2_scale, emb + (size_t)g * rows * e,
-                col_kv + (size_t)g * rec_len);
+    for (int k = 0; k < count; k++)
+        col_one(m, x, y, rows, features, groups ? groups[k] : k, bases, digits, chunk, ind_q, a2_scale,
+                emb + (size_t)k * rows * e, col_kv + (size_t)k * rec_len);
     free(ind_q);
     free(scale);
+    free(a2_scale);
+}
+
+void orc_fit_columns(const tah_model_desc *m, const float *x, const float *y, int rows, int features,
+                     const int *bases, int digits, int chunk, float *col_kv, float *emb) {
+    orc_fit_columns_of(m, x, y, rows, features, NULL, 0, bases, digits, chunk, col_kv, emb);
+}
+
+/* The fit's cells of n given training rows (x [n][features], y [n]) after the column stage, from a fitted column
+ * cache col_kv [features][digits][blocks][2][e][inds]: each digit's cell (input cell plus that digit's label
+ * embedding) through every block against the block's cached inducing keys and values, the digits averaged
+ * (src/fit.rs:360-423). emb [features][n][e]. */
+void orc_fit_cells_rows(const tah_model_desc *m, const float *col_kv, const int *bases, int digits, const float *x,
+                        const float *y, int n, int features, float *emb) {
+    int e = m->e, inds = m->inds, nb = m->col_blocks;
+    size_t rec_len = (size_t)digits * nb * 2 * e * inds;
+    float *a2_scale = xcalloc(e, sizeof(float));
+    for (int i = 0; i < e; i++) a2_scale[i] = 1.0f / sqrtf((float)hd_of(&m->col_a2[0]));
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int g = 0; g < features; g++) {
+        float *plain = xcalloc(e, sizeof(float)), *cell = xcalloc(e, sizeof(float)), *sum = xcalloc(e, sizeof(float));
+        for (int r = 0; r < n; r++) {
+            input_cell(m, x + (size_t)r * features, features, g, plain);
+            for (int j = 0; j < e; j++) sum[j] = 0.0f;
+            for (int dg = 0; dg < digits; dg++) {
+                memcpy(cell, plain, sizeof(float) * e);
+                int divisor = 1;
+                for (int k = dg + 1; k < digits; k++) divisor *= bases[k];
+                float yv = digits > 1 ? (float)(((int)y[r] / divisor) % bases[dg]) : y[r];
+                add_y(m, m->col_y, yv, cell, e);
+                for (int bi = 0; bi < nb; bi++) {
+                    const float *rk = col_kv + (size_t)g * rec_len + ((size_t)dg * nb + bi) * 2 * e * inds;
+                    cached_block(&m->col_a2[bi], a2_scale, rk, rk + (size_t)e * inds, inds, cell);
+                }
+                if (digits > 1)
+                    for (int j = 0; j < e; j++) sum[j] += cell[j];
+            }
+            float *out = emb + ((size_t)g * n + r) * e;
+            if (digits > 1) {
+                float inv = 1.0f / (float)digits;
+                for (int j = 0; j < e; j++) out[j] = sum[j] * inv;
+            } else {
+                memcpy(out, cell, sizeof(float) * e);
+            }
+        }
+        free(plain);
+        free(cell);
+        free(sum);
+    }
     free(a2_scale);
 }
 
@@ -717,6 +771,45 @@ void orc_fit_icl(const tah_model_desc *m, float *h, int rows, int chunk, int kv_
         }
     }
     free(kv);
+    free(q);
+    free(att);
+}
+
+/* One in-context layer's keys and values for n given rows h [n][d] (src/fit.rs:627-663, before the chunk layout):
+ * kv [n][2d], keys then values of each row. */
+void orc_kv_rows(const tah_model_desc *m, int layer, const float *h, int n, float *kv) {
+    const tah_block *b = &m->icl[layer];
+    int d = b->d;
+#pragma omp parallel for schedule(dynamic, 16)
+    for (int r = 0; r < n; r++) {
+        float *t = xcalloc(d, sizeof(float));
+        orc_layer_norm(h + (size_t)r * d, d, b->n1w, b->n1b, t);
+        orc_linear(b->in_w + (size_t)d * d, b->in_b + d, t, d, 2 * d, kv + (size_t)r * 2 * d);
+        free(t);
+    }
+}
+
+/* n rows h [n][d] (in place) through in-context layer `layer`: query (scaled by scale [d]), attention over the
+ * layer's stored records, output projection and residual, feed-forward (src/fit.rs:700-744 for training rows over
+ * exact f32 records; src/predict.rs:413-568 for test rows). */
+void orc_icl_step(const tah_model_desc *m, int layer, const float *scale, const uint8_t *records, int kv_format,
+                  int rows, int chunk, float *h, int n) {
+    const tah_block *b = &m->icl[layer];
+    int d = b->d;
+    float *q = xcalloc((size_t)n * d, sizeof(float));
+    float *att = xcalloc((size_t)n * d, sizeof(float));
+#pragma omp parallel for schedule(dynamic, 16)
+    for (int r = 0; r < n; r++) orc_query(b, scale, h + (size_t)r * d, q + (size_t)r * d);
+    orc_attend_records(q, n, records, kv_format, rows, chunk, d, b->heads, 1, att);
+#pragma omp parallel for schedule(dynamic, 16)
+    for (int r = 0; r < n; r++) {
+        float *x = h + (size_t)r * d;
+        float *t = xcalloc(d, sizeof(float));
+        orc_linear(b->out_w, b->out_b, att + (size_t)r * d, d, d, t);
+        for (int j = 0; j < d; j++) x[j] += t[j];
+        orc_feed_forward(b, x);
+        free(t);
+    }
     free(q);
     free(att);
 }

@@ -57,6 +57,11 @@ void orc_fit_columns(const tah_model_desc *m, const float *x, const float *y, in
                      const int *bases, int digits, int chunk, float *col_kv, float *emb);
 /* Row stage at fit (src/fit.rs:486-540 with row_forward src/nn.rs:357-419): emb [features][rows][e] to
  * representations reps [rows][d]. */
+void orc_fit_columns_of(const tah_model_desc *m, const float *x, const float *y, int rows, int features,
+                        const int *groups, int ngroups, const int *bases, int digits, int chunk, float *col_kv,
+                        float *emb);
+void orc_fit_cells_rows(const tah_model_desc *m, const float *col_kv, const int *bases, int digits, const float *x,
+                        const float *y, int n, int features, float *emb);
 void orc_fit_rows(const tah_model_desc *m, const float *emb, int rows, int features, float *reps);
 /* In-context stage at fit for one problem (src/fit.rs:577-747, CPU path): h [rows][d] already has the target's
  * embedding added and is consumed. Writes scales [layers][d] and each layer's stored records into
@@ -66,6 +71,11 @@ void orc_fit_icl(const tah_model_desc *m, float *h, int rows, int chunk, int kv_
                  uint8_t *const *records, float *kv_f32);
 /* Fit-time all-rows attention of one layer (src/fit.rs:700-744): queries q [rows][d] (scaled) over the exact f32
  * keys and values of the same rows in chunk layout (kv, 2*rows*d floats), out [rows][d] (before out-proj). */
+/* One in-context layer's keys and values [n][2d] for given rows; one in-context layer step of given rows over stored
+ * records (in place). */
+void orc_kv_rows(const tah_model_desc *m, int layer, const float *h, int n, float *kv);
+void orc_icl_step(const tah_model_desc *m, int layer, const float *scale, const uint8_t *records, int kv_format,
+                  int rows, int chunk, float *h, int n);
 void orc_fit_attend(const float *q, const float *kv, int rows, int chunk, int d, int heads, float *out);
 
 /* Column stage at prediction (src/predict.rs:282-353): x [n][features], col_kv as fitted; tok receives

@@ -54,6 +54,11 @@ def lib():
             "orc_fit_rows": (None, [md, p, i, i, p]),
             "orc_fit_icl": (None, [md, p, i, i, i, p, u8pp, p]),
             "orc_fit_attend": (None, [p, p, i, i, i, i, p]),
+            "orc_kv_rows": (None, [md, i, p, i, p]),
+            "orc_fit_columns_of": (None, [md, p, p, i, i, ctypes.POINTER(ctypes.c_int), i, ctypes.POINTER(ctypes.c_int),
+                                          i, i, p, p]),
+            "orc_fit_cells_rows": (None, [md, p, ctypes.POINTER(ctypes.c_int), i, p, p, i, i, p]),
+            "orc_icl_step": (None, [md, i, p, abi.U8P, i, i, i, p, i]),
             "orc_embed": (None, [md, p, i, p, i, i, p]),
             "orc_represent": (None, [md, p, i, i, p]),
             "orc_set_threads": (None, [i]), "orc_threads": (i, []),
@@ -143,6 +148,35 @@ def fit_columns(model, x, y, bases, chunk):
     return col_kv, emb
 
 
+def fit_columns_of(model, x, y, groups, bases, chunk):
+    """The fit's column stage for the listed feature groups only: col_kv [len(groups)][digits][blocks][2][e][inds]
+    and the groups' cells [len(groups)][rows][e]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.ascontiguousarray(y, dtype=np.float32)
+    rows, features = x.shape
+    digits = len(bases)
+    col_kv = np.zeros((len(groups), digits, len(model.col_a2), 2, model.e, model.inds), np.float32)
+    emb = np.zeros((len(groups), rows, model.e), np.float32)
+    gs = (ctypes.c_int * len(groups))(*groups)
+    b = (ctypes.c_int * digits)(*bases)
+    lib().orc_fit_columns_of(ctypes.byref(model.desc()), fp(x), fp(y), rows, features, gs, len(groups), b, digits,
+                             chunk, fp(col_kv), fp(emb))
+    return col_kv, emb
+
+
+def fit_cells_rows(model, col_kv, bases, x, y):
+    """The fit's cells [features][n][e] of the given training rows after the column stage, from a fitted column
+    cache (col_kv [features][digits][blocks][2][e][inds])."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.ascontiguousarray(y, dtype=np.float32)
+    n, features = x.shape
+    emb = np.zeros((features, n, model.e), np.float32)
+    b = (ctypes.c_int * len(bases))(*bases)
+    lib().orc_fit_cells_rows(ctypes.byref(model.desc()), fp(np.ascontiguousarray(col_kv, dtype=np.float32)), b,
+                             len(bases), fp(x), fp(y), n, features, fp(emb))
+    return emb
+
+
 def fit_rows(model, emb):
     features, rows, _ = emb.shape
     reps = np.zeros((rows, model.d), np.float32)
@@ -180,6 +214,23 @@ def fit_raw(model, x, y, classes, chunk=256, kv_format=abi.KV_F32):
         scales.append(s)
         layers.append(l)
     return Fitted(rows, features, classes, chunk, kv_format, plan, col_kv, scales, layers)
+
+
+def kv_rows(model, layer, h):
+    """In-context layer `layer`'s keys and values [n][2d] of given rows h [n][d] (norm1 and the key/value
+    projection, `src/fit.rs:627-663`)."""
+    h = np.ascontiguousarray(h, dtype=np.float32)
+    out = np.zeros((h.shape[0], 2 * model.d), np.float32)
+    lib().orc_kv_rows(ctypes.byref(model.desc()), int(layer), fp(h), h.shape[0], fp(out))
+    return out
+
+
+def icl_step(model, layer, scale, records, kv_format, rows, chunk, h):
+    """Given rows h [n][d] through one in-context layer over its stored records (a copy is returned)."""
+    h = np.ascontiguousarray(h, dtype=np.float32).copy()
+    lib().orc_icl_step(ctypes.byref(model.desc()), int(layer), fp(np.ascontiguousarray(scale, dtype=np.float32)),
+                       u8(np.ascontiguousarray(records)), int(kv_format), int(rows), int(chunk), fp(h), h.shape[0])
+    return h
 
 
 # ---- prediction ---------------------------------------------------------------------------------------------

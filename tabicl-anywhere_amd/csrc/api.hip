@@ -3,6 +3,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <initializer_list>
 #include <memory>
 #include <new>
 
@@ -76,6 +77,32 @@ struct Loans {
         for (void *p : held) dev->pool.give(p);
     }
 };
+
+static size_t busy_bytes(const Pool &p) {
+    size_t b = 0;
+    for (auto &x : p.bufs)
+        if (x.busy) b += x.bytes;
+    return b;
+}
+
+// Rows a call takes at a time: all n when their working memory fits the room the budget leaves, else the largest
+// halving of n that fits (rows are independent); an OutOfMemory error when not even one row fits.
+template <class F>
+static int batch_rows(const tah_dev *dev, int n, F bytes_of) {
+    const size_t used = busy_bytes(dev->pool);
+    const size_t room = dev->pool.budget > used ? dev->pool.budget - used : 0;
+    int b = std::max(n, 1);
+    while (b > 1 && bytes_of(b) > room) b = (b + 1) / 2;
+    if (bytes_of(b) > room) throw BudgetError{"graphics card: one row does not fit the working-memory budget"};
+    return b;
+}
+
+// Bytes Loans takes for buffers of these many floats (each rounded to 256 bytes, with the pool's slack).
+static size_t loan_bytes(std::initializer_list<size_t> floats) {
+    size_t b = 0;
+    for (size_t f : floats) b += ((f * sizeof(float) + 255) & ~size_t(255)) + 256;
+    return b;
+}
 
 struct SinkError {
     int status;
@@ -651,16 +678,28 @@ static void check_stage(const tah_weights *w, const tah_model *model, int nq, in
     if (nq < 0 || out_n <= 0 || out_n > w->outputs) throw ArgError{"stage: bad row or output count"};
 }
 
+// Working bytes of the in-context stage for k rows (stage_bufs plus the rows' own copy and their outputs).
+static size_t stage_batch_bytes(const tah_weights *w, const tah_model *model, int k, int out_n) {
+    const size_t kk = (size_t)k;
+    return loan_bytes({kk * w->d, kk * out_n, kk * w->d, kk * w->d, kk * w->d, kk * stage_floats_wide(w)}) +
+           attention_work_bytes(shape_of(model, w->icl_heads, k)) + 256;
+}
+
 extern "C" int tah_stage_dev(tah_dev *dev, const tah_weights *w, const tah_model *model, const float *h_dev, int32_t nq,
                              int32_t out_n, float *out_dev) {
     if (!h_dev || !out_dev) return TAH_E_ARG;
     return guarded(dev, [&] {
         check_stage(w, model, nq, out_n);
         if (nq == 0) return TAH_OK;
-        Loans loans(dev);
-        float *h = loans.take<float>((size_t)nq * w->d);
-        TAH_HIP(hipMemcpyAsync(h, h_dev, sizeof(float) * nq * w->d, hipMemcpyDeviceToDevice, dev->stream));
-        stage_rows(dev, w, model, h, nq, out_n, out_dev, loans);
+        const int batch = batch_rows(dev, nq, [&](int k) { return stage_batch_bytes(w, model, k, out_n); });
+        for (int r0 = 0; r0 < nq; r0 += batch) {
+            const int k = std::min(batch, nq - r0);
+            Loans loans(dev);
+            float *h = loans.take<float>((size_t)k * w->d);
+            TAH_HIP(hipMemcpyAsync(h, h_dev + (size_t)r0 * w->d, sizeof(float) * k * w->d, hipMemcpyDeviceToDevice,
+                                   dev->stream));
+            stage_rows(dev, w, model, h, k, out_n, out_dev + (size_t)r0 * out_n, loans);
+        }
         return TAH_OK;
     });
 }
@@ -671,13 +710,19 @@ extern "C" int tah_stage(tah_dev *dev, const tah_weights *w, const tah_model *mo
     return guarded(dev, [&] {
         check_stage(w, model, nq, out_n);
         if (nq == 0) return TAH_OK;
-        Loans loans(dev);
-        float *hd = loans.take<float>((size_t)nq * w->d);
-        float *od = loans.take<float>((size_t)nq * out_n);
-        TAH_HIP(hipMemcpyAsync(hd, h, sizeof(float) * nq * w->d, hipMemcpyHostToDevice, dev->stream));
-        stage_rows(dev, w, model, hd, nq, out_n, od, loans);
-        TAH_HIP(hipMemcpyAsync(out, od, sizeof(float) * nq * out_n, hipMemcpyDeviceToHost, dev->stream));
-        TAH_HIP(hipStreamSynchronize(dev->stream));
+        const int batch = batch_rows(dev, nq, [&](int k) { return stage_batch_bytes(w, model, k, out_n); });
+        for (int r0 = 0; r0 < nq; r0 += batch) {
+            const int k = std::min(batch, nq - r0);
+            Loans loans(dev);
+            float *hd = loans.take<float>((size_t)k * w->d);
+            float *od = loans.take<float>((size_t)k * out_n);
+            TAH_HIP(hipMemcpyAsync(hd, h + (size_t)r0 * w->d, sizeof(float) * k * w->d, hipMemcpyHostToDevice,
+                                   dev->stream));
+            stage_rows(dev, w, model, hd, k, out_n, od, loans);
+            TAH_HIP(hipMemcpyAsync(out + (size_t)r0 * out_n, od, sizeof(float) * k * out_n, hipMemcpyDeviceToHost,
+                                   dev->stream));
+            TAH_HIP(hipStreamSynchronize(dev->stream));  // the loans go back to the pool with the batch
+        }
         return TAH_OK;
     });
 }
@@ -959,14 +1004,23 @@ extern "C" int tah_embed(tah_dev *dev, const tah_weights *w, const tah_model *mo
     return guarded(dev, [&] {
         check_columns(w, model);
         if (n <= 0) return TAH_OK;
-        const int T = w->cls + model->features;
-        Loans loans(dev);
-        float *xd = loans.take<float>((size_t)n * model->features);
-        float *td = loans.take<float>((size_t)n * T * w->e);
-        TAH_HIP(hipMemcpyAsync(xd, x, sizeof(float) * n * model->features, hipMemcpyHostToDevice, dev->stream));
-        embed_rows(dev, w, model, xd, n, td, loans);
-        TAH_HIP(hipMemcpyAsync(tok, td, sizeof(float) * n * T * w->e, hipMemcpyDeviceToHost, dev->stream));
-        TAH_HIP(hipStreamSynchronize(dev->stream));
+        const int F = model->features, T = w->cls + F;
+        const size_t per_tok = (size_t)T * w->e;
+        const int batch = batch_rows(dev, n, [&](int k) {
+            const size_t kk = (size_t)k;
+            return loan_bytes({kk * F, kk * per_tok, kk * F * w->e, column_stage_floats(w, k, F, model->digits)});
+        });
+        for (int r0 = 0; r0 < n; r0 += batch) {
+            const int k = std::min(batch, n - r0);
+            Loans loans(dev);
+            float *xd = loans.take<float>((size_t)k * F);
+            float *td = loans.take<float>((size_t)k * per_tok);
+            TAH_HIP(hipMemcpyAsync(xd, x + (size_t)r0 * F, sizeof(float) * k * F, hipMemcpyHostToDevice, dev->stream));
+            embed_rows(dev, w, model, xd, k, td, loans);
+            TAH_HIP(hipMemcpyAsync(tok + (size_t)r0 * per_tok, td, sizeof(float) * k * per_tok, hipMemcpyDeviceToHost,
+                                   dev->stream));
+            TAH_HIP(hipStreamSynchronize(dev->stream));
+        }
         return TAH_OK;
     });
 }
@@ -978,15 +1032,23 @@ extern "C" int tah_represent(tah_dev *dev, const tah_weights *w, const float *to
         if (w->row.empty()) throw ArgError{"weights lack the row stage"};
         if (n <= 0) return TAH_OK;
         if (tokens <= w->cls) throw ArgError{"represent: too few tokens"};
-        Loans loans(dev);
-        const size_t nt = (size_t)n * tokens * w->e;
-        float *td = loans.take<float>(nt), *rd = loans.take<float>((size_t)n * w->d);
-        float *scratch = loans.take<float>(row_stage_floats(w, n, tokens));
+        const size_t per_tok = (size_t)tokens * w->e;
         const float *tabs = rope_tables(w, tokens);
-        TAH_HIP(hipMemcpyAsync(td, tok, nt * sizeof(float), hipMemcpyHostToDevice, dev->stream));
-        row_stage(dev->stream, w, td, n, tokens, tabs, tabs + (size_t)tokens * w->rope_half, rd, scratch);
-        TAH_HIP(hipMemcpyAsync(rep, rd, sizeof(float) * n * w->d, hipMemcpyDeviceToHost, dev->stream));
-        TAH_HIP(hipStreamSynchronize(dev->stream));
+        const int batch = batch_rows(dev, n, [&](int k) {
+            return loan_bytes({(size_t)k * per_tok, (size_t)k * w->d, row_stage_floats(w, k, tokens)});
+        });
+        for (int r0 = 0; r0 < n; r0 += batch) {
+            const int k = std::min(batch, n - r0);
+            Loans loans(dev);
+            float *td = loans.take<float>((size_t)k * per_tok), *rd = loans.take<float>((size_t)k * w->d);
+            float *scratch = loans.take<float>(row_stage_floats(w, k, tokens));
+            TAH_HIP(hipMemcpyAsync(td, tok + (size_t)r0 * per_tok, sizeof(float) * k * per_tok, hipMemcpyHostToDevice,
+                                   dev->stream));
+            row_stage(dev->stream, w, td, k, tokens, tabs, tabs + (size_t)tokens * w->rope_half, rd, scratch);
+            TAH_HIP(hipMemcpyAsync(rep + (size_t)r0 * w->d, rd, sizeof(float) * k * w->d, hipMemcpyDeviceToHost,
+                                   dev->stream));
+            TAH_HIP(hipStreamSynchronize(dev->stream));
+        }
         return TAH_OK;
     });
 }
@@ -1003,13 +1065,6 @@ static size_t predict_batch_bytes(const tah_weights *w, const tah_model *model, 
     return bytes;
 }
 
-static size_t busy_bytes(const Pool &p) {
-    size_t b = 0;
-    for (auto &x : p.bufs)
-        if (x.busy) b += x.bytes;
-    return b;
-}
-
 // All three stages for n rows x (on the card) into out [n][out_n] (on the card), in sub-batches that fit the
 // working-memory budget (the reference's chain, src/gpu.rs:2171-2224); rows are independent.
 static void predict_rows(tah_dev *dev, const tah_weights *w, const tah_model *model, const float *x, int n, int out_n,
@@ -1018,12 +1073,7 @@ static void predict_rows(tah_dev *dev, const tah_weights *w, const tah_model *mo
     check_stage(w, model, n, out_n);
     const int T = w->cls + model->features;
     const float *tabs = rope_tables(w, T);
-    const size_t used = busy_bytes(dev->pool);
-    const size_t room = dev->pool.budget > used ? dev->pool.budget - used : 0;
-    int batch = n;
-    while (batch > 1 && predict_batch_bytes(w, model, batch) > room) batch = (batch + 1) / 2;
-    if (predict_batch_bytes(w, model, batch) > room)
-        throw BudgetError{"graphics card: one row does not fit the working-memory budget"};
+    const int batch = batch_rows(dev, n, [&](int k) { return predict_batch_bytes(w, model, k); });
     for (int r0 = 0; r0 < n; r0 += batch) {
         const int k = std::min(batch, n - r0);
         Loans loans(dev);

@@ -9,7 +9,6 @@ problem's in-context stage (`tah_in_context`), which hands back every layer's st
 """
 from __future__ import annotations
 
-import ctypes
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -106,12 +105,7 @@ def fit_raw(gpu, weights, x, y, classes: int, chunk: int = 256, kv_format: int =
     plan = Plan.new(m.max_classes, y, classes)
     digits = len(plan.bases)
     ind_scales = np.stack([query_scale(b, rows) for b in m.col_a1]).astype(F)
-    col_kv = np.empty((features, digits, len(m.col_a2), 2, m.e, m.inds), F)
-    reps = np.empty((rows, m.d), F)
-    bases = (ctypes.c_int32 * digits)(*plan.bases)
-    gpu._check(gpu._l.tah_fit_represent(gpu._h, weights._h, x.ctypes.data_as(abi.F32P), y.ctypes.data_as(abi.F32P),
-                                        rows, features, bases, digits, ind_scales.ctypes.data_as(abi.F32P),
-                                        col_kv.ctypes.data_as(abi.F32P), reps.ctypes.data_as(abi.F32P)))
+    col_kv, reps = gpu.fit_represent(weights, x, y, plan.bases, ind_scales)
     fitted = Fitted(rows, features, classes, chunk, kv_format, plan, col_kv)
     for node in plan.nodes:
         n_rows = rows if node.rows is None else len(node.rows)

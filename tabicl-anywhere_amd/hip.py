@@ -177,6 +177,27 @@ class Gpu:
                                                  ctypes.c_void_p(out_ptr)))
 
     # ---- fitting: fit::Attend (src/fit.rs:45-74) ---------------------------------------------------------------
+    def fit_represent(self, weights: "GpuWeights", x, y, bases, ind_scales):
+        """The column and row stages of a fit with the cells kept on the card (`Attend::columns` + `Attend::rows`):
+        x [rows][features] normalised, y [rows] class indices or standardised targets, `bases` the label digits'
+        bases, ind_scales [col_blocks][e] each block's query scale for the inducing points. Returns
+        (col_kv [features][digits][blocks][2][e][inds], reps [rows][d])."""
+        m = weights.model
+        x, y = _f32(x), _f32(y).reshape(-1)
+        if x.ndim != 2 or y.size != x.shape[0]:
+            raise ValueError("fit_represent: x must be [rows][features] and y [rows]")
+        rows, features = x.shape
+        digits = len(bases)
+        ind_scales = _f32(ind_scales)
+        if ind_scales.size != len(m.col_a1) * m.e:
+            raise ValueError(f"fit_represent: ind_scales must be [{len(m.col_a1)}][{m.e}]")
+        col_kv = np.empty((features, digits, len(m.col_a2), 2, m.e, m.inds), np.float32)
+        reps = np.empty((rows, m.d), np.float32)
+        b = (ctypes.c_int32 * digits)(*[int(v) for v in bases])
+        self._check(self._l.tah_fit_represent(self._h, weights._h, _fp(x), _fp(y), rows, features, b, digits,
+                                              _fp(ind_scales), _fp(col_kv), _fp(reps)))
+        return col_kv, reps
+
     def quantile_stats(self, q, alphas) -> np.ndarray:
         """Per row of a regression member's outputs `q` ([rows][n] predicted quantiles), the row read as a
         distribution (`QuantileDist`, `src/table.rs:292-346`): [rows][3 + len(alphas)] float32 holding the mean, the

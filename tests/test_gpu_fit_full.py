@@ -66,16 +66,19 @@ def test_fit_tiny_matches_reference(gpu, tiny_model, tiny_raw):
     assert np.abs(scores - tiny_raw.f32s("logits").reshape(16, 3)).max() < TOL
 
 
-def compare_fits(got, want, kv_format, tol_scale=1.0):
+def compare_fits(got, want, kv_format):
+    """Two fits of a small model (two in-context layers) compared whole, at the absolute tolerance."""
     assert got.plan.bases == want.plan.bases and len(got.layers) == len(want.layers)
     err = np.abs(got.col_kv - want.col_kv).max()
-    assert err < TOL * tol_scale * max(1.0, np.abs(want.col_kv).max()), err
+    say("  column cache worst", err)
+    assert err < TOL, err
     for ni in range(len(want.layers)):
         assert np.abs(got.scales[ni] - want.scales[ni]).max() <= 2e-7 * max(1.0, np.abs(want.scales[ni]).max())
         for l in range(len(want.layers[ni])):
             if kv_format == abi.KV_F32:
                 a, b = got.layers[ni][l].view(np.float32), want.layers[ni][l].view(np.float32)
-                assert np.abs(a - b).max() < TOL * tol_scale * max(1.0, np.abs(b).max()), (ni, l)
+                say(f"  node {ni} layer {l} keys/values worst", np.abs(a - b).max())
+                assert np.abs(a - b).max() < TOL, (ni, l)
 
 
 def test_fit_many_classes_with_label_digits(gpu, tiny_model):
@@ -111,23 +114,41 @@ def test_fit_regression_model(gpu):
     assert np.abs(predict_card(gpu, w, got, xt) - orc.predict_raw(m, want, xt)).max() < TOL
 
 
-@pytest.mark.parametrize("kv_format", [abi.KV_F32, abi.KV_I16])
-def test_fit_full_size(gpu, kv_format):
+def test_fit_full_size(gpu):
     """The full-size architecture (3 column blocks over 128 inducing points, 3 row blocks, 12 in-context layers)
-    fitted on the card for 700 rows x 16 features, against the oracle; then predictions from both caches."""
-    say(f"fit full fmt={kv_format}")
+    fitted on the card for 700 rows x 16 features: the whole column cache against the oracle's column stage, every
+    row's representation, and every layer's keys and values of every row recomputed from the card's own records of
+    the layer before; then the i16 fit of the same table is the quantiser applied to the f32 one, bit for bit, and
+    predictions from both caches agree with the oracle's over the same caches."""
+    import workloads as W
+
+    say("fit full 700 x 16")
     m = M.Model.random(M.FULL_CLASSIFIER, seed=2)
     rng = np.random.default_rng(16)
-    x = rng.standard_normal((700, 16)).astype(np.float32)
-    y = np.argmax(x[:, :10] + 0.5 * rng.standard_normal((700, 10)), axis=1).astype(np.float32)
+    rows, features, chunk = 700, 16, 256
+    x = rng.standard_normal((rows, features)).astype(np.float32)
+    y = np.argmax(x[:, :10] + 0.5 * rng.standard_normal((rows, 10)), axis=1).astype(np.float32)
     w = gpu.weights(m)
-    got = fit.fit_raw(gpu, w, x, y, 10, chunk=256, kv_format=kv_format)
-    want = orc.fit_raw(m, x, y, 10, chunk=256, kv_format=kv_format)
-    say("  col_kv worst", np.abs(got.col_kv - want.col_kv).max())
-    compare_fits(got, want, kv_format, tol_scale=4.0)
+    plan, col_kv, reps, h, scales, layers = W.fit_pieces(gpu, w, m, x, y, 10, chunk, abi.KV_F32)
+    want_col, emb = orc.fit_columns(m, x, y, plan.bases, chunk)
+    err = np.abs(col_kv - want_col).max()
+    say("  column cache worst", err)
+    assert err < TOL
+    err = np.abs(reps - orc.fit_rows(m, orc.fit_cells_rows(m, col_kv, plan.bases, x, y))).max()
+    say("  representations worst", err)
+    assert err < TOL
+    W.check_layers(m, h, layers, scales, rows, chunk, np.arange(rows), TOL, say)
+    fq = fit.fit_raw(gpu, w, x, y, 10, chunk=chunk, kv_format=abi.KV_I16)
+    for l in range(m.icl_layers):
+        rec = layers[l].view(np.float32)
+        want = np.concatenate([orc.pack(rec[2 * m.d * c0:2 * m.d * (c0 + min(chunk, rows - c0))], m.d,
+                                        min(chunk, rows - c0), abi.KV_I16) for c0 in range(0, rows, chunk)])
+        assert np.array_equal(fq.layers[0][l], want), l
     xt = rng.standard_normal((16, 16)).astype(np.float32)
-    a = predict_card(gpu, w, got, xt)
-    b = orc.predict_raw(m, want, xt)
-    tol = TOL if kv_format == abi.KV_F32 else 5e-3
-    say("  scores worst", np.abs(a - b).max(), "scale", np.abs(b).max())
-    assert np.abs(a - b).max() < tol * max(1.0, np.abs(b).max())
+    for fmt, lay in ((abi.KV_F32, layers), (abi.KV_I16, fq.layers[0])):
+        fo = W.fitted_of(plan, col_kv, scales, lay, rows, features, 10, chunk, fmt)
+        f = fit.Fitted(rows, features, 10, chunk, fmt, plan, col_kv, [scales], [lay])
+        a = predict_card(gpu, w, f, xt)
+        b = orc.predict_raw(m, fo, xt)
+        say(f"  format {fmt}: scores worst", np.abs(a - b).max())
+        assert np.abs(a - b).max() < TOL

@@ -187,4 +187,4 @@ def test_stage_full_size(gpu, full_model, full_weights, kv_format, nq):
     vm.free()
     err = np.abs(got - want).max()
     say("  worst", err, "scale", np.abs(want).max())
-    assert err < SCORE_TOL * max(1.0, np.abs(want).max())
+    assert err < SCORE_TOL

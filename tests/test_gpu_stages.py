@@ -106,9 +106,17 @@ def test_stages_full_size(gpu, full_model, full_weights, features, n):
                         col_kv, [scales], [layers])
     tok = gpu.embed(full_weights, vm, x)
     want_tok = orc.embed(m, fitted, x)
-    err = np.abs(tok - want_tok).max()
-    say("  embed worst", err, "scale", np.abs(want_tok).max())
-    assert err < TOL * max(1.0, np.abs(want_tok).max())
+    plain = [r for r in range(n) if r != 2 or n <= 2]
+    err = np.abs(tok[plain] - want_tok[plain]).max()
+    say("  embed worst", err, "(rows without the -100 sentinel)")
+    assert err < TOL
+    if n > 2:
+        # the sentinel row's cells are -100 and their blocks' layer norms cancel most of their bits: the same
+        # arithmetic in another order differs in the last bits of numbers near 100, so that row is compared
+        # relative to its size
+        rel = (np.abs(tok[2] - want_tok[2]) / np.maximum(1.0, np.abs(want_tok[2]))).max()
+        say("  embed, -100 row: worst relative", rel)
+        assert rel < TOL
     rep = gpu.represent(full_weights, want_tok)
     want_rep = orc.represent(m, want_tok)
     err = np.abs(rep - want_rep).max()
@@ -118,7 +126,7 @@ def test_stages_full_size(gpu, full_model, full_weights, features, n):
     want = orc.predict_raw(m, fitted, x)
     err = np.abs(scores - want).max()
     say("  predict worst", err, "scale", np.abs(want).max())
-    assert err < TOL * max(1.0, np.abs(want).max())
+    assert err < TOL
 
 
 def test_stages_many_cells(gpu, full_model, full_weights):
@@ -141,7 +149,7 @@ def test_stages_many_cells(gpu, full_model, full_weights):
     want_tok = orc.embed(m, fitted, x)
     err = np.abs(tok - want_tok).max()
     say("  embed worst", err, "scale", np.abs(want_tok).max())
-    assert err < TOL * max(1.0, np.abs(want_tok).max())
+    assert err < TOL
     rep = gpu.represent(full_weights, want_tok)
     want_rep = orc.represent(m, want_tok)
     err = np.abs(rep - want_rep).max()

@@ -48,6 +48,44 @@ def test_in_context_cache_matches_reference(tiny_model, tiny_raw, tiny_fit):
                 assert np.abs(chunk - want[:, c0:c0 + rc]).max() < 2.5 * TINY, (kind, l, c0)
 
 
+def test_layer_by_layer_cache_matches_reference(tiny_model, tiny_raw):
+    """The per-layer pieces the large-fit tests recompute sampled rows with: keys and values of given rows
+    (`kv_rows`) and one in-context layer over stored records (`icl_step`), from the reference's own row
+    representations, against its golden in-context cache of both layers."""
+    m = tiny_model
+    d, n = m.d, 120
+    y = tiny_raw.i32s("y_train").astype(np.float32)
+    h = tiny_raw.f32s("train_rep").reshape(n, d).copy()
+    m.add_y(m.t["icl_y"], y, h)
+    scales = np.stack([orc.query_scale(b, n) for b in m.icl])
+    for l in range(m.icl_layers):
+        kv = orc.kv_rows(m, l, h)
+        for which, kind in enumerate(["icl_k", "icl_v"]):
+            want = to_ours(tiny_raw.f32s(f"{kind}{l}"), m.icl_heads, n, d // m.icl_heads)
+            assert np.abs(kv[:, which * d:(which + 1) * d].T - want).max() < 2.5 * TINY, (kind, l)
+        # the layer's stored records (f32, chunks of 48) from these keys and values, then every row through it
+        rec = np.concatenate([np.ascontiguousarray(np.concatenate([kv[c0:c0 + 48, :d].T, kv[c0:c0 + 48, d:].T]))
+                              .astype(np.float32).reshape(-1).view(np.uint8) for c0 in range(0, n, 48)])
+        h = orc.icl_step(m, l, scales[l], rec, abi.KV_F32, n, 48, h)
+
+
+@pytest.mark.parametrize("bases,classes", [([3], 3), ([4, 4], 14)])
+def test_column_stage_pieces_agree_with_the_whole(tiny_model, bases, classes):
+    """The column stage for a subset of feature groups, and the cells of sampled rows from a fitted column cache,
+    are the whole stage's numbers bit for bit (groups are independent; a row's cells depend only on its own inputs
+    and its groups' caches), with label digits and a -100 row included."""
+    m = tiny_model
+    rng = np.random.default_rng(len(bases))
+    x = rng.standard_normal((150, 6)).astype(np.float32)
+    x[3, :] = -100.0
+    y = rng.integers(0, classes, 150).astype(np.float32)
+    col, emb = orc.fit_columns(m, x, y, bases, 32)
+    col2, emb2 = orc.fit_columns_of(m, x, y, [4, 1], bases, 32)
+    assert np.array_equal(col2, col[[4, 1]]) and np.array_equal(emb2, emb[[4, 1]])
+    rows = [0, 3, 77, 149]
+    assert np.array_equal(orc.fit_cells_rows(m, col, bases, x[rows], y[rows]), emb[:, rows])
+
+
 def test_prediction_stages_match_reference(tiny_model, tiny_raw, tiny_fit):
     m = tiny_model
     xt = tiny_raw.f32s("x_test").reshape(16, 7)
