@@ -192,6 +192,40 @@ int tah_fit_represent(tah_dev *dev, const tah_weights *w, const float *x, const 
                       int32_t features, const int32_t *bases, int32_t digits, const float *ind_scales,
                       float *col_kv_out, float *reps_out);
 
+/* The fit hooks one at a time, with the trait's own layouts, for an unmodified fit_raw_async (src/fit.rs:425-545).
+ *
+ * Attend::column_batch (src/fit.rs:54, Gpu src/gpu.rs:1502-1510): how many feature groups of `rows` training cells
+ * tah_columns takes per call within the working-memory budget left now; 0 when the column stage is not offered
+ * (weights uploaded without the fitting blocks, or not even one group fits). */
+size_t tah_column_batch(const tah_dev *dev, const tah_weights *w, int32_t rows);
+/* Attend::columns (src/fit.rs:57, Gpu src/gpu.rs:1512-1614): the column stage for `groups` feature groups at once
+ * (one label digit). cells [rows][groups][e] holds their training cells through the input layer with the target's
+ * embedding added, and is replaced by the cells after the stage; ind_q [col_blocks][inds][e] is each block's
+ * inducing-point queries (scaled); rec receives what col_kv stores for these groups,
+ * [groups][col_blocks][2][e][inds]. More groups than tah_column_batch allows fail with TAH_E_BUDGET. */
+int tah_columns(tah_dev *dev, const tah_weights *w, float *cells, int32_t rows, int32_t groups, const float *ind_q,
+                float *rec);
+/* Attend::row_batch (src/fit.rs:60, Gpu src/gpu.rs:1616-1622): how many rows of `features` cells tah_rows takes per
+ * call; 0 when the row stage is not offered. */
+size_t tah_row_batch(const tah_dev *dev, const tah_weights *w, int32_t features);
+/* Attend::rows (src/fit.rs:63, Gpu src/gpu.rs:1624-1648): the row stage for n rows, cells [n][features][e] (after
+ * the column stage) to reps [n][d]. */
+int tah_rows(tah_dev *dev, const tah_weights *w, const float *cells, int32_t n, int32_t features, float *reps);
+/* Attend::attend_fits (src/fit.rs:50, Gpu src/gpu.rs:1498-1500): 1 if tah_attend can take a layer of `rows` rows of
+ * width d within the working-memory budget, else 0 (the CPU then does that attention). */
+int tah_attend_fits(const tah_dev *dev, int32_t rows, int32_t d);
+/* Gpu::attend_rows (src/gpu.rs:1306-1322): attention outputs [nq][d] of queries q [nq][d] (already scaled) over keys
+ * k and values v, each row-major [n][d], in full precision. */
+int tah_attend_rows(tah_dev *dev, const float *q, const float *k, const float *v, int32_t nq, int32_t n, int32_t d,
+                    int32_t heads, float *out);
+/* Gpu::calibrate (src/gpu.rs:1355-1383): how fast this card does the in-context attention, in multiply-adds per
+ * second: the best of repeated runs (at least three, then for about `ms` milliseconds) of 256 queries over 2,048 keys
+ * (d = 512, 8 heads), timed from host buffers to host buffers. */
+int tah_calibrate(tah_dev *dev, double ms, double *rate);
+/* Gpu::stages (src/gpu.rs:744-746): fitting stages this device has done (each fit hook call it took; a
+ * tah_fit_represent call counts as two, the column and the row stage). */
+uint64_t tah_stages(const tah_dev *dev);
+
 /* Receives layer `layer`'s stored records (tah_kv_record summed over its chunks, in host memory valid for the
  * duration of the call) while the in-context stage is fitted; non-zero stops the fit with TAH_E_SINK. */
 typedef int (*tah_layer_sink)(void *ctx, int32_t layer, const uint8_t *records, size_t bytes);

@@ -114,6 +114,15 @@ SIGNATURES = {
                                   ctypes.c_int32, F32P]),
     "tah_in_context": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, F32P, ctypes.c_int32, F32P, ctypes.c_int32,
                                       ctypes.c_int32, LAYER_SINK, ctypes.c_void_p]),
+    "tah_column_batch": (ctypes.c_size_t, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32]),
+    "tah_columns": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, F32P, ctypes.c_int32, ctypes.c_int32, F32P, F32P]),
+    "tah_row_batch": (ctypes.c_size_t, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32]),
+    "tah_rows": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, F32P, ctypes.c_int32, ctypes.c_int32, F32P]),
+    "tah_attend_fits": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32]),
+    "tah_attend_rows": (ctypes.c_int, [ctypes.c_void_p, F32P, F32P, F32P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                       ctypes.c_int32, F32P]),
+    "tah_calibrate": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_double, ctypes.POINTER(ctypes.c_double)]),
+    "tah_stages": (ctypes.c_uint64, [ctypes.c_void_p]),
     "tah_quantile_stats": (ctypes.c_int, [ctypes.c_void_p, F32P, ctypes.c_int32, ctypes.c_int32, F32P,
                                           ctypes.c_int32, F32P]),
     "tah_quantile_stats_dev": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, F32P,

@@ -1,6 +1,7 @@
 // The C ABI (include/tah.h): device handles, working memory, weights and fitted models on the card, and the
 // in-context passes built from the kernels. Host code only; every kernel lives in the other sources.
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstring>
 #include <initializer_list>
@@ -17,10 +18,11 @@ namespace tah {
 void *Pool::take(size_t want, int device) {
     want = (want + 255) & ~size_t(255);
     if (want == 0) want = 256;
-    // the smallest idle buffer that is big enough (and not absurdly bigger)
+    // the smallest idle buffer that is big enough and at most an eighth bigger (so a call's buffers never hold more
+    // than 9/8 of what it asked for, which the batch sizes allow for)
     int best = -1;
     for (size_t i = 0; i < bufs.size(); i++)
-        if (!bufs[i].busy && bufs[i].bytes >= want && bufs[i].bytes <= 2 * want + (size_t(1) << 20) &&
+        if (!bufs[i].busy && bufs[i].bytes >= want && bufs[i].bytes <= want + want / 8 &&
             (best < 0 || bufs[i].bytes < bufs[best].bytes))
             best = (int)i;
     if (best >= 0) {
@@ -85,6 +87,12 @@ static size_t busy_bytes(const Pool &p) {
     return b;
 }
 
+// The same for one buffer of `bytes` bytes.
+static size_t loan_raw(size_t bytes) {
+    const size_t want = (bytes + 255) & ~size_t(255);
+    return want + want / 8 + 256;
+}
+
 // Rows a call takes at a time: all n when their working memory fits the room the budget leaves, else the largest
 // halving of n that fits (rows are independent); an OutOfMemory error when not even one row fits.
 template <class F>
@@ -97,10 +105,14 @@ static int batch_rows(const tah_dev *dev, int n, F bytes_of) {
     return b;
 }
 
-// Bytes Loans takes for buffers of these many floats (each rounded to 256 bytes, with the pool's slack).
+// Bytes Loans may hold for buffers of these many floats: each rounded to 256 bytes, and up to an eighth more when
+// the pool hands out an idle buffer a little larger than asked.
 static size_t loan_bytes(std::initializer_list<size_t> floats) {
     size_t b = 0;
-    for (size_t f : floats) b += ((f * sizeof(float) + 255) & ~size_t(255)) + 256;
+    for (size_t f : floats) {
+        const size_t want = (f * sizeof(float) + 255) & ~size_t(255);
+        b += want + want / 8 + 256;
+    }
     return b;
 }
 
@@ -682,7 +694,7 @@ static void check_stage(const tah_weights *w, const tah_model *model, int nq, in
 static size_t stage_batch_bytes(const tah_weights *w, const tah_model *model, int k, int out_n) {
     const size_t kk = (size_t)k;
     return loan_bytes({kk * w->d, kk * out_n, kk * w->d, kk * w->d, kk * w->d, kk * stage_floats_wide(w)}) +
-           attention_work_bytes(shape_of(model, w->icl_heads, k)) + 256;
+           loan_raw(attention_work_bytes(shape_of(model, w->icl_heads, k)));
 }
 
 extern "C" int tah_stage_dev(tah_dev *dev, const tah_weights *w, const tah_model *model, const float *h_dev, int32_t nq,
@@ -807,6 +819,7 @@ extern "C" int tah_attend(tah_dev *dev, const float *q, const float *kv, int32_t
         attention(dev->stream, a, qd, reinterpret_cast<const uint8_t *>(kvd), od, work, imgp);
         TAH_HIP(hipMemcpyAsync(out, od, n * sizeof(float), hipMemcpyDeviceToHost, dev->stream));
         TAH_HIP(hipStreamSynchronize(dev->stream));
+        dev->stages++;
         return TAH_OK;
     });
 }
@@ -937,6 +950,7 @@ extern "C" int tah_in_context(tah_dev *dev, const tah_weights *w, const float *h
         const int rc = sink(ctx, L - 1, static_cast<const uint8_t *>(dev->pinned[(L - 1) & 1]), lbytes);
         TAH_HIP(hipStreamSynchronize(s));
         if (rc != 0) throw SinkError{rc};
+        dev->stages++;
         return TAH_OK;
     });
 }
@@ -1057,12 +1071,10 @@ extern "C" int tah_represent(tah_dev *dev, const tah_weights *w, const float *to
 static size_t predict_batch_bytes(const tah_weights *w, const tah_model *model, int k) {
     const int T = w->cls + model->features;
     const size_t kk = (size_t)k;
-    const size_t floats[] = {kk * T * w->e, kk * w->d, kk * model->features * w->e,
-                             column_stage_floats(w, k, model->features, model->digits), row_stage_floats(w, k, T),
-                             kk * w->d, kk * w->d, kk * w->d, kk * std::max(icl_mid(w), w->dec_hidden)};
-    size_t bytes = attention_work_bytes(shape_of(model, model->heads, k)) + 256;
-    for (size_t f : floats) bytes += align256(f * sizeof(float)) + 256;
-    return bytes;
+    return loan_bytes({kk * T * w->e, kk * w->d, kk * model->features * w->e,
+                       column_stage_floats(w, k, model->features, model->digits), row_stage_floats(w, k, T), kk * w->d,
+                       kk * w->d, kk * w->d, kk * std::max(icl_mid(w), w->dec_hidden)}) +
+           loan_raw(attention_work_bytes(shape_of(model, model->heads, k)));
 }
 
 // All three stages for n rows x (on the card) into out [n][out_n] (on the card), in sub-batches that fit the
@@ -1114,23 +1126,92 @@ extern "C" int tah_predict_rows(tah_dev *dev, const tah_weights *w, const tah_mo
 }
 
 // ---- the column and row stages of a fit (Attend::columns + Attend::rows, cells kept on the card) -----------------
+
+// Widest hidden layer of the column blocks' feed-forwards.
+static int column_ff(const tah_weights *w) {
+    int ff = 0;
+    for (auto &b : w->col_a1) ff = std::max(ff, b.ff);
+    for (auto &b : w->col_a2) ff = std::max(ff, b.ff);
+    return ff;
+}
+
+// Working buffers of the column blocks for a batch of g feature groups of `rows` cells each.
+struct ColumnBufs {
+    float *t, *q, *att, *mid, *acc, *hid, *ht, *hmid, *kv2;
+    void *work;
+};
+
+static size_t column_bufs_bytes(const tah_weights *w, int rows, int g) {
+    const size_t M = (size_t)g * rows, I = (size_t)g * w->inds, e = w->e, ff = column_ff(w);
+    return loan_bytes({M * e, M * e, M * e, M * std::max<size_t>(ff, 2 * e), I * e, I * e, I * e, I * ff, I * 2 * e}) +
+           loan_raw(ind_attention_work_bytes(w, rows, g));
+}
+
+static ColumnBufs column_bufs(const tah_weights *w, int rows, int g, Loans &loans) {
+    const size_t M = (size_t)g * rows, I = (size_t)g * w->inds, e = w->e, ff = column_ff(w);
+    ColumnBufs b;
+    b.t = loans.take<float>(M * e);
+    b.q = loans.take<float>(M * e);
+    b.att = loans.take<float>(M * e);
+    b.mid = loans.take<float>(M * std::max<size_t>(ff, 2 * e));
+    b.acc = loans.take<float>(I * e);
+    b.hid = loans.take<float>(I * e);
+    b.ht = loans.take<float>(I * e);
+    b.hmid = loans.take<float>(I * ff);
+    b.kv2 = loans.take<float>(I * 2 * e);
+    b.work = loans.take<uint8_t>(ind_attention_work_bytes(w, rows, g));
+    return b;
+}
+
+// Every column block for g feature groups whose cells (group-major [g][rows][e], through the input layer with the
+// target's embedding added) are in `cells`, in place (src/fit.rs:366-406): per block, the inducing points' queries
+// indq [blocks][inds][e] attend to the cells, the inducing points' output projection and feed-forward, their keys
+// and values for the second attention written to the column cache (col_kv + g0 * gstride + off + block's place),
+// then every cell through the block against them.
+static void column_blocks(hipStream_t s, const tah_weights *w, float *cells, int rows, int g, const float *indq,
+                          float *col_kv, size_t gstride, size_t off, int g0, const ColumnBufs &b) {
+    const int e = w->e, inds = w->inds, nb = w->col_blocks;
+    const size_t per = 2 * (size_t)e * inds, M = (size_t)g * rows, I = (size_t)g * inds;
+    for (int bi = 0; bi < nb; bi++) {
+        const DevBlock &a1 = w->col_a1[bi], &a2 = w->col_a2[bi];
+        // the inducing points look at this batch's cells (src/fit.rs:366-392)
+        layer_norm(s, (int)M, e, cells, e, a1.n1w, a1.n1b, b.t, e);
+        gemm(s, (int)M, 2 * e, e, b.t, e, a1.in_w + (size_t)e * e, a1.in_b + e, b.mid, 2 * e, EPI_NONE, nullptr, 0);
+        ind_attention(s, w, rows, g, indq + (size_t)bi * inds * e, b.mid, b.acc, b.work);
+        gemm(s, (int)I, e, e, b.acc, e, a1.out_w, a1.out_b, b.hid, e, EPI_NONE, nullptr, 0);
+        add_ind(s, I * e, inds, e, w->col_ind + (size_t)bi * inds * e, b.hid);
+        layer_norm(s, (int)I, e, b.hid, e, a1.n2w, a1.n2b, b.ht, e);
+        gemm(s, (int)I, a1.ff, e, b.ht, e, a1.l1w, a1.l1b, b.hmid, a1.ff, EPI_GELU, nullptr, 0);
+        gemm(s, (int)I, e, a1.ff, b.hmid, a1.ff, a1.l2w, a1.l2b, b.hid, e, EPI_RESID, b.hid, e);
+        // their keys and values for the second attention: what prediction reuses (src/fit.rs:393-403)
+        layer_norm(s, (int)I, e, b.hid, e, a2.n1w, a2.n1b, b.ht, e);
+        gemm(s, (int)I, 2 * e, e, b.ht, e, a2.in_w + (size_t)e * e, a2.in_b + e, b.kv2, 2 * e, EPI_NONE, nullptr, 0);
+        const size_t at = off + (size_t)bi * per;
+        col_records(s, g, inds, e, b.kv2, col_kv, gstride, at, g0);
+        // every cell against them (src/fit.rs:404-406)
+        column_block(s, w, a2, cells, rows, g, 1, rows, col_kv + (size_t)g0 * gstride + at, gstride, b.t, b.q, b.att,
+                     M * e * sizeof(float), b.mid);
+    }
+}
+
+static void check_fit_weights(const tah_weights *w) {
+    if (w->col_a1.empty() || w->col_a2.empty() || w->row.empty() || !w->col_ind || !w->col_scale)
+        throw ArgError{"fit: the weights lack the column or row stage (upload them with the fitting blocks)"};
+}
+
 extern "C" int tah_fit_represent(tah_dev *dev, const tah_weights *w, const float *x, const float *y, int32_t rows,
                                  int32_t features, const int32_t *bases, int32_t digits, const float *ind_scales,
                                  float *col_kv_out, float *reps_out) {
     if (!w || !x || !y || !bases || !ind_scales || !col_kv_out || !reps_out) return TAH_E_ARG;
     return guarded(dev, [&] {
         if (rows <= 0 || features <= 0 || digits <= 0) throw ArgError{"fit: bad rows, features or digits"};
-        if (w->col_a1.empty() || w->col_a2.empty() || w->row.empty() || !w->col_ind || !w->col_scale)
-            throw ArgError{"fit: the weights lack the column or row stage (upload them with the fitting blocks)"};
+        check_fit_weights(w);
         for (int i = 0; i < digits; i++)
             if (bases[i] <= 0) throw ArgError{"fit: label digit bases must be positive"};
         const int e = w->e, inds = w->inds, nb = w->col_blocks, d = w->d;
         const int T = w->cls + features;
         const size_t per = 2 * (size_t)e * inds, gstride = (size_t)digits * nb * per;
         hipStream_t s = dev->stream;
-        int ff = 0;
-        for (auto &b : w->col_a1) ff = std::max(ff, b.ff);
-        for (auto &b : w->col_a2) ff = std::max(ff, b.ff);
         Loans keep(dev);
         float *xd = keep.take<float>((size_t)rows * features), *yd = keep.take<float>(rows);
         float *sc = keep.take<float>((size_t)nb * e), *indq = keep.take<float>((size_t)nb * inds * e);
@@ -1154,33 +1235,18 @@ extern "C" int tah_fit_represent(tah_dev *dev, const tah_weights *w, const float
             query_modulate(s, inds, a1, sc + (size_t)bi * e, qb, qscr);
         }
         // feature groups in batches that fit the working memory
-        auto group_bytes = [&](int gb) {
-            const size_t M = (size_t)gb * rows, I = (size_t)gb * inds;
-            const size_t f[] = {M * e, M * e, M * e, M * std::max<size_t>(ff, 2 * e), digits > 1 ? M * e : 0,
-                                digits > 1 ? M * e : 0, I * e, I * e, I * e, I * ff, I * 2 * e};
-            size_t b = ind_attention_work_bytes(w, rows, gb) + 256;
-            for (size_t v : f) b += align256(v * sizeof(float)) + 256;
-            return b;
-        };
-        size_t used = 0;
-        for (auto &b : dev->pool.bufs)
-            if (b.busy) used += b.bytes;
-        const size_t room = dev->pool.budget > used ? dev->pool.budget - used : 0;
-        int gb = features;
-        while (gb > 1 && group_bytes(gb) > room) gb = (gb + 1) / 2;
-        if (group_bytes(gb) > room) throw BudgetError{"graphics card: one feature group does not fit the working-memory budget"};
+        const int gb = batch_rows(dev, features, [&](int g) {
+            const size_t M = (size_t)g * rows;
+            return column_bufs_bytes(w, rows, g) + (digits > 1 ? loan_bytes({M * e, M * e}) : 0);
+        });
         for (int g0 = 0; g0 < features; g0 += gb) {
             const int g = std::min(gb, features - g0);
-            const size_t M = (size_t)g * rows, I = (size_t)g * inds;
+            const size_t M = (size_t)g * rows;
             Loans loans(dev);
             float *cells = emb + (size_t)g0 * rows * e;
-            float *t = loans.take<float>(M * e), *q = loans.take<float>(M * e), *att = loans.take<float>(M * e);
-            float *mid = loans.take<float>(M * std::max<size_t>(ff, 2 * e));
+            const ColumnBufs cb = column_bufs(w, rows, g, loans);
             float *plain = digits > 1 ? loans.take<float>(M * e) : nullptr;
             float *sum = digits > 1 ? loans.take<float>(M * e) : nullptr;
-            float *acc = loans.take<float>(I * e), *hid = loans.take<float>(I * e), *ht = loans.take<float>(I * e);
-            float *hmid = loans.take<float>(I * ff), *kv2 = loans.take<float>(I * 2 * e);
-            void *work = loans.take<uint8_t>(ind_attention_work_bytes(w, rows, g));
             fit_cells(s, w, xd, rows, features, g0, g, cells);
             if (digits > 1) {
                 TAH_HIP(hipMemcpyAsync(plain, cells, M * e * sizeof(float), hipMemcpyDeviceToDevice, s));
@@ -1191,42 +1257,16 @@ extern "C" int tah_fit_represent(tah_dev *dev, const tah_weights *w, const float
                 int divisor = 1;
                 for (int k = dg + 1; k < digits; k++) divisor *= bases[k];
                 add_y_cells(s, w, yd, rows, g, digits, divisor, bases[dg], cells);
-                for (int bi = 0; bi < nb; bi++) {
-                    const DevBlock &a1 = w->col_a1[bi], &a2 = w->col_a2[bi];
-                    // the inducing points look at this batch's cells (src/fit.rs:366-392)
-                    layer_norm(s, (int)M, e, cells, e, a1.n1w, a1.n1b, t, e);
-                    gemm(s, (int)M, 2 * e, e, t, e, a1.in_w + (size_t)e * e, a1.in_b + e, mid, 2 * e, EPI_NONE, nullptr, 0);
-                    ind_attention(s, w, rows, g, indq + (size_t)bi * inds * e, mid, acc, work);
-                    gemm(s, (int)I, e, e, acc, e, a1.out_w, a1.out_b, hid, e, EPI_NONE, nullptr, 0);
-                    add_ind(s, I * e, inds, e, w->col_ind + (size_t)bi * inds * e, hid);
-                    layer_norm(s, (int)I, e, hid, e, a1.n2w, a1.n2b, ht, e);
-                    gemm(s, (int)I, a1.ff, e, ht, e, a1.l1w, a1.l1b, hmid, a1.ff, EPI_GELU, nullptr, 0);
-                    gemm(s, (int)I, e, a1.ff, hmid, a1.ff, a1.l2w, a1.l2b, hid, e, EPI_RESID, hid, e);
-                    // their keys and values for the second attention: what prediction reuses (src/fit.rs:393-403)
-                    layer_norm(s, (int)I, e, hid, e, a2.n1w, a2.n1b, ht, e);
-                    gemm(s, (int)I, 2 * e, e, ht, e, a2.in_w + (size_t)e * e, a2.in_b + e, kv2, 2 * e, EPI_NONE, nullptr, 0);
-                    const size_t off = ((size_t)dg * nb + bi) * per;
-                    col_records(s, g, inds, e, kv2, col_kv, gstride, off, g0);
-                    // every cell against them (src/fit.rs:404-406)
-                    column_block(s, w, a2, cells, rows, g, 1, rows, col_kv + (size_t)g0 * gstride + off, gstride, t, q, att,
-                                 M * e * sizeof(float), mid);
-                }
+                column_blocks(s, w, cells, rows, g, indq, col_kv, gstride, (size_t)dg * nb * per, g0, cb);
                 if (digits > 1) add_to(s, M * e, cells, sum);
             }
             if (digits > 1) scale_by(s, M * e, sum, 1.0f / (float)digits, cells);
         }
         // the row stage in batches of rows (src/fit.rs:516-539)
         const float *tabs = rope_tables(w, T);
-        size_t used2 = 0;
-        for (auto &b : dev->pool.bufs)
-            if (b.busy) used2 += b.bytes;
-        const size_t room2 = dev->pool.budget > used2 ? dev->pool.budget - used2 : 0;
-        auto row_bytes = [&](int rb) {
-            return align256(sizeof(float) * (size_t)rb * T * e) + align256(sizeof(float) * row_stage_floats(w, rb, T)) + 512;
-        };
-        int rb = rows;
-        while (rb > 1 && row_bytes(rb) > room2) rb = (rb + 1) / 2;
-        if (row_bytes(rb) > room2) throw BudgetError{"graphics card: one row does not fit the working-memory budget"};
+        const int rb = batch_rows(dev, rows, [&](int k) {
+            return loan_bytes({(size_t)k * T * e, row_stage_floats(w, k, T)});
+        });
         for (int r0 = 0; r0 < rows; r0 += rb) {
             const int k = std::min(rb, rows - r0);
             Loans loans(dev);
@@ -1238,6 +1278,194 @@ extern "C" int tah_fit_represent(tah_dev *dev, const tah_weights *w, const float
         TAH_HIP(hipMemcpyAsync(col_kv_out, col_kv, sizeof(float) * features * gstride, hipMemcpyDeviceToHost, s));
         TAH_HIP(hipMemcpyAsync(reps_out, reps, sizeof(float) * rows * d, hipMemcpyDeviceToHost, s));
         TAH_HIP(hipStreamSynchronize(s));
+        dev->stages += 2;  // the column and the row stage
         return TAH_OK;
     });
 }
+
+// ---- the fit hooks one at a time, as fit::Attend offers them (src/fit.rs:45-74) ----------------------------------
+
+// Bytes a tah_columns call borrows for g groups of `rows` cells.
+static size_t columns_call_bytes(const tah_weights *w, int rows, int g) {
+    const size_t M = (size_t)g * rows, e = w->e, nb = w->col_blocks;
+    return column_bufs_bytes(w, rows, g) + loan_bytes({M * e, M * e, (size_t)g * nb * 2 * e * w->inds, nb * w->inds * e});
+}
+
+// Bytes a tah_rows call borrows for n rows of `features` cells.
+static size_t rows_call_bytes(const tah_weights *w, int n, int features) {
+    const size_t T = (size_t)w->cls + features, k = n;
+    return loan_bytes({k * features * w->e, k * T * w->e, k * w->d, row_stage_floats(w, n, (int)T)});
+}
+
+// The room the budget leaves now, read under the device's lock.
+static size_t room_of(const tah_dev *dev_) {
+    auto *dev = const_cast<tah_dev *>(dev_);
+    std::lock_guard<std::mutex> g(dev->lock);
+    const size_t used = busy_bytes(dev->pool);
+    return dev->pool.budget > used ? dev->pool.budget - used : 0;
+}
+
+// The largest count up to cap whose bytes (growing with the count) fit the room; 0 if not even one does.
+template <class F>
+static size_t largest_fitting(size_t room, int cap, F bytes_of) {
+    int lo = 0, hi = std::max(cap, 1);  // lo fits (or is 0), everything above hi is out of reach
+    while (lo < hi) {
+        const int mid = lo + (hi - lo + 1) / 2;
+        if (bytes_of(mid) <= room)
+            lo = mid;
+        else
+            hi = mid - 1;
+    }
+    return (size_t)lo;
+}
+
+extern "C" size_t tah_column_batch(const tah_dev *dev, const tah_weights *w, int32_t rows) {
+    if (!dev || !w || rows <= 0 || w->col_a1.empty() || w->col_a2.empty() || !w->col_ind || !w->col_scale) return 0;
+    // a batch's cells are one launch's rows at most
+    const int cap = (int)std::min<long>(4096, std::max<long>(1, 0x7FFFFFFFL / ((long)rows * w->e)));
+    return largest_fitting(room_of(dev), cap, [&](int g) { return columns_call_bytes(w, rows, g); });
+}
+
+extern "C" int tah_columns(tah_dev *dev, const tah_weights *w, float *cells, int32_t rows, int32_t groups,
+                           const float *ind_q, float *rec) {
+    if (!w || !cells || !ind_q || !rec) return TAH_E_ARG;
+    return guarded(dev, [&] {
+        if (rows <= 0 || groups <= 0) throw ArgError{"columns: bad rows or groups"};
+        check_fit_weights(w);
+        const size_t room = dev->pool.budget > busy_bytes(dev->pool) ? dev->pool.budget - busy_bytes(dev->pool) : 0;
+        if (columns_call_bytes(w, rows, groups) > room)
+            throw BudgetError{"graphics card: these feature groups do not fit the working-memory budget "
+                              "(tah_column_batch says how many do)"};
+        const int e = w->e, inds = w->inds, nb = w->col_blocks;
+        const size_t M = (size_t)groups * rows, per = 2 * (size_t)e * inds, gstride = (size_t)nb * per;
+        hipStream_t s = dev->stream;
+        Loans loans(dev);
+        float *by_row = loans.take<float>(M * e), *by_group = loans.take<float>(M * e);
+        float *rec_d = loans.take<float>((size_t)groups * gstride), *indq = loans.take<float>((size_t)nb * inds * e);
+        const ColumnBufs cb = column_bufs(w, rows, groups, loans);
+        TAH_HIP(hipMemcpyAsync(by_row, cells, M * e * sizeof(float), hipMemcpyHostToDevice, s));
+        TAH_HIP(hipMemcpyAsync(indq, ind_q, (size_t)nb * inds * e * sizeof(float), hipMemcpyHostToDevice, s));
+        regroup(s, rows, groups, e, by_row, by_group, true);
+        column_blocks(s, w, by_group, rows, groups, indq, rec_d, gstride, 0, 0, cb);
+        regroup(s, rows, groups, e, by_group, by_row, false);
+        TAH_HIP(hipMemcpyAsync(cells, by_row, M * e * sizeof(float), hipMemcpyDeviceToHost, s));
+        TAH_HIP(hipMemcpyAsync(rec, rec_d, (size_t)groups * gstride * sizeof(float), hipMemcpyDeviceToHost, s));
+        TAH_HIP(hipStreamSynchronize(s));
+        dev->stages++;
+        return TAH_OK;
+    });
+}
+
+extern "C" size_t tah_row_batch(const tah_dev *dev, const tah_weights *w, int32_t features) {
+    if (!dev || !w || features <= 0 || w->row.empty() || !w->cls_tokens) return 0;
+    return largest_fitting(room_of(dev), 32768, [&](int n) { return rows_call_bytes(w, n, features); });
+}
+
+extern "C" int tah_rows(tah_dev *dev, const tah_weights *w, const float *cells, int32_t n, int32_t features,
+                        float *reps) {
+    if (!w || !cells || !reps) return TAH_E_ARG;
+    return guarded(dev, [&] {
+        if (n <= 0 || features <= 0) throw ArgError{"rows: bad row or feature count"};
+        if (w->row.empty() || !w->cls_tokens) throw ArgError{"weights lack the row stage"};
+        const size_t room = dev->pool.budget > busy_bytes(dev->pool) ? dev->pool.budget - busy_bytes(dev->pool) : 0;
+        if (rows_call_bytes(w, n, features) > room)
+            throw BudgetError{"graphics card: these rows do not fit the working-memory budget (tah_row_batch says how "
+                              "many do)"};
+        const int T = w->cls + features, e = w->e;
+        hipStream_t s = dev->stream;
+        const float *tabs = rope_tables(w, T);
+        Loans loans(dev);
+        float *cd = loans.take<float>((size_t)n * features * e), *tok = loans.take<float>((size_t)n * T * e);
+        float *rd = loans.take<float>((size_t)n * w->d), *scratch = loans.take<float>(row_stage_floats(w, n, T));
+        TAH_HIP(hipMemcpyAsync(cd, cells, sizeof(float) * n * features * e, hipMemcpyHostToDevice, s));
+        assemble_tokens(s, w, cd, n, features, tok);
+        row_stage(s, w, tok, n, T, tabs, tabs + (size_t)T * w->rope_half, rd, scratch);
+        TAH_HIP(hipMemcpyAsync(reps, rd, sizeof(float) * n * w->d, hipMemcpyDeviceToHost, s));
+        TAH_HIP(hipStreamSynchronize(s));
+        dev->stages++;
+        return TAH_OK;
+    });
+}
+
+// Bytes tah_attend (or tah_attend_rows with nq queries) borrows for keys and values of `rows` rows.
+static size_t attend_call_bytes(int nq, int rows, int d, int heads) {
+    const AttnShape a{nq, rows, 256, d, heads, TAH_KV_F32};
+    size_t b = loan_bytes({(size_t)nq * d, 2 * (size_t)rows * d, 2 * (size_t)rows * d, (size_t)nq * d}) +
+               loan_raw(attention_work_bytes(a));
+    if (nq >= 32 && kv_images_apply(TAH_KV_F32, d, heads)) b += loan_raw(kv_images_bytes(rows, 256, heads));
+    return b;
+}
+
+extern "C" int tah_attend_fits(const tah_dev *dev, int32_t rows, int32_t d) {
+    if (!dev || rows <= 0 || d <= 0) return 0;
+    const int heads = std::max(1, d / 64);  // head width 64 or less: what the attention kernels take
+    if (d % heads != 0 || d / heads > 64) return 0;
+    return attend_call_bytes(rows, rows, d, heads) <= dev->pool.budget ? 1 : 0;
+}
+
+// Attention outputs [nq][d] of queries q over row-major keys k and values v [n][d], all on the host.
+static void attend_rows_on(tah_dev *dev, const float *q, const float *k, const float *v, int nq, int n, int d, int heads,
+                           float *out) {
+    hipStream_t s = dev->stream;
+    Loans loans(dev);
+    const int chunk = 256;
+    float *qd = loans.take<float>((size_t)nq * d), *kv = loans.take<float>(2 * (size_t)n * d);
+    float *rec = loans.take<float>(2 * (size_t)n * d), *od = loans.take<float>((size_t)nq * d);
+    const AttnShape a{nq, n, chunk, d, heads, TAH_KV_F32};
+    void *work = loans.take<uint8_t>(attention_work_bytes(a));
+    TAH_HIP(hipMemcpyAsync(qd, q, sizeof(float) * nq * d, hipMemcpyHostToDevice, s));
+    // keys and values each in one contiguous upload (rec as staging), then side by side on the card, [n][2d], as the
+    // projection leaves them at fit
+    TAH_HIP(hipMemcpyAsync(rec, k, sizeof(float) * n * d, hipMemcpyHostToDevice, s));
+    TAH_HIP(hipMemcpyAsync(rec + (size_t)n * d, v, sizeof(float) * n * d, hipMemcpyHostToDevice, s));
+    TAH_HIP(hipMemcpy2DAsync(kv, 2 * d * sizeof(float), rec, d * sizeof(float), d * sizeof(float), n,
+                             hipMemcpyDeviceToDevice, s));
+    TAH_HIP(hipMemcpy2DAsync(kv + d, 2 * d * sizeof(float), rec + (size_t)n * d, d * sizeof(float), d * sizeof(float), n,
+                             hipMemcpyDeviceToDevice, s));
+    to_records(s, n, d, chunk, kv, rec);
+    KvImages img;
+    const KvImages *imgp = loan_images(s, loans, a, reinterpret_cast<const uint8_t *>(rec), img);
+    attention(s, a, qd, reinterpret_cast<const uint8_t *>(rec), od, work, imgp);
+    TAH_HIP(hipMemcpyAsync(out, od, sizeof(float) * nq * d, hipMemcpyDeviceToHost, s));
+    TAH_HIP(hipStreamSynchronize(s));
+}
+
+extern "C" int tah_attend_rows(tah_dev *dev, const float *q, const float *k, const float *v, int32_t nq, int32_t n,
+                               int32_t d, int32_t heads, float *out) {
+    if (!q || !k || !v || !out) return TAH_E_ARG;
+    return guarded(dev, [&] {
+        if (nq < 0 || n <= 0 || d <= 0 || heads <= 0 || d % heads) throw ArgError{"attend_rows: bad shape"};
+        if (nq > 0) attend_rows_on(dev, q, k, v, nq, n, d, heads, out);
+        return TAH_OK;
+    });
+}
+
+extern "C" int tah_calibrate(tah_dev *dev, double ms, double *rate) {
+    if (!rate) return TAH_E_ARG;
+    return guarded(dev, [&] {
+        const int nq = 256, n = 2048, d = 512, heads = 8;
+        // fixed pseudo-random inputs in [-0.5, 0.5): a 64-bit linear congruential sequence, top 24 bits
+        std::vector<float> q((size_t)nq * d), k((size_t)n * d), v((size_t)n * d), out((size_t)nq * d);
+        uint64_t st = 0x9E3779B97F4A7C15ull;
+        auto next = [&] {
+            st = st * 6364136223846793005ull + 1442695040888963407ull;
+            return (float)(st >> 40) / (float)(1u << 24) - 0.5f;
+        };
+        for (auto *vec : {&q, &k, &v})
+            for (float &x : *vec) x = next();
+        double best = 0.0, spent = 0.0;
+        for (int i = 0;; i++) {
+            const auto t0 = std::chrono::steady_clock::now();
+            attend_rows_on(dev, q.data(), k.data(), v.data(), nq, n, d, heads, out.data());
+            const double secs = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+            spent += secs;
+            // multiply-adds of the scores and of the weighted values
+            best = std::max(best, 2.0 * nq * n * d / std::max(secs, 1e-9));
+            if (i >= 2 && spent * 1e3 > ms) break;
+        }
+        *rate = best;
+        return TAH_OK;
+    });
+}
+
+extern "C" uint64_t tah_stages(const tah_dev *dev) { return dev ? dev->stages.load() : 0; }

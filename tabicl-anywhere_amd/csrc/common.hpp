@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstddef>
 #include <cstdint>
 #include <mutex>
@@ -69,6 +70,8 @@ struct tah_dev {
     std::string last_error;
     std::string name;
     tah::Pool pool;
+    // fitting stages the card has done (each call of a fit hook it took rather than declined)
+    std::atomic<uint64_t> stages{0};
     // this device's copy of the library's static scratch array (tah_stage_dev_noalloc), resolved at tah_open with
     // the device current: a device address, unlike the array's name in host code
     uint8_t *noalloc = nullptr;
@@ -260,6 +263,9 @@ void scale_by(hipStream_t s, size_t count, const float *src, float f, float *dst
 void add_to(hipStream_t s, size_t count, const float *x, float *sum);
 void add_ind(hipStream_t s, size_t count, int inds, int e, const float *ind, float *hid);
 void col_records(hipStream_t s, int gb, int inds, int e, const float *kv2, float *col_kv, size_t gstride, size_t off, int g0);
+// cells between the trait's row-major [rows][g][e] and the fit's group-major [g][rows][e] (to_group_major says which
+// way).
+void regroup(hipStream_t s, int rows, int g, int e, const float *src, float *dst, bool to_group_major);
 void tokens_gmajor(hipStream_t s, const tah_weights *w, int rb, int r0, int rows, int features, const float *emb, float *tok);
 size_t ind_attention_work_bytes(const tah_weights *w, int rows, int gb);
 void ind_attention(hipStream_t s, const tah_weights *w, int rows, int gb, const float *indq, const float *kv, float *out,

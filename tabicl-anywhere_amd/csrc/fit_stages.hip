@@ -221,6 +221,25 @@ __global__ __launch_bounds__(256) void k_tokens_gmajor(int rb, int r0, int rows,
     tok[i] = t < cls ? cls_tokens[t * e + o] : emb[((size_t)(t - cls) * rows + r0 + r) * e + o];
 }
 
+// One cell of e floats a thread group: [rows][g][e] <-> [g][rows][e].
+__global__ __launch_bounds__(256) void k_regroup(int rows, int g, int e, const float *__restrict__ src,
+                                                  float *__restrict__ dst, bool to_gmajor) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)rows * g * e) return;
+    const int o = (int)(i % e);
+    const size_t cell = i / e;  // in the destination's order
+    size_t r, gi;
+    if (to_gmajor) {
+        gi = cell / rows;
+        r = cell % rows;
+        dst[i] = src[(r * g + gi) * e + o];
+    } else {
+        r = cell / g;
+        gi = cell % g;
+        dst[i] = src[(gi * rows + r) * e + o];
+    }
+}
+
 void merge_splits(hipStream_t s, int nq, int d, int heads, int splits, const float *part_o, const float *part_ml,
                   float *out);
 
@@ -259,6 +278,12 @@ void add_ind(hipStream_t s, size_t count, int inds, int e, const float *ind, flo
 void col_records(hipStream_t s, int gb, int inds, int e, const float *kv2, float *col_kv, size_t gstride, size_t off, int g0) {
     const size_t count = (size_t)gb * 2 * e * inds;
     hipLaunchKernelGGL(k_col_records, blocks_of(count), dim3(256), 0, s, gb, inds, e, kv2, col_kv, gstride, off, g0);
+    TAH_LAUNCHED();
+}
+
+void regroup(hipStream_t s, int rows, int g, int e, const float *src, float *dst, bool to_group_major) {
+    const size_t count = (size_t)rows * g * e;
+    hipLaunchKernelGGL(k_regroup, blocks_of(count), dim3(256), 0, s, rows, g, e, src, dst, to_group_major);
     TAH_LAUNCHED();
 }
 

@@ -53,6 +53,36 @@ def gelu(x: np.ndarray) -> np.ndarray:
     return (F(0.5) * x * (F(1.0) + erf1(x * F(0.70710678118654752440)))).astype(F)
 
 
+def tanh1(x: np.ndarray) -> np.ndarray:
+    """`kern::tanh1` (`src/kern.rs:263-268`): tanh through one exponential, in float32."""
+    e = exp1(F(2.0) * np.clip(np.asarray(x, F), F(-10.0), F(10.0)))
+    return ((e - F(1.0)) / (e + F(1.0))).astype(F)
+
+
+def layer_norm(x: np.ndarray, w: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """`kern::layer_norm` (`src/kern.rs:326-347`) over the last axis: mean, then biased variance, eps 1e-5."""
+    x = np.asarray(x, F)
+    mean = (x.sum(axis=-1, keepdims=True, dtype=F) / F(x.shape[-1])).astype(F)
+    c = (x - mean).astype(F)
+    var = ((c * c).sum(axis=-1, keepdims=True, dtype=F) / F(x.shape[-1])).astype(F)
+    return (c * (F(1.0) / np.sqrt(var + F(1e-5))) * w + b).astype(F)
+
+
+def query(block, scale: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """`nn::query` (`src/nn.rs:130-152`) for rows x [n][d]: the scaled query projection of norm1(x), modulated per
+    head by the block's query MLP when it has one."""
+    t = block.t
+    d, hd = block.d, block.hd
+    q = (layer_norm(x, t["n1w"], t["n1b"]) @ t["in_w"].reshape(3 * d, d)[:d].T + t["in_b"][:d]).astype(F)
+    scale = np.asarray(scale, F)
+    if block.ss_hidden == 0:
+        return (q * scale).astype(F)
+    qh = q.reshape(-1, block.heads, hd)
+    hid = gelu(qh @ t["q0w"].reshape(block.ss_hidden, hd).T + t["q0b"])
+    mm = (hid @ t["q2w"].reshape(hd, block.ss_hidden).T + t["q2b"]).astype(F)
+    return (qh * (scale.reshape(block.heads, hd) * (F(1.0) + tanh1(mm)))).reshape(q.shape).astype(F)
+
+
 def query_scale(block, n: int) -> np.ndarray:
     """`Block::query_scale` (`src/nn.rs:97-107`): what every query of the block is multiplied by with n keys."""
     inv = F(1.0) / np.sqrt(F(block.hd))
@@ -65,6 +95,72 @@ def query_scale(block, n: int) -> np.ndarray:
     s = np.add.accumulate((w2 * hid[None, :]).astype(F), axis=1, dtype=F)[:, -1]
     out = (s + block.t["b2b"]).astype(F)
     return (out * inv).astype(F)
+
+
+def input_cells(m, x: np.ndarray, y: np.ndarray, g0: int, gn: int) -> np.ndarray:
+    """The training cells of feature groups g0.. g0 + gn, [rows][gn][e], as `fit_raw_async` builds them for the column
+    hook (`src/fit.rs:430-447`): each group's values one, two and four places to the right (`group_values`), the
+    input layer (a cell whose values are all -100 stays -100), then the target's embedding (`Model::add_y`)."""
+    rows, features = x.shape
+    e, group = m.e, m.group
+    w_in, b_in = m.t["in_w"].reshape(e, group), m.t["in_b"]
+    cells = np.empty((rows, gn, e), F)
+    for gi in range(gn):
+        vals = x[:, [(g0 + gi + (1 << k)) % features for k in range(group)]]
+        c = (vals @ w_in.T + b_in).astype(F)
+        c[np.all(vals == F(-100.0), axis=1)] = F(-100.0)
+        cells[:, gi] = c
+    table = m.t["col_y"]
+    if m.max_classes > 0:
+        cells += table.reshape(-1, e)[y.astype(np.intp)][:, None, :]
+    else:
+        tw = table.reshape(2, e)
+        cells += (tw[0][None, :] * y[:, None] + tw[1][None, :])[:, None, :]
+    return cells
+
+
+def fit_raw_hooks(gpu, weights, x, y, classes: int, chunk: int = 256, kv_format: int = abi.KV_F32) -> "Fitted":
+    """`fit_raw_async` (`src/fit.rs:285-752`) exactly as the reference drives an accelerator through `fit::Attend`:
+    the host builds each batch of feature groups' cells and the inducing points' queries, the card's `columns`
+    takes as many groups per call as `column_batch` allows, the host regroups the cells by feature, the card's
+    `rows` takes `row_batch` rows per call, and `in_context` fits every problem. The reference offers the column
+    hook for one label digit only; more digits go through `fit_raw` (the whole column stage on the card)."""
+    m = weights.model
+    x = np.ascontiguousarray(x, F)
+    y = np.ascontiguousarray(y, F)
+    rows, features = x.shape
+    chunk = max(int(chunk), 8)
+    plan = Plan.new(m.max_classes, y, classes)
+    if len(plan.bases) != 1:
+        raise ValueError("fit_raw_hooks: the column hook takes one label digit; use fit_raw for more")
+    e, nb = m.e, len(m.col_a2)
+    ind_q = np.stack([query(b, query_scale(b, rows), m.t["col_ind"].reshape(nb, m.inds, e)[i])
+                      for i, b in enumerate(m.col_a1)]).astype(F)
+    col_batch = gpu.column_batch(weights, rows)
+    row_batch = gpu.row_batch(weights, features)
+    if col_batch == 0 or row_batch == 0:
+        raise ValueError("fit_raw_hooks: the card does not offer the column or row stage at this size")
+    emb = np.empty((features, rows, e), F)  # the cells by feature group, as the reference keeps them between stages
+    col_kv = np.empty((features, 1, nb, 2, e, m.inds), F)
+    for g0 in range(0, features, col_batch):
+        gn = min(col_batch, features - g0)
+        cells = input_cells(m, x, y, g0, gn)
+        col_kv[g0:g0 + gn, 0] = gpu.columns(weights, cells, rows, gn, ind_q)
+        emb[g0:g0 + gn] = cells.transpose(1, 0, 2)
+    reps = np.empty((rows, m.d), F)
+    for r0 in range(0, rows, row_batch):
+        rn = min(row_batch, rows - r0)
+        reps[r0:r0 + rn] = gpu.rows(weights, np.ascontiguousarray(emb[:, r0:r0 + rn].transpose(1, 0, 2)))
+    fitted = Fitted(rows, features, classes, chunk, kv_format, plan, col_kv)
+    for node in plan.nodes:
+        h = reps.copy() if node.rows is None else reps[np.asarray(node.rows, np.int64)]
+        m.add_y(m.t["icl_y"], np.asarray(node.y, F), h)
+        scales = np.stack([query_scale(b, rows if node.rows is None else len(node.rows)) for b in m.icl]).astype(F)
+        layers = []
+        gpu.in_context_fit(weights, h, scales, kv_format, chunk, lambda l, rec: layers.append(rec.copy()))
+        fitted.scales.append(scales)
+        fitted.layers.append(layers)
+    return fitted
 
 
 @dataclass

@@ -177,6 +177,64 @@ class Gpu:
                                                  ctypes.c_void_p(out_ptr)))
 
     # ---- fitting: fit::Attend (src/fit.rs:45-74) ---------------------------------------------------------------
+    # the hooks one at a time (Attend::column_batch, columns, row_batch, rows, attend_fits; src/fit.rs:45-74)
+    def column_batch(self, weights: "GpuWeights", rows: int) -> int:
+        """Feature groups of `rows` cells `columns` takes per call (0: not offered)."""
+        return int(self._l.tah_column_batch(self._h, weights._h, int(rows)))
+
+    def columns(self, weights: "GpuWeights", cells, rows: int, groups: int, ind_q) -> np.ndarray:
+        """The column stage for `groups` feature groups: `cells` [rows][groups][e] (input layer and target embedding
+        applied) is replaced in place by the cells after the stage; returns what col_kv stores for the groups,
+        [groups][blocks][2][e][inds]. `ind_q` is each block's inducing-point queries, [blocks][inds][e]."""
+        m = weights.model
+        if not (isinstance(cells, np.ndarray) and cells.dtype == np.float32 and cells.flags.c_contiguous
+                and cells.size == rows * groups * m.e):
+            raise ValueError(f"columns: cells must be a contiguous float32 [rows][groups][{m.e}] array")
+        ind_q = _f32(ind_q)
+        if ind_q.size != len(m.col_a1) * m.inds * m.e:
+            raise ValueError(f"columns: ind_q must be [{len(m.col_a1)}][{m.inds}][{m.e}]")
+        rec = np.empty((groups, len(m.col_a2), 2, m.e, m.inds), np.float32)
+        self._check(self._l.tah_columns(self._h, weights._h, _fp(cells), int(rows), int(groups), _fp(ind_q), _fp(rec)))
+        return rec
+
+    def row_batch(self, weights: "GpuWeights", features: int) -> int:
+        """Rows of `features` cells `rows` takes per call (0: not offered)."""
+        return int(self._l.tah_row_batch(self._h, weights._h, int(features)))
+
+    def rows(self, weights: "GpuWeights", cells) -> np.ndarray:
+        """The row stage: cells [n][features][e] to representations [n][d]."""
+        m = weights.model
+        cells = _f32(cells)
+        if cells.ndim != 3 or cells.shape[2] != m.e:
+            raise ValueError(f"rows: cells must be [n][features][{m.e}]")
+        reps = np.empty((cells.shape[0], m.d), np.float32)
+        self._check(self._l.tah_rows(self._h, weights._h, _fp(cells), int(cells.shape[0]), int(cells.shape[1]), _fp(reps)))
+        return reps
+
+    def attend_fits(self, rows: int, d: int) -> bool:
+        return bool(self._l.tah_attend_fits(self._h, int(rows), int(d)))
+
+    def attend_rows(self, q, k, v, d: int, heads: int) -> np.ndarray:
+        """`Gpu::attend_rows`: attention outputs [nq][d] of scaled queries over row-major keys and values [n][d]."""
+        q, k, v = _rows_of(q, d, "attend_rows"), _rows_of(k, d, "attend_rows"), _rows_of(v, d, "attend_rows")
+        if k.shape != v.shape:
+            raise ValueError("attend_rows: keys and values must have the same shape")
+        out = np.empty((q.shape[0], d), np.float32)
+        self._check(self._l.tah_attend_rows(self._h, _fp(q), _fp(k), _fp(v), q.shape[0], k.shape[0], int(d), int(heads),
+                                            _fp(out)))
+        return out
+
+    def calibrate(self, ms: float = 100.0) -> float:
+        """`Gpu::calibrate`: the card's in-context attention rate in multiply-adds per second."""
+        rate = ctypes.c_double()
+        self._check(self._l.tah_calibrate(self._h, float(ms), ctypes.byref(rate)))
+        return rate.value
+
+    @property
+    def stages(self) -> int:
+        """Fitting stages the card has done (`Gpu::stages`)."""
+        return int(self._l.tah_stages(self._h))
+
     def fit_represent(self, weights: "GpuWeights", x, y, bases, ind_scales):
         """The column and row stages of a fit with the cells kept on the card (`Attend::columns` + `Attend::rows`):
         x [rows][features] normalised, y [rows] class indices or standardised targets, `bases` the label digits'
