@@ -35,9 +35,38 @@ sys.path.insert(0, ROOT)
 ROWS, FEATURES, CHUNK, BATCH, CLASSES = 10000, 100, 256, 2048, 10
 PEAK_F16_MFMA = 2.5e15  # MI355X dense fp16 matrix FLOP/s
 PEAK_SPLIT_F32 = PEAK_F16_MFMA / 3  # f32 work at three fp16 products per f32 product
+PEAK_HBM = 8.0e12  # MI355X HBM3E bytes/s
 # HBM bytes per launch of the roofline kernel, from rocprofv3 FETCH_SIZE and WRITE_SIZE runs of this bench scaled by
 # the counters' reading on its own 256 MiB copy (profiles/attention_f32_2048x10000_memory.md)
 TRAFFIC_BYTES = 75.6e6
+
+
+def pass_cost(model, n, rows=ROWS, features=FEATURES, kv_bytes=4):
+    """Algorithmic cost of one prediction pass of n rows against one member (one problem, one label digit):
+    (bytes, flops). Bytes: every in-context layer's stored keys and values read once (plus the per-chunk scales of
+    an integer cache), the column cache, the weights at f32, the rows in and the scores out. Flops: the in-context
+    attention (4 N d per row and layer), the in-context dense layers, the decoder, the column stage (3 blocks over the
+    128 inducing points per feature) and the row stage (3 blocks over T = cls + features tokens)."""
+    d, L, e, inds, cls = model.d, model.icl_layers, model.e, model.inds, model.cls
+    ff, heads, hd, T, C = 2 * d, model.icl_heads, d // model.icl_heads, cls + features, model.outputs
+    chunks = -(-rows // CHUNK)
+    kv = L * (2 * rows * d * kv_bytes + (chunks * 8 * d if kv_bytes < 4 else 0))
+    col = features * 3 * 2 * e * inds * 4
+    # the weights prediction reads: not the inducing points and their blocks (fit only), and of the column and
+    # in-context blocks only the query third of the input projection (their keys and values come from the caches)
+    def block_floats(b, query_only):
+        return sum(a.size // 3 if query_only and k in ("in_w", "in_b") else a.size for k, a in b.t.items())
+
+    weights = 4 * (sum(a.size for k, a in model.t.items() if k != "col_ind")
+                   + sum(block_floats(b, True) for b in model.col_a2 + model.icl)
+                   + sum(block_floats(b, False) for b in model.row))
+    nbytes = kv + col + weights + n * (features + C) * 4
+    per_row = (4 * rows * d * L
+               + 2 * L * (2 * d * d + 2 * d * ff + heads * 2 * hd * hd)
+               + 2 * (ff * d + C * ff)
+               + 2 * features * 3 * (6 * e * e + 2 * inds * e)
+               + 2 * (2 * T * (8 * e * e + 2 * T * e) + 2 * e * e * T + cls * (6 * e * e + 2 * T * e)))
+    return nbytes, n * per_row
 
 
 def log(*a):
@@ -126,6 +155,31 @@ def main():
         per_batch[str(n)] = round(n / (ms / 1e3), 1)
         log(f"prediction, {n} rows: {ms:.3f} ms, {per_batch[str(n)]:,.0f} rows/s")
     per_batch[str(BATCH)] = round(rows_s, 1)
+    # fractions of the roofline at each batch: the pass's algorithmic bytes at 8 TB/s and flops at the split-fp16
+    # ceiling, against the measured time (one row is HBM-bound, 64 rows and more MFMA-bound)
+    roof_by_batch = {}
+    for n_s, rps in per_batch.items():
+        n = int(n_s)
+        nbytes, flops = pass_cost(model, n)
+        t = n / rps
+        roof_by_batch[n_s] = {"hbm_frac": round(nbytes / PEAK_HBM / t, 4), "mfma_frac": round(flops / PEAK_SPLIT_F32 / t, 4),
+                              "bytes": nbytes, "flops": flops}
+
+    # one row after flushing the 256 MB MALL (a 1 GiB copy between runs), each cache format: the cold-cache latency
+    flush_a, flush_b = dm.DeviceBuffer(1 << 30), dm.DeviceBuffer(1 << 30)
+    cold = {}
+
+    def one_row_cold(vmx, label):
+        times = []
+        for _ in range(7):
+            dm.copy(flush_b, flush_a, 1 << 30)
+            timer.start()
+            gpu.predict_dev(w, vmx, x_dev.ptr, 1, CLASSES, out_dev.ptr)
+            times.append(timer.stop())
+        cold[label] = round(float(np.median(times)), 4)
+        log(f"prediction, 1 row after a MALL flush, {label} cache: {cold[label]:.3f} ms")
+
+    one_row_cold(vm, "f32")
 
     # ---- the same table with the cache quantised to i16 and to i8 (dequantised inside the kernels) -----------------
     per_cache = {"f32": round(rows_s, 1)}
@@ -142,7 +196,10 @@ def main():
         ms = timer.stop() / args.steps
         per_cache[name] = round(BATCH / (ms / 1e3), 1)
         log(f"prediction, {BATCH} rows, {name} cache: {ms:.3f} ms, {per_cache[name]:,.0f} rows/s")
+        one_row_cold(vq, name)
         vq.free()
+    flush_a.free()
+    flush_b.free()
 
     # ---- the in-context stage alone and its attention kernel ---------------------------------------------------
     rng = np.random.default_rng(5)
@@ -188,7 +245,7 @@ def main():
     st_dev.free()
 
     # a plain 256 MiB device-to-device copy: the known-size reference that the memory counters of a profile of
-    # this run are scaled by (profiles/README.md)
+    # this run are scaled by (profiles/attention_f32_2048x10000_memory.md)
     cal_a, cal_b = dm.DeviceBuffer(256 << 20), dm.DeviceBuffer(256 << 20)
     dm.copy(cal_b, cal_a, 256 << 20)
     dm.synchronize()
@@ -201,19 +258,26 @@ def main():
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import oracle as orc
 
-        threads = min(16, os.cpu_count() or 1)
+        threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
         orc.set_threads(threads)
+        cpu_model = "unknown"
+        try:
+            with open("/proc/cpuinfo") as fh:
+                cpu_model = next((ln.split(":", 1)[1].strip() for ln in fh if ln.startswith("model name")), cpu_model)
+        except OSError:
+            pass
         sample = 256
         t0 = time.perf_counter()
         want = orc.predict_raw(model, fitted, x_test[:sample])
         secs = time.perf_counter() - t0
         got = gpu.predict(w, vm, x_test[:sample], CLASSES)
         cpu = {"value": round(sample / secs, 2), "unit": "rows/s", "cores": threads, "kind": "port",
+               "cpu_model": cpu_model,
                "sample": f"{sample} of the test rows through all three stages against the card-fitted caches (C "
-                         f"restatement of the reference CPU path, {threads} OpenMP threads, {secs:.1f} s; largest "
-                         f"score difference to the card {np.abs(got - want).max():.1e})"}
-        log(f"cpu baseline: {cpu['value']} rows/s on {threads} threads")
-        fr = 1000
+                         f"restatement of the reference CPU path, {threads} OpenMP threads = the cores this process "
+                         f"may use, {secs:.1f} s; largest score difference to the card {np.abs(got - want).max():.1e})"}
+        log(f"cpu baseline: {cpu['value']} rows/s on {threads} threads ({cpu_model})")
+        fr = 2500
         t0 = time.perf_counter()
         orc.fit_raw(model, x_train[:fr], y_train[:fr], CLASSES, CHUNK)
         cpu_fit = time.perf_counter() - t0
@@ -221,8 +285,12 @@ def main():
         fitmod.fit_raw(gpu, w, x_train[:fr], y_train[:fr], CLASSES, CHUNK)
         gpu_fit = time.perf_counter() - t0
         fit_sample = {"rows": fr, "features": FEATURES, "cpu_s": round(cpu_fit, 3), "gpu_s": round(gpu_fit, 4),
-                      "cores": threads, "kind": "port"}
-        log(f"fit sample {fr} x {FEATURES}: cpu {cpu_fit:.2f} s, card {gpu_fit:.3f} s")
+                      "speedup": round(cpu_fit / gpu_fit, 1), "cores": threads, "kind": "port",
+                      "note": "the same 2,500-row sample of the training table fitted by the C restatement of the "
+                              "reference CPU path and by the card; the column and row stages grow linearly with "
+                              "rows and the in-context stage with rows squared, so the full 10,000-row fit is "
+                              "4 to 16 times the sample on the CPU"}
+        log(f"fit sample {fr} x {FEATURES}: cpu {cpu_fit:.2f} s, card {gpu_fit:.3f} s ({cpu_fit / gpu_fit:.0f}x)")
         tab = importlib.import_module("tabicl-anywhere_amd.table")
         hs = 512
         t0 = time.perf_counter()
@@ -263,6 +331,13 @@ def main():
                      "kernel": "k_attn_split64 (+ split merge)", "ms_per_launch": round(att_ms, 4),
                      "basis": "algorithmic f32 FLOP (4 x queries x keys x d) per launch / launch time, against the "
                               "dense fp16 MFMA peak / 3 (each f32 product is three fp16 products)"},
+        "step_roofline": {"bound": "mfma", "achieved": round(pass_cost(model, BATCH)[1] / (ms_step / 1e3) / 1e12, 2),
+                          "peak": round(PEAK_SPLIT_F32 / 1e12, 1), "unit": "TFLOP/s",
+                          "frac": round(pass_cost(model, BATCH)[1] / (ms_step / 1e3) / PEAK_SPLIT_F32, 4),
+                          "basis": "algorithmic f32 FLOP of a whole 2,048-row prediction pass (all three stages) / "
+                                   "ms_per_step, against the split-fp16 ceiling"},
+        "roofline_by_batch": roof_by_batch,
+        "one_row_after_mall_flush_ms": cold,
         "cpu_baseline": cpu,
         "fit_sample": fit_sample,
     }

@@ -14,6 +14,7 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from . import abi
+from .bundle import write as bundle_write
 from .plan import Plan, parse_tree
 
 F = np.float32
@@ -188,6 +189,31 @@ class Fitted:
     def meta(self) -> np.ndarray:
         return np.array([self.rows, self.features, self.classes, self.chunk, self.kv_format, self.digits,
                          len(self.plan.nodes)], np.int32)
+
+    def raw_entries(self, prefix: str = "") -> list:
+        """The member's tensors as `raw_entries` declares them (`src/fit.rs:224-241`), in that order: `(name, dtype,
+        dims)` of meta, tree, col_kv, then per problem its query scales and every layer's stored records."""
+        tree = self.plan.tree(self.rows)
+        out = [(f"{prefix}meta", "int32", [7]), (f"{prefix}tree", "int32", [len(tree)]),
+               (f"{prefix}col_kv", "float32", list(self.col_kv.shape))]
+        for ni, layers in enumerate(self.layers):
+            out.append((f"{prefix}n{ni}_scale", "float32", list(np.shape(self.scales[ni]))))
+            out += [(f"{prefix}n{ni}_kv{l}", "uint8", [int(rec.size)]) for l, rec in enumerate(layers)]
+        return out
+
+    def tensors(self, prefix: str = "") -> dict:
+        """name -> array, in `raw_entries` order, for `bundle.write`."""
+        t = {f"{prefix}meta": self.meta(), f"{prefix}tree": np.asarray(self.plan.tree(self.rows), np.int32),
+             f"{prefix}col_kv": np.ascontiguousarray(self.col_kv, F)}
+        for ni, layers in enumerate(self.layers):
+            t[f"{prefix}n{ni}_scale"] = np.ascontiguousarray(self.scales[ni], F)
+            for l, rec in enumerate(layers):
+                t[f"{prefix}n{ni}_kv{l}"] = np.ascontiguousarray(rec, np.uint8)
+        return t
+
+    def write(self, path=None, prefix: str = "") -> bytes:
+        """The member as a `.tirs` bundle (the bytes; also written to `path` if given)."""
+        return bundle_write(path, self.tensors(prefix))
 
 
 def fit_raw(gpu, weights, x, y, classes: int, chunk: int = 256, kv_format: int = abi.KV_F32) -> Fitted:
