@@ -188,3 +188,24 @@ def test_stage_full_size(gpu, full_model, full_weights, kv_format, nq):
     err = np.abs(got - want).max()
     say("  worst", err, "scale", np.abs(want).max())
     assert err < SCORE_TOL
+
+
+@pytest.mark.parametrize("kv_format", [abi.KV_F32, abi.KV_I8])
+@pytest.mark.parametrize("nq,rows", [(1024, 3000), (2048, 10000)])
+def test_stage_large_batches_sampled(gpu, full_model, full_weights, kv_format, nq, rows):
+    """The whole in-context stage for a large batch (the attention's few key ranges merged inside the output
+    projection), 24 of its rows against the oracle on the same inputs (rows are independent)."""
+    say(f"stage large batch fmt={kv_format} nq={nq} rows={rows}")
+    rng = np.random.default_rng(nq + rows + kv_format)
+    d, L, chunk = full_model.d, full_model.icl_layers, 256
+    layers = random_layers(rng, L, rows, chunk, d, kv_format)
+    scales = np.stack([orc.query_scale(b, rows) for b in full_model.icl])
+    vm = gpu.load(full_weights, kv_format, rows, chunk, layers, scales)
+    h = rng.standard_normal((nq, d)).astype(np.float32)
+    got = gpu.in_context(full_weights, vm, h, 10)
+    sample = np.sort(rng.choice(nq, 24, replace=False))
+    want = orc.in_context(full_model, scales, layers, kv_format, rows, chunk, h[sample], 10)
+    vm.free()
+    err = np.abs(got[sample] - want).max()
+    say("  worst", err, "scale", np.abs(want).max())
+    assert err < SCORE_TOL and np.isfinite(got).all()
