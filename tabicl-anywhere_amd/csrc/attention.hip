@@ -20,9 +20,9 @@
 //    keys). Scores are formed transposed, S^T = K Q^T, so that each lane owns one query (lane % 16) in both
 //    products; the softmax then needs only two cross-lane steps, and O^T = V^T P^T takes each lane's own weights as
 //    its B operand with no transpose through LDS.
-//  * k_attn_decode64: head width 64 and few queries, from the records: 256 threads per (key range, head, 8
-//    queries), K/V tiles loaded with 128-bit loads, lane = key for the scores and lane = coordinate for the
-//    weighted sum; wavefronts whose query slots are empty skip the arithmetic (one query: wavefront 0 alone).
+//  * k_attn_decode_w: head width 64 and few queries, from the records: 256 threads per (four key blocks, head, 8
+//    queries), each wavefront streaming a key block of its own with no barrier (lane = key for the scores, lane =
+//    coordinate for the weighted sum), integer codes scaled through the query and the sums.
 //  * k_attn_decode: any other head width up to 64 (the tiny test models): the same with one wavefront.
 // All of them leave the running maximum in log2 units (score * log2 e) for the split merge (head width 64:
 // k_attn_merge64 for few key ranges, k_attn_merge_many for many; k_attn_merge otherwise).
@@ -377,89 +377,185 @@ __global__ __launch_bounds__(64) void k_attn_decode(int nq, int rows, int chunk,
 }
 
 // ---- decode kernel for head width 64: few queries, bandwidth-bound ------------------------------------------
-// grid (splits, heads, query groups of QG); 256 threads. The K and V tiles of each key block are loaded with the
-// same 128-bit loads as the MFMA kernel (every thread has 32 keys' worth of loads in flight); wavefront w then
-// owns queries w and w + 4 of the group: lane = key for the scores and the softmax, lane = coordinate for the
-// weighted values.
+// ---- decode kernel with independent wavefronts: head width 64, at most QG queries ------------------------------
+// grid (splits, heads, query groups of QG); 256 threads. Each wavefront streams its own key blocks of the
+// workgroup's range (kb0 + w, kb0 + w + 4, ...) straight from the stored records, with no barrier between blocks, so
+// every wavefront keeps a whole block's loads in flight: the scores with lane = key (a coordinate's 64 keys are one
+// coalesced row of the record), the weighted values with lane = coordinate (its 64 keys are 64 contiguous values).
+// Integer codes are used as stored: the chunk's key scales multiply the query and its value scales the block's
+// weighted sum (Soft::update_int, src/nn.rs:233-258). The wavefronts' (m, l, o) are merged through LDS at the end.
 template <int FMT>
-__global__ __launch_bounds__(256) void k_attn_decode64(int nq, int rows, int chunk, int d, int heads,
-                                                        const float *__restrict__ q, const uint8_t *__restrict__ records,
-                                                        int kb_per_split, float *__restrict__ part_o,
-                                                        float *__restrict__ part_ml, float *__restrict__ out) {
-    __shared__ float Ks[64][KP];       // [coordinate][key]
-    __shared__ float Vt[KB][KB + 1];   // [key][coordinate]
+__device__ __forceinline__ float raw_at(const uint8_t *body, size_t i) {
+    if (FMT == TAH_KV_F32) return reinterpret_cast<const float *>(body)[i];
+    if (FMT == TAH_KV_I16) return (float)reinterpret_cast<const int16_t *>(body)[i];
+    return (float)reinterpret_cast<const int8_t *>(body)[i];
+}
+
+// The 64 values of stacked coordinate c for keys o.. o + 63 of a record (raw: codes unscaled), zero past nk.
+template <int FMT>
+__device__ __forceinline__ void row64(const uint8_t *body, int rc, int c, int o, int nk, bool fast, float (&v)[64]) {
+    if (fast) {
+        if (FMT == TAH_KV_F32) {
+            const float4 *p = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(body) + (size_t)c * rc + o);
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const float4 x = p[i];
+                v[4 * i] = x.x;
+                v[4 * i + 1] = x.y;
+                v[4 * i + 2] = x.z;
+                v[4 * i + 3] = x.w;
+            }
+        } else if (FMT == TAH_KV_I16) {
+            const uint4 *p = reinterpret_cast<const uint4 *>(reinterpret_cast<const int16_t *>(body) + (size_t)c * rc + o);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const uint4 x = p[i];
+                const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    v[8 * i + 2 * j] = (float)(int16_t)(w[j] & 0xffffu);
+                    v[8 * i + 2 * j + 1] = (float)(int16_t)(w[j] >> 16);
+                }
+            }
+        } else {
+            const uint4 *p = reinterpret_cast<const uint4 *>(reinterpret_cast<const int8_t *>(body) + (size_t)c * rc + o);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint4 x = p[i];
+                const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+#pragma unroll
+                    for (int b = 0; b < 4; b++) v[16 * i + 4 * j + b] = (float)(int8_t)((w[j] >> (8 * b)) & 0xffu);
+            }
+        }
+    } else {
+        // every load in bounds (the key clamped to the block's last), the keys past it zeroed after: no branches
+#pragma unroll
+        for (int k = 0; k < 64; k++) {
+            const float x = raw_at<FMT>(body, (size_t)c * rc + o + min(k, nk - 1));
+            v[k] = k < nk ? x : 0.0f;
+        }
+    }
+}
+
+template <int FMT>
+__global__ __launch_bounds__(256) void k_attn_decode_w(int nq, int rows, int chunk, int d, int heads,
+                                                       const float *__restrict__ q, const uint8_t *__restrict__ records,
+                                                       int kb_per_split, float *__restrict__ part_o,
+                                                       float *__restrict__ part_ml, float *__restrict__ out) {
     __shared__ float Qs[QG][64];
-    __shared__ float Ps[QG][KB];
+    __shared__ float Qk[4][QG][64];  // INT: each wavefront's queries times its block's key scales
+    __shared__ float Ps[4][QG][KB];
+    __shared__ float Wml[4][QG][2];
+    __shared__ float Wo[4][QG][64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int split = blockIdx.x, h = blockIdx.y, q0 = blockIdx.z * QG;
     const int splits = gridDim.x;
+    const int nqg = min(QG, nq - q0);
     const KeyBlocks kbs = key_blocks(rows, chunk);
     const int kb0 = split * kb_per_split, kb1 = min(kbs.n_kb, kb0 + kb_per_split);
+    constexpr bool INT = FMT != TAH_KV_F32;
+    const int width = FMT == TAH_KV_F32 ? 4 : (FMT == TAH_KV_I16 ? 2 : 1);
     for (int i = tid; i < QG * 64; i += 256) {
         const int qi = i >> 6, c = i & 63;
-        Qs[qi][c] = q0 + qi < nq ? q[(size_t)(q0 + qi) * d + h * 64 + c] : 0.0f;
+        Qs[qi][c] = qi < nqg ? q[(size_t)(q0 + qi) * d + h * 64 + c] : 0.0f;
     }
-    const int qa = wave, qb = wave + 4;  // this wavefront's two queries
-    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f}, o[2] = {0.0f, 0.0f};
-    const int lc = tid >> 2, seg = (tid & 3) * 16;
-    const int width = FMT == TAH_KV_F32 ? 4 : (FMT == TAH_KV_I16 ? 2 : 1);
-    // the next block's tiles are read into registers while the current one is used
-    auto tiles = [&](int kb, float (&tk)[16], float (&tv)[16]) {
+    __syncthreads();
+    float m[QG], l[QG], o[QG];
+#pragma unroll
+    for (int qi = 0; qi < QG; qi++) {
+        m[qi] = -INFINITY;
+        l[qi] = 0.0f;
+        o[qi] = 0.0f;
+    }
+    for (int kb = kb0 + wave; kb < kb1; kb += 4) {
         const Where w = locate(kbs, kb, records, FMT, d, chunk);
+        const uint8_t *body = INT ? w.rec + 8 * (size_t)d : w.rec;
+        const bool kin = lane < w.nk;
         const bool fast = w.nk == KB && ((size_t)w.rc * width) % 16 == 0;
-        load16<FMT>(w.rec, d, w.rc, h * 64 + lc, w.o + seg, w.nk - seg, fast, tk);
-        load16<FMT>(w.rec, d, w.rc, d + h * 64 + lc, w.o + seg, w.nk - seg, fast, tv);
-    };
-    float tk[16], tv[16];
-    if (kb0 < kb1) tiles(kb0, tk, tv);
-    for (int kb = kb0; kb < kb1; kb++) {
-        const Where w = locate(kbs, kb, records, FMT, d, chunk);
-        __syncthreads();  // the previous block's tiles are no longer read
+        // keys: lane = key, coordinates 0..63 of this head (lanes past the block's keys read its last key and are
+        // masked below); values: lane = coordinate, keys 0..63 of the block
+        float kc[64], vr[64];
+        const int kl = min(lane, w.nk - 1);
 #pragma unroll
-        for (int i = 0; i < 16; i += 4) *reinterpret_cast<float4 *>(&Ks[lc][seg + i]) = make_float4(tk[i], tk[i + 1], tk[i + 2], tk[i + 3]);
+        for (int c = 0; c < 64; c++) kc[c] = raw_at<FMT>(body, (size_t)(h * 64 + c) * w.rc + w.o + kl);
+        row64<FMT>(body, w.rc, d + h * 64 + lane, w.o, w.nk, fast, vr);
+        float vs = 1.0f;
+        if (INT) {
+            // the chunk's scales of this head: keys' multiply the queries (lane = coordinate), values' the sums
+            const float *sc = reinterpret_cast<const float *>(w.rec);
+            const float ks = sc[h * 64 + lane];
+            vs = sc[d + h * 64 + lane];
 #pragma unroll
-        for (int i = 0; i < 16; i++) Vt[seg + i][lc] = tv[i];
-        if (kb + 1 < kb1) tiles(kb + 1, tk, tv);
-        __syncthreads();
+            for (int qi = 0; qi < QG; qi++)
+                if (qi < nqg) Qk[wave][qi][lane] = Qs[qi][lane] * ks;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int qi = j ? qb : qa;
-            if (q0 + qi >= nq) continue;  // (wavefront-uniform) no query in this slot
+        for (int qi = 0; qi < QG; qi++) {
+            if (qi >= nqg) break;  // (uniform) no query in this slot
             float sc = 0.0f;
-#pragma unroll 16
-            for (int c = 0; c < 64; c++) sc += Qs[qi][c] * Ks[c][lane];
-            if (lane >= w.nk) sc = -INFINITY;
-            const float mnew = fmaxf(m[j], wave_max(sc));
-            const float alpha = fast_exp(m[j] - mnew);
-            const float p = lane < w.nk ? fast_exp(sc - mnew) : 0.0f;
-            l[j] = l[j] * alpha + wave_sum(p);
-            m[j] = mnew;
-            o[j] *= alpha;
-            Ps[qi][lane] = p;
-        }
-        __syncthreads();
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int qi = j ? qb : qa;
-            if (q0 + qi >= nq) continue;
-            float a = 0.0f;
-#pragma unroll 16
-            for (int k = 0; k < KB; k++) a += Ps[qi][k] * Vt[k][lane];
-            o[j] += a;
+            for (int c = 0; c < 64; c++) sc += (INT ? Qk[wave][qi][c] : Qs[qi][c]) * kc[c];
+            if (!kin) sc = -INFINITY;
+            const float mnew = fmaxf(m[qi], wave_max(sc));
+            const float alpha = fast_exp(m[qi] - mnew);
+            const float p = kin ? fast_exp(sc - mnew) : 0.0f;
+            l[qi] = l[qi] * alpha + wave_sum(p);
+            m[qi] = mnew;
+            o[qi] *= alpha;
+            Ps[wave][qi][lane] = p;
         }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int qi = 0; qi < QG; qi++) {
+            if (qi >= nqg) break;
+            float a = 0.0f;
+#pragma unroll
+            for (int k = 0; k < KB; k++) a += Ps[wave][qi][k] * vr[k];
+            o[qi] += INT ? a * vs : a;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();  // the weights are read before the next block's are written
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const int qr = q0 + (j ? qb : qa);
-        if (qr >= nq) continue;
+    for (int qi = 0; qi < QG; qi++) {
+        if (qi >= nqg) break;
+        Wo[wave][qi][lane] = o[qi];
+        if (lane == 0) {
+            Wml[wave][qi][0] = m[qi];
+            Wml[wave][qi][1] = l[qi];
+        }
+    }
+    __syncthreads();
+    // wavefront w finishes queries w and w + 4
+    for (int qi = wave; qi < nqg; qi += 4) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            if (Wml[u][qi][1] > 0.0f) M = fmaxf(M, Wml[u][qi][0]);
+        float L = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float f = Wml[u][qi][1] > 0.0f ? fast_exp(Wml[u][qi][0] - M) : 0.0f;
+            L += Wml[u][qi][1] * f;
+            O += Wo[u][qi][lane] * f;
+        }
+        const int qr = q0 + qi;
         if (splits == 1) {
-            out[(size_t)qr * d + h * 64 + lane] = o[j] / l[j];
+            out[(size_t)qr * d + h * 64 + lane] = O / L;
         } else {
             const size_t at = ((size_t)split * nq + qr) * heads + h;
-            part_o[at * 64 + lane] = o[j];
+            part_o[at * 64 + lane] = O;
             if (lane == 0) {
-                part_ml[at * 2] = m[j] * LOG2E;
-                part_ml[at * 2 + 1] = l[j];
+                part_ml[at * 2] = M * LOG2E;
+                part_ml[at * 2 + 1] = L;
             }
         }
     }
@@ -1044,6 +1140,12 @@ static AttnPlan plan(const AttnShape &a, bool images) {
     // enough workgroups to fill the 256 compute units about once (twice for the smaller workgroups of two or more
     // query tiles), each with at least 2 key blocks: more, shorter key ranges measured slower at every batch (the
     // merge and each workgroup's fixed costs grow with them; 64 queries: 22 us at 256 workgroups against 36 at 632)
+    if (!p.mfma && hd == 64) {
+        // the decode kernel's wavefronts each take a key block of their own: four blocks a workgroup
+        p.kb_per_split = std::min(4, k.n_kb);
+        p.splits = (k.n_kb + p.kb_per_split - 1) / p.kb_per_split;
+        return p;
+    }
     const long target = p.waves == 8 ? 256 : (p.groups == 1 ? 256 : 512);
     long want = (target + (long)p.groups * a.heads - 1) / ((long)p.groups * a.heads);
     want = std::max(1L, std::min(want, (long)(k.n_kb + 1) / 2));
@@ -1067,7 +1169,7 @@ static void launch(hipStream_t s, const AttnShape &a, const AttnPlan &p, const f
         hipLaunchKernelGGL(k_attn_mfma64<FMT>, dim3(p.groups * a.heads * p.splits), dim3(256), 0, s, a.nq, a.rows,
                            a.chunk, a.d, a.heads, q, records, p.kb_per_split, p.groups, p.splits, part_o, part_ml, out);
     } else if (a.d / a.heads == 64) {
-        hipLaunchKernelGGL(k_attn_decode64<FMT>, dim3(p.splits, a.heads, p.groups), dim3(256), 0, s, a.nq, a.rows,
+        hipLaunchKernelGGL(k_attn_decode_w<FMT>, dim3(p.splits, a.heads, p.groups), dim3(256), 0, s, a.nq, a.rows,
                            a.chunk, a.d, a.heads, q, records, p.kb_per_split, part_o, part_ml, out);
     } else {
         hipLaunchKernelGGL(k_attn_decode<FMT>, dim3(p.splits, a.heads, p.groups), dim3(64), 0, s, a.nq, a.rows, a.chunk,

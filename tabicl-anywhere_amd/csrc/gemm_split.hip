@@ -453,6 +453,37 @@ __global__ __launch_bounds__(256) void k_qmlp64(int M, int heads, float *__restr
     qmlp64_lane(xv, r32, g, w0, s0, b0, w2, s2, b2, scale + (size_t)(m % heads) * 64, live ? qr : nullptr);
 }
 
+// The same for a few rows (at most QR_ROWS): one workgroup per row, wavefront h its query-head h, in plain f32. The
+// MLP's two 64 x 64 weight matrices (shared by the heads) are staged in LDS once per workgroup, rows padded so that
+// lane j's reads of row j hit distinct banks; lane j forms hidden unit j, then output j, each a 64-term dot product
+// summed in order and the bias added after, as the reference's linear does (src/kern.rs:125-130).
+constexpr int QR_ROWS = 8;
+__global__ __launch_bounds__(512) void k_qmlp_rows(int heads, float *__restrict__ q, const float *__restrict__ w0,
+                                                   const float *__restrict__ b0, const float *__restrict__ w2,
+                                                   const float *__restrict__ b2, const float *__restrict__ scale) {
+    __shared__ float W0[64][65], W2[64][65], xs[8][64], hs[8][64];
+    const int tid = threadIdx.x, lane = tid & 63, h = tid >> 6;
+    for (int i = tid; i < 64 * 64; i += 512) {
+        W0[i >> 6][i & 63] = w0[i];
+        W2[i >> 6][i & 63] = w2[i];
+    }
+    float *qr = q + ((size_t)blockIdx.x * heads + h) * 64;
+    const bool live = h < heads;
+    const float x = live ? qr[lane] : 0.0f;
+    xs[h][lane] = x;
+    __syncthreads();
+    float a = 0.0f;
+#pragma unroll 16
+    for (int k = 0; k < 64; k++) a += W0[lane][k] * xs[h][k];
+    hs[h][lane] = gelu(a + b0[lane]);
+    __syncthreads();
+    float o = 0.0f;
+#pragma unroll 16
+    for (int k = 0; k < 64; k++) o += W2[lane][k] * hs[h][k];
+    o += b2[lane];
+    if (live) qr[lane] = x * (scale[h * 64 + lane] * (1.0f + tanh1(o)));
+}
+
 bool qmlp_fused(const DevBlock &b) {
     return b.heads > 0 && b.d == 64 * b.heads && b.ss_hidden == 64 && b.q0_s.img && b.q2_s.img && b.q0_s.K == 64 &&
            b.q2_s.K == 64 && b.q0_s.N == 64 && b.q2_s.N == 64;
@@ -461,6 +492,11 @@ bool qmlp_fused(const DevBlock &b) {
 void qmlp(hipStream_t s, int rows, const DevBlock &b, const float *scale, float *q) {
     const int M = rows * b.heads;
     if (M <= 0) return;
+    if (rows <= QR_ROWS && b.heads <= 8 && b.q0w && b.q2w) {
+        hipLaunchKernelGGL(k_qmlp_rows, dim3(rows), dim3(512), 0, s, b.heads, q, b.q0w, b.q0b, b.q2w, b.q2b, scale);
+        TAH_LAUNCHED();
+        return;
+    }
     hipLaunchKernelGGL(k_qmlp64, dim3((M + 127) / 128), dim3(256), 0, s, M, b.heads, q, b.q0_s.img, b.q0_s.shift, b.q0b,
                        b.q2_s.img, b.q2_s.shift, b.q2b, scale);
     TAH_LAUNCHED();
