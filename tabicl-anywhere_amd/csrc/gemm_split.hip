@@ -429,6 +429,218 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
     }
 }
 
+// Few rows (9 to FEW_ROWS: the in-context stage of a small batch): one workgroup per 32 rows x 32 TN columns, its
+// eight wavefronts splitting K = 128 NST eight ways (NST 16-column steps each, one power of two per row and
+// wavefront). With so few steps a pipelined loop waits for memory once per step or two; here every global read of
+// the workgroup is issued at its start -- the wavefront's weight steps, its rows' slice of X, the epilogue's bias and
+// residual (a bias is required), with LN the norm's weights and with QM the query MLP's weight images, biases and scales (both staged in
+// LDS) -- so that one memory latency precedes the products. The partial products, unscaled to f32, are summed
+// through LDS in wavefront order; wavefront w finishes accumulators 2 w and 2 w + 1 of every tile (two adjacent
+// columns of the lane's row). With QM (one head of 64 columns a workgroup, TN = 2) the finished tile goes through
+// LDS to wavefront 0, which runs the head's query MLP (qmlp64_lane) from the staged weights.
+constexpr int FEW_WAVES = 8;
+constexpr int FEW_ROWS = 256;
+constexpr int GEMV_SPLIT_ROWS = 8;  // up to this many rows the f32 kernels (k_gemv) take the dense layers
+constexpr int QPITCH = 68;  // row pitch of the query tile in LDS
+
+template <int EPI, bool LN, int TN, int NST, bool QM>
+__global__ __launch_bounds__(512) void k_dense_few(int M, const float *__restrict__ X, int ldx,
+                                                    const uint8_t *__restrict__ wimg, int wshift,
+                                                    const float *__restrict__ b, float *Y, int ldy, SplitEpi ea,
+                                                    const float *__restrict__ lnw, const float *__restrict__ lnb) {
+    static_assert(!QM || (TN == 2 && LN && EPI == EPI_NONE), "the query MLP follows the normed query projection");
+    static_assert(!LN || NST == 4, "the fused layer norm takes K = 512, one column a thread");
+    constexpr int K = 16 * NST * FEW_WAVES, KS = K / 16;
+    __shared__ float2 red[FEW_WAVES][TN][8][64];  // [wavefront][tile][accumulator pair][lane]
+    __shared__ float rsum[FEW_WAVES][32];
+    __shared__ float lns[LN ? 2 * K : 1];
+    __shared__ __align__(16) uint8_t qimg[QM ? 2 * 8 * 2048 : 16];
+    __shared__ float qvec[QM ? 3 * 64 : 1];
+    __shared__ __align__(16) float qt[QM ? 32 * QPITCH : 4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r32 = lane & 31, g = lane >> 5;
+    const int m = blockIdx.y * 32 + r32;
+    const bool live = m < M;
+    const int mr = live ? m : 0;  // rows past M read row 0 and are never stored
+    const int nt0 = blockIdx.x * TN;
+    const int k0 = wave * 16 * NST;
+
+    halfx8 wh[NST][TN], wl[NST][TN];
+    const uint8_t *wp = wimg + ((size_t)nt0 * KS + wave * NST) * 2048 + (g * 32 + r32) * 16;
+#pragma unroll
+    for (int j = 0; j < NST; j++)
+#pragma unroll
+        for (int T = 0; T < TN; T++) {
+            const uint8_t *src = wp + ((size_t)T * KS + j) * 2048;
+            wh[j][T] = *reinterpret_cast<const halfx8 *>(src);
+            wl[j][T] = *reinterpret_cast<const halfx8 *>(src + 1024);
+        }
+    float xv[NST][8];
+    const float *xrow = X + (size_t)mr * ldx + k0 + 8 * g;
+#pragma unroll
+    for (int j = 0; j < NST; j++) load8(xrow + 16 * j, xv[j]);
+    // this thread's outputs: accumulators 2 wave, 2 wave + 1 of each tile, i.e. columns nc, nc + 1 of the tile
+    const int nc = 16 * (wave >> 2) + 8 * g + 2 * (wave & 3);
+    float2 bias[TN], res[TN];
+#pragma unroll
+    for (int T = 0; T < TN; T++) {
+        const int n = 32 * (nt0 + T) + nc;
+        bias[T] = *reinterpret_cast<const float2 *>(b + n);
+        res[T] = EPI == EPI_RESID ? *reinterpret_cast<const float2 *>(ea.R + (size_t)mr * ea.ldr + n)
+                                  : make_float2(0.0f, 0.0f);
+    }
+    float lw = 0.0f, lb = 0.0f;
+    if (LN) {
+        lw = lnw[tid];
+        lb = lnb[tid];
+    }
+    u32x4 qs[4];
+    float qv = 0.0f;
+    if (QM) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            qs[i] = *reinterpret_cast<const u32x4 *>((i < 2 ? ea.w0 : ea.w2) + 16 * (tid + 512 * (i & 1)));
+        // threads 0..191: b0, b2, the head's scales (the rest reread the last scale, unused)
+        qv = *(tid < 64 ? ea.b0 + tid : tid < 128 ? ea.b2 + (tid - 64) : ea.scale + 64 * blockIdx.x + min(tid - 128, 63));
+    }
+
+    if (LN) {
+        // this wavefront holds columns k0 .. k0 + 63 of its 32 rows; the rows' sums go through LDS (two passes:
+        // mean, then biased variance; eps 1e-5)
+        lns[tid] = lw;
+        lns[K + tid] = lb;
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NST; j++)
+#pragma unroll
+            for (int t = 0; t < 8; t++) sum += xv[j][t];
+        sum += __shfl_xor(sum, 32, 64);
+        if (g == 0) rsum[wave][r32] = sum;
+        __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (int i = 0; i < FEW_WAVES; i++) tot += rsum[i][r32];
+        const float mean = tot / (float)K;
+        float sq = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NST; j++)
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const float dv = xv[j][t] - mean;
+                sq += dv * dv;
+            }
+        sq += __shfl_xor(sq, 32, 64);
+        __syncthreads();
+        if (g == 0) rsum[wave][r32] = sq;
+        __syncthreads();
+        tot = 0.0f;
+#pragma unroll
+        for (int i = 0; i < FEW_WAVES; i++) tot += rsum[i][r32];
+        const float inv = 1.0f / sqrtf(tot / (float)K + 1e-5f);
+#pragma unroll
+        for (int j = 0; j < NST; j++)
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const int c = k0 + 16 * j + 8 * g + t;
+                xv[j][t] = (xv[j][t] - mean) * inv * lns[c] + lns[K + c];
+            }
+    }
+    float xmax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NST; j++)
+#pragma unroll
+        for (int t = 0; t < 8; t++) xmax = fmaxf(xmax, fabsf(xv[j][t]));
+    xmax = fmaxf(xmax, __shfl_xor(xmax, 32, 64));
+    const int e = shift_for_max(xmax);
+    const float f = ldexpf(1.0f, e);
+    floatx16 acc[TN];
+#pragma unroll
+    for (int T = 0; T < TN; T++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[T][v] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NST; j++) {
+        halfx8 xh, xl;
+        split8(xv[j], f, xh, xl);
+#pragma unroll
+        for (int T = 0; T < TN; T++) acc[T] = mfma16x3(wh[j][T], wl[j][T], xh, xl, acc[T]);
+    }
+    const float u = ldexpf(1.0f, -(wshift + e));
+#pragma unroll
+    for (int T = 0; T < TN; T++)
+#pragma unroll
+        for (int p = 0; p < 8; p++) red[wave][T][p][lane] = make_float2(acc[T][2 * p] * u, acc[T][2 * p + 1] * u);
+    if (QM) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) *reinterpret_cast<u32x4 *>(qimg + 16 * (tid + 512 * i)) = qs[i];
+        if (tid < 192) qvec[tid] = qv;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int T = 0; T < TN; T++) {
+        float2 s = red[0][T][wave][lane];
+#pragma unroll
+        for (int i = 1; i < FEW_WAVES; i++) {
+            const float2 o = red[i][T][wave][lane];
+            s.x += o.x;
+            s.y += o.y;
+        }
+        float y0 = s.x + bias[T].x, y1 = s.y + bias[T].y;
+        if (EPI == EPI_GELU) {
+            y0 = gelu(y0);
+            y1 = gelu(y1);
+        }
+        if (EPI == EPI_RESID) {
+            y0 += res[T].x;
+            y1 += res[T].y;
+        }
+        if (QM) {
+            qt[r32 * QPITCH + 32 * T + nc] = y0;
+            qt[r32 * QPITCH + 32 * T + nc + 1] = y1;
+        } else if (live) {
+            *reinterpret_cast<float2 *>(Y + (size_t)m * ldy + 32 * (nt0 + T) + nc) = make_float2(y0, y1);
+        }
+    }
+    if (QM) {
+        __syncthreads();
+        if (wave != 0) return;
+        float xq[4][8];
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) load8(&qt[r32 * QPITCH + 16 * ks + 8 * g], xq[ks]);
+        qmlp64_lane(xq, r32, g, qimg, ea.s0, qvec, qimg + 8 * 2048, ea.s2, qvec + 64, qvec + 128,
+                    live ? Y + (size_t)m * ldy + 64 * blockIdx.x : nullptr);
+    }
+}
+
+template <int NST>
+static void launch_few(hipStream_t s, int M, int N, const float *X, int ldx, const uint8_t *img, int shift,
+                       const float *b, float *Y, int ldy, Epi epi, const SplitEpi &ea, const float *lnw,
+                       const float *lnb) {
+    const dim3 grid(N / 32, (M + 31) / 32);
+    const bool ln = lnw != nullptr;
+    if (NST == 4 && ln) {
+        if (epi == EPI_NONE)
+            hipLaunchKernelGGL((k_dense_few<EPI_NONE, NST == 4, 1, NST, false>), grid, dim3(512), 0, s, M, X, ldx, img,
+                               shift, b, Y, ldy, ea, lnw, lnb);
+        else if (epi == EPI_GELU)
+            hipLaunchKernelGGL((k_dense_few<EPI_GELU, NST == 4, 1, NST, false>), grid, dim3(512), 0, s, M, X, ldx, img,
+                               shift, b, Y, ldy, ea, lnw, lnb);
+        else
+            hipLaunchKernelGGL((k_dense_few<EPI_RESID, NST == 4, 1, NST, false>), grid, dim3(512), 0, s, M, X, ldx,
+                               img, shift, b, Y, ldy, ea, lnw, lnb);
+    } else if (epi == EPI_NONE) {
+        hipLaunchKernelGGL((k_dense_few<EPI_NONE, false, 1, NST, false>), grid, dim3(512), 0, s, M, X, ldx, img, shift,
+                           b, Y, ldy, ea, nullptr, nullptr);
+    } else if (epi == EPI_GELU) {
+        hipLaunchKernelGGL((k_dense_few<EPI_GELU, false, 1, NST, false>), grid, dim3(512), 0, s, M, X, ldx, img, shift,
+                           b, Y, ldy, ea, nullptr, nullptr);
+    } else {
+        hipLaunchKernelGGL((k_dense_few<EPI_RESID, false, 1, NST, false>), grid, dim3(512), 0, s, M, X, ldx, img,
+                           shift, b, Y, ldy, ea, nullptr, nullptr);
+    }
+    TAH_LAUNCHED();
+}
+
 // grid ceil(M / 128); 256 threads: q [rows * heads][64] in place, wavefront w the query-heads of rows 32 (4 x + w) +
 // 0..31 of that view.
 __global__ __launch_bounds__(256) void k_qmlp64(int M, int heads, float *__restrict__ q, const uint8_t *__restrict__ w0,
@@ -594,6 +806,12 @@ void query_split(hipStream_t s, int M, const float *X, int ldx, const DevBlock &
     ea.s2 = b.q2_s.shift;
     ea.b2 = b.q2b;
     const int d = b.d;
+    if (M <= FEW_ROWS) {
+        hipLaunchKernelGGL((k_dense_few<EPI_NONE, true, 2, 4, true>), dim3(d / 64, (M + 31) / 32), dim3(512), 0, s, M,
+                           X, ldx, b.in_s.img, b.in_s.shift, b.in_b, q, d, ea, b.n1w, b.n1b);
+        TAH_LAUNCHED();
+        return;
+    }
     // a workgroup per head: against one per two heads, twice the workgroups each stream half the weights and
     // finish their heads' query MLPs in parallel (64 rows 1.338 -> 1.316 ms a prediction, 2,048 rows 4.618 -> 4.604)
     hipLaunchKernelGGL((k_gemm_splitk4<EPI_NONE, true, 2, true>), dim3(d / 64, (M + 31) / 32), dim3(256), 0, s, M, d,
@@ -606,9 +824,21 @@ void dense(hipStream_t s, int M, int N, int K, const float *X, int ldx, const fl
     const bool img = w.img && gemm_split_fits(N, K) && K == w.K && w.row0 % 32 == 0 && N + w.row0 <= w.N &&
                      ldx % 4 == 0 && ldy % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 &&
                      (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
+    const bool epis = epi == EPI_NONE || epi == EPI_GELU || epi == EPI_RESID;
+    if (img && epis && b && M > GEMV_SPLIT_ROWS && M <= FEW_ROWS && N % 32 == 0 && (K == 512 || (K == 1024 && !lnw))) {
+        if ((ldx % 4) || (reinterpret_cast<uintptr_t>(X) & 15) || (R && ldr % 2))
+            throw ArgError{"dense: rows must be 16-byte aligned"};
+        const SplitEpi ea{R, ldr, nullptr, 1};
+        const uint8_t *sub = w.img + (size_t)(w.row0 / 32) * (w.K / 16) * 2048;
+        if (K == 512)
+            launch_few<4>(s, M, N, X, ldx, sub, w.shift, b, Y, ldy, epi, ea, lnw, lnb);
+        else
+            launch_few<8>(s, M, N, X, ldx, sub, w.shift, b, Y, ldy, epi, ea, nullptr, nullptr);
+        return;
+    }
     // from 64 rows the split kernels win (two tiles a workgroup below 512 rows: a 64-row prediction 1.285 against
     // 1.316 ms on the f32 kernels, 256 rows 1.52 against 1.61 ms with four tiles)
-    const bool split = img && M >= 64 && (epi == EPI_NONE || epi == EPI_GELU || epi == EPI_RESID);
+    const bool split = img && M >= 64 && epis;
     const bool k4 = split && N % 128 == 0 && K % 64 == 0 && K >= 256 && K <= 4 * SPLITK_MAX_KQ;
     if (lnw && !split && W && gemm_ln_fits(M, K, X, ldx, W)) {
         // few rows: the layer norm inside the product's kernel
