@@ -225,6 +225,13 @@ int tah_calibrate(tah_dev *dev, double ms, double *rate);
 /* Gpu::stages (src/gpu.rs:744-746): fitting stages this device has done (each fit hook call it took; a
  * tah_fit_represent call counts as two, the column and the row stage). */
 uint64_t tah_stages(const tah_dev *dev);
+/* No counterpart in the reference: a measurement hook for benchmarks. Arms HIP events around each launch of the
+ * many-query attention kernel (the in-context attention of 32 or more queries over tile images) on this device's
+ * stream, for up to `launches` launches (0 disarms); one probe per process, arming again resets it. */
+int tah_probe_attention(tah_dev *dev, int32_t launches);
+/* Synchronises the device's stream; *launches = the launches recorded since arming or the last read, *ms = their
+ * summed duration in milliseconds. TAH_E_ARG if the probe is not armed for this device. */
+int tah_probe_read(tah_dev *dev, double *ms, int32_t *launches);
 
 /* Receives layer `layer`'s stored records (tah_kv_record summed over its chunks, in host memory valid for the
  * duration of the call) while the in-context stage is fitted; non-zero stops the fit with TAH_E_SINK. */

@@ -123,6 +123,8 @@ SIGNATURES = {
                                        ctypes.c_int32, F32P]),
     "tah_calibrate": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_double, ctypes.POINTER(ctypes.c_double)]),
     "tah_stages": (ctypes.c_uint64, [ctypes.c_void_p]),
+    "tah_probe_attention": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32]),
+    "tah_probe_read": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int32)]),
     "tah_quantile_stats": (ctypes.c_int, [ctypes.c_void_p, F32P, ctypes.c_int32, ctypes.c_int32, F32P,
                                           ctypes.c_int32, F32P]),
     "tah_quantile_stats_dev": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, F32P,

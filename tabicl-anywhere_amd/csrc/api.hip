@@ -1469,3 +1469,18 @@ extern "C" int tah_calibrate(tah_dev *dev, double ms, double *rate) {
 }
 
 extern "C" uint64_t tah_stages(const tah_dev *dev) { return dev ? dev->stages.load() : 0; }
+
+extern "C" int tah_probe_attention(tah_dev *dev, int32_t launches) {
+    return guarded(dev, [&] {
+        probe_arm(dev->stream, launches);
+        return TAH_OK;
+    });
+}
+
+extern "C" int tah_probe_read(tah_dev *dev, double *ms, int32_t *launches) {
+    if (!ms || !launches) return TAH_E_ARG;
+    return guarded(dev, [&] {
+        *launches = probe_read(dev->stream, ms);
+        return TAH_OK;
+    });
+}

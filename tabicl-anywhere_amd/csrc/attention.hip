@@ -28,6 +28,10 @@
 // k_attn_merge64 for few key ranges, k_attn_merge_many for many; k_attn_merge otherwise).
 #include <algorithm>
 
+#include <atomic>
+#include <mutex>
+#include <vector>
+
 #include "common.hpp"
 #include "device_math.hpp"
 
@@ -1178,6 +1182,65 @@ static void launch(hipStream_t s, const AttnShape &a, const AttnPlan &p, const f
     TAH_LAUNCHED();
 }
 
+// ---- launch probe ---------------------------------------------------------------------------------------------------
+// While armed for a stream, each launch of the many-query kernel (k_attn_split64) on it is bracketed by a pair of HIP
+// events, up to the armed number of launches; probe_read sums their elapsed times. One probe per process.
+namespace {
+std::mutex probe_mu;
+std::atomic<bool> probe_on{false};
+hipStream_t probe_stream = nullptr;
+std::vector<hipEvent_t> probe_ev;
+int probe_used = 0;
+
+void probe_free() {
+    for (hipEvent_t e : probe_ev) (void)hipEventDestroy(e);
+    probe_ev.clear();
+    probe_used = 0;
+    probe_stream = nullptr;
+    probe_on = false;
+}
+
+// the next unused pair of events if the probe is armed for s, else null
+hipEvent_t *probe_slot(hipStream_t s) {
+    if (!probe_on.load(std::memory_order_relaxed)) return nullptr;
+    std::lock_guard<std::mutex> lk(probe_mu);
+    if (s != probe_stream || 2 * (probe_used + 1) > (int)probe_ev.size()) return nullptr;
+    return &probe_ev[2 * probe_used++];
+}
+}  // namespace
+
+void probe_arm(hipStream_t s, int launches) {
+    std::lock_guard<std::mutex> lk(probe_mu);
+    probe_free();
+    if (launches <= 0) return;
+    probe_ev.resize(2 * (size_t)launches);
+    for (size_t i = 0; i < probe_ev.size(); i++) {
+        if (hipEventCreate(&probe_ev[i]) != hipSuccess) {
+            probe_ev.resize(i);
+            probe_free();
+            throw ArgError{"probe: cannot create its events"};
+        }
+    }
+    probe_stream = s;
+    probe_on = true;
+}
+
+int probe_read(hipStream_t s, double *ms) {
+    std::lock_guard<std::mutex> lk(probe_mu);
+    if (!probe_on || s != probe_stream) throw ArgError{"probe: not armed for this device"};
+    TAH_HIP(hipStreamSynchronize(s));
+    double total = 0.0;
+    for (int i = 0; i < probe_used; i++) {
+        float t = 0.0f;
+        TAH_HIP(hipEventElapsedTime(&t, probe_ev[2 * i], probe_ev[2 * i + 1]));
+        total += t;
+    }
+    *ms = total;
+    const int n = probe_used;
+    probe_used = 0;
+    return n;
+}
+
 void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t *records, float *out, void *work,
                const KvImages *img) {
     if (a.nq <= 0) return;
@@ -1192,6 +1255,8 @@ void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t 
         part_ml = part_o + (size_t)p.splits * a.nq * a.heads * hd;
     }
     if (p.split16) {
+        hipEvent_t *pe = probe_slot(s);
+        if (pe) TAH_HIP(hipEventRecord(pe[0], s));
         if (p.waves == 8)
             hipLaunchKernelGGL(k_attn_split64<8>, dim3(p.groups * a.heads * p.splits), dim3(512), 0, s, a.nq, a.rows,
                                a.chunk, a.d, a.heads, q, img->images, img->kvmax, p.kb_per_split, p.groups, p.splits,
@@ -1201,6 +1266,7 @@ void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t 
                                a.chunk, a.d, a.heads, q, img->images, img->kvmax, p.kb_per_split, p.groups, p.splits,
                                part_o, part_ml, out);
         TAH_LAUNCHED();
+        if (pe) TAH_HIP(hipEventRecord(pe[1], s));
     } else switch (a.kv_format) {
         case TAH_KV_F32: launch<TAH_KV_F32>(s, a, p, q, records, out, part_o, part_ml); break;
         case TAH_KV_I16: launch<TAH_KV_I16>(s, a, p, q, records, out, part_o, part_ml); break;

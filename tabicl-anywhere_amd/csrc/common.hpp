@@ -234,6 +234,11 @@ KvImages kv_images_at(uint8_t *base, int rows, int chunk, int heads);
 void kv_images(hipStream_t s, int rows, int chunk, int d, int heads, int kv_format, const uint8_t *records,
                KvImages img);
 // img (optional): the layer's images, used for 32 queries or more.
+// Launch probe of the many-query attention kernel (attention.hip): arm for a stream with room for `launches`
+// launches (0 disarms); read synchronises the stream, returns the launches recorded since the last read and their
+// summed duration in ms.
+void probe_arm(hipStream_t s, int launches);
+int probe_read(hipStream_t s, double *ms);
 void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t *records, float *out, void *work,
                const KvImages *img = nullptr);
 

@@ -235,6 +235,17 @@ class Gpu:
         """Fitting stages the card has done (`Gpu::stages`)."""
         return int(self._l.tah_stages(self._h))
 
+    def probe_attention(self, launches: int) -> None:
+        """Bracket each of the next `launches` launches of the many-query attention kernel on this device's stream
+        with HIP events (0 disarms). A measurement hook of this library, not of the reference."""
+        self._check(self._l.tah_probe_attention(self._h, int(launches)))
+
+    def probe_read(self):
+        """(launches recorded since arming or the last read, their summed duration in ms); synchronises."""
+        ms, n = ctypes.c_double(), ctypes.c_int32()
+        self._check(self._l.tah_probe_read(self._h, ctypes.byref(ms), ctypes.byref(n)))
+        return int(n.value), float(ms.value)
+
     def fit_represent(self, weights: "GpuWeights", x, y, bases, ind_scales):
         """The column and row stages of a fit with the cells kept on the card (`Attend::columns` + `Attend::rows`):
         x [rows][features] normalised, y [rows] class indices or standardised targets, `bases` the label digits'
