@@ -15,12 +15,7 @@
 //    instructions). Operands are scaled by powers of two first (exact): each query to a maximum near 2^14, each
 //    head's keys and values by the layer's maximum, and the softmax weights to at most 2^15, so that no half
 //    overflows and the low halves stay normal for all but negligible elements.
-//  * k_attn_mfma64: head width 64 and at least 32 queries, on v_mfma_f32_16x16x4_f32 straight from the records
-//    (used where no images were made). 4 wavefronts x 32 queries share LDS tiles of K and V (64 coordinates x 64
-//    keys). Scores are formed transposed, S^T = K Q^T, so that each lane owns one query (lane % 16) in both
-//    products; the softmax then needs only two cross-lane steps, and O^T = V^T P^T takes each lane's own weights as
-//    its B operand with no transpose through LDS.
-//  * k_attn_decode_w: head width 64 and few queries, from the records: 256 threads per (four key blocks, head, 8
+//  * k_attn_decode_w: head width 64 and few queries (or no images), from the records: 256 threads per (four key blocks, head, 8
 //    queries), each wavefront streaming a key block of its own with no barrier (lane = key for the scores, lane =
 //    coordinate for the weighted sum), integer codes scaled through the query and the sums.
 //  * k_attn_decode: any other head width up to 64 (the tiny test models): the same with one wavefront.
@@ -38,8 +33,10 @@
 namespace tah {
 
 constexpr int KB = 64;   // keys per block
-constexpr int KP = 68;   // padded LDS row of a K or V tile
 constexpr int QG = 8;    // queries per decode workgroup
+// From this many queries the matrix kernel (one read of the images for up to 128 queries) beats the decode kernel
+// (one read of the records per 8 queries)
+constexpr int SPLIT16_MIN_Q = QG + 1;
 
 struct KeyBlocks {
     int bpc;       // key blocks per full chunk
@@ -129,180 +126,6 @@ __device__ __forceinline__ void load16(const uint8_t *rec, int d, int rc, int c,
     } else {
 #pragma unroll
         for (int i = 0; i < 16; i++) dst[i] = i < nk_left ? rec_value<FMT>(rec, d, rc, c, o16 + i) : 0.0f;
-    }
-}
-
-// ---- MFMA kernel: head width 64 ------------------------------------------------------------------------------
-// A flat grid of qtiles x heads x splits workgroups of 256 threads; each workgroup attends 128 queries (4 wavefronts
-// x 2 groups of 16) of one head to one key range. Each wavefront owns two query groups so that every K or V value
-// it reads from LDS feeds two MFMAs (LDS bandwidth, not the matrix cores, bounded the one-group form). The flat
-// index is remapped so that the query tiles sharing a (head, key range) run on the same XCD: workgroup i is
-// dispatched to XCD i % 8, and the tiles of one (head, range) then read the same K/V tiles through one L2.
-constexpr int QW = 2;  // query groups of 16 per wavefront
-
-template <int FMT>
-__global__ __launch_bounds__(256) void k_attn_mfma64(int nq, int rows, int chunk, int d, int heads,
-                                                      const float *__restrict__ q, const uint8_t *__restrict__ records,
-                                                      int kb_per_split, int qtiles, int splits,
-                                                      float *__restrict__ part_o, float *__restrict__ part_ml,
-                                                      float *__restrict__ out) {
-    __shared__ float Ks[64][KP];
-    __shared__ float Vs[64][KP];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int total = qtiles * heads * splits;
-    int flat = blockIdx.x;
-    if (total % 8 == 0) flat = (flat % 8) * (total / 8) + flat / 8;
-    const int qt = flat % qtiles, pair = flat / qtiles;
-    const int h = pair % heads, split = pair / heads;
-    const KeyBlocks kbs = key_blocks(rows, chunk);
-    const int kb0 = split * kb_per_split, kb1 = min(kbs.n_kb, kb0 + kb_per_split);
-    const int r16 = lane & 15, g4 = lane >> 4;
-    int qrow[QW];
-    bool qlive[QW];
-    // this lane's query coordinates: c = 16 cs + 4 g4 + t for cs, t in 0..3
-    float qreg[QW][16];
-#pragma unroll
-    for (int j = 0; j < QW; j++) {
-        qrow[j] = qt * 64 * QW + wave * 16 * QW + j * 16 + r16;
-        qlive[j] = qrow[j] < nq;
-#pragma unroll
-        for (int cs = 0; cs < 4; cs++) {
-            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (qlive[j]) v = *reinterpret_cast<const float4 *>(q + (size_t)qrow[j] * d + h * 64 + 16 * cs + 4 * g4);
-            qreg[j][4 * cs] = v.x;
-            qreg[j][4 * cs + 1] = v.y;
-            qreg[j][4 * cs + 2] = v.z;
-            qreg[j][4 * cs + 3] = v.w;
-        }
-    }
-    float m[QW], l[QW];
-    floatx4 acc_o[QW][4];
-#pragma unroll
-    for (int j = 0; j < QW; j++) {
-        m[j] = -INFINITY;
-        l[j] = 0.0f;
-#pragma unroll
-        for (int db = 0; db < 4; db++) acc_o[j][db] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
-
-    const int lc = tid >> 2, seg = (tid & 3) * 16;  // loader: coordinate row and 16-key segment
-    const int width = FMT == TAH_KV_F32 ? 4 : (FMT == TAH_KV_I16 ? 2 : 1);
-    // the next key block's K and V, loaded into registers while the current block is multiplied
-    float tk[16], tv[16];
-    if (kb0 < kb1) {
-        const Where w0 = locate(kbs, kb0, records, FMT, d, chunk);
-        const bool fast0 = w0.nk == KB && ((size_t)w0.rc * width) % 16 == 0;
-        load16<FMT>(w0.rec, d, w0.rc, h * 64 + lc, w0.o + seg, w0.nk - seg, fast0, tk);
-        load16<FMT>(w0.rec, d, w0.rc, d + h * 64 + lc, w0.o + seg, w0.nk - seg, fast0, tv);
-    }
-    for (int kb = kb0; kb < kb1; kb++) {
-        const Where w = locate(kbs, kb, records, FMT, d, chunk);
-        __syncthreads();  // the previous block's tiles are no longer read
-#pragma unroll
-        for (int i = 0; i < 16; i += 4) {
-            *reinterpret_cast<float4 *>(&Ks[lc][seg + i]) = make_float4(tk[i], tk[i + 1], tk[i + 2], tk[i + 3]);
-            *reinterpret_cast<float4 *>(&Vs[lc][seg + i]) = make_float4(tv[i], tv[i + 1], tv[i + 2], tv[i + 3]);
-        }
-        if (kb + 1 < kb1) {
-            const Where wn = locate(kbs, kb + 1, records, FMT, d, chunk);
-            const bool fastn = wn.nk == KB && ((size_t)wn.rc * width) % 16 == 0;
-            load16<FMT>(wn.rec, d, wn.rc, h * 64 + lc, wn.o + seg, wn.nk - seg, fastn, tk);
-            load16<FMT>(wn.rec, d, wn.rc, d + h * 64 + lc, wn.o + seg, wn.nk - seg, fastn, tv);
-        }
-        __syncthreads();
-
-        // S^T = K Q^T: lane holds S[q = r16 of group j][key = 16 kb4 + 4 g4 + v]
-        floatx4 sacc[QW][4];
-#pragma unroll
-        for (int j = 0; j < QW; j++)
-#pragma unroll
-            for (int kb4 = 0; kb4 < 4; kb4++) sacc[j][kb4] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int cs = 0; cs < 4; cs++)
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const int c = 16 * cs + 4 * g4 + t;
-#pragma unroll
-                for (int kb4 = 0; kb4 < 4; kb4++) {
-                    const float a = Ks[c][16 * kb4 + r16];
-#pragma unroll
-                    for (int j = 0; j < QW; j++)
-                        sacc[j][kb4] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, qreg[j][4 * cs + t], sacc[j][kb4], 0, 0, 0);
-                }
-            }
-        // online softmax per query over the block's 64 keys (16 on this lane, the rest on lanes ^16, ^32)
-#pragma unroll
-        for (int j = 0; j < QW; j++) {
-            float mb = -INFINITY;
-#pragma unroll
-            for (int kb4 = 0; kb4 < 4; kb4++)
-#pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    if (16 * kb4 + 4 * g4 + v >= w.nk) sacc[j][kb4][v] = -INFINITY;
-                    mb = fmaxf(mb, sacc[j][kb4][v]);
-                }
-            mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
-            mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
-            const float mnew = fmaxf(m[j], mb);
-            const float alpha = fast_exp(m[j] - mnew);
-            float lb = 0.0f;
-#pragma unroll
-            for (int kb4 = 0; kb4 < 4; kb4++)
-#pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    const float p = fast_exp(sacc[j][kb4][v] - mnew);
-                    sacc[j][kb4][v] = p;
-                    lb += p;
-                }
-            lb += __shfl_xor(lb, 16, 64);
-            lb += __shfl_xor(lb, 32, 64);
-            l[j] = l[j] * alpha + lb;
-            m[j] = mnew;
-#pragma unroll
-            for (int db = 0; db < 4; db++) acc_o[j][db] *= alpha;
-        }
-        // O^T += V^T P^T: lane holds O[q = r16 of group j][dim = 16 db + 4 g4 + v]
-#pragma unroll
-        for (int kb4 = 0; kb4 < 4; kb4++) {
-            float vv[4][4];
-#pragma unroll
-            for (int db = 0; db < 4; db++) {
-                const float4 v4 = *reinterpret_cast<const float4 *>(&Vs[16 * db + r16][16 * kb4 + 4 * g4]);
-                vv[db][0] = v4.x;
-                vv[db][1] = v4.y;
-                vv[db][2] = v4.z;
-                vv[db][3] = v4.w;
-            }
-            // consecutive MFMAs go to different accumulators
-#pragma unroll
-            for (int v = 0; v < 4; v++)
-#pragma unroll
-                for (int db = 0; db < 4; db++)
-#pragma unroll
-                    for (int j = 0; j < QW; j++)
-                        acc_o[j][db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[db][v], sacc[j][kb4][v], acc_o[j][db], 0, 0, 0);
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < QW; j++) {
-        if (!qlive[j]) continue;
-        if (splits == 1) {
-            const float inv = 1.0f / l[j];
-#pragma unroll
-            for (int db = 0; db < 4; db++)
-                *reinterpret_cast<float4 *>(out + (size_t)qrow[j] * d + h * 64 + 16 * db + 4 * g4) =
-                    make_float4(acc_o[j][db][0] * inv, acc_o[j][db][1] * inv, acc_o[j][db][2] * inv, acc_o[j][db][3] * inv);
-        } else {
-            const size_t at = ((size_t)split * nq + qrow[j]) * heads + h;
-#pragma unroll
-            for (int db = 0; db < 4; db++)
-                *reinterpret_cast<float4 *>(part_o + at * 64 + 16 * db + 4 * g4) =
-                    make_float4(acc_o[j][db][0], acc_o[j][db][1], acc_o[j][db][2], acc_o[j][db][3]);
-            if (g4 == 0) {
-                part_ml[at * 2] = m[j] * LOG2E;
-                part_ml[at * 2 + 1] = l[j];
-            }
-        }
     }
 }
 
@@ -668,8 +491,9 @@ __global__ __launch_bounds__(256) void k_kv_images(int rows, int chunk, int d, i
 }
 
 // ---- split-fp16 MFMA kernel: head width 64 over tile images --------------------------------------------------
-// A flat grid of qtiles x heads x splits workgroups (remapped XCD by XCD as in k_attn_mfma64) of WAVES wavefronts x
-// 32 queries, two wavefronts a SIMD: 8 wavefronts (256 queries, one workgroup a compute unit) for many queries, 4 (two
+// A flat grid of qtiles x heads x splits workgroups of WAVES wavefronts x 32 queries (the flat index remapped so that
+// the query tiles sharing a (head, key range) run on the same XCD: workgroup i is dispatched to XCD i % 8, and the
+// tiles of one (head, range) then read the same images through one L2), two wavefronts a SIMD: 8 wavefronts (256 queries, one workgroup a compute unit) for many queries, 4 (two
 // workgroups a compute unit) otherwise. Key blocks of 64 stream through LDS in two rings of two 16 KB buffers, one
 // for the blocks' key halves (K hi, K lo) and one for their value halves (V hi, V lo), copied global -> LDS directly
 // (global_load_lds_dwordx4); one barrier per block.
@@ -1088,7 +912,7 @@ void merge_splits(hipStream_t s, int nq, int d, int heads, int splits, const flo
 
 // ---- planning and launch --------------------------------------------------------------------------------------
 struct AttnPlan {
-    bool mfma, split16;
+    bool split16;
     int splits, kb_per_split, groups, waves;
 };
 
@@ -1134,17 +958,16 @@ static AttnPlan plan(const AttnShape &a, bool images) {
     AttnPlan p;
     const KeyBlocks k = key_blocks(a.rows, a.chunk);
     const int hd = a.d / a.heads;
-    p.mfma = hd == 64 && a.nq >= 32;
-    p.split16 = p.mfma && images && kv_images_apply(a.kv_format, a.d, a.heads);
+    p.split16 = hd == 64 && a.nq >= SPLIT16_MIN_Q && images && kv_images_apply(a.kv_format, a.d, a.heads);
     // k_attn_split64: 256 queries a workgroup (one a compute unit, one wave of them) from 512 queries on, else 128
     // (two a compute unit, two waves of them)
     p.waves = p.split16 && a.nq >= 512 ? 8 : 4;
-    const int per_group = p.split16 ? 32 * p.waves : (p.mfma ? 64 * QW : QG);
+    const int per_group = p.split16 ? 32 * p.waves : QG;
     p.groups = (a.nq + per_group - 1) / per_group;
     // enough workgroups to fill the 256 compute units about once (twice for the smaller workgroups of two or more
     // query tiles), each with at least 2 key blocks: more, shorter key ranges measured slower at every batch (the
     // merge and each workgroup's fixed costs grow with them; 64 queries: 22 us at 256 workgroups against 36 at 632)
-    if (!p.mfma && hd == 64) {
+    if (!p.split16 && hd == 64) {
         // the decode kernel's wavefronts each take a key block of their own: four blocks a workgroup
         p.kb_per_split = std::min(4, k.n_kb);
         p.splits = (k.n_kb + p.kb_per_split - 1) / p.kb_per_split;
@@ -1169,10 +992,7 @@ size_t attention_work_bytes(const AttnShape &a) {
 template <int FMT>
 static void launch(hipStream_t s, const AttnShape &a, const AttnPlan &p, const float *q, const uint8_t *records, float *out,
                    float *part_o, float *part_ml) {
-    if (p.mfma) {
-        hipLaunchKernelGGL(k_attn_mfma64<FMT>, dim3(p.groups * a.heads * p.splits), dim3(256), 0, s, a.nq, a.rows,
-                           a.chunk, a.d, a.heads, q, records, p.kb_per_split, p.groups, p.splits, part_o, part_ml, out);
-    } else if (a.d / a.heads == 64) {
+    if (a.d / a.heads == 64) {
         hipLaunchKernelGGL(k_attn_decode_w<FMT>, dim3(p.splits, a.heads, p.groups), dim3(256), 0, s, a.nq, a.rows,
                            a.chunk, a.d, a.heads, q, records, p.kb_per_split, part_o, part_ml, out);
     } else {
