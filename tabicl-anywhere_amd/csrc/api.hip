@@ -523,7 +523,7 @@ static KvImages images_of(const tah_model *m, int l) {
 
 // The images of f32 records rec32 in a loaned buffer when the split-fp16 kernel applies to a's queries, else none.
 static const KvImages *loan_images(hipStream_t s, Loans &loans, const AttnShape &a, const uint8_t *rec32, KvImages &img) {
-    if (a.nq <= 8 || !kv_images_apply(a.kv_format, a.d, a.heads)) return nullptr;
+    if (a.nq < TAH_SPLIT16_MIN_Q || !kv_images_apply(a.kv_format, a.d, a.heads)) return nullptr;
     img = kv_images_at(loans.take<uint8_t>(kv_images_bytes(a.rows, a.chunk, a.heads)), a.rows, a.chunk, a.heads);
     kv_images(s, a.rows, a.chunk, a.d, a.heads, a.kv_format, rec32, img);
     return &img;
@@ -900,7 +900,7 @@ extern "C" int tah_in_context(tah_dev *dev, const tah_weights *w, const float *h
         const AttnShape a{rows, rows, chunk, d, w->icl_heads, TAH_KV_F32};
         void *work = loans.take<uint8_t>(attention_work_bytes(a));
         KvImages img;
-        const bool use_img = rows > 8 && kv_images_apply(TAH_KV_F32, d, w->icl_heads);
+        const bool use_img = rows >= TAH_SPLIT16_MIN_Q && kv_images_apply(TAH_KV_F32, d, w->icl_heads);
         if (use_img)
             img = kv_images_at(loans.take<uint8_t>(kv_images_bytes(rows, chunk, w->icl_heads)), rows, chunk, w->icl_heads);
         staging(dev, lbytes);
@@ -1392,7 +1392,7 @@ static size_t attend_call_bytes(int nq, int rows, int d, int heads) {
     const AttnShape a{nq, rows, 256, d, heads, TAH_KV_F32};
     size_t b = loan_bytes({(size_t)nq * d, 2 * (size_t)rows * d, 2 * (size_t)rows * d, (size_t)nq * d}) +
                loan_raw(attention_work_bytes(a));
-    if (nq > 8 && kv_images_apply(TAH_KV_F32, d, heads)) b += loan_raw(kv_images_bytes(rows, 256, heads));
+    if (nq >= TAH_SPLIT16_MIN_Q && kv_images_apply(TAH_KV_F32, d, heads)) b += loan_raw(kv_images_bytes(rows, 256, heads));
     return b;
 }
 

@@ -35,8 +35,9 @@ namespace tah {
 constexpr int KB = 64;   // keys per block
 constexpr int QG = 8;    // queries per decode workgroup
 // From this many queries the matrix kernel (one read of the images for up to 128 queries) beats the decode kernel
-// (one read of the records per 8 queries)
-constexpr int SPLIT16_MIN_Q = QG + 1;
+// (whose work grows with the queries: 3 rows 0.888 ms a prediction either way, 4 rows 0.924 -> 0.902 ms, 8 rows
+// 1.127 -> 0.913 ms with the matrix kernel)
+constexpr int SPLIT16_MIN_Q = TAH_SPLIT16_MIN_Q;
 
 struct KeyBlocks {
     int bpc;       // key blocks per full chunk

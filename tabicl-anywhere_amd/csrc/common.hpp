@@ -234,6 +234,9 @@ KvImages kv_images_at(uint8_t *base, int rows, int chunk, int heads);
 void kv_images(hipStream_t s, int rows, int chunk, int d, int heads, int kv_format, const uint8_t *records,
                KvImages img);
 // img (optional): the layer's images, used for 32 queries or more.
+// Queries from which the attention runs on the matrix cores over tile images (made for transient layers from then on)
+constexpr int TAH_SPLIT16_MIN_Q = 4;
+
 // Launch probe of the many-query attention kernel (attention.hip): arm for a stream with room for `launches`
 // launches (0 disarms); read synchronises the stream, returns the launches recorded since the last read and their
 // summed duration in ms.

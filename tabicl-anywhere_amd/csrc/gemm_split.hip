@@ -436,18 +436,20 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
     }
 }
 
-// Few rows (9 to FEW_ROWS: the in-context stage of a small batch): one workgroup per 32 rows x 32 TN columns, its
+// Few rows (4 to FEW_ROWS: the in-context stage of a small batch): one workgroup per 32 rows x 32 TN columns, its
 // eight wavefronts splitting K = 128 NST eight ways (NST 16-column steps each, one power of two per row and
 // wavefront). With so few steps a pipelined loop waits for memory once per step or two; here every global read of
 // the workgroup is issued at its start -- the wavefront's weight steps, its rows' slice of X, the epilogue's bias and
-// residual (a bias is required), with LN the norm's weights and with QM the query MLP's weight images, biases and scales (both staged in
-// LDS) -- so that one memory latency precedes the products. The partial products, unscaled to f32, are summed
+// residual (a bias is required), with LN the norm's weights and with QM the query MLP's weight images, biases and
+// scales (both staged in LDS) -- so that one memory latency precedes the products. The partial products, unscaled to f32, are summed
 // through LDS in wavefront order; wavefront w finishes accumulators 2 w and 2 w + 1 of every tile (two adjacent
 // columns of the lane's row). With QM (one head of 64 columns a workgroup, TN = 2) the finished tile goes through
 // LDS to wavefront 0, which runs the head's query MLP (qmlp64_lane) from the staged weights.
 constexpr int FEW_WAVES = 8;
 constexpr int FEW_ROWS = 256;
-constexpr int GEMV_SPLIT_ROWS = 8;  // up to this many rows the f32 kernels (k_gemv) take the dense layers
+// up to this many rows the f32 kernels (k_gemv, k_qmlp_rows) take the dense layers: their work grows with the rows,
+// and from 4 rows k_dense_few is faster
+constexpr int GEMV_SPLIT_ROWS = 3;
 constexpr int QPITCH = 68;  // row pitch of the query tile in LDS
 
 template <int EPI, bool LN, int TN, int NST, bool QM>
@@ -797,7 +799,7 @@ static void launch_splitk4(hipStream_t s, int M, int N, int K, const float *X, i
 
 bool query_split_fits(const DevBlock &b, int M, const float *X, int ldx, const float *Y) {
     const SplitW &w = b.in_s;
-    return M > 8 && w.img && b.in_b && w.row0 == 0 && w.K == b.d && b.d == 512 && b.d % 128 == 0 && b.heads > 0 &&
+    return M > GEMV_SPLIT_ROWS && w.img && b.in_b && w.row0 == 0 && w.K == b.d && b.d == 512 && b.d % 128 == 0 && b.heads > 0 &&
            b.d == 64 * b.heads && qmlp_fused(b) && b.n1w && b.n1b && ldx % 4 == 0 &&
            (reinterpret_cast<uintptr_t>(X) & 15) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0 &&
            (size_t)(M + 31) / 32 <= 65535;

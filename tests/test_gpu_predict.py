@@ -53,7 +53,7 @@ def random_layers(rng, layers, rows, chunk, d, kv_format, scale=1.0):
 
 @pytest.mark.parametrize("kv_format", [abi.KV_F32, abi.KV_I16, abi.KV_I8])
 @pytest.mark.parametrize("rows,chunk", [(10000, 256), (1000, 48), (37, 8), (50, 64)])
-@pytest.mark.parametrize("nq", [1, 7, 9, 16, 64, 130])
+@pytest.mark.parametrize("nq", [1, 3, 4, 7, 9, 16, 64, 130])
 def test_attention_full_width(gpu, full_model, full_weights, kv_format, rows, chunk, nq):
     """AttendCached::attend at d = 512, 8 heads of 64: decode path below 64 queries, MFMA path above."""
     say(f"attention d=512 fmt={kv_format} rows={rows} chunk={chunk} nq={nq}")
@@ -171,7 +171,7 @@ def test_stage_tiny_matches_oracle_and_reference(gpu, tiny_model, tiny_raw):
 
 
 @pytest.mark.parametrize("kv_format", [abi.KV_F32, abi.KV_I16, abi.KV_I8])
-@pytest.mark.parametrize("nq", [1, 7, 8, 20, 64, 200, 600])
+@pytest.mark.parametrize("nq", [1, 3, 4, 7, 8, 20, 64, 200, 600])
 def test_stage_full_size(gpu, full_model, full_weights, kv_format, nq):
     """The whole in-context stage (12 layers of 8 x 64 heads, d = 512, then the decoder) over a stored cache of
     2,000 rows, against the oracle on the same inputs."""
