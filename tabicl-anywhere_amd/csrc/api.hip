@@ -518,21 +518,23 @@ static const uint8_t *layer_of(const tah_model *m, int l) { return m->records + 
 static KvImages images_of(const tah_model *m, int l) {
     if (!m->images) return KvImages{};
     uint8_t *base = m->records + (size_t)l * m->layer_bytes + align256(layer_bytes(m->kv_format, m->rows, m->chunk, m->d));
-    return kv_images_at(base, m->rows, m->chunk, m->heads);
+    return kv_images_at(base, m->rows, m->chunk, m->heads, m->kv_format);
 }
 
 // The images of f32 records rec32 in a loaned buffer when the split-fp16 kernel applies to a's queries, else none.
 static const KvImages *loan_images(hipStream_t s, Loans &loans, const AttnShape &a, const uint8_t *rec32, KvImages &img) {
     if (a.nq < TAH_SPLIT16_MIN_Q || !kv_images_apply(a.kv_format, a.d, a.heads)) return nullptr;
-    img = kv_images_at(loans.take<uint8_t>(kv_images_bytes(a.rows, a.chunk, a.heads)), a.rows, a.chunk, a.heads);
+    img = kv_images_at(loans.take<uint8_t>(kv_images_bytes(a.rows, a.chunk, a.heads, a.kv_format)), a.rows, a.chunk,
+                       a.heads, a.kv_format);
     kv_images(s, a.rows, a.chunk, a.d, a.heads, a.kv_format, rec32, img);
     return &img;
 }
 
-// Per layer: the records as they are, then (f32, head width 64) the layer's split-fp16 tile images.
+// Per layer: the records as they are, then (head width 64) the layer's tile images (split-fp16 values for f32 and i16
+// records, the codes and their scales for i8).
 static size_t model_layer_bytes(int kv_format, int rows, int chunk, int d, int heads) {
     size_t b = align256(layer_bytes(kv_format, rows, chunk, d));
-    if (kv_images_apply(kv_format, d, heads)) b += align256(kv_images_bytes(rows, chunk, heads));
+    if (kv_images_apply(kv_format, d, heads)) b += align256(kv_images_bytes(rows, chunk, heads, kv_format));
     return b;
 }
 
@@ -902,7 +904,8 @@ extern "C" int tah_in_context(tah_dev *dev, const tah_weights *w, const float *h
         KvImages img;
         const bool use_img = rows >= TAH_SPLIT16_MIN_Q && kv_images_apply(TAH_KV_F32, d, w->icl_heads);
         if (use_img)
-            img = kv_images_at(loans.take<uint8_t>(kv_images_bytes(rows, chunk, w->icl_heads)), rows, chunk, w->icl_heads);
+            img = kv_images_at(loans.take<uint8_t>(kv_images_bytes(rows, chunk, w->icl_heads, TAH_KV_F32)), rows, chunk,
+                               w->icl_heads, TAH_KV_F32);
         staging(dev, lbytes);
         TAH_HIP(hipMemcpyAsync(h, h_host, n * sizeof(float), hipMemcpyHostToDevice, s));
         TAH_HIP(hipMemcpyAsync(sc, scales, sizeof(float) * L * d, hipMemcpyHostToDevice, s));
@@ -1392,7 +1395,7 @@ static size_t attend_call_bytes(int nq, int rows, int d, int heads) {
     const AttnShape a{nq, rows, 256, d, heads, TAH_KV_F32};
     size_t b = loan_bytes({(size_t)nq * d, 2 * (size_t)rows * d, 2 * (size_t)rows * d, (size_t)nq * d}) +
                loan_raw(attention_work_bytes(a));
-    if (nq >= TAH_SPLIT16_MIN_Q && kv_images_apply(TAH_KV_F32, d, heads)) b += loan_raw(kv_images_bytes(rows, 256, heads));
+    if (nq >= TAH_SPLIT16_MIN_Q && kv_images_apply(TAH_KV_F32, d, heads)) b += loan_raw(kv_images_bytes(rows, 256, heads, TAH_KV_F32));
     return b;
 }
 

@@ -398,9 +398,21 @@ __global__ __launch_bounds__(256) void k_attn_decode_w(int nq, int rows, int chu
 // keys are scaled by 2^sk and values by 2^sv, the powers of two that bring the layer's largest magnitude of that
 // head below 2^14; kvmax holds those maxima (f32 bits) per head, [heads][2].
 constexpr int IMG = 32768;
+// i8 caches: code images. The codes are integers of at most 127 in magnitude, exact in fp16, so an image holds them
+// as they are, one plane each (K codes [key][coordinate], then V codes [coordinate][key], in the layout of the
+// planes above), and the scales stay beside them: per (chunk, head) the head's 64 key scales, its 64 value scales
+// (a zero scale, whose coordinate's codes are all zero, stored as 1) and the 64 ratios of the previous chunk's value
+// scales to these (1 for the first chunk): scale table [chunks][heads][3][64]. Scores are then (q * key scales) .
+// codes, two products of the split query with the codes; the weighted sums codes . weights, two products of the split
+// weights, kept in units of the current chunk's value scales (multiplied by the ratios when a chunk begins, by the
+// value scales at the end).
+constexpr int IMG8 = 16384;
+constexpr int SCL = 768;  // bytes of one (chunk, head)'s scales
 
-__host__ __device__ inline size_t image_bytes_of(int rows, int chunk, int heads) {
-    return (size_t)key_blocks(rows, chunk).n_kb * heads * IMG;
+__host__ __device__ inline int img_bytes(bool codes) { return codes ? IMG8 : IMG; }
+
+__host__ __device__ inline size_t image_bytes_of(int rows, int chunk, int heads, bool codes) {
+    return (size_t)key_blocks(rows, chunk).n_kb * heads * img_bytes(codes);
 }
 
 // rows r and r + 1 already sit in different bank halves (128-byte rows); rows of one parity among 16 consecutive ones
@@ -491,6 +503,58 @@ __global__ __launch_bounds__(256) void k_kv_images(int rows, int chunk, int d, i
     }
 }
 
+// grid (key blocks, heads); 256 threads: one code image of an i8 layer, and (by a chunk's first block) the chunk's
+// scales of the head. Thread t: coordinate t / 4, keys 16 (t % 4) .. + 15 of the block (zeros past its end).
+__global__ __launch_bounds__(256) void k_kv_codes(int rows, int chunk, int d, int heads, const uint8_t *__restrict__ records,
+                                                  uint8_t *__restrict__ images, float *__restrict__ scales) {
+    __shared__ _Float16 Ks[64][KB + 8];  // [coordinate][key]
+    __shared__ _Float16 Vs[64][KB + 8];
+    const int kb = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    const KeyBlocks kbs = key_blocks(rows, chunk);
+    const Where w = locate(kbs, kb, records, TAH_KV_I8, d, chunk);
+    const int lc = tid >> 2, seg = (tid & 3) * 16;
+    const int8_t *body = reinterpret_cast<const int8_t *>(w.rec + 8 * (size_t)d);
+    const int8_t *kr = body + (size_t)(h * 64 + lc) * w.rc + w.o, *vr = body + (size_t)(d + h * 64 + lc) * w.rc + w.o;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const bool in = seg + i < w.nk;
+        Ks[lc][seg + i] = (_Float16)(in ? (float)kr[seg + i] : 0.0f);
+        Vs[lc][seg + i] = (_Float16)(in ? (float)vr[seg + i] : 0.0f);
+    }
+    if (kb % kbs.bpc == 0 && tid < 192) {
+        // the record's scales: d key scales then d value scales (the previous chunk's record precedes it)
+        const int ci = kb / kbs.bpc, c = tid & 63;
+        const float *sc = reinterpret_cast<const float *>(w.rec);
+        float v;
+        if (tid < 64) {
+            v = sc[h * 64 + c];
+        } else {
+            const float vs = sc[d + h * 64 + c], vsn = vs == 0.0f ? 1.0f : vs;
+            if (tid < 128) {
+                v = vsn;
+            } else {
+                const float *pc = reinterpret_cast<const float *>(w.rec - record_bytes(TAH_KV_I8, d, chunk));
+                const float pv = ci == 0 ? 1.0f : pc[d + h * 64 + c];
+                v = ci == 0 ? 1.0f : (pv == 0.0f ? 1.0f : pv) / vsn;
+            }
+        }
+        scales[((size_t)ci * heads + h) * 192 + tid] = v;
+    }
+    __syncthreads();
+    uint8_t *img = images + ((size_t)kb * heads + h) * IMG8;
+    for (int u = tid; u < 512; u += 256) {
+        const int r = u >> 3, c = u & 7;
+        halfx8 kc, vc;
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            kc[t] = Ks[8 * c + t][r];  // key r, coordinate 8c + t
+            vc[t] = Vs[r][8 * c + t];  // coordinate r, key 8c + t
+        }
+        *reinterpret_cast<halfx8 *>(img + r * 128 + swz(r, c) * 16) = kc;
+        *reinterpret_cast<halfx8 *>(img + 8192 + r * 128 + swz(r, c) * 16) = vc;
+    }
+}
+
 // ---- split-fp16 MFMA kernel: head width 64 over tile images --------------------------------------------------
 // A flat grid of qtiles x heads x splits workgroups of WAVES wavefronts x 32 queries (the flat index remapped so that
 // the query tiles sharing a (head, key range) run on the same XCD: workgroup i is dispatched to XCD i % 8, and the
@@ -514,11 +578,12 @@ __global__ __launch_bounds__(256) void k_kv_images(int rows, int chunk, int d, i
 // more than 3 (then the sums are rescaled): weights exp2(t - ref + 12) stay below 2^15, inside fp16, and most blocks
 // skip the rescaling.
 
-// Half an image (its keys or its values, 16 KB) into an LDS buffer, 16 bytes a lane: in copy i, wavefront w fills
-// the 1 KB at chunk 64 (WAVES i + w) (a wavefront-uniform LDS base; the lanes' offsets are implicit).
-template <int WAVES>
+// Half an image (its keys or its values: BYTES, 16 KB of split values or 8 KB of codes) into an LDS buffer, 16 bytes
+// a lane: in copy i, wavefront w fills the 1 KB at chunk 64 (WAVES i + w) (a wavefront-uniform LDS base; the lanes'
+// offsets are implicit).
+template <int WAVES, int BYTES>
 __device__ __forceinline__ void half_image_to_lds(const uint8_t *src, uint8_t *dst, int tid) {
-    constexpr int T = 64 * WAVES, CHUNKS = IMG / 32;
+    constexpr int T = 64 * WAVES, CHUNKS = BYTES / 16;
     const int w = tid >> 6;
 #pragma unroll
     for (int i = 0; i < (CHUNKS + T - 1) / T; i++) {
@@ -534,14 +599,26 @@ struct Flag {
     static constexpr bool value = B;
 };
 
-template <int WAVES>
+// With CODES (i8 caches) the images hold the codes and `scl` the scales (k_kv_codes): the scores are two products of
+// the query, multiplied by the chunk's key scales and split again whenever a block starts a new chunk (the raw query
+// waits in LDS), with the key codes; the weighted sums two products of the split weights with the value codes, kept
+// in units of the current chunk's value scales (multiplied by the table's ratios when a block begins a chunk, by the
+// last chunk's value scales at the end: no second set of sums). The scales of a chunk are copied into a four-deep LDS
+// ring (DMA, two blocks ahead like the images), which a chunk's blocks use until the one after next begins.
+template <int WAVES, bool CODES>
 __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows, int chunk, int d, int heads,
                                                                const float *__restrict__ q,
                                                                const uint8_t *__restrict__ images,
-                                                               const uint32_t *__restrict__ kvmax, int kb_per_split,
+                                                               const uint32_t *__restrict__ kvmax,
+                                                               const float *__restrict__ scl, int kb_per_split,
                                                                int qtiles, int splits, float *__restrict__ part_o,
                                                                float *__restrict__ part_ml, float *__restrict__ out) {
-    __shared__ __align__(16) uint8_t kt[2][IMG / 2], vt[2][IMG / 2];
+    constexpr int HB = CODES ? IMG8 / 2 : IMG / 2;  // bytes of an image's keys (or values)
+    constexpr int IS = CODES ? IMG8 : IMG;          // bytes of an image
+    __shared__ __align__(16) uint8_t kt[2][HB], vt[2][HB];
+    __shared__ __align__(16) float sb[CODES ? 4 : 1][192];  // CODES: scale ring, [chunk % 4][key, value, ratio]
+    // CODES: each lane's 32 query coordinates, kept for the per-chunk splits: [wavefront][8 chunks of 4][lane][4]
+    __shared__ __align__(16) float qraw[CODES ? WAVES : 1][CODES ? 8 * 64 * 4 : 4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int total = qtiles * heads * splits;
     int flat = blockIdx.x;
@@ -553,12 +630,22 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows
     const int r32 = lane & 31, g = lane >> 5;
     const int qrow = qt * 32 * WAVES + wave * 32 + r32;
     const bool qlive = qrow < nq;
-    const uint8_t *head_images = images + (size_t)h * IMG;
-    const size_t kb_stride = (size_t)heads * IMG;
+    const uint8_t *head_images = images + (size_t)h * IS;
+    const size_t kb_stride = (size_t)heads * IS;
+    // CODES: chunk ci's scales of this head into ring slot ci % 4 (wavefront 0, 48 lanes x 16 bytes)
+    auto scales_to_lds = [&](int ci) {
+        if (wave == 0 && lane < 48)
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t *>(scl + ((size_t)ci * heads + h) * 192 + 4 * lane),
+                                             reinterpret_cast<uint8_t *>(&sb[ci & 3][0]), 16, 0, 0);
+    };
     if (kb0 < kb1) {
-        half_image_to_lds<WAVES>(head_images + kb0 * kb_stride, kt[0], tid);
-        half_image_to_lds<WAVES>(head_images + kb0 * kb_stride + IMG / 2, vt[0], tid);
-        if (kb0 + 1 < kb1) half_image_to_lds<WAVES>(head_images + (kb0 + 1) * kb_stride, kt[1], tid);
+        half_image_to_lds<WAVES, HB>(head_images + kb0 * kb_stride, kt[0], tid);
+        half_image_to_lds<WAVES, HB>(head_images + kb0 * kb_stride + HB, vt[0], tid);
+        if (kb0 + 1 < kb1) half_image_to_lds<WAVES, HB>(head_images + (kb0 + 1) * kb_stride, kt[1], tid);
+        if constexpr (CODES) {
+            scales_to_lds(kb0 / kbs.bpc);
+            if (kb0 + 1 < kb1 && (kb0 + 1) % kbs.bpc == 0) scales_to_lds((kb0 + 1) / kbs.bpc);
+        }
     }
 
     // this lane's query coordinates 16 dc + 8 g + t, scaled to a maximum magnitude near 2^14 and split
@@ -574,45 +661,93 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows
         qv[dc][0] = a.x; qv[dc][1] = a.y; qv[dc][2] = a.z; qv[dc][3] = a.w;
         qv[dc][4] = b.x; qv[dc][5] = b.y; qv[dc][6] = b.z; qv[dc][7] = b.w;
     }
-    float qmax = 0.0f;
-#pragma unroll
-    for (int dc = 0; dc < 4; dc++)
-#pragma unroll
-        for (int t = 0; t < 8; t++) qmax = fmaxf(qmax, fabsf(qv[dc][t]));
-    qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
-    const int eq = shift_for(__float_as_uint(qmax));
+    // the query split into fp16 halves at a maximum near 2^14 (CODES: times chunk ci's key scales first); returns the
+    // factor that takes a raw score to score * log2 e
     halfx8 qh[4], ql[4];
+    if constexpr (CODES) {
 #pragma unroll
-    for (int dc = 0; dc < 4; dc++) {
-        u32x4 hw, lw;
+        for (int dc = 0; dc < 4; dc++)
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-            uint32_t hi, lo;
-            split2(ldexpf(qv[dc][2 * t], eq), ldexpf(qv[dc][2 * t + 1], eq), hi, lo);
-            hw[t] = hi;
-            lw[t] = lo;
-        }
-        qh[dc] = __builtin_bit_cast(halfx8, hw);
-        ql[dc] = __builtin_bit_cast(halfx8, lw);
+            for (int hf = 0; hf < 2; hf++)
+                *reinterpret_cast<float4 *>(&qraw[wave][((2 * dc + hf) * 64 + lane) * 4]) =
+                    make_float4(qv[dc][4 * hf], qv[dc][4 * hf + 1], qv[dc][4 * hf + 2], qv[dc][4 * hf + 3]);
     }
-    const int sk = shift_for(kvmax[h * 2]), sv = shift_for(kvmax[h * 2 + 1]);
-    const float to_log2 = ldexpf(LOG2E, -(sk + eq));  // raw score -> score * log2 e
+    auto qsplit = [&](int ci) {
+        float qs[4][8];
+#pragma unroll
+        for (int dc = 0; dc < 4; dc++) {
+            if constexpr (CODES) {
+                float ks[8];
+                load8(&sb[ci & 3][16 * dc + 8 * g], ks);
+#pragma unroll
+                for (int hf = 0; hf < 2; hf++) {
+                    const float4 r4 = *reinterpret_cast<const float4 *>(&qraw[wave][((2 * dc + hf) * 64 + lane) * 4]);
+                    qs[dc][4 * hf] = r4.x * ks[4 * hf];
+                    qs[dc][4 * hf + 1] = r4.y * ks[4 * hf + 1];
+                    qs[dc][4 * hf + 2] = r4.z * ks[4 * hf + 2];
+                    qs[dc][4 * hf + 3] = r4.w * ks[4 * hf + 3];
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < 8; t++) qs[dc][t] = qv[dc][t];
+            }
+        }
+        float qmax = 0.0f;
+#pragma unroll
+        for (int dc = 0; dc < 4; dc++)
+#pragma unroll
+            for (int t = 0; t < 8; t++) qmax = fmaxf(qmax, fabsf(qs[dc][t]));
+        qmax = fmaxf(qmax, __shfl_xor(qmax, 32, 64));
+        const int eq = shift_for(__float_as_uint(qmax));
+#pragma unroll
+        for (int dc = 0; dc < 4; dc++) {
+            u32x4 hw, lw;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                uint32_t hi, lo;
+                split2(ldexpf(qs[dc][2 * t], eq), ldexpf(qs[dc][2 * t + 1], eq), hi, lo);
+                hw[t] = hi;
+                lw[t] = lo;
+            }
+            qh[dc] = __builtin_bit_cast(halfx8, hw);
+            ql[dc] = __builtin_bit_cast(halfx8, lw);
+        }
+        return ldexpf(LOG2E, -((CODES ? 0 : shift_for(kvmax[h * 2])) + eq));
+    };
+    const int sv = CODES ? 0 : shift_for(kvmax[h * 2 + 1]);
+    float tl_q = CODES ? 0.0f : qsplit(0);  // CODES: split per chunk, below
+    int qchunk = -1;
 
     // A-operand row of this lane in a 32-key half: key sigma(r32)
     const int krow = sigma32(r32);
     float ref = -INFINITY, l = 0.0f;
-    floatx16 acc_o[2];
+    floatx16 acc_o[2];  // CODES: in units of the current chunk's value scales
 #pragma unroll
     for (int db = 0; db < 2; db++)
 #pragma unroll
         for (int v = 0; v < 16; v++) acc_o[db][v] = 0.0f;
+    // CODES: acc_o *= row `which` (1 value scales, 2 ratios) of chunk ci's scales; accumulator v of dim block db holds
+    // coordinate 32 db + 8 (v / 4) + 4 g + v % 4
+    auto scale_sums = [&](int ci, int which) {
+        const float *f = &sb[ci & 3][64 * which];
+#pragma unroll
+        for (int db = 0; db < 2; db++)
+#pragma unroll
+            for (int v4 = 0; v4 < 4; v4++) {
+                const float4 f4 = *reinterpret_cast<const float4 *>(f + 32 * db + 8 * v4 + 4 * g);
+                acc_o[db][4 * v4] *= f4.x;
+                acc_o[db][4 * v4 + 1] *= f4.y;
+                acc_o[db][4 * v4 + 2] *= f4.z;
+                acc_o[db][4 * v4 + 3] *= f4.w;
+            }
+    };
     floatx16 zero;
 #pragma unroll
     for (int v = 0; v < 16; v++) zero[v] = 0.0f;
 
     // block kb's raw scores: keys past the block's end set to -inf, then the maximum over the query's 64 keys (both
     // halves of the wavefront) in log2 units
-    auto mask_and_max = [&](floatx16 (&sc)[2], int kb) {
+    auto mask_and_max = [&](floatx16 (&sc)[2], int kb, float to_log2) {
         const int ci = kb / kbs.bpc;
         const int nk = min(KB, (ci == kbs.n_chunks - 1 ? kbs.last_rc : chunk) - (kb % kbs.bpc) * KB);
         if (nk < KB) {
@@ -631,7 +766,19 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows
         const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mb), __float_as_uint(mb), false, false);
         return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * to_log2;
     };
-    // S^T of a block from its key half in LDS, products in the order the operands are read (coordinate step outer)
+    // CODES: the query split for block kb's chunk, if that is not the current split already (outside the products'
+    // scheduling regions, so that the split's temporaries are dead before them)
+    auto query_for = [&](int kb) {
+        if constexpr (CODES) {
+            const int ci = kb / kbs.bpc;
+            if (ci != qchunk) {
+                tl_q = qsplit(ci);
+                qchunk = ci;
+            }
+        }
+    };
+    // S^T of a block from its key half in LDS, products in the order the operands are read (coordinate step outer);
+    // returns the block's raw-score factor
     auto scores = [&](const uint8_t *tile, floatx16 (&sc)[2]) {
         halfx8 khi[4][2], klo[4][2];
 #pragma unroll
@@ -641,7 +788,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows
                 const int r = 32 * kh + krow;
                 const int off = r * 128 + swz(r, 2 * dc + g) * 16;
                 khi[dc][kh] = *reinterpret_cast<const halfx8 *>(tile + off);
-                klo[dc][kh] = *reinterpret_cast<const halfx8 *>(tile + 8192 + off);
+                if constexpr (!CODES) klo[dc][kh] = *reinterpret_cast<const halfx8 *>(tile + 8192 + off);
             }
 #pragma unroll
         for (int dc = 0; dc < 4; dc++)
@@ -649,18 +796,25 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows
             for (int kh = 0; kh < 2; kh++) {
                 sc[kh] = mfma16(khi[dc][kh], qh[dc], dc == 0 ? zero : sc[kh]);
                 sc[kh] = mfma16(khi[dc][kh], ql[dc], sc[kh]);
-                sc[kh] = mfma16(klo[dc][kh], qh[dc], sc[kh]);
+                if constexpr (!CODES) sc[kh] = mfma16(klo[dc][kh], qh[dc], sc[kh]);
             }
+        return tl_q;
     };
     // step kb: cur holds block kb's scores; with NEXT, block kb + 1's go into nxt
-    auto step = [&](auto next_flag, floatx16 (&cur)[2], floatx16 (&nxt)[2], int kb) {
+    // step kb: cur holds block kb's scores (raw-score factor tl_cur); with NEXT, block kb + 1's go into nxt (tl_nxt)
+    auto step = [&](auto next_flag, floatx16 (&cur)[2], floatx16 (&nxt)[2], float tl_cur, float &tl_nxt, int kb) {
         constexpr bool NEXT = decltype(next_flag)::value;
         const int sl = (kb - kb0) & 1;
         __builtin_amdgcn_s_waitcnt(0);  // this wavefront's copies of keys kb + 1 and values kb have landed
         __syncthreads();                // everyone's have, and step kb - 1's buffers are no longer read
-        if (kb + 2 < kb1) half_image_to_lds<WAVES>(head_images + (kb + 2) * kb_stride, kt[sl], tid);
-        if (kb + 1 < kb1) half_image_to_lds<WAVES>(head_images + (kb + 1) * kb_stride + IMG / 2, vt[sl ^ 1], tid);
-        const float mb = mask_and_max(cur, kb);
+        if (kb + 2 < kb1) half_image_to_lds<WAVES, HB>(head_images + (kb + 2) * kb_stride, kt[sl], tid);
+        if (kb + 1 < kb1) half_image_to_lds<WAVES, HB>(head_images + (kb + 1) * kb_stride + HB, vt[sl ^ 1], tid);
+        if constexpr (CODES) {
+            if (kb + 2 < kb1 && (kb + 2) % kbs.bpc == 0) scales_to_lds((kb + 2) / kbs.bpc);
+            if (kb > kb0 && kb % kbs.bpc == 0) scale_sums(kb / kbs.bpc, 2);  // block kb begins a chunk
+        }
+        if constexpr (NEXT) query_for(kb + 1);
+        const float mb = mask_and_max(cur, kb, tl_cur);
         const bool grow = mb > ref + 3.0f;
         if (__any(grow)) {
             const float nref = grow ? mb : ref;
@@ -671,7 +825,8 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows
             ref = nref;
         }
         const float off = 12.0f - ref;
-        if constexpr (NEXT) scores(kt[sl ^ 1], nxt);
+        const float to_log2 = tl_cur;
+        if constexpr (NEXT) tl_nxt = scores(kt[sl ^ 1], nxt);
         // block kb's weights, split into fp16 halves for the products
         halfx8 ph[2][2], pl[2][2];
         float ps = 0.0f;
@@ -704,13 +859,36 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows
                     const int r = 32 * db + r32;
                     const int voff = r * 128 + swz(r, 4 * kh + 2 * hh + g) * 16;
                     const halfx8 vhi = *reinterpret_cast<const halfx8 *>(vtile + voff);
-                    const halfx8 vlo = *reinterpret_cast<const halfx8 *>(vtile + 8192 + voff);
-                    acc_o[db] = mfma16(vhi, ph[kh][hh], acc_o[db]);
-                    acc_o[db] = mfma16(vhi, pl[kh][hh], acc_o[db]);
-                    acc_o[db] = mfma16(vlo, ph[kh][hh], acc_o[db]);
+                    if constexpr (CODES) {
+                        acc_o[db] = mfma16(vhi, ph[kh][hh], acc_o[db]);
+                        acc_o[db] = mfma16(vhi, pl[kh][hh], acc_o[db]);
+                    } else {
+                        const halfx8 vlo = *reinterpret_cast<const halfx8 *>(vtile + 8192 + voff);
+                        acc_o[db] = mfma16(vhi, ph[kh][hh], acc_o[db]);
+                        acc_o[db] = mfma16(vhi, pl[kh][hh], acc_o[db]);
+                        acc_o[db] = mfma16(vlo, ph[kh][hh], acc_o[db]);
+                    }
                 }
         l += ps;
-        if constexpr (NEXT) {
+        if constexpr (NEXT && CODES) {
+            // one region: 8 key and 8 value operand reads, 16 + 16 products and the weights' VALU work
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+                if (i < 6) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+                if (i < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+        } else if constexpr (NEXT) {
             // one region: 16 key and 16 value operand reads, 24 + 24 products and 160 VALU operations (the weights
             // and their sum), dealt out as 4 VALU operations a product while the scores run and 2 after
             __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
@@ -735,24 +913,28 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows
         }
     };
     if (kb0 < kb1) {
-        floatx16 sa[2], sb[2];
+        floatx16 sa[2], sbk[2];
+        float ta = 0.0f, tb = 0.0f;
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        scores(kt[0], sa);
+        query_for(kb0);
+        ta = scores(kt[0], sa);
         // two steps an iteration, so that the score registers swap roles without copies
         for (int kb = kb0;; kb += 2) {
             if (kb + 1 >= kb1) {
-                step(Flag<false>{}, sa, sb, kb);
+                step(Flag<false>{}, sa, sbk, ta, tb, kb);
                 break;
             }
-            step(Flag<true>{}, sa, sb, kb);
+            step(Flag<true>{}, sa, sbk, ta, tb, kb);
             if (kb + 2 >= kb1) {
-                step(Flag<false>{}, sb, sa, kb + 1);
+                step(Flag<false>{}, sbk, sa, tb, ta, kb + 1);
                 break;
             }
-            step(Flag<true>{}, sb, sa, kb + 1);
+            step(Flag<true>{}, sbk, sa, tb, ta, kb + 1);
         }
     }
+    if constexpr (CODES)
+        if (kb0 < kb1) scale_sums((kb1 - 1) / kbs.bpc, 1);  // into true units: the last chunk's value scales
     l += __shfl_xor(l, 32, 64);
     if (!qlive) return;
     // accumulator v of dim block db holds coordinate 32 db + 8 (v / 4) + 4 g + v % 4
@@ -921,8 +1103,11 @@ bool kv_images_apply(int kv_format, int d, int heads) {
     return kv_format >= TAH_KV_F32 && kv_format <= TAH_KV_I8 && heads > 0 && d == 64 * heads;
 }
 
-size_t kv_images_bytes(int rows, int chunk, int heads) {
-    return ((image_bytes_of(rows, chunk, heads) + 255) / 256) * 256 + 256 + sizeof(uint32_t) * 2 * (size_t)heads;
+size_t kv_images_bytes(int rows, int chunk, int heads, int kv_format) {
+    const bool codes = kv_format == TAH_KV_I8;
+    const size_t tail =
+        codes ? (size_t)key_blocks(rows, chunk).n_chunks * heads * SCL : sizeof(uint32_t) * 2 * (size_t)heads;
+    return ((image_bytes_of(rows, chunk, heads, codes) + 255) / 256) * 256 + 256 + tail;
 }
 
 template <int FMT>
@@ -940,6 +1125,14 @@ static void launch_images(hipStream_t s, int rows, int chunk, int d, int heads, 
 void kv_images(hipStream_t s, int rows, int chunk, int d, int heads, int kv_format, const uint8_t *records,
                KvImages img) {
     if (!kv_images_apply(kv_format, d, heads)) throw ArgError{"key/value images need head width 64"};
+    if ((kv_format == TAH_KV_I8) != img.codes) throw ArgError{"key/value images: laid out for another format"};
+    if (img.codes) {
+        const KeyBlocks k = key_blocks(rows, chunk);
+        hipLaunchKernelGGL(k_kv_codes, dim3(k.n_kb, heads), dim3(256), 0, s, rows, chunk, d, heads, records,
+                           img.images, img.scales);
+        TAH_LAUNCHED();
+        return;
+    }
     switch (kv_format) {
         case TAH_KV_F32: launch_images<TAH_KV_F32>(s, rows, chunk, d, heads, records, img); break;
         case TAH_KV_I16: launch_images<TAH_KV_I16>(s, rows, chunk, d, heads, records, img); break;
@@ -947,10 +1140,13 @@ void kv_images(hipStream_t s, int rows, int chunk, int d, int heads, int kv_form
     }
 }
 
-KvImages kv_images_at(uint8_t *base, int rows, int chunk, int heads) {
+KvImages kv_images_at(uint8_t *base, int rows, int chunk, int heads, int kv_format) {
     KvImages img;
+    img.codes = kv_format == TAH_KV_I8;
     img.images = base;
-    img.kvmax = reinterpret_cast<uint32_t *>(base + ((image_bytes_of(rows, chunk, heads) + 255) / 256) * 256);
+    uint8_t *tail = base + ((image_bytes_of(rows, chunk, heads, img.codes) + 255) / 256) * 256;
+    if (img.codes) img.scales = reinterpret_cast<float *>(tail);
+    else img.kvmax = reinterpret_cast<uint32_t *>(tail);
     return img;
 }
 
@@ -982,9 +1178,14 @@ static AttnPlan plan(const AttnShape &a, bool images) {
     return p;
 }
 
+// Every caller makes a layer's tile images from TAH_SPLIT16_MIN_Q queries on where they apply (head width 64), and
+// attention() refuses such a shape without them: the plan below is the one that runs.
+static bool images_expected(const AttnShape &a) {
+    return a.nq >= TAH_SPLIT16_MIN_Q && kv_images_apply(a.kv_format, a.d, a.heads);
+}
+
 size_t attention_work_bytes(const AttnShape &a) {
-    const AttnPlan p0 = plan(a, false), p1 = plan(a, true);  // either kernel may run
-    const AttnPlan &p = p0.splits > p1.splits ? p0 : p1;
+    const AttnPlan p = plan(a, images_expected(a));
     if (p.splits == 1) return 0;
     const int hd = a.d / a.heads;
     return sizeof(float) * (size_t)p.splits * a.nq * a.heads * (hd + 2) + 256;
@@ -1069,7 +1270,9 @@ void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t 
     if (a.d % a.heads != 0 || hd > 64 || a.rows <= 0 || a.chunk <= 0)
         throw ArgError{"attention: head width must divide d and be at most 64, rows and chunk positive"};
     if ((size_t)a.nq > (size_t)65535 * 8) throw ArgError{"attention: too many queries for one launch"};
-    const AttnPlan p = plan(a, img != nullptr && img->images != nullptr);
+    const bool have = img != nullptr && img->images != nullptr;
+    if (images_expected(a) && !have) throw ArgError{"attention: head width 64 from 4 queries on needs the tile images"};
+    const AttnPlan p = plan(a, have);
     float *part_o = nullptr, *part_ml = nullptr;
     if (p.splits > 1) {
         part_o = static_cast<float *>(work);
@@ -1078,14 +1281,24 @@ void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t 
     if (p.split16) {
         hipEvent_t *pe = probe_slot(s);
         if (pe) TAH_HIP(hipEventRecord(pe[0], s));
-        if (p.waves == 8)
-            hipLaunchKernelGGL(k_attn_split64<8>, dim3(p.groups * a.heads * p.splits), dim3(512), 0, s, a.nq, a.rows,
-                               a.chunk, a.d, a.heads, q, img->images, img->kvmax, p.kb_per_split, p.groups, p.splits,
-                               part_o, part_ml, out);
+        const dim3 grid(p.groups * a.heads * p.splits);
+        if (img->codes != (a.kv_format == TAH_KV_I8)) throw ArgError{"attention: images of another cache format"};
+        if (p.waves == 8 && img->codes)
+            hipLaunchKernelGGL((k_attn_split64<8, true>), grid, dim3(512), 0, s, a.nq, a.rows, a.chunk, a.d, a.heads, q,
+                               img->images, nullptr, img->scales, p.kb_per_split, p.groups, p.splits, part_o, part_ml,
+                               out);
+        else if (p.waves == 8)
+            hipLaunchKernelGGL((k_attn_split64<8, false>), grid, dim3(512), 0, s, a.nq, a.rows, a.chunk, a.d, a.heads,
+                               q, img->images, img->kvmax, nullptr, p.kb_per_split, p.groups, p.splits, part_o, part_ml,
+                               out);
+        else if (img->codes)
+            hipLaunchKernelGGL((k_attn_split64<4, true>), grid, dim3(256), 0, s, a.nq, a.rows, a.chunk, a.d, a.heads, q,
+                               img->images, nullptr, img->scales, p.kb_per_split, p.groups, p.splits, part_o, part_ml,
+                               out);
         else
-            hipLaunchKernelGGL(k_attn_split64<4>, dim3(p.groups * a.heads * p.splits), dim3(256), 0, s, a.nq, a.rows,
-                               a.chunk, a.d, a.heads, q, img->images, img->kvmax, p.kb_per_split, p.groups, p.splits,
-                               part_o, part_ml, out);
+            hipLaunchKernelGGL((k_attn_split64<4, false>), grid, dim3(256), 0, s, a.nq, a.rows, a.chunk, a.d, a.heads,
+                               q, img->images, img->kvmax, nullptr, p.kb_per_split, p.groups, p.splits, part_o, part_ml,
+                               out);
         TAH_LAUNCHED();
         if (pe) TAH_HIP(hipEventRecord(pe[1], s));
     } else switch (a.kv_format) {

@@ -226,11 +226,13 @@ void pack(hipStream_t s, int rows, int d, int chunk, int fmt, const float *rec32
 // head's largest magnitudes: the split-fp16 attention kernel's input, built once per stored layer.
 struct KvImages {
     uint8_t *images = nullptr;
-    uint32_t *kvmax = nullptr;
+    uint32_t *kvmax = nullptr;  // f32 and i16: the heads' largest |K|, |V|
+    float *scales = nullptr;    // i8 (codes): per (chunk, head) the key then value scales
+    bool codes = false;         // i8: the images hold the codes, not split values
 };
 bool kv_images_apply(int kv_format, int d, int heads);
-size_t kv_images_bytes(int rows, int chunk, int heads);
-KvImages kv_images_at(uint8_t *base, int rows, int chunk, int heads);
+size_t kv_images_bytes(int rows, int chunk, int heads, int kv_format);
+KvImages kv_images_at(uint8_t *base, int rows, int chunk, int heads, int kv_format);
 void kv_images(hipStream_t s, int rows, int chunk, int d, int heads, int kv_format, const uint8_t *records,
                KvImages img);
 // img (optional): the layer's images, used for 32 queries or more.
