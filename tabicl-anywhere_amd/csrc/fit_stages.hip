@@ -208,36 +208,39 @@ __global__ __launch_bounds__(256) void k_ind_attn_plain(int gb, int rows, int in
     for (int c = 0; c < hd; c++) o[c] /= l;
 }
 
-// tok [rb][T][e]: class tokens then cells of rows r0.. from emb [features][rows][e].
+// tok [rb][T][e]: class tokens then cells of rows r0.. from emb [features][rows][e]. A workgroup per row, 16 bytes a
+// thread (e a multiple of 4).
 __global__ __launch_bounds__(256) void k_tokens_gmajor(int rb, int r0, int rows, int cls, int features, int e,
                                                         const float *__restrict__ cls_tokens,
                                                         const float *__restrict__ emb, float *__restrict__ tok) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int T = cls + features;
-    if (i >= (size_t)rb * T * e) return;
-    const int o = (int)(i % e);
-    const int t = (int)((i / e) % T);
-    const size_t r = i / ((size_t)e * T);
-    tok[i] = t < cls ? cls_tokens[t * e + o] : emb[((size_t)(t - cls) * rows + r0 + r) * e + o];
+    const int r = blockIdx.x;
+    if (r >= rb) return;
+    const int e4 = e / 4, T = cls + features;
+    float4 *dst = reinterpret_cast<float4 *>(tok + (size_t)r * T * e);
+    for (int i = threadIdx.x; i < T * e4; i += 256) {
+        const int t = i / e4, o = i - t * e4;
+        const float4 *src = t < cls ? reinterpret_cast<const float4 *>(cls_tokens + (size_t)t * e)
+                                    : reinterpret_cast<const float4 *>(emb + ((size_t)(t - cls) * rows + r0 + r) * e);
+        dst[i] = src[o];
+    }
 }
 
-// One cell of e floats a thread group: [rows][g][e] <-> [g][rows][e].
+// Cells of e floats between [rows][g][e] and [g][rows][e]: e / 4 threads a cell, 16 bytes each (e a multiple of 4).
 __global__ __launch_bounds__(256) void k_regroup(int rows, int g, int e, const float *__restrict__ src,
                                                   float *__restrict__ dst, bool to_gmajor) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (size_t)rows * g * e) return;
-    const int o = (int)(i % e);
-    const size_t cell = i / e;  // in the destination's order
-    size_t r, gi;
+    const int e4 = e / 4, per = 256 / e4;
+    const int slot = threadIdx.x / e4, o = threadIdx.x - slot * e4;
+    const long cell = (long)blockIdx.x * per + slot;  // in the destination's order
+    if (slot >= per || cell >= (long)rows * g) return;
+    long from;
     if (to_gmajor) {
-        gi = cell / rows;
-        r = cell % rows;
-        dst[i] = src[(r * g + gi) * e + o];
+        const long gi = cell / rows, r = cell - gi * rows;
+        from = r * g + gi;
     } else {
-        r = cell / g;
-        gi = cell % g;
-        dst[i] = src[(gi * rows + r) * e + o];
+        const long r = cell / g, gi = cell - r * g;
+        from = gi * rows + r;
     }
+    reinterpret_cast<float4 *>(dst)[cell * e4 + o] = reinterpret_cast<const float4 *>(src)[from * e4 + o];
 }
 
 void merge_splits(hipStream_t s, int nq, int d, int heads, int splits, const float *part_o, const float *part_ml,
@@ -282,15 +285,17 @@ void col_records(hipStream_t s, int gb, int inds, int e, const float *kv2, float
 }
 
 void regroup(hipStream_t s, int rows, int g, int e, const float *src, float *dst, bool to_group_major) {
-    const size_t count = (size_t)rows * g * e;
-    hipLaunchKernelGGL(k_regroup, blocks_of(count), dim3(256), 0, s, rows, g, e, src, dst, to_group_major);
+    if (e % 4 || e > 1024) throw ArgError{"regroup: cell width must be a multiple of 4, at most 1024"};
+    const size_t per = 256 / (e / 4);
+    hipLaunchKernelGGL(k_regroup, dim3((unsigned)(((size_t)rows * g + per - 1) / per)), dim3(256), 0, s, rows, g, e, src,
+                       dst, to_group_major);
     TAH_LAUNCHED();
 }
 
 void tokens_gmajor(hipStream_t s, const tah_weights *w, int rb, int r0, int rows, int features, const float *emb, float *tok) {
-    const size_t count = (size_t)rb * (w->cls + features) * w->e;
-    hipLaunchKernelGGL(k_tokens_gmajor, blocks_of(count), dim3(256), 0, s, rb, r0, rows, w->cls, features, w->e,
-                       w->cls_tokens, emb, tok);
+    if (w->e % 4) throw ArgError{"row stage: embedding width must be a multiple of 4"};
+    hipLaunchKernelGGL(k_tokens_gmajor, dim3(rb), dim3(256), 0, s, rb, r0, rows, w->cls, features, w->e, w->cls_tokens,
+                       emb, tok);
     TAH_LAUNCHED();
 }
 

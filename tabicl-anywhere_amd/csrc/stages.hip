@@ -582,27 +582,29 @@ __global__ __launch_bounds__(256) void k_row_attn_plain(int n, int T, int nq_tok
 }
 
 // ---- small copies ------------------------------------------------------------------------------------------
-// tok [n][T][e]: class tokens, then the row's cells (cells [n][features][e]).
+// tok [n][T][e]: class tokens, then the row's cells (cells [n][features][e]). A workgroup per row (grid.x rows in
+// slabs of grid.y), 16 bytes a thread: a row of tok is the class tokens then the row's cells, both contiguous.
 __global__ __launch_bounds__(256) void k_tokens(int n, int cls, int features, int e, const float *__restrict__ cls_tokens,
                                                  const float *__restrict__ cells, float *__restrict__ tok) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int T = cls + features;
-    if (i >= (size_t)n * T * e) return;
-    const int o = (int)(i % e);
-    const int t = (int)((i / e) % T);
-    const size_t r = i / ((size_t)e * T);
-    tok[i] = t < cls ? cls_tokens[t * e + o] : cells[(r * features + (t - cls)) * e + o];
+    const int r = blockIdx.x;
+    if (r >= n) return;
+    const int head4 = cls * e / 4, body4 = features * e / 4;
+    float4 *dst = reinterpret_cast<float4 *>(tok + (size_t)r * (cls + features) * e);
+    const float4 *ct = reinterpret_cast<const float4 *>(cls_tokens);
+    const float4 *src = reinterpret_cast<const float4 *>(cells + (size_t)r * features * e);
+    for (int i = threadIdx.x; i < head4; i += 256) dst[i] = ct[i];
+    for (int i = threadIdx.x; i < body4; i += 256) dst[head4 + i] = src[i];
 }
 
-// dst [n][k][e] = the first k tokens of each row of src [n][T][e].
+// dst [n][k][e] = the first k tokens of each row of src [n][T][e]: a workgroup per row, 16 bytes a thread.
 __global__ __launch_bounds__(256) void k_first_tokens(int n, int T, int k, int e, const float *__restrict__ src,
                                                        float *__restrict__ dst) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (size_t)n * k * e) return;
-    const int o = (int)(i % e);
-    const int t = (int)((i / e) % k);
-    const size_t r = i / ((size_t)e * k);
-    dst[i] = src[(r * T + t) * e + o];
+    const int r = blockIdx.x;
+    if (r >= n) return;
+    const int c4 = k * e / 4;
+    const float4 *s4 = reinterpret_cast<const float4 *>(src + (size_t)r * T * e);
+    float4 *d4 = reinterpret_cast<float4 *>(dst + (size_t)r * k * e);
+    for (int i = threadIdx.x; i < c4; i += 256) d4[i] = s4[i];
 }
 
 __global__ __launch_bounds__(256) void k_accumulate(size_t count, const float *__restrict__ x, float *__restrict__ sum) {
@@ -814,7 +816,7 @@ void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, co
             // the last block: only the class tokens are queried and updated
             const int M = n * cls;
             attend(cls, ac);
-            hipLaunchKernelGGL(k_first_tokens, blocks_for((size_t)M * e), dim3(256), 0, s, n, T, cls, e, tok, xc);
+            hipLaunchKernelGGL(k_first_tokens, dim3(n), dim3(256), 0, s, n, T, cls, e, tok, xc);
             TAH_LAUNCHED();
             out_projection(s, M, ac, b, xc);
             feed_forward(s, M, xc, b, t, mid);
@@ -824,8 +826,8 @@ void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, co
 }
 
 void assemble_tokens(hipStream_t s, const tah_weights *w, const float *cells, int n, int features, float *tok) {
-    const size_t count = (size_t)n * (w->cls + features) * w->e;
-    hipLaunchKernelGGL(k_tokens, blocks_for(count), dim3(256), 0, s, n, w->cls, features, w->e, w->cls_tokens, cells, tok);
+    if (w->e % 4) throw ArgError{"row stage: embedding width must be a multiple of 4"};
+    hipLaunchKernelGGL(k_tokens, dim3(n), dim3(256), 0, s, n, w->cls, features, w->e, w->cls_tokens, cells, tok);
     TAH_LAUNCHED();
 }
 
