@@ -40,35 +40,25 @@ __device__ __forceinline__ void dma_to_lds(const uint8_t *src, uint8_t *dst, int
 
 constexpr int FFW = 4;  // wavefronts (of 32 rows each) per k_ff128 workgroup (eight, one workgroup a CU, measured slower)
 
-// grid ceil(M / (32 FFW)); 64 FFW threads. x [M][128] in place.
-__global__ __launch_bounds__(64 * FFW, 2) void k_ff128(int M, float *__restrict__ x, const float *__restrict__ lnw,
-                                                   const float *__restrict__ lnb, const uint8_t *__restrict__ w1img,
-                                                   const float *__restrict__ b1, int s1,
-                                                   const uint8_t *__restrict__ w2img, const float *__restrict__ b2,
-                                                   int s2) {
-    constexpr int E = 128;
-    __shared__ __align__(16) uint8_t slab[2][SLAB];
-    __shared__ __align__(16) float bias1[256];  // b1, read next to the GELU it feeds (an LDS read's short wait)
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int r32 = lane & 31, g = lane >> 5;
-    const int m = blockIdx.x * 32 * FFW + wave * 32 + r32;
-    const bool live = m < M;
-    dma_to_lds<64 * FFW>(w1img, slab[0], SLAB, tid);
+// The feed-forward body's start, by all 256 threads of a workgroup: the first weight slice's copy into slab (two
+// slices, 64 KB of LDS) and the first layer's bias into bias1 (256 floats of LDS).
+__device__ __forceinline__ void ff128_start(uint8_t *slab, float *bias1, const uint8_t *__restrict__ w1img,
+                                            const float *__restrict__ b1, int tid) {
+    dma_to_lds<64 * FFW>(w1img, slab, SLAB, tid);
     if (tid < 64) reinterpret_cast<float4 *>(bias1)[tid] = reinterpret_cast<const float4 *>(b1)[tid];
+}
 
-    // this lane's half of row m: columns 16 ks + 8 g + t
-    float xv[8][8];
-#pragma unroll
-    for (int ks = 0; ks < 8; ks++) {
-        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), b = a;
-        if (live) {
-            const float *src = x + (size_t)m * E + 16 * ks + 8 * g;
-            a = *reinterpret_cast<const float4 *>(src);
-            b = *reinterpret_cast<const float4 *>(src + 4);
-        }
-        xv[ks][0] = a.x; xv[ks][1] = a.y; xv[ks][2] = a.z; xv[ks][3] = a.w;
-        xv[ks][4] = b.x; xv[ks][5] = b.y; xv[ks][6] = b.z; xv[ks][7] = b.w;
-    }
+// x += l2(gelu(l1(norm2 x))) + b2 for 32 rows a wavefront (after ff128_start, all 256 threads): xv holds this lane's
+// half of its row (columns 16 ks + 8 g + t); xrow is the row's storage, which holds x (read back for the residual
+// add) and takes the result (not where !live).
+__device__ __forceinline__ void ff128_rows(float (&xv)[8][8], bool live, float *xrow, uint8_t *slab, const float *bias1,
+                                           const float *__restrict__ lnw, const float *__restrict__ lnb,
+                                           const uint8_t *__restrict__ w1img, int s1,
+                                           const uint8_t *__restrict__ w2img, const float *__restrict__ b2, int s2,
+                                           int tid) {
+    constexpr int E = 128;
+    const int lane = tid & 63;
+    const int r32 = lane & 31, g = lane >> 5;
     // layer normalisation (two passes, biased variance, eps 1e-5)
     float sum = 0.0f;
 #pragma unroll
@@ -122,8 +112,8 @@ __global__ __launch_bounds__(64 * FFW, 2) void k_ff128(int M, float *__restrict_
     auto next = [&](int j) {
         __builtin_amdgcn_s_waitcnt(0);  // this wavefront's copies of slice j have landed
         __syncthreads();                // everyone's have; slice j - 1's buffer is free
-        if (j + 1 < 4 * NSL) dma_to_lds<64 * FFW>(slice(j + 1), slab[(j + 1) & 1], SLAB, tid);
-        return static_cast<const uint8_t *>(slab[j & 1]);
+        if (j + 1 < 4 * NSL) dma_to_lds<64 * FFW>(slice(j + 1), slab + ((j + 1) & 1) * SLAB, SLAB, tid);
+        return static_cast<const uint8_t *>(slab + (j & 1) * SLAB);
     };
     // acc[T] += (rows 32 T .. 32 T + 31 of the slice's weights) B over the slice's CPS 16-column steps
     auto mma = [&](floatx16 (&acc)[4], const uint8_t *sl, const halfx8 *bh, const halfx8 *bl, int rows) {
@@ -216,7 +206,7 @@ __global__ __launch_bounds__(64 * FFW, 2) void k_ff128(int M, float *__restrict_
 #pragma unroll
         for (int hh = 0; hh < 2; hh++) {
             const int c0 = 32 * T + 16 * hh + 8 * g;
-            float *dst = x + (size_t)m * E + c0;
+            float *dst = xrow + c0;
             const float4 ra = *reinterpret_cast<const float4 *>(dst), rb = *reinterpret_cast<const float4 *>(dst + 4);
             const float4 ba = *reinterpret_cast<const float4 *>(b2 + c0), bb = *reinterpret_cast<const float4 *>(b2 + c0 + 4);
             float yv[8];
@@ -227,6 +217,37 @@ __global__ __launch_bounds__(64 * FFW, 2) void k_ff128(int M, float *__restrict_
             *reinterpret_cast<float4 *>(dst + 4) = make_float4(yv[4] * u2 + bb.x + rb.x, yv[5] * u2 + bb.y + rb.y,
                                                                yv[6] * u2 + bb.z + rb.z, yv[7] * u2 + bb.w + rb.w);
         }
+}
+
+// grid ceil(M / (32 FFW)); 64 FFW threads. x [M][128] in place.
+__global__ __launch_bounds__(64 * FFW, 2) void k_ff128(int M, float *__restrict__ x, const float *__restrict__ lnw,
+                                                   const float *__restrict__ lnb, const uint8_t *__restrict__ w1img,
+                                                   const float *__restrict__ b1, int s1,
+                                                   const uint8_t *__restrict__ w2img, const float *__restrict__ b2,
+                                                   int s2) {
+    constexpr int E = 128;
+    __shared__ __align__(16) uint8_t slab[2 * SLAB];
+    __shared__ __align__(16) float bias1[256];  // b1, read next to the GELU it feeds (an LDS read's short wait)
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r32 = lane & 31, g = lane >> 5;
+    const int m = blockIdx.x * 32 * FFW + wave * 32 + r32;
+    const bool live = m < M;
+    ff128_start(slab, bias1, w1img, b1, tid);
+
+    // this lane's half of row m: columns 16 ks + 8 g + t
+    float xv[8][8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) {
+        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), b = a;
+        if (live) {
+            const float *src = x + (size_t)m * E + 16 * ks + 8 * g;
+            a = *reinterpret_cast<const float4 *>(src);
+            b = *reinterpret_cast<const float4 *>(src + 4);
+        }
+        xv[ks][0] = a.x; xv[ks][1] = a.y; xv[ks][2] = a.z; xv[ks][3] = a.w;
+        xv[ks][4] = b.x; xv[ks][5] = b.y; xv[ks][6] = b.z; xv[ks][7] = b.w;
+    }
+    ff128_rows(xv, live, x + (size_t)(live ? m : 0) * E, slab, bias1, lnw, lnb, w1img, s1, w2img, b2, s2, tid);
 }
 
 void ff_block(hipStream_t s, int M, float *x, const DevBlock &b) {
@@ -443,15 +464,22 @@ __global__ __launch_bounds__(256) void k_cell_images(const float *__restrict__ k
 //    in (global_load_lds) while the current one is used: one barrier per head.
 // The output projection's input is scaled by one power of two for all heads, lowered (and the sums rescaled) when a
 // head's values are larger than all before: every head's output is at most its values' largest magnitude.
+// With FF the block's feed-forward half follows in the same kernel (ff128_rows, its weight slices in the same 64 KB
+// of LDS): the cells' new values stay in registers as its input; they are written out as well, for its residual add.
+template <bool FF>
 __global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t sg, float *cells,
                                                         const float *__restrict__ n1w, const float *__restrict__ n1b,
                                                         const uint8_t *__restrict__ qimg, int qshift,
                                                         const float *__restrict__ qb, const float *__restrict__ qscale,
                                                         const uint8_t *__restrict__ images, const int *__restrict__ shifts,
                                                         const uint8_t *__restrict__ oimg, int oshift,
-                                                        const float *__restrict__ ob) {
+                                                        const float *__restrict__ ob, const float *__restrict__ n2w, const float *__restrict__ n2b,
+                                                        const uint8_t *__restrict__ w1img, const float *__restrict__ b1,
+                                                        int s1, const uint8_t *__restrict__ w2img,
+                                                        const float *__restrict__ b2, int s2) {
     constexpr int E = 128;
     __shared__ __align__(16) uint8_t lds[65536];
+    __shared__ __align__(16) float ffb[FF ? 256 : 4];  // FF: the first feed-forward layer's bias
     __shared__ __align__(16) uint8_t zero[16], ones[16];  // eight fp16 zeros, eight fp16 ones
     __shared__ __align__(16) float qbs[2][128];  // the query bias and scale
     uint8_t *const wo = lds;           // output projection steps, four slots of 8 KB
@@ -672,10 +700,11 @@ __global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t 
             acc[T] = mfma16x3(ah, al, oh, ol, acc[T]);
         }
     }
-    if (!live) return;
+    if (!FF && !live) return;
     // column of accumulator v of tile T: 32 T + 16 (v / 8) + 8 g + v % 8
     const float u = ldexpf(1.0f, -(so + oshift));
     float *xrow = cells + m * E;
+    float xn[8][8];  // the new values as the feed-forward's input: columns 16 ks + 8 g + t
 #pragma unroll
     for (int T = 0; T < 4; T++)
 #pragma unroll
@@ -684,18 +713,20 @@ __global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t 
             float bv[8], xr[8];
             load8(ob + n0, bv);
             load8(xrow + n0, xr);
-            float4 y0, y1;
-            y0.x = xr[0] + acc[T][8 * hh + 0] * u + bv[0];
-            y0.y = xr[1] + acc[T][8 * hh + 1] * u + bv[1];
-            y0.z = xr[2] + acc[T][8 * hh + 2] * u + bv[2];
-            y0.w = xr[3] + acc[T][8 * hh + 3] * u + bv[3];
-            y1.x = xr[4] + acc[T][8 * hh + 4] * u + bv[4];
-            y1.y = xr[5] + acc[T][8 * hh + 5] * u + bv[5];
-            y1.z = xr[6] + acc[T][8 * hh + 6] * u + bv[6];
-            y1.w = xr[7] + acc[T][8 * hh + 7] * u + bv[7];
-            *reinterpret_cast<float4 *>(xrow + n0) = y0;
-            *reinterpret_cast<float4 *>(xrow + n0 + 4) = y1;
+#pragma unroll
+            for (int t = 0; t < 8; t++) xn[2 * T + hh][t] = xr[t] + acc[T][8 * hh + t] * u + bv[t];
+            if (live) {
+                *reinterpret_cast<float4 *>(xrow + n0) = make_float4(xn[2 * T + hh][0], xn[2 * T + hh][1],
+                                                                     xn[2 * T + hh][2], xn[2 * T + hh][3]);
+                *reinterpret_cast<float4 *>(xrow + n0 + 4) = make_float4(xn[2 * T + hh][4], xn[2 * T + hh][5],
+                                                                         xn[2 * T + hh][6], xn[2 * T + hh][7]);
+            }
         }
+    if constexpr (FF) {
+        __syncthreads();  // every wavefront is done with the attention's LDS (no copy is in flight after head 7)
+        ff128_start(lds, ffb, w1img, b1, tid);
+        ff128_rows(xn, live, xrow, lds, ffb, n2w, n2b, w1img, s1, w2img, b2, s2, tid);
+    }
 }
 
 // ---- fused row block, attention half ------------------------------------------------------------------------------
@@ -710,14 +741,20 @@ __global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t 
 //    head's power of two (one wavefront-pair's maximum each, across wavefronts through LDS): threads 0..127 a key
 //    each, threads 128..255 a value each, for the next head while the current one is attended (two barriers a head);
 //  * keys past T are masked; the attention and the output projection then run as in k_cell_block.
+// With FF the block's feed-forward half follows in the same kernel, as in k_cell_block.
+template <bool FF>
 __global__ __launch_bounds__(256, 2) void k_row_block(int T, float *tok, const float *__restrict__ kv,
                                                        const float *__restrict__ cosv, const float *__restrict__ sinv,
                                                        const float *__restrict__ n1w, const float *__restrict__ n1b,
                                                        const uint8_t *__restrict__ qimg, int qshift,
                                                        const float *__restrict__ qb, const uint8_t *__restrict__ oimg,
-                                                       int oshift, const float *__restrict__ ob) {
+                                                       int oshift, const float *__restrict__ ob, const float *__restrict__ n2w, const float *__restrict__ n2b,
+                                                       const uint8_t *__restrict__ w1img, const float *__restrict__ b1,
+                                                       int s1, const uint8_t *__restrict__ w2img,
+                                                       const float *__restrict__ b2, int s2) {
     constexpr int E = 128;
     __shared__ __align__(16) uint8_t lds[65536];
+    __shared__ __align__(16) float ffb[FF ? 256 : 4];  // FF: the first feed-forward layer's bias
     __shared__ __align__(16) uint8_t zero[16], ones[16];
     __shared__ __align__(16) float qbs[128];
     __shared__ __align__(16) float cst[2][128][8];  // cos, sin of token t, pair k
@@ -1021,8 +1058,9 @@ __global__ __launch_bounds__(256, 2) void k_row_block(int T, float *tok, const f
             qa[2] = qa[3];
         }
     }
-    if (!live) return;
+    if (!FF && !live) return;
     const float u = ldexpf(1.0f, -(so + oshift));
+    float xn[8][8];  // the new values as the feed-forward's input: columns 16 ks + 8 g + t
 #pragma unroll
     for (int T4 = 0; T4 < 4; T4++)
 #pragma unroll
@@ -1031,31 +1069,42 @@ __global__ __launch_bounds__(256, 2) void k_row_block(int T, float *tok, const f
             float bv[8], xr[8];
             load8(ob + n0, bv);
             load8(xrow + n0, xr);
-            float4 y0, y1;
-            y0.x = xr[0] + acc[T4][8 * hh + 0] * u + bv[0];
-            y0.y = xr[1] + acc[T4][8 * hh + 1] * u + bv[1];
-            y0.z = xr[2] + acc[T4][8 * hh + 2] * u + bv[2];
-            y0.w = xr[3] + acc[T4][8 * hh + 3] * u + bv[3];
-            y1.x = xr[4] + acc[T4][8 * hh + 4] * u + bv[4];
-            y1.y = xr[5] + acc[T4][8 * hh + 5] * u + bv[5];
-            y1.z = xr[6] + acc[T4][8 * hh + 6] * u + bv[6];
-            y1.w = xr[7] + acc[T4][8 * hh + 7] * u + bv[7];
-            *reinterpret_cast<float4 *>(xrow + n0) = y0;
-            *reinterpret_cast<float4 *>(xrow + n0 + 4) = y1;
+#pragma unroll
+            for (int t = 0; t < 8; t++) xn[2 * T4 + hh][t] = xr[t] + acc[T4][8 * hh + t] * u + bv[t];
+            if (live) {
+                *reinterpret_cast<float4 *>(xrow + n0) = make_float4(xn[2 * T4 + hh][0], xn[2 * T4 + hh][1],
+                                                                     xn[2 * T4 + hh][2], xn[2 * T4 + hh][3]);
+                *reinterpret_cast<float4 *>(xrow + n0 + 4) = make_float4(xn[2 * T4 + hh][4], xn[2 * T4 + hh][5],
+                                                                         xn[2 * T4 + hh][6], xn[2 * T4 + hh][7]);
+            }
         }
+    if constexpr (FF) {
+        __syncthreads();  // every wavefront is done with the attention's LDS (no copy is in flight after head 7)
+        ff128_start(lds, ffb, w1img, b1, tid);
+        ff128_rows(xn, live, xrow, lds, ffb, n2w, n2b, w1img, s1, w2img, b2, s2, tid);
+    }
 }
 
 bool row_block_fits(const DevBlock &b, int T) {
     return b.d == 128 && b.heads == 8 && b.inimg && b.outimg && T >= 1 && T <= 128;
 }
 
+bool block_ff_fits(const DevBlock &b) { return ff_fused_shape(b.d, b.ff) && b.l1img && b.l2img; }
+
 void row_block(hipStream_t s, int n, int T, float *tok, const float *kv, const float *cosv, const float *sinv,
-               const DevBlock &b) {
+               const DevBlock &b, bool ff) {
     if (n <= 0) return;
     if (!row_block_fits(b, T) || (reinterpret_cast<uintptr_t>(tok) & 15) || (reinterpret_cast<uintptr_t>(kv) & 15))
         throw ArgError{"row_block: needs e = 128, 8 heads, weight images, at most 128 tokens and aligned rows"};
-    hipLaunchKernelGGL(k_row_block, dim3(n), dim3(256), 0, s, T, tok, kv, cosv, sinv, b.n1w, b.n1b, b.inimg, b.ins,
-                       b.in_b, b.outimg, b.outs, b.out_b);
+    if (ff && !block_ff_fits(b)) throw ArgError{"row_block: no fused feed-forward weights for this shape"};
+    if (ff)
+        hipLaunchKernelGGL(k_row_block<true>, dim3(n), dim3(256), 0, s, T, tok, kv, cosv, sinv, b.n1w, b.n1b, b.inimg,
+                           b.ins, b.in_b, b.outimg, b.outs, b.out_b, b.n2w, b.n2b, b.l1img, b.l1b, b.l1s, b.l2img,
+                           b.l2b, b.l2s);
+    else
+        hipLaunchKernelGGL(k_row_block<false>, dim3(n), dim3(256), 0, s, T, tok, kv, cosv, sinv, b.n1w, b.n1b, b.inimg,
+                           b.ins, b.in_b, b.outimg, b.outs, b.out_b, nullptr, nullptr, nullptr, nullptr, 0, nullptr,
+                           nullptr, 0);
     TAH_LAUNCHED();
 }
 
@@ -1066,16 +1115,23 @@ bool cell_block_fits(const DevBlock &b) {
 size_t cell_block_work_bytes(int groups) { return (size_t)groups * 8 * (CIMG + 2 * sizeof(int)); }
 
 void cell_block(hipStream_t s, int n, int groups, size_t sr, size_t sg, float *cells, const DevBlock &b,
-                const float *qscale, const float *kvbase, size_t gstride, void *work) {
+                const float *qscale, const float *kvbase, size_t gstride, void *work, bool ff) {
     if (n <= 0 || groups <= 0) return;
     if (!cell_block_fits(b) || (reinterpret_cast<uintptr_t>(cells) & 15) || (reinterpret_cast<uintptr_t>(work) & 15))
         throw ArgError{"cell_block: needs e = 128, 8 heads, weight images and 16-byte aligned cells and work"};
+    if (ff && !block_ff_fits(b)) throw ArgError{"cell_block: no fused feed-forward weights for this shape"};
     uint8_t *images = static_cast<uint8_t *>(work);
     int *shifts = reinterpret_cast<int *>(images + (size_t)groups * 8 * CIMG);
     hipLaunchKernelGGL(k_cell_images, dim3(groups, 8), dim3(256), 0, s, kvbase, gstride, images, shifts);
     TAH_LAUNCHED();
-    hipLaunchKernelGGL(k_cell_block, dim3((n + 127) / 128, groups), dim3(256), 0, s, n, sr, sg, cells, b.n1w, b.n1b,
-                       b.inimg, b.ins, b.in_b, qscale, images, shifts, b.outimg, b.outs, b.out_b);
+    if (ff)
+        hipLaunchKernelGGL(k_cell_block<true>, dim3((n + 127) / 128, groups), dim3(256), 0, s, n, sr, sg, cells, b.n1w,
+                           b.n1b, b.inimg, b.ins, b.in_b, qscale, images, shifts, b.outimg, b.outs, b.out_b, b.n2w,
+                           b.n2b, b.l1img, b.l1b, b.l1s, b.l2img, b.l2b, b.l2s);
+    else
+        hipLaunchKernelGGL(k_cell_block<false>, dim3((n + 127) / 128, groups), dim3(256), 0, s, n, sr, sg, cells, b.n1w,
+                           b.n1b, b.inimg, b.ins, b.in_b, qscale, images, shifts, b.outimg, b.outs, b.out_b, nullptr,
+                           nullptr, nullptr, nullptr, 0, nullptr, nullptr, 0);
     TAH_LAUNCHED();
 }
 

@@ -193,12 +193,14 @@ void ff_block(hipStream_t s, int M, float *x, const DevBlock &b);
 bool cell_block_fits(const DevBlock &b);
 // The attention half of a row block for every token of n rows of T tokens (tok [n][T][e] in place), from the keys
 // and values kv [n][T][2 e] the projection made (unrotated); e = 128, 8 heads of 16, T <= 128 (row_block_fits).
+// With ff (block_ff_fits) either kernel runs the block's feed-forward half as well, in the same launch.
 bool row_block_fits(const DevBlock &b, int T);
+bool block_ff_fits(const DevBlock &b);
 void row_block(hipStream_t s, int n, int T, float *tok, const float *kv, const float *cosv, const float *sinv,
-               const DevBlock &b);
+               const DevBlock &b, bool ff);
 size_t cell_block_work_bytes(int groups);
 void cell_block(hipStream_t s, int n, int groups, size_t sr, size_t sg, float *cells, const DevBlock &b,
-                const float *qscale, const float *kvbase, size_t gstride, void *work);
+                const float *qscale, const float *kvbase, size_t gstride, void *work, bool ff);
 // Y [M][N] = epi(X' W^T + b) for K = 128 and N a multiple of 128, W as such an image (scaled by 2^shift), X' = X or
 // layer_norm(X) with lnw/lnb; EPI_NONE, EPI_SCALE (by scale [N]) or EPI_RESID (adds R, may alias Y).
 void rows128(hipStream_t s, int M, int N, const float *X, int ldx, const uint8_t *wimg, int wshift, const float *b,

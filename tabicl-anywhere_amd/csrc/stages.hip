@@ -676,9 +676,11 @@ void column_block(hipStream_t s, const tah_weights *w, const DevBlock &b, float 
     const int e = w->e;
     const int M = n * groups;
     if (cell_block_fits(b) && w->inds == 128 && cell_block_work_bytes(groups) <= att_bytes) {
-        // the attention half in one kernel; the query and attention buffers are not needed, att holds the images
-        cell_block(s, n, groups, sr, sg, cells, b, w->col_scale, kvbase, gstride, att);
-        feed_forward(s, M, cells, b, t, mid);
+        // the attention half in one kernel, and the feed-forward half in it too where the fused kernel takes the
+        // shape; the query and attention buffers are not needed, att holds the images
+        const bool ff = block_ff_fits(b) && M > SMALL_ROWS;
+        cell_block(s, n, groups, sr, sg, cells, b, w->col_scale, kvbase, gstride, att, ff);
+        if (!ff) feed_forward(s, M, cells, b, t, mid);
         return;
     }
     if (b.inimg && b.ss_hidden == 0 && M > SMALL_ROWS) {
@@ -787,11 +789,13 @@ void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, co
         const DevBlock &b = w->row[bi];
         if (bi < last && fused && row_block_fits(b, T) && n >= ROW_BLOCK_MIN) {
             // keys and values by the projection (its second and third 128-row blocks), then the attention half of
-            // the block in one kernel; qkv holds [R][2 e]
+            // the block in one kernel (and the feed-forward half in it too where the fused kernel takes the shape);
+            // qkv holds [R][2 e]
             rows128(s, (int)R, 2 * e, tok, e, b.inimg + (size_t)128 * e * 4, b.ins, b.in_b + e, qkv, 2 * e, EPI_NONE,
                     nullptr, 0, nullptr, b.n1w, b.n1b);
-            row_block(s, n, T, tok, qkv, cosv, sinv, b);
-            feed_forward(s, (int)R, tok, b, t, mid);
+            const bool ff = block_ff_fits(b) && R > SMALL_ROWS;
+            row_block(s, n, T, tok, qkv, cosv, sinv, b, ff);
+            if (!ff) feed_forward(s, (int)R, tok, b, t, mid);
             continue;
         }
         if (b.inimg && R > SMALL_ROWS) {
