@@ -384,13 +384,21 @@ __global__ __launch_bounds__(256) void k_row_attn16(int n, int T, int nq_tok, in
 // with one cross-lane exchange and multiplied by 1 / sqrt(16)): S^T = K Q^T for four 32-key tiles (K in sigma32
 // order), a plain softmax over the row's tokens (weights at most 2^12), and O^T = V^T P^T with the weights straight
 // from the accumulators as the B operand; V^T fills 16 of the 32 A-operand rows (the rest are zeros).
-__global__ __launch_bounds__(256) void k_row_attn_x3(int n, int T, int nq_tok, int e, const float *__restrict__ qkv,
+// One dimension of n x heads workgroups: consecutive workgroups go to the eight XCDs in turn, and workgroup i takes
+// (row, head) number (i % 8) G / 8 + i / 8, heads fastest: an XCD runs a row's heads together, so its L2 reads the
+// row's keys and values once. Query token t of row r at q + r * q_row + t * q_tok (the projection's [T][3 e]
+// layout, or the class tokens' own [cls][e]).
+__global__ __launch_bounds__(256) void k_row_attn_x3(int n, int T, int nq_tok, int e, int heads,
+                                                      const float *__restrict__ qkv,
+                                                      const float *__restrict__ q, size_t q_row, int q_tok,
                                                       const float *__restrict__ cosv, const float *__restrict__ sinv,
                                                       float *__restrict__ out) {
     __shared__ __align__(16) _Float16 Kh[2][128][8], Kl[2][128][8];
     __shared__ __align__(16) _Float16 Vh[8][2][16][8], Vl[8][2][16][8];
     __shared__ float red[2][4];
-    const int r = blockIdx.x, h = blockIdx.y;
+    const int G = gridDim.x;
+    const int item = G % 8 == 0 ? (blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+    const int r = item / heads, h = item - r * heads;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *base = qkv + (size_t)r * T * 3 * e;
     // keys and values, one token a thread
@@ -463,7 +471,7 @@ __global__ __launch_bounds__(256) void k_row_attn_x3(int n, int T, int nq_tok, i
     {
         float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), b = a;
         if (live) {
-            const float *qp = base + (size_t)qt * 3 * e + h * 16 + 8 * g;
+            const float *qp = q + (size_t)r * q_row + (size_t)qt * q_tok + h * 16 + 8 * g;
             a = *reinterpret_cast<const float4 *>(qp);
             b = *reinterpret_cast<const float4 *>(qp + 4);
         }
@@ -639,6 +647,7 @@ constexpr int SMALL_ROWS = 128;
 // projections, the attention (a workgroup per row and head) and the output projection separately (measured: one
 // row 0.84 -> 0.76 ms a prediction, 64 rows 1.43 -> 1.40 ms).
 constexpr int ROW_BLOCK_MIN = 128;
+constexpr int CLS_QUERIES_MIN = 512;
 
 // x [M][e] += l2(gelu(l1(norm2 x))): the fused kernel where the block's shape has one (above SMALL_ROWS rows), else
 // two GEMMs with the norm folded into the first where it fits, else layer_norm and two GEMMs (t [M][e] and mid [M][ff]
@@ -773,9 +782,14 @@ void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, co
     const int last = w->row_blocks - 1;
     const bool mfma = hd == 16 && T <= 256;
     const bool fused = hd == 16 && half == 8 && T <= 128;  // rotary positions applied inside k_row_attn_x3
+    // the queries k_row_attn_x3 reads: the projection's [T][3 e] rows, or (the last block) the class tokens' [cls][e]
+    const float *q_of = qkv;
+    size_t q_row = (size_t)T * 3 * e;
+    int q_tok = 3 * e;
     auto attend = [&](int nq_tok, float *dst) {
         if (fused)
-            hipLaunchKernelGGL(k_row_attn_x3, dim3(n, heads), dim3(256), 0, s, n, T, nq_tok, e, qkv, cosv, sinv, dst);
+            hipLaunchKernelGGL(k_row_attn_x3, dim3(n * heads), dim3(256), 0, s, n, T, nq_tok, e, heads, qkv, q_of,
+                               q_row, q_tok, cosv, sinv, dst);
         else if (mfma && T <= 128)
             hipLaunchKernelGGL(k_row_attn16<8>, dim3(n, heads), dim3(256), 0, s, n, T, nq_tok, e, qkv, dst);
         else if (mfma)
@@ -796,6 +810,26 @@ void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, co
             const bool ff = block_ff_fits(b) && R > SMALL_ROWS;
             row_block(s, n, T, tok, qkv, cosv, sinv, b, ff);
             if (!ff) feed_forward(s, (int)R, tok, b, t, mid);
+            continue;
+        }
+        if (bi == last && fused && b.inimg && n >= CLS_QUERIES_MIN) {
+            // the last block queries only the class tokens: keys and values for every token (the projection's second
+            // and third 128-row blocks, into qkv's [T][3 e] rows), queries for the class tokens alone, from their
+            // gathered copy (which the block then updates); below CLS_QUERIES_MIN rows the extra launch costs more
+            // than the other tokens' queries (2,048 rows 4.30 -> 4.25 ms, 64 and 256 rows 5 us slower)
+            rows128(s, (int)R, 2 * e, tok, e, b.inimg + (size_t)128 * e * 4, b.ins, b.in_b + e, qkv + e, 3 * e, EPI_NONE,
+                    nullptr, 0, nullptr, b.n1w, b.n1b);
+            const int M = n * cls;
+            hipLaunchKernelGGL(k_first_tokens, dim3(n), dim3(256), 0, s, n, T, cls, e, tok, xc);
+            TAH_LAUNCHED();
+            rows128(s, M, e, xc, e, b.inimg, b.ins, b.in_b, ac, e, EPI_NONE, nullptr, 0, nullptr, b.n1w, b.n1b);
+            q_of = ac;
+            q_row = (size_t)cls * e;
+            q_tok = e;
+            attend(cls, att);
+            out_projection(s, M, att, b, xc);
+            feed_forward(s, M, xc, b, t, mid);
+            layer_norm(s, M, e, xc, e, w->out_lnw, w->out_lnb, rep, e);
             continue;
         }
         if (b.inimg && R > SMALL_ROWS) {
