@@ -374,6 +374,100 @@ __global__ __launch_bounds__(256) void k_row_attn16(int n, int T, int nq_tok, in
     }
 }
 
+// ---- the class tokens' attention within each row: head width 16, at most 4 queries, T <= 128 ----------------------
+// grid n rows; 64 x heads threads (at most 8 heads), wavefront h head h. Few queries against at most 128 keys: plain f32 arithmetic,
+// each row's keys and values read once by its workgroup (the heads' slices of a token side by side). Lane l takes
+// tokens l and l + 64: their keys (rotated, the k_rope formula) and values, the scores of the (rotated, 1 / sqrt(16))
+// queries, the softmax over the row's tokens by wavefront reductions; the weights and values then go through LDS,
+// and lane c = 16 i + j forms coordinate j of query i's output. Keys of token t of row r at kv + r * kv_row +
+// t * kv_tok (values e floats further), query i at q + r * q_row + i * q_tok.
+constexpr int CLS_MAXQ = 4;
+__global__ __launch_bounds__(512) void k_cls_attn(int n, int T, int nq, int e, const float *__restrict__ kv,
+                                                   size_t kv_row, int kv_tok, const float *__restrict__ q, size_t q_row,
+                                                   int q_tok, const float *__restrict__ cosv,
+                                                   const float *__restrict__ sinv, float *__restrict__ out) {
+    __shared__ float ps[8][CLS_MAXQ][128];            // [head][query][token] weights
+    __shared__ __align__(16) float vs[8][128][16];    // [head][token][coordinate] values
+    const int r = blockIdx.x, h = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const float *kr = kv + (size_t)r * kv_row + h * 16;
+    float k2[2][16];
+    bool tl[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int t = lane + 64 * j;
+        tl[j] = t < T;
+        const float *kp = kr + (size_t)(tl[j] ? t : 0) * kv_tok;
+        float v16[16];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 a = *reinterpret_cast<const float4 *>(kp + 4 * i);
+            const float4 b = *reinterpret_cast<const float4 *>(kp + e + 4 * i);
+            k2[j][4 * i] = a.x; k2[j][4 * i + 1] = a.y; k2[j][4 * i + 2] = a.z; k2[j][4 * i + 3] = a.w;
+            v16[4 * i] = b.x; v16[4 * i + 1] = b.y; v16[4 * i + 2] = b.z; v16[4 * i + 3] = b.w;
+        }
+        float cs[8], sn[8];
+        load8(cosv + (tl[j] ? t : 0) * 8, cs);
+        load8(sinv + (tl[j] ? t : 0) * 8, sn);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float a = k2[j][k], b = k2[j][k + 8];
+            k2[j][k] = a * cs[k] - b * sn[k];
+            k2[j][k + 8] = b * cs[k] + a * sn[k];
+        }
+        if (tl[j]) {
+#pragma unroll
+            for (int c = 0; c < 16; c += 4)
+                *reinterpret_cast<float4 *>(&vs[h][t][c]) = make_float4(v16[c], v16[c + 1], v16[c + 2], v16[c + 3]);
+        }
+    }
+    float lsum[CLS_MAXQ];
+#pragma unroll
+    for (int i = 0; i < CLS_MAXQ; i++) {
+        if (i >= nq) break;
+        // query i of head h, rotated at position i and scaled by 1 / sqrt(16) (every lane reads the same 64 bytes)
+        float qv[16];
+        load8(q + (size_t)r * q_row + (size_t)i * q_tok + h * 16, qv);
+        load8(q + (size_t)r * q_row + (size_t)i * q_tok + h * 16 + 8, qv + 8);
+        float cs[8], sn[8];
+        load8(cosv + i * 8, cs);
+        load8(sinv + i * 8, sn);
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float a = qv[k], b = qv[k + 8];
+            qv[k] = (a * cs[k] - b * sn[k]) * 0.25f;
+            qv[k + 8] = (b * cs[k] + a * sn[k]) * 0.25f;
+        }
+        float sc[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            float a = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 16; c++) a += qv[c] * k2[j][c];
+            sc[j] = tl[j] ? a : -INFINITY;
+        }
+        const float mx = wave_max(fmaxf(sc[0], sc[1]));
+        float l = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const float pj = tl[j] ? exp2_hw((sc[j] - mx) * LOG2E) : 0.0f;
+            ps[h][i][lane + 64 * j] = pj;
+            l += pj;
+        }
+        lsum[i] = wave_sum(l);
+    }
+    __syncthreads();
+    // lane 16 i + j: coordinate j of query i's output, the weighted values summed over the tokens in order
+    const int qi = lane >> 4, c = lane & 15;
+    if (qi >= nq) return;
+    float o = 0.0f;
+    for (int t = 0; t < T; t++) o += ps[h][qi][t] * vs[h][t][c];
+    float l = lsum[0];
+#pragma unroll
+    for (int i = 1; i < CLS_MAXQ; i++)
+        if (qi == i) l = lsum[i];
+    out[((size_t)r * nq + qi) * e + h * 16 + c] = o / l;
+}
+
 // ---- attention within each row on split-fp16 MFMA, rotary positions folded in: head width 16, T <= 128 ---------
 // grid (rows, heads); 256 threads. The row's keys and values of head h are loaded once per workgroup (one thread per
 // token), the keys rotated (RoPE, the k_rope formula), both scaled by the power of two that brings the head's
@@ -823,10 +917,16 @@ void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, co
             hipLaunchKernelGGL(k_first_tokens, dim3(n), dim3(256), 0, s, n, T, cls, e, tok, xc);
             TAH_LAUNCHED();
             rows128(s, M, e, xc, e, b.inimg, b.ins, b.in_b, ac, e, EPI_NONE, nullptr, 0, nullptr, b.n1w, b.n1b);
-            q_of = ac;
-            q_row = (size_t)cls * e;
-            q_tok = e;
-            attend(cls, att);
+            if (cls <= CLS_MAXQ && heads <= 8 && hd == 16) {
+                hipLaunchKernelGGL(k_cls_attn, dim3(n), dim3(64 * heads), 0, s, n, T, cls, e, qkv + e,
+                                   (size_t)T * 3 * e, 3 * e, ac, (size_t)cls * e, e, cosv, sinv, att);
+                TAH_LAUNCHED();
+            } else {
+                q_of = ac;
+                q_row = (size_t)cls * e;
+                q_tok = e;
+                attend(cls, att);
+            }
             out_projection(s, M, att, b, xc);
             feed_forward(s, M, xc, b, t, mid);
             layer_norm(s, M, e, xc, e, w->out_lnw, w->out_lnb, rep, e);
