@@ -18,10 +18,58 @@
 namespace tah {
 
 // ---- input layer -------------------------------------------------------------------------------------------
-// 32 threads per cell, four outputs a thread (e a multiple of 4); 32-bit index arithmetic throughout.
+// A workgroup per table row, four outputs a thread (e a multiple of 4); 32-bit index arithmetic throughout. From
+// INPUT_ROWS_MIN rows (2,048 rows: 48.7 -> about 33 us); below, where one row's workgroup would serialise its cells,
+// k_input_cells_few (one row: 0.642 against 0.652 ms a prediction; 256 rows 1.284 against 1.290 ms).
+constexpr int INPUT_ROWS_MIN = 1024;
 __global__ __launch_bounds__(256) void k_input_cells(int n, int features, int group, int e, const float *__restrict__ x,
                                                       const float *__restrict__ in_w, const float *__restrict__ in_b,
                                                       float *__restrict__ cells) {
+    // a workgroup per table row: the row's values in LDS; thread t keeps the weights of outputs 4 (t % 32) + 0..3
+    // (of each 128 the cell has) and writes them for cells t / 32, t / 32 + 8, ...
+    __shared__ float xs[1024];
+    const int r = blockIdx.x;
+    if (r >= n) return;
+    for (int j = threadIdx.x; j < features; j += 256) xs[j] = x[(size_t)r * features + j];
+    __syncthreads();
+    const int q = threadIdx.x & 31;
+    float *row = cells + (size_t)r * features * e;
+    for (int o = 4 * q; o < e; o += 128) {
+        // in_w rows o .. o + 3 are 4 * group consecutive floats (16-byte aligned: o is a multiple of 4)
+        float wv[32];
+        const float4 *wp = reinterpret_cast<const float4 *>(in_w + (size_t)o * group);
+        for (int i = 0; i < group; i++) {
+            const float4 t = wp[i];
+            wv[4 * i] = t.x; wv[4 * i + 1] = t.y; wv[4 * i + 2] = t.z; wv[4 * i + 3] = t.w;
+        }
+        const float4 bb = *reinterpret_cast<const float4 *>(in_b + o);
+        for (int g = threadIdx.x >> 5; g < features; g += 8) {
+            float vals[8];
+            bool missing = true;
+            for (int k = 0; k < group; k++) {
+                int j = g + (1 << k);
+                while (j >= features) j -= features;
+                vals[k] = xs[j];
+                missing = missing && vals[k] == -100.0f;
+            }
+            float4 v = make_float4(-100.0f, -100.0f, -100.0f, -100.0f);
+            if (!missing) {
+                float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                for (int k = 0; k < group; k++) {
+#pragma unroll
+                    for (int u = 0; u < 4; u++) acc[u] += wv[u * group + k] * vals[k];
+                }
+                v = make_float4(acc[0] + bb.x, acc[1] + bb.y, acc[2] + bb.z, acc[3] + bb.w);
+            }
+            *reinterpret_cast<float4 *>(row + (size_t)g * e + o) = v;
+        }
+    }
+}
+
+// Few table rows (below INPUT_ROWS_MIN): 32 threads a cell, so that the cells of one row spread over workgroups.
+__global__ __launch_bounds__(256) void k_input_cells_few(int n, int features, int group, int e, const float *__restrict__ x,
+                                                          const float *__restrict__ in_w, const float *__restrict__ in_b,
+                                                          float *__restrict__ cells) {
     const int cell = blockIdx.x * 8 + (threadIdx.x >> 5), q = threadIdx.x & 31;
     if (cell >= n * features) return;
     const int r = cell / features, g = cell - r * features;
@@ -38,7 +86,6 @@ __global__ __launch_bounds__(256) void k_input_cells(int n, int features, int gr
     for (int o = 4 * q; o < e; o += 128) {
         float4 v = make_float4(-100.0f, -100.0f, -100.0f, -100.0f);
         if (!missing) {
-            // in_w rows o .. o + 3 are 4 * group consecutive floats (16-byte aligned: o is a multiple of 4)
             float wv[32];
             const float4 *wp = reinterpret_cast<const float4 *>(in_w + (size_t)o * group);
             for (int i = 0; i < group; i++) {
@@ -728,8 +775,12 @@ void input_cells(hipStream_t s, const tah_weights *w, const float *x, int n, int
     if (w->group > 8 || w->group < 1) throw ArgError{"column stage: feature group size must be 1..8"};
     if (w->e % 4) throw ArgError{"column stage: embedding width must be a multiple of 4"};
     if ((size_t)n * features > (size_t)INT32_MAX) throw ArgError{"column stage: too many cells"};
-    hipLaunchKernelGGL(k_input_cells, dim3((unsigned)(((size_t)n * features + 7) / 8)), dim3(256), 0, s, n, features,
-                       w->group, w->e, x, w->in_w, w->in_b, cells);
+    if (n >= INPUT_ROWS_MIN && features <= 1024)
+        hipLaunchKernelGGL(k_input_cells, dim3(n), dim3(256), 0, s, n, features, w->group, w->e, x, w->in_w, w->in_b,
+                           cells);
+    else
+        hipLaunchKernelGGL(k_input_cells_few, dim3((unsigned)(((size_t)n * features + 7) / 8)), dim3(256), 0, s, n,
+                           features, w->group, w->e, x, w->in_w, w->in_b, cells);
     TAH_LAUNCHED();
 }
 
