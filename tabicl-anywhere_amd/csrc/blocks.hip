@@ -48,18 +48,12 @@ __device__ __forceinline__ void ff128_start(uint8_t *slab, float *bias1, const u
     if (tid < 64) reinterpret_cast<float4 *>(bias1)[tid] = reinterpret_cast<const float4 *>(b1)[tid];
 }
 
-// x += l2(gelu(l1(norm2 x))) + b2 for 32 rows a wavefront (after ff128_start, all 256 threads): xv holds this lane's
-// half of its row (columns 16 ks + 8 g + t); xrow is the row's storage, which holds x (read back for the residual
-// add) and takes the result (not where !live).
-__device__ __forceinline__ void ff128_rows(float (&xv)[8][8], bool live, float *xrow, uint8_t *slab, const float *bias1,
-                                           const float *__restrict__ lnw, const float *__restrict__ lnb,
-                                           const uint8_t *__restrict__ w1img, int s1,
-                                           const uint8_t *__restrict__ w2img, const float *__restrict__ b2, int s2,
-                                           int tid) {
+// Layer normalisation of this lane's half row xv (columns 16 ks + 8 g + t; the other half on lane l ^ 32) with
+// lnw / lnb in place (two passes, biased variance, eps 1e-5), then its split as the B operand of a 128-column product,
+// scaled by the row's power of two 2^sx (its largest magnitude below 2^14); returns sx.
+__device__ __forceinline__ int norm_split(float (&xv)[8][8], const float *__restrict__ lnw,
+                                          const float *__restrict__ lnb, int g, halfx8 (&xh)[8], halfx8 (&xl)[8]) {
     constexpr int E = 128;
-    const int lane = tid & 63;
-    const int r32 = lane & 31, g = lane >> 5;
-    // layer normalisation (two passes, biased variance, eps 1e-5)
     float sum = 0.0f;
 #pragma unroll
     for (int ks = 0; ks < 8; ks++)
@@ -94,16 +88,47 @@ __device__ __forceinline__ void ff128_rows(float (&xv)[8][8], bool live, float *
     }
     xmax = fmaxf(xmax, __shfl_xor(xmax, 32, 64));
     const int sx = shift_for_max(xmax);
-    halfx8 xh[8], xl[8];
 #pragma unroll
     for (int ks = 0; ks < 8; ks++) split8(xv[ks], ldexpf(1.0f, sx), xh[ks], xl[ks]);
+    return sx;
+}
+
+// The next block's key and value projection, formed from a feed-forward's result in the same kernel (ff128_rows with
+// KV): img the [2 e][e] weight image (the keys' 128 rows, then the values'), shift its power of two, lnw / lnb the
+// next block's first normalisation, b its 2 e biases, out the lane's token's [2 e] row (keys, then values).
+struct KvNext {
+    const uint8_t *img;
+    int shift;
+    const float *lnw, *lnb, *b;
+    float *out;
+};
+
+// x += l2(gelu(l1(norm2 x))) + b2 for 32 rows a wavefront (after ff128_start, all 256 threads): xv holds this lane's
+// half of its row (columns 16 ks + 8 g + t); xrow is the row's storage, which holds x (read back for the residual
+// add) and takes the result (not where !live). With KV the result goes on, still in registers, through kn's
+// normalisation and projection (its four weight slices streamed after W2's) to kn.out (not where !live).
+template <bool KV = false>
+__device__ __forceinline__ void ff128_rows(float (&xv)[8][8], bool live, float *xrow, uint8_t *slab, const float *bias1,
+                                           const float *__restrict__ lnw, const float *__restrict__ lnb,
+                                           const uint8_t *__restrict__ w1img, int s1,
+                                           const uint8_t *__restrict__ w2img, const float *__restrict__ b2, int s2,
+                                           int tid, const KvNext &kn = KvNext{}) {
+    constexpr int E = 128;
+    const int lane = tid & 63;
+    const int r32 = lane & 31, g = lane >> 5;
+    halfx8 xh[8], xl[8];
+    const int sx = norm_split(xv, lnw, lnb, g, xh, xl);
 
     // H^T = W1 X^T in two halves of 128 hidden units (4 tiles of 32 each); the weights stream as slices of CPS
     // 16-column steps, W1's (half-major) then W2's, slice j into buffer j % 2
     const int arow = sigma32(r32);
-    // slices 0 .. 2 NSL - 1: W1 (two 128-row blocks), then 2 NSL .. 4 NSL - 1: W2 (128 rows, 256 columns)
+    // slices 0 .. 2 NSL - 1: W1 (two 128-row blocks), then 2 NSL .. 4 NSL - 1: W2 (128 rows, 256 columns), then
+    // with KV 4 NSL .. 6 NSL - 1: the next block's key and value weights (two 128-row blocks)
+    constexpr int NSLICES = (KV ? 6 : 4) * NSL;
     auto slice = [&](int j) {
-        return j < 2 * NSL ? w1img + (size_t)j * SLAB : w2img + (size_t)(j - 2 * NSL) * SLAB;
+        return j < 2 * NSL   ? w1img + (size_t)j * SLAB
+               : j < 4 * NSL ? w2img + (size_t)(j - 2 * NSL) * SLAB
+                             : kn.img + (size_t)(j - 4 * NSL) * SLAB;
     };
     halfx8 hh8[16], hl8[16];  // the hidden layer, split: 16-unit step k = 2 T + hh of half 0, then of half 1
     static_assert(NSL == 2, "two slices a 128-row weight block: two tiles of the other half activated a slice");
@@ -112,7 +137,7 @@ __device__ __forceinline__ void ff128_rows(float (&xv)[8][8], bool live, float *
     auto next = [&](int j) {
         __builtin_amdgcn_s_waitcnt(0);  // this wavefront's copies of slice j have landed
         __syncthreads();                // everyone's have; slice j - 1's buffer is free
-        if (j + 1 < 4 * NSL) dma_to_lds<64 * FFW>(slice(j + 1), slab + ((j + 1) & 1) * SLAB, SLAB, tid);
+        if (j + 1 < NSLICES) dma_to_lds<64 * FFW>(slice(j + 1), slab + ((j + 1) & 1) * SLAB, SLAB, tid);
         return static_cast<const uint8_t *>(slab + (j & 1) * SLAB);
     };
     // acc[T] += (rows 32 T .. 32 T + 31 of the slice's weights) B over the slice's CPS 16-column steps
@@ -198,8 +223,9 @@ __device__ __forceinline__ void ff128_rows(float (&xv)[8][8], bool live, float *
     }
 #pragma unroll
     for (int st = 0; st < NSL; st++) mma(y, next(3 * NSL + st), hh8 + 8 + CPS * st, hl8 + 8 + CPS * st, E);
-    if (!live) return;
-    // output column of accumulator v of tile T: 32 T + 16 (v / 8) + 8 g + v % 8; x += y + b2
+    if (!KV && !live) return;
+    // output column of accumulator v of tile T: 32 T + 16 (v / 8) + 8 g + v % 8; x += y + b2 (a lane that is not live
+    // reads its row's first token, which is there, and stores nothing)
     const float u2 = ldexpf(1.0f, -(sh1 + s2));
 #pragma unroll
     for (int T = 0; T < 4; T++)
@@ -207,16 +233,49 @@ __device__ __forceinline__ void ff128_rows(float (&xv)[8][8], bool live, float *
         for (int hh = 0; hh < 2; hh++) {
             const int c0 = 32 * T + 16 * hh + 8 * g;
             float *dst = xrow + c0;
-            const float4 ra = *reinterpret_cast<const float4 *>(dst), rb = *reinterpret_cast<const float4 *>(dst + 4);
-            const float4 ba = *reinterpret_cast<const float4 *>(b2 + c0), bb = *reinterpret_cast<const float4 *>(b2 + c0 + 4);
-            float yv[8];
+            float rv[8], bv[8], xo[8];
+            load8(dst, rv);
+            load8(b2 + c0, bv);
 #pragma unroll
-            for (int t = 0; t < 8; t++) yv[t] = y[T][8 * hh + t];
-            *reinterpret_cast<float4 *>(dst) = make_float4(yv[0] * u2 + ba.x + ra.x, yv[1] * u2 + ba.y + ra.y,
-                                                           yv[2] * u2 + ba.z + ra.z, yv[3] * u2 + ba.w + ra.w);
-            *reinterpret_cast<float4 *>(dst + 4) = make_float4(yv[4] * u2 + bb.x + rb.x, yv[5] * u2 + bb.y + rb.y,
-                                                               yv[6] * u2 + bb.z + rb.z, yv[7] * u2 + bb.w + rb.w);
+            for (int t = 0; t < 8; t++) xo[t] = y[T][8 * hh + t] * u2 + bv[t] + rv[t];
+            if (live) {
+                *reinterpret_cast<float4 *>(dst) = make_float4(xo[0], xo[1], xo[2], xo[3]);
+                *reinterpret_cast<float4 *>(dst + 4) = make_float4(xo[4], xo[5], xo[6], xo[7]);
+            }
+            if constexpr (KV) {
+#pragma unroll
+                for (int t = 0; t < 8; t++) xv[2 * T + hh][t] = xo[t];
+            }
         }
+    if constexpr (KV) {
+        // the next block's keys (slices 4 NSL ..) then values (6 NSL - NSL ..): 128 outputs each, as four 32-row tiles
+        const int sk = norm_split(xv, kn.lnw, kn.lnb, g, xh, xl);
+        const float uk = ldexpf(1.0f, -(sk + kn.shift));
+#pragma unroll
+        for (int part = 0; part < 2; part++) {
+            floatx16 a[4];
+#pragma unroll
+            for (int T = 0; T < 4; T++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) a[T][v] = 0.0f;
+#pragma unroll
+            for (int st = 0; st < NSL; st++) mma(a, next(4 * NSL + NSL * part + st), xh + CPS * st, xl + CPS * st, 128);
+#pragma unroll
+            for (int T = 0; T < 4; T++)
+#pragma unroll
+                for (int hh = 0; hh < 2; hh++) {
+                    const int c0 = 128 * part + 32 * T + 16 * hh + 8 * g;
+                    float bv[8], o[8];
+                    load8(kn.b + c0, bv);
+#pragma unroll
+                    for (int t = 0; t < 8; t++) o[t] = a[T][8 * hh + t] * uk + bv[t];
+                    if (live) {
+                        *reinterpret_cast<float4 *>(kn.out + c0) = make_float4(o[0], o[1], o[2], o[3]);
+                        *reinterpret_cast<float4 *>(kn.out + c0 + 4) = make_float4(o[4], o[5], o[6], o[7]);
+                    }
+                }
+        }
+    }
 }
 
 // grid ceil(M / (32 FFW)); 64 FFW threads. x [M][128] in place.
@@ -741,9 +800,11 @@ __global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t 
 //    head's power of two (one wavefront-pair's maximum each, across wavefronts through LDS): threads 0..127 a key
 //    each, threads 128..255 a value each, for the next head while the current one is attended (two barriers a head);
 //  * keys past T are masked; the attention and the output projection then run as in k_cell_block.
-// With FF the block's feed-forward half follows in the same kernel, as in k_cell_block.
-template <bool FF>
-__global__ __launch_bounds__(256, 2) void k_row_block(int T, float *tok, const float *__restrict__ kv,
+// With FF the block's feed-forward half follows in the same kernel, as in k_cell_block; with KV as well the next
+// row block's keys and values (kn.out [n][T][2 e], which may be kv itself: a workgroup reads only its own row's keys
+// and values, all of them before its feed-forward half starts).
+template <bool FF, bool KV>
+__global__ __launch_bounds__(256, 2) void k_row_block(int T, float *tok, const float *kv,
                                                        const float *__restrict__ cosv, const float *__restrict__ sinv,
                                                        const float *__restrict__ n1w, const float *__restrict__ n1b,
                                                        const uint8_t *__restrict__ qimg, int qshift,
@@ -751,7 +812,8 @@ __global__ __launch_bounds__(256, 2) void k_row_block(int T, float *tok, const f
                                                        int oshift, const float *__restrict__ ob, const float *__restrict__ n2w, const float *__restrict__ n2b,
                                                        const uint8_t *__restrict__ w1img, const float *__restrict__ b1,
                                                        int s1, const uint8_t *__restrict__ w2img,
-                                                       const float *__restrict__ b2, int s2) {
+                                                       const float *__restrict__ b2, int s2, KvNext kn) {
+    static_assert(FF || !KV, "the next block's keys and values come from the feed-forward's registers");
     constexpr int E = 128;
     __shared__ __align__(16) uint8_t lds[65536];
     __shared__ __align__(16) float ffb[FF ? 256 : 4];  // FF: the first feed-forward layer's bias
@@ -1081,7 +1143,12 @@ __global__ __launch_bounds__(256, 2) void k_row_block(int T, float *tok, const f
     if constexpr (FF) {
         __syncthreads();  // every wavefront is done with the attention's LDS (no copy is in flight after head 7)
         ff128_start(lds, ffb, w1img, b1, tid);
-        ff128_rows(xn, live, xrow, lds, ffb, n2w, n2b, w1img, s1, w2img, b2, s2, tid);
+        if constexpr (KV) {
+            kn.out += ((size_t)row * T + (live ? tk : 0)) * 2 * E;
+            ff128_rows<true>(xn, live, xrow, lds, ffb, n2w, n2b, w1img, s1, w2img, b2, s2, tid, kn);
+        } else {
+            ff128_rows(xn, live, xrow, lds, ffb, n2w, n2b, w1img, s1, w2img, b2, s2, tid);
+        }
     }
 }
 
@@ -1091,20 +1158,32 @@ bool row_block_fits(const DevBlock &b, int T) {
 
 bool block_ff_fits(const DevBlock &b) { return ff_fused_shape(b.d, b.ff) && b.l1img && b.l2img; }
 
+bool row_kv_fits(const DevBlock &next) { return next.d == 128 && next.inimg && next.in_b && next.n1w && next.n1b; }
+
 void row_block(hipStream_t s, int n, int T, float *tok, const float *kv, const float *cosv, const float *sinv,
-               const DevBlock &b, bool ff) {
+               const DevBlock &b, bool ff, const DevBlock *next, float *kv_next) {
     if (n <= 0) return;
     if (!row_block_fits(b, T) || (reinterpret_cast<uintptr_t>(tok) & 15) || (reinterpret_cast<uintptr_t>(kv) & 15))
         throw ArgError{"row_block: needs e = 128, 8 heads, weight images, at most 128 tokens and aligned rows"};
     if (ff && !block_ff_fits(b)) throw ArgError{"row_block: no fused feed-forward weights for this shape"};
-    if (ff)
-        hipLaunchKernelGGL(k_row_block<true>, dim3(n), dim3(256), 0, s, T, tok, kv, cosv, sinv, b.n1w, b.n1b, b.inimg,
-                           b.ins, b.in_b, b.outimg, b.outs, b.out_b, b.n2w, b.n2b, b.l1img, b.l1b, b.l1s, b.l2img,
-                           b.l2b, b.l2s);
-    else
-        hipLaunchKernelGGL(k_row_block<false>, dim3(n), dim3(256), 0, s, T, tok, kv, cosv, sinv, b.n1w, b.n1b, b.inimg,
-                           b.ins, b.in_b, b.outimg, b.outs, b.out_b, nullptr, nullptr, nullptr, nullptr, 0, nullptr,
-                           nullptr, 0);
+    if (next && (!ff || !row_kv_fits(*next) || !kv_next || (reinterpret_cast<uintptr_t>(kv_next) & 15)))
+        throw ArgError{"row_block: the next block's keys and values need the fused feed-forward, e = 128, its "
+                       "projection image and an aligned destination"};
+    if (next) {
+        const KvNext kn{next->inimg + (size_t)128 * 128 * 4, next->ins, next->n1w, next->n1b, next->in_b + 128,
+                        kv_next};
+        hipLaunchKernelGGL((k_row_block<true, true>), dim3(n), dim3(256), 0, s, T, tok, kv, cosv, sinv, b.n1w, b.n1b,
+                           b.inimg, b.ins, b.in_b, b.outimg, b.outs, b.out_b, b.n2w, b.n2b, b.l1img, b.l1b, b.l1s,
+                           b.l2img, b.l2b, b.l2s, kn);
+    } else if (ff) {
+        hipLaunchKernelGGL((k_row_block<true, false>), dim3(n), dim3(256), 0, s, T, tok, kv, cosv, sinv, b.n1w, b.n1b,
+                           b.inimg, b.ins, b.in_b, b.outimg, b.outs, b.out_b, b.n2w, b.n2b, b.l1img, b.l1b, b.l1s,
+                           b.l2img, b.l2b, b.l2s, KvNext{});
+    } else {
+        hipLaunchKernelGGL((k_row_block<false, false>), dim3(n), dim3(256), 0, s, T, tok, kv, cosv, sinv, b.n1w,
+                           b.n1b, b.inimg, b.ins, b.in_b, b.outimg, b.outs, b.out_b, nullptr, nullptr, nullptr,
+                           nullptr, 0, nullptr, nullptr, 0, KvNext{});
+    }
     TAH_LAUNCHED();
 }
 

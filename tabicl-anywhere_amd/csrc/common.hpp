@@ -193,11 +193,14 @@ void ff_block(hipStream_t s, int M, float *x, const DevBlock &b);
 bool cell_block_fits(const DevBlock &b);
 // The attention half of a row block for every token of n rows of T tokens (tok [n][T][e] in place), from the keys
 // and values kv [n][T][2 e] the projection made (unrotated); e = 128, 8 heads of 16, T <= 128 (row_block_fits).
-// With ff (block_ff_fits) either kernel runs the block's feed-forward half as well, in the same launch.
+// With ff (block_ff_fits) either kernel runs the block's feed-forward half as well, in the same launch; the row
+// block with next as well (ff, row_kv_fits) forms that block's keys and values [n][T][2 e] from the result into
+// kv_next (which may be kv).
 bool row_block_fits(const DevBlock &b, int T);
 bool block_ff_fits(const DevBlock &b);
+bool row_kv_fits(const DevBlock &next);
 void row_block(hipStream_t s, int n, int T, float *tok, const float *kv, const float *cosv, const float *sinv,
-               const DevBlock &b, bool ff);
+               const DevBlock &b, bool ff, const DevBlock *next = nullptr, float *kv_next = nullptr);
 size_t cell_block_work_bytes(int groups);
 void cell_block(hipStream_t s, int n, int groups, size_t sr, size_t sg, float *cells, const DevBlock &b,
                 const float *qscale, const float *kvbase, size_t gstride, void *work, bool ff);

@@ -944,33 +944,47 @@ void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, co
                                heads, qkv, dst);
         TAH_LAUNCHED();
     };
+    // the last block's path: only the class tokens queried (from CLS_QUERIES_MIN rows), by k_cls_attn where it
+    // takes the shape
+    const bool cls_path = fused && w->row[last].inimg && n >= CLS_QUERIES_MIN;
+    const bool cls_kernel = cls_path && cls <= CLS_MAXQ && heads <= 8;
+    bool kv_ready = false;  // the previous row block formed this block's keys and values, qkv [R][2 e]
     for (int bi = 0; bi <= last; bi++) {
         const DevBlock &b = w->row[bi];
         if (bi < last && fused && row_block_fits(b, T) && n >= ROW_BLOCK_MIN) {
-            // keys and values by the projection (its second and third 128-row blocks), then the attention half of
-            // the block in one kernel (and the feed-forward half in it too where the fused kernel takes the shape);
-            // qkv holds [R][2 e]
-            rows128(s, (int)R, 2 * e, tok, e, b.inimg + (size_t)128 * e * 4, b.ins, b.in_b + e, qkv, 2 * e, EPI_NONE,
-                    nullptr, 0, nullptr, b.n1w, b.n1b);
+            // keys and values by the projection (its second and third 128-row blocks, qkv [R][2 e]) unless the
+            // previous block formed them, then the attention half of the block in one kernel (and the feed-forward
+            // half in it too where the fused kernel takes the shape, and then the next block's keys and values as
+            // well where that block reads them as qkv [R][2 e]: a row block's or the class-token kernel)
+            if (!kv_ready)
+                rows128(s, (int)R, 2 * e, tok, e, b.inimg + (size_t)128 * e * 4, b.ins, b.in_b + e, qkv, 2 * e,
+                        EPI_NONE, nullptr, 0, nullptr, b.n1w, b.n1b);
             const bool ff = block_ff_fits(b) && R > SMALL_ROWS;
-            row_block(s, n, T, tok, qkv, cosv, sinv, b, ff);
+            const DevBlock &nb = w->row[bi + 1];
+            const bool chain = ff && row_kv_fits(nb) &&
+                               (bi + 1 < last ? row_block_fits(nb, T) : cls_kernel);
+            row_block(s, n, T, tok, qkv, cosv, sinv, b, ff, chain ? &nb : nullptr, qkv);
+            kv_ready = chain;
             if (!ff) feed_forward(s, (int)R, tok, b, t, mid);
             continue;
         }
-        if (bi == last && fused && b.inimg && n >= CLS_QUERIES_MIN) {
+        if (bi == last && cls_path) {
             // the last block queries only the class tokens: keys and values for every token (the projection's second
-            // and third 128-row blocks, into qkv's [T][3 e] rows), queries for the class tokens alone, from their
-            // gathered copy (which the block then updates); below CLS_QUERIES_MIN rows the extra launch costs more
-            // than the other tokens' queries (2,048 rows 4.30 -> 4.25 ms, 64 and 256 rows 5 us slower)
-            rows128(s, (int)R, 2 * e, tok, e, b.inimg + (size_t)128 * e * 4, b.ins, b.in_b + e, qkv + e, 3 * e, EPI_NONE,
-                    nullptr, 0, nullptr, b.n1w, b.n1b);
+            // and third 128-row blocks: qkv [R][2 e] for k_cls_attn, unless the previous block formed them, else into
+            // qkv's [T][3 e] rows), queries for the class tokens alone, from their gathered copy (which the block
+            // then updates); below CLS_QUERIES_MIN rows the extra launch costs more than the other tokens' queries
+            // (2,048 rows 4.30 -> 4.25 ms, 64 and 256 rows 5 us slower)
+            if (!kv_ready)
+                rows128(s, (int)R, 2 * e, tok, e, b.inimg + (size_t)128 * e * 4, b.ins, b.in_b + e,
+                        cls_kernel ? qkv : qkv + e, cls_kernel ? 2 * e : 3 * e, EPI_NONE, nullptr, 0, nullptr, b.n1w,
+                        b.n1b);
             const int M = n * cls;
             hipLaunchKernelGGL(k_first_tokens, dim3(n), dim3(256), 0, s, n, T, cls, e, tok, xc);
             TAH_LAUNCHED();
             rows128(s, M, e, xc, e, b.inimg, b.ins, b.in_b, ac, e, EPI_NONE, nullptr, 0, nullptr, b.n1w, b.n1b);
-            if (cls <= CLS_MAXQ && heads <= 8 && hd == 16) {
-                hipLaunchKernelGGL(k_cls_attn, dim3(n), dim3(64 * heads), 0, s, n, T, cls, e, qkv + e,
-                                   (size_t)T * 3 * e, 3 * e, ac, (size_t)cls * e, e, cosv, sinv, att);
+            if (cls_kernel) {
+                hipLaunchKernelGGL(k_cls_attn, dim3(n), dim3(64 * heads), 0, s, n, T, cls, e, qkv, (size_t)T * 2 * e,
+                                   2 * e, ac, (size_t)cls * e, e, cosv, sinv, att);
                 TAH_LAUNCHED();
             } else {
                 q_of = ac;
