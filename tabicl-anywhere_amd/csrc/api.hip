@@ -503,6 +503,7 @@ extern "C" void tah_weights_free(tah_weights *w) {
     if (!w) return;
     (void)hipSetDevice(w->ordinal);
     for (auto &r : w->rope) (void)hipFree(r.second);
+    if (w->cls_kv) (void)hipFree(w->cls_kv);
     if (w->arena) (void)hipFree(w->arena);
     delete w;
 }
@@ -1000,6 +1001,18 @@ static const float *rope_tables(const tah_weights *w_, int T) {
     return d;
 }
 
+// The class tokens' keys and values in the first row block (class_token_kv), made on the card the first time they
+// are needed and kept with the weights (they depend on the weights alone).
+static const float *class_kv(tah_dev *dev, const tah_weights *w_) {
+    auto *w = const_cast<tah_weights *>(w_);  // the cache is not part of the weights' value
+    if (w->cls_kv) return w->cls_kv;
+    float *d = nullptr;
+    TAH_HIP(hipMalloc(&d, (size_t)w->cls * 3 * w->e * sizeof(float)));
+    w->cls_kv = d;
+    class_token_kv(dev->stream, w, d, d + (size_t)w->cls * 2 * w->e);
+    return d;
+}
+
 static void check_columns(const tah_weights *w, const tah_model *model) {
     if (!model->col_kv) throw ArgError{"the model holds no column cache (tah_model_set_columns)"};
     if (w->col_a2.empty() || w->row.empty() || !w->col_scale) throw ArgError{"weights lack the column or row stage"};
@@ -1094,9 +1107,23 @@ static void predict_rows(tah_dev *dev, const tah_weights *w, const tah_model *mo
         Loans loans(dev);
         float *tok = loans.take<float>((size_t)k * T * w->e);
         float *rep = loans.take<float>((size_t)k * w->d);
-        embed_rows(dev, w, model, x + (size_t)r0 * model->features, k, tok, loans);
-        float *scratch = loans.take<float>(row_stage_floats(w, k, T));
-        row_stage(dev->stream, w, tok, k, T, tabs, tabs + (size_t)T * w->rope_half, rep, scratch);
+        const float *xr = x + (size_t)r0 * model->features;
+        float *scratch = nullptr;
+        bool kv_ready = false;
+        if (column_tokens_fits(w, k, model->features, model->digits)) {
+            // the column stage straight into the tokens, and the first row block's keys and values from its last
+            // block's kernel where the row stage takes them
+            float *cs = loans.take<float>(column_stage_floats(w, k, model->features, model->digits));
+            scratch = loans.take<float>(row_stage_floats(w, k, T));
+            kv_ready = row_stage_takes_kv(w, k, T);
+            column_stage_tokens(dev->stream, w, model->col_kv, xr, k, model->features, tok,
+                                kv_ready ? row_stage_kv(w, k, T, scratch) : nullptr,
+                                kv_ready ? class_kv(dev, w) : nullptr, cs);
+        } else {
+            embed_rows(dev, w, model, xr, k, tok, loans);
+            scratch = loans.take<float>(row_stage_floats(w, k, T));
+        }
+        row_stage(dev->stream, w, tok, k, T, tabs, tabs + (size_t)T * w->rope_half, rep, scratch, kv_ready);
         stage_rows(dev, w, model, rep, k, out_n, out + (size_t)r0 * out_n, loans);
     }
 }

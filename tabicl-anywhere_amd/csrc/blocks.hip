@@ -525,7 +525,9 @@ __global__ __launch_bounds__(256) void k_cell_images(const float *__restrict__ k
 // head's values are larger than all before: every head's output is at most its values' largest magnitude.
 // With FF the block's feed-forward half follows in the same kernel (ff128_rows, its weight slices in the same 64 KB
 // of LDS): the cells' new values stay in registers as its input; they are written out as well, for its residual add.
-template <bool FF>
+// With KV as well the result goes on to the first row block's keys and values (ff128_rows with KV): cell (r, g)'s at
+// kn.out + (r sr + g sg) 2 e.
+template <bool FF, bool KV>
 __global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t sg, float *cells,
                                                         const float *__restrict__ n1w, const float *__restrict__ n1b,
                                                         const uint8_t *__restrict__ qimg, int qshift,
@@ -535,7 +537,8 @@ __global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t 
                                                         const float *__restrict__ ob, const float *__restrict__ n2w, const float *__restrict__ n2b,
                                                         const uint8_t *__restrict__ w1img, const float *__restrict__ b1,
                                                         int s1, const uint8_t *__restrict__ w2img,
-                                                        const float *__restrict__ b2, int s2) {
+                                                        const float *__restrict__ b2, int s2, KvNext kn) {
+    static_assert(FF || !KV, "the next block's keys and values come from the feed-forward's registers");
     constexpr int E = 128;
     __shared__ __align__(16) uint8_t lds[65536];
     __shared__ __align__(16) float ffb[FF ? 256 : 4];  // FF: the first feed-forward layer's bias
@@ -784,7 +787,12 @@ __global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t 
     if constexpr (FF) {
         __syncthreads();  // every wavefront is done with the attention's LDS (no copy is in flight after head 7)
         ff128_start(lds, ffb, w1img, b1, tid);
-        ff128_rows(xn, live, xrow, lds, ffb, n2w, n2b, w1img, s1, w2img, b2, s2, tid);
+        if constexpr (KV) {
+            kn.out += m * 2 * E;
+            ff128_rows<true>(xn, live, xrow, lds, ffb, n2w, n2b, w1img, s1, w2img, b2, s2, tid, kn);
+        } else {
+            ff128_rows(xn, live, xrow, lds, ffb, n2w, n2b, w1img, s1, w2img, b2, s2, tid);
+        }
     }
 }
 
@@ -1194,23 +1202,35 @@ bool cell_block_fits(const DevBlock &b) {
 size_t cell_block_work_bytes(int groups) { return (size_t)groups * 8 * (CIMG + 2 * sizeof(int)); }
 
 void cell_block(hipStream_t s, int n, int groups, size_t sr, size_t sg, float *cells, const DevBlock &b,
-                const float *qscale, const float *kvbase, size_t gstride, void *work, bool ff) {
+                const float *qscale, const float *kvbase, size_t gstride, void *work, bool ff, const DevBlock *next,
+                float *kv_next) {
     if (n <= 0 || groups <= 0) return;
     if (!cell_block_fits(b) || (reinterpret_cast<uintptr_t>(cells) & 15) || (reinterpret_cast<uintptr_t>(work) & 15))
         throw ArgError{"cell_block: needs e = 128, 8 heads, weight images and 16-byte aligned cells and work"};
     if (ff && !block_ff_fits(b)) throw ArgError{"cell_block: no fused feed-forward weights for this shape"};
+    if (next && (!ff || !row_kv_fits(*next) || !kv_next || (reinterpret_cast<uintptr_t>(kv_next) & 15)))
+        throw ArgError{"cell_block: the row block's keys and values need the fused feed-forward, e = 128, its "
+                       "projection image and an aligned destination"};
     uint8_t *images = static_cast<uint8_t *>(work);
     int *shifts = reinterpret_cast<int *>(images + (size_t)groups * 8 * CIMG);
     hipLaunchKernelGGL(k_cell_images, dim3(groups, 8), dim3(256), 0, s, kvbase, gstride, images, shifts);
     TAH_LAUNCHED();
-    if (ff)
-        hipLaunchKernelGGL(k_cell_block<true>, dim3((n + 127) / 128, groups), dim3(256), 0, s, n, sr, sg, cells, b.n1w,
-                           b.n1b, b.inimg, b.ins, b.in_b, qscale, images, shifts, b.outimg, b.outs, b.out_b, b.n2w,
-                           b.n2b, b.l1img, b.l1b, b.l1s, b.l2img, b.l2b, b.l2s);
-    else
-        hipLaunchKernelGGL(k_cell_block<false>, dim3((n + 127) / 128, groups), dim3(256), 0, s, n, sr, sg, cells, b.n1w,
-                           b.n1b, b.inimg, b.ins, b.in_b, qscale, images, shifts, b.outimg, b.outs, b.out_b, nullptr,
-                           nullptr, nullptr, nullptr, 0, nullptr, nullptr, 0);
+    const dim3 grid((n + 127) / 128, groups);
+    if (next) {
+        const KvNext kn{next->inimg + (size_t)128 * 128 * 4, next->ins, next->n1w, next->n1b, next->in_b + 128,
+                        kv_next};
+        hipLaunchKernelGGL((k_cell_block<true, true>), grid, dim3(256), 0, s, n, sr, sg, cells, b.n1w, b.n1b, b.inimg,
+                           b.ins, b.in_b, qscale, images, shifts, b.outimg, b.outs, b.out_b, b.n2w, b.n2b, b.l1img,
+                           b.l1b, b.l1s, b.l2img, b.l2b, b.l2s, kn);
+    } else if (ff) {
+        hipLaunchKernelGGL((k_cell_block<true, false>), grid, dim3(256), 0, s, n, sr, sg, cells, b.n1w, b.n1b, b.inimg,
+                           b.ins, b.in_b, qscale, images, shifts, b.outimg, b.outs, b.out_b, b.n2w, b.n2b, b.l1img,
+                           b.l1b, b.l1s, b.l2img, b.l2b, b.l2s, KvNext{});
+    } else {
+        hipLaunchKernelGGL((k_cell_block<false, false>), grid, dim3(256), 0, s, n, sr, sg, cells, b.n1w, b.n1b,
+                           b.inimg, b.ins, b.in_b, qscale, images, shifts, b.outimg, b.outs, b.out_b, nullptr, nullptr,
+                           nullptr, nullptr, 0, nullptr, nullptr, 0, KvNext{});
+    }
     TAH_LAUNCHED();
 }
 

@@ -123,6 +123,9 @@ struct tah_weights {
     // position * frequency, [2][T][rope_half] on the card; rope_host is the frequencies as uploaded
     std::vector<float> rope_host;
     std::vector<std::pair<int, float *>> rope;
+    // the class tokens' keys and values in the first row block, [cls][2 e] (then cls e floats of room), made on the
+    // card the first time prediction needs them and kept with the weights
+    float *cls_kv = nullptr;
 };
 
 struct tah_model {
@@ -202,8 +205,11 @@ bool row_kv_fits(const DevBlock &next);
 void row_block(hipStream_t s, int n, int T, float *tok, const float *kv, const float *cosv, const float *sinv,
                const DevBlock &b, bool ff, const DevBlock *next = nullptr, float *kv_next = nullptr);
 size_t cell_block_work_bytes(int groups);
+// With next as well (ff, row_kv_fits) the column block's result goes on to that row block's keys and values: cell
+// (r, g)'s [2 e] at kv_next + (r sr + g sg) 2 e.
 void cell_block(hipStream_t s, int n, int groups, size_t sr, size_t sg, float *cells, const DevBlock &b,
-                const float *qscale, const float *kvbase, size_t gstride, void *work, bool ff);
+                const float *qscale, const float *kvbase, size_t gstride, void *work, bool ff,
+                const DevBlock *next = nullptr, float *kv_next = nullptr);
 // Y [M][N] = epi(X' W^T + b) for K = 128 and N a multiple of 128, W as such an image (scaled by 2^shift), X' = X or
 // layer_norm(X) with lnw/lnb; EPI_NONE, EPI_SCALE (by scale [N]) or EPI_RESID (adds R, may alias Y).
 void rows128(hipStream_t s, int M, int N, const float *X, int ldx, const uint8_t *wimg, int wshift, const float *b,
@@ -257,14 +263,31 @@ void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t 
 void quantile_stats(hipStream_t s, int rows, int n, const float *q, int na, const float *alphas, float *stats);
 
 // Column and row stages (stages.hip).
-void input_cells(hipStream_t s, const tah_weights *w, const float *x, int n, int features, float *cells);
+// The input layer for n rows x [n][features]: cells [n][cls + features][e], the weights' class tokens first where
+// cls > 0 (cls 0: [n][features][e]); with kv (cls > 0) the class tokens' first-row-block keys and values cls_kv
+// [cls][2 e] into kv [n][cls + features][2 e] as well.
+void input_cells(hipStream_t s, const tah_weights *w, const float *x, int n, int features, float *cells, int cls = 0,
+                 float *kv = nullptr, const float *cls_kv = nullptr);
 size_t column_stage_floats(const tah_weights *w, int n, int features, int digits);
 void column_stage(hipStream_t s, const tah_weights *w, const float *col_kv, int digits, const float *x, int n,
                   int features, float *cells, float *scratch);
 void assemble_tokens(hipStream_t s, const tah_weights *w, const float *cells, int n, int features, float *tok);
+// The column stage written straight into the row stage's tokens tok [n][cls + features][e] (no copy), where every
+// column block runs as one fused kernel (column_tokens_fits: one label digit, the fused shapes); with kv as well
+// the last column block forms the first row block's keys and values there ([n][T][2 e]: row_stage_kv of the row
+// stage's scratch, for row_stage with kv_ready; where row_stage_takes_kv), the class tokens' from cls_kv
+// (class_token_kv). scratch holds column_stage_floats floats.
+bool column_tokens_fits(const tah_weights *w, int n, int features, int digits);
+void column_stage_tokens(hipStream_t s, const tah_weights *w, const float *col_kv, const float *x, int n,
+                         int features, float *tok, float *kv, const float *cls_kv, float *scratch);
+// The first row block's keys and values of the class tokens, [cls][2 e] into out (tmp: cls e floats).
+void class_token_kv(hipStream_t s, const tah_weights *w, float *out, float *tmp);
 size_t row_stage_floats(const tah_weights *w, int n, int T);
+bool row_stage_takes_kv(const tah_weights *w, int n, int T);
+float *row_stage_kv(const tah_weights *w, int n, int T, float *scratch);
+// kv_ready: the first row block's keys and values are in row_stage_kv(scratch) already (row_stage_takes_kv).
 void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, const float *cosv, const float *sinv,
-               float *rep, float *scratch);
+               float *rep, float *scratch, bool kv_ready = false);
 // att: att_bytes of scratch (the fused kernel needs cell_block_work_bytes(groups) of it, else M e floats)
 void column_block(hipStream_t s, const tah_weights *w, const DevBlock &b, float *cells, int n, int groups, size_t sr,
                   size_t sg, const float *kvbase, size_t gstride, float *t, float *q, float *att, size_t att_bytes,

@@ -22,18 +22,34 @@ namespace tah {
 // INPUT_ROWS_MIN rows (2,048 rows: 48.7 -> about 33 us); below, where one row's workgroup would serialise its cells,
 // k_input_cells_few (one row: 0.642 against 0.652 ms a prediction; 256 rows 1.284 against 1.290 ms).
 constexpr int INPUT_ROWS_MIN = 1024;
+// The output rows hold cls class tokens (cls_tokens [cls][e]) before the cells: [n][cls + features][e] (cls 0: the
+// cells alone); with kv as well the first row block's keys and values [n][cls + features][2 e] get the class tokens'
+// (cls_kv [cls][2 e]).
 __global__ __launch_bounds__(256) void k_input_cells(int n, int features, int group, int e, const float *__restrict__ x,
                                                       const float *__restrict__ in_w, const float *__restrict__ in_b,
-                                                      float *__restrict__ cells) {
+                                                      float *__restrict__ cells, int cls,
+                                                      const float *__restrict__ cls_tokens, float *__restrict__ kv,
+                                                      const float *__restrict__ cls_kv) {
     // a workgroup per table row: the row's values in LDS; thread t keeps the weights of outputs 4 (t % 32) + 0..3
     // (of each 128 the cell has) and writes them for cells t / 32, t / 32 + 8, ...
     __shared__ float xs[1024];
     const int r = blockIdx.x;
     if (r >= n) return;
     for (int j = threadIdx.x; j < features; j += 256) xs[j] = x[(size_t)r * features + j];
+    const size_t T = (size_t)cls + features;
+    if (cls > 0) {
+        float4 *t4 = reinterpret_cast<float4 *>(cells + (size_t)r * T * e);
+        const float4 *c4 = reinterpret_cast<const float4 *>(cls_tokens);
+        for (int i = threadIdx.x; i < cls * e / 4; i += 256) t4[i] = c4[i];
+        if (kv) {
+            float4 *k4 = reinterpret_cast<float4 *>(kv + (size_t)r * T * 2 * e);
+            const float4 *ck4 = reinterpret_cast<const float4 *>(cls_kv);
+            for (int i = threadIdx.x; i < cls * e / 2; i += 256) k4[i] = ck4[i];
+        }
+    }
     __syncthreads();
     const int q = threadIdx.x & 31;
-    float *row = cells + (size_t)r * features * e;
+    float *row = cells + ((size_t)r * T + cls) * e;
     for (int o = 4 * q; o < e; o += 128) {
         // in_w rows o .. o + 3 are 4 * group consecutive floats (16-byte aligned: o is a multiple of 4)
         float wv[32];
@@ -66,10 +82,11 @@ __global__ __launch_bounds__(256) void k_input_cells(int n, int features, int gr
     }
 }
 
-// Few table rows (below INPUT_ROWS_MIN): 32 threads a cell, so that the cells of one row spread over workgroups.
+// Few table rows (below INPUT_ROWS_MIN): 32 threads a cell, so that the cells of one row spread over workgroups;
+// row r's cells at cells + r ldr (the class tokens, if any, by k_class_tokens).
 __global__ __launch_bounds__(256) void k_input_cells_few(int n, int features, int group, int e, const float *__restrict__ x,
                                                           const float *__restrict__ in_w, const float *__restrict__ in_b,
-                                                          float *__restrict__ cells) {
+                                                          float *__restrict__ cells, size_t ldr) {
     const int cell = blockIdx.x * 8 + (threadIdx.x >> 5), q = threadIdx.x & 31;
     if (cell >= n * features) return;
     const int r = cell / features, g = cell - r * features;
@@ -82,7 +99,7 @@ __global__ __launch_bounds__(256) void k_input_cells_few(int n, int features, in
         vals[k] = xr[j];
         missing = missing && vals[k] == -100.0f;
     }
-    float *dst = cells + (size_t)cell * e;
+    float *dst = cells + (size_t)r * ldr + (size_t)g * e;
     for (int o = 4 * q; o < e; o += 128) {
         float4 v = make_float4(-100.0f, -100.0f, -100.0f, -100.0f);
         if (!missing) {
@@ -745,6 +762,23 @@ __global__ __launch_bounds__(256) void k_tokens(int n, int cls, int features, in
     for (int i = threadIdx.x; i < body4; i += 256) dst[head4 + i] = src[i];
 }
 
+// The class tokens of tok [n][T][e] (cls_tokens [cls][e] at tokens 0 .. cls - 1 of every row) and, with kv, their
+// keys and values in kv [n][T][2 e] (cls_kv [cls][2 e]): a workgroup per row, 16 bytes a thread.
+__global__ __launch_bounds__(256) void k_class_tokens(int n, int T, int cls, int e, const float *__restrict__ cls_tokens,
+                                                       float *__restrict__ tok, const float *__restrict__ cls_kv,
+                                                       float *__restrict__ kv) {
+    const int r = blockIdx.x;
+    if (r >= n) return;
+    float4 *t4 = reinterpret_cast<float4 *>(tok + (size_t)r * T * e);
+    const float4 *c4 = reinterpret_cast<const float4 *>(cls_tokens);
+    for (int i = threadIdx.x; i < cls * e / 4; i += 256) t4[i] = c4[i];
+    if (kv) {
+        float4 *k4 = reinterpret_cast<float4 *>(kv + (size_t)r * T * 2 * e);
+        const float4 *ck4 = reinterpret_cast<const float4 *>(cls_kv);
+        for (int i = threadIdx.x; i < cls * e / 2; i += 256) k4[i] = ck4[i];
+    }
+}
+
 // dst [n][k][e] = the first k tokens of each row of src [n][T][e]: a workgroup per row, 16 bytes a thread.
 __global__ __launch_bounds__(256) void k_first_tokens(int n, int T, int k, int e, const float *__restrict__ src,
                                                        float *__restrict__ dst) {
@@ -771,16 +805,26 @@ __global__ __launch_bounds__(256) void k_divide(size_t count, const float *__res
 static dim3 blocks_for(size_t count) { return dim3((unsigned)((count + 255) / 256)); }
 
 // ---- host side ---------------------------------------------------------------------------------------------
-void input_cells(hipStream_t s, const tah_weights *w, const float *x, int n, int features, float *cells) {
+void input_cells(hipStream_t s, const tah_weights *w, const float *x, int n, int features, float *cells, int cls,
+                 float *kv, const float *cls_kv) {
     if (w->group > 8 || w->group < 1) throw ArgError{"column stage: feature group size must be 1..8"};
     if (w->e % 4) throw ArgError{"column stage: embedding width must be a multiple of 4"};
     if ((size_t)n * features > (size_t)INT32_MAX) throw ArgError{"column stage: too many cells"};
-    if (n >= INPUT_ROWS_MIN && features <= 1024)
+    if (cls < 0 || (cls > 0 && cls != w->cls) || (kv && (!cls || !cls_kv)))
+        throw ArgError{"column stage: class tokens are the weights' own, and their keys and values need them"};
+    const int T = cls + features;
+    if (n >= INPUT_ROWS_MIN && features <= 1024) {
         hipLaunchKernelGGL(k_input_cells, dim3(n), dim3(256), 0, s, n, features, w->group, w->e, x, w->in_w, w->in_b,
-                           cells);
-    else
-        hipLaunchKernelGGL(k_input_cells_few, dim3((unsigned)(((size_t)n * features + 7) / 8)), dim3(256), 0, s, n,
-                           features, w->group, w->e, x, w->in_w, w->in_b, cells);
+                           cells, cls, w->cls_tokens, kv, cls_kv);
+        TAH_LAUNCHED();
+        return;
+    }
+    if (cls > 0) {
+        hipLaunchKernelGGL(k_class_tokens, dim3(n), dim3(256), 0, s, n, T, cls, w->e, w->cls_tokens, cells, cls_kv, kv);
+        TAH_LAUNCHED();
+    }
+    hipLaunchKernelGGL(k_input_cells_few, dim3((unsigned)(((size_t)n * features + 7) / 8)), dim3(256), 0, s, n,
+                       features, w->group, w->e, x, w->in_w, w->in_b, cells + (size_t)cls * w->e, (size_t)T * w->e);
     TAH_LAUNCHED();
 }
 
@@ -822,6 +866,11 @@ static void out_projection(hipStream_t s, int M, const float *att, const DevBloc
         dense(s, M, e, e, att, e, b.out_w, b.out_s, b.out_b, x, e, EPI_RESID, x, e);
 }
 
+// The column blocks run as the fused kernel (k_cell_block, a workgroup per 128 rows of a feature) from this many
+// rows: below, its workgroups run part-empty and each streams the block's weights for a few cells (one row 0.645 ->
+// 0.706 ms a prediction, 64 rows 1.080 -> 1.088; 256 rows 1.287 -> 1.268).
+constexpr int CELL_BLOCK_MIN = 128;
+
 // One column block (cached_block with a2) for all cells in place: n rows x groups, cell (r, g) at row r * sr + g * sg
 // of cells; K/V of group g at kvbase + g * gstride.
 void column_block(hipStream_t s, const tah_weights *w, const DevBlock &b, float *cells, int n, int groups, size_t sr,
@@ -829,7 +878,7 @@ void column_block(hipStream_t s, const tah_weights *w, const DevBlock &b, float 
                   float *mid) {
     const int e = w->e;
     const int M = n * groups;
-    if (cell_block_fits(b) && w->inds == 128 && cell_block_work_bytes(groups) <= att_bytes) {
+    if (cell_block_fits(b) && w->inds == 128 && n >= CELL_BLOCK_MIN && cell_block_work_bytes(groups) <= att_bytes) {
         // the attention half in one kernel, and the feed-forward half in it too where the fused kernel takes the
         // shape; the query and attention buffers are not needed, att holds the images
         const bool ff = block_ff_fits(b) && M > SMALL_ROWS;
@@ -864,11 +913,25 @@ void column_block(hipStream_t s, const tah_weights *w, const DevBlock &b, float 
     feed_forward(s, M, cells, b, t, mid);
 }
 
+static bool column_fused(const tah_weights *w, int n) {
+    bool fused = w->inds == 128 && !w->col_a2.empty() && n >= CELL_BLOCK_MIN;
+    for (auto &b : w->col_a2) fused = fused && cell_block_fits(b);
+    return fused;
+}
+
+// The column stage's attention buffer: M e floats, or, where the blocks run as the fused kernel, its images of the
+// groups' inducing keys and values (cell_block_work_bytes) where those are larger (below 257 rows at 100 features).
+static size_t column_att_floats(const tah_weights *w, int n, int features) {
+    const size_t M = (size_t)n * features;
+    if (!column_fused(w, n)) return M * w->e;
+    return std::max(M * w->e, (cell_block_work_bytes(features) + sizeof(float) - 1) / sizeof(float));
+}
+
 size_t column_stage_floats(const tah_weights *w, int n, int features, int digits) {
     int ff = 0;
     for (auto &b : w->col_a2) ff = std::max(ff, b.ff);
     const size_t M = (size_t)n * features;
-    return M * (4 * (size_t)w->e + ff) + (digits > 1 ? 2 * M * w->e : 0);
+    return M * (3 * (size_t)w->e + ff) + column_att_floats(w, n, features) + (digits > 1 ? 2 * M * w->e : 0);
 }
 
 // The column stage at prediction for n rows x [n][features] (device): cells [n * features][e] after the stage.
@@ -879,7 +942,7 @@ void column_stage(hipStream_t s, const tah_weights *w, const float *col_kv, int 
     int ff = 0;
     for (auto &b : w->col_a2) ff = std::max(ff, b.ff);
     const size_t M = (size_t)n * features;
-    const size_t natt = M * e;
+    const size_t natt = column_att_floats(w, n, features);
     float *t = scratch, *q = t + M * e, *att = q + M * e, *mid = att + natt;
     float *plain = mid + M * ff, *sum = plain + M * e;
     const size_t per = 2 * (size_t)e * w->inds, gstride = (size_t)digits * nb * per;
@@ -905,6 +968,42 @@ void column_stage(hipStream_t s, const tah_weights *w, const float *col_kv, int 
     TAH_LAUNCHED();
 }
 
+bool column_tokens_fits(const tah_weights *w, int n, int features, int digits) {
+    if (digits != 1 || !column_fused(w, n) || (size_t)n * features <= (size_t)SMALL_ROWS) return false;
+    for (auto &b : w->col_a2)
+        if (!block_ff_fits(b)) return false;
+    return true;
+}
+
+void column_stage_tokens(hipStream_t s, const tah_weights *w, const float *col_kv, const float *x, int n,
+                         int features, float *tok, float *kv, const float *cls_kv, float *scratch) {
+    if (!column_tokens_fits(w, n, features, 1)) throw ArgError{"column stage: no fused path for this shape"};
+    if (kv && !row_kv_fits(w->row.at(0))) throw ArgError{"column stage: the first row block takes no fused keys"};
+    const int e = w->e, nb = w->col_blocks, cls = w->cls, T = cls + features;
+    const size_t M = (size_t)n * features;
+    float *att = scratch + 2 * M * e;  // column_stage's layout: its attention buffer holds the kernel's images
+    const size_t per = 2 * (size_t)e * w->inds, gstride = (size_t)nb * per;
+    input_cells(s, w, x, n, features, tok, cls, kv, cls_kv);
+    float *cells = tok + (size_t)cls * e;
+    for (int bi = 0; bi < nb; bi++) {
+        const bool last = bi == nb - 1 && kv;
+        cell_block(s, n, features, T, 1, cells, w->col_a2[bi], w->col_scale, col_kv + bi * per, gstride, att, true,
+                   last ? &w->row[0] : nullptr, last ? kv + (size_t)cls * 2 * e : nullptr);
+    }
+}
+
+void class_token_kv(hipStream_t s, const tah_weights *w, float *out, float *tmp) {
+    const DevBlock &b = w->row.at(0);
+    const int e = w->e, cls = w->cls;
+    const float *W = b.in_w + (size_t)e * e;  // the projection's key then value rows ([3 e][e])
+    if (gemm_ln_fits(cls, e, w->cls_tokens, e, W)) {
+        gemm(s, cls, 2 * e, e, w->cls_tokens, e, W, b.in_b + e, out, 2 * e, EPI_NONE, nullptr, 0, b.n1w, b.n1b);
+    } else {
+        layer_norm(s, cls, e, w->cls_tokens, e, b.n1w, b.n1b, tmp, e);
+        gemm(s, cls, 2 * e, e, tmp, e, W, b.in_b + e, out, 2 * e, EPI_NONE, nullptr, 0);
+    }
+}
+
 size_t row_stage_floats(const tah_weights *w, int n, int T) {
     int ff = 0;
     for (auto &b : w->row) ff = std::max(ff, b.ff);
@@ -912,9 +1011,28 @@ size_t row_stage_floats(const tah_weights *w, int n, int T) {
     return R * ((size_t)w->e * 5 + ff) + 2 * (size_t)T * w->rope_half + (size_t)n * w->cls * w->e * 2;
 }
 
+// The row stage's fused kernels: head width 16 with the rotary tables' 8 frequencies, at most 128 tokens (the
+// rotary positions applied inside the attention kernels).
+static bool row_fused(const tah_weights *w, int T) {
+    return w->row_heads > 0 && w->e / w->row_heads == 16 && w->e % w->row_heads == 0 && w->rope_half == 8 && T <= 128;
+}
+
+// Whether row block bi runs as k_row_block (one kernel, a workgroup per row) for n rows of T tokens.
+static bool row_block_path(const tah_weights *w, int bi, int n, int T) {
+    return bi < w->row_blocks - 1 && row_fused(w, T) && row_block_fits(w->row[bi], T) && n >= ROW_BLOCK_MIN;
+}
+
+bool row_stage_takes_kv(const tah_weights *w, int n, int T) {
+    return w->row_blocks >= 2 && row_block_path(w, 0, n, T) && row_kv_fits(w->row[0]);
+}
+
+float *row_stage_kv(const tah_weights *w, int n, int T, float *scratch) { return scratch + (size_t)n * T * w->e; }
+
 // The row stage for n rows: tok [n][T][e] (consumed) to rep [n][cls * e]. cosv/sinv [T][half] on the card.
 void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, const float *cosv, const float *sinv,
-               float *rep, float *scratch) {
+               float *rep, float *scratch, bool kv_ready) {
+    if (kv_ready && !row_stage_takes_kv(w, n, T))
+        throw ArgError{"row stage: the first block's keys and values were formed for a path it does not take"};
     const int e = w->e, heads = w->row_heads, cls = w->cls;
     int ff = 0;
     for (auto &b : w->row) ff = std::max(ff, b.ff);
@@ -926,7 +1044,7 @@ void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, co
     const float inv = 1.0f / sqrtf((float)hd);
     const int last = w->row_blocks - 1;
     const bool mfma = hd == 16 && T <= 256;
-    const bool fused = hd == 16 && half == 8 && T <= 128;  // rotary positions applied inside k_row_attn_x3
+    const bool fused = row_fused(w, T);  // rotary positions applied inside k_row_attn_x3
     // the queries k_row_attn_x3 reads: the projection's [T][3 e] rows, or (the last block) the class tokens' [cls][e]
     const float *q_of = qkv;
     size_t q_row = (size_t)T * 3 * e;
@@ -948,10 +1066,10 @@ void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, co
     // takes the shape
     const bool cls_path = fused && w->row[last].inimg && n >= CLS_QUERIES_MIN;
     const bool cls_kernel = cls_path && cls <= CLS_MAXQ && heads <= 8;
-    bool kv_ready = false;  // the previous row block formed this block's keys and values, qkv [R][2 e]
+    // kv_ready: this block's keys and values are in qkv [R][2 e] already (formed by the block before it)
     for (int bi = 0; bi <= last; bi++) {
         const DevBlock &b = w->row[bi];
-        if (bi < last && fused && row_block_fits(b, T) && n >= ROW_BLOCK_MIN) {
+        if (row_block_path(w, bi, n, T)) {
             // keys and values by the projection (its second and third 128-row blocks, qkv [R][2 e]) unless the
             // previous block formed them, then the attention half of the block in one kernel (and the feed-forward
             // half in it too where the fused kernel takes the shape, and then the next block's keys and values as
@@ -961,8 +1079,7 @@ void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, co
                         EPI_NONE, nullptr, 0, nullptr, b.n1w, b.n1b);
             const bool ff = block_ff_fits(b) && R > SMALL_ROWS;
             const DevBlock &nb = w->row[bi + 1];
-            const bool chain = ff && row_kv_fits(nb) &&
-                               (bi + 1 < last ? row_block_fits(nb, T) : cls_kernel);
+            const bool chain = ff && row_kv_fits(nb) && (bi + 1 < last ? row_block_path(w, bi + 1, n, T) : cls_kernel);
             row_block(s, n, T, tok, qkv, cosv, sinv, b, ff, chain ? &nb : nullptr, qkv);
             kv_ready = chain;
             if (!ff) feed_forward(s, (int)R, tok, b, t, mid);
