@@ -39,7 +39,7 @@ PEAK_SPLIT_F32 = PEAK_F16_MFMA / 3  # f32 work at three fp16 products per f32 pr
 PEAK_HBM = 8.0e12  # MI355X HBM3E bytes/s
 # HBM bytes per launch of the roofline kernel, from rocprofv3 FETCH_SIZE and WRITE_SIZE runs of this bench scaled by
 # the counters' reading on its own 256 MiB copy (profiles/attention_f32_2048x10000_memory.md)
-TRAFFIC_BYTES = 76.6e6
+TRAFFIC_BYTES = 76.3e6
 
 
 def pass_cost(model, n, rows=ROWS, features=FEATURES, kv_bytes=4):
