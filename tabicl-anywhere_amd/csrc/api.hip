@@ -593,6 +593,7 @@ extern "C" void tah_model_free(tah_model *m) {
     (void)hipSetDevice(m->ordinal);
     if (m->records) (void)hipFree(m->records);
     if (m->col_kv) (void)hipFree(m->col_kv);
+    if (m->col_img) (void)hipFree(m->col_img);
     delete m;
 }
 
@@ -968,13 +969,29 @@ extern "C" int tah_model_set_columns(tah_dev *dev, tah_model *model, const tah_w
         const size_t n = (size_t)features * digits * w->col_blocks * 2 * w->e * w->inds;
         if (model->col_kv) {
             (void)hipFree(model->col_kv);
+            model->bytes -= align256((size_t)model->features * model->digits * w->col_blocks * 2 * w->e * w->inds *
+                                     sizeof(float));
             model->col_kv = nullptr;
         }
+        if (model->col_img) {
+            (void)hipFree(model->col_img);
+            model->bytes -= align256(column_images_bytes(w, model->features, model->digits));
+            model->col_img = nullptr;
+        }
+        model->features = model->digits = 0;
         TAH_HIP(hipMalloc(&model->col_kv, n * sizeof(float)));
         TAH_HIP(hipMemcpy(model->col_kv, col_kv, n * sizeof(float), hipMemcpyHostToDevice));
+        model->bytes += align256(n * sizeof(float));
+        // the column blocks' key/value images, made once here instead of at every prediction
+        const size_t ib = column_images_bytes(w, features, digits);
+        if (ib) {
+            TAH_HIP(hipMalloc(&model->col_img, ib));
+            column_images(dev->stream, w, model->col_kv, features, digits, model->col_img);
+            TAH_HIP(hipStreamSynchronize(dev->stream));
+            model->bytes += align256(ib);
+        }
         model->features = features;
         model->digits = digits;
-        model->bytes += align256(n * sizeof(float));
         return TAH_OK;
     });
 }
@@ -1024,7 +1041,7 @@ static void embed_rows(tah_dev *dev, const tah_weights *w, const tah_model *mode
     const int features = model->features;
     float *cells = loans.take<float>((size_t)n * features * w->e);
     float *scratch = loans.take<float>(column_stage_floats(w, n, features, model->digits));
-    column_stage(dev->stream, w, model->col_kv, model->digits, x, n, features, cells, scratch);
+    column_stage(dev->stream, w, model->col_kv, model->digits, x, n, features, cells, scratch, model->col_img);
     assemble_tokens(dev->stream, w, cells, n, features, tok);
 }
 
@@ -1118,7 +1135,7 @@ static void predict_rows(tah_dev *dev, const tah_weights *w, const tah_model *mo
             kv_ready = row_stage_takes_kv(w, k, T);
             column_stage_tokens(dev->stream, w, model->col_kv, xr, k, model->features, tok,
                                 kv_ready ? row_stage_kv(w, k, T, scratch) : nullptr,
-                                kv_ready ? class_kv(dev, w) : nullptr, cs);
+                                kv_ready ? class_kv(dev, w) : nullptr, cs, model->col_img);
         } else {
             embed_rows(dev, w, model, xr, k, tok, loans);
             scratch = loans.take<float>(row_stage_floats(w, k, T));

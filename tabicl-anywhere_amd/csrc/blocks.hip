@@ -1201,9 +1201,18 @@ bool cell_block_fits(const DevBlock &b) {
 
 size_t cell_block_work_bytes(int groups) { return (size_t)groups * 8 * (CIMG + 2 * sizeof(int)); }
 
+void cell_images(hipStream_t s, int groups, const float *kvbase, size_t gstride, void *work) {
+    if (groups <= 0) return;
+    if (reinterpret_cast<uintptr_t>(work) & 15) throw ArgError{"cell_images: the work buffer must be 16-byte aligned"};
+    uint8_t *images = static_cast<uint8_t *>(work);
+    int *shifts = reinterpret_cast<int *>(images + (size_t)groups * 8 * CIMG);
+    hipLaunchKernelGGL(k_cell_images, dim3(groups, 8), dim3(256), 0, s, kvbase, gstride, images, shifts);
+    TAH_LAUNCHED();
+}
+
 void cell_block(hipStream_t s, int n, int groups, size_t sr, size_t sg, float *cells, const DevBlock &b,
                 const float *qscale, const float *kvbase, size_t gstride, void *work, bool ff, const DevBlock *next,
-                float *kv_next) {
+                float *kv_next, bool images_ready) {
     if (n <= 0 || groups <= 0) return;
     if (!cell_block_fits(b) || (reinterpret_cast<uintptr_t>(cells) & 15) || (reinterpret_cast<uintptr_t>(work) & 15))
         throw ArgError{"cell_block: needs e = 128, 8 heads, weight images and 16-byte aligned cells and work"};
@@ -1213,8 +1222,7 @@ void cell_block(hipStream_t s, int n, int groups, size_t sr, size_t sg, float *c
                        "projection image and an aligned destination"};
     uint8_t *images = static_cast<uint8_t *>(work);
     int *shifts = reinterpret_cast<int *>(images + (size_t)groups * 8 * CIMG);
-    hipLaunchKernelGGL(k_cell_images, dim3(groups, 8), dim3(256), 0, s, kvbase, gstride, images, shifts);
-    TAH_LAUNCHED();
+    if (!images_ready) cell_images(s, groups, kvbase, gstride, work);
     const dim3 grid((n + 127) / 128, groups);
     if (next) {
         const KvNext kn{next->inimg + (size_t)128 * 128 * 4, next->ins, next->n1w, next->n1b, next->in_b + 128,

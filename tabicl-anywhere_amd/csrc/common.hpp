@@ -138,6 +138,7 @@ struct tah_model {
     float *scales = nullptr;     // [layers][d]
     size_t bytes = 0;
     float *col_kv = nullptr;     // [features][digits][blocks][2][e][inds] (tah_model_set_columns)
+    uint8_t *col_img = nullptr;  // the column blocks' key/value images of col_kv (column_images), where they apply
     int features = 0, digits = 0;
 };
 
@@ -207,9 +208,13 @@ void row_block(hipStream_t s, int n, int T, float *tok, const float *kv, const f
 size_t cell_block_work_bytes(int groups);
 // With next as well (ff, row_kv_fits) the column block's result goes on to that row block's keys and values: cell
 // (r, g)'s [2 e] at kv_next + (r sr + g sg) 2 e.
+// images_ready: work holds the groups' images already (cell_images of the same kvbase), else they are made first.
 void cell_block(hipStream_t s, int n, int groups, size_t sr, size_t sg, float *cells, const DevBlock &b,
                 const float *qscale, const float *kvbase, size_t gstride, void *work, bool ff,
-                const DevBlock *next = nullptr, float *kv_next = nullptr);
+                const DevBlock *next = nullptr, float *kv_next = nullptr, bool images_ready = false);
+// The groups' key/value images for cell_block (group g's keys and values at kvbase + g gstride) into work
+// (cell_block_work_bytes(groups), 16-byte aligned).
+void cell_images(hipStream_t s, int groups, const float *kvbase, size_t gstride, void *work);
 // Y [M][N] = epi(X' W^T + b) for K = 128 and N a multiple of 128, W as such an image (scaled by 2^shift), X' = X or
 // layer_norm(X) with lnw/lnb; EPI_NONE, EPI_SCALE (by scale [N]) or EPI_RESID (adds R, may alias Y).
 void rows128(hipStream_t s, int M, int N, const float *X, int ldx, const uint8_t *wimg, int wshift, const float *b,
@@ -269,8 +274,13 @@ void quantile_stats(hipStream_t s, int rows, int n, const float *q, int na, cons
 void input_cells(hipStream_t s, const tah_weights *w, const float *x, int n, int features, float *cells, int cls = 0,
                  float *kv = nullptr, const float *cls_kv = nullptr);
 size_t column_stage_floats(const tah_weights *w, int n, int features, int digits);
+// col_images: the model's column images (column_images_bytes, made by column_images), or nullptr (made per call).
 void column_stage(hipStream_t s, const tah_weights *w, const float *col_kv, int digits, const float *x, int n,
-                  int features, float *cells, float *scratch);
+                  int features, float *cells, float *scratch, const uint8_t *col_images = nullptr);
+// The column blocks' key/value images of a fitted column cache, made once per model (where the blocks run as the
+// fused kernel, else 0 bytes): [digits][blocks] of cell_block_work_bytes(features) each.
+size_t column_images_bytes(const tah_weights *w, int features, int digits);
+void column_images(hipStream_t s, const tah_weights *w, const float *col_kv, int features, int digits, uint8_t *out);
 void assemble_tokens(hipStream_t s, const tah_weights *w, const float *cells, int n, int features, float *tok);
 // The column stage written straight into the row stage's tokens tok [n][cls + features][e] (no copy), where every
 // column block runs as one fused kernel (column_tokens_fits: one label digit, the fused shapes); with kv as well
@@ -279,7 +289,8 @@ void assemble_tokens(hipStream_t s, const tah_weights *w, const float *cells, in
 // (class_token_kv). scratch holds column_stage_floats floats.
 bool column_tokens_fits(const tah_weights *w, int n, int features, int digits);
 void column_stage_tokens(hipStream_t s, const tah_weights *w, const float *col_kv, const float *x, int n,
-                         int features, float *tok, float *kv, const float *cls_kv, float *scratch);
+                         int features, float *tok, float *kv, const float *cls_kv, float *scratch,
+                         const uint8_t *col_images = nullptr);
 // The first row block's keys and values of the class tokens, [cls][2 e] into out (tmp: cls e floats).
 void class_token_kv(hipStream_t s, const tah_weights *w, float *out, float *tmp);
 size_t row_stage_floats(const tah_weights *w, int n, int T);
@@ -289,9 +300,10 @@ float *row_stage_kv(const tah_weights *w, int n, int T, float *scratch);
 void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, const float *cosv, const float *sinv,
                float *rep, float *scratch, bool kv_ready = false);
 // att: att_bytes of scratch (the fused kernel needs cell_block_work_bytes(groups) of it, else M e floats)
+// ready: the groups' images for the fused kernel (cell_images of kvbase), or nullptr.
 void column_block(hipStream_t s, const tah_weights *w, const DevBlock &b, float *cells, int n, int groups, size_t sr,
                   size_t sg, const float *kvbase, size_t gstride, float *t, float *q, float *att, size_t att_bytes,
-                  float *mid);
+                  float *mid, const uint8_t *ready = nullptr);
 
 // The column stage of a fit (fit_stages.hip).
 void fit_cells(hipStream_t s, const tah_weights *w, const float *x, int rows, int features, int g0, int gb, float *cells);

@@ -875,14 +875,15 @@ constexpr int CELL_BLOCK_MIN = 128;
 // of cells; K/V of group g at kvbase + g * gstride.
 void column_block(hipStream_t s, const tah_weights *w, const DevBlock &b, float *cells, int n, int groups, size_t sr,
                   size_t sg, const float *kvbase, size_t gstride, float *t, float *q, float *att, size_t att_bytes,
-                  float *mid) {
+                  float *mid, const uint8_t *ready) {
     const int e = w->e;
     const int M = n * groups;
     if (cell_block_fits(b) && w->inds == 128 && n >= CELL_BLOCK_MIN && cell_block_work_bytes(groups) <= att_bytes) {
         // the attention half in one kernel, and the feed-forward half in it too where the fused kernel takes the
         // shape; the query and attention buffers are not needed, att holds the images
         const bool ff = block_ff_fits(b) && M > SMALL_ROWS;
-        cell_block(s, n, groups, sr, sg, cells, b, w->col_scale, kvbase, gstride, att, ff);
+        cell_block(s, n, groups, sr, sg, cells, b, w->col_scale, kvbase, gstride,
+                   ready ? const_cast<uint8_t *>(ready) : static_cast<void *>(att), ff, nullptr, nullptr, ready);
         if (!ff) feed_forward(s, M, cells, b, t, mid);
         return;
     }
@@ -936,8 +937,23 @@ size_t column_stage_floats(const tah_weights *w, int n, int features, int digits
 
 // The column stage at prediction for n rows x [n][features] (device): cells [n * features][e] after the stage.
 // col_kv [features][digits][blocks][2][e][inds] on the card. scratch holds column_stage_floats floats.
+size_t column_images_bytes(const tah_weights *w, int features, int digits) {
+    bool fits = w->inds == 128 && !w->col_a2.empty();
+    for (auto &b : w->col_a2) fits = fits && cell_block_fits(b);
+    return fits ? (size_t)digits * w->col_blocks * cell_block_work_bytes(features) : 0;
+}
+
+void column_images(hipStream_t s, const tah_weights *w, const float *col_kv, int features, int digits, uint8_t *out) {
+    const int nb = w->col_blocks;
+    const size_t per = 2 * (size_t)w->e * w->inds, gstride = (size_t)digits * nb * per;
+    const size_t each = cell_block_work_bytes(features);
+    for (int dg = 0; dg < digits; dg++)
+        for (int bi = 0; bi < nb; bi++)
+            cell_images(s, features, col_kv + ((size_t)dg * nb + bi) * per, gstride, out + ((size_t)dg * nb + bi) * each);
+}
+
 void column_stage(hipStream_t s, const tah_weights *w, const float *col_kv, int digits, const float *x, int n,
-                  int features, float *cells, float *scratch) {
+                  int features, float *cells, float *scratch, const uint8_t *col_images) {
     const int e = w->e, nb = w->col_blocks;
     int ff = 0;
     for (auto &b : w->col_a2) ff = std::max(ff, b.ff);
@@ -946,11 +962,15 @@ void column_stage(hipStream_t s, const tah_weights *w, const float *col_kv, int 
     float *t = scratch, *q = t + M * e, *att = q + M * e, *mid = att + natt;
     float *plain = mid + M * ff, *sum = plain + M * e;
     const size_t per = 2 * (size_t)e * w->inds, gstride = (size_t)digits * nb * per;
+    const size_t each = cell_block_work_bytes(features);
+    auto ready = [&](int dg, int bi) {
+        return col_images ? col_images + ((size_t)dg * nb + bi) * each : nullptr;
+    };
     input_cells(s, w, x, n, features, cells);
     if (digits == 1) {
         for (int bi = 0; bi < nb; bi++)
             column_block(s, w, w->col_a2[bi], cells, n, features, features, 1, col_kv + bi * per, gstride, t, q, att,
-                         natt * sizeof(float), mid);
+                         natt * sizeof(float), mid, ready(0, bi));
         return;
     }
     const size_t count = M * e;
@@ -960,7 +980,7 @@ void column_stage(hipStream_t s, const tah_weights *w, const float *col_kv, int 
         if (dg > 0) TAH_HIP(hipMemcpyAsync(cells, plain, count * sizeof(float), hipMemcpyDeviceToDevice, s));
         for (int bi = 0; bi < nb; bi++)
             column_block(s, w, w->col_a2[bi], cells, n, features, features, 1, col_kv + ((size_t)dg * nb + bi) * per, gstride,
-                         t, q, att, natt * sizeof(float), mid);
+                         t, q, att, natt * sizeof(float), mid, ready(dg, bi));
         hipLaunchKernelGGL(k_accumulate, blocks_for(count), dim3(256), 0, s, count, cells, sum);
         TAH_LAUNCHED();
     }
@@ -976,7 +996,8 @@ bool column_tokens_fits(const tah_weights *w, int n, int features, int digits) {
 }
 
 void column_stage_tokens(hipStream_t s, const tah_weights *w, const float *col_kv, const float *x, int n,
-                         int features, float *tok, float *kv, const float *cls_kv, float *scratch) {
+                         int features, float *tok, float *kv, const float *cls_kv, float *scratch,
+                         const uint8_t *col_images) {
     if (!column_tokens_fits(w, n, features, 1)) throw ArgError{"column stage: no fused path for this shape"};
     if (kv && !row_kv_fits(w->row.at(0))) throw ArgError{"column stage: the first row block takes no fused keys"};
     const int e = w->e, nb = w->col_blocks, cls = w->cls, T = cls + features;
@@ -987,8 +1008,10 @@ void column_stage_tokens(hipStream_t s, const tah_weights *w, const float *col_k
     float *cells = tok + (size_t)cls * e;
     for (int bi = 0; bi < nb; bi++) {
         const bool last = bi == nb - 1 && kv;
-        cell_block(s, n, features, T, 1, cells, w->col_a2[bi], w->col_scale, col_kv + bi * per, gstride, att, true,
-                   last ? &w->row[0] : nullptr, last ? kv + (size_t)cls * 2 * e : nullptr);
+        const uint8_t *ready = col_images ? col_images + (size_t)bi * cell_block_work_bytes(features) : nullptr;
+        cell_block(s, n, features, T, 1, cells, w->col_a2[bi], w->col_scale, col_kv + bi * per, gstride,
+                   ready ? const_cast<uint8_t *>(ready) : static_cast<void *>(att), true, last ? &w->row[0] : nullptr,
+                   last ? kv + (size_t)cls * 2 * e : nullptr, ready != nullptr);
     }
 }
 
