@@ -80,12 +80,15 @@ def test_embed_with_label_digits_and_missing_cells(gpu, tiny_model):
     assert np.abs(got - want).max() < TOL
 
 
-@pytest.mark.parametrize("features,n", [(100, 24), (150, 24), (100, 1), (100, 130), (124, 130)])
+@pytest.mark.parametrize("features,n", [(100, 24), (150, 24), (100, 1), (100, 130), (124, 130), (100, 520),
+                                        (100, 1030)])
 def test_stages_full_size(gpu, full_model, full_weights, features, n):
     """Full-size column stage (3 blocks, 8 x 16 heads, 128 inducing points per group) and row stage (104, 128 or
     154 tokens, RoPE) against the oracle, then all three stages with a stored in-context cache. One row takes the
     single-row routes (the fused column block over its key/value images, the f32 projections and feed-forward);
-    130 rows the fused row block (up to 128 tokens, its largest row)."""
+    from 128 rows the fused column and row blocks, the column stage written into the tokens and each block forming
+    the next one's keys and values (130 rows: up to 128 tokens, the row block's largest row); from 512 rows the last
+    row block's class-token attention; from 1,024 rows the input layer a workgroup per table row."""
     say(f"stages full features={features} n={n}")
     m = full_model
     rng = np.random.default_rng(features + n)
