@@ -225,12 +225,155 @@ __device__ __forceinline__ void qmlp64_lane(const float (&xv)[4][8], int r32, in
         }
 }
 
+// The same query MLP for a workgroup's finished 32-row tile of NH heads, shared out: wavefront 2 h + T forms hidden
+// tile T (32 units) and then output tile T of head h on the matrix cores, and all NT threads take the element-wise
+// work between (GELU, then the modulation and the store), which on one wavefront a head was most of the tail.
+// qt: the tile's query values, [32 rows][ldq] with head h at column 64 h; hs, ys: [NH][32][QMP] of LDS each (the
+// hidden layer, the MLP's output). Same operations per value as qmlp64_lane: the products sum in the same order and
+// each row's powers of two are taken over the same 64 values, so the results are the same bits. The weights, biases
+// and the heads' 64 NH scales come read (qmlp64_read); Y: row 0 of the tile at head 0's first column; rows: the
+// tile's live rows (the others are not stored). Wavefronts 2 NH.. only join the element-wise phases; the caller has
+// made qt visible to the whole workgroup.
+constexpr int QMP = 68;  // row pitch of the hidden layer and output tiles in LDS
+
+// The operands of qmlp64_tile a thread reads, issued by qmlp64_read where their latency can overlap other work.
+template <int CH>
+struct QmlpOps {
+    halfx8 a0h[4], a0l[4], a2h[4], a2l[4];  // the wavefront's tile of W0 and of W2, four 16-column steps
+    float bz[2][8], by[2][8];               // b0 and b2 at the lane's 16 hidden / output columns
+    float4 scv[CH];                         // the scales of the thread's chunks in the modulation
+};
+
+template <int NH, int NT>
+__device__ __forceinline__ QmlpOps<NH * 512 / NT> qmlp64_read(int tid, const uint8_t *w0, const float *b0,
+                                                              const uint8_t *w2, const float *b2, const float *sc) {
+    static_assert(NT >= 128 * NH && (NH * 512) % NT == 0, "two wavefronts a head, whole float4 chunks a thread");
+    constexpr int CH = NH * 512 / NT;  // float4 chunks of the heads' 32 x 64 values a thread
+    const int lane = tid & 63, wave = tid >> 6, r32 = lane & 31, g = lane >> 5, T = wave & 1;
+    QmlpOps<CH> o;
+    if (wave < 2 * NH) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const size_t off = ((size_t)T * 4 + ks) * 2048 + (g * 32 + r32) * 16;
+            o.a0h[ks] = *reinterpret_cast<const halfx8 *>(w0 + off);
+            o.a0l[ks] = *reinterpret_cast<const halfx8 *>(w0 + off + 1024);
+            o.a2h[ks] = *reinterpret_cast<const halfx8 *>(w2 + off);
+            o.a2l[ks] = *reinterpret_cast<const halfx8 *>(w2 + off + 1024);
+        }
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            load8(b0 + 32 * T + 16 * hh + 8 * g, o.bz[hh]);
+            load8(b2 + 32 * T + 16 * hh + 8 * g, o.by[hh]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < CH; i++) {
+        const int c = tid + NT * i;
+        o.scv[i] = *reinterpret_cast<const float4 *>(sc + 64 * (c >> 9) + 4 * (c & 15));
+    }
+    return o;
+}
+
+template <int NH, int NT>
+__device__ __forceinline__ void qmlp64_tile(const float *qt, int ldq, float *hs, float *ys, int tid,
+                                            const QmlpOps<NH * 512 / NT> &o, int s0, int s2, float *Y, int ldy,
+                                            int rows) {
+    constexpr int CH = NH * 512 / NT;
+    const int lane = tid & 63, wave = tid >> 6, r32 = lane & 31, g = lane >> 5;
+    const bool mm = wave < 2 * NH;
+    const int h = mm ? wave >> 1 : 0, T = wave & 1;
+    float *hrow = hs + (h * 32 + r32) * QMP;
+    if (mm) {
+        float xv[4][8];
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) load8(&qt[r32 * ldq + 64 * h + 16 * ks + 8 * g], xv[ks]);
+        float xmax = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+            for (int t = 0; t < 8; t++) xmax = fmaxf(xmax, fabsf(xv[ks][t]));
+        xmax = fmaxf(xmax, __shfl_xor(xmax, 32, 64));
+        const int sx = shift_for_max(xmax);
+        floatx16 acc;
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[v] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            halfx8 xh, xl;
+            split8(xv[ks], ldexpf(1.0f, sx), xh, xl);
+            acc = mfma16x3(o.a0h[ks], o.a0l[ks], xh, xl, acc);
+        }
+        const float u0 = ldexpf(1.0f, -(sx + s0));
+        // hidden unit 32 T + 16 hh + 8 g + t of the lane's row: its pre-activation
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            float z[8];
+#pragma unroll
+            for (int t = 0; t < 8; t++) z[t] = acc[8 * hh + t] * u0 + o.bz[hh][t];
+            *reinterpret_cast<float4 *>(hrow + 32 * T + 16 * hh + 8 * g) = make_float4(z[0], z[1], z[2], z[3]);
+            *reinterpret_cast<float4 *>(hrow + 32 * T + 16 * hh + 8 * g + 4) = make_float4(z[4], z[5], z[6], z[7]);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < CH; i++) {
+        const int c = tid + NT * i;
+        float4 *p = reinterpret_cast<float4 *>(hs + (c >> 4) * QMP + 4 * (c & 15));
+        const float4 z = *p;
+        *p = make_float4(gelu(z.x), gelu(z.y), gelu(z.z), gelu(z.w));
+    }
+    __syncthreads();
+    if (mm) {
+        float hv[4][8];
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) load8(hrow + 16 * ks + 8 * g, hv[ks]);
+        float hmax = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+            for (int t = 0; t < 8; t++) hmax = fmaxf(hmax, fabsf(hv[ks][t]));
+        hmax = fmaxf(hmax, __shfl_xor(hmax, 32, 64));
+        const int sh = shift_for_max(hmax);
+        floatx16 acc;
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[v] = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            halfx8 hh8, hl8;
+            split8(hv[ks], ldexpf(1.0f, sh), hh8, hl8);
+            acc = mfma16x3(o.a2h[ks], o.a2l[ks], hh8, hl8, acc);
+        }
+        const float u2 = ldexpf(1.0f, -(sh + s2));
+        float *yrow = ys + (h * 32 + r32) * QMP + 32 * T + 8 * g;
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            float y[8];
+#pragma unroll
+            for (int t = 0; t < 8; t++) y[t] = acc[8 * hh + t] * u2 + o.by[hh][t];
+            *reinterpret_cast<float4 *>(yrow + 16 * hh) = make_float4(y[0], y[1], y[2], y[3]);
+            *reinterpret_cast<float4 *>(yrow + 16 * hh + 4) = make_float4(y[4], y[5], y[6], y[7]);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < CH; i++) {
+        const int c = tid + NT * i, hr = c >> 4, hd = hr >> 5, r = hr & 31, c4 = 4 * (c & 15);
+        if (r >= rows) continue;
+        const float4 y = *reinterpret_cast<const float4 *>(ys + hr * QMP + c4);
+        const float4 q = *reinterpret_cast<const float4 *>(qt + r * ldq + 64 * hd + c4);
+        const float4 s = o.scv[i];
+        *reinterpret_cast<float4 *>(Y + (size_t)r * ldy + 64 * hd + c4) =
+            make_float4(q.x * (s.x * (1.0f + tanh1(y.x))), q.y * (s.y * (1.0f + tanh1(y.y))),
+                        q.z * (s.z * (1.0f + tanh1(y.z))), q.w * (s.w * (1.0f + tanh1(y.w))));
+    }
+}
+
 // Few rows and long rows (the in-context stage: 2,048 queries, K = 512 or 1024): one workgroup per 32 rows x 128
 // columns, its four wavefronts splitting K four ways (each a quarter, in chunks of 128 with their own per-row
 // powers of two), then summing their partial products -- unscaled to f32 -- through LDS; wavefront w finishes
 // tile w. Four times the wavefronts of k_gemm_split on the same grid of outputs, each with a quarter of the
 // dependent chain. With QM (the query projection, 64 or 128 columns = one or two heads of 64), the finished tile
-// goes through LDS and wavefront 0 (and 1) runs the query MLP on one head each (qmlp64_lane): no separate launch.
+// goes through LDS and the workgroup runs the heads' query MLP on it (qmlp64_tile): no separate launch.
 constexpr int SPLITK_MAX_KQ = 512;  // each wavefront's share of K at most (K at most 2048)
 
 template <int EPI, bool LN, int TN, bool QM = false>
@@ -238,8 +381,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
                                                           const uint8_t *__restrict__ wimg, int wshift,
                                                           const float *__restrict__ b, float *Y, int ldy, SplitEpi ea,
                                                           const float *__restrict__ lnw, const float *__restrict__ lnb) {
-    __shared__ float red[4][TN][16][64];  // [wavefront][tile][accumulator][lane]
-    __shared__ float rsum[4][32];        // LN: per-wavefront partial row sums
+    __shared__ __align__(16) float red[4][TN][16][64];  // [wavefront][tile][accumulator][lane]
+    __shared__ float rsum[4][32];                       // LN: per-wavefront partial row sums
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r32 = lane & 31, g = lane >> 5;
     // one dimension of (N / 32 TN) x ceil(M / 32) workgroups; consecutive workgroups go to the eight XCDs in turn, so
@@ -356,13 +499,17 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
             for (int T = 0; T < TN; T++) acc[T] = mfma16x3(wb[j % 3][T][0], wb[j % 3][T][1], xh, xl, acc[T]);
         }
     }
+    // with QM, the query MLP's operands are read now, their latency behind the partial sums' reduction
+    QmlpOps<(TN / 2) * 512 / 256> qo;
+    if constexpr (QM)
+        qo = qmlp64_read<TN / 2, 256>(tid, ea.w0, ea.b0, ea.w2, ea.b2, ea.scale + 64 * (TN / 2) * bxt);
     const float u = ldexpf(1.0f, -(wshift + eprev));
 #pragma unroll
     for (int T = 0; T < TN; T++)
 #pragma unroll
         for (int v = 0; v < 16; v++) red[wave][T][v][lane] = acc[T][v] * u;
     __syncthreads();
-    if (QM) {
+    if constexpr (QM) {
         static_assert(TN == 4 || TN == 2, "the fused query MLP takes whole heads (64 columns) per workgroup");
         constexpr int LD = 32 * TN + 4;  // the tile's row pitch in LDS
         // wavefront w: tile w of four (rows r32, columns 32 w + 16 hh + 8 g + t of the workgroup's), or half w % 2 of
@@ -389,15 +536,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
             for (int t = 0; t < 8; t++) qt[r32 * LD + 32 * T + 16 * hh + 8 * g + t] = yq[hh][t];
         }
         __syncthreads();
-        if (wave >= TN / 2) return;
-        float xv[4][8];
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++)
-#pragma unroll
-            for (int t = 0; t < 8; t++) xv[ks][t] = qt[r32 * LD + 64 * wave + 16 * ks + 8 * g + t];
-        const int head = TN / 2 * bxt + wave;
-        qmlp64_lane(xv, r32, g, ea.w0, ea.s0, ea.b0, ea.w2, ea.s2, ea.b2, ea.scale + 64 * head,
-                    live ? Y + (size_t)m * ldy + 64 * head : nullptr);
+        // the hidden layer and the MLP's output after the tile, in the partial sums' LDS
+        static_assert(32 * LD + 2 * (TN / 2) * 32 * QMP <= 4 * TN * 16 * 64, "the query MLP's tiles fit in LDS");
+        float *hs = qt + 32 * LD;
+        const int m0 = tile / gx * 32;
+        qmlp64_tile<TN / 2, 256>(qt, LD, hs, hs + (TN / 2) * 32 * QMP, tid, qo, ea.s0, ea.s2,
+                                 Y + (size_t)m0 * ldy + 64 * (TN / 2) * bxt, ldy, min(32, M - m0));
         return;
     }
     if (!live) return;
@@ -444,7 +588,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
 // scales (both staged in LDS) -- so that one memory latency precedes the products. The partial products, unscaled to f32, are summed
 // through LDS in wavefront order; wavefront w finishes accumulators 2 w and 2 w + 1 of every tile (two adjacent
 // columns of the lane's row). With QM (one head of 64 columns a workgroup, TN = 2) the finished tile goes through
-// LDS to wavefront 0, which runs the head's query MLP (qmlp64_lane) from the staged weights.
+// LDS and the workgroup runs the head's query MLP on it (qmlp64_tile) from the staged weights.
 constexpr int FEW_WAVES = 8;
 constexpr int FEW_ROWS = 256;
 // up to this many rows the f32 kernels (k_gemv, k_qmlp_rows) take the dense layers: their work grows with the rows,
@@ -460,7 +604,7 @@ __global__ __launch_bounds__(512) void k_dense_few(int M, const float *__restric
     static_assert(!QM || (TN == 2 && LN && EPI == EPI_NONE), "the query MLP follows the normed query projection");
     static_assert(!LN || NST == 4, "the fused layer norm takes K = 512, one column a thread");
     constexpr int K = 16 * NST * FEW_WAVES, KS = K / 16;
-    __shared__ float2 red[FEW_WAVES][TN][8][64];  // [wavefront][tile][accumulator pair][lane]
+    __shared__ __align__(16) float2 red[FEW_WAVES][TN][8][64];  // [wavefront][tile][accumulator pair][lane]
     __shared__ float rsum[FEW_WAVES][32];
     __shared__ float lns[LN ? 2 * K : 1];
     __shared__ __align__(16) uint8_t qimg[QM ? 2 * 8 * 2048 : 16];
@@ -611,13 +755,13 @@ __global__ __launch_bounds__(512) void k_dense_few(int M, const float *__restric
         }
     }
     if (QM) {
-        __syncthreads();
-        if (wave != 0) return;
-        float xq[4][8];
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) load8(&qt[r32 * QPITCH + 16 * ks + 8 * g], xq[ks]);
-        qmlp64_lane(xq, r32, g, qimg, ea.s0, qvec, qimg + 8 * 2048, ea.s2, qvec + 64, qvec + 128,
-                    live ? Y + (size_t)m * ldy + 64 * blockIdx.x : nullptr);
+        __syncthreads();  // the tile is whole and the partial sums are all read: their LDS takes the MLP's tiles
+        static_assert(2 * 32 * QMP * 4 <= sizeof(red), "the query MLP's tiles fit in LDS");
+        float *hs = reinterpret_cast<float *>(&red[0][0][0][0]);
+        const int m0 = blockIdx.y * 32;
+        const QmlpOps<1> qo = qmlp64_read<1, 512>(tid, qimg, qvec, qimg + 8 * 2048, qvec + 64, qvec + 128);
+        qmlp64_tile<1, 512>(qt, QPITCH, hs, hs + 32 * QMP, tid, qo, ea.s0, ea.s2, Y + (size_t)m0 * ldy + 64 * blockIdx.x,
+                            ldy, min(32, M - m0));
     }
 }
 
@@ -797,6 +941,9 @@ static void launch_splitk4(hipStream_t s, int M, int N, int K, const float *X, i
         launch_splitk4_tiles<LN, 4>(s, M, N, K, X, ldx, img, shift, b, Y, ldy, epi, ea, lnw, lnb);
 }
 
+// the query projection's one-head-a-workgroup grid up to this many workgroups: the card's compute units
+constexpr long QUERY_ONE_HEAD_TILES = 256;
+
 bool query_split_fits(const DevBlock &b, int M, const float *X, int ldx, const float *Y) {
     const SplitW &w = b.in_s;
     return M > GEMV_SPLIT_ROWS && w.img && b.in_b && w.row0 == 0 && w.K == b.d && b.d == 512 && b.d % 128 == 0 && b.heads > 0 &&
@@ -821,10 +968,16 @@ void query_split(hipStream_t s, int M, const float *X, int ldx, const DevBlock &
         TAH_LAUNCHED();
         return;
     }
-    // a workgroup per head: against one per two heads, twice the workgroups each stream half the weights and
-    // finish their heads' query MLPs in parallel (64 rows 1.338 -> 1.316 ms a prediction, 2,048 rows 4.618 -> 4.604)
-    hipLaunchKernelGGL((k_gemm_splitk4<EPI_NONE, true, 2, true>), dim3((d / 64) * ((M + 31) / 32)), dim3(256), 0, s, M,
-                       d, d, X, ldx, b.in_s.img, b.in_s.shift, b.in_b, q, d, ea, b.n1w, b.n1b);
+    // a workgroup per head while that grid fits one workgroup a compute unit (twice the workgroups, each streaming
+    // half the weights: 1,024 rows 10.3 against 12.9 us), two heads a workgroup beyond (1,536 rows 13.1 against 14.6
+    // us, 2,048 rows 13.6 against 15.2, 10,000 rows 48.2 against 57.7)
+    const long tiles = (long)(d / 64) * ((M + 31) / 32);
+    if (tiles <= QUERY_ONE_HEAD_TILES)
+        hipLaunchKernelGGL((k_gemm_splitk4<EPI_NONE, true, 2, true>), dim3(tiles), dim3(256), 0, s, M, d, d, X, ldx,
+                           b.in_s.img, b.in_s.shift, b.in_b, q, d, ea, b.n1w, b.n1b);
+    else
+        hipLaunchKernelGGL((k_gemm_splitk4<EPI_NONE, true, 4, true>), dim3(tiles / 2), dim3(256), 0, s, M, d, d, X,
+                           ldx, b.in_s.img, b.in_s.shift, b.in_b, q, d, ea, b.n1w, b.n1b);
     TAH_LAUNCHED();
 }
 
