@@ -512,6 +512,37 @@ __global__ __launch_bounds__(256) void k_cell_images(const float *__restrict__ k
     }
 }
 
+// The input layer's value of one cell at coordinates c0 .. c0 + 7 (InCells with IN_GROUP values a group; the
+// products summed over the group in order, then the bias, as k_input_cells forms them): vals are the cell's group
+// values, missing whether all are -100.
+constexpr int IN_GROUP = 3;
+__device__ __forceinline__ void in_cell_vals(const InCells &ic, int r, int f, float (&vals)[IN_GROUP], bool &missing) {
+    missing = true;
+    const float *xr = ic.x + (size_t)r * ic.features;
+#pragma unroll
+    for (int k = 0; k < IN_GROUP; k++) {
+        vals[k] = xr[(f + (1 << k)) % ic.features];
+        missing = missing && vals[k] == -100.0f;
+    }
+}
+__device__ __forceinline__ void in_cell8(const InCells &ic, const float (&vals)[IN_GROUP], bool missing, int c0,
+                                         float (&out)[8]) {
+    float wv[8 * IN_GROUP], bv[8];
+#pragma unroll
+    for (int i = 0; i < 2 * IN_GROUP; i++) {
+        const float4 t = *reinterpret_cast<const float4 *>(ic.in_w + (size_t)c0 * IN_GROUP + 4 * i);
+        wv[4 * i] = t.x; wv[4 * i + 1] = t.y; wv[4 * i + 2] = t.z; wv[4 * i + 3] = t.w;
+    }
+    load8(ic.in_b + c0, bv);
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+        float a = 0.0f;
+#pragma unroll
+        for (int k = 0; k < IN_GROUP; k++) a += wv[t * IN_GROUP + k] * vals[k];
+        out[t] = missing ? -100.0f : a + bv[t];
+    }
+}
+
 // grid (ceil(n / 128), groups); 256 threads; wavefront w owns cells of rows 128 x + 32 w + 0..31 of group blockIdx.y
 // (cell (r, g) at row r sr + g sg of cells), lane l cell l % 32, as the B operand of every product:
 //  * query projection H^T = Wq X^T as in k_rows128 (its accumulators hold, for each head, eight consecutive query
@@ -526,8 +557,9 @@ __global__ __launch_bounds__(256) void k_cell_images(const float *__restrict__ k
 // With FF the block's feed-forward half follows in the same kernel (ff128_rows, its weight slices in the same 64 KB
 // of LDS): the cells' new values stay in registers as its input; they are written out as well, for its residual add.
 // With KV as well the result goes on to the first row block's keys and values (ff128_rows with KV): cell (r, g)'s at
-// kn.out + (r sr + g sg) 2 e.
-template <bool FF, bool KV>
+// kn.out + (r sr + g sg) 2 e. With IN the cells' values are the input layer's (in_cell8, from the table rows ic),
+// formed again for the residual add, and the cells are only written.
+template <bool FF, bool KV, bool IN = false>
 __global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t sg, float *cells,
                                                         const float *__restrict__ n1w, const float *__restrict__ n1b,
                                                         const uint8_t *__restrict__ qimg, int qshift,
@@ -537,7 +569,8 @@ __global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t 
                                                         const float *__restrict__ ob, const float *__restrict__ n2w, const float *__restrict__ n2b,
                                                         const uint8_t *__restrict__ w1img, const float *__restrict__ b1,
                                                         int s1, const uint8_t *__restrict__ w2img,
-                                                        const float *__restrict__ b2, int s2, KvNext kn) {
+                                                        const float *__restrict__ b2, int s2, KvNext kn,
+                                                        InCells ic) {
     static_assert(FF || !KV, "the next block's keys and values come from the feed-forward's registers");
     constexpr int E = 128;
     __shared__ __align__(16) uint8_t lds[65536];
@@ -563,16 +596,24 @@ __global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t 
 
     // this wavefront's cells: layer norm, then split as the B operand (coordinates 16 ks + 8 g + t)
     float xv[8][8];
+    if constexpr (IN) {
+        float vals[IN_GROUP];
+        bool missing;
+        in_cell_vals(ic, live ? r : 0, grp, vals, missing);
 #pragma unroll
-    for (int ks = 0; ks < 8; ks++) {
-        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), c = a;
-        if (live) {
-            const float *src = cells + m * E + 16 * ks + 8 * g;
-            a = *reinterpret_cast<const float4 *>(src);
-            c = *reinterpret_cast<const float4 *>(src + 4);
+        for (int ks = 0; ks < 8; ks++) in_cell8(ic, vals, missing, 16 * ks + 8 * g, xv[ks]);
+    } else {
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), c = a;
+            if (live) {
+                const float *src = cells + m * E + 16 * ks + 8 * g;
+                a = *reinterpret_cast<const float4 *>(src);
+                c = *reinterpret_cast<const float4 *>(src + 4);
+            }
+            xv[ks][0] = a.x; xv[ks][1] = a.y; xv[ks][2] = a.z; xv[ks][3] = a.w;
+            xv[ks][4] = c.x; xv[ks][5] = c.y; xv[ks][6] = c.z; xv[ks][7] = c.w;
         }
-        xv[ks][0] = a.x; xv[ks][1] = a.y; xv[ks][2] = a.z; xv[ks][3] = a.w;
-        xv[ks][4] = c.x; xv[ks][5] = c.y; xv[ks][6] = c.z; xv[ks][7] = c.w;
     }
     {
         float sum = 0.0f;
@@ -767,6 +808,9 @@ __global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t 
     const float u = ldexpf(1.0f, -(so + oshift));
     float *xrow = cells + m * E;
     float xn[8][8];  // the new values as the feed-forward's input: columns 16 ks + 8 g + t
+    float ivals[IN_GROUP];  // IN: the cell's group values again
+    bool imiss = false;
+    if constexpr (IN) in_cell_vals(ic, live ? r : 0, grp, ivals, imiss);
 #pragma unroll
     for (int T = 0; T < 4; T++)
 #pragma unroll
@@ -774,7 +818,10 @@ __global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t 
             const int n0 = 32 * T + 16 * hh + 8 * g;
             float bv[8], xr[8];
             load8(ob + n0, bv);
-            load8(xrow + n0, xr);
+            if constexpr (IN)
+                in_cell8(ic, ivals, imiss, n0, xr);
+            else
+                load8(xrow + n0, xr);
 #pragma unroll
             for (int t = 0; t < 8; t++) xn[2 * T + hh][t] = xr[t] + acc[T][8 * hh + t] * u + bv[t];
             if (live) {
@@ -1199,6 +1246,8 @@ bool cell_block_fits(const DevBlock &b) {
     return b.d == 128 && b.heads == 8 && b.ss_hidden == 0 && b.inimg && b.outimg;
 }
 
+int in_cells_group() { return IN_GROUP; }
+
 size_t cell_block_work_bytes(int groups) { return (size_t)groups * 8 * (CIMG + 2 * sizeof(int)); }
 
 void cell_images(hipStream_t s, int groups, const float *kvbase, size_t gstride, void *work) {
@@ -1212,8 +1261,13 @@ void cell_images(hipStream_t s, int groups, const float *kvbase, size_t gstride,
 
 void cell_block(hipStream_t s, int n, int groups, size_t sr, size_t sg, float *cells, const DevBlock &b,
                 const float *qscale, const float *kvbase, size_t gstride, void *work, bool ff, const DevBlock *next,
-                float *kv_next, bool images_ready) {
+                float *kv_next, bool images_ready, const InCells *in) {
     if (n <= 0 || groups <= 0) return;
+    if (in && (!ff || next || !in->x || !in->in_w || !in->in_b || in->features != groups ||
+               in->group != IN_GROUP || b.d != 128 || (reinterpret_cast<uintptr_t>(in->in_w) & 15) ||
+               (reinterpret_cast<uintptr_t>(in->in_b) & 15)))
+        throw ArgError{"cell_block: the input layer goes into the first block only, with its feed-forward half, "
+                       "three values a group, e = 128, one group a feature and aligned weights"};
     if (!cell_block_fits(b) || (reinterpret_cast<uintptr_t>(cells) & 15) || (reinterpret_cast<uintptr_t>(work) & 15))
         throw ArgError{"cell_block: needs e = 128, 8 heads, weight images and 16-byte aligned cells and work"};
     if (ff && !block_ff_fits(b)) throw ArgError{"cell_block: no fused feed-forward weights for this shape"};
@@ -1229,15 +1283,19 @@ void cell_block(hipStream_t s, int n, int groups, size_t sr, size_t sg, float *c
                         kv_next};
         hipLaunchKernelGGL((k_cell_block<true, true>), grid, dim3(256), 0, s, n, sr, sg, cells, b.n1w, b.n1b, b.inimg,
                            b.ins, b.in_b, qscale, images, shifts, b.outimg, b.outs, b.out_b, b.n2w, b.n2b, b.l1img,
-                           b.l1b, b.l1s, b.l2img, b.l2b, b.l2s, kn);
+                           b.l1b, b.l1s, b.l2img, b.l2b, b.l2s, kn, InCells{});
+    } else if (ff && in) {
+        hipLaunchKernelGGL((k_cell_block<true, false, true>), grid, dim3(256), 0, s, n, sr, sg, cells, b.n1w, b.n1b,
+                           b.inimg, b.ins, b.in_b, qscale, images, shifts, b.outimg, b.outs, b.out_b, b.n2w, b.n2b,
+                           b.l1img, b.l1b, b.l1s, b.l2img, b.l2b, b.l2s, KvNext{}, *in);
     } else if (ff) {
         hipLaunchKernelGGL((k_cell_block<true, false>), grid, dim3(256), 0, s, n, sr, sg, cells, b.n1w, b.n1b, b.inimg,
                            b.ins, b.in_b, qscale, images, shifts, b.outimg, b.outs, b.out_b, b.n2w, b.n2b, b.l1img,
-                           b.l1b, b.l1s, b.l2img, b.l2b, b.l2s, KvNext{});
+                           b.l1b, b.l1s, b.l2img, b.l2b, b.l2s, KvNext{}, InCells{});
     } else {
         hipLaunchKernelGGL((k_cell_block<false, false>), grid, dim3(256), 0, s, n, sr, sg, cells, b.n1w, b.n1b,
                            b.inimg, b.ins, b.in_b, qscale, images, shifts, b.outimg, b.outs, b.out_b, nullptr, nullptr,
-                           nullptr, nullptr, 0, nullptr, nullptr, 0, KvNext{});
+                           nullptr, nullptr, 0, nullptr, nullptr, 0, KvNext{}, InCells{});
     }
     TAH_LAUNCHED();
 }

@@ -206,12 +206,23 @@ bool row_kv_fits(const DevBlock &next);
 void row_block(hipStream_t s, int n, int T, float *tok, const float *kv, const float *cosv, const float *sinv,
                const DevBlock &b, bool ff, const DevBlock *next = nullptr, float *kv_next = nullptr);
 size_t cell_block_work_bytes(int groups);
+// The column stage's input layer as the first column block's input: cell (r, g) = in_w vals + in_b over the row's
+// group values vals[k] = x[r][(g + 2^k) mod features] (k < group), or all -100 where every one of them is -100.
+struct InCells {
+    const float *x;            // the table rows [n][features]
+    const float *in_w, *in_b;  // [e][group], [e]
+    int features, group;
+};
 // With next as well (ff, row_kv_fits) the column block's result goes on to that row block's keys and values: cell
 // (r, g)'s [2 e] at kv_next + (r sr + g sg) 2 e.
 // images_ready: work holds the groups' images already (cell_images of the same kvbase), else they are made first.
+// in (with ff and without next, groups of in_cells_group() values): the cells' values are formed from the table
+// rows (InCells) instead of read; the block writes them whole (groups = features).
+int in_cells_group();
 void cell_block(hipStream_t s, int n, int groups, size_t sr, size_t sg, float *cells, const DevBlock &b,
                 const float *qscale, const float *kvbase, size_t gstride, void *work, bool ff,
-                const DevBlock *next = nullptr, float *kv_next = nullptr, bool images_ready = false);
+                const DevBlock *next = nullptr, float *kv_next = nullptr, bool images_ready = false,
+                const InCells *in = nullptr);
 // The groups' key/value images for cell_block (group g's keys and values at kvbase + g gstride) into work
 // (cell_block_work_bytes(groups), 16-byte aligned).
 void cell_images(hipStream_t s, int groups, const float *kvbase, size_t gstride, void *work);

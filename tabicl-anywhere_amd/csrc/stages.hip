@@ -1004,14 +1004,28 @@ void column_stage_tokens(hipStream_t s, const tah_weights *w, const float *col_k
     const size_t M = (size_t)n * features;
     float *att = scratch + 2 * M * e;  // column_stage's layout: its attention buffer holds the kernel's images
     const size_t per = 2 * (size_t)e * w->inds, gstride = (size_t)nb * per;
-    input_cells(s, w, x, n, features, tok, cls, kv, cls_kv);
+    // the input layer inside the first column block (the cells formed from the table rows there, not written and
+    // read back), unless that block is also the last, which forms the row block's keys and values
+    const bool fused_input = (nb > 1 || !kv) && w->group == in_cells_group();
+    const InCells in{x, w->in_w, w->in_b, features, w->group};
+    if (fused_input) {
+        if (cls < 0 || (kv && (!cls || !cls_kv)))
+            throw ArgError{"column stage: class tokens are the weights' own, and their keys and values need them"};
+        if (cls > 0) {
+            hipLaunchKernelGGL(k_class_tokens, dim3(n), dim3(256), 0, s, n, T, cls, e, w->cls_tokens, tok, cls_kv,
+                               kv);
+            TAH_LAUNCHED();
+        }
+    } else {
+        input_cells(s, w, x, n, features, tok, cls, kv, cls_kv);
+    }
     float *cells = tok + (size_t)cls * e;
     for (int bi = 0; bi < nb; bi++) {
         const bool last = bi == nb - 1 && kv;
         const uint8_t *ready = col_images ? col_images + (size_t)bi * cell_block_work_bytes(features) : nullptr;
         cell_block(s, n, features, T, 1, cells, w->col_a2[bi], w->col_scale, col_kv + bi * per, gstride,
                    ready ? const_cast<uint8_t *>(ready) : static_cast<void *>(att), true, last ? &w->row[0] : nullptr,
-                   last ? kv + (size_t)cls * 2 * e : nullptr, ready != nullptr);
+                   last ? kv + (size_t)cls * 2 * e : nullptr, ready != nullptr, bi == 0 && fused_input ? &in : nullptr);
     }
 }
 
