@@ -665,6 +665,8 @@ static void stage_rows_with(tah_dev *dev, const tah_weights *w, const tah_model 
         const float *scale = model->scales + (size_t)l * d;
         if (query_split_fits(b, nq, h, d, q)) {
             query_split(s, nq, h, d, b, scale, q);
+        } else if (query_rows_fits(b, nq, h, d, q)) {
+            query_rows(s, nq, h, d, b, scale, q);
         } else {
             dense(s, nq, d, d, h, d, b.in_w, b.in_s.rows(0), b.in_b, q, d, EPI_NONE, nullptr, 0, b.n1w, b.n1b, t);
             query_modulate(s, nq, b, scale, q, mid);

@@ -184,6 +184,9 @@ bool qmlp_fused(const DevBlock &b);
 bool query_split_fits(const DevBlock &b, int M, const float *X, int ldx, const float *Y);
 void query_split(hipStream_t s, int M, const float *X, int ldx, const DevBlock &b, const float *scale, float *q);
 void qmlp(hipStream_t s, int rows, const DevBlock &b, const float *scale, float *q);
+// the same for one to three rows (d = 512): a workgroup per head, projection and query MLP in one launch
+bool query_rows_fits(const DevBlock &b, int M, const float *X, int ldx, const float *Y);
+void query_rows(hipStream_t s, int M, const float *X, int ldx, const DevBlock &b, const float *scale, float *q);
 
 // Fused feed-forward sub-block (blocks.hip): x [M][128] += l2(gelu(l1(layer_norm2(x)))) in one kernel, the hidden
 // layer kept in registers; for blocks of width 128 and hidden width 256 (ff_fused_shape), else the caller runs

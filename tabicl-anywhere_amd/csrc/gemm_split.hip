@@ -849,6 +849,128 @@ __global__ __launch_bounds__(512) void k_qmlp_rows(int heads, float *__restrict_
     if (live) qr[lane] = x * (scale[h * 64 + lane] * (1.0f + tanh1(o)));
 }
 
+// The query of one to QROWS rows in one launch (src/nn.rs:130-152: layer_norm1, the query projection, the query MLP
+// and the modulation), a workgroup per head of 64 columns, d = 512, in plain f32. Thread t forms column t / 16's
+// partial dot product over the K columns 4 (t % 16 + 16 i) .. + 3, i < 8; every global read of the workgroup -- its 64 weight
+// rows (128 KB), the MLP's two matrices, the biases and scales -- is issued at its start, so that one memory latency
+// precedes the sums, where the projection and the MLP as two launches took two (the MLP's on one workgroup). The
+// rows are normalised once in LDS; the 16 partials of a column, or of a hidden or output unit of the MLP, are summed
+// across their 16 lanes.
+constexpr int QROWS = 3;
+__global__ __launch_bounds__(1024) void k_query_rows(int M, const float *__restrict__ X, int ldx,
+                                                     const float *__restrict__ W, const float *__restrict__ bq,
+                                                     const float *__restrict__ n1w, const float *__restrict__ n1b,
+                                                     const float *__restrict__ w0, const float *__restrict__ b0,
+                                                     const float *__restrict__ w2, const float *__restrict__ b2,
+                                                     const float *__restrict__ scale, float *__restrict__ Y, int ldy) {
+    constexpr int D = 512;
+    __shared__ __align__(16) float xs[QROWS][D];
+    __shared__ float stat[QROWS][2];
+    __shared__ __align__(16) float qs[QROWS][64], hs[QROWS][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = blockIdx.x, c = tid >> 4, sl = tid & 15;
+    // columns 4 (sl + 16 i) .. + 3 of the weight row, i < 8: each load instruction reads 256 contiguous bytes of a
+    // row per 16 lanes (a thread's 128 contiguous bytes took 15.6 us a launch, 64 rows touched per instruction)
+    float4 wv[8];
+    const float4 *wp = reinterpret_cast<const float4 *>(W + (size_t)(64 * h + c) * D) + sl;
+#pragma unroll
+    for (int i = 0; i < 8; i++) wv[i] = wp[16 * i];
+    // the MLP: thread t's unit j = t / 16 and K slice 4 (t % 16) of both matrices
+    const float4 m0 = *reinterpret_cast<const float4 *>(w0 + c * 64 + 4 * sl);
+    const float4 m2 = *reinterpret_cast<const float4 *>(w2 + c * 64 + 4 * sl);
+    const float bqc = bq[64 * h + c], b0c = b0[c], b2c = b2[c], scc = scale[64 * h + c];
+    // the rows, four values a thread, with their norm weights
+    const bool xt = tid < M * (D / 4);
+    const int xr = tid / (D / 4), xk = 4 * (tid % (D / 4));
+    float4 g4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), c4 = g4;
+    if (xt) {
+        *reinterpret_cast<float4 *>(&xs[xr][xk]) = *reinterpret_cast<const float4 *>(X + (size_t)xr * ldx + xk);
+        g4 = *reinterpret_cast<const float4 *>(n1w + xk);
+        c4 = *reinterpret_cast<const float4 *>(n1b + xk);
+    }
+    __syncthreads();
+    if (wave < M) {
+        // row `wave`: two passes (mean, then biased variance; eps 1e-5)
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < D / 64; i++) sum += xs[wave][lane + 64 * i];
+        const float mean = wave_sum(sum) / (float)D;
+        float sq = 0.0f;
+#pragma unroll
+        for (int i = 0; i < D / 64; i++) {
+            const float dv = xs[wave][lane + 64 * i] - mean;
+            sq += dv * dv;
+        }
+        const float inv = 1.0f / sqrtf(wave_sum(sq) / (float)D + 1e-5f);
+        if (lane == 0) {
+            stat[wave][0] = mean;
+            stat[wave][1] = inv;
+        }
+    }
+    __syncthreads();
+    if (xt) {
+        const float mean = stat[xr][0], inv = stat[xr][1];
+        float4 x = *reinterpret_cast<const float4 *>(&xs[xr][xk]);
+        x.x = (x.x - mean) * inv * g4.x + c4.x;
+        x.y = (x.y - mean) * inv * g4.y + c4.y;
+        x.z = (x.z - mean) * inv * g4.z + c4.z;
+        x.w = (x.w - mean) * inv * g4.w + c4.w;
+        *reinterpret_cast<float4 *>(&xs[xr][xk]) = x;
+    }
+    __syncthreads();
+    // the projection: column c, K slice sl; the slice sums over the 16 lanes of the column
+    auto sum16 = [](float v) {
+#pragma unroll
+        for (int m = 8; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+        return v;
+    };
+#pragma unroll
+    for (int r = 0; r < QROWS; r++) {
+        if (r >= M) break;
+        float a = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4 x = *reinterpret_cast<const float4 *>(&xs[r][4 * sl + 64 * i]);
+            a += (wv[i].x * x.x + wv[i].y * x.y) + (wv[i].z * x.z + wv[i].w * x.w);
+        }
+        a = sum16(a);
+        if (sl == 0) qs[r][c] = a + bqc;
+    }
+    __syncthreads();
+    // hidden unit c of the MLP
+#pragma unroll
+    for (int r = 0; r < QROWS; r++) {
+        if (r >= M) break;
+        const float4 x = *reinterpret_cast<const float4 *>(&qs[r][4 * sl]);
+        const float a = sum16((m0.x * x.x + m0.y * x.y) + (m0.z * x.z + m0.w * x.w));
+        if (sl == 0) hs[r][c] = gelu(a + b0c);
+    }
+    __syncthreads();
+    // output c of the MLP, then the modulation of query coordinate c
+#pragma unroll
+    for (int r = 0; r < QROWS; r++) {
+        if (r >= M) break;
+        const float4 x = *reinterpret_cast<const float4 *>(&hs[r][4 * sl]);
+        const float o = sum16((m2.x * x.x + m2.y * x.y) + (m2.z * x.z + m2.w * x.w)) + b2c;
+        if (sl == 0) Y[(size_t)r * ldy + 64 * h + c] = qs[r][c] * (scc * (1.0f + tanh1(o)));
+    }
+}
+
+bool query_rows_fits(const DevBlock &b, int M, const float *X, int ldx, const float *Y) {
+    return M >= 1 && M <= QROWS && b.d == 512 && b.heads == 8 && qmlp_fused(b) && b.in_w && b.in_b && b.n1w && b.n1b &&
+           b.q0w && b.q0b && b.q2w && b.q2b && ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(b.in_w) & 15) == 0 && (reinterpret_cast<uintptr_t>(b.q0w) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(b.q2w) & 15) == 0 && (reinterpret_cast<uintptr_t>(b.n1w) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(b.n1b) & 15) == 0 && Y != nullptr;
+}
+
+void query_rows(hipStream_t s, int M, const float *X, int ldx, const DevBlock &b, const float *scale, float *q) {
+    if (!query_rows_fits(b, M, X, ldx, q)) throw ArgError{"query_rows: shape not supported"};
+    hipLaunchKernelGGL(k_query_rows, dim3(b.heads), dim3(1024), 0, s, M, X, ldx, b.in_w, b.in_b, b.n1w, b.n1b, b.q0w,
+                       b.q0b, b.q2w, b.q2b, scale, q, b.d);
+    TAH_LAUNCHED();
+}
+
 bool qmlp_fused(const DevBlock &b) {
     return b.heads > 0 && b.d == 64 * b.heads && b.ss_hidden == 64 && b.q0_s.img && b.q2_s.img && b.q0_s.K == 64 &&
            b.q2_s.K == 64 && b.q0_s.N == 64 && b.q2_s.N == 64;

@@ -171,7 +171,7 @@ def test_stage_tiny_matches_oracle_and_reference(gpu, tiny_model, tiny_raw):
 
 
 @pytest.mark.parametrize("kv_format", [abi.KV_F32, abi.KV_I16, abi.KV_I8])
-@pytest.mark.parametrize("nq", [1, 3, 4, 7, 8, 20, 64, 200, 600])
+@pytest.mark.parametrize("nq", [1, 2, 3, 4, 7, 8, 20, 64, 200, 600])
 def test_stage_full_size(gpu, full_model, full_weights, kv_format, nq):
     """The whole in-context stage (12 layers of 8 x 64 heads, d = 512, then the decoder) over a stored cache of
     2,000 rows, against the oracle on the same inputs."""
