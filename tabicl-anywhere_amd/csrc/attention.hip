@@ -20,7 +20,7 @@
 //    coordinate for the weighted sum), integer codes scaled through the query and the sums.
 //  * k_attn_decode: any other head width up to 64 (the tiny test models): the same with one wavefront.
 // All of them leave the running maximum in log2 units (score * log2 e) for the split merge (head width 64:
-// k_attn_merge64 for few key ranges, k_attn_merge_many for many; k_attn_merge otherwise).
+// k_attn_merge64 for few key ranges, k_attn_merge_w for many; k_attn_merge otherwise).
 #include <algorithm>
 
 #include <atomic>
@@ -1025,66 +1025,45 @@ __global__ __launch_bounds__(256) void k_attn_merge64(int items, int heads, int 
     *reinterpret_cast<float4 *>(out + ((size_t)qr * heads + h) * 64 + c4) = make_float4(O.x / L, O.y / L, O.z / L, O.w / L);
 }
 
-// Head width 64, maxima in log2 units, many splits (the few-query kernel's short key ranges): one workgroup of
-// 1024 threads per (query, head), lane = coordinate. Wavefront w takes splits w, w + 16, ..., MW_PER of them a pass
-// with every load issued before any is used, and sums them against its own running maximum; the 16 wavefronts'
-// sums are then rescaled to the largest maximum through LDS. One memory latency per pass rather than one per split.
-constexpr int MW_WAVES = 16, MW_PER = 16;
-__global__ __launch_bounds__(1024) void k_attn_merge_many(int items, int splits, const float *__restrict__ part_o,
-                                                          const float *__restrict__ part_ml, float *__restrict__ out) {
-    __shared__ float wo[MW_WAVES][64], wml[MW_WAVES][2];
-    const int i = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// Split merge for head width 64 and many key ranges: a wavefront per (query, head), four a workgroup, lane =
+// coordinate; its ranges in passes of MWW with every load of a pass issued before the sums, no LDS (64 queries x 8
+// heads over 32 ranges: 3.9 us, where a 1,024-thread workgroup per (query, head) combining its wavefronts through
+// LDS took 7.6 us).
+constexpr int MWW = 16;
+__global__ __launch_bounds__(256) void k_attn_merge_w(int items, int splits, const float *__restrict__ part_o,
+                                                      const float *__restrict__ part_ml, float *__restrict__ out) {
+    const int lane = threadIdx.x & 63;
+    const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (i >= items) return;
     const size_t stride = (size_t)items;  // between splits, in (query, head) items
     float M = -INFINITY, L = 0.0f, O = 0.0f;
-    for (int s0 = wave; s0 < splits; s0 += MW_WAVES * MW_PER) {
-        float2 ml[MW_PER];
-        float po[MW_PER];
+    for (int s0 = 0; s0 < splits; s0 += MWW) {
+        float2 ml[MWW];
+        float po[MWW];
 #pragma unroll
-        for (int u = 0; u < MW_PER; u++) {
-            const int sp = s0 + u * MW_WAVES;
-            if (sp < splits) {
-                const size_t at = sp * stride + i;
-                ml[u] = *reinterpret_cast<const float2 *>(part_ml + at * 2);
-                po[u] = part_o[at * 64 + lane];
-            } else {
-                ml[u] = make_float2(-INFINITY, 0.0f);
-                po[u] = 0.0f;
-            }
+        for (int u = 0; u < MWW; u++) {
+            // past the last range: its own values reread (in bounds) and given no weight
+            const size_t at = (size_t)min(s0 + u, splits - 1) * stride + i;
+            ml[u] = *reinterpret_cast<const float2 *>(part_ml + at * 2);
+            po[u] = part_o[at * 64 + lane];
+            if (s0 + u >= splits) ml[u] = make_float2(-INFINITY, 0.0f);
         }
         float cm = M;
 #pragma unroll
-        for (int u = 0; u < MW_PER; u++)
+        for (int u = 0; u < MWW; u++)
             if (ml[u].y > 0.0f) cm = fmaxf(cm, ml[u].x);
         const float r = M == -INFINITY ? 0.0f : exp2_hw(M - cm);
         L *= r;
         O *= r;
         M = cm;
 #pragma unroll
-        for (int u = 0; u < MW_PER; u++) {
+        for (int u = 0; u < MWW; u++) {
             const float f = ml[u].y > 0.0f ? exp2_hw(ml[u].x - M) : 0.0f;
             L += ml[u].y * f;
             O += po[u] * f;
         }
     }
-    wo[wave][lane] = O;
-    if (lane == 0) {
-        wml[wave][0] = M;
-        wml[wave][1] = L;
-    }
-    __syncthreads();
-    if (wave) return;
-    float GM = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < MW_WAVES; w++)
-        if (wml[w][1] > 0.0f) GM = fmaxf(GM, wml[w][0]);
-    float GL = 0.0f, GO = 0.0f;
-#pragma unroll
-    for (int w = 0; w < MW_WAVES; w++) {
-        const float f = wml[w][1] > 0.0f ? exp2_hw(wml[w][0] - GM) : 0.0f;
-        GL += wml[w][1] * f;
-        GO += wo[w][lane] * f;
-    }
-    out[(size_t)i * 64 + lane] = GO / GL;
+    out[(size_t)i * 64 + lane] = O / L;
 }
 
 void merge_splits(hipStream_t s, int nq, int d, int heads, int splits, const float *part_o, const float *part_ml,
@@ -1311,9 +1290,9 @@ void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t 
         if (a.d == 64 * a.heads && p.splits <= 16)  // many queries, few splits (else lanes over splits win)
             hipLaunchKernelGGL(k_attn_merge64, dim3((a.nq * a.heads + 15) / 16), dim3(256), 0, s, a.nq * a.heads,
                                a.heads, p.splits, part_o, part_ml, out);
-        else if (a.d == 64 * a.heads && (long)a.nq * a.heads <= 512)  // few items: a workgroup each
-            hipLaunchKernelGGL(k_attn_merge_many, dim3(a.nq * a.heads), dim3(1024), 0, s, a.nq * a.heads, p.splits,
-                               part_o, part_ml, out);
+        else if (a.d == 64 * a.heads)
+            hipLaunchKernelGGL(k_attn_merge_w, dim3((a.nq * a.heads + 3) / 4), dim3(256), 0, s, a.nq * a.heads,
+                               p.splits, part_o, part_ml, out);
         else
             hipLaunchKernelGGL(k_attn_merge, dim3(a.nq * a.heads), dim3(64), 0, s, a.nq, a.d, a.heads, p.splits, 1,
                                part_o, part_ml, out);
