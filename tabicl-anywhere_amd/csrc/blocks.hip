@@ -324,7 +324,9 @@ void ff_block(hipStream_t s, int M, float *x, const DevBlock &b) {
 // operand; the weights, one block of 128 output columns at a time (64 KB: the same image as the feed-forward's,
 // 128-row blocks of 16-column steps), are copied global -> LDS by DMA and shared by the four wavefronts, and each
 // block's four 32-column tiles are formed with sigma32-ordered rows so that the epilogue writes eight consecutive
-// columns per lane. Two workgroups share a compute unit (2 x 64 KB of LDS).
+// columns per lane. Two workgroups share a compute unit (2 x 64 KB of LDS). grid (row tiles of 128, column groups):
+// with few row tiles the column blocks are dealt out over blockIdx.y (each workgroup then splits its rows for its
+// blocks only), so that their weight copies run on different compute units at once rather than one after another.
 template <int EPI, bool LN>
 __global__ __launch_bounds__(256, 2) void k_rows128(int M, int N, const float *__restrict__ X, int ldx,
                                                      const uint8_t *__restrict__ wimg, int wshift,
@@ -337,7 +339,8 @@ __global__ __launch_bounds__(256, 2) void k_rows128(int M, int N, const float *_
     const int r32 = lane & 31, g = lane >> 5;
     const int m = blockIdx.x * 128 + wave * 32 + r32;
     const bool live = m < M;
-    dma_to_lds(wimg, wl, BLK, tid);
+    const int cb0 = blockIdx.y, cbs = gridDim.y;  // this workgroup's column blocks: cb0, cb0 + cbs, ...
+    dma_to_lds(wimg + (size_t)cb0 * BLK, wl, BLK, tid);
 
     float xv[8][8];
 #pragma unroll
@@ -394,7 +397,7 @@ __global__ __launch_bounds__(256, 2) void k_rows128(int M, int N, const float *_
     const float u = ldexpf(1.0f, -(sx + wshift));
     const int arow = sigma32(r32);
 
-    for (int cb = 0; cb < N / 128; cb++) {
+    for (int cb = cb0; cb < N / 128; cb += cbs) {
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();  // block cb of the weights is in LDS
         floatx16 acc[4];
@@ -412,7 +415,7 @@ __global__ __launch_bounds__(256, 2) void k_rows128(int M, int N, const float *_
                 acc[T] = mfma16x3(ah, al, xh[ks], xl[ks], acc[T]);
             }
         __syncthreads();  // everyone is done with block cb
-        if (cb + 1 < N / 128) dma_to_lds(wimg + (size_t)(cb + 1) * BLK, wl, BLK, tid);
+        if (cb + cbs < N / 128) dma_to_lds(wimg + (size_t)(cb + cbs) * BLK, wl, BLK, tid);
         if (!live) continue;
         // column of accumulator v of tile T: 128 cb + 32 T + 16 (v / 8) + 8 g + v % 8
 #pragma unroll
@@ -1307,7 +1310,13 @@ void rows128(hipStream_t s, int M, int N, const float *X, int ldx, const uint8_t
     if (!wimg || N <= 0 || N % 128 || ldx % 4 || ldy % 4 || (reinterpret_cast<uintptr_t>(X) & 15) ||
         (reinterpret_cast<uintptr_t>(Y) & 15))
         throw ArgError{"rows128: needs a weight image, output width a multiple of 128 and 16-byte aligned rows"};
-    const dim3 grid((M + 127) / 128);
+    // column blocks over workgroups while that fills the compute units at most twice over (two workgroups a unit),
+    // and only where the output does not overlap the input (a workgroup's rows are read once, before any block)
+    const int tiles = (M + 127) / 128, blocks = N / 128;
+    const char *xb = reinterpret_cast<const char *>(X), *yb = reinterpret_cast<const char *>(Y);
+    const bool apart = yb >= xb + ((size_t)(M - 1) * ldx + 128) * sizeof(float) ||
+                       xb >= yb + ((size_t)(M - 1) * ldy + N) * sizeof(float);
+    const dim3 grid(tiles, apart && (long)tiles * blocks <= 512 ? blocks : 1);
     const bool ln = lnw != nullptr;
     if (epi == EPI_NONE && ln)
         hipLaunchKernelGGL((k_rows128<EPI_NONE, true>), grid, dim3(256), 0, s, M, N, X, ldx, wimg, wshift, b, Y, ldy, R,
