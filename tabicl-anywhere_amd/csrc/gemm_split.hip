@@ -596,6 +596,11 @@ constexpr int FEW_ROWS = 256;
 constexpr int GEMV_SPLIT_ROWS = 3;
 constexpr int QPITCH = 68;  // row pitch of the query tile in LDS
 
+// 16 bytes a lane from src to dst + 16 lane by DMA (dst wavefront-uniform)
+__device__ __forceinline__ void copy16_to_lds(const float *src, uint8_t *dst) {
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4 *>(src), dst, 16, 0, 0);
+}
+
 template <int EPI, bool LN, int TN, int NST, bool QM>
 __global__ __launch_bounds__(512) void k_dense_few(int M, const float *__restrict__ X, int ldx,
                                                     const uint8_t *__restrict__ wimg, int wshift,
@@ -604,7 +609,12 @@ __global__ __launch_bounds__(512) void k_dense_few(int M, const float *__restric
     static_assert(!QM || (TN == 2 && LN && EPI == EPI_NONE), "the query MLP follows the normed query projection");
     static_assert(!LN || NST == 4, "the fused layer norm takes K = 512, one column a thread");
     constexpr int K = 16 * NST * FEW_WAVES, KS = K / 16;
-    __shared__ __align__(16) float2 red[FEW_WAVES][TN][8][64];  // [wavefront][tile][accumulator pair][lane]
+    // per wavefront: its rows' K slice (32 rows x 4 NST float4, xrow_at's order), then over it the wavefront's partial
+    // sums [tile][accumulator pair][lane] (float2)
+    constexpr int STG = 32 * 64 * NST;  // bytes
+    static_assert(TN * 8 * 64 * 8 <= STG, "a wavefront's partial sums fit its staging");
+    __shared__ __align__(16) uint8_t stage[FEW_WAVES * STG];
+    auto red = [&](int w, int T, int pr) { return reinterpret_cast<float2 *>(stage + w * STG) + (T * 8 + pr) * 64; };
     __shared__ float rsum[FEW_WAVES][32];
     __shared__ float lns[LN ? 2 * K : 1];
     __shared__ __align__(16) uint8_t qimg[QM ? 2 * 8 * 2048 : 16];
@@ -628,10 +638,26 @@ __global__ __launch_bounds__(512) void k_dense_few(int M, const float *__restric
             wh[j][T] = *reinterpret_cast<const halfx8 *>(src);
             wl[j][T] = *reinterpret_cast<const halfx8 *>(src + 1024);
         }
-    float xv[NST][8];
-    const float *xrow = X + (size_t)mr * ldx + k0 + 8 * g;
+    // this wavefront's rows, columns k0 .. k0 + 16 NST - 1, copied into its staging by DMA: copy i, lane l fills
+    // float4 slot 64 i + l, which holds row (64 i + l) / (4 NST), float4 column c ^ (row % 16) of it with c the slot
+    // within the row -- each copy reads whole runs of rows (a lane a row, as the B operand wants them, touched 32 rows
+    // a load: 64 rows 5.9 -> 4.6 us for the output projection), and the B operand's reads, a row a lane, fall on
+    // distinct bank groups
+    {
+        constexpr int F4 = 4 * NST;  // float4 per row
+        const int m0 = blockIdx.y * 32;
+        static_assert(NST == 4 || NST == 8, "16 or 32 float4 a row: the swizzle stays inside the row");
 #pragma unroll
-    for (int j = 0; j < NST; j++) load8(xrow + 16 * j, xv[j]);
+        for (int i = 0; i < 2 * NST; i++) {
+            const int slot = 64 * i + lane, row = slot / F4, c = (slot % F4) ^ (row & 15);
+            const float *src = X + (size_t)min(m0 + row, M - 1) * ldx + k0 + 4 * c;
+            copy16_to_lds(src, stage + wave * STG + 1024 * i);
+        }
+    }
+    auto xrow_at = [&](int j, int hf) {  // row r32, float4 column 4 j + 2 g + hf
+        const int c = 4 * j + 2 * g + hf;
+        return *reinterpret_cast<const float4 *>(stage + wave * STG + 16 * (r32 * 4 * NST + (c ^ (r32 & 15))));
+    };
     // this thread's outputs: accumulators 2 wave, 2 wave + 1 of each tile, i.e. columns nc, nc + 1 of the tile
     const int nc = 16 * (wave >> 2) + 8 * g + 2 * (wave & 3);
     float2 bias[TN], res[TN];
@@ -657,6 +683,17 @@ __global__ __launch_bounds__(512) void k_dense_few(int M, const float *__restric
         qv = *(tid < 64 ? ea.b0 + tid : tid < 128 ? ea.b2 + (tid - 64) : ea.scale + 64 * blockIdx.x + min(tid - 128, 63));
     }
 
+    float xv[NST][8];
+    __builtin_amdgcn_s_waitcnt(0);  // every read of this thread, its rows' copies included, has landed
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();  // and every lane's: the wavefront's staging is whole
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int j = 0; j < NST; j++) {
+        const float4 a = xrow_at(j, 0), c = xrow_at(j, 1);
+        xv[j][0] = a.x; xv[j][1] = a.y; xv[j][2] = a.z; xv[j][3] = a.w;
+        xv[j][4] = c.x; xv[j][5] = c.y; xv[j][6] = c.z; xv[j][7] = c.w;
+    }
     if (LN) {
         // this wavefront holds columns k0 .. k0 + 63 of its 32 rows; the rows' sums go through LDS (two passes:
         // mean, then biased variance; eps 1e-5)
@@ -719,10 +756,11 @@ __global__ __launch_bounds__(512) void k_dense_few(int M, const float *__restric
         for (int T = 0; T < TN; T++) acc[T] = mfma16x3(wh[j][T], wl[j][T], xh, xl, acc[T]);
     }
     const float u = ldexpf(1.0f, -(wshift + e));
+    // (the staging's rows were all read into xv before the products: the partial sums may overwrite them)
 #pragma unroll
     for (int T = 0; T < TN; T++)
 #pragma unroll
-        for (int p = 0; p < 8; p++) red[wave][T][p][lane] = make_float2(acc[T][2 * p] * u, acc[T][2 * p + 1] * u);
+        for (int p = 0; p < 8; p++) red(wave, T, p)[lane] = make_float2(acc[T][2 * p] * u, acc[T][2 * p + 1] * u);
     if (QM) {
 #pragma unroll
         for (int i = 0; i < 4; i++) *reinterpret_cast<u32x4 *>(qimg + 16 * (tid + 512 * i)) = qs[i];
@@ -731,10 +769,10 @@ __global__ __launch_bounds__(512) void k_dense_few(int M, const float *__restric
     __syncthreads();
 #pragma unroll
     for (int T = 0; T < TN; T++) {
-        float2 s = red[0][T][wave][lane];
+        float2 s = red(0, T, wave)[lane];
 #pragma unroll
         for (int i = 1; i < FEW_WAVES; i++) {
-            const float2 o = red[i][T][wave][lane];
+            const float2 o = red(i, T, wave)[lane];
             s.x += o.x;
             s.y += o.y;
         }
@@ -756,8 +794,8 @@ __global__ __launch_bounds__(512) void k_dense_few(int M, const float *__restric
     }
     if (QM) {
         __syncthreads();  // the tile is whole and the partial sums are all read: their LDS takes the MLP's tiles
-        static_assert(2 * 32 * QMP * 4 <= sizeof(red), "the query MLP's tiles fit in LDS");
-        float *hs = reinterpret_cast<float *>(&red[0][0][0][0]);
+        static_assert(2 * 32 * QMP * 4 <= sizeof(stage), "the query MLP's tiles fit in LDS");
+        float *hs = reinterpret_cast<float *>(stage);
         const int m0 = blockIdx.y * 32;
         const QmlpOps<1> qo = qmlp64_read<1, 512>(tid, qimg, qvec, qimg + 8 * 2048, qvec + 64, qvec + 128);
         qmlp64_tile<1, 512>(qt, QPITCH, hs, hs + 32 * QMP, tid, qo, ea.s0, ea.s2, Y + (size_t)m0 * ldy + 64 * blockIdx.x,
