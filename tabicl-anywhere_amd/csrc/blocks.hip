@@ -309,11 +309,160 @@ __global__ __launch_bounds__(64 * FFW, 2) void k_ff128(int M, float *__restrict_
     ff128_rows(xv, live, x + (size_t)(live ? m : 0) * E, slab, bias1, lnw, lnb, w1img, s1, w2img, b2, s2, tid);
 }
 
+// The same sub-block for few rows (grids of at most one workgroup a compute unit): 64 rows a workgroup, each row
+// group of 32 on two wavefronts that take one half of the 256 hidden units each -- wavefront w rows 32 (2 x + w / 2)
+// .. + 31, hidden units 128 (w % 2) .. + 127 -- so that each wavefront's chain of products and GELU is half as long
+// and twice the compute units share the rows (6,400 rows: 19 us a launch on 100 workgroups, where 50 of 128 rows with one wavefront a row group took 23 us).
+// Both halves' weight slices stream together, two 32 KB slices a step through a two-step ring (128 KB of LDS): step
+// 0 / 1 W1's column halves (K) of both hidden halves, step 2 / 3 W2's columns over each hidden half. The odd
+// wavefront's sums over its half go through LDS to the even one, which adds its own, the bias and the residual.
+__global__ __launch_bounds__(256, 1) void k_ff128h(int M, float *__restrict__ x, const float *__restrict__ lnw,
+                                                   const float *__restrict__ lnb, const uint8_t *__restrict__ w1img,
+                                                   const float *__restrict__ b1, int s1,
+                                                   const uint8_t *__restrict__ w2img, const float *__restrict__ b2,
+                                                   int s2) {
+    constexpr int E = 128, STEP = 2 * SLAB;
+    static_assert(NSL == 2 && 2 * 32 * 2 * E * 4 <= STEP, "two slices a step; the half sums fit a step buffer");
+    __shared__ __align__(16) uint8_t ring[2 * STEP];
+    __shared__ __align__(16) float bias1[256];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r32 = lane & 31, g = lane >> 5;
+    const int rg = wave >> 1, hf = wave & 1;
+    const int m = blockIdx.x * 64 + rg * 32 + r32;
+    const bool live = m < M;
+    // step t's two slices: W1 (t < 2) block h, K half t: slice 2 h + t; W2 (t >= 2) K steps of hidden half h,
+    // K half t - 2: slice 2 NSL + 2 h + (t - 2); half h's slice lands at h * SLAB of the step's buffer
+    auto step_copy = [&](int t) {
+        uint8_t *dst = ring + (t & 1) * STEP;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint8_t *src = t < 2 ? w1img + (size_t)(2 * h + t) * SLAB : w2img + (size_t)(2 * h + t - 2) * SLAB;
+            dma_to_lds<256>(src, dst + h * SLAB, SLAB, tid);
+        }
+    };
+    step_copy(0);
+    if (tid < 64) reinterpret_cast<float4 *>(bias1)[tid] = reinterpret_cast<const float4 *>(b1)[tid];
+    float xv[8][8];
+    float *xrow = x + (size_t)(live ? m : 0) * E;
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) {
+        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), c = a;
+        if (live) {
+            a = *reinterpret_cast<const float4 *>(xrow + 16 * ks + 8 * g);
+            c = *reinterpret_cast<const float4 *>(xrow + 16 * ks + 8 * g + 4);
+        }
+        xv[ks][0] = a.x; xv[ks][1] = a.y; xv[ks][2] = a.z; xv[ks][3] = a.w;
+        xv[ks][4] = c.x; xv[ks][5] = c.y; xv[ks][6] = c.z; xv[ks][7] = c.w;
+    }
+    halfx8 xh[8], xl[8];
+    const int sx = norm_split(xv, lnw, lnb, g, xh, xl);
+    const int arow = sigma32(r32);
+    // wait for step t (and free step t - 1's buffer), start step t + 1's copies; this wavefront's slice of step t
+    auto next = [&](int t) {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (t + 1 < 4) step_copy(t + 1);
+        return static_cast<const uint8_t *>(ring + (t & 1) * STEP + hf * SLAB);
+    };
+    auto mma = [&](floatx16 (&acc)[4], const uint8_t *sl, const halfx8 *bh, const halfx8 *bl, int rows) {
+#pragma unroll
+        for (int c = 0; c < CPS; c++)
+#pragma unroll
+            for (int T = 0; T < 4; T++) {
+                const int n = 32 * T + arow;
+                const halfx8 ah = *reinterpret_cast<const halfx8 *>(sl + c * 8192 + (g * rows + n) * 16);
+                const halfx8 al = *reinterpret_cast<const halfx8 *>(sl + c * 8192 + ((2 + g) * rows + n) * 16);
+                acc[T] = mfma16x3(ah, al, bh[c], bl[c], acc[T]);
+            }
+    };
+    floatx16 acc[4], y[4];
+#pragma unroll
+    for (int T = 0; T < 4; T++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            acc[T][v] = 0.0f;
+            y[T][v] = 0.0f;
+        }
+    // H^T over this wavefront's hidden half: W1's two column halves
+#pragma unroll
+    for (int t = 0; t < 2; t++) mma(acc, next(t), xh + CPS * t, xl + CPS * t, 128);
+    // bias and GELU (hidden unit of accumulator v of tile T: 128 hf + 32 T + 16 (v / 8) + 8 g + v % 8), then the
+    // half's split at its own power of two
+    const float u1 = ldexpf(1.0f, -(sx + s1));
+    float mx = 0.0f;
+#pragma unroll
+    for (int T = 0; T < 4; T++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            float bv[8];
+            load8(bias1 + 128 * hf + 32 * T + 16 * hh + 8 * g, bv);
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const float hv = gelu(acc[T][8 * hh + t] * u1 + bv[t]);
+                acc[T][8 * hh + t] = hv;
+                mx = fmaxf(mx, fabsf(hv));
+            }
+        }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const int sh = shift_for_max(mx);
+    halfx8 hh8[8], hl8[8];
+#pragma unroll
+    for (int T = 0; T < 4; T++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            float hv[8];
+#pragma unroll
+            for (int t = 0; t < 8; t++) hv[t] = acc[T][8 * hh + t];
+            split8(hv, ldexpf(1.0f, sh), hh8[2 * T + hh], hl8[2 * T + hh]);
+        }
+    // Y^T over this half's hidden units: W2's two K halves of it
+#pragma unroll
+    for (int t = 2; t < 4; t++) mma(y, next(t), hh8 + CPS * (t - 2), hl8 + CPS * (t - 2), E);
+    // the odd wavefront's sums (unscaled) into step 0's buffer (free: every wavefront is past step 2), then the even
+    // one finishes: x += y_even + y_odd + b2 (output column of accumulator v of tile T: 32 T + 16 (v / 8) + 8 g + v % 8)
+    const float u2 = ldexpf(1.0f, -(sh + s2));
+    float *half_sums = reinterpret_cast<float *>(ring) + rg * 32 * 2 * E;  // [32 rows][2 E]: this row group's
+    if (hf) {
+#pragma unroll
+        for (int T = 0; T < 4; T++)
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                float o[8];
+#pragma unroll
+                for (int t = 0; t < 8; t++) o[t] = y[T][8 * hh + t] * u2;
+                float *dst = half_sums + r32 * 2 * E + 32 * T + 16 * hh + 8 * g;
+                *reinterpret_cast<float4 *>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+                *reinterpret_cast<float4 *>(dst + 4) = make_float4(o[4], o[5], o[6], o[7]);
+            }
+    }
+    __syncthreads();
+    if (hf || !live) return;
+#pragma unroll
+    for (int T = 0; T < 4; T++)
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const int c0 = 32 * T + 16 * hh + 8 * g;
+            float rv[8], bv[8], ov[8], xo[8];
+            load8(xrow + c0, rv);
+            load8(b2 + c0, bv);
+            load8(half_sums + r32 * 2 * E + c0, ov);
+#pragma unroll
+            for (int t = 0; t < 8; t++) xo[t] = ((y[T][8 * hh + t] * u2 + ov[t]) + bv[t]) + rv[t];
+            *reinterpret_cast<float4 *>(xrow + c0) = make_float4(xo[0], xo[1], xo[2], xo[3]);
+            *reinterpret_cast<float4 *>(xrow + c0 + 4) = make_float4(xo[4], xo[5], xo[6], xo[7]);
+        }
+}
+
 void ff_block(hipStream_t s, int M, float *x, const DevBlock &b) {
     if (M <= 0) return;
     if (!ff_fused_shape(b.d, b.ff) || !b.l1img || !b.l2img) throw ArgError{"ff_block: no fused weights for this shape"};
-    hipLaunchKernelGGL(k_ff128, dim3((M + 32 * FFW - 1) / (32 * FFW)), dim3(64 * FFW), 0, s, M, x, b.n2w, b.n2b, b.l1img, b.l1b, b.l1s,
-                       b.l2img, b.l2b, b.l2s);
+    // few rows: the hidden-split kernel while its grid fits the compute units once
+    if ((M + 63) / 64 <= 256)
+        hipLaunchKernelGGL(k_ff128h, dim3((M + 63) / 64), dim3(256), 0, s, M, x, b.n2w, b.n2b, b.l1img, b.l1b, b.l1s,
+                           b.l2img, b.l2b, b.l2s);
+    else
+        hipLaunchKernelGGL(k_ff128, dim3((M + 32 * FFW - 1) / (32 * FFW)), dim3(64 * FFW), 0, s, M, x, b.n2w, b.n2b,
+                           b.l1img, b.l1b, b.l1s, b.l2img, b.l2b, b.l2s);
     TAH_LAUNCHED();
 }
 
