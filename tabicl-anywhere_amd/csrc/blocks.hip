@@ -312,7 +312,8 @@ __global__ __launch_bounds__(64 * FFW, 2) void k_ff128(int M, float *__restrict_
 // The same sub-block for few rows (grids of at most one workgroup a compute unit): 64 rows a workgroup, each row
 // group of 32 on two wavefronts that take one half of the 256 hidden units each -- wavefront w rows 32 (2 x + w / 2)
 // .. + 31, hidden units 128 (w % 2) .. + 127 -- so that each wavefront's chain of products and GELU is half as long
-// and twice the compute units share the rows (6,400 rows: 19 us a launch on 100 workgroups, where 50 of 128 rows with one wavefront a row group took 23 us).
+// and twice the compute units share the rows (6,400 rows: 19 us a launch on 100 workgroups, where 50 workgroups of
+// 128 rows with one wavefront a row group took 23 us).
 // Both halves' weight slices stream together, two 32 KB slices a step through a two-step ring (128 KB of LDS): step
 // 0 / 1 W1's column halves (K) of both hidden halves, step 2 / 3 W2's columns over each hidden half. The odd
 // wavefront's sums over its half go through LDS to the even one, which adds its own, the bias and the residual.
