@@ -316,6 +316,63 @@ __global__ __launch_bounds__(256) void k_cell_attn_x3(int n, size_t sr, size_t s
     *reinterpret_cast<float4 *>(dst + 8 + 4 * g) = make_float4(o[4] * f, o[5] * f, o[6] * f, o[7] * f);
 }
 
+// The same for a few rows (at most CELL_FEW_ROWS): a wavefront per (group, head), four a workgroup, lane = keys
+// lane and lane + 64, in plain f32: the head's 16 key and value coordinates of the lane's two keys read once
+// (each a coalesced 256-byte row of the column cache), then per row the scores, a softmax by wavefront reductions
+// and the 16 weighted sums (one row: 10.5 us where k_cell_attn_x3 staged split images for 128-row tiles).
+constexpr int CELL_FEW_ROWS = 3;
+__global__ __launch_bounds__(256) void k_cell_attn_few(int n, int groups, int heads, size_t sr, size_t sg, int e,
+                                                        const float *__restrict__ q, const float *__restrict__ kvbase,
+                                                        size_t gstride, float *__restrict__ out) {
+    constexpr int INDS = 128;
+    const int lane = threadIdx.x & 63;
+    const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (item >= groups * heads) return;
+    const int grp = item / heads, h = item % heads;
+    const float *K = kvbase + (size_t)grp * gstride, *V = K + (size_t)e * INDS;
+    float k0[16], k1[16], v0[16], v1[16];
+#pragma unroll
+    for (int c = 0; c < 16; c++) {
+        const size_t row = (size_t)(h * 16 + c) * INDS;
+        k0[c] = K[row + lane];
+        k1[c] = K[row + lane + 64];
+        v0[c] = V[row + lane];
+        v1[c] = V[row + lane + 64];
+    }
+    for (int r = 0; r < n; r++) {
+        const size_t m = (size_t)r * sr + (size_t)grp * sg;
+        const float *qr = q + m * e + h * 16;
+        float qv[16];
+#pragma unroll
+        for (int c = 0; c < 16; c += 4) {
+            const float4 x = *reinterpret_cast<const float4 *>(qr + c);
+            qv[c] = x.x;
+            qv[c + 1] = x.y;
+            qv[c + 2] = x.z;
+            qv[c + 3] = x.w;
+        }
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 16; c++) {
+            s0 += qv[c] * k0[c];
+            s1 += qv[c] * k1[c];
+        }
+        const float mx = wave_max(fmaxf(s0, s1));
+        const float p0 = fast_exp(s0 - mx), p1 = fast_exp(s1 - mx);
+        const float l = wave_sum(p0 + p1);
+        float o[16];
+#pragma unroll
+        for (int c = 0; c < 16; c++) o[c] = wave_sum(p0 * v0[c] + p1 * v1[c]);
+        if (lane < 16) {
+            float oc = o[0];
+#pragma unroll
+            for (int c = 1; c < 16; c++)
+                if (lane == c) oc = o[c];
+            out[m * e + h * 16 + lane] = oc / l;
+        }
+    }
+}
+
 // Any head width and key count (the tiny test models): one thread per (cell, head).
 __global__ __launch_bounds__(256) void k_cell_attn_plain(int n, int groups, size_t sr, size_t sg, int e, int heads,
                                                           int inds, const float *__restrict__ q,
@@ -901,7 +958,10 @@ void column_block(hipStream_t s, const tah_weights *w, const DevBlock &b, float 
     }
     const int hd = e / b.heads;
     const dim3 grid((n + 63) / 64, b.heads, groups);
-    if (hd == 16 && w->inds == 128)
+    if (hd == 16 && w->inds == 128 && n <= CELL_FEW_ROWS && (e % 4) == 0)
+        hipLaunchKernelGGL(k_cell_attn_few, dim3((groups * b.heads + 3) / 4), dim3(256), 0, s, n, groups, b.heads, sr, sg,
+                           e, q, kvbase, gstride, att);
+    else if (hd == 16 && w->inds == 128)
         hipLaunchKernelGGL(k_cell_attn_x3, dim3((n + 127) / 128, b.heads, groups), dim3(256), 0, s, n, sr, sg, e, q,
                            kvbase, gstride, att);
     else if (hd == 16 && w->inds == 256)
