@@ -121,6 +121,10 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(int M, int N, int K, const fl
 // k_layer_norm; 16 threads a row), and the products read them from there: the separate layer-norm launch, which at
 // these sizes costs as much as the product, goes away.
 constexpr int SKINNY_LN_K = 1024;  // widest rows the fused layer norm takes
+// most rows the 16 x 16 tile kernel takes (the column and row stages' width-128 layers of up to 16 table rows: 3 rows
+// 0.817 -> 0.707 ms a prediction, 8 rows 0.826 -> 0.753, 16 rows 0.845 -> 0.832, against the 64 x 64 tiles; from
+// 32 table rows, 3,300 rows, the stages' tile kernels are faster)
+constexpr int SKINNY_ROWS = 2048;
 template <int EPI, bool LN>
 __global__ __launch_bounds__(256) void k_gemm_skinny(int M, int N, int K, const float *__restrict__ X, int ldx,
                                                       const float *__restrict__ W, const float *__restrict__ b,
@@ -320,11 +324,11 @@ static void launch(hipStream_t s, int M, int N, int K, const float *X, int ldx, 
             hipLaunchKernelGGL((k_gemv<EPI, false>), dim3((N + 3) / 4), dim3(256), 0, s, M, N, K, X, ldx, W, b, Y, ldy,
                                ea, nullptr, nullptr);
     } else if (lnw) {
-        if (!(aligned && M <= 256 && K <= SKINNY_LN_K)) throw ArgError{"gemm: fused layer norm needs the few-rows kernel"};
+        if (!(aligned && M <= SKINNY_ROWS && K <= SKINNY_LN_K)) throw ArgError{"gemm: fused layer norm needs the few-rows kernel"};
         dim3 grid((N + 15) / 16, (M + 15) / 16);
         hipLaunchKernelGGL((k_gemm_skinny<EPI, true>), grid, dim3(256), 0, s, M, N, K, X, ldx, W, b, Y, ldy, ea, lnw,
                            lnb);
-    } else if (aligned && (M <= 256 || N <= 32)) {  // few rows, or few columns (the decoder's last layer)
+    } else if (aligned && (M <= SKINNY_ROWS || N <= 32)) {  // few rows, or few columns (the decoder's last layer)
         dim3 grid((N + 15) / 16, (M + 15) / 16);
         hipLaunchKernelGGL((k_gemm_skinny<EPI, false>), grid, dim3(256), 0, s, M, N, K, X, ldx, W, b, Y, ldy, ea,
                            nullptr, nullptr);
@@ -363,7 +367,7 @@ void gemm(hipStream_t s, int M, int N, int K, const float *X, int ldx, const flo
 }
 
 bool gemm_ln_fits(int M, int K, const float *X, int ldx, const float *W) {
-    return M <= 256 && K <= SKINNY_LN_K && K % 4 == 0 && ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 &&
+    return M <= SKINNY_ROWS && K <= SKINNY_LN_K && K % 4 == 0 && ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 &&
            (reinterpret_cast<uintptr_t>(W) & 15) == 0;
 }
 

@@ -885,11 +885,11 @@ void input_cells(hipStream_t s, const tah_weights *w, const float *x, int n, int
     TAH_LAUNCHED();
 }
 
-// At most this many rows (two 128-row tiles: the cells or tokens of one or two table rows, or 64 rows' class tokens),
-// the width-128 projections and feed-forward run on the f32 kernels, whose grids spread the weights over many compute
-// units, rather than on the tile kernels, which stream every weight through each tile's workgroup (two rows 0.763 ->
-// 0.661 ms, 64 rows 0.918 -> 0.905 ms; from 300 rows the f32 kernels' larger tiles lose: three rows 0.816 -> 0.877).
-constexpr int SMALL_ROWS = 256;
+// At most this many rows (the cells or tokens of up to 16 table rows, or 512 rows' class tokens), the width-128
+// projections and feed-forward run on the f32 kernels (16 x 16 tiles, SKINNY_ROWS), whose grids spread the weights
+// over many compute units, rather than on the tile kernels, which stream every weight through each tile's workgroup
+// (two rows 0.763 -> 0.661 ms, three 0.817 -> 0.707, eight 0.826 -> 0.753, 64 rows 0.918 -> 0.902).
+constexpr int SMALL_ROWS = 2048;
 // The row block's fused kernel (k_row_block, a workgroup per table row) from this many table rows up; below, the
 // projections, the attention (a workgroup per row and head) and the output projection separately (measured: one
 // row 0.84 -> 0.76 ms a prediction, 64 rows 1.43 -> 1.40 ms).
