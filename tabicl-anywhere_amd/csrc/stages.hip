@@ -925,9 +925,9 @@ static void out_projection(hipStream_t s, int M, const float *att, const DevBloc
 }
 
 // The column blocks run as the fused kernel (k_cell_block, a workgroup per 128 rows of a feature) from this many
-// rows: below, its workgroups run part-empty and each streams the block's weights for a few cells (one row 0.645 ->
-// 0.706 ms a prediction, 64 rows 1.080 -> 1.088; 256 rows 1.287 -> 1.268).
-constexpr int CELL_BLOCK_MIN = 128;
+// rows: below, its workgroups run mostly empty and each streams the block's weights for a few cells (one row 0.645
+// -> 0.706 ms a prediction; from 32 rows it pays: 64 rows 0.903 -> 0.895 ms, 256 rows 1.287 -> 1.268).
+constexpr int CELL_BLOCK_MIN = 32;
 
 // One column block (cached_block with a2) for all cells in place: n rows x groups, cell (r, g) at row r * sr + g * sg
 // of cells; K/V of group g at kvbase + g * gstride.

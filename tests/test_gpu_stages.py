@@ -80,8 +80,8 @@ def test_embed_with_label_digits_and_missing_cells(gpu, tiny_model):
     assert np.abs(got - want).max() < TOL
 
 
-@pytest.mark.parametrize("features,n", [(100, 24), (150, 24), (100, 1), (100, 130), (124, 130), (100, 520),
-                                        (100, 1030)])
+@pytest.mark.parametrize("features,n", [(100, 24), (150, 24), (100, 1), (100, 3), (100, 64), (100, 130), (124, 130),
+                                        (100, 520), (100, 1030)])
 def test_stages_full_size(gpu, full_model, full_weights, features, n):
     """Full-size column stage (3 blocks, 8 x 16 heads, 128 inducing points per group) and row stage (104, 128 or
     154 tokens, RoPE) against the oracle, then all three stages with a stored in-context cache. One row takes the
