@@ -590,7 +590,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
 // columns of the lane's row). With QM (one head of 64 columns a workgroup, TN = 2) the finished tile goes through
 // LDS and the workgroup runs the head's query MLP on it (qmlp64_tile) from the staged weights.
 constexpr int FEW_WAVES = 8;
-constexpr int FEW_ROWS = 256;
+// up to this many rows (the split-K kernel beyond: 384 rows 1.509 -> 1.330 ms a prediction, 512 rows 1.683 ->
+// 1.525, 1,024 rows 2.496 -> 2.403 ms; at 2,048 rows the split-K kernel's four tiles a workgroup win)
+constexpr int FEW_ROWS = 1024;
 // up to this many rows the f32 kernels (k_gemv, k_qmlp_rows) take the dense layers: their work grows with the rows,
 // and from 4 rows k_dense_few is faster
 constexpr int GEMV_SPLIT_ROWS = 3;
