@@ -376,13 +376,22 @@ __device__ __forceinline__ void qmlp64_tile(const float *qt, int ldq, float *hs,
 // goes through LDS and the workgroup runs the heads' query MLP on it (qmlp64_tile): no separate launch.
 constexpr int SPLITK_MAX_KQ = 512;  // each wavefront's share of K at most (K at most 2048)
 
+// 16 bytes a lane from src to dst + 16 lane by DMA (dst wavefront-uniform)
+__device__ __forceinline__ void copy16_to_lds(const float *src, uint8_t *dst) {
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4 *>(src), dst, 16, 0, 0);
+}
+
+
 template <int EPI, bool LN, int TN, bool QM = false>
 __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, const float *__restrict__ X, int ldx,
                                                           const uint8_t *__restrict__ wimg, int wshift,
                                                           const float *__restrict__ b, float *Y, int ldy, SplitEpi ea,
                                                           const float *__restrict__ lnw, const float *__restrict__ lnb) {
-    __shared__ __align__(16) float red[4][TN][16][64];  // [wavefront][tile][accumulator][lane]
-    __shared__ float rsum[4][32];                       // LN: per-wavefront partial row sums
+    // per wavefront 16 KB: its rows' 128-column chunk (32 rows x 32 float4, swizzled) while the products run, then
+    // its partial sums [tile][accumulator][lane]
+    __shared__ __align__(16) float stage[4][16 * 64 * 4];
+    auto red = [&](int w, int T, int v) { return &stage[w][(T * 16 + v) * 64]; };
+    __shared__ float rsum[4][32];  // LN: per-wavefront partial row sums
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r32 = lane & 31, g = lane >> 5;
     // one dimension of (N / 32 TN) x ceil(M / 32) workgroups; consecutive workgroups go to the eight XCDs in turn, so
@@ -396,7 +405,6 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
     const bool live = m < M;
     const int nt0 = bxt * TN;
     const int KS = K / 16, kq = K / 4, kend = (wave + 1) * kq;
-    const float *xrow = X + (size_t)(live ? m : 0) * ldx;
     floatx16 acc[TN];
 #pragma unroll
     for (int T = 0; T < TN; T++)
@@ -422,18 +430,32 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
     for (int it = 0; it < (LN ? 1 : SPLITK_MAX_KQ / 128); it++) {  // with the layer norm, K = 512
         const int k0 = wave * kq + 128 * it;
         if (k0 >= kend) break;
-        const int nks = min(8, (kend - k0) / 16);
         float xv[8][8];
+        {
+            // a whole chunk (K is a multiple of 512): the wavefront's 32 rows x 128 columns copied into its staging by DMA, copy i lane l
+            // filling float4 slot 64 i + l = row (64 i + l) / 32, float4 column ((64 i + l) % 32) ^ (row % 16), so
+            // that each load instruction reads whole runs of two rows (a lane a row, as below, touched 32 rows an
+            // instruction) and the reads back, a row a lane, fall on distinct bank groups; rows past M read row M - 1
+            const int m0 = tile / gx * 32;
+            uint8_t *st = reinterpret_cast<uint8_t *>(stage[wave]);
 #pragma unroll
-        for (int ks = 0; ks < 8; ks++) {
-            float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f), c = a;
-            if (live && ks < nks) {
-                const float *src = xrow + k0 + 16 * ks + 8 * g;
-                a = *reinterpret_cast<const float4 *>(src);
-                c = *reinterpret_cast<const float4 *>(src + 4);
+            for (int i = 0; i < 16; i++) {
+                const int slot = 64 * i + lane, row = slot >> 5, c = (slot & 31) ^ (row & 15);
+                copy16_to_lds(X + (size_t)min(m0 + row, M - 1) * ldx + k0 + 4 * c, st + 1024 * i);
             }
-            xv[ks][0] = a.x; xv[ks][1] = a.y; xv[ks][2] = a.z; xv[ks][3] = a.w;
-            xv[ks][4] = c.x; xv[ks][5] = c.y; xv[ks][6] = c.z; xv[ks][7] = c.w;
+            __builtin_amdgcn_s_waitcnt(0);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++) {
+#pragma unroll
+                for (int hf = 0; hf < 2; hf++) {
+                    const int c = 4 * ks + 2 * g + hf;
+                    const float4 a = *reinterpret_cast<const float4 *>(st + 16 * (r32 * 32 + (c ^ (r32 & 15))));
+                    xv[ks][4 * hf] = a.x; xv[ks][4 * hf + 1] = a.y; xv[ks][4 * hf + 2] = a.z; xv[ks][4 * hf + 3] = a.w;
+                }
+            }
         }
         if (LN) {
             // K = 512: this wavefront holds columns 128 w .. 128 w + 127 of its 32 rows; the row's sums go
@@ -490,7 +512,6 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
         const float f = ldexpf(1.0f, e);
 #pragma unroll
         for (int ks = 0; ks < 8; ks++) {
-            if (ks >= nks) break;
             const int j = 8 * it + ks;
             if (j + 2 < nsteps) wload(j + 2, wb[(j + 2) % 3]);
             halfx8 xh, xl;
@@ -507,7 +528,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
 #pragma unroll
     for (int T = 0; T < TN; T++)
 #pragma unroll
-        for (int v = 0; v < 16; v++) red[wave][T][v][lane] = acc[T][v] * u;
+        for (int v = 0; v < 16; v++) red(wave, T, v)[lane] = acc[T][v] * u;
     __syncthreads();
     if constexpr (QM) {
         static_assert(TN == 4 || TN == 2, "the fused query MLP takes whole heads (64 columns) per workgroup");
@@ -523,12 +544,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
 #pragma unroll
             for (int t = 0; t < 8; t++) {
                 const int v = 8 * hh + t;
-                yq[hh][t] = (((red[0][T][v][lane] + red[1][T][v][lane]) + red[2][T][v][lane]) + red[3][T][v][lane]) +
+                yq[hh][t] = (((red(0, T, v)[lane] + red(1, T, v)[lane]) + red(2, T, v)[lane]) + red(3, T, v)[lane]) +
                             b[n0 + t];
             }
         }
         __syncthreads();  // the partial sums are all read: their LDS holds the tile next, [32 rows][LD]
-        float *qt = &red[0][0][0][0];
+        float *qt = &stage[0][0];
 #pragma unroll
         for (int hh = 0; hh < 2; hh++) {
             if (TN == 2 && hh != (wave & 1)) continue;
@@ -537,7 +558,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
         }
         __syncthreads();
         // the hidden layer and the MLP's output after the tile, in the partial sums' LDS
-        static_assert(32 * LD + 2 * (TN / 2) * 32 * QMP <= 4 * TN * 16 * 64, "the query MLP's tiles fit in LDS");
+        static_assert(32 * LD + 2 * (TN / 2) * 32 * QMP <= 4 * 16 * 64 * 4, "the query MLP's tiles fit in LDS");
         float *hs = qt + 32 * LD;
         const int m0 = tile / gx * 32;
         qmlp64_tile<TN / 2, 256>(qt, LD, hs, hs + (TN / 2) * 32 * QMP, tid, qo, ea.s0, ea.s2,
@@ -555,7 +576,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
 #pragma unroll
         for (int t = 0; t < 8; t++) {
             const int v = 8 * hh + t;
-            yv[t] = ((red[0][T][v][lane] + red[1][T][v][lane]) + red[2][T][v][lane]) + red[3][T][v][lane];
+            yv[t] = ((red(0, T, v)[lane] + red(1, T, v)[lane]) + red(2, T, v)[lane]) + red(3, T, v)[lane];
         }
         if (b) {
             const float4 ba = *reinterpret_cast<const float4 *>(b + n0);
@@ -597,11 +618,6 @@ constexpr int FEW_ROWS = 1024;
 // and from 4 rows k_dense_few is faster
 constexpr int GEMV_SPLIT_ROWS = 3;
 constexpr int QPITCH = 68;  // row pitch of the query tile in LDS
-
-// 16 bytes a lane from src to dst + 16 lane by DMA (dst wavefront-uniform)
-__device__ __forceinline__ void copy16_to_lds(const float *src, uint8_t *dst) {
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4 *>(src), dst, 16, 0, 0);
-}
 
 template <int EPI, bool LN, int TN, int NST, bool QM>
 __global__ __launch_bounds__(512) void k_dense_few(int M, const float *__restrict__ X, int ldx,
@@ -1163,7 +1179,7 @@ void dense(hipStream_t s, int M, int N, int K, const float *X, int ldx, const fl
     // from 64 rows the split kernels win (two tiles a workgroup below 512 rows: a 64-row prediction 1.285 against
     // 1.316 ms on the f32 kernels, 256 rows 1.52 against 1.61 ms with four tiles)
     const bool split = img && M >= 64 && epis;
-    const bool k4 = split && N % 128 == 0 && K % 64 == 0 && K >= 256 && K <= 4 * SPLITK_MAX_KQ;
+    const bool k4 = split && N % 128 == 0 && K % 512 == 0 && K <= 4 * SPLITK_MAX_KQ;  // whole 128-column chunks
     if (lnw && !split && W && gemm_ln_fits(M, K, X, ldx, W)) {
         // few rows: the layer norm inside the product's kernel
         gemm(s, M, N, K, X, ldx, W, b, Y, ldy, epi, R, ldr, lnw, lnb);
