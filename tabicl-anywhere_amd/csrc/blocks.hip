@@ -323,7 +323,8 @@ __global__ __launch_bounds__(256, 1) void k_ff128h(int M, float *__restrict__ x,
                                                    const uint8_t *__restrict__ w2img, const float *__restrict__ b2,
                                                    int s2) {
     constexpr int E = 128, STEP = 2 * SLAB;
-    static_assert(NSL == 2 && 2 * 32 * 2 * E * 4 <= STEP, "two slices a step; the half sums fit a step buffer");
+    constexpr int HP = E + 4;  // the half sums' row pitch in floats: rows 16 bytes apart in the banks
+    static_assert(NSL == 2 && 2 * 32 * HP * 4 <= STEP, "two slices a step; the half sums fit a step buffer");
     __shared__ __align__(16) uint8_t ring[2 * STEP];
     __shared__ __align__(16) float bias1[256];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -422,7 +423,7 @@ __global__ __launch_bounds__(256, 1) void k_ff128h(int M, float *__restrict__ x,
     // the odd wavefront's sums (unscaled) into step 0's buffer (free: every wavefront is past step 2), then the even
     // one finishes: x += y_even + y_odd + b2 (output column of accumulator v of tile T: 32 T + 16 (v / 8) + 8 g + v % 8)
     const float u2 = ldexpf(1.0f, -(sh + s2));
-    float *half_sums = reinterpret_cast<float *>(ring) + rg * 32 * 2 * E;  // [32 rows][2 E]: this row group's
+    float *half_sums = reinterpret_cast<float *>(ring) + rg * 32 * HP;  // [32 rows][HP]: this row group's
     if (hf) {
 #pragma unroll
         for (int T = 0; T < 4; T++)
@@ -431,7 +432,7 @@ __global__ __launch_bounds__(256, 1) void k_ff128h(int M, float *__restrict__ x,
                 float o[8];
 #pragma unroll
                 for (int t = 0; t < 8; t++) o[t] = y[T][8 * hh + t] * u2;
-                float *dst = half_sums + r32 * 2 * E + 32 * T + 16 * hh + 8 * g;
+                float *dst = half_sums + r32 * HP + 32 * T + 16 * hh + 8 * g;
                 *reinterpret_cast<float4 *>(dst) = make_float4(o[0], o[1], o[2], o[3]);
                 *reinterpret_cast<float4 *>(dst + 4) = make_float4(o[4], o[5], o[6], o[7]);
             }
@@ -446,7 +447,7 @@ __global__ __launch_bounds__(256, 1) void k_ff128h(int M, float *__restrict__ x,
             float rv[8], bv[8], ov[8], xo[8];
             load8(xrow + c0, rv);
             load8(b2 + c0, bv);
-            load8(half_sums + r32 * 2 * E + c0, ov);
+            load8(half_sums + r32 * HP + c0, ov);
 #pragma unroll
             for (int t = 0; t < 8; t++) xo[t] = ((y[T][8 * hh + t] * u2 + ov[t]) + bv[t]) + rv[t];
             *reinterpret_cast<float4 *>(xrow + c0) = make_float4(xo[0], xo[1], xo[2], xo[3]);
