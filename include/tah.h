@@ -157,6 +157,13 @@ int tah_stage_dev_noalloc(tah_dev *dev, const tah_weights *w, const tah_model *m
  * src/fit.rs:6-7) to a model on the card, as VramModel holds it. */
 int tah_model_set_columns(tah_dev *dev, tah_model *model, const tah_weights *w, const float *col_kv, int32_t features,
                           int32_t digits);
+/* Card bytes tah_model_set_columns adds to a model of these weights: the column cache and the key/value images of
+ * the column blocks it makes from it (a part of Gpu::model_bytes, src/gpu.rs:2064-2068, for a member whose column
+ * cache the card holds). */
+size_t tah_columns_bytes(const tah_weights *w, int32_t features, int32_t digits);
+/* Card bytes a loaded model holds now: what tah_model_bytes counted at load plus what tah_model_set_columns added
+ * (VramModel's size as the VRAM tier accounts it, src/gpu.rs:2495-2611). */
+size_t tah_model_held_bytes(const tah_model *m);
 /* The column stage at prediction (embed, src/predict.rs:282-353): x [n][features] (already normalised) to tokens
  * [n][cls + features][e], class tokens first. */
 int tah_embed(tah_dev *dev, const tah_weights *w, const tah_model *model, const float *x, int32_t n, float *tok);

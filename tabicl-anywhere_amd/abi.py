@@ -101,6 +101,8 @@ SIGNATURES = {
                                              ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]),
     "tah_model_set_columns": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, F32P, ctypes.c_int32,
                                              ctypes.c_int32]),
+    "tah_columns_bytes": (ctypes.c_size_t, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32]),
+    "tah_model_held_bytes": (ctypes.c_size_t, [ctypes.c_void_p]),
     "tah_embed": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, F32P, ctypes.c_int32, F32P]),
     "tah_represent": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, F32P, ctypes.c_int32, ctypes.c_int32, F32P]),
     "tah_predict_rows": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, F32P, ctypes.c_int32,

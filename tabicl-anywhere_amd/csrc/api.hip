@@ -444,7 +444,19 @@ extern "C" int tah_weights_upload(tah_dev *dev, const tah_model_desc *m, tah_wei
         pk.add(m->col_y, ytab * e, &w->col_y);
         pk.add(m->cls_tokens, (size_t)m->cls * e, &w->cls_tokens);
         pk.add(m->rope_freqs, m->rope_half, &w->rope_freqs);
-        if (m->rope_freqs && m->rope_half > 0) w->rope_host.assign(m->rope_freqs, m->rope_freqs + m->rope_half);
+        // Rope::new (src/nn.rs:304-321) for every position a row can have
+        std::vector<float> rope;
+        if (m->rope_freqs && m->rope_half > 0) {
+            const size_t half = m->rope_half;
+            rope.resize(2 * (size_t)ROPE_POSITIONS * half);
+            for (int p = 0; p < ROPE_POSITIONS; p++)
+                for (size_t i = 0; i < half; i++) {
+                    const float a = (float)p * m->rope_freqs[i];
+                    rope[(size_t)p * half + i] = cosf(a);
+                    rope[((size_t)ROPE_POSITIONS + p) * half + i] = sinf(a);
+                }
+            pk.add(rope.data(), rope.size(), &w->rope_tab);
+        }
         pk.add(m->out_lnw, e, &w->out_lnw);
         pk.add(m->out_lnb, e, &w->out_lnb);
         pk.add(m->icl_y, ytab * d, &w->icl_y);
@@ -476,6 +488,14 @@ extern "C" int tah_weights_upload(tah_dev *dev, const tah_model_desc *m, tah_wei
             w->row.resize(m->row_blocks);
             for (int i = 0; i < m->row_blocks; i++) add_block(pk, m->row[i], w->row[i]);
         }
+        // room for the class tokens' first-row-block keys and values, filled on the card below
+        std::vector<float> cls_room;
+        const bool cls_kv = !w->row.empty() && m->cls > 0 && m->cls_tokens;
+        const float *cls_at = nullptr;
+        if (cls_kv) {
+            cls_room.assign((size_t)m->cls * 3 * e, 0.0f);
+            pk.add(cls_room.data(), cls_room.size(), &cls_at);
+        }
         try {
             TAH_HIP(hipMalloc(&w->arena, std::max<size_t>(pk.bytes, 256)));
             w->bytes = pk.bytes;
@@ -485,6 +505,11 @@ extern "C" int tah_weights_upload(tah_dev *dev, const tah_model_desc *m, tah_wei
                 TAH_HIP(hipMemcpy(dst, it.src, it.bytes, hipMemcpyHostToDevice));
                 *it.dst = dst;
                 at += align256(it.bytes);
+            }
+            if (cls_kv) {
+                w->cls_kv = const_cast<float *>(cls_at);
+                class_token_kv(dev->stream, w, w->cls_kv, w->cls_kv + (size_t)w->cls * 2 * w->e);
+                TAH_HIP(hipStreamSynchronize(dev->stream));
             }
         } catch (...) {
             if (w->arena) (void)hipFree(w->arena);
@@ -502,8 +527,6 @@ extern "C" void tah_weights_free(tah_weights *w) {
     // independent of the device handle, which may already be closed; hipFree waits for work that uses the memory
     if (!w) return;
     (void)hipSetDevice(w->ordinal);
-    for (auto &r : w->rope) (void)hipFree(r.second);
-    if (w->cls_kv) (void)hipFree(w->cls_kv);
     if (w->arena) (void)hipFree(w->arena);
     delete w;
 }
@@ -963,6 +986,14 @@ extern "C" int tah_in_context(tah_dev *dev, const tah_weights *w, const float *h
 }
 
 // ---- the column and row stages, and whole prediction from feature rows ------------------------------------------
+extern "C" size_t tah_columns_bytes(const tah_weights *w, int32_t features, int32_t digits) {
+    if (!w || features <= 0 || digits <= 0 || w->col_a2.empty()) return 0;
+    const size_t n = (size_t)features * digits * w->col_blocks * 2 * w->e * w->inds;
+    return align256(n * sizeof(float)) + align256(column_images_bytes(w, features, digits));
+}
+
+extern "C" size_t tah_model_held_bytes(const tah_model *m) { return m ? m->bytes : 0; }
+
 extern "C" int tah_model_set_columns(tah_dev *dev, tah_model *model, const tah_weights *w, const float *col_kv,
                                      int32_t features, int32_t digits) {
     if (!model || !w || !col_kv) return TAH_E_ARG;
@@ -998,38 +1029,14 @@ extern "C" int tah_model_set_columns(tah_dev *dev, tah_model *model, const tah_w
     });
 }
 
-// cos and sin of position * frequency for T positions ([T][half] each), as Rope::new (src/nn.rs:304-321): made on
-// the host the first time a token count is seen and kept on the card with the weights, so prediction never waits
-// for the host here again.
-static const float *rope_tables(const tah_weights *w_, int T) {
-    auto *w = const_cast<tah_weights *>(w_);  // the cache is not part of the weights' value
-    for (auto &r : w->rope)
-        if (r.first == T) return r.second;
-    const int half = w->rope_half;
-    std::vector<float> tab(2 * (size_t)T * half);
-    for (int p = 0; p < T; p++)
-        for (int i = 0; i < half; i++) {
-            const float a = (float)p * w->rope_host[i];
-            tab[(size_t)p * half + i] = cosf(a);
-            tab[(size_t)T * half + (size_t)p * half + i] = sinf(a);
-        }
-    float *d = nullptr;
-    TAH_HIP(hipMalloc(&d, std::max<size_t>(tab.size(), 1) * sizeof(float)));
-    w->rope.push_back({T, d});
-    TAH_HIP(hipMemcpy(d, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice));
-    return d;
-}
-
-// The class tokens' keys and values in the first row block (class_token_kv), made on the card the first time they
-// are needed and kept with the weights (they depend on the weights alone).
-static const float *class_kv(tah_dev *dev, const tah_weights *w_) {
-    auto *w = const_cast<tah_weights *>(w_);  // the cache is not part of the weights' value
-    if (w->cls_kv) return w->cls_kv;
-    float *d = nullptr;
-    TAH_HIP(hipMalloc(&d, (size_t)w->cls * 3 * w->e * sizeof(float)));
-    w->cls_kv = d;
-    class_token_kv(dev->stream, w, d, d + (size_t)w->cls * 2 * w->e);
-    return d;
+// The rotary tables of a row of T tokens (Rope::new, src/nn.rs:304-321): a prefix of the ones made at upload.
+struct RopeTabs {
+    const float *cos, *sin;
+};
+static RopeTabs rope_tables(const tah_weights *w, int T) {
+    if (!w->rope_tab) throw ArgError{"weights lack the rotary frequencies"};
+    if (T > ROPE_POSITIONS) throw ArgError{"row stage: more tokens than the rotary tables cover"};
+    return RopeTabs{w->rope_tab, w->rope_tab + (size_t)ROPE_POSITIONS * w->rope_half};
 }
 
 static void check_columns(const tah_weights *w, const tah_model *model) {
@@ -1082,7 +1089,7 @@ extern "C" int tah_represent(tah_dev *dev, const tah_weights *w, const float *to
         if (n <= 0) return TAH_OK;
         if (tokens <= w->cls) throw ArgError{"represent: too few tokens"};
         const size_t per_tok = (size_t)tokens * w->e;
-        const float *tabs = rope_tables(w, tokens);
+        const RopeTabs tabs = rope_tables(w, tokens);
         const int batch = batch_rows(dev, n, [&](int k) {
             return loan_bytes({(size_t)k * per_tok, (size_t)k * w->d, row_stage_floats(w, k, tokens)});
         });
@@ -1093,7 +1100,7 @@ extern "C" int tah_represent(tah_dev *dev, const tah_weights *w, const float *to
             float *scratch = loans.take<float>(row_stage_floats(w, k, tokens));
             TAH_HIP(hipMemcpyAsync(td, tok + (size_t)r0 * per_tok, sizeof(float) * k * per_tok, hipMemcpyHostToDevice,
                                    dev->stream));
-            row_stage(dev->stream, w, td, k, tokens, tabs, tabs + (size_t)tokens * w->rope_half, rd, scratch);
+            row_stage(dev->stream, w, td, k, tokens, tabs.cos, tabs.sin, rd, scratch);
             TAH_HIP(hipMemcpyAsync(rep + (size_t)r0 * w->d, rd, sizeof(float) * k * w->d, hipMemcpyDeviceToHost,
                                    dev->stream));
             TAH_HIP(hipStreamSynchronize(dev->stream));
@@ -1119,7 +1126,7 @@ static void predict_rows(tah_dev *dev, const tah_weights *w, const tah_model *mo
     check_columns(w, model);
     check_stage(w, model, n, out_n);
     const int T = w->cls + model->features;
-    const float *tabs = rope_tables(w, T);
+    const RopeTabs tabs = rope_tables(w, T);
     const int batch = batch_rows(dev, n, [&](int k) { return predict_batch_bytes(w, model, k); });
     for (int r0 = 0; r0 < n; r0 += batch) {
         const int k = std::min(batch, n - r0);
@@ -1137,12 +1144,12 @@ static void predict_rows(tah_dev *dev, const tah_weights *w, const tah_model *mo
             kv_ready = row_stage_takes_kv(w, k, T);
             column_stage_tokens(dev->stream, w, model->col_kv, xr, k, model->features, tok,
                                 kv_ready ? row_stage_kv(w, k, T, scratch) : nullptr,
-                                kv_ready ? class_kv(dev, w) : nullptr, cs, model->col_img);
+                                kv_ready ? w->cls_kv : nullptr, cs, model->col_img);
         } else {
             embed_rows(dev, w, model, xr, k, tok, loans);
             scratch = loans.take<float>(row_stage_floats(w, k, T));
         }
-        row_stage(dev->stream, w, tok, k, T, tabs, tabs + (size_t)T * w->rope_half, rep, scratch, kv_ready);
+        row_stage(dev->stream, w, tok, k, T, tabs.cos, tabs.sin, rep, scratch, kv_ready);
         stage_rows(dev, w, model, rep, k, out_n, out + (size_t)r0 * out_n, loans);
     }
 }
@@ -1312,7 +1319,7 @@ extern "C" int tah_fit_represent(tah_dev *dev, const tah_weights *w, const float
             if (digits > 1) scale_by(s, M * e, sum, 1.0f / (float)digits, cells);
         }
         // the row stage in batches of rows (src/fit.rs:516-539)
-        const float *tabs = rope_tables(w, T);
+        const RopeTabs tabs = rope_tables(w, T);
         const int rb = batch_rows(dev, rows, [&](int k) {
             return loan_bytes({(size_t)k * T * e, row_stage_floats(w, k, T)});
         });
@@ -1322,7 +1329,7 @@ extern "C" int tah_fit_represent(tah_dev *dev, const tah_weights *w, const float
             float *tok = loans.take<float>((size_t)k * T * e);
             float *scratch = loans.take<float>(row_stage_floats(w, k, T));
             tokens_gmajor(s, w, k, r0, rows, features, emb, tok);
-            row_stage(s, w, tok, k, T, tabs, tabs + (size_t)T * w->rope_half, reps + (size_t)r0 * d, scratch);
+            row_stage(s, w, tok, k, T, tabs.cos, tabs.sin, reps + (size_t)r0 * d, scratch);
         }
         TAH_HIP(hipMemcpyAsync(col_kv_out, col_kv, sizeof(float) * features * gstride, hipMemcpyDeviceToHost, s));
         TAH_HIP(hipMemcpyAsync(reps_out, reps, sizeof(float) * rows * d, hipMemcpyDeviceToHost, s));
@@ -1422,13 +1429,13 @@ extern "C" int tah_rows(tah_dev *dev, const tah_weights *w, const float *cells, 
                               "many do)"};
         const int T = w->cls + features, e = w->e;
         hipStream_t s = dev->stream;
-        const float *tabs = rope_tables(w, T);
+        const RopeTabs tabs = rope_tables(w, T);
         Loans loans(dev);
         float *cd = loans.take<float>((size_t)n * features * e), *tok = loans.take<float>((size_t)n * T * e);
         float *rd = loans.take<float>((size_t)n * w->d), *scratch = loans.take<float>(row_stage_floats(w, n, T));
         TAH_HIP(hipMemcpyAsync(cd, cells, sizeof(float) * n * features * e, hipMemcpyHostToDevice, s));
         assemble_tokens(s, w, cd, n, features, tok);
-        row_stage(s, w, tok, n, T, tabs, tabs + (size_t)T * w->rope_half, rd, scratch);
+        row_stage(s, w, tok, n, T, tabs.cos, tabs.sin, rd, scratch);
         TAH_HIP(hipMemcpyAsync(reps, rd, sizeof(float) * n * w->d, hipMemcpyDeviceToHost, s));
         TAH_HIP(hipStreamSynchronize(s));
         dev->stages++;

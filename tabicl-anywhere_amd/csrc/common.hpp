@@ -119,14 +119,16 @@ struct tah_weights {
     const float *icl_y, *lnw, *lnb, *dec0w, *dec0b, *dec2w, *dec2b;
     SplitW dec0_s;  // the decoder's first layer as a gemm_split image
     const float *col_scale;  // [e]: 1 / sqrt(column head width), what the column blocks' queries are multiplied by
-    // the row stage's rotary tables, made once per token count T and kept with the weights: cos then sin of
-    // position * frequency, [2][T][rope_half] on the card; rope_host is the frequencies as uploaded
-    std::vector<float> rope_host;
-    std::vector<std::pair<int, float *>> rope;
-    // the class tokens' keys and values in the first row block, [cls][2 e] (then cls e floats of room), made on the
-    // card the first time prediction needs them and kept with the weights
+    // the row stage's rotary tables, made at upload for positions 0 .. ROPE_POSITIONS - 1 (any token count up to
+    // that reads a prefix): cos then sin of position * frequency, [2][ROPE_POSITIONS][rope_half], or null
+    const float *rope_tab = nullptr;
+    // the class tokens' keys and values in the first row block, [cls][2 e] (then cls e floats of room), made at upload
+    // (they depend on the weights alone), or null without a row stage
     float *cls_kv = nullptr;
 };
+
+// Token positions the rotary tables cover: a row of at most this many tokens (class tokens and features).
+constexpr int ROPE_POSITIONS = 16384;
 
 struct tah_model {
     tah_dev *dev;

@@ -393,6 +393,16 @@ class VramModel:
                                                           int(features), int(digits)))
         self.features, self.digits = int(features), int(digits)
 
+    def bytes(self) -> int:
+        """Card bytes this problem holds now: its layers as loaded, plus its column cache and the column blocks'
+        key/value images once `set_columns` has run."""
+        return int(self.gpu._l.tah_model_held_bytes(self._h)) if getattr(self, "_h", None) else 0
+
+    @staticmethod
+    def columns_bytes(weights: "GpuWeights", features: int, digits: int) -> int:
+        """Card bytes `set_columns` adds: the column cache and the column blocks' key/value images made from it."""
+        return int(abi.lib().tah_columns_bytes(weights._h, int(features), int(digits)))
+
     @staticmethod
     def model_bytes(weights: "GpuWeights", kv_format: int, rows: int, chunk: int) -> int:
         """Card bytes a problem of `rows` stored rows takes once loaded (`Gpu::model_bytes`, src/gpu.rs:2064-2068):

@@ -38,6 +38,10 @@ FULL_CLASSIFIER = {
     "bias_free_ln": False, "recompute": False,
 }
 FULL_REGRESSOR = dict(FULL_CLASSIFIER, max_classes=0, bias_free_ln=True)
+# The reference's tiny test architecture (tools/make_tiny.py:15-41): embedding 8, two blocks in each stage, two heads,
+# 8 inducing points, 2 class tokens (d = 16), 99 quantiles.
+TINY_CLASSIFIER = dict(FULL_CLASSIFIER, num_quantiles=99, embed_dim=8, col_num_blocks=2, col_nhead=2, col_num_inds=8,
+                       row_num_blocks=2, row_nhead=2, row_num_cls=2, icl_num_blocks=2, icl_nhead=2)
 
 
 class ModelError(ValueError):

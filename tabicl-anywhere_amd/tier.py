@@ -120,11 +120,12 @@ class VramTier:
     @staticmethod
     def problem_bytes(f, weights: hip.GpuWeights, node: int) -> int:
         """Card bytes of problem `node` of the fitted member `f` once loaded (`Gpu::model_bytes`,
-        `src/gpu.rs:2063-2068`): its records and their images, plus the column cache when the member is one problem
-        of one label digit (then prediction runs all three stages on the card)."""
+        `src/gpu.rs:2063-2068`): its layers as the card holds them, plus the column cache and the column blocks'
+        key/value images when the member is one problem of one label digit (then prediction runs all three stages on
+        the card). The same figure the loaded problem reports (`VramModel.bytes`)."""
         n = hip.VramModel.model_bytes(weights, f.kv_format, f.nodes[node].rows, f.chunk)
         if len(f.nodes) == 1 and f.digits == 1:
-            n += f.col_kv.size * 4
+            n += hip.VramModel.columns_bytes(weights, f.features, f.digits)
         return n
 
     def _room_for(self, tenant: str, nbytes: int) -> bool:

@@ -84,16 +84,19 @@ def test_config2_fit_and_predict_10k(gpu, clf):
     check_representations(m, col_kv, reps, plan.bases, x, y, sample)
     assert np.abs(scales - np.stack([orc.query_scale(b, rows) for b in m.icl])).max() <= 2e-7 * np.abs(scales).max()
     W.check_layers(m, h[sample], layers, scales, rows, chunk, sample, KV_TOL, say)
-    # 2,048 predictions against the fitted caches; 64 of them through the oracle
+    # 2,048 predictions against the fitted caches, every one of them through the oracle
     vm = gpu.load(w, abi.KV_F32, rows, chunk, layers, scales)
     vm.set_columns(col_kv, features, 1)
     got = gpu.predict(w, vm, xt, classes)
-    ts = np.sort(rng.choice(nt, 64, replace=False))
+    t0 = time.perf_counter()
     want = orc.predict_raw(m, W.fitted_of(plan, col_kv, scales, layers, rows, features, classes, chunk, abi.KV_F32),
-                           xt[ts])
-    err = float(np.abs(got[ts] - want).max())
-    say(f"  scores of 64 of {nt} predicted rows: worst {err:.2e}")
-    assert err < KV_TOL and np.isfinite(got).all()
+                           xt)
+    err = float(np.abs(got - want).max())
+    p_err = float(np.abs(T.finish_proba(got.astype(np.float64), 1, 0.9)
+                         - T.finish_proba(want.astype(np.float64), 1, 0.9)).max())
+    say(f"  scores of all {nt} predicted rows: worst {err:.2e}; probabilities worst {p_err:.2e} "
+        f"(oracle {time.perf_counter() - t0:.1f} s)")
+    assert err < KV_TOL and p_err < PROBA_TOL and np.isfinite(got).all()
     vm.free()
     w.free()
 

@@ -148,16 +148,23 @@ def test_in_context_fit_full_size(gpu, full_model, kv_format):
                 assert np.abs(sa - sb).max() <= 1e-5 * np.abs(sb).max(), (l, ci)
                 ca, cb = a[8 * d:].view(it).astype(np.int32), b[8 * d:].view(it).astype(np.int32)
                 assert np.abs(ca - cb).max() <= 1, (l, ci)
-    # predictions from the card's cache and the oracle's agree
+    # predictions over the card's cache: the card against the oracle on the same stored records, absolutely
     hq = rng.standard_normal((32, d)).astype(np.float32)
     vm = gpu.load(w, kv_format, rows, chunk, layers, scales)
     got = gpu.in_context(w, vm, hq, 10)
-    want = orc.in_context(m, scales, o_layers, kv_format, rows, chunk, hq, 10)
     vm.free()
+    same = orc.in_context(m, scales, layers, kv_format, rows, chunk, hq, 10)
+    err = float(np.abs(got - same).max())
+    say(f"  predictions over the same cache worst {err:.2e}")
+    assert err < TOL
+    # and over the oracle's own fit of the same rows: two fits whose twelve layers each round differently, so the
+    # caches differ by the fit's own rounding (and the integer caches by a code step at ties); their predictions are
+    # compared relative to the scores' magnitude, since that drift grows with it
+    other = orc.in_context(m, scales, o_layers, kv_format, rows, chunk, hq, 10)
     tol = TOL if kv_format == abi.KV_F32 else 5e-3
-    err = np.abs(got - want).max()
-    say("  predictions worst", err, "scale", np.abs(want).max())
-    assert err < tol * max(1.0, np.abs(want).max())
+    drift = float(np.abs(got - other).max())
+    say(f"  predictions over the oracle's fit worst {drift:.2e}, scores up to {np.abs(other).max():.2f}")
+    assert drift < tol * max(1.0, np.abs(other).max())
 
 
 def test_sink_can_stop_the_fit(gpu, tiny_model):

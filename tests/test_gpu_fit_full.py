@@ -27,17 +27,40 @@ def gpu():
     g.close()
 
 
-def predict_card(gpu, w, fitted, x):
-    """Scores from the card for a fitted member: all three stages for one problem, or the column and row stages
-    then each problem's in-context stage and the tree walk (src/predict.rs:661-693)."""
+def node_outputs_card(gpu, w, fitted, x):
+    """Each class-tree node's raw outputs from the card: the column and row stages, then every node's in-context
+    stage (src/predict.rs:661-693 before the walk)."""
     vms = [gpu.load(w, fitted.kv_format, node.rows, fitted.chunk, fitted.layers[i], fitted.scales[i])
            for i, node in enumerate(fitted.nodes)]
     vms[0].set_columns(fitted.col_kv, fitted.features, fitted.digits)
-    if len(vms) == 1:
-        return gpu.predict(w, vms[0], x, fitted.classes)
     rep = gpu.represent(w, gpu.embed(w, vms[0], x))
     outs = [gpu.in_context(w, vm, rep, node.k) for vm, node in zip(vms, fitted.nodes)]
-    return planmod.tree_scores(fitted.nodes, outs, fitted.classes)
+    for vm in vms:
+        vm.free()
+    return outs
+
+
+def node_outputs_oracle(m, fitted, x):
+    rep = orc.represent(m, orc.embed(m, fitted, x))
+    return [orc.in_context(m, fitted.scales[ni], fitted.layers[ni], fitted.kv_format, node.rows, fitted.chunk, rep,
+                           node.k) for ni, node in enumerate(fitted.nodes)]
+
+
+def tree_proba(nodes, outs, classes):
+    """The class probabilities the tree walk multiplies out (before the reference's 0.9 ln(p + 1e-6) scores)."""
+    return (np.exp(planmod.tree_scores(nodes, outs, classes).astype(np.float64) / 0.9) - 1e-6).clip(0.0)
+
+
+def predict_card(gpu, w, fitted, x):
+    """Scores from the card for a fitted member: all three stages for one problem, or the column and row stages
+    then each problem's in-context stage and the tree walk (src/predict.rs:661-693)."""
+    if len(fitted.nodes) > 1:
+        return planmod.tree_scores(fitted.nodes, node_outputs_card(gpu, w, fitted, x), fitted.classes)
+    vm = gpu.load(w, fitted.kv_format, fitted.nodes[0].rows, fitted.chunk, fitted.layers[0], fitted.scales[0])
+    vm.set_columns(fitted.col_kv, fitted.features, fitted.digits)
+    out = gpu.predict(w, vm, x, fitted.classes)
+    vm.free()
+    return out
 
 
 def test_fit_tiny_matches_reference(gpu, tiny_model, tiny_raw):
@@ -95,9 +118,15 @@ def test_fit_many_classes_with_label_digits(gpu, tiny_model):
     assert got.plan.bases == [4, 4] and len(got.plan.nodes) == 3
     compare_fits(got, want, abi.KV_F32)
     xt = rng.standard_normal((20, 6)).astype(np.float32)
-    s_card = predict_card(gpu, w, got, xt)
-    s_orc = orc.predict_raw(m, want, xt)
-    assert np.abs(s_card - s_orc).max() < TOL * 10  # through the tree's softmax and log
+    # each node's raw scores from the card's caches against the oracle's over its own fit, absolutely; then the
+    # probabilities the tree multiplies out at the probability tolerance (the final 0.9 ln(p + 1e-6) scores magnify
+    # differences of small probabilities by 1/p, so they are compared as probabilities)
+    o_card = node_outputs_card(gpu, w, got, xt)
+    o_orc = node_outputs_oracle(m, want, xt)
+    err = max(float(np.abs(a - b).max()) for a, b in zip(o_card, o_orc))
+    p_err = float(np.abs(tree_proba(got.nodes, o_card, 14) - tree_proba(want.nodes, o_orc, 14)).max())
+    say(f"  node scores worst {err:.2e}, tree probabilities worst {p_err:.2e}")
+    assert err < TOL and p_err < 1e-5
 
 
 def test_fit_regression_model(gpu):
@@ -152,3 +181,53 @@ def test_fit_full_size(gpu):
         b = orc.predict_raw(m, fo, xt)
         say(f"  format {fmt}: scores worst", np.abs(a - b).max())
         assert np.abs(a - b).max() < TOL
+
+
+def test_config1_tiny_random_model(gpu):
+    """The smallest workload as specified: the reference's tiny architecture with seeded random weights, 256
+    training rows x 10 N(0, 1) features, 3 classes from the argmax of a seeded random projection, f32 cache, one
+    member, 64 test rows. The card's fit against the oracle's whole (column cache, scales, every layer's keys and
+    values), and all 64 rows' scores and probabilities against the oracle's over its own fit."""
+    import workloads as W
+
+    m = M.Model.random(M.TINY_CLASSIFIER, seed=0)
+    x, y, xt = W.tiny_table()
+    w = gpu.weights(m)
+    got = fit.fit_raw(gpu, w, x, y, 3, chunk=256)
+    want = orc.fit_raw(m, x, y, 3, chunk=256)
+    compare_fits(got, want, abi.KV_F32)
+    s_card = predict_card(gpu, w, got, xt)
+    s_orc = orc.predict_raw(m, want, xt)
+    err = float(np.abs(s_card - s_orc).max())
+    T = pkg("table")
+    p_err = float(np.abs(T.finish_proba(s_card.astype(np.float64), 1, 0.9)
+                         - T.finish_proba(s_orc.astype(np.float64), 1, 0.9)).max())
+    say(f"  config 1, 64 rows: scores worst {err:.2e}, probabilities worst {p_err:.2e}")
+    assert err < TOL and p_err < 1e-5 and np.isfinite(s_card).all()
+    w.free()
+
+
+@pytest.mark.parametrize("bases", [[5, 5, 5], [3, 4, 2]])
+def test_label_digits_on_card_are_single_digit_stages(gpu, tiny_model, bases):
+    """The card's label-digit column stage pinned by what the digits mean (src/fit.rs:356-363): digit j of label y
+    is (y // prod_{i>j} b_i) % b_j, and each digit's slice of the card's column cache equals the card's one-digit
+    stage fitted on those labels; the whole cache also matches the oracle's."""
+    m = tiny_model
+    rng = np.random.default_rng(7 + sum(bases))
+    rows, features = 150, 6
+    total = int(np.prod(bases))
+    x = rng.standard_normal((rows, features)).astype(np.float32)
+    y = rng.integers(0, total, rows)
+    w = gpu.weights(m)
+    ind_scales = np.stack([fit.query_scale(b, rows) for b in m.col_a1])
+    col, _ = gpu.fit_represent(w, x, y.astype(np.float32), bases, ind_scales)
+    worst = 0.0
+    for j in range(len(bases)):
+        yj = (y // int(np.prod(bases[j + 1:], dtype=np.int64))) % bases[j]
+        col1, _ = gpu.fit_represent(w, x, yj.astype(np.float32), [bases[j]], ind_scales)
+        worst = max(worst, float(np.abs(col[:, j] - col1[:, 0]).max()))
+    want, _ = orc.fit_columns(m, x, y.astype(np.float32), bases, 256)
+    err = float(np.abs(col - want).max())
+    say(f"  digits {bases}: per-digit slices against one-digit stages {worst:.2e}; against the oracle {err:.2e}")
+    assert worst == 0.0 and err < TOL
+    w.free()

@@ -94,3 +94,19 @@ def test_model_larger_than_tenant_budget_stays_off_the_card(setup):
     for _ in range(3):
         assert h.rows("m0/", xt, 3) is None  # the CPU answers, every time
     assert t.on_card("carol") == (0, 0) and t.fallbacks == 0
+
+
+def test_tier_counts_what_the_card_holds(setup):
+    """The tier's byte figures are what the loaded problems really hold on the card: their layers, the column cache
+    and the column blocks' key/value images (`VramModel.bytes`, read from the library after loading)."""
+    gpu, w, members, xt, want = setup
+    one = tier.VramTier.problem_bytes(members["m0/"], w, 0)
+    t = tier.VramTier(gpu, 4 * one, 2 * one)
+    assert t.preload("dave", "a", members, w, "m0/", 0) and t.preload("erin", "a", members, w, "m0/", 0)
+    held = [r.vm.bytes() for r in t._map.values() if r.vm is not None]
+    say(f"  tier: {one} bytes a problem by its estimate; held {held}")
+    assert held == [one, one]
+    assert t.on_card("dave") == (sum(held), one)
+    t.evict("dave")
+    t.evict("erin")
+    assert t.on_card("dave") == (0, 0)

@@ -86,6 +86,37 @@ def test_column_stage_pieces_agree_with_the_whole(tiny_model, bases, classes):
     assert np.array_equal(orc.fit_cells_rows(m, col, bases, x[rows], y[rows]), emb[:, rows])
 
 
+@pytest.mark.parametrize("bases", [[5, 5, 5], [3, 4, 2]])
+def test_label_digits_are_single_digit_stages(tiny_model, bases):
+    """The label-digit column stage (src/fit.rs:356-363) pinned by its meaning rather than its formula: with digits
+    b_0..b_{k-1}, digit j of label y is y_j = (y // prod_{i>j} b_i) % b_j (the mixed-radix expansion, most significant
+    digit first), and the stage runs each digit as a one-digit stage of its own over the same input cells. So each
+    digit's slice of the cache equals a one-digit stage fitted on the labels y_j, and the cells are the digits'
+    cells averaged (summed in digit order, times 1/k). A divisor of b_{j+1} alone, a reversed digit order or a
+    digit taken before the division fails it from the third digit on."""
+    m = tiny_model
+    rng = np.random.default_rng(sum(bases))
+    total = int(np.prod(bases))
+    x = rng.standard_normal((90, 6)).astype(np.float32)
+    x[5, :] = -100.0
+    y = rng.integers(0, total, 90)
+    col, emb = orc.fit_columns(m, x, y.astype(np.float32), bases, 32)
+    # the expansion checked against its definition: the digits rebuild the label
+    digits = []
+    for j in range(len(bases)):
+        digits.append((y // int(np.prod(bases[j + 1:], dtype=np.int64))) % bases[j])
+    rebuilt = np.zeros_like(y)
+    for j, dj in enumerate(digits):
+        rebuilt = rebuilt * bases[j] + dj
+    assert np.array_equal(rebuilt, y)
+    acc = None
+    for j, dj in enumerate(digits):
+        col1, emb1 = orc.fit_columns(m, x, dj.astype(np.float32), [bases[j]], 32)
+        assert np.array_equal(col[:, j], col1[:, 0]), f"digit {j}"
+        acc = emb1.copy() if acc is None else (acc + emb1).astype(np.float32)
+    assert np.array_equal(emb, (acc * np.float32(1.0 / len(bases))).astype(np.float32))
+
+
 def test_prediction_stages_match_reference(tiny_model, tiny_raw, tiny_fit):
     m = tiny_model
     xt = tiny_raw.f32s("x_test").reshape(16, 7)
@@ -286,3 +317,19 @@ def test_tree_scores_brute_force():
             leaf = sm(outs[child][r].astype(np.float64))
             for j, cls_ in enumerate(nodes[child].map):
                 assert abs(probs[r, cls_] - root[gi] * leaf[j]) < 1e-5
+
+
+def test_tiny_workload_on_the_cpu_path():
+    """The tiny workload (the reference's tiny architecture, seeded weights, 256 x 10 training rows, 3 classes, 64
+    test rows) through the CPU path: every score finite, and the same scores (to summation order) at any chunk size
+    (tests/pipeline.rs:56-64), the short last chunk included."""
+    import workloads as W
+
+    M = pkg("model")
+    m = M.Model.random(M.TINY_CLASSIFIER, seed=0)
+    x, y, xt = W.tiny_table()
+    assert sorted(set(y.astype(int).tolist())) == [0, 1, 2]
+    a = orc.predict_raw(m, orc.fit_raw(m, x, y, 3, chunk=256), xt)
+    b = orc.predict_raw(m, orc.fit_raw(m, x, y, 3, chunk=48), xt)
+    assert a.shape == (64, 3) and np.isfinite(a).all()
+    assert np.abs(a - b).max() < 1e-5

@@ -6,7 +6,8 @@ layer's arithmetic:
   benchmark predicts against;
 * 50k x 200 regression: 150 N(0, 1) columns, 30 log-normal (sigma 1.5), 20 categorical codes 0..11, 10% of cells
   missing at random; target = a seeded random MLP of the filled cells + N(0, 0.1);
-* 100k x 100, 120 classes: a seeded 120-component Gaussian mixture, the label is the component.
+* 100k x 100, 120 classes: a seeded 120-component Gaussian mixture, the label is the component;
+* 256 + 64 x 10 for the tiny architecture: X ~ N(0, 1) (seed 0), 3 classes = argmax(X W) with W ~ N(0, 1) (seed 1).
 """
 import numpy as np
 
@@ -23,6 +24,14 @@ def classification_table(rows, features=100, classes=10, seed_x=3, seed_w=4):
     w = rw.standard_normal((features, classes))
     g = rw.gumbel(size=(rows, classes))
     return x, np.argmax(x.astype(np.float64) @ w + g, axis=1).astype(np.float32)
+
+
+def tiny_table(train=256, test=64, features=10, classes=3, seed_x=0, seed_w=1):
+    """(x_train, y_train, x_test) of the tiny workload: labels from the argmax of a seeded random projection."""
+    x = np.random.default_rng(seed_x).standard_normal((train + test, features)).astype(np.float32)
+    w = np.random.default_rng(seed_w).standard_normal((features, classes))
+    y = np.argmax(x.astype(np.float64) @ w, axis=1).astype(np.float32)
+    return x[:train], y[:train], x[train:]
 
 
 def regression_table(rows, seed=7):
