@@ -119,8 +119,10 @@ void tah_weights_free(tah_weights *w);
 /* ---- fitted model on the card: VramModel::model_bytes / load (src/gpu.rs:2064-2116), but from the bundle's own
  * chunk records as they are stored (n{j}_kv{l}), any of the three formats, no re-layout on the host.
  * layer_records[l] points at layer l's bytes (tah_kv_record summed over its chunks); scales is n{j}_scale,
- * [layers][d]. tah_model_bytes (like Gpu::model_bytes, from the weights' shape) counts the records, the split-fp16
- * tile images the card builds from them (head width 64), and the scales; 0 without weights. */
+ * [layers][d]. A layer of head width 64 is held once, as the tiles the card makes of its records (f32: split-fp16
+ * images; i16: the codes with their dequantisation factors; i8: the codes as fp16 with the scales), which every
+ * attention kernel reads; other head widths keep the records. tah_model_bytes (like Gpu::model_bytes, from the
+ * weights' shape) counts what the layers are held as, and the scales; 0 without weights. */
 size_t tah_model_bytes(const tah_weights *w, int32_t kv_format, int32_t rows, int32_t chunk);
 int tah_model_load(tah_dev *dev, const tah_weights *w, int32_t kv_format, int32_t rows, int32_t chunk,
                    const uint8_t *const *layer_records, const float *scales, tah_model **out);

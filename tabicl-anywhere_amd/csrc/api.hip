@@ -536,13 +536,14 @@ static AttnShape shape_of(const tah_model *m, int heads, int nq) {
     return AttnShape{nq, m->rows, m->chunk, m->d, heads, m->kv_format};
 }
 
-static const uint8_t *layer_of(const tah_model *m, int l) { return m->records + (size_t)l * m->layer_bytes; }
+// Layer l's stored records (a model whose layers are held as tiles keeps none), or its tiles.
+static const uint8_t *layer_of(const tah_model *m, int l) {
+    return m->images ? nullptr : m->records + (size_t)l * m->layer_bytes;
+}
 
-// Layer l's tile images (they follow its records), or none.
 static KvImages images_of(const tah_model *m, int l) {
     if (!m->images) return KvImages{};
-    uint8_t *base = m->records + (size_t)l * m->layer_bytes + align256(layer_bytes(m->kv_format, m->rows, m->chunk, m->d));
-    return kv_images_at(base, m->rows, m->chunk, m->heads, m->kv_format);
+    return kv_images_at(m->records + (size_t)l * m->layer_bytes, m->rows, m->chunk, m->heads, m->kv_format);
 }
 
 // The images of f32 records rec32 in a loaned buffer when the split-fp16 kernel applies to a's queries, else none.
@@ -554,12 +555,12 @@ static const KvImages *loan_images(hipStream_t s, Loans &loans, const AttnShape 
     return &img;
 }
 
-// Per layer: the records as they are, then (head width 64) the layer's tile images (split-fp16 values for f32 and i16
-// records, the codes and their scales for i8).
+// Per layer: (head width 64) the layer's tiles in place of its records (split-fp16 images of f32 records, the codes
+// of i16 and i8 records with their factors or scales), each format held once; other head widths keep the records as
+// they are.
 static size_t model_layer_bytes(int kv_format, int rows, int chunk, int d, int heads) {
-    size_t b = align256(layer_bytes(kv_format, rows, chunk, d));
-    if (kv_images_apply(kv_format, d, heads)) b += align256(kv_images_bytes(rows, chunk, heads, kv_format));
-    return b;
+    if (kv_images_apply(kv_format, d, heads)) return align256(kv_images_bytes(rows, chunk, heads, kv_format));
+    return align256(layer_bytes(kv_format, rows, chunk, d));
 }
 
 extern "C" size_t tah_model_bytes(const tah_weights *w, int32_t kv_format, int32_t rows, int32_t chunk) {
@@ -589,19 +590,28 @@ extern "C" int tah_model_load(tah_dev *dev, const tah_weights *w, int32_t kv_for
         m->layer_bytes = model_layer_bytes(kv_format, rows, chunk, w->d, w->icl_heads);
         m->images = kv_images_apply(kv_format, w->d, w->icl_heads);
         m->bytes = tah_model_bytes(w, kv_format, rows, chunk);
+        const size_t lb = layer_bytes(kv_format, rows, chunk, w->d);
+        uint8_t *staging = nullptr;  // one layer's records on their way into its tiles
         try {
             TAH_HIP(hipMalloc(&m->records, m->bytes));
             m->scales = reinterpret_cast<float *>(m->records + (size_t)m->layers * m->layer_bytes);
-            for (int l = 0; l < m->layers; l++)
-                TAH_HIP(hipMemcpy(m->records + (size_t)l * m->layer_bytes, layer_records[l],
-                                  layer_bytes(kv_format, rows, chunk, w->d), hipMemcpyHostToDevice));
-            TAH_HIP(hipMemcpy(m->scales, scales, sizeof(float) * m->layers * m->d, hipMemcpyHostToDevice));
-            if (m->images) {
-                for (int l = 0; l < m->layers; l++)
-                    kv_images(dev->stream, rows, chunk, m->d, m->heads, kv_format, layer_of(m, l), images_of(m, l));
-                TAH_HIP(hipStreamSynchronize(dev->stream));
+            if (m->images) TAH_HIP(hipMalloc(&staging, lb));
+            for (int l = 0; l < m->layers; l++) {
+                if (m->images) {
+                    // the copy waits for the previous layer's tiles to be made from the staging buffer
+                    TAH_HIP(hipMemcpyAsync(staging, layer_records[l], lb, hipMemcpyHostToDevice, dev->stream));
+                    kv_images(dev->stream, rows, chunk, m->d, m->heads, kv_format, staging, images_of(m, l));
+                    TAH_HIP(hipStreamSynchronize(dev->stream));
+                } else {
+                    TAH_HIP(hipMemcpy(m->records + (size_t)l * m->layer_bytes, layer_records[l], lb,
+                                      hipMemcpyHostToDevice));
+                }
             }
+            TAH_HIP(hipMemcpy(m->scales, scales, sizeof(float) * m->layers * m->d, hipMemcpyHostToDevice));
+            if (staging) TAH_HIP(hipFree(staging));
+            staging = nullptr;
         } catch (...) {
+            if (staging) (void)hipFree(staging);
             if (m->records) (void)hipFree(m->records);
             delete m;
             throw;

@@ -130,6 +130,45 @@ __device__ __forceinline__ void load16(const uint8_t *rec, int d, int rc, int c,
     }
 }
 
+// ---- tiles: the form in which a layer of head width 64 is held on the card (its records are not kept) --------------
+// f32 caches: split images, the keys and values split into fp16 halves and laid out as the split kernel's LDS image.
+// One image per (key block, head), 32 KB: K hi, K lo as [64 keys][64 coordinates] and V hi, V lo as
+// [64 coordinates][64 keys], fp16, each 128-byte row split in eight 16-byte chunks stored XOR-swizzled by row: the
+// 64-bank LDS serves a 128-bit read 16 lanes at a time, and the 16 rows one such group reads (at one logical chunk)
+// then fall on 16 different 16-byte bank groups. Keys past the end of a short block are zeros. Each head's
+// keys are scaled by 2^sk and values by 2^sv, the powers of two that bring the layer's largest magnitude of that
+// head below 2^14; kvmax holds those maxima (f32 bits) per head, [heads][2].
+constexpr int IMG = 32768;
+// i8 caches: code images. The codes are integers of at most 127 in magnitude, exact in fp16, so an image holds them
+// as they are, one plane each (K codes [key][coordinate], then V codes [coordinate][key], in the layout of the
+// planes above), and the scales stay beside them: per (chunk, head) the head's 64 key scales, its 64 value scales
+// (a zero scale, whose coordinate's codes are all zero, stored as 1) and the 64 ratios of the previous chunk's value
+// scales to these (1 for the first chunk): scale table [chunks][heads][3][64]. Scores are then (q * key scales) .
+// codes, two products of the split query with the codes; the weighted sums codes . weights, two products of the split
+// weights, kept in units of the current chunk's value scales (multiplied by the ratios when a chunk begins, by the
+// value scales at the end).
+constexpr int IMG8 = 16384;
+constexpr int SCL = 768;  // bytes of one (chunk, head)'s scales
+// i16 caches: code tiles, 16 KB per (key block, head): the K codes as [64 keys][64 coordinates] then the V codes as
+// [64 coordinates][64 keys], int16, each 128-byte row in order (not swizzled: the attention kernel swizzles as it
+// writes its LDS images, and the decode kernel reads whole rows), zeros past a short block's end. The codes are not
+// exact in fp16 (up to 32767), so the attention kernel dequantises them itself: beside the tiles, per (chunk, head),
+// 64 key factors then 64 value factors, each the chunk's scale of that coordinate times 2^sk (2^sv), the power of
+// two that brings the head's largest dequantised |K| (|V|) below 2^14, as for f32 images (kvmax, the maxima, [heads][2]
+// in front of the factors): factor table [chunks][heads][2][64].
+constexpr int IMG16 = 16384;
+constexpr int FAC = 512;  // bytes of one (chunk, head)'s factors
+
+__host__ __device__ constexpr int img_bytes(int fmt) { return fmt == TAH_KV_F32 ? IMG : (fmt == TAH_KV_I16 ? IMG16 : IMG8); }
+
+__host__ __device__ inline size_t image_bytes_of(int rows, int chunk, int heads, int fmt) {
+    return (size_t)key_blocks(rows, chunk).n_kb * heads * img_bytes(fmt);
+}
+
+// rows r and r + 1 already sit in different bank halves (128-byte rows); rows of one parity among 16 consecutive ones
+// get eight different chunks
+__device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 7); }
+
 // ---- decode kernel: any head width <= 64, few queries --------------------------------------------------------
 // grid (splits, heads, query groups of QG); 64 threads.
 template <int FMT>
@@ -267,11 +306,45 @@ __device__ __forceinline__ void row64(const uint8_t *body, int rc, int c, int o,
     }
 }
 
-template <int FMT>
+// A tile row (64 values, widened to f32, unscaled) of key block kb's tile (the layouts of the split images, code tiles
+// and code images below): VALS false the K row of key r, true the V row of coordinate r.
+template <int FMT, bool VALS>
+__device__ __forceinline__ void tile_row(const uint8_t *tile, int r, float (&v)[64]) {
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        if constexpr (FMT == TAH_KV_I16) {
+            const uint4 x = *reinterpret_cast<const uint4 *>(tile + (VALS ? 8192 : 0) + r * 128 + c * 16);
+            const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                v[8 * c + 2 * t] = (float)(int16_t)(w[t] & 0xffffu);
+                v[8 * c + 2 * t + 1] = (float)(int16_t)(w[t] >> 16);
+            }
+        } else {
+            const int off = (FMT == TAH_KV_F32 ? (VALS ? 16384 : 0) : (VALS ? 8192 : 0)) + r * 128 + swz(r, c) * 16;
+            const halfx8 hi = *reinterpret_cast<const halfx8 *>(tile + off);
+            if constexpr (FMT == TAH_KV_F32) {
+                const halfx8 lo = *reinterpret_cast<const halfx8 *>(tile + off + 8192);
+#pragma unroll
+                for (int t = 0; t < 8; t++) v[8 * c + t] = (float)hi[t] + (float)lo[t];
+            } else {
+#pragma unroll
+                for (int t = 0; t < 8; t++) v[8 * c + t] = (float)hi[t];
+            }
+        }
+    }
+}
+
+// TILES: over a layer's tiles (records is then the tiles' base; kvmax the f32 and i16 maxima, scl the i16 factors or
+// the i8 scales) instead of its records: lane = key reads its key's 64 coordinates as one row of the tile, lane =
+// coordinate its 64 keys; every format is scaled through the query (keys) and the sums (values) as integer codes are.
+template <int FMT, bool TILES>
 __global__ __launch_bounds__(256) void k_attn_decode_w(int nq, int rows, int chunk, int d, int heads,
                                                        const float *__restrict__ q, const uint8_t *__restrict__ records,
-                                                       int kb_per_split, float *__restrict__ part_o,
-                                                       float *__restrict__ part_ml, float *__restrict__ out) {
+                                                       const uint32_t *__restrict__ kvmax,
+                                                       const float *__restrict__ scl, int kb_per_split,
+                                                       float *__restrict__ part_o, float *__restrict__ part_ml,
+                                                       float *__restrict__ out) {
     __shared__ float Qs[QG][64];
     __shared__ float Qk[4][QG][64];  // INT: each wavefront's queries times its block's key scales
     __shared__ float Ps[4][QG][KB];
@@ -283,8 +356,14 @@ __global__ __launch_bounds__(256) void k_attn_decode_w(int nq, int rows, int chu
     const int nqg = min(QG, nq - q0);
     const KeyBlocks kbs = key_blocks(rows, chunk);
     const int kb0 = split * kb_per_split, kb1 = min(kbs.n_kb, kb0 + kb_per_split);
-    constexpr bool INT = FMT != TAH_KV_F32;
+    constexpr bool INT = FMT != TAH_KV_F32 || TILES;  // keys scaled through the query, values through the sums
     const int width = FMT == TAH_KV_F32 ? 4 : (FMT == TAH_KV_I16 ? 2 : 1);
+    // TILES, f32 and i16: the head's powers of two (the tiles hold K 2^sk, V 2^sv)
+    float uk = 1.0f, uv = 1.0f;
+    if constexpr (TILES && FMT != TAH_KV_I8) {
+        uk = ldexpf(1.0f, -shift_for(kvmax[h * 2]));
+        uv = ldexpf(1.0f, -shift_for(kvmax[h * 2 + 1]));
+    }
     for (int i = tid; i < QG * 64; i += 256) {
         const int qi = i >> 6, c = i & 63;
         Qs[qi][c] = qi < nqg ? q[(size_t)(q0 + qi) * d + h * 64 + c] : 0.0f;
@@ -306,15 +385,36 @@ __global__ __launch_bounds__(256) void k_attn_decode_w(int nq, int rows, int chu
         // masked below); values: lane = coordinate, keys 0..63 of the block
         float kc[64], vr[64];
         const int kl = min(lane, w.nk - 1);
+        float ks = 1.0f, vs = 1.0f;
+        if constexpr (TILES) {
+            const uint8_t *tile = records + ((size_t)kb * heads + h) * img_bytes(FMT);
+            tile_row<FMT, false>(tile, kl, kc);
+            tile_row<FMT, true>(tile, lane, vr);
+            const int ci = kb / kbs.bpc;
+            if constexpr (FMT == TAH_KV_F32) {
+                ks = uk;
+                vs = uv;
+            } else if constexpr (FMT == TAH_KV_I16) {
+                const float *fac = scl + ((size_t)ci * heads + h) * 128;
+                ks = fac[lane] * uk;
+                vs = fac[64 + lane] * uv;
+            } else {
+                const float *sc8 = scl + ((size_t)ci * heads + h) * 192;
+                ks = sc8[lane];
+                vs = sc8[64 + lane];
+            }
+        } else {
 #pragma unroll
-        for (int c = 0; c < 64; c++) kc[c] = raw_at<FMT>(body, (size_t)(h * 64 + c) * w.rc + w.o + kl);
-        row64<FMT>(body, w.rc, d + h * 64 + lane, w.o, w.nk, fast, vr);
-        float vs = 1.0f;
+            for (int c = 0; c < 64; c++) kc[c] = raw_at<FMT>(body, (size_t)(h * 64 + c) * w.rc + w.o + kl);
+            row64<FMT>(body, w.rc, d + h * 64 + lane, w.o, w.nk, fast, vr);
+            if constexpr (INT) {
+                // the chunk's scales of this head: keys' multiply the queries (lane = coordinate), values' the sums
+                const float *sc = reinterpret_cast<const float *>(w.rec);
+                ks = sc[h * 64 + lane];
+                vs = sc[d + h * 64 + lane];
+            }
+        }
         if (INT) {
-            // the chunk's scales of this head: keys' multiply the queries (lane = coordinate), values' the sums
-            const float *sc = reinterpret_cast<const float *>(w.rec);
-            const float ks = sc[h * 64 + lane];
-            vs = sc[d + h * 64 + lane];
 #pragma unroll
             for (int qi = 0; qi < QG; qi++)
                 if (qi < nqg) Qk[wave][qi][lane] = Qs[qi][lane] * ks;
@@ -389,35 +489,6 @@ __global__ __launch_bounds__(256) void k_attn_decode_w(int nq, int rows, int chu
     }
 }
 
-// ---- tile images: keys and values (f32, or i16/i8 codes dequantised with their chunk's per-coordinate scales) split
-// into fp16 halves, laid out as the split kernel's LDS image -----------------------------------------------------
-// One image per (key block, head), 32 KB: K hi, K lo as [64 keys][64 coordinates] and V hi, V lo as
-// [64 coordinates][64 keys], fp16, each 128-byte row split in eight 16-byte chunks stored XOR-swizzled by row: the
-// 64-bank LDS serves a 128-bit read 16 lanes at a time, and the 16 rows one such group reads (at one logical chunk)
-// then fall on 16 different 16-byte bank groups. Keys past the end of a short block are zeros. Each head's
-// keys are scaled by 2^sk and values by 2^sv, the powers of two that bring the layer's largest magnitude of that
-// head below 2^14; kvmax holds those maxima (f32 bits) per head, [heads][2].
-constexpr int IMG = 32768;
-// i8 caches: code images. The codes are integers of at most 127 in magnitude, exact in fp16, so an image holds them
-// as they are, one plane each (K codes [key][coordinate], then V codes [coordinate][key], in the layout of the
-// planes above), and the scales stay beside them: per (chunk, head) the head's 64 key scales, its 64 value scales
-// (a zero scale, whose coordinate's codes are all zero, stored as 1) and the 64 ratios of the previous chunk's value
-// scales to these (1 for the first chunk): scale table [chunks][heads][3][64]. Scores are then (q * key scales) .
-// codes, two products of the split query with the codes; the weighted sums codes . weights, two products of the split
-// weights, kept in units of the current chunk's value scales (multiplied by the ratios when a chunk begins, by the
-// value scales at the end).
-constexpr int IMG8 = 16384;
-constexpr int SCL = 768;  // bytes of one (chunk, head)'s scales
-
-__host__ __device__ inline int img_bytes(bool codes) { return codes ? IMG8 : IMG; }
-
-__host__ __device__ inline size_t image_bytes_of(int rows, int chunk, int heads, bool codes) {
-    return (size_t)key_blocks(rows, chunk).n_kb * heads * img_bytes(codes);
-}
-
-// rows r and r + 1 already sit in different bank halves (128-byte rows); rows of one parity among 16 consecutive ones
-// get eight different chunks
-__device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 7); }
 
 __global__ __launch_bounds__(64) void k_zero_u32(int n, uint32_t *__restrict__ p) {
     const int i = blockIdx.x * 64 + threadIdx.x;
@@ -555,6 +626,49 @@ __global__ __launch_bounds__(256) void k_kv_codes(int rows, int chunk, int d, in
     }
 }
 
+// grid (key blocks, heads); 256 threads: one code tile of an i16 layer, and (by a chunk's first block) the chunk's
+// dequantisation factors of the head. Thread t: coordinate t / 4, keys 16 (t % 4) .. + 15 of the block (zeros past
+// its end). kvmax (k_kv_absmax) holds the head's largest dequantised |K| and |V|.
+__global__ __launch_bounds__(256) void k_kv_tiles16(int rows, int chunk, int d, int heads,
+                                                    const uint8_t *__restrict__ records,
+                                                    const uint32_t *__restrict__ kvmax, uint8_t *__restrict__ tiles,
+                                                    float *__restrict__ factors) {
+    __shared__ int16_t Ks[64][KB + 8];  // [coordinate][key]
+    const int kb = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    const KeyBlocks kbs = key_blocks(rows, chunk);
+    const Where w = locate(kbs, kb, records, TAH_KV_I16, d, chunk);
+    const int lc = tid >> 2, seg = (tid & 3) * 16;
+    const int16_t *body = reinterpret_cast<const int16_t *>(w.rec + 8 * (size_t)d);
+    const int16_t *kr = body + (size_t)(h * 64 + lc) * w.rc + w.o, *vr = body + (size_t)(d + h * 64 + lc) * w.rc + w.o;
+    uint8_t *tile = tiles + ((size_t)kb * heads + h) * IMG16;
+    int16_t vv[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const bool in = seg + i < w.nk;
+        Ks[lc][seg + i] = in ? kr[seg + i] : (int16_t)0;
+        vv[i] = in ? vr[seg + i] : (int16_t)0;
+    }
+    // V codes: row lc, keys seg .. seg + 15
+    *reinterpret_cast<uint4 *>(tile + 8192 + lc * 128 + seg * 2) = *reinterpret_cast<const uint4 *>(vv);
+    *reinterpret_cast<uint4 *>(tile + 8192 + lc * 128 + seg * 2 + 16) = *reinterpret_cast<const uint4 *>(vv + 8);
+    if (kb % kbs.bpc == 0 && tid < 128) {
+        // the record's scales: d key scales then d value scales
+        const int ci = kb / kbs.bpc, c = tid & 63, which = tid >> 6;
+        const float *sc = reinterpret_cast<const float *>(w.rec);
+        const float f = ldexpf(1.0f, shift_for(kvmax[h * 2 + which]));
+        factors[((size_t)ci * heads + h) * 128 + tid] = sc[which * d + h * 64 + c] * f;
+    }
+    __syncthreads();
+    // K codes: row = key, 8 coordinates a 16-byte chunk
+    for (int u = tid; u < 512; u += 256) {
+        const int r = u >> 3, c = u & 7;
+        int16_t kc[8];
+#pragma unroll
+        for (int t = 0; t < 8; t++) kc[t] = Ks[8 * c + t][r];
+        *reinterpret_cast<uint4 *>(tile + r * 128 + c * 16) = *reinterpret_cast<const uint4 *>(kc);
+    }
+}
+
 // ---- split-fp16 MFMA kernel: head width 64 over tile images --------------------------------------------------
 // A flat grid of qtiles x heads x splits workgroups of WAVES wavefronts x 32 queries (the flat index remapped so that
 // the query tiles sharing a (head, key range) run on the same XCD: workgroup i is dispatched to XCD i % 8, and the
@@ -594,6 +708,46 @@ __device__ __forceinline__ void half_image_to_lds(const uint8_t *src, uint8_t *d
     }
 }
 
+// i16 staging (k_attn_split64 with STAGED): half a code tile (8 KB, keys or values) into a staging slot's half by DMA,
+// and (wavefronts with fac_lanes: 16 lanes x 16 bytes) its chunk's 64 factors beside it.
+template <int WAVES>
+__device__ __forceinline__ void stage_half16(const uint8_t *src, const float *fac, uint8_t *dst, uint8_t *fdst, int tid,
+                                             bool fac_lanes) {
+    half_image_to_lds<WAVES, IMG16 / 2>(src, dst, tid);
+    if (fac_lanes && (tid & 63) < 16)
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t *>(fac + 4 * (tid & 63)), fdst, 16, 0, 0);
+}
+
+// A staging slot's key codes into the split image kdst (K hi, K lo) and its value codes into vdst (V hi, V lo), either
+// null for none: the dequantised values (code times its coordinate's factor, in f32) split into fp16 halves, written
+// swizzled as the images are; each thread takes 16 bytes (8 codes) of a 128-byte row at a time.
+template <int WAVES>
+__device__ __forceinline__ void convert16(const uint8_t *st, uint8_t *kdst, uint8_t *vdst, int tid) {
+#pragma unroll
+    for (int i = 0; i < 512 / (64 * WAVES); i++) {
+        const int u = tid + 64 * WAVES * i, r = u >> 3, c = u & 7;
+        const int off = r * 128 + swz(r, c) * 16;
+        if (kdst) {
+            // key r, coordinates 8 c .. 8 c + 7, each with its own factor
+            float f[8];
+            load8(reinterpret_cast<const float *>(st + IMG16) + 8 * c, f);
+            halfx8 hi, lo;
+            dequant_split8(*reinterpret_cast<const uint4 *>(st + r * 128 + c * 16), f, hi, lo);
+            *reinterpret_cast<halfx8 *>(kdst + off) = hi;
+            *reinterpret_cast<halfx8 *>(kdst + 8192 + off) = lo;
+        }
+        if (vdst) {
+            // coordinate r, keys 8 c .. 8 c + 7, one factor
+            const float fv = reinterpret_cast<const float *>(st + IMG16 + 256)[r];
+            const float f[8] = {fv, fv, fv, fv, fv, fv, fv, fv};
+            halfx8 hi, lo;
+            dequant_split8(*reinterpret_cast<const uint4 *>(st + IMG16 / 2 + r * 128 + c * 16), f, hi, lo);
+            *reinterpret_cast<halfx8 *>(vdst + off) = hi;
+            *reinterpret_cast<halfx8 *>(vdst + 8192 + off) = lo;
+        }
+    }
+}
+
 template <bool B>
 struct Flag {
     static constexpr bool value = B;
@@ -605,7 +759,14 @@ struct Flag {
 // in units of the current chunk's value scales (multiplied by the table's ratios when a block begins a chunk, by the
 // last chunk's value scales at the end: no second set of sums). The scales of a chunk are copied into a four-deep LDS
 // ring (DMA, two blocks ahead like the images), which a chunk's blocks use until the one after next begins.
-template <int WAVES, bool CODES>
+//
+// With an i16 cache (STAGED) the tiles hold codes (k_kv_tiles16), which are not exact in fp16: each half tile (8 KB of
+// codes) and its chunk's factors are copied into one of two LDS staging slots by DMA, one block earlier than an image
+// would be, and at the next step every thread dequantises 8 codes of each half (code times its coordinate's factor,
+// in f32) and writes them split into the same LDS images as an f32 layer's, which the rest of the kernel reads
+// unchanged. In step kb the staging slot of its parity holds keys kb + 2 and values kb + 1 (converted then), and the
+// copies bring keys kb + 3 and values kb + 2 into the other.
+template <int WAVES, int FMT>
 __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows, int chunk, int d, int heads,
                                                                const float *__restrict__ q,
                                                                const uint8_t *__restrict__ images,
@@ -613,12 +774,17 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows
                                                                const float *__restrict__ scl, int kb_per_split,
                                                                int qtiles, int splits, float *__restrict__ part_o,
                                                                float *__restrict__ part_ml, float *__restrict__ out) {
-    constexpr int HB = CODES ? IMG8 / 2 : IMG / 2;  // bytes of an image's keys (or values)
-    constexpr int IS = CODES ? IMG8 : IMG;          // bytes of an image
+    constexpr bool CODES = FMT == TAH_KV_I8;    // fp16 code images, scales applied in the kernel
+    constexpr bool STAGED = FMT == TAH_KV_I16;  // int16 code tiles dequantised into split images in the kernel
+    constexpr int HB = CODES ? IMG8 / 2 : IMG / 2;  // bytes of an LDS image's keys (or values)
+    constexpr int IS = img_bytes(FMT);              // bytes of a tile in memory
+    constexpr int SG = IMG16 + 2 * 256;             // STAGED: a staging slot, codes then key and value factors
     __shared__ __align__(16) uint8_t kt[2][HB], vt[2][HB];
     __shared__ __align__(16) float sb[CODES ? 4 : 1][192];  // CODES: scale ring, [chunk % 4][key, value, ratio]
-    // CODES: each lane's 32 query coordinates, kept for the per-chunk splits: [wavefront][8 chunks of 4][lane][4]
-    __shared__ __align__(16) float qraw[CODES ? WAVES : 1][CODES ? 8 * 64 * 4 : 4];
+    // CODES: each lane's 32 query coordinates, kept for the per-chunk splits: [wavefront][8 chunks of 4][lane][4];
+    // STAGED: the two staging slots (one array for both: the compiler's host pass refuses the kernel with them apart)
+    __shared__ __align__(16) uint8_t side[CODES ? WAVES * 8192 : (STAGED ? 2 * SG : 16)];
+    float (*qraw)[8 * 64 * 4] = reinterpret_cast<float (*)[8 * 64 * 4]>(side);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int total = qtiles * heads * splits;
     int flat = blockIdx.x;
@@ -638,10 +804,38 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows
             __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t *>(scl + ((size_t)ci * heads + h) * 192 + 4 * lane),
                                              reinterpret_cast<uint8_t *>(&sb[ci & 3][0]), 16, 0, 0);
     };
+    // STAGED: block kb's key codes and its chunk's key factors into staging slot sl; its value codes and value factors
+    auto stage_keys = [&](int kb, int sl) {
+        stage_half16<WAVES>(head_images + kb * kb_stride, scl + ((size_t)(kb / kbs.bpc) * heads + h) * 128,
+                            side + sl * SG, side + sl * SG + IMG16, tid, wave == 0);
+    };
+    auto stage_values = [&](int kb, int sl) {
+        stage_half16<WAVES>(head_images + kb * kb_stride + IMG16 / 2,
+                            scl + ((size_t)(kb / kbs.bpc) * heads + h) * 128 + 64, side + sl * SG + IMG16 / 2,
+                            side + sl * SG + IMG16 + 256, tid, wave == WAVES - 1);
+    };
+    auto convert = [&](int sl, int kdst, int vdst) {
+        convert16<WAVES>(side + sl * SG, kdst >= 0 ? kt[kdst] : nullptr, vdst >= 0 ? vt[vdst] : nullptr, tid);
+    };
     if (kb0 < kb1) {
-        half_image_to_lds<WAVES, HB>(head_images + kb0 * kb_stride, kt[0], tid);
-        half_image_to_lds<WAVES, HB>(head_images + kb0 * kb_stride + HB, vt[0], tid);
-        if (kb0 + 1 < kb1) half_image_to_lds<WAVES, HB>(head_images + (kb0 + 1) * kb_stride, kt[1], tid);
+        if constexpr (STAGED) {
+            // the first two blocks' keys and the first block's values converted here; then the staging slot of
+            // step kb0 filled (keys kb0 + 2, values kb0 + 1)
+            stage_keys(kb0, 0);
+            stage_values(kb0, 0);
+            if (kb0 + 1 < kb1) stage_keys(kb0 + 1, 1);
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            convert(0, 0, 0);
+            if (kb0 + 1 < kb1) convert(1, 1, -1);
+            __syncthreads();  // both slots are read before slot 0 is written again
+            if (kb0 + 2 < kb1) stage_keys(kb0 + 2, 0);
+            if (kb0 + 1 < kb1) stage_values(kb0 + 1, 0);
+        } else {
+            half_image_to_lds<WAVES, HB>(head_images + kb0 * kb_stride, kt[0], tid);
+            half_image_to_lds<WAVES, HB>(head_images + kb0 * kb_stride + HB, vt[0], tid);
+            if (kb0 + 1 < kb1) half_image_to_lds<WAVES, HB>(head_images + (kb0 + 1) * kb_stride, kt[1], tid);
+        }
         if constexpr (CODES) {
             scales_to_lds(kb0 / kbs.bpc);
             if (kb0 + 1 < kb1 && (kb0 + 1) % kbs.bpc == 0) scales_to_lds((kb0 + 1) / kbs.bpc);
@@ -807,8 +1001,15 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows
         const int sl = (kb - kb0) & 1;
         __builtin_amdgcn_s_waitcnt(0);  // this wavefront's copies of keys kb + 1 and values kb have landed
         __syncthreads();                // everyone's have, and step kb - 1's buffers are no longer read
-        if (kb + 2 < kb1) half_image_to_lds<WAVES, HB>(head_images + (kb + 2) * kb_stride, kt[sl], tid);
-        if (kb + 1 < kb1) half_image_to_lds<WAVES, HB>(head_images + (kb + 1) * kb_stride + HB, vt[sl ^ 1], tid);
+        if constexpr (STAGED) {
+            convert(sl, kb + 2 < kb1 ? sl : -1, kb + 1 < kb1 ? (sl ^ 1) : -1);
+            if (kb + 3 < kb1) stage_keys(kb + 3, sl ^ 1);
+            if (kb + 2 < kb1) stage_values(kb + 2, sl ^ 1);
+            __builtin_amdgcn_sched_barrier(0);  // the conversion stays out of the products' scheduling region
+        } else {
+            if (kb + 2 < kb1) half_image_to_lds<WAVES, HB>(head_images + (kb + 2) * kb_stride, kt[sl], tid);
+            if (kb + 1 < kb1) half_image_to_lds<WAVES, HB>(head_images + (kb + 1) * kb_stride + HB, vt[sl ^ 1], tid);
+        }
         if constexpr (CODES) {
             if (kb + 2 < kb1 && (kb + 2) % kbs.bpc == 0) scales_to_lds((kb + 2) / kbs.bpc);
             if (kb > kb0 && kb % kbs.bpc == 0) scale_sums(kb / kbs.bpc, 2);  // block kb begins a chunk
@@ -1082,53 +1283,58 @@ bool kv_images_apply(int kv_format, int d, int heads) {
     return kv_format >= TAH_KV_F32 && kv_format <= TAH_KV_I8 && heads > 0 && d == 64 * heads;
 }
 
+// The tiles, then (256-aligned) a 256-byte slot for f32 and i16's maxima, then the i8 scales or the i16 factors.
 size_t kv_images_bytes(int rows, int chunk, int heads, int kv_format) {
-    const bool codes = kv_format == TAH_KV_I8;
-    const size_t tail =
-        codes ? (size_t)key_blocks(rows, chunk).n_chunks * heads * SCL : sizeof(uint32_t) * 2 * (size_t)heads;
-    return ((image_bytes_of(rows, chunk, heads, codes) + 255) / 256) * 256 + 256 + tail;
+    const size_t chunks = key_blocks(rows, chunk).n_chunks;
+    const size_t tail = kv_format == TAH_KV_I8 ? chunks * heads * SCL
+                                                : (kv_format == TAH_KV_I16 ? chunks * heads * FAC : 0);
+    return ((image_bytes_of(rows, chunk, heads, kv_format) + 255) / 256) * 256 +
+           ((sizeof(uint32_t) * 2 * (size_t)heads + 255) / 256) * 256 + tail;
 }
 
 template <int FMT>
-static void launch_images(hipStream_t s, int rows, int chunk, int d, int heads, const uint8_t *records, KvImages img) {
+static void launch_absmax(hipStream_t s, int rows, int chunk, int d, int heads, const uint8_t *records, KvImages img) {
     const KeyBlocks k = key_blocks(rows, chunk);
     hipLaunchKernelGGL(k_zero_u32, dim3((2 * heads + 63) / 64), dim3(64), 0, s, 2 * heads, img.kvmax);
     TAH_LAUNCHED();
     hipLaunchKernelGGL(k_kv_absmax<FMT>, dim3(k.n_kb, heads), dim3(256), 0, s, rows, chunk, d, heads, records, img.kvmax);
     TAH_LAUNCHED();
-    hipLaunchKernelGGL(k_kv_images<FMT>, dim3(k.n_kb, heads), dim3(256), 0, s, rows, chunk, d, heads, records, img.kvmax,
-                       img.images);
-    TAH_LAUNCHED();
 }
 
 void kv_images(hipStream_t s, int rows, int chunk, int d, int heads, int kv_format, const uint8_t *records,
                KvImages img) {
-    if (!kv_images_apply(kv_format, d, heads)) throw ArgError{"key/value images need head width 64"};
-    if ((kv_format == TAH_KV_I8) != img.codes) throw ArgError{"key/value images: laid out for another format"};
-    if (img.codes) {
-        const KeyBlocks k = key_blocks(rows, chunk);
-        hipLaunchKernelGGL(k_kv_codes, dim3(k.n_kb, heads), dim3(256), 0, s, rows, chunk, d, heads, records,
-                           img.images, img.scales);
-        TAH_LAUNCHED();
-        return;
-    }
+    if (!kv_images_apply(kv_format, d, heads)) throw ArgError{"key/value tiles need head width 64"};
+    if (kv_format != img.fmt) throw ArgError{"key/value tiles: laid out for another format"};
+    const KeyBlocks k = key_blocks(rows, chunk);
     switch (kv_format) {
-        case TAH_KV_F32: launch_images<TAH_KV_F32>(s, rows, chunk, d, heads, records, img); break;
-        case TAH_KV_I16: launch_images<TAH_KV_I16>(s, rows, chunk, d, heads, records, img); break;
-        default: launch_images<TAH_KV_I8>(s, rows, chunk, d, heads, records, img); break;
+        case TAH_KV_F32:
+            launch_absmax<TAH_KV_F32>(s, rows, chunk, d, heads, records, img);
+            hipLaunchKernelGGL(k_kv_images<TAH_KV_F32>, dim3(k.n_kb, heads), dim3(256), 0, s, rows, chunk, d, heads,
+                               records, img.kvmax, img.images);
+            break;
+        case TAH_KV_I16:
+            launch_absmax<TAH_KV_I16>(s, rows, chunk, d, heads, records, img);
+            hipLaunchKernelGGL(k_kv_tiles16, dim3(k.n_kb, heads), dim3(256), 0, s, rows, chunk, d, heads, records,
+                               img.kvmax, img.images, img.scales);
+            break;
+        default:
+            hipLaunchKernelGGL(k_kv_codes, dim3(k.n_kb, heads), dim3(256), 0, s, rows, chunk, d, heads, records,
+                               img.images, img.scales);
+            break;
     }
+    TAH_LAUNCHED();
 }
 
 KvImages kv_images_at(uint8_t *base, int rows, int chunk, int heads, int kv_format) {
     KvImages img;
-    img.codes = kv_format == TAH_KV_I8;
+    img.fmt = kv_format;
     img.images = base;
-    uint8_t *tail = base + ((image_bytes_of(rows, chunk, heads, img.codes) + 255) / 256) * 256;
-    if (img.codes) img.scales = reinterpret_cast<float *>(tail);
-    else img.kvmax = reinterpret_cast<uint32_t *>(tail);
+    uint8_t *tail = base + ((image_bytes_of(rows, chunk, heads, kv_format) + 255) / 256) * 256;
+    img.kvmax = reinterpret_cast<uint32_t *>(tail);
+    if (kv_format != TAH_KV_F32)
+        img.scales = reinterpret_cast<float *>(tail + ((sizeof(uint32_t) * 2 * (size_t)heads + 255) / 256) * 256);
     return img;
 }
-
 
 static AttnPlan plan(const AttnShape &a, bool images) {
     AttnPlan p;
@@ -1136,8 +1342,8 @@ static AttnPlan plan(const AttnShape &a, bool images) {
     const int hd = a.d / a.heads;
     p.split16 = hd == 64 && a.nq >= SPLIT16_MIN_Q && images && kv_images_apply(a.kv_format, a.d, a.heads);
     // k_attn_split64: 256 queries a workgroup (one a compute unit, one wave of them) from 512 queries on, else 128
-    // (two a compute unit, two waves of them)
-    p.waves = p.split16 && a.nq >= 512 ? 8 : 4;
+    // (two a compute unit, two waves of them); an i16 layer's (whose staging takes 33 KB of LDS more) always 256
+    p.waves = p.split16 && (a.nq >= 512 || a.kv_format == TAH_KV_I16) ? 8 : 4;
     const int per_group = p.split16 ? 32 * p.waves : QG;
     p.groups = (a.nq + per_group - 1) / per_group;
     // enough workgroups to fill the 256 compute units about once (twice for the smaller workgroups of two or more
@@ -1157,8 +1363,8 @@ static AttnPlan plan(const AttnShape &a, bool images) {
     return p;
 }
 
-// Every caller makes a layer's tile images from TAH_SPLIT16_MIN_Q queries on where they apply (head width 64), and
-// attention() refuses such a shape without them: the plan below is the one that runs.
+// Callers hand a layer of head width 64 over as tiles from TAH_SPLIT16_MIN_Q queries on (a fitted model's layers at
+// any query count), and attention() refuses such a shape without them: the plan below is the one that runs.
 static bool images_expected(const AttnShape &a) {
     return a.nq >= TAH_SPLIT16_MIN_Q && kv_images_apply(a.kv_format, a.d, a.heads);
 }
@@ -1171,15 +1377,29 @@ size_t attention_work_bytes(const AttnShape &a) {
 }
 
 template <int FMT>
-static void launch(hipStream_t s, const AttnShape &a, const AttnPlan &p, const float *q, const uint8_t *records, float *out,
-                   float *part_o, float *part_ml) {
-    if (a.d / a.heads == 64) {
-        hipLaunchKernelGGL(k_attn_decode_w<FMT>, dim3(p.splits, a.heads, p.groups), dim3(256), 0, s, a.nq, a.rows,
-                           a.chunk, a.d, a.heads, q, records, p.kb_per_split, part_o, part_ml, out);
+static void launch(hipStream_t s, const AttnShape &a, const AttnPlan &p, const float *q, const uint8_t *records,
+                   const KvImages *img, float *out, float *part_o, float *part_ml) {
+    if (img) {
+        hipLaunchKernelGGL((k_attn_decode_w<FMT, true>), dim3(p.splits, a.heads, p.groups), dim3(256), 0, s, a.nq,
+                           a.rows, a.chunk, a.d, a.heads, q, img->images, img->kvmax, img->scales, p.kb_per_split,
+                           part_o, part_ml, out);
+    } else if (a.d / a.heads == 64) {
+        hipLaunchKernelGGL((k_attn_decode_w<FMT, false>), dim3(p.splits, a.heads, p.groups), dim3(256), 0, s, a.nq,
+                           a.rows, a.chunk, a.d, a.heads, q, records, nullptr, nullptr, p.kb_per_split, part_o,
+                           part_ml, out);
     } else {
         hipLaunchKernelGGL(k_attn_decode<FMT>, dim3(p.splits, a.heads, p.groups), dim3(64), 0, s, a.nq, a.rows, a.chunk,
                            a.d, a.heads, q, records, p.kb_per_split, part_o, part_ml, out);
     }
+    TAH_LAUNCHED();
+}
+
+template <int WAVES, int FMT>
+static void launch_split(hipStream_t s, const AttnShape &a, const AttnPlan &p, const float *q, const KvImages &img,
+                         float *out, float *part_o, float *part_ml) {
+    hipLaunchKernelGGL((k_attn_split64<WAVES, FMT>), dim3(p.groups * a.heads * p.splits), dim3(64 * WAVES), 0, s, a.nq,
+                       a.rows, a.chunk, a.d, a.heads, q, img.images, img.kvmax, img.scales, p.kb_per_split, p.groups,
+                       p.splits, part_o, part_ml, out);
     TAH_LAUNCHED();
 }
 
@@ -1250,7 +1470,10 @@ void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t 
         throw ArgError{"attention: head width must divide d and be at most 64, rows and chunk positive"};
     if ((size_t)a.nq > (size_t)65535 * 8) throw ArgError{"attention: too many queries for one launch"};
     const bool have = img != nullptr && img->images != nullptr;
-    if (images_expected(a) && !have) throw ArgError{"attention: head width 64 from 4 queries on needs the tile images"};
+    if (images_expected(a) && !have) throw ArgError{"attention: head width 64 from 4 queries on needs the tiles"};
+    if (have && (img->fmt != a.kv_format || !kv_images_apply(a.kv_format, a.d, a.heads)))
+        throw ArgError{"attention: tiles of another cache format or shape"};
+    if (!have && !records) throw ArgError{"attention: neither records nor tiles"};
     const AttnPlan p = plan(a, have);
     float *part_o = nullptr, *part_ml = nullptr;
     if (p.splits > 1) {
@@ -1260,30 +1483,22 @@ void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t 
     if (p.split16) {
         hipEvent_t *pe = probe_slot(s);
         if (pe) TAH_HIP(hipEventRecord(pe[0], s));
-        const dim3 grid(p.groups * a.heads * p.splits);
-        if (img->codes != (a.kv_format == TAH_KV_I8)) throw ArgError{"attention: images of another cache format"};
-        if (p.waves == 8 && img->codes)
-            hipLaunchKernelGGL((k_attn_split64<8, true>), grid, dim3(512), 0, s, a.nq, a.rows, a.chunk, a.d, a.heads, q,
-                               img->images, nullptr, img->scales, p.kb_per_split, p.groups, p.splits, part_o, part_ml,
-                               out);
-        else if (p.waves == 8)
-            hipLaunchKernelGGL((k_attn_split64<8, false>), grid, dim3(512), 0, s, a.nq, a.rows, a.chunk, a.d, a.heads,
-                               q, img->images, img->kvmax, nullptr, p.kb_per_split, p.groups, p.splits, part_o, part_ml,
-                               out);
-        else if (img->codes)
-            hipLaunchKernelGGL((k_attn_split64<4, true>), grid, dim3(256), 0, s, a.nq, a.rows, a.chunk, a.d, a.heads, q,
-                               img->images, nullptr, img->scales, p.kb_per_split, p.groups, p.splits, part_o, part_ml,
-                               out);
-        else
-            hipLaunchKernelGGL((k_attn_split64<4, false>), grid, dim3(256), 0, s, a.nq, a.rows, a.chunk, a.d, a.heads,
-                               q, img->images, img->kvmax, nullptr, p.kb_per_split, p.groups, p.splits, part_o, part_ml,
-                               out);
-        TAH_LAUNCHED();
+        switch (a.kv_format) {
+            case TAH_KV_F32:
+                if (p.waves == 8) launch_split<8, TAH_KV_F32>(s, a, p, q, *img, out, part_o, part_ml);
+                else launch_split<4, TAH_KV_F32>(s, a, p, q, *img, out, part_o, part_ml);
+                break;
+            case TAH_KV_I16: launch_split<8, TAH_KV_I16>(s, a, p, q, *img, out, part_o, part_ml); break;
+            default:
+                if (p.waves == 8) launch_split<8, TAH_KV_I8>(s, a, p, q, *img, out, part_o, part_ml);
+                else launch_split<4, TAH_KV_I8>(s, a, p, q, *img, out, part_o, part_ml);
+                break;
+        }
         if (pe) TAH_HIP(hipEventRecord(pe[1], s));
     } else switch (a.kv_format) {
-        case TAH_KV_F32: launch<TAH_KV_F32>(s, a, p, q, records, out, part_o, part_ml); break;
-        case TAH_KV_I16: launch<TAH_KV_I16>(s, a, p, q, records, out, part_o, part_ml); break;
-        case TAH_KV_I8: launch<TAH_KV_I8>(s, a, p, q, records, out, part_o, part_ml); break;
+        case TAH_KV_F32: launch<TAH_KV_F32>(s, a, p, q, records, have ? img : nullptr, out, part_o, part_ml); break;
+        case TAH_KV_I16: launch<TAH_KV_I16>(s, a, p, q, records, have ? img : nullptr, out, part_o, part_ml); break;
+        case TAH_KV_I8: launch<TAH_KV_I8>(s, a, p, q, records, have ? img : nullptr, out, part_o, part_ml); break;
         default: throw ArgError{"attention: unknown key/value format"};
     }
     if (p.splits > 1) {

@@ -254,21 +254,22 @@ size_t attention_work_bytes(const AttnShape &a);
 void to_records(hipStream_t s, int rows, int d, int chunk, const float *kv, float *rec32);
 // f32 chunk records to i16/i8 records (the reference's quantiser, bit for bit).
 void pack(hipStream_t s, int rows, int d, int chunk, int fmt, const float *rec32, uint8_t *recq);
-// Keys and values of one layer (any format, dequantised) as fp16 hi/lo tile images (head width 64 only), with each
-// head's largest magnitudes: the split-fp16 attention kernel's input, built once per stored layer.
+// Keys and values of one stored layer as tiles per (key block of 64, head), the form a fitted layer of head width 64
+// is held in on the card (its records are not kept) and the attention kernels read: f32 as fp16 hi/lo split images,
+// i16 as code tiles with dequantisation factors, i8 as fp16 code images with the chunks' scales (attention.hip).
 struct KvImages {
     uint8_t *images = nullptr;
-    uint32_t *kvmax = nullptr;  // f32 and i16: the heads' largest |K|, |V|
-    float *scales = nullptr;    // i8 (codes): per (chunk, head) the key then value scales
-    bool codes = false;         // i8: the images hold the codes, not split values
+    uint32_t *kvmax = nullptr;  // f32 and i16: the heads' largest |K|, |V| (dequantised)
+    float *scales = nullptr;    // i8: per (chunk, head) the key scales, value scales and ratios; i16: the factors
+    int fmt = TAH_KV_F32;       // the stored format the tiles were made from
 };
 bool kv_images_apply(int kv_format, int d, int heads);
 size_t kv_images_bytes(int rows, int chunk, int heads, int kv_format);
 KvImages kv_images_at(uint8_t *base, int rows, int chunk, int heads, int kv_format);
 void kv_images(hipStream_t s, int rows, int chunk, int d, int heads, int kv_format, const uint8_t *records,
                KvImages img);
-// img (optional): the layer's images, used for 32 queries or more.
-// Queries from which the attention runs on the matrix cores over tile images (made for transient layers from then on)
+// Queries from which the attention runs on the matrix cores over tile images (made for transient f32 layers of the
+// fit from then on; a fitted model's layers of head width 64 are held as tiles at any query count)
 constexpr int TAH_SPLIT16_MIN_Q = 4;
 
 // Launch probe of the many-query attention kernel (attention.hip): arm for a stream with room for `launches`
@@ -276,6 +277,8 @@ constexpr int TAH_SPLIT16_MIN_Q = 4;
 // summed duration in ms.
 void probe_arm(hipStream_t s, int launches);
 int probe_read(hipStream_t s, double *ms);
+// Over the layer's tiles when img holds them (any query count), else over its chunk records (head width 64: fewer
+// than TAH_SPLIT16_MIN_Q queries only).
 void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t *records, float *out, void *work,
                const KvImages *img = nullptr);
 

@@ -160,6 +160,22 @@ __device__ __forceinline__ void split8(const float *v, float f, halfx8 &hi, half
     lo = __builtin_bit_cast(halfx8, lw);
 }
 
+// eight int16 codes (16 bytes, in order) times their factors f, in f32, as hi/lo halves: the dequantised values of
+// an i16 cache, split as split8 splits floats
+__device__ __forceinline__ void dequant_split8(uint4 codes, const float (&f)[8], halfx8 &hi, halfx8 &lo) {
+    const uint32_t w[4] = {codes.x, codes.y, codes.z, codes.w};
+    u32x4 hw, lw;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        uint32_t a, b;
+        split2((float)(int16_t)(w[t] & 0xffffu) * f[2 * t], (float)(int16_t)(w[t] >> 16) * f[2 * t + 1], a, b);
+        hw[t] = a;
+        lw[t] = b;
+    }
+    hi = __builtin_bit_cast(halfx8, hw);
+    lo = __builtin_bit_cast(halfx8, lw);
+}
+
 // Row i of a 32-row MFMA A operand holding row sigma(i) (bits 3 and 2 swapped): the accumulators v = 8 hh .. 8 hh + 7
 // of lane l of a 32 x 32 v_mfma_f32_32x32x16 result then hold rows 16 hh + 8 (l / 32) + 0..7 -- eight consecutive
 // rows, which is how a B operand of a following product over those rows wants them.
