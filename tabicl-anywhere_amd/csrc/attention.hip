@@ -34,10 +34,12 @@ namespace tah {
 
 constexpr int KB = 64;   // keys per block
 constexpr int QG = 8;    // queries per decode workgroup
-// From this many queries the matrix kernel (one read of the images for up to 128 queries) beats the decode kernel
-// (whose work grows with the queries: 3 rows 0.888 ms a prediction either way, 4 rows 0.924 -> 0.902 ms, 8 rows
-// 1.127 -> 0.913 ms with the matrix kernel)
-constexpr int SPLIT16_MIN_Q = TAH_SPLIT16_MIN_Q;
+// Queries from which a layer's tiles are read by the matrix kernel rather than the decode kernel. Over f32 images and
+// i8 code images from one query: the matrix kernel reads a tile with whole-row DMA copies, where the decode kernel's
+// lanes each read a row of their own (one row: 0.694 -> 0.575 ms a prediction, 0.595 ms from the records before the
+// layers were held as tiles). Over i16 code tiles from 4 (its kernel has 8 wavefronts and a staging ring, one
+// workgroup a compute unit: one row after a MALL flush 0.813 -> 0.930 ms with it).
+inline int split16_min_q(int kv_format) { return kv_format == TAH_KV_I16 ? TAH_SPLIT16_MIN_Q : 1; }
 
 struct KeyBlocks {
     int bpc;       // key blocks per full chunk
@@ -325,8 +327,9 @@ __device__ __forceinline__ void tile_row(const uint8_t *tile, int r, float (&v)[
             const halfx8 hi = *reinterpret_cast<const halfx8 *>(tile + off);
             if constexpr (FMT == TAH_KV_F32) {
                 const halfx8 lo = *reinterpret_cast<const halfx8 *>(tile + off + 8192);
+                const u32x4 hw = __builtin_bit_cast(u32x4, hi), lw = __builtin_bit_cast(u32x4, lo);
 #pragma unroll
-                for (int t = 0; t < 8; t++) v[8 * c + t] = (float)hi[t] + (float)lo[t];
+                for (int t = 0; t < 4; t++) join2(hw[t], lw[t], v[8 * c + 2 * t], v[8 * c + 2 * t + 1]);
             } else {
 #pragma unroll
                 for (int t = 0; t < 8; t++) v[8 * c + t] = (float)hi[t];
@@ -1340,7 +1343,7 @@ static AttnPlan plan(const AttnShape &a, bool images) {
     AttnPlan p;
     const KeyBlocks k = key_blocks(a.rows, a.chunk);
     const int hd = a.d / a.heads;
-    p.split16 = hd == 64 && a.nq >= SPLIT16_MIN_Q && images && kv_images_apply(a.kv_format, a.d, a.heads);
+    p.split16 = hd == 64 && a.nq >= split16_min_q(a.kv_format) && images && kv_images_apply(a.kv_format, a.d, a.heads);
     // k_attn_split64: 256 queries a workgroup (one a compute unit, one wave of them) from 512 queries on, else 128
     // (two a compute unit, two waves of them); an i16 layer's (whose staging takes 33 KB of LDS more) always 256
     p.waves = p.split16 && (a.nq >= 512 || a.kv_format == TAH_KV_I16) ? 8 : 4;
@@ -1369,11 +1372,15 @@ static bool images_expected(const AttnShape &a) {
     return a.nq >= TAH_SPLIT16_MIN_Q && kv_images_apply(a.kv_format, a.d, a.heads);
 }
 
+// Room for the split partials of whichever plan runs: over tiles where they apply (a fitted layer of head width 64 is
+// read as tiles at any query count), or below TAH_SPLIT16_MIN_Q queries also over records (a transient layer).
 size_t attention_work_bytes(const AttnShape &a) {
-    const AttnPlan p = plan(a, images_expected(a));
-    if (p.splits == 1) return 0;
+    const bool tiles = kv_images_apply(a.kv_format, a.d, a.heads);
+    int splits = plan(a, tiles).splits;
+    if (!images_expected(a)) splits = std::max(splits, plan(a, false).splits);
+    if (splits == 1) return 0;
     const int hd = a.d / a.heads;
-    return sizeof(float) * (size_t)p.splits * a.nq * a.heads * (hd + 2) + 256;
+    return sizeof(float) * (size_t)splits * a.nq * a.heads * (hd + 2) + 256;
 }
 
 template <int FMT>

@@ -146,6 +146,13 @@ __device__ __forceinline__ void split2(float a, float b, uint32_t &hi, uint32_t 
     lo = bits(__builtin_amdgcn_cvt_pkrtz(ra, rb));
 }
 
+// The floats hi + lo of two split values (hi: their two fp16 high halves, lo: their low halves), exact, one
+// v_fma_mix_f32 each (hi * 1 + lo with both read as fp16).
+__device__ __forceinline__ void join2(uint32_t hi, uint32_t lo, float &x, float &y) {
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,1]" : "=v"(x) : "v"(hi), "v"(lo));
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,1] op_sel_hi:[1,0,1]" : "=v"(y) : "v"(hi), "v"(lo));
+}
+
 // eight floats times f (a power of two) as hi/lo halves
 __device__ __forceinline__ void split8(const float *v, float f, halfx8 &hi, halfx8 &lo) {
     u32x4 hw, lw;
