@@ -4,16 +4,16 @@ comparison would span twelve layers of rounding:
 
 * 10,000 x 100, 10 classes, f32, 1 member: the column cache of three feature groups against the oracle's column
   stage over all rows; sampled rows' representations from the card's column cache; every layer's keys and values of
-  64 sampled training rows, each layer recomputed from the card's records of the layer before; 2,048 predictions,
-  64 of them against the oracle over the card's caches.
+  64 sampled training rows, each layer recomputed from the card's records of the layer before; all 2,048
+  predictions against the oracle over the card's caches (scores and probabilities).
 * The same table, 8 members (feature orders and class shifts, both normalisations) with i16 and i8 caches: each
   quantised build bit for bit the quantiser applied to the card's f32 build; ensemble probabilities of 2,048 rows,
-  16 against the oracle over the same caches; the quantised caches' probabilities against the f32 ones.
+  128 against the oracle over the same caches; the quantised caches' probabilities against the f32 ones.
 * 50,000 x 200 regression table (skewed, categorical and missing cells, preprocessed), 8 members, f32 cache:
-  per-layer and representation checks on one member, raw outputs and quantile statistics of sampled rows of every
-  member against the oracle.
+  per-layer and representation checks on one member, raw outputs and quantile statistics of 32 sampled rows of
+  every member against the oracle.
 * 100,000 x 100, 120 classes (label digits [5, 5, 5], a 31-node class tree), i16 cache, then 2,048 predictions with
-  a 256 MB working-memory budget: the plan, sampled representations, and sampled scores against the oracle over
+  a 256 MB working-memory budget: the plan, 32 sampled rows' representations and scores against the oracle over
   the card's caches; the budgeted answers equal the unbudgeted ones.
 """
 import sys
@@ -112,7 +112,7 @@ def test_config3_ensemble_i16_i8(gpu, clf):
     say(f"config 3: {len(members)} members, i16 and i8 caches, {nt} rows")
     w = gpu.weights(m)
     rng = np.random.default_rng(33)
-    ts = np.sort(rng.choice(nt, 16, replace=False))
+    ts = np.sort(rng.choice(nt, 128, replace=False))
     sums = {fmt: np.zeros((nt, classes)) for fmt in (abi.KV_F32, abi.KV_I16, abi.KV_I8)}
     want_sums = {fmt: np.zeros((len(ts), classes)) for fmt in (abi.KV_I16, abi.KV_I8)}
     for i, mb in enumerate(members):
@@ -165,7 +165,7 @@ def test_config4_regression_50k(gpu):
     members = P.ensemble(len(prep.keep), 1, 2, 8, 42)
     w = gpu.weights(m)
     rng = np.random.default_rng(44)
-    ts = np.sort(rng.choice(nt, 8, replace=False))
+    ts = np.sort(rng.choice(nt, 32, replace=False))
     alphas = np.array([0.05, 0.95])
     out = dict(mean=np.zeros(nt), variance=np.zeros(nt), median=np.zeros(nt), quantiles=np.zeros((nt, 2)))
     for i, mb in enumerate(members):
@@ -190,7 +190,7 @@ def test_config4_regression_50k(gpu):
         host = np.array([[d.mean(), d.variance(), d.icdf(0.5)] + [d.icdf(a) for a in alphas]
                          for d in map(T.QuantileDist, want)])
         serr = float(np.abs(st - host).max())
-        say(f"  member {i}: raw outputs of 8 sampled rows {err:.2e}, their statistics {serr:.2e}")
+        say(f"  member {i}: raw outputs of 32 sampled rows {err:.2e}, their statistics {serr:.2e}")
         assert err < KV_TOL and serr < KV_TOL
         T.add_regression(out, q, alphas, ym, ys, gpu=gpu)
         del layers
@@ -241,14 +241,14 @@ def test_config5_many_classes_100k(gpu, clf):
     assert peak <= 256 << 20 and gpu.overdrawn() == 0
     assert np.abs(budgeted - whole).max() < 1e-5
     rng = np.random.default_rng(55)
-    ts = np.sort(rng.choice(nt, 8, replace=False))
+    ts = np.sort(rng.choice(nt, 32, replace=False))
     fo = orc.Fitted(rows, features, classes, chunk, abi.KV_I16, f.plan, f.col_kv, f.scales, f.layers)
     t0 = time.perf_counter()
     want_rep = orc.represent(m, orc.embed(m, fo, xt[ts]))
     err_rep = float(np.abs(rep[ts] - want_rep).max())
     want = orc.predict_raw(m, fo, xt[ts])
     err = float(np.abs(whole[ts] - want).max())
-    say(f"  8 sampled rows: representations {err_rep:.2e}, scores {err:.2e} (oracle {time.perf_counter() - t0:.1f} s)")
+    say(f"  32 sampled rows: representations {err_rep:.2e}, scores {err:.2e} (oracle {time.perf_counter() - t0:.1f} s)")
     assert err_rep < KV_TOL and err < KV_TOL
     acc = float(np.mean(np.argmax(whole, axis=1) == W.mixture_rows(means, nt, seed=62)[1]))
     say(f"  accuracy on the mixture's test rows {acc:.3f}")

@@ -197,11 +197,12 @@ def test_stage_full_size(gpu, full_model, full_weights, kv_format, nq):
     assert err < SCORE_TOL
 
 
-@pytest.mark.parametrize("kv_format", [abi.KV_F32, abi.KV_I8])
-@pytest.mark.parametrize("nq,rows", [(1024, 3000), (2048, 10000)])
-def test_stage_large_batches_sampled(gpu, full_model, full_weights, kv_format, nq, rows):
-    """The whole in-context stage for a large batch (the attention's few key ranges merged inside the output
-    projection), 24 of its rows against the oracle on the same inputs (rows are independent)."""
+@pytest.mark.parametrize("kv_format", [abi.KV_F32, abi.KV_I16, abi.KV_I8])
+@pytest.mark.parametrize("nq,rows,checked", [(1024, 3000, 1024), (2048, 10000, 256)])
+def test_stage_large_batches_sampled(gpu, full_model, full_weights, kv_format, nq, rows, checked):
+    """The whole in-context stage for a large batch (the 8-wavefront attention kernel, few key ranges, the split-K
+    dense layers), `checked` of its rows against the oracle on the same inputs (rows are independent): all 1,024 at
+    3,000 stored rows, 256 at 10,000."""
     say(f"stage large batch fmt={kv_format} nq={nq} rows={rows}")
     rng = np.random.default_rng(nq + rows + kv_format)
     d, L, chunk = full_model.d, full_model.icl_layers, 256
@@ -210,7 +211,7 @@ def test_stage_large_batches_sampled(gpu, full_model, full_weights, kv_format, n
     vm = gpu.load(full_weights, kv_format, rows, chunk, layers, scales)
     h = rng.standard_normal((nq, d)).astype(np.float32)
     got = gpu.in_context(full_weights, vm, h, 10)
-    sample = np.sort(rng.choice(nq, 24, replace=False))
+    sample = np.sort(rng.choice(nq, checked, replace=False))
     want = orc.in_context(full_model, scales, layers, kv_format, rows, chunk, h[sample], 10)
     vm.free()
     err = np.abs(got[sample] - want).max()
