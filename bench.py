@@ -22,7 +22,7 @@ decoder 1024 -> 10). Synthetic table: X ~ N(0, 1) of 10,000 training + 2,048 tes
 * regression_head: 2,048 rows x 8 members of 999 predicted quantiles read as distributions on the card (mean,
   variance, median and six quantiles a row, tah_quantile_stats), and a sample of rows through the host statement.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--cpu-fit-rows N]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--cpu-fit-rows N] [--rows-only N --kv FMT]
 """
 import argparse
 import importlib
@@ -95,6 +95,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (for profiler runs)")
     ap.add_argument("--cpu-fit-rows", type=int, default=2500,
                     help="training rows of the CPU fit sample (10000: the whole table, about a minute of CPU work)")
+    ap.add_argument("--rows-only", type=int, default=0,
+                    help="profiling: after the fit, only predict this many rows 45 times (5 warm-up) and print the time")
+    ap.add_argument("--kv", choices=("f32", "i16", "i8"), default="f32", help="cache format of --rows-only")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}); multi-GPU sharding is a design note, not built",
@@ -114,6 +117,29 @@ def main():
     gpu = hip.Gpu(0)
     log("device:", gpu.name)
     w = gpu.weights(model)
+
+    if args.rows_only > 0:
+        # a profiler's view of one batch size: the fit in the chosen format, then 45 predictions of that many rows
+        fmt = {"f32": abi.KV_F32, "i16": abi.KV_I16, "i8": abi.KV_I8}[args.kv]
+        n = min(args.rows_only, BATCH)
+        fq = fitmod.fit_raw(gpu, w, x_train, y_train, CLASSES, CHUNK, fmt)
+        vq = gpu.load(w, fmt, ROWS, CHUNK, fq.layers[0], fq.scales[0])
+        vq.set_columns(fq.col_kv, FEATURES, 1)
+        xq, oq = dm.DeviceBuffer.of(x_test), dm.DeviceBuffer(BATCH * CLASSES * 4)
+        for _ in range(5):
+            gpu.predict_dev(w, vq, xq.ptr, n, CLASSES, oq.ptr)
+        gpu.sync()
+        tq = dm.EventTimer(gpu.stream)
+        tq.start()
+        for _ in range(40):
+            gpu.predict_dev(w, vq, xq.ptr, n, CLASSES, oq.ptr)
+        log(f"prediction, {n} rows, {args.kv} cache: {tq.stop() / 40:.4f} ms (45 predictions after the fit)")
+        for b in (xq, oq):
+            b.free()
+        vq.free()
+        w.free()
+        gpu.close()
+        return
 
     # ---- fit on the card ------------------------------------------------------------------------------------
     fitmod.fit_raw(gpu, w, x_train[:1000], y_train[:1000], CLASSES, CHUNK)  # warm-up (kernels loaded, pool grown)
