@@ -151,15 +151,15 @@ constexpr int IMG = 32768;
 // value scales at the end).
 constexpr int IMG8 = 16384;
 constexpr int SCL = 768;  // bytes of one (chunk, head)'s scales
-// i16 caches: code tiles, 16 KB per (key block, head): the K codes as [64 keys][64 coordinates] then the V codes as
-// [64 coordinates][64 keys], int16, each 128-byte row in order (not swizzled: the attention kernel swizzles as it
-// writes its LDS images, and the decode kernel reads whole rows), zeros past a short block's end. The codes are not
-// exact in fp16 (up to 32767), so the attention kernel dequantises them itself: beside the tiles, per (chunk, head),
-// 64 key factors then 64 value factors, each the chunk's scale of that coordinate times 2^sk (2^sv), the power of
-// two that brings the head's largest dequantised |K| (|V|) below 2^14, as for f32 images (kvmax, the maxima, [heads][2]
-// in front of the factors): factor table [chunks][heads][2][64].
-constexpr int IMG16 = 16384;
-constexpr int FAC = 512;  // bytes of one (chunk, head)'s factors
+// i16 caches: code tiles, 16.5 KB per (key block, head): the K codes as [64 keys][64 coordinates], then the block's
+// chunk's 64 key factors, then the V codes as [64 coordinates][64 keys], then its 64 value factors; int16 codes in
+// 128-byte rows in order (not swizzled: the attention kernel swizzles as it writes its LDS images, and the decode
+// kernel reads whole rows), zeros past a short block's end. The codes are not exact in fp16 (up to 32767), so the
+// attention kernel dequantises them itself: each factor is the chunk's scale of that coordinate times 2^sk (2^sv),
+// the power of two that brings the head's largest dequantised |K| (|V|) below 2^14, as for f32 images (kvmax, the
+// maxima, [heads][2]). Every block carries its chunk's factors, so that one copy brings a half tile and its factors.
+constexpr int HALF16 = 8192 + 256;  // a half tile: 64 rows of codes, then 64 factors
+constexpr int IMG16 = 2 * HALF16;
 
 __host__ __device__ constexpr int img_bytes(int fmt) { return fmt == TAH_KV_F32 ? IMG : (fmt == TAH_KV_I16 ? IMG16 : IMG8); }
 
@@ -315,7 +315,7 @@ __device__ __forceinline__ void tile_row(const uint8_t *tile, int r, float (&v)[
 #pragma unroll
     for (int c = 0; c < 8; c++) {
         if constexpr (FMT == TAH_KV_I16) {
-            const uint4 x = *reinterpret_cast<const uint4 *>(tile + (VALS ? 8192 : 0) + r * 128 + c * 16);
+            const uint4 x = *reinterpret_cast<const uint4 *>(tile + (VALS ? HALF16 : 0) + r * 128 + c * 16);
             const uint32_t w[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
             for (int t = 0; t < 4; t++) {
@@ -398,9 +398,8 @@ __global__ __launch_bounds__(256) void k_attn_decode_w(int nq, int rows, int chu
                 ks = uk;
                 vs = uv;
             } else if constexpr (FMT == TAH_KV_I16) {
-                const float *fac = scl + ((size_t)ci * heads + h) * 128;
-                ks = fac[lane] * uk;
-                vs = fac[64 + lane] * uv;
+                ks = reinterpret_cast<const float *>(tile + 8192)[lane] * uk;
+                vs = reinterpret_cast<const float *>(tile + HALF16 + 8192)[lane] * uv;
             } else {
                 const float *sc8 = scl + ((size_t)ci * heads + h) * 192;
                 ks = sc8[lane];
@@ -629,13 +628,11 @@ __global__ __launch_bounds__(256) void k_kv_codes(int rows, int chunk, int d, in
     }
 }
 
-// grid (key blocks, heads); 256 threads: one code tile of an i16 layer, and (by a chunk's first block) the chunk's
-// dequantisation factors of the head. Thread t: coordinate t / 4, keys 16 (t % 4) .. + 15 of the block (zeros past
+// grid (key blocks, heads); 256 threads: one code tile of an i16 layer with its chunk's dequantisation factors. Thread t: coordinate t / 4, keys 16 (t % 4) .. + 15 of the block (zeros past
 // its end). kvmax (k_kv_absmax) holds the head's largest dequantised |K| and |V|.
 __global__ __launch_bounds__(256) void k_kv_tiles16(int rows, int chunk, int d, int heads,
                                                     const uint8_t *__restrict__ records,
-                                                    const uint32_t *__restrict__ kvmax, uint8_t *__restrict__ tiles,
-                                                    float *__restrict__ factors) {
+                                                    const uint32_t *__restrict__ kvmax, uint8_t *__restrict__ tiles) {
     __shared__ int16_t Ks[64][KB + 8];  // [coordinate][key]
     const int kb = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
     const KeyBlocks kbs = key_blocks(rows, chunk);
@@ -652,14 +649,14 @@ __global__ __launch_bounds__(256) void k_kv_tiles16(int rows, int chunk, int d, 
         vv[i] = in ? vr[seg + i] : (int16_t)0;
     }
     // V codes: row lc, keys seg .. seg + 15
-    *reinterpret_cast<uint4 *>(tile + 8192 + lc * 128 + seg * 2) = *reinterpret_cast<const uint4 *>(vv);
-    *reinterpret_cast<uint4 *>(tile + 8192 + lc * 128 + seg * 2 + 16) = *reinterpret_cast<const uint4 *>(vv + 8);
-    if (kb % kbs.bpc == 0 && tid < 128) {
-        // the record's scales: d key scales then d value scales
-        const int ci = kb / kbs.bpc, c = tid & 63, which = tid >> 6;
+    *reinterpret_cast<uint4 *>(tile + HALF16 + lc * 128 + seg * 2) = *reinterpret_cast<const uint4 *>(vv);
+    *reinterpret_cast<uint4 *>(tile + HALF16 + lc * 128 + seg * 2 + 16) = *reinterpret_cast<const uint4 *>(vv + 8);
+    if (tid < 128) {
+        // the record's scales (d key scales then d value scales) times the head's powers of two, after each half
+        const int c = tid & 63, which = tid >> 6;
         const float *sc = reinterpret_cast<const float *>(w.rec);
         const float f = ldexpf(1.0f, shift_for(kvmax[h * 2 + which]));
-        factors[((size_t)ci * heads + h) * 128 + tid] = sc[which * d + h * 64 + c] * f;
+        reinterpret_cast<float *>(tile + which * HALF16 + 8192)[c] = sc[which * d + h * 64 + c] * f;
     }
     __syncthreads();
     // K codes: row = key, 8 coordinates a 16-byte chunk
@@ -701,24 +698,23 @@ __global__ __launch_bounds__(256) void k_kv_tiles16(int rows, int chunk, int d, 
 template <int WAVES, int BYTES>
 __device__ __forceinline__ void half_image_to_lds(const uint8_t *src, uint8_t *dst, int tid) {
     constexpr int T = 64 * WAVES, CHUNKS = BYTES / 16;
+    static_assert(BYTES % 16 == 0, "whole 16-byte copies");
     const int w = tid >> 6;
 #pragma unroll
     for (int i = 0; i < (CHUNKS + T - 1) / T; i++) {
         const int base = i * T + 64 * w;
-        if (CHUNKS % T == 0 || base < CHUNKS)
+        // lanes past the last copy stay idle (a copy a lane: each writes its own 16 bytes at dst + 16 (base + lane))
+        if (CHUNKS % T == 0 || base + (tid & 63) < CHUNKS)
             __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint4 *>(src) + base + (tid & 63), dst + 16 * base, 16,
                                              0, 0);
     }
 }
 
-// i16 staging (k_attn_split64 with STAGED): half a code tile (8 KB, keys or values) into a staging slot's half by DMA,
-// and (wavefronts with fac_lanes: 16 lanes x 16 bytes) its chunk's 64 factors beside it.
+// i16 staging (k_attn_split64 with STAGED): half a code tile (8 KB of codes and its 256 bytes of factors, keys or
+// values) into a staging slot's half by DMA: 528 copies of 16 bytes, the last 16 by wavefront 0.
 template <int WAVES>
-__device__ __forceinline__ void stage_half16(const uint8_t *src, const float *fac, uint8_t *dst, uint8_t *fdst, int tid,
-                                             bool fac_lanes) {
-    half_image_to_lds<WAVES, IMG16 / 2>(src, dst, tid);
-    if (fac_lanes && (tid & 63) < 16)
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t *>(fac + 4 * (tid & 63)), fdst, 16, 0, 0);
+__device__ __forceinline__ void stage_half16(const uint8_t *src, uint8_t *dst, int tid) {
+    half_image_to_lds<WAVES, HALF16>(src, dst, tid);
 }
 
 // A staging slot's key codes into the split image kdst (K hi, K lo) and its value codes into vdst (V hi, V lo), either
@@ -733,7 +729,7 @@ __device__ __forceinline__ void convert16(const uint8_t *st, uint8_t *kdst, uint
         if (kdst) {
             // key r, coordinates 8 c .. 8 c + 7, each with its own factor
             float f[8];
-            load8(reinterpret_cast<const float *>(st + IMG16) + 8 * c, f);
+            load8(reinterpret_cast<const float *>(st + 8192) + 8 * c, f);
             halfx8 hi, lo;
             dequant_split8(*reinterpret_cast<const uint4 *>(st + r * 128 + c * 16), f, hi, lo);
             *reinterpret_cast<halfx8 *>(kdst + off) = hi;
@@ -741,10 +737,10 @@ __device__ __forceinline__ void convert16(const uint8_t *st, uint8_t *kdst, uint
         }
         if (vdst) {
             // coordinate r, keys 8 c .. 8 c + 7, one factor
-            const float fv = reinterpret_cast<const float *>(st + IMG16 + 256)[r];
+            const float fv = reinterpret_cast<const float *>(st + HALF16 + 8192)[r];
             const float f[8] = {fv, fv, fv, fv, fv, fv, fv, fv};
             halfx8 hi, lo;
-            dequant_split8(*reinterpret_cast<const uint4 *>(st + IMG16 / 2 + r * 128 + c * 16), f, hi, lo);
+            dequant_split8(*reinterpret_cast<const uint4 *>(st + HALF16 + r * 128 + c * 16), f, hi, lo);
             *reinterpret_cast<halfx8 *>(vdst + off) = hi;
             *reinterpret_cast<halfx8 *>(vdst + 8192 + off) = lo;
         }
@@ -764,8 +760,8 @@ struct Flag {
 // ring (DMA, two blocks ahead like the images), which a chunk's blocks use until the one after next begins.
 //
 // With an i16 cache (STAGED) the tiles hold codes (k_kv_tiles16), which are not exact in fp16: each half tile (8 KB of
-// codes) and its chunk's factors are copied into one of two LDS staging slots by DMA, one block earlier than an image
-// would be, and at the next step every thread dequantises 8 codes of each half (code times its coordinate's factor,
+// codes and its 256 bytes of factors) is copied into one of two LDS staging slots by DMA, one block earlier than an
+// image would be, and at the next step every thread dequantises 8 codes of each half (code times its coordinate's factor,
 // in f32) and writes them split into the same LDS images as an f32 layer's, which the rest of the kernel reads
 // unchanged. In step kb the staging slot of its parity holds keys kb + 2 and values kb + 1 (converted then), and the
 // copies bring keys kb + 3 and values kb + 2 into the other.
@@ -781,7 +777,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows
     constexpr bool STAGED = FMT == TAH_KV_I16;  // int16 code tiles dequantised into split images in the kernel
     constexpr int HB = CODES ? IMG8 / 2 : IMG / 2;  // bytes of an LDS image's keys (or values)
     constexpr int IS = img_bytes(FMT);              // bytes of a tile in memory
-    constexpr int SG = IMG16 + 2 * 256;             // STAGED: a staging slot, codes then key and value factors
+    constexpr int SG = IMG16;                       // STAGED: a staging slot, a whole code tile
     __shared__ __align__(16) uint8_t kt[2][HB], vt[2][HB];
     __shared__ __align__(16) float sb[CODES ? 4 : 1][192];  // CODES: scale ring, [chunk % 4][key, value, ratio]
     // CODES: each lane's 32 query coordinates, kept for the per-chunk splits: [wavefront][8 chunks of 4][lane][4];
@@ -807,15 +803,10 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows
             __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint8_t *>(scl + ((size_t)ci * heads + h) * 192 + 4 * lane),
                                              reinterpret_cast<uint8_t *>(&sb[ci & 3][0]), 16, 0, 0);
     };
-    // STAGED: block kb's key codes and its chunk's key factors into staging slot sl; its value codes and value factors
-    auto stage_keys = [&](int kb, int sl) {
-        stage_half16<WAVES>(head_images + kb * kb_stride, scl + ((size_t)(kb / kbs.bpc) * heads + h) * 128,
-                            side + sl * SG, side + sl * SG + IMG16, tid, wave == 0);
-    };
+    // STAGED: block kb's key codes and key factors into staging slot sl; its value codes and value factors
+    auto stage_keys = [&](int kb, int sl) { stage_half16<WAVES>(head_images + kb * kb_stride, side + sl * SG, tid); };
     auto stage_values = [&](int kb, int sl) {
-        stage_half16<WAVES>(head_images + kb * kb_stride + IMG16 / 2,
-                            scl + ((size_t)(kb / kbs.bpc) * heads + h) * 128 + 64, side + sl * SG + IMG16 / 2,
-                            side + sl * SG + IMG16 + 256, tid, wave == WAVES - 1);
+        stage_half16<WAVES>(head_images + kb * kb_stride + HALF16, side + sl * SG + HALF16, tid);
     };
     auto convert = [&](int sl, int kdst, int vdst) {
         convert16<WAVES>(side + sl * SG, kdst >= 0 ? kt[kdst] : nullptr, vdst >= 0 ? vt[vdst] : nullptr, tid);
@@ -1286,11 +1277,10 @@ bool kv_images_apply(int kv_format, int d, int heads) {
     return kv_format >= TAH_KV_F32 && kv_format <= TAH_KV_I8 && heads > 0 && d == 64 * heads;
 }
 
-// The tiles, then (256-aligned) a 256-byte slot for f32 and i16's maxima, then the i8 scales or the i16 factors.
+// The tiles, then (256-aligned) a 256-byte slot for f32 and i16's maxima, then the i8 scales.
 size_t kv_images_bytes(int rows, int chunk, int heads, int kv_format) {
     const size_t chunks = key_blocks(rows, chunk).n_chunks;
-    const size_t tail = kv_format == TAH_KV_I8 ? chunks * heads * SCL
-                                                : (kv_format == TAH_KV_I16 ? chunks * heads * FAC : 0);
+    const size_t tail = kv_format == TAH_KV_I8 ? chunks * heads * SCL : 0;
     return ((image_bytes_of(rows, chunk, heads, kv_format) + 255) / 256) * 256 +
            ((sizeof(uint32_t) * 2 * (size_t)heads + 255) / 256) * 256 + tail;
 }
@@ -1318,7 +1308,7 @@ void kv_images(hipStream_t s, int rows, int chunk, int d, int heads, int kv_form
         case TAH_KV_I16:
             launch_absmax<TAH_KV_I16>(s, rows, chunk, d, heads, records, img);
             hipLaunchKernelGGL(k_kv_tiles16, dim3(k.n_kb, heads), dim3(256), 0, s, rows, chunk, d, heads, records,
-                               img.kvmax, img.images, img.scales);
+                               img.kvmax, img.images);
             break;
         default:
             hipLaunchKernelGGL(k_kv_codes, dim3(k.n_kb, heads), dim3(256), 0, s, rows, chunk, d, heads, records,
@@ -1334,7 +1324,7 @@ KvImages kv_images_at(uint8_t *base, int rows, int chunk, int heads, int kv_form
     img.images = base;
     uint8_t *tail = base + ((image_bytes_of(rows, chunk, heads, kv_format) + 255) / 256) * 256;
     img.kvmax = reinterpret_cast<uint32_t *>(tail);
-    if (kv_format != TAH_KV_F32)
+    if (kv_format == TAH_KV_I8)
         img.scales = reinterpret_cast<float *>(tail + ((sizeof(uint32_t) * 2 * (size_t)heads + 255) / 256) * 256);
     return img;
 }

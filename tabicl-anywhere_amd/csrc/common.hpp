@@ -260,7 +260,7 @@ void pack(hipStream_t s, int rows, int d, int chunk, int fmt, const float *rec32
 struct KvImages {
     uint8_t *images = nullptr;
     uint32_t *kvmax = nullptr;  // f32 and i16: the heads' largest |K|, |V| (dequantised)
-    float *scales = nullptr;    // i8: per (chunk, head) the key scales, value scales and ratios; i16: the factors
+    float *scales = nullptr;    // i8: per (chunk, head) the key scales, value scales and ratios
     int fmt = TAH_KV_F32;       // the stored format the tiles were made from
 };
 bool kv_images_apply(int kv_format, int d, int heads);

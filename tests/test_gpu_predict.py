@@ -123,19 +123,19 @@ def test_attention_magnitudes(gpu, full_model, full_weights, kv_scale, q_scale):
 def test_model_bytes(gpu, full_weights):
     """Gpu::model_bytes at 10,000 rows, chunk 256 (157 key blocks of 64 over 40 chunks, 8 heads of 64): each layer held
     once, as tiles in place of its records: f32 as 32 KB split images per (key block, head) with the heads' maxima;
-    i16 as 16 KB code tiles with 512 bytes of factors per (chunk, head); i8 as 16 KB code images with 768 bytes of
-    scales per (chunk, head); then the query scales. The 16-bit formats stay under the reference's 285 MB resident
+    i16 as 16.5 KB code tiles (each half with its 64 factors) with the heads' maxima; i8 as 16 KB code images with
+    768 bytes of scales per (chunk, head); then the query scales. The 16-bit formats stay under the reference's 285 MB resident
     model (README.md:100) with room for nothing else of the layer."""
     def a256(n):
         return (n + 255) // 256 * 256
 
-    tiles = {abi.KV_F32: 32768, abi.KV_I16: 16384, abi.KV_I8: 16384}
-    tail = {abi.KV_F32: 0, abi.KV_I16: 40 * 8 * 512, abi.KV_I8: 40 * 8 * 768}
+    tiles = {abi.KV_F32: 32768, abi.KV_I16: 2 * (8192 + 256), abi.KV_I8: 16384}
+    tail = {abi.KV_F32: 0, abi.KV_I16: 0, abi.KV_I8: 40 * 8 * 768}
     for fmt in (abi.KV_F32, abi.KV_I16, abi.KV_I8):
         want = 12 * a256(a256(157 * 8 * tiles[fmt]) + 256 + tail[fmt]) + a256(12 * 512 * 4)
         assert hip.VramModel.model_bytes(full_weights, fmt, 10000, 256) == want, fmt
     i16 = hip.VramModel.model_bytes(full_weights, abi.KV_I16, 10000, 256)
-    assert i16 <= 260e6 and i16 <= 12 * 20_643_840 * 1.01  # within 1% of the stored i16 records
+    assert i16 <= 260e6 and i16 <= 12 * 20_643_840 * 1.03  # within 3% of the stored i16 records
     assert hip.VramModel.model_bytes(full_weights, abi.KV_F32, 0, 256) == 0
 
 
