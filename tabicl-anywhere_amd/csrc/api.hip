@@ -1119,13 +1119,17 @@ extern "C" int tah_represent(tah_dev *dev, const tah_weights *w, const float *to
     });
 }
 
-// Working bytes a sub-batch of k rows borrows in predict_rows (every buffer it and stage_rows take).
+// Working bytes of predict_rows for k rows, as it borrows them: the tokens and representations; the column stage's
+// cells and scratch (none when it writes the tokens itself over the model's column images); the row stage's scratch
+// (row_stage_floats: compact where only the fused kernels run); the in-context stage's buffers.
 static size_t predict_batch_bytes(const tah_weights *w, const tah_model *model, int k) {
     const int T = w->cls + model->features;
     const size_t kk = (size_t)k;
-    return loan_bytes({kk * T * w->e, kk * w->d, kk * model->features * w->e,
-                       column_stage_floats(w, k, model->features, model->digits), row_stage_floats(w, k, T), kk * w->d,
-                       kk * w->d, kk * w->d, kk * std::max(icl_mid(w), w->dec_hidden)}) +
+    const bool direct = column_tokens_fits(w, k, model->features, model->digits);
+    const size_t cells = direct ? 0 : kk * model->features * w->e;
+    const size_t col = direct && model->col_img ? 0 : column_stage_floats(w, k, model->features, model->digits);
+    return loan_bytes({kk * T * w->e, kk * w->d, cells, col, row_stage_floats(w, k, T), kk * w->d, kk * w->d, kk * w->d,
+                       kk * std::max(icl_mid(w), w->dec_hidden)}) +
            loan_raw(attention_work_bytes(shape_of(model, model->heads, k)));
 }
 
@@ -1149,7 +1153,7 @@ static void predict_rows(tah_dev *dev, const tah_weights *w, const tah_model *mo
         if (column_tokens_fits(w, k, model->features, model->digits)) {
             // the column stage straight into the tokens, and the first row block's keys and values from its last
             // block's kernel where the row stage takes them
-            float *cs = loans.take<float>(column_stage_floats(w, k, model->features, model->digits));
+            float *cs = model->col_img ? nullptr : loans.take<float>(column_stage_floats(w, k, model->features, model->digits));
             scratch = loans.take<float>(row_stage_floats(w, k, T));
             kv_ready = row_stage_takes_kv(w, k, T);
             column_stage_tokens(dev->stream, w, model->col_kv, xr, k, model->features, tok,

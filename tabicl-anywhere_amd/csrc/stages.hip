@@ -1063,7 +1063,9 @@ void column_stage_tokens(hipStream_t s, const tah_weights *w, const float *col_k
     if (kv && !row_kv_fits(w->row.at(0))) throw ArgError{"column stage: the first row block takes no fused keys"};
     const int e = w->e, nb = w->col_blocks, cls = w->cls, T = cls + features;
     const size_t M = (size_t)n * features;
-    float *att = scratch + 2 * M * e;  // column_stage's layout: its attention buffer holds the kernel's images
+    if (!col_images && !scratch) throw ArgError{"column stage: no images and no scratch for them"};
+    // column_stage's layout: its attention buffer holds the kernel's images (none needed over the model's own)
+    float *att = col_images ? nullptr : scratch + 2 * M * e;
     const size_t per = 2 * (size_t)e * w->inds, gstride = (size_t)nb * per;
     // the input layer inside the first column block (the cells formed from the table rows there, not written and
     // read back), unless that block is also the last, which forms the row block's keys and values
@@ -1102,12 +1104,6 @@ void class_token_kv(hipStream_t s, const tah_weights *w, float *out, float *tmp)
     }
 }
 
-size_t row_stage_floats(const tah_weights *w, int n, int T) {
-    int ff = 0;
-    for (auto &b : w->row) ff = std::max(ff, b.ff);
-    const size_t R = (size_t)n * T;
-    return R * ((size_t)w->e * 5 + ff) + 2 * (size_t)T * w->rope_half + (size_t)n * w->cls * w->e * 2;
-}
 
 // The row stage's fused kernels: head width 16 with the rotary tables' 8 frequencies, at most 128 tokens (the
 // rotary positions applied inside the attention kernels).
@@ -1124,7 +1120,33 @@ bool row_stage_takes_kv(const tah_weights *w, int n, int T) {
     return w->row_blocks >= 2 && row_block_path(w, 0, n, T) && row_kv_fits(w->row[0]);
 }
 
-float *row_stage_kv(const tah_weights *w, int n, int T, float *scratch) { return scratch + (size_t)n * T * w->e; }
+// Whether row_stage runs n rows of T tokens on the fused kernels alone: every block before the last as k_row_block
+// with its feed-forward half inside, the last through the class-token path and k_cls_attn. Its scratch is then
+// compact: the keys and values [n T][2 e] and the class tokens' buffers ([n cls] rows), not the per-token buffers of
+// the unfused kernels.
+static bool row_stage_compact(const tah_weights *w, int n, int T) {
+    const int last = w->row_blocks - 1;
+    if (last < 1 || !row_fused(w, T)) return false;
+    const size_t R = (size_t)n * T;
+    for (int bi = 0; bi < last; bi++)
+        if (!row_block_path(w, bi, n, T) || !block_ff_fits(w->row[bi]) || R <= SMALL_ROWS) return false;
+    return w->row[last].inimg && n >= CLS_QUERIES_MIN && w->cls <= CLS_MAXQ && w->row_heads <= 8;
+}
+
+// The row stage's scratch, in floats; row_stage lays it out as:
+//   compact:  t [M][e], qkv [R][2 e], att [M][e], mid [M][ff], xc [M][e], ac [M][e]      (M = n cls, R = n T)
+//   else:     t [R][e], qkv [R][3 e], att [R][e], mid [R][ff], xc [M][e], ac [M][e]
+size_t row_stage_floats(const tah_weights *w, int n, int T) {
+    int ff = 0;
+    for (auto &b : w->row) ff = std::max(ff, b.ff);
+    const size_t R = (size_t)n * T, M = (size_t)n * w->cls, e = w->e;
+    if (row_stage_compact(w, n, T)) return R * 2 * e + M * (4 * e + ff);
+    return R * (5 * e + ff) + M * 2 * e;
+}
+
+float *row_stage_kv(const tah_weights *w, int n, int T, float *scratch) {
+    return scratch + (row_stage_compact(w, n, T) ? (size_t)n * w->cls : (size_t)n * T) * w->e;
+}
 
 // The row stage for n rows: tok [n][T][e] (consumed) to rep [n][cls * e]. cosv/sinv [T][half] on the card.
 void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, const float *cosv, const float *sinv,
@@ -1134,9 +1156,11 @@ void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, co
     const int e = w->e, heads = w->row_heads, cls = w->cls;
     int ff = 0;
     for (auto &b : w->row) ff = std::max(ff, b.ff);
-    const size_t R = (size_t)n * T;
-    float *t = scratch, *qkv = t + R * e, *att = qkv + R * 3 * e, *mid = att + R * e;
-    float *xc = mid + R * ff, *ac = xc + (size_t)n * cls * e;
+    const size_t R = (size_t)n * T, M = (size_t)n * cls;
+    const bool compact = row_stage_compact(w, n, T);  // the layouts of row_stage_floats
+    const size_t rt = compact ? M : R;                // rows of t, att and mid
+    float *t = scratch, *qkv = t + rt * e, *att = qkv + R * (compact ? 2 : 3) * e, *mid = att + rt * e;
+    float *xc = mid + rt * ff, *ac = xc + M * e;
     const int hd = e / heads, half = w->rope_half;
     if (2 * half != hd) throw ArgError{"row stage: rotary frequencies must cover half the head width"};
     const float inv = 1.0f / sqrtf((float)hd);
