@@ -369,10 +369,10 @@ __device__ __forceinline__ void qmlp64_tile(const float *qt, int ldq, float *hs,
 }
 
 // Few rows and long rows (the in-context stage: 2,048 queries, K = 512 or 1024): one workgroup per 32 rows x 128
-// columns, its four wavefronts splitting K four ways (each a quarter, in chunks of 128 with their own per-row
+// columns, its W wavefronts splitting K W ways (four or eight, each in chunks of CW columns with their own per-row
 // powers of two), then summing their partial products -- unscaled to f32 -- through LDS; wavefront w finishes
-// tile w. Four times the wavefronts of k_gemm_split on the same grid of outputs, each with a quarter of the
-// dependent chain. With QM (the query projection, 64 or 128 columns = one or two heads of 64), the finished tile
+// tile w (W = 4) or half of tile w / 2 (W = 8). W times the wavefronts of k_gemm_split on the same grid of outputs,
+// each with 1 / W of the dependent chain. With QM (the query projection, 64 or 128 columns = one or two heads of 64), the finished tile
 // goes through LDS and the workgroup runs the heads' query MLP on it (qmlp64_tile): no separate launch.
 constexpr int SPLITK_MAX_KQ = 512;  // each wavefront's share of K at most (K at most 2048)
 
@@ -382,16 +382,22 @@ __device__ __forceinline__ void copy16_to_lds(const float *src, uint8_t *dst) {
 }
 
 
-template <int EPI, bool LN, int TN, bool QM = false>
-__global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, const float *__restrict__ X, int ldx,
-                                                          const uint8_t *__restrict__ wimg, int wshift,
-                                                          const float *__restrict__ b, float *Y, int ldy, SplitEpi ea,
-                                                          const float *__restrict__ lnw, const float *__restrict__ lnb) {
-    // per wavefront 16 KB: its rows' 128-column chunk (32 rows x 32 float4, swizzled) while the products run, then
-    // its partial sums [tile][accumulator][lane]
-    __shared__ __align__(16) float stage[4][16 * 64 * 4];
+// W = 8 (four tiles a workgroup only, no QM): eight wavefronts split K eight ways, two a SIMD, each with half the
+// dependent chain of four; a wavefront's chunk is then CW = 64 columns when K = 512.
+template <int EPI, bool LN, int TN, bool QM = false, int W = 4, int CW = 128>
+__global__ __launch_bounds__(64 * W, 2) void k_gemm_splitk4(int M, int N, int K, const float *__restrict__ X, int ldx,
+                                                             const uint8_t *__restrict__ wimg, int wshift,
+                                                             const float *__restrict__ b, float *Y, int ldy, SplitEpi ea,
+                                                             const float *__restrict__ lnw, const float *__restrict__ lnb) {
+    static_assert(W == 4 || (W == 8 && TN == 4), "eight wavefronts: four tiles a workgroup");
+    static_assert(CW == 128 || CW == 64, "chunks of 64 or 128 columns");
+    constexpr int C4 = CW / 4;  // float4 columns of a chunk row
+    constexpr bool HALVES = TN == 2 || W == 8;  // a wavefront finishes half a tile
+    // per wavefront 16 KB: its rows' chunk (32 rows x C4 float4, swizzled) while the products run, then its partial
+    // sums [tile][accumulator][lane]
+    __shared__ __align__(16) float stage[W][16 * 64 * 4];
     auto red = [&](int w, int T, int v) { return &stage[w][(T * 16 + v) * 64]; };
-    __shared__ float rsum[4][32];  // LN: per-wavefront partial row sums
+    __shared__ float rsum[W][32];  // LN: per-wavefront partial row sums
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r32 = lane & 31, g = lane >> 5;
     // one dimension of (N / 32 TN) x ceil(M / 32) workgroups; consecutive workgroups go to the eight XCDs in turn, so
@@ -404,7 +410,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
     const int m = tile / gx * 32 + r32;
     const bool live = m < M;
     const int nt0 = bxt * TN;
-    const int KS = K / 16, kq = K / 4, kend = (wave + 1) * kq;
+    const int KS = K / 16, kq = K / W, kend = (wave + 1) * kq;
     floatx16 acc[TN];
 #pragma unroll
     for (int T = 0; T < TN; T++)
@@ -427,20 +433,21 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
     wload(0, wb[0]);
     if (nsteps > 1) wload(1, wb[1]);
 #pragma unroll
-    for (int it = 0; it < (LN ? 1 : SPLITK_MAX_KQ / 128); it++) {  // with the layer norm, K = 512
-        const int k0 = wave * kq + 128 * it;
+    for (int it = 0; it < (LN ? 1 : SPLITK_MAX_KQ / CW); it++) {  // with the layer norm, K = W CW = 512
+        const int k0 = wave * kq + CW * it;
         if (k0 >= kend) break;
-        float xv[8][8];
+        float xv[CW / 16][8];
         {
-            // a whole chunk (K is a multiple of 512): the wavefront's 32 rows x 128 columns copied into its staging by DMA, copy i lane l
-            // filling float4 slot 64 i + l = row (64 i + l) / 32, float4 column ((64 i + l) % 32) ^ (row % 16), so
-            // that each load instruction reads whole runs of two rows (a lane a row, as below, touched 32 rows an
-            // instruction) and the reads back, a row a lane, fall on distinct bank groups; rows past M read row M - 1
+            // a whole chunk (K is a multiple of W CW): the wavefront's 32 rows x CW columns copied into its staging by
+            // DMA, copy i lane l filling float4 slot 64 i + l = row (64 i + l) / C4, float4 column ((64 i + l) % C4) ^
+            // (row % 16), so that each load instruction reads whole runs of rows (a lane a row, as below, touched 32
+            // rows an instruction) and the reads back, a row a lane, fall on distinct bank groups; rows past M read
+            // row M - 1
             const int m0 = tile / gx * 32;
             uint8_t *st = reinterpret_cast<uint8_t *>(stage[wave]);
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int slot = 64 * i + lane, row = slot >> 5, c = (slot & 31) ^ (row & 15);
+            for (int i = 0; i < CW / 8; i++) {
+                const int slot = 64 * i + lane, row = slot / C4, c = (slot % C4) ^ (row & 15);
                 copy16_to_lds(X + (size_t)min(m0 + row, M - 1) * ldx + k0 + 4 * c, st + 1024 * i);
             }
             __builtin_amdgcn_s_waitcnt(0);
@@ -448,30 +455,36 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-            for (int ks = 0; ks < 8; ks++) {
+            for (int ks = 0; ks < CW / 16; ks++) {
 #pragma unroll
                 for (int hf = 0; hf < 2; hf++) {
                     const int c = 4 * ks + 2 * g + hf;
-                    const float4 a = *reinterpret_cast<const float4 *>(st + 16 * (r32 * 32 + (c ^ (r32 & 15))));
+                    const float4 a = *reinterpret_cast<const float4 *>(st + 16 * (r32 * C4 + (c ^ (r32 & 15))));
                     xv[ks][4 * hf] = a.x; xv[ks][4 * hf + 1] = a.y; xv[ks][4 * hf + 2] = a.z; xv[ks][4 * hf + 3] = a.w;
                 }
             }
         }
         if (LN) {
-            // K = 512: this wavefront holds columns 128 w .. 128 w + 127 of its 32 rows; the row's sums go
+            // K = 512: this wavefront holds columns CW w .. CW w + CW - 1 of its 32 rows; the row's sums go
             // through LDS (two passes: mean, then biased variance; eps 1e-5)
+            auto row_total = [&]() {
+                float t = rsum[0][r32];
+#pragma unroll
+                for (int w = 1; w < W; w++) t += rsum[w][r32];
+                return t;
+            };
             float sum = 0.0f;
 #pragma unroll
-            for (int ks = 0; ks < 8; ks++)
+            for (int ks = 0; ks < CW / 16; ks++)
 #pragma unroll
                 for (int t = 0; t < 8; t++) sum += xv[ks][t];
             sum += __shfl_xor(sum, 32, 64);
             if (g == 0) rsum[wave][r32] = sum;
             __syncthreads();
-            const float mean = (((rsum[0][r32] + rsum[1][r32]) + rsum[2][r32]) + rsum[3][r32]) / (float)K;
+            const float mean = row_total() / (float)K;
             float sq = 0.0f;
 #pragma unroll
-            for (int ks = 0; ks < 8; ks++)
+            for (int ks = 0; ks < CW / 16; ks++)
 #pragma unroll
                 for (int t = 0; t < 8; t++) {
                     const float dv = xv[ks][t] - mean;
@@ -481,10 +494,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
             __syncthreads();
             if (g == 0) rsum[wave][r32] = sq;
             __syncthreads();
-            const float inv = 1.0f / sqrtf((((rsum[0][r32] + rsum[1][r32]) + rsum[2][r32]) + rsum[3][r32]) / (float)K +
-                                           1e-5f);
+            const float inv = 1.0f / sqrtf(row_total() / (float)K + 1e-5f);
 #pragma unroll
-            for (int ks = 0; ks < 8; ks++) {
+            for (int ks = 0; ks < CW / 16; ks++) {
                 float wv[8], bv[8];
                 const int c0 = k0 + 16 * ks + 8 * g;
 #pragma unroll
@@ -498,7 +510,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
         }
         float xmax = 0.0f;
 #pragma unroll
-        for (int ks = 0; ks < 8; ks++)
+        for (int ks = 0; ks < CW / 16; ks++)
 #pragma unroll
             for (int t = 0; t < 8; t++) xmax = fmaxf(xmax, fabsf(xv[ks][t]));
         xmax = fmaxf(xmax, __shfl_xor(xmax, 32, 64));
@@ -511,8 +523,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
         eprev = e;
         const float f = ldexpf(1.0f, e);
 #pragma unroll
-        for (int ks = 0; ks < 8; ks++) {
-            const int j = 8 * it + ks;
+        for (int ks = 0; ks < CW / 16; ks++) {
+            const int j = (CW / 16) * it + ks;
             if (j + 2 < nsteps) wload(j + 2, wb[(j + 2) % 3]);
             halfx8 xh, xl;
             split8(xv[ks], f, xh, xl);
@@ -521,9 +533,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
         }
     }
     // with QM, the query MLP's operands are read now, their latency behind the partial sums' reduction
-    QmlpOps<(TN / 2) * 512 / 256> qo;
+    QmlpOps<(TN / 2) * 512 / (64 * W)> qo;
     if constexpr (QM)
-        qo = qmlp64_read<TN / 2, 256>(tid, ea.w0, ea.b0, ea.w2, ea.b2, ea.scale + 64 * (TN / 2) * bxt);
+        qo = qmlp64_read<TN / 2, 64 * W>(tid, ea.w0, ea.b0, ea.w2, ea.b2, ea.scale + 64 * (TN / 2) * bxt);
     const float u = ldexpf(1.0f, -(wshift + eprev));
 #pragma unroll
     for (int T = 0; T < TN; T++)
@@ -534,49 +546,55 @@ __global__ __launch_bounds__(256, 2) void k_gemm_splitk4(int M, int N, int K, co
         static_assert(TN == 4 || TN == 2, "the fused query MLP takes whole heads (64 columns) per workgroup");
         constexpr int LD = 32 * TN + 4;  // the tile's row pitch in LDS
         // wavefront w: tile w of four (rows r32, columns 32 w + 16 hh + 8 g + t of the workgroup's), or half w % 2 of
-        // tile w / 2 of two; bias added
-        const int T = TN == 4 ? wave : wave >> 1;
+        // tile w / 2 (of two; of four with W = 8); bias added
+        const int T = HALVES ? wave >> 1 : wave;
         float yq[2][8];
 #pragma unroll
         for (int hh = 0; hh < 2; hh++) {
-            if (TN == 2 && hh != (wave & 1)) continue;
+            if (HALVES && hh != (wave & 1)) continue;
             const int n0 = 32 * (nt0 + T) + 16 * hh + 8 * g;
 #pragma unroll
             for (int t = 0; t < 8; t++) {
                 const int v = 8 * hh + t;
-                yq[hh][t] = (((red(0, T, v)[lane] + red(1, T, v)[lane]) + red(2, T, v)[lane]) + red(3, T, v)[lane]) +
-                            b[n0 + t];
+                float y = red(0, T, v)[lane];
+#pragma unroll
+                for (int w = 1; w < W; w++) y += red(w, T, v)[lane];
+                yq[hh][t] = y + b[n0 + t];
             }
         }
         __syncthreads();  // the partial sums are all read: their LDS holds the tile next, [32 rows][LD]
         float *qt = &stage[0][0];
 #pragma unroll
         for (int hh = 0; hh < 2; hh++) {
-            if (TN == 2 && hh != (wave & 1)) continue;
+            if (HALVES && hh != (wave & 1)) continue;
 #pragma unroll
             for (int t = 0; t < 8; t++) qt[r32 * LD + 32 * T + 16 * hh + 8 * g + t] = yq[hh][t];
         }
         __syncthreads();
         // the hidden layer and the MLP's output after the tile, in the partial sums' LDS
-        static_assert(32 * LD + 2 * (TN / 2) * 32 * QMP <= 4 * 16 * 64 * 4, "the query MLP's tiles fit in LDS");
+        static_assert(32 * LD + 2 * (TN / 2) * 32 * QMP <= W * 16 * 64 * 4, "the query MLP's tiles fit in LDS");
         float *hs = qt + 32 * LD;
         const int m0 = tile / gx * 32;
-        qmlp64_tile<TN / 2, 256>(qt, LD, hs, hs + (TN / 2) * 32 * QMP, tid, qo, ea.s0, ea.s2,
-                                 Y + (size_t)m0 * ldy + 64 * (TN / 2) * bxt, ldy, min(32, M - m0));
+        qmlp64_tile<TN / 2, 64 * W>(qt, LD, hs, hs + (TN / 2) * 32 * QMP, tid, qo, ea.s0, ea.s2,
+                                    Y + (size_t)m0 * ldy + 64 * (TN / 2) * bxt, ldy, min(32, M - m0));
         return;
     }
     if (!live) return;
-    // wavefront w sums tile w (both halves) of four, or half w % 2 of tile w / 2 of two
-    const int T = TN == 4 ? wave : wave >> 1;
+    // wavefront w sums tile w (both halves) of four, or half w % 2 of tile w / 2 (of two; of four with W = 8), the
+    // partials in wavefront order
+    const int T = HALVES ? wave >> 1 : wave;
 #pragma unroll
     for (int hh = 0; hh < 2; hh++) {
-        if (TN == 2 && hh != (wave & 1)) continue;
+        if (HALVES && hh != (wave & 1)) continue;
         const int n0 = 32 * (nt0 + T) + 16 * hh + 8 * g;
         float yv[8];
 #pragma unroll
         for (int t = 0; t < 8; t++) {
             const int v = 8 * hh + t;
-            yv[t] = ((red(0, T, v)[lane] + red(1, T, v)[lane]) + red(2, T, v)[lane]) + red(3, T, v)[lane];
+            float y = red(0, T, v)[lane];
+#pragma unroll
+            for (int w = 1; w < W; w++) y += red(w, T, v)[lane];
+            yv[t] = y;
         }
         if (b) {
             const float4 ba = *reinterpret_cast<const float4 *>(b + n0);
@@ -1083,23 +1101,23 @@ void gemm_split(hipStream_t s, int M, int N, int K, const float *X, int ldx, con
     }
 }
 
-template <bool LN, int TN>
+template <bool LN, int TN, int W = 4, int CW = 128>
 static void launch_splitk4_tiles(hipStream_t s, int M, int N, int K, const float *X, int ldx, const uint8_t *img,
                                  int shift, const float *b, float *Y, int ldy, Epi epi, const SplitEpi &ea,
                                  const float *lnw, const float *lnb) {
     const dim3 grid((N / (32 * TN)) * ((M + 31) / 32));
     switch (epi) {
         case EPI_NONE:
-            hipLaunchKernelGGL((k_gemm_splitk4<EPI_NONE, LN, TN>), grid, dim3(256), 0, s, M, N, K, X, ldx, img, shift, b,
-                               Y, ldy, ea, lnw, lnb);
+            hipLaunchKernelGGL((k_gemm_splitk4<EPI_NONE, LN, TN, false, W, CW>), grid, dim3(64 * W), 0, s, M, N, K, X,
+                               ldx, img, shift, b, Y, ldy, ea, lnw, lnb);
             break;
         case EPI_GELU:
-            hipLaunchKernelGGL((k_gemm_splitk4<EPI_GELU, LN, TN>), grid, dim3(256), 0, s, M, N, K, X, ldx, img, shift, b,
-                               Y, ldy, ea, lnw, lnb);
+            hipLaunchKernelGGL((k_gemm_splitk4<EPI_GELU, LN, TN, false, W, CW>), grid, dim3(64 * W), 0, s, M, N, K, X,
+                               ldx, img, shift, b, Y, ldy, ea, lnw, lnb);
             break;
         default:
-            hipLaunchKernelGGL((k_gemm_splitk4<EPI_RESID, LN, TN>), grid, dim3(256), 0, s, M, N, K, X, ldx, img, shift, b,
-                               Y, ldy, ea, lnw, lnb);
+            hipLaunchKernelGGL((k_gemm_splitk4<EPI_RESID, LN, TN, false, W, CW>), grid, dim3(64 * W), 0, s, M, N, K, X,
+                               ldx, img, shift, b, Y, ldy, ea, lnw, lnb);
             break;
     }
     TAH_LAUNCHED();
@@ -1113,10 +1131,23 @@ template <bool LN>
 static void launch_splitk4(hipStream_t s, int M, int N, int K, const float *X, int ldx, const uint8_t *img, int shift,
                            const float *b, float *Y, int ldy, Epi epi, const SplitEpi &ea, const float *lnw,
                            const float *lnb) {
-    if (M <= SPLITK_TWO_TILES_ROWS && N % 64 == 0)
+    if (M <= SPLITK_TWO_TILES_ROWS && N % 64 == 0) {
         launch_splitk4_tiles<LN, 2>(s, M, N, K, X, ldx, img, shift, b, Y, ldy, epi, ea, lnw, lnb);
-    else
-        launch_splitk4_tiles<LN, 4>(s, M, N, K, X, ldx, img, shift, b, Y, ldy, epi, ea, lnw, lnb);
+        return;
+    }
+    // eight wavefronts where the four-tile grid is one workgroup a compute unit and no layer norm spans them
+    // (2,048 rows: out-projection 10.2 -> 10.0 us, second feed-forward layer 15.3 -> 14.4 us; the first feed-forward
+    // layer's 512 workgroups would run in two rounds, 16.6 -> 19.5 us)
+    if constexpr (!LN) {
+        if (K == 512 || K == 1024) {
+            if (K == 512)
+                launch_splitk4_tiles<LN, 4, 8, 64>(s, M, N, K, X, ldx, img, shift, b, Y, ldy, epi, ea, lnw, lnb);
+            else
+                launch_splitk4_tiles<LN, 4, 8, 128>(s, M, N, K, X, ldx, img, shift, b, Y, ldy, epi, ea, lnw, lnb);
+            return;
+        }
+    }
+    launch_splitk4_tiles<LN, 4>(s, M, N, K, X, ldx, img, shift, b, Y, ldy, epi, ea, lnw, lnb);
 }
 
 // the query projection's one-head-a-workgroup grid up to this many workgroups: the card's compute units
@@ -1148,14 +1179,15 @@ void query_split(hipStream_t s, int M, const float *X, int ldx, const DevBlock &
     }
     // a workgroup per head while that grid fits one workgroup a compute unit (twice the workgroups, each streaming
     // half the weights: 1,024 rows 10.3 against 12.9 us), two heads a workgroup beyond (1,536 rows 13.1 against 14.6
-    // us, 2,048 rows 13.6 against 15.2, 10,000 rows 48.2 against 57.7)
+    // us, 2,048 rows 13.6 against 15.2, 10,000 rows 48.2 against 57.7), on eight wavefronts (2,048 rows 15.7 -> 13.6
+    // us)
     const long tiles = (long)(d / 64) * ((M + 31) / 32);
     if (tiles <= QUERY_ONE_HEAD_TILES)
         hipLaunchKernelGGL((k_gemm_splitk4<EPI_NONE, true, 2, true>), dim3(tiles), dim3(256), 0, s, M, d, d, X, ldx,
                            b.in_s.img, b.in_s.shift, b.in_b, q, d, ea, b.n1w, b.n1b);
     else
-        hipLaunchKernelGGL((k_gemm_splitk4<EPI_NONE, true, 4, true>), dim3(tiles / 2), dim3(256), 0, s, M, d, d, X,
-                           ldx, b.in_s.img, b.in_s.shift, b.in_b, q, d, ea, b.n1w, b.n1b);
+        hipLaunchKernelGGL((k_gemm_splitk4<EPI_NONE, true, 4, true, 8, 64>), dim3(tiles / 2), dim3(512), 0, s, M, d,
+                           d, X, ldx, b.in_s.img, b.in_s.shift, b.in_b, q, d, ea, b.n1w, b.n1b);
     TAH_LAUNCHED();
 }
 
