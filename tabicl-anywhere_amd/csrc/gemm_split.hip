@@ -1126,6 +1126,8 @@ static void launch_splitk4_tiles(hipStream_t s, int M, int N, int K, const float
 // Four tiles a workgroup from 2,048 rows (two, with twice the workgroups, measured slower there); two below 512 rows,
 // where the few workgroups each stream half the weights
 constexpr int SPLITK_TWO_TILES_ROWS = 512;
+// workgroups of eight wavefronts the card runs at once (one a compute unit)
+constexpr long SPLITK_ONE_ROUND = 256;
 
 template <bool LN>
 static void launch_splitk4(hipStream_t s, int M, int N, int K, const float *X, int ldx, const uint8_t *img, int shift,
@@ -1135,11 +1137,11 @@ static void launch_splitk4(hipStream_t s, int M, int N, int K, const float *X, i
         launch_splitk4_tiles<LN, 2>(s, M, N, K, X, ldx, img, shift, b, Y, ldy, epi, ea, lnw, lnb);
         return;
     }
-    // eight wavefronts where the four-tile grid is one workgroup a compute unit and no layer norm spans them
+    // eight wavefronts where the four-tile grid is at most one workgroup a compute unit and no layer norm spans them
     // (2,048 rows: out-projection 10.2 -> 10.0 us, second feed-forward layer 15.3 -> 14.4 us; the first feed-forward
-    // layer's 512 workgroups would run in two rounds, 16.6 -> 19.5 us)
+    // layer's 512 workgroups would run in two rounds, 16.6 -> 19.5 us, and so would 10,000 rows' grids: 46 -> 67 us)
     if constexpr (!LN) {
-        if (K == 512 || K == 1024) {
+        if ((K == 512 || K == 1024) && (long)(N / 128) * ((M + 31) / 32) <= SPLITK_ONE_ROUND) {
             if (K == 512)
                 launch_splitk4_tiles<LN, 4, 8, 64>(s, M, N, K, X, ldx, img, shift, b, Y, ldy, epi, ea, lnw, lnb);
             else
@@ -1179,15 +1181,18 @@ void query_split(hipStream_t s, int M, const float *X, int ldx, const DevBlock &
     }
     // a workgroup per head while that grid fits one workgroup a compute unit (twice the workgroups, each streaming
     // half the weights: 1,024 rows 10.3 against 12.9 us), two heads a workgroup beyond (1,536 rows 13.1 against 14.6
-    // us, 2,048 rows 13.6 against 15.2, 10,000 rows 48.2 against 57.7), on eight wavefronts (2,048 rows 15.7 -> 13.6
-    // us)
+    // us, 2,048 rows 13.6 against 15.2, 10,000 rows 48.2 against 57.7), on eight wavefronts while those are one round
+    // of workgroups (2,048 rows 15.7 -> 13.6 us)
     const long tiles = (long)(d / 64) * ((M + 31) / 32);
     if (tiles <= QUERY_ONE_HEAD_TILES)
         hipLaunchKernelGGL((k_gemm_splitk4<EPI_NONE, true, 2, true>), dim3(tiles), dim3(256), 0, s, M, d, d, X, ldx,
                            b.in_s.img, b.in_s.shift, b.in_b, q, d, ea, b.n1w, b.n1b);
-    else
+    else if (tiles / 2 <= SPLITK_ONE_ROUND)
         hipLaunchKernelGGL((k_gemm_splitk4<EPI_NONE, true, 4, true, 8, 64>), dim3(tiles / 2), dim3(512), 0, s, M, d,
                            d, X, ldx, b.in_s.img, b.in_s.shift, b.in_b, q, d, ea, b.n1w, b.n1b);
+    else
+        hipLaunchKernelGGL((k_gemm_splitk4<EPI_NONE, true, 4, true>), dim3(tiles / 2), dim3(256), 0, s, M, d, d, X,
+                           ldx, b.in_s.img, b.in_s.shift, b.in_b, q, d, ea, b.n1w, b.n1b);
     TAH_LAUNCHED();
 }
 
