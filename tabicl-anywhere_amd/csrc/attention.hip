@@ -1130,8 +1130,21 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows
     }
     if constexpr (CODES)
         if (kb0 < kb1) scale_sums((kb1 - 1) / kbs.bpc, 1);  // into true units: the last chunk's value scales
-    l += __shfl_xor(l, 32, 64);
-    if (!qlive) return;
+    // the two halves of the wavefront hold the same queries' sums over different keys (lanes l and l ^ 32)
+    if constexpr (STAGED) {
+        l += __shfl_xor(l, 32, 64);
+    } else {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false, false);
+        l = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+    // the output's row and lane half again from the thread index, through an opaque copy: the values formed before
+    // the loop would otherwise be held across it (spilled, at 256 registers); the i16 kernel keeps them (with the
+    // copy, its allocation reloads a copy address at every block instead)
+    int tid_e = tid;
+    if constexpr (!STAGED) asm volatile("" : "+v"(tid_e));
+    const int lane_e = tid_e & 63, g_e = lane_e >> 5;
+    const int qrow_e = qt * 32 * WAVES + (tid_e >> 6) * 32 + (lane_e & 31);
+    if (qrow_e >= nq) return;
     // accumulator v of dim block db holds coordinate 32 db + 8 (v / 4) + 4 g + v % 4
     const float unscale = ldexpf(1.0f, -sv);
     if (splits == 1) {
@@ -1140,19 +1153,19 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows
         for (int db = 0; db < 2; db++)
 #pragma unroll
             for (int v4 = 0; v4 < 4; v4++)
-                *reinterpret_cast<float4 *>(out + (size_t)qrow * d + h * 64 + 32 * db + 8 * v4 + 4 * g) =
+                *reinterpret_cast<float4 *>(out + (size_t)qrow_e * d + h * 64 + 32 * db + 8 * v4 + 4 * g_e) =
                     make_float4(acc_o[db][4 * v4] * f, acc_o[db][4 * v4 + 1] * f, acc_o[db][4 * v4 + 2] * f,
                                 acc_o[db][4 * v4 + 3] * f);
     } else {
-        const size_t at = ((size_t)split * nq + qrow) * heads + h;
+        const size_t at = ((size_t)split * nq + qrow_e) * heads + h;
 #pragma unroll
         for (int db = 0; db < 2; db++)
 #pragma unroll
             for (int v4 = 0; v4 < 4; v4++)
-                *reinterpret_cast<float4 *>(part_o + at * 64 + 32 * db + 8 * v4 + 4 * g) =
+                *reinterpret_cast<float4 *>(part_o + at * 64 + 32 * db + 8 * v4 + 4 * g_e) =
                     make_float4(acc_o[db][4 * v4] * unscale, acc_o[db][4 * v4 + 1] * unscale,
                                 acc_o[db][4 * v4 + 2] * unscale, acc_o[db][4 * v4 + 3] * unscale);
-        if (g == 0) {
+        if (g_e == 0) {
             part_ml[at * 2] = ref;
             part_ml[at * 2 + 1] = l;
         }
