@@ -41,8 +41,9 @@ PEAK_F16_MFMA = 2.5e15  # MI355X dense fp16 matrix FLOP/s
 PEAK_SPLIT_F32 = PEAK_F16_MFMA / 3  # f32 work at three fp16 products per f32 product
 PEAK_HBM = 8.0e12  # MI355X HBM3E bytes/s
 # HBM bytes per launch of the roofline kernel, from rocprofv3 FETCH_SIZE and WRITE_SIZE runs of this bench scaled by
-# the counters' reading on its own 256 MiB copy (profiles/attention_f32_2048x10000_memory.md)
-TRAFFIC_BYTES = 76.3e6
+# the counters' reading on its own 1 GiB copies (profiles/attention_f32_2048x10000_memory.md): 58.2 MB read + 17.3 MB
+# written
+TRAFFIC_BYTES = 75.5e6
 
 
 def pass_cost(model, n, rows=ROWS, features=FEATURES, kv_bytes=4):
