@@ -1114,18 +1114,19 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows
         __syncthreads();
         query_for(kb0);
         ta = scores(kt[0], sa);
-        // two steps an iteration, so that the score registers swap roles without copies
-        for (int kb = kb0;; kb += 2) {
-            if (kb + 1 >= kb1) {
-                step(Flag<false>{}, sa, sbk, ta, tb, kb);
-                break;
-            }
+        // two steps an iteration, so that the score registers swap roles without copies, and the last one or two
+        // blocks after the loop: with an exit between the loop's two steps the compiler kept the weighted sums and
+        // the scores in other registers on each side of it and copied them (about 40 moves a step, and spills)
+        int kb = kb0;
+        for (; kb + 2 < kb1; kb += 2) {
             step(Flag<true>{}, sa, sbk, ta, tb, kb);
-            if (kb + 2 >= kb1) {
-                step(Flag<false>{}, sbk, sa, tb, ta, kb + 1);
-                break;
-            }
             step(Flag<true>{}, sbk, sa, tb, ta, kb + 1);
+        }
+        if (kb + 1 < kb1) {
+            step(Flag<true>{}, sa, sbk, ta, tb, kb);
+            step(Flag<false>{}, sbk, sa, tb, ta, kb + 1);
+        } else {
+            step(Flag<false>{}, sa, sbk, ta, tb, kb);
         }
     }
     if constexpr (CODES)
