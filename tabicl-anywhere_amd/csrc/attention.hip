@@ -1132,17 +1132,13 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows
     if constexpr (CODES)
         if (kb0 < kb1) scale_sums((kb1 - 1) / kbs.bpc, 1);  // into true units: the last chunk's value scales
     // the two halves of the wavefront hold the same queries' sums over different keys (lanes l and l ^ 32)
-    if constexpr (STAGED) {
-        l += __shfl_xor(l, 32, 64);
-    } else {
+    {
         const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false, false);
         l = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
     }
-    // the output's row and lane half again from the thread index, through an opaque copy: the values formed before
-    // the loop would otherwise be held across it (spilled, at 256 registers); the i16 kernel keeps them (with the
-    // copy, its allocation reloads a copy address at every block instead)
+    // the output's row and lane half again from the thread index, through an opaque copy: not held across the loop
     int tid_e = tid;
-    if constexpr (!STAGED) asm volatile("" : "+v"(tid_e));
+    asm volatile("" : "+v"(tid_e));
     const int lane_e = tid_e & 63, g_e = lane_e >> 5;
     const int qrow_e = qt * 32 * WAVES + (tid_e >> 6) * 32 + (lane_e & 31);
     if (qrow_e >= nq) return;
