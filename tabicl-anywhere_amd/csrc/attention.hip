@@ -1084,20 +1084,22 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows
                 if (i < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             }
         } else if constexpr (NEXT) {
-            // one region: 16 key and 16 value operand reads, 24 + 24 products and 160 VALU operations (the weights
-            // and their sum), dealt out as 4 VALU operations a product while the scores run and 2 after
+            // one region: 16 key and 16 value operand reads, 24 + 24 products and the weights' VALU work (their
+            // exponents, splits and sum), two VALU operations placed after each product and the rest left to the
+            // scheduler (four a product while the scores run, as the loop had with its register copies, measured
+            // 2-3% slower a launch: 0.1161 -> 0.1127 ms)
             __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
             }
 #pragma unroll
             for (int i = 0; i < 24; i++) {
