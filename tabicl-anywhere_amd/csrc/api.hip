@@ -182,12 +182,18 @@ extern "C" int tah_open(int32_t ordinal, tah_dev **out) {
         TAH_HIP(hipGetDeviceProperties(&prop, ordinal));
         dev->name = std::string(prop.name) + " (" + prop.gcnArchName + ")";
         TAH_HIP(hipStreamCreateWithFlags(&dev->stream, hipStreamNonBlocking));
+        TAH_HIP(hipStreamCreateWithFlags(&dev->side, hipStreamNonBlocking));
+        TAH_HIP(hipEventCreateWithFlags(&dev->fork_ev, hipEventDisableTiming));
+        TAH_HIP(hipEventCreateWithFlags(&dev->join_ev, hipEventDisableTiming));
         void *p = nullptr;
         TAH_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
         dev->noalloc = static_cast<uint8_t *>(p);
         return TAH_OK;
     });
     if (rc != TAH_OK) {
+        if (dev->fork_ev) (void)hipEventDestroy(dev->fork_ev);
+        if (dev->join_ev) (void)hipEventDestroy(dev->join_ev);
+        if (dev->side) (void)hipStreamDestroy(dev->side);
         if (dev->stream) (void)hipStreamDestroy(dev->stream);
         delete dev;
         return rc;
@@ -208,6 +214,10 @@ extern "C" void tah_close(tah_dev *dev) {
             if (dev->pinned[i]) (void)hipHostFree(dev->pinned[i]);
             if (dev->copied[i]) (void)hipEventDestroy(dev->copied[i]);
         }
+        if (dev->side) (void)hipStreamSynchronize(dev->side);
+        if (dev->fork_ev) (void)hipEventDestroy(dev->fork_ev);
+        if (dev->join_ev) (void)hipEventDestroy(dev->join_ev);
+        if (dev->side) (void)hipStreamDestroy(dev->side);
         if (dev->stream) (void)hipStreamDestroy(dev->stream);
     }
     delete dev;
@@ -1119,18 +1129,41 @@ extern "C" int tah_represent(tah_dev *dev, const tah_weights *w, const float *to
     });
 }
 
+// From this many rows a batch's column and row stages run as two halves, the second on the device's side stream:
+// each half's kernels then fill the other's last round of workgroups (a column block's 1,600 workgroups at 2,048 rows
+// are 3.125 rounds of the 512 the card runs at once). The halves' rows are independent and their outputs the same.
+constexpr int TWO_HALVES_ROWS = 1024;
+static bool two_halves(const tah_weights *w, const tah_model *model, int k) {
+    return k >= TWO_HALVES_ROWS && model->col_img && column_tokens_fits(w, k / 2, model->features, model->digits) &&
+           column_tokens_fits(w, k - k / 2, model->features, model->digits);
+}
+
+// Joins the side stream back into the main one when it leaves scope (before the loans declared ahead of it go back
+// to the pool), also when a launch threw.
+struct SideJoin {
+    tah_dev *dev;
+    ~SideJoin() {
+        (void)hipEventRecord(dev->join_ev, dev->side);
+        (void)hipStreamWaitEvent(dev->stream, dev->join_ev, 0);
+    }
+};
+
 // Working bytes of predict_rows for k rows, as it borrows them: the tokens and representations; the column stage's
 // cells and scratch (none when it writes the tokens itself over the model's column images); the row stage's scratch
-// (row_stage_floats: compact where only the fused kernels run); the in-context stage's buffers.
+// (row_stage_floats: compact where only the fused kernels run; one for each half when they run apart); the
+// in-context stage's buffers.
 static size_t predict_batch_bytes(const tah_weights *w, const tah_model *model, int k) {
     const int T = w->cls + model->features;
     const size_t kk = (size_t)k;
+    const size_t in_context = loan_bytes({kk * w->d, kk * w->d, kk * w->d, kk * std::max(icl_mid(w), w->dec_hidden)}) +
+                              loan_raw(attention_work_bytes(shape_of(model, model->heads, k)));
+    if (two_halves(w, model, k))
+        return loan_bytes({kk * T * w->e, kk * w->d, row_stage_floats(w, k / 2, T), row_stage_floats(w, k - k / 2, T)}) +
+               in_context;
     const bool direct = column_tokens_fits(w, k, model->features, model->digits);
     const size_t cells = direct ? 0 : kk * model->features * w->e;
     const size_t col = direct && model->col_img ? 0 : column_stage_floats(w, k, model->features, model->digits);
-    return loan_bytes({kk * T * w->e, kk * w->d, cells, col, row_stage_floats(w, k, T), kk * w->d, kk * w->d, kk * w->d,
-                       kk * std::max(icl_mid(w), w->dec_hidden)}) +
-           loan_raw(attention_work_bytes(shape_of(model, model->heads, k)));
+    return loan_bytes({kk * T * w->e, kk * w->d, cells, col, row_stage_floats(w, k, T)}) + in_context;
 }
 
 // All three stages for n rows x (on the card) into out [n][out_n] (on the card), in sub-batches that fit the
@@ -1148,6 +1181,29 @@ static void predict_rows(tah_dev *dev, const tah_weights *w, const tah_model *mo
         float *tok = loans.take<float>((size_t)k * T * w->e);
         float *rep = loans.take<float>((size_t)k * w->d);
         const float *xr = x + (size_t)r0 * model->features;
+        if (two_halves(w, model, k)) {
+            // the first half on the main stream, the second on the side stream after what the main stream holds so
+            // far; the main stream then waits for the side stream's half (SideJoin, also on an error)
+            TAH_HIP(hipEventRecord(dev->fork_ev, dev->stream));
+            TAH_HIP(hipStreamWaitEvent(dev->side, dev->fork_ev, 0));
+            {
+                const SideJoin join{dev};
+                const int half[2] = {k / 2, k - k / 2};
+                for (int hf = 0; hf < 2; hf++) {
+                    const hipStream_t s = hf ? dev->side : dev->stream;
+                    const int r = hf ? half[0] : 0, m = half[hf];
+                    float *sc = loans.take<float>(row_stage_floats(w, m, T));
+                    const bool kv = row_stage_takes_kv(w, m, T);
+                    float *tk = tok + (size_t)r * T * w->e;
+                    column_stage_tokens(s, w, model->col_kv, xr + (size_t)r * model->features, m, model->features, tk,
+                                        kv ? row_stage_kv(w, m, T, sc) : nullptr, kv ? w->cls_kv : nullptr, nullptr,
+                                        model->col_img);
+                    row_stage(s, w, tk, m, T, tabs.cos, tabs.sin, rep + (size_t)r * w->d, sc, kv);
+                }
+            }
+            stage_rows(dev, w, model, rep, k, out_n, out + (size_t)r0 * out_n, loans);
+            continue;
+        }
         float *scratch = nullptr;
         bool kv_ready = false;
         if (column_tokens_fits(w, k, model->features, model->digits)) {

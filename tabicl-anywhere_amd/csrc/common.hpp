@@ -75,6 +75,10 @@ struct tah_dev {
     // this device's copy of the library's static scratch array (tah_stage_dev_noalloc), resolved at tah_open with
     // the device current: a device address, unlike the array's name in host code
     uint8_t *noalloc = nullptr;
+    // a second stream (default priority) for work that runs beside the main stream's, and the events that fork to it
+    // and join back
+    hipStream_t side = nullptr;
+    hipEvent_t fork_ev = nullptr, join_ev = nullptr;
 };
 
 // A block's tensors on the card (device pointers; nullptr where absent).
