@@ -1361,8 +1361,13 @@ static AttnPlan plan(const AttnShape &a, bool images) {
         return p;
     }
     const long target = p.waves == 8 ? 256 : (p.groups == 1 ? 256 : 512);
-    long want = (target + (long)p.groups * a.heads - 1) / ((long)p.groups * a.heads);
-    want = std::max(1L, std::min(want, (long)(k.n_kb + 1) / 2));
+    // the key ranges: of the counts just below and just above target / (query tiles x heads), the one whose rounds of
+    // workgroups times blocks per range is least (768 queries: 10 ranges, 240 workgroups in one round, where 11 made
+    // 264, a second round of 8)
+    const long per = (long)p.groups * a.heads, most = std::max(1L, (long)(k.n_kb + 1) / 2);
+    auto cost = [&](long s) { return ((per * s + target - 1) / target) * ((k.n_kb + s - 1) / s); };
+    const long lo = std::max(1L, std::min(target / per, most)), hi = std::max(1L, std::min((target + per - 1) / per, most));
+    const long want = cost(hi) < cost(lo) ? hi : lo;
     p.kb_per_split = (int)((k.n_kb + want - 1) / want);
     p.splits = (k.n_kb + p.kb_per_split - 1) / p.kb_per_split;
     return p;
