@@ -108,7 +108,7 @@ size_t tah_overdrawn(const tah_dev *dev);
 int tah_release(tah_dev *dev);
 int tah_sync(tah_dev *dev);
 /* The device handle's HIP stream (a hipStream_t), for callers that time or order work around _dev calls. A call may
-   fork part of its work onto a second stream of the handle (the column and row stages of 1,024 rows or more, as two
+   fork part of its work onto a second stream of the handle (the column and row stages of 768 rows or more, as two
    halves); it joins that stream back into this one before it returns, so that ordering on this stream orders all of
    the call's work (a graph captured on it takes the fork and the join with it). */
 void *tah_stream(tah_dev *dev);

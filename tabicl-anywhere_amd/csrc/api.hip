@@ -1132,7 +1132,9 @@ extern "C" int tah_represent(tah_dev *dev, const tah_weights *w, const float *to
 // From this many rows a batch's column and row stages run as two halves, the second on the device's side stream:
 // each half's kernels then fill the other's last round of workgroups (a column block's 1,600 workgroups at 2,048 rows
 // are 3.125 rounds of the 512 the card runs at once). The halves' rows are independent and their outputs the same.
-constexpr int TWO_HALVES_ROWS = 1024;
+// Measured per batch size: 768 rows 2.005 -> 1.955 ms as halves; 512 and 640 rows slower (1.478 -> 1.552, 1.802 ->
+// 1.851 ms), 896 unchanged.
+constexpr int TWO_HALVES_ROWS = 768;
 static bool two_halves(const tah_weights *w, const tah_model *model, int k) {
     return k >= TWO_HALVES_ROWS && model->col_img && column_tokens_fits(w, k / 2, model->features, model->digits) &&
            column_tokens_fits(w, k - k / 2, model->features, model->digits);
