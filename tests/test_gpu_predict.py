@@ -71,14 +71,17 @@ def test_attention_full_width(gpu, full_model, full_weights, kv_format, rows, ch
     assert err < SCORE_TOL
 
 
-@pytest.mark.parametrize("kv_format", [abi.KV_F32, abi.KV_I8])
-def test_attention_many_queries(gpu, full_model, full_weights, kv_format):
-    """2,048 queries (16 tiles of 128 x 8 heads x 8 key ranges): the batched path and its four-coordinate split merge,
-    against the oracle."""
-    say(f"attention 2048 queries fmt={kv_format}")
-    rng = np.random.default_rng(2048 + kv_format)
+@pytest.mark.parametrize("kv_format", [abi.KV_F32, abi.KV_I16, abi.KV_I8])
+@pytest.mark.parametrize("nq", [2048, 1280, 640])
+def test_attention_many_queries(gpu, full_model, full_weights, kv_format, nq):
+    """Many queries over 3,000 stored rows (47 key blocks), against the oracle: 2,048 (8 tiles of 256 queries x 8
+    heads x 4 key ranges of 12 blocks, the last 11), 1,280 (5 tiles x 8 heads x 6 ranges of 8 blocks, the last 7: the
+    range count that keeps 240 workgroups in one round, where rounding up would make 7 ranges and 280) and 640 (3
+    tiles, the last only half live, x 8 heads x 10 ranges of 5 blocks, the last 2)."""
+    say(f"attention {nq} queries fmt={kv_format}")
+    rng = np.random.default_rng(nq + kv_format)
     d, L = full_model.d, full_model.icl_layers
-    rows, chunk, nq = 3000, 256, 2048
+    rows, chunk = 3000, 256
     layers = random_layers(rng, 1, rows, chunk, d, kv_format, scale=0.5) * L
     vm = gpu.load(full_weights, kv_format, rows, chunk, layers, np.ones((L, d), np.float32))
     q = (rng.standard_normal((nq, d)) * 0.3).astype(np.float32)
@@ -198,11 +201,12 @@ def test_stage_full_size(gpu, full_model, full_weights, kv_format, nq):
 
 
 @pytest.mark.parametrize("kv_format", [abi.KV_F32, abi.KV_I16, abi.KV_I8])
-@pytest.mark.parametrize("nq,rows,checked", [(1024, 3000, 1024), (2048, 10000, 256)])
+@pytest.mark.parametrize("nq,rows,checked", [(1024, 3000, 1024), (2048, 10000, 256), (768, 3000, 768), (1280, 3000, 320)])
 def test_stage_large_batches_sampled(gpu, full_model, full_weights, kv_format, nq, rows, checked):
     """The whole in-context stage for a large batch (the 8-wavefront attention kernel, few key ranges, the split-K
     dense layers), `checked` of its rows against the oracle on the same inputs (rows are independent): all 1,024 at
-    3,000 stored rows, 256 at 10,000."""
+    3,000 stored rows, 256 at 10,000; all 768 (the few-row dense kernels, 3 query tiles) and 320 of 1,280 (the split-K
+    dense layers over 40 row tiles, 5 query tiles)."""
     say(f"stage large batch fmt={kv_format} nq={nq} rows={rows}")
     rng = np.random.default_rng(nq + rows + kv_format)
     d, L, chunk = full_model.d, full_model.icl_layers, 256
