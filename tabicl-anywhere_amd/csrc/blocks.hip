@@ -105,14 +105,14 @@ struct KvNext {
 
 // x += l2(gelu(l1(norm2 x))) + b2 for 32 rows a wavefront (after ff128_start, all 256 threads): xv holds this lane's
 // half of its row (columns 16 ks + 8 g + t); xrow is the row's storage, which holds x (read back for the residual
-// add) and takes the result (not where !live). With KV the result goes on, still in registers, through kn's
+// add) and takes the result (not where !live or !keep). With KV the result goes on, still in registers, through kn's
 // normalisation and projection (its four weight slices streamed after W2's) to kn.out (not where !live).
 template <bool KV = false>
 __device__ __forceinline__ void ff128_rows(float (&xv)[8][8], bool live, float *xrow, uint8_t *slab, const float *bias1,
                                            const float *__restrict__ lnw, const float *__restrict__ lnb,
                                            const uint8_t *__restrict__ w1img, int s1,
                                            const uint8_t *__restrict__ w2img, const float *__restrict__ b2, int s2,
-                                           int tid, const KvNext &kn = KvNext{}) {
+                                           int tid, const KvNext &kn = KvNext{}, bool keep = true) {
     constexpr int E = 128;
     const int lane = tid & 63;
     const int r32 = lane & 31, g = lane >> 5;
@@ -238,7 +238,7 @@ __device__ __forceinline__ void ff128_rows(float (&xv)[8][8], bool live, float *
             load8(b2 + c0, bv);
 #pragma unroll
             for (int t = 0; t < 8; t++) xo[t] = y[T][8 * hh + t] * u2 + bv[t] + rv[t];
-            if (live) {
+            if (live && keep) {
                 *reinterpret_cast<float4 *>(dst) = make_float4(xo[0], xo[1], xo[2], xo[3]);
                 *reinterpret_cast<float4 *>(dst + 4) = make_float4(xo[4], xo[5], xo[6], xo[7]);
             }
@@ -1013,7 +1013,7 @@ __global__ __launch_bounds__(256, 2) void k_cell_block(int n, size_t sr, size_t 
 // row block's keys and values (kn.out [n][T][2 e], which may be kv itself: a workgroup reads only its own row's keys
 // and values, all of them before its feed-forward half starts).
 template <bool FF, bool KV>
-__global__ __launch_bounds__(256, 2) void k_row_block(int T, float *tok, const float *kv,
+__global__ __launch_bounds__(256, 2) void k_row_block(int T, int keep, float *tok, const float *kv,
                                                        const float *__restrict__ cosv, const float *__restrict__ sinv,
                                                        const float *__restrict__ n1w, const float *__restrict__ n1b,
                                                        const uint8_t *__restrict__ qimg, int qshift,
@@ -1354,7 +1354,7 @@ __global__ __launch_bounds__(256, 2) void k_row_block(int T, float *tok, const f
         ff128_start(lds, ffb, w1img, b1, tid);
         if constexpr (KV) {
             kn.out += ((size_t)row * T + (live ? tk : 0)) * 2 * E;
-            ff128_rows<true>(xn, live, xrow, lds, ffb, n2w, n2b, w1img, s1, w2img, b2, s2, tid, kn);
+            ff128_rows<true>(xn, live, xrow, lds, ffb, n2w, n2b, w1img, s1, w2img, b2, s2, tid, kn, tk < keep);
         } else {
             ff128_rows(xn, live, xrow, lds, ffb, n2w, n2b, w1img, s1, w2img, b2, s2, tid);
         }
@@ -1370,7 +1370,7 @@ bool block_ff_fits(const DevBlock &b) { return ff_fused_shape(b.d, b.ff) && b.l1
 bool row_kv_fits(const DevBlock &next) { return next.d == 128 && next.inimg && next.in_b && next.n1w && next.n1b; }
 
 void row_block(hipStream_t s, int n, int T, float *tok, const float *kv, const float *cosv, const float *sinv,
-               const DevBlock &b, bool ff, const DevBlock *next, float *kv_next) {
+               const DevBlock &b, bool ff, const DevBlock *next, float *kv_next, int keep) {
     if (n <= 0) return;
     if (!row_block_fits(b, T) || (reinterpret_cast<uintptr_t>(tok) & 15) || (reinterpret_cast<uintptr_t>(kv) & 15))
         throw ArgError{"row_block: needs e = 128, 8 heads, weight images, at most 128 tokens and aligned rows"};
@@ -1378,18 +1378,21 @@ void row_block(hipStream_t s, int n, int T, float *tok, const float *kv, const f
     if (next && (!ff || !row_kv_fits(*next) || !kv_next || (reinterpret_cast<uintptr_t>(kv_next) & 15)))
         throw ArgError{"row_block: the next block's keys and values need the fused feed-forward, e = 128, its "
                        "projection image and an aligned destination"};
+    if (keep < 0) keep = T;
+    if (keep > T || (keep < T && !next))
+        throw ArgError{"row_block: only a block that forms the next one's keys and values may leave tokens unwritten"};
     if (next) {
         const KvNext kn{next->inimg + (size_t)128 * 128 * 4, next->ins, next->n1w, next->n1b, next->in_b + 128,
                         kv_next};
-        hipLaunchKernelGGL((k_row_block<true, true>), dim3(n), dim3(256), 0, s, T, tok, kv, cosv, sinv, b.n1w, b.n1b,
+        hipLaunchKernelGGL((k_row_block<true, true>), dim3(n), dim3(256), 0, s, T, keep, tok, kv, cosv, sinv, b.n1w, b.n1b,
                            b.inimg, b.ins, b.in_b, b.outimg, b.outs, b.out_b, b.n2w, b.n2b, b.l1img, b.l1b, b.l1s,
                            b.l2img, b.l2b, b.l2s, kn);
     } else if (ff) {
-        hipLaunchKernelGGL((k_row_block<true, false>), dim3(n), dim3(256), 0, s, T, tok, kv, cosv, sinv, b.n1w, b.n1b,
+        hipLaunchKernelGGL((k_row_block<true, false>), dim3(n), dim3(256), 0, s, T, T, tok, kv, cosv, sinv, b.n1w, b.n1b,
                            b.inimg, b.ins, b.in_b, b.outimg, b.outs, b.out_b, b.n2w, b.n2b, b.l1img, b.l1b, b.l1s,
                            b.l2img, b.l2b, b.l2s, KvNext{});
     } else {
-        hipLaunchKernelGGL((k_row_block<false, false>), dim3(n), dim3(256), 0, s, T, tok, kv, cosv, sinv, b.n1w,
+        hipLaunchKernelGGL((k_row_block<false, false>), dim3(n), dim3(256), 0, s, T, T, tok, kv, cosv, sinv, b.n1w,
                            b.n1b, b.inimg, b.ins, b.in_b, b.outimg, b.outs, b.out_b, nullptr, nullptr, nullptr,
                            nullptr, 0, nullptr, nullptr, 0, KvNext{});
     }

@@ -208,12 +208,13 @@ bool cell_block_fits(const DevBlock &b);
 // and values kv [n][T][2 e] the projection made (unrotated); e = 128, 8 heads of 16, T <= 128 (row_block_fits).
 // With ff (block_ff_fits) either kernel runs the block's feed-forward half as well, in the same launch; the row
 // block with next as well (ff, row_kv_fits) forms that block's keys and values [n][T][2 e] from the result into
-// kv_next (which may be kv).
+// kv_next (which may be kv), and then stores only the first keep tokens of each row's new values (the rest are
+// then left as the attention half wrote them: for a next block that updates only those tokens).
 bool row_block_fits(const DevBlock &b, int T);
 bool block_ff_fits(const DevBlock &b);
 bool row_kv_fits(const DevBlock &next);
 void row_block(hipStream_t s, int n, int T, float *tok, const float *kv, const float *cosv, const float *sinv,
-               const DevBlock &b, bool ff, const DevBlock *next = nullptr, float *kv_next = nullptr);
+               const DevBlock &b, bool ff, const DevBlock *next = nullptr, float *kv_next = nullptr, int keep = -1);
 size_t cell_block_work_bytes(int groups);
 // The column stage's input layer as the first column block's input: cell (r, g) = in_w vals + in_b over the row's
 // group values vals[k] = x[r][(g + 2^k) mod features] (k < group), or all -100 where every one of them is -100.

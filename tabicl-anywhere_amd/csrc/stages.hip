@@ -1202,7 +1202,9 @@ void row_stage(hipStream_t s, const tah_weights *w, float *tok, int n, int T, co
             const bool ff = block_ff_fits(b) && R > SMALL_ROWS;
             const DevBlock &nb = w->row[bi + 1];
             const bool chain = ff && row_kv_fits(nb) && (bi + 1 < last ? row_block_path(w, bi + 1, n, T) : cls_kernel);
-            row_block(s, n, T, tok, qkv, cosv, sinv, b, ff, chain ? &nb : nullptr, qkv);
+            // before the class-token path only the class tokens' new values are read again (by k_first_tokens): the
+            // others' are not stored (105 MB less written at 2,048 rows of 104 tokens)
+            row_block(s, n, T, tok, qkv, cosv, sinv, b, ff, chain ? &nb : nullptr, qkv, chain && bi + 1 == last ? cls : T);
             kv_ready = chain;
             if (!ff) feed_forward(s, (int)R, tok, b, t, mid);
             continue;
