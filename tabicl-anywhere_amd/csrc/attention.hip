@@ -1203,6 +1203,8 @@ __global__ __launch_bounds__(64) void k_attn_merge(int nq, int d, int heads, int
     }
 }
 
+constexpr int MERGE64_MAX = 16;  // k_attn_merge64 takes at most this many key ranges
+
 // Head width 64, maxima in log2 units: 16 threads per (query, head), four coordinates each, every split's (m, l) and
 // partial sums loaded independently (one wave of loads in flight, not a chain).
 __global__ __launch_bounds__(256) void k_attn_merge64(int items, int heads, int splits, const float *__restrict__ part_o,
@@ -1210,24 +1212,32 @@ __global__ __launch_bounds__(256) void k_attn_merge64(int items, int heads, int 
     const int i = blockIdx.x * 16 + (threadIdx.x >> 4), c4 = (threadIdx.x & 15) * 4;
     if (i >= items) return;
     const size_t stride = (size_t)items;  // between splits, in (query, head) items
+    // all loads issued before any value is used (a loop over the ranges had each range's loads wait for the last's)
+    float2 ml[MERGE64_MAX];
+    float4 po[MERGE64_MAX];
+#pragma unroll
+    for (int sp = 0; sp < MERGE64_MAX; sp++)
+        if (sp < splits) {
+            const size_t at = sp * stride + i;
+            ml[sp] = *reinterpret_cast<const float2 *>(part_ml + at * 2);
+            po[sp] = *reinterpret_cast<const float4 *>(part_o + at * 64 + c4);
+        }
     float M = -INFINITY;
-    for (int sp = 0; sp < splits; sp++) {
-        const float2 ml = *reinterpret_cast<const float2 *>(part_ml + (sp * stride + i) * 2);
-        if (ml.y > 0.0f) M = fmaxf(M, ml.x);
-    }
+#pragma unroll
+    for (int sp = 0; sp < MERGE64_MAX; sp++)
+        if (sp < splits && ml[sp].y > 0.0f) M = fmaxf(M, ml[sp].x);
     float L = 0.0f;
     float4 O = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int sp = 0; sp < splits; sp++) {
-        const size_t at = sp * stride + i;
-        const float2 ml = *reinterpret_cast<const float2 *>(part_ml + at * 2);
-        const float4 po = *reinterpret_cast<const float4 *>(part_o + at * 64 + c4);
-        const float f = ml.y > 0.0f ? exp2_hw(ml.x - M) : 0.0f;
-        L += ml.y * f;
-        O.x += po.x * f;
-        O.y += po.y * f;
-        O.z += po.z * f;
-        O.w += po.w * f;
-    }
+#pragma unroll
+    for (int sp = 0; sp < MERGE64_MAX; sp++)
+        if (sp < splits) {
+            const float f = ml[sp].y > 0.0f ? exp2_hw(ml[sp].x - M) : 0.0f;
+            L += ml[sp].y * f;
+            O.x += po[sp].x * f;
+            O.y += po[sp].y * f;
+            O.z += po[sp].z * f;
+            O.w += po[sp].w * f;
+        }
     const int qr = i / heads, h = i - qr * heads;
     *reinterpret_cast<float4 *>(out + ((size_t)qr * heads + h) * 64 + c4) = make_float4(O.x / L, O.y / L, O.z / L, O.w / L);
 }
@@ -1516,7 +1526,7 @@ void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t 
         default: throw ArgError{"attention: unknown key/value format"};
     }
     if (p.splits > 1) {
-        if (a.d == 64 * a.heads && p.splits <= 16)  // many queries, few splits (else lanes over splits win)
+        if (a.d == 64 * a.heads && p.splits <= MERGE64_MAX)  // many queries, few splits (else lanes over splits win)
             hipLaunchKernelGGL(k_attn_merge64, dim3((a.nq * a.heads + 15) / 16), dim3(256), 0, s, a.nq * a.heads,
                                a.heads, p.splits, part_o, part_ml, out);
         else if (a.d == 64 * a.heads)
