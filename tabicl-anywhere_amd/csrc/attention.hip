@@ -1361,16 +1361,19 @@ static AttnPlan plan(const AttnShape &a, bool images) {
     p.waves = p.split16 && (a.nq >= 512 || a.kv_format == TAH_KV_I16) ? 8 : 4;
     const int per_group = p.split16 ? 32 * p.waves : QG;
     p.groups = (a.nq + per_group - 1) / per_group;
-    // enough workgroups to fill the 256 compute units about once (twice for the smaller workgroups of two or more
-    // query tiles), each with at least 2 key blocks: more, shorter key ranges measured slower at every batch (the
-    // merge and each workgroup's fixed costs grow with them; 64 queries: 22 us at 256 workgroups against 36 at 632)
+    // enough workgroups to fill the 256 compute units about once, each with at least 2 key blocks: more, shorter key
+    // ranges measured slower at every batch (the merge and each workgroup's fixed costs grow with them; 64 queries:
+    // 22 us at 256 workgroups against 36 at 632; f32 tiles at two workgroups a compute unit for two or more 128-query
+    // tiles, up to 32 ranges: 256 / 384 rows 1.122 / 1.338 ms against 1.097 / 1.291 ms at one, whose 16 or fewer
+    // ranges k_attn_merge64 takes). The i8 code images, half the products and bytes a block, keep two workgroups a
+    // compute unit there (at one, 160-448 rows took 2-4% longer).
     if (!p.split16 && hd == 64) {
         // the decode kernel's wavefronts each take a key block of their own: four blocks a workgroup
         p.kb_per_split = std::min(4, k.n_kb);
         p.splits = (k.n_kb + p.kb_per_split - 1) / p.kb_per_split;
         return p;
     }
-    const long target = p.waves == 8 ? 256 : (p.groups == 1 ? 256 : 512);
+    const long target = p.waves == 4 && p.groups > 1 && a.kv_format == TAH_KV_I8 ? 512 : 256;
     // the key ranges: of the counts just below and just above target / (query tiles x heads), the one whose rounds of
     // workgroups times blocks per range is least (768 queries: 10 ranges, 240 workgroups in one round, where 11 made
     // 264, a second round of 8)
