@@ -1357,8 +1357,11 @@ static AttnPlan plan(const AttnShape &a, bool images) {
     const int hd = a.d / a.heads;
     p.split16 = hd == 64 && a.nq >= split16_min_q(a.kv_format) && images && kv_images_apply(a.kv_format, a.d, a.heads);
     // k_attn_split64: 256 queries a workgroup (one a compute unit, one wave of them) from 512 queries on, else 128
-    // (two a compute unit, two waves of them); an i16 layer's (whose staging takes 33 KB of LDS more) always 256
-    p.waves = p.split16 && (a.nq >= 512 || a.kv_format == TAH_KV_I16) ? 8 : 4;
+    // (two a compute unit, two waves of them); an i16 layer's (whose staging takes 33 KB of LDS more, one workgroup a
+    // compute unit) 256 from 129 queries on, and 128 for one tile of up to 128 queries (its wavefronts without live
+    // queries then do not share the SIMDs: 4 / 16 / 64 rows 0.771 / 0.882 / 0.931 -> 0.762 / 0.877 / 0.928 ms;
+    // at 256 and 384 rows four wavefronts were 4.5% slower)
+    p.waves = p.split16 && (a.nq >= 512 || (a.kv_format == TAH_KV_I16 && a.nq > 128)) ? 8 : 4;
     const int per_group = p.split16 ? 32 * p.waves : QG;
     p.groups = (a.nq + per_group - 1) / per_group;
     // enough workgroups to fill the 256 compute units about once, each with at least 2 key blocks: more, shorter key
@@ -1515,7 +1518,10 @@ void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t 
                 if (p.waves == 8) launch_split<8, TAH_KV_F32>(s, a, p, q, *img, out, part_o, part_ml);
                 else launch_split<4, TAH_KV_F32>(s, a, p, q, *img, out, part_o, part_ml);
                 break;
-            case TAH_KV_I16: launch_split<8, TAH_KV_I16>(s, a, p, q, *img, out, part_o, part_ml); break;
+            case TAH_KV_I16:
+                if (p.waves == 8) launch_split<8, TAH_KV_I16>(s, a, p, q, *img, out, part_o, part_ml);
+                else launch_split<4, TAH_KV_I16>(s, a, p, q, *img, out, part_o, part_ml);
+                break;
             default:
                 if (p.waves == 8) launch_split<8, TAH_KV_I8>(s, a, p, q, *img, out, part_o, part_ml);
                 else launch_split<4, TAH_KV_I8>(s, a, p, q, *img, out, part_o, part_ml);
