@@ -1356,12 +1356,14 @@ static AttnPlan plan(const AttnShape &a, bool images) {
     const KeyBlocks k = key_blocks(a.rows, a.chunk);
     const int hd = a.d / a.heads;
     p.split16 = hd == 64 && a.nq >= split16_min_q(a.kv_format) && images && kv_images_apply(a.kv_format, a.d, a.heads);
-    // k_attn_split64: 256 queries a workgroup (one a compute unit, one wave of them) from 512 queries on, else 128
-    // (two a compute unit, two waves of them); an i16 layer's (whose staging takes 33 KB of LDS more, one workgroup a
-    // compute unit) 256 from 129 queries on, and 128 for one tile of up to 128 queries (its wavefronts without live
-    // queries then do not share the SIMDs: 4 / 16 / 64 rows 0.771 / 0.882 / 0.931 -> 0.762 / 0.877 / 0.928 ms;
-    // at 256 and 384 rows four wavefronts were 4.5% slower)
-    p.waves = p.split16 && (a.nq >= 512 || (a.kv_format == TAH_KV_I16 && a.nq > 128)) ? 8 : 4;
+    // k_attn_split64: 256 queries a workgroup (one a compute unit, one wave of them) from 768 queries on, else 128
+    // (at 512 / 640 rows f32 1.376 / 1.740 -> 1.368 / 1.717 ms and i8 1.337 / 1.705 -> 1.330 / 1.676 ms with the
+    // smaller tiles than from 512; from 1,024 or 1,536 queries f32 was slower at 768 to 1,280); an i16 layer's (whose
+    // staging takes 33 KB of LDS more, one workgroup a compute unit) 256 from 129 queries on, and 128 for one tile of
+    // up to 128 queries (its wavefronts without live queries then do not share the SIMDs: 4 / 16 / 64 rows 0.771 /
+    // 0.882 / 0.931 -> 0.762 / 0.877 / 0.928 ms; at 256 and 384 rows four wavefronts were 4.5% slower)
+    const int eight_from = a.kv_format == TAH_KV_I16 ? 129 : 768;
+    p.waves = p.split16 && a.nq >= eight_from ? 8 : 4;
     const int per_group = p.split16 ? 32 * p.waves : QG;
     p.groups = (a.nq + per_group - 1) / per_group;
     // enough workgroups to fill the 256 compute units about once, each with at least 2 key blocks: more, shorter key

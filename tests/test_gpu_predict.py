@@ -76,8 +76,9 @@ def test_attention_full_width(gpu, full_model, full_weights, kv_format, rows, ch
 def test_attention_many_queries(gpu, full_model, full_weights, kv_format, nq):
     """Many queries over 3,000 stored rows (47 key blocks), against the oracle: 2,048 (8 tiles of 256 queries x 8
     heads x 4 key ranges of 12 blocks, the last 11), 1,280 (5 tiles x 8 heads x 6 ranges of 8 blocks, the last 7: the
-    range count that keeps 240 workgroups in one round, where rounding up would make 7 ranges and 280) and 640 (3
-    tiles, the last only half live, x 8 heads x 10 ranges of 5 blocks, the last 2)."""
+    range count that keeps 240 workgroups in one round, where rounding up would make 7 ranges and 280) and 640 (f32
+    and i8: 5 tiles of 128 queries x 8 heads x 6 or 12 ranges; i16: 3 tiles of 256, the last only half live, x 8
+    heads x 10 ranges of 5 blocks, the last 2)."""
     say(f"attention {nq} queries fmt={kv_format}")
     rng = np.random.default_rng(nq + kv_format)
     d, L = full_model.d, full_model.icl_layers
