@@ -15,9 +15,9 @@
 //    instructions). Operands are scaled by powers of two first (exact): each query to a maximum near 2^14, each
 //    head's keys and values by the layer's maximum, and the softmax weights to at most 2^15, so that no half
 //    overflows and the low halves stay normal for all but negligible elements.
-//  * k_attn_decode_w: head width 64 and few queries (or no images), from the records: 256 threads per (four key blocks, head, 8
-//    queries), each wavefront streaming a key block of its own with no barrier (lane = key for the scores, lane =
-//    coordinate for the weighted sum), integer codes scaled through the query and the sums.
+//  * k_attn_decode_w: head width 64 and few queries (or no images), from the records: 256 threads per (six key
+//    blocks, head, 8 queries), each wavefront streaming a key block at a time with no barrier (lane = key for the
+//    scores, lane = coordinate for the weighted sum), integer codes scaled through the query and the sums.
 //  * k_attn_decode: any other head width up to 64 (the tiny test models): the same with one wavefront.
 // All of them leave the running maximum in log2 units (score * log2 e) for the split merge (head width 64:
 // k_attn_merge64 for few key ranges, k_attn_merge_w for many; k_attn_merge otherwise).
@@ -1373,8 +1373,10 @@ static AttnPlan plan(const AttnShape &a, bool images) {
     // ranges k_attn_merge64 takes). The i8 code images, half the products and bytes a block, keep two workgroups a
     // compute unit there (at one, 160-448 rows took 2-4% longer).
     if (!p.split16 && hd == 64) {
-        // the decode kernel's wavefronts each take a key block of their own: four blocks a workgroup
-        p.kb_per_split = std::min(4, k.n_kb);
+        // the decode kernel's wavefronts each take a key block of their own: six blocks a workgroup, two of its four
+        // wavefronts taking a second (fewer ranges for the merge: an i16 row 0.583 -> 0.556 ms, two rows 0.640 ->
+        // 0.621 ms against four blocks; three rows unchanged; 8 / 12 / 16 blocks slower)
+        p.kb_per_split = std::min(6, k.n_kb);
         p.splits = (k.n_kb + p.kb_per_split - 1) / p.kb_per_split;
         return p;
     }
