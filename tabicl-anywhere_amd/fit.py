@@ -9,6 +9,9 @@ problem's in-context stage (`tah_in_context`), which hands back every layer's st
 """
 from __future__ import annotations
 
+import os
+import threading
+from concurrent.futures import ThreadPoolExecutor
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -18,6 +21,32 @@ from .bundle import write as bundle_write
 from .plan import Plan, parse_tree
 
 F = np.float32
+
+# A layer's records (41 MB at 10,000 rows in f32) are copied out of the card's staging buffer before the sink returns,
+# and a fresh array's pages fault in on first touch: one thread took 4.1 ms a layer, longer than the card's own work
+# on the next layer, which it holds up. Eight slices on as many threads (numpy releases the interpreter for the copy).
+_COPY_THREADS = max(1, min(8, os.cpu_count() or 1))
+_COPY_MIN = 1 << 22  # smaller records are copied on the calling thread
+_copy_pool = None
+_copy_lock = threading.Lock()
+
+
+def copy_records(rec: np.ndarray) -> np.ndarray:
+    """A copy of a layer's records (a 1-D array), sliced over a few threads when large."""
+    global _copy_pool
+    out = np.empty_like(rec)
+    n = rec.size
+    if _COPY_THREADS == 1 or n < _COPY_MIN:
+        np.copyto(out, rec)
+        return out
+    with _copy_lock:
+        if _copy_pool is None:
+            _copy_pool = ThreadPoolExecutor(_COPY_THREADS, thread_name_prefix="tah-records")
+    step = -(-n // _COPY_THREADS)
+    parts = [(i, min(n, i + step)) for i in range(0, n, step)]
+    for f in [_copy_pool.submit(np.copyto, out[a:b], rec[a:b]) for a, b in parts]:
+        f.result()
+    return out
 
 
 def exp1(x: np.ndarray) -> np.ndarray:
@@ -158,7 +187,7 @@ def fit_raw_hooks(gpu, weights, x, y, classes: int, chunk: int = 256, kv_format:
         m.add_y(m.t["icl_y"], np.asarray(node.y, F), h)
         scales = np.stack([query_scale(b, rows if node.rows is None else len(node.rows)) for b in m.icl]).astype(F)
         layers = []
-        gpu.in_context_fit(weights, h, scales, kv_format, chunk, lambda l, rec: layers.append(rec.copy()))
+        gpu.in_context_fit(weights, h, scales, kv_format, chunk, lambda l, rec: layers.append(copy_records(rec)))
         fitted.scales.append(scales)
         fitted.layers.append(layers)
     return fitted
@@ -240,7 +269,7 @@ def fit_raw(gpu, weights, x, y, classes: int, chunk: int = 256, kv_format: int =
         m.add_y(m.t["icl_y"], np.asarray(node.y, F), h)
         scales = np.stack([query_scale(b, n_rows) for b in m.icl]).astype(F)
         layers = []
-        gpu.in_context_fit(weights, h, scales, kv_format, chunk, lambda l, rec: layers.append(rec.copy()))
+        gpu.in_context_fit(weights, h, scales, kv_format, chunk, lambda l, rec: layers.append(copy_records(rec)))
         fitted.scales.append(scales)
         fitted.layers.append(layers)
     return fitted

@@ -45,3 +45,16 @@ def test_bundle_round_trip(tmp_path):
     g = B.Bundle.open(os.path.join(GOLDEN, "tiny-raw.tirs"))
     again = B.write(None, {e.name: g.array(e.name) for e in g.entries})
     assert again == bytes(g.data)
+
+
+def test_copy_records_is_an_exact_copy():
+    """The fit's record copy (sliced over threads from 4 MiB on) returns the same bytes, in a new array, at sizes
+    below, at and above the threshold and not a multiple of the slice count."""
+    rng = np.random.default_rng(5)
+    for n in (0, 1, 4095, 1 << 22, (1 << 22) + 1, 41_156_608 + 7):
+        src = rng.integers(0, 256, n, dtype=np.uint8)
+        got = fit.copy_records(src)
+        assert got.dtype == np.uint8 and got.shape == src.shape
+        assert np.array_equal(got, src)
+        if n:
+            assert not np.shares_memory(got, src)
