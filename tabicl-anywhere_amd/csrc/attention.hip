@@ -1381,13 +1381,16 @@ static AttnPlan plan(const AttnShape &a, bool images) {
         return p;
     }
     const long target = p.waves == 4 && p.groups > 1 && a.kv_format == TAH_KV_I8 ? 512 : 256;
-    // the key ranges: of the counts just below and just above target / (query tiles x heads), the one whose rounds of
-    // workgroups times blocks per range is least (768 queries: 10 ranges, 240 workgroups in one round, where 11 made
-    // 264, a second round of 8)
+    // the key ranges: the count whose rounds of workgroups times (blocks per range + 2, a workgroup's fixed cost in
+    // blocks: its queries' load and split, its partials, their share of the merge) is least, the fewest ranges of
+    // equal cost (768 queries: 10 ranges, 240 workgroups in one round, where 11 made 264, a second round of 8; the
+    // fit's 10,000 queries: 4 ranges, 5 rounds of 40 blocks, where one range made 320 workgroups, 2 rounds of 157;
+    // without the fixed cost the count would grow to 32 ranges of 5 blocks at 768 queries, which measured slower)
     const long per = (long)p.groups * a.heads, most = std::max(1L, (long)(k.n_kb + 1) / 2);
-    auto cost = [&](long s) { return ((per * s + target - 1) / target) * ((k.n_kb + s - 1) / s); };
-    const long lo = std::max(1L, std::min(target / per, most)), hi = std::max(1L, std::min((target + per - 1) / per, most));
-    const long want = cost(hi) < cost(lo) ? hi : lo;
+    auto cost = [&](long s) { return ((per * s + target - 1) / target) * ((k.n_kb + s - 1) / s + 2); };
+    long want = 1;
+    for (long s = 2; s <= most; s++)
+        if (cost(s) < cost(want)) want = s;
     p.kb_per_split = (int)((k.n_kb + want - 1) / want);
     p.splits = (k.n_kb + p.kb_per_split - 1) / p.kb_per_split;
     return p;
