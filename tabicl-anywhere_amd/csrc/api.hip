@@ -1302,9 +1302,16 @@ static void column_blocks(hipStream_t s, const tah_weights *w, float *cells, int
     const size_t per = 2 * (size_t)e * inds, M = (size_t)g * rows, I = (size_t)g * inds;
     for (int bi = 0; bi < nb; bi++) {
         const DevBlock &a1 = w->col_a1[bi], &a2 = w->col_a2[bi];
-        // the inducing points look at this batch's cells (src/fit.rs:366-392)
-        layer_norm(s, (int)M, e, cells, e, a1.n1w, a1.n1b, b.t, e);
-        gemm(s, (int)M, 2 * e, e, b.t, e, a1.in_w + (size_t)e * e, a1.in_b + e, b.mid, 2 * e, EPI_NONE, nullptr, 0);
+        // the inducing points look at this batch's cells (src/fit.rs:366-392): the cells' keys and values, their
+        // layer norm inside the projection's kernel where the block has its weight image (1,000,000 cells: 1.4 ms
+        // as a norm and a product apart, each row read and written once more)
+        if (a1.inimg && e == 128) {
+            rows128(s, (int)M, 2 * e, cells, e, a1.inimg + (size_t)128 * e * 4, a1.ins, a1.in_b + e, b.mid, 2 * e,
+                    EPI_NONE, nullptr, 0, nullptr, a1.n1w, a1.n1b);
+        } else {
+            layer_norm(s, (int)M, e, cells, e, a1.n1w, a1.n1b, b.t, e);
+            gemm(s, (int)M, 2 * e, e, b.t, e, a1.in_w + (size_t)e * e, a1.in_b + e, b.mid, 2 * e, EPI_NONE, nullptr, 0);
+        }
         ind_attention(s, w, rows, g, indq + (size_t)bi * inds * e, b.mid, b.acc, b.work);
         gemm(s, (int)I, e, e, b.acc, e, a1.out_w, a1.out_b, b.hid, e, EPI_NONE, nullptr, 0);
         add_ind(s, I * e, inds, e, w->col_ind + (size_t)bi * inds * e, b.hid);
