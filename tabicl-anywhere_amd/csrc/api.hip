@@ -958,10 +958,10 @@ extern "C" int tah_in_context(tah_dev *dev, const tah_weights *w, const float *h
         TAH_HIP(hipMemcpyAsync(sc, scales, sizeof(float) * L * d, hipMemcpyHostToDevice, s));
         for (int l = 0; l < L; l++) {
             const DevBlock &b = w->icl[l];
-            // keys and values of every row, stored (src/fit.rs:627-663)
-            layer_norm(s, rows, d, h, d, b.n1w, b.n1b, t, d);
-            dense(s, rows, 2 * d, d, t, d, b.in_w + (size_t)d * d, b.in_s.rows(d), b.in_b + d, kv, 2 * d, EPI_NONE,
-                  nullptr, 0);
+            // keys and values of every row, stored (src/fit.rs:627-663); the layer norms inside the products' kernels
+            // where they take them (the split-K kernels from 1,025 rows), else into t first
+            dense(s, rows, 2 * d, d, h, d, b.in_w + (size_t)d * d, b.in_s.rows(d), b.in_b + d, kv, 2 * d, EPI_NONE,
+                  nullptr, 0, b.n1w, b.n1b, t);
             to_records(s, rows, d, chunk, kv, rec32);
             const uint8_t *stored = reinterpret_cast<const uint8_t *>(rec32);
             if (kv_format != TAH_KV_F32) {
@@ -975,14 +975,13 @@ extern "C" int tah_in_context(tah_dev *dev, const tah_weights *w, const float *h
             if (!last) {
                 // every row attends to all rows over the exact keys and values, then the rest of the block
                 // (src/fit.rs:667-744)
-                dense(s, rows, d, d, t, d, b.in_w, b.in_s.rows(0), b.in_b, q, d, EPI_NONE, nullptr, 0);
+                dense(s, rows, d, d, h, d, b.in_w, b.in_s.rows(0), b.in_b, q, d, EPI_NONE, nullptr, 0, b.n1w, b.n1b, t);
                 query_modulate(s, rows, b, sc + (size_t)l * d, q, mid);
                 if (use_img)
                     kv_images(s, rows, chunk, d, w->icl_heads, TAH_KV_F32, reinterpret_cast<const uint8_t *>(rec32), img);
                 attention(s, a, q, reinterpret_cast<const uint8_t *>(rec32), att, work, use_img ? &img : nullptr);
                 dense(s, rows, d, d, att, d, b.out_w, b.out_s, b.out_b, h, d, EPI_RESID, h, d);
-                layer_norm(s, rows, d, h, d, b.n2w, b.n2b, t, d);
-                dense(s, rows, b.ff, d, t, d, b.l1w, b.l1_s, b.l1b, mid, b.ff, EPI_GELU, nullptr, 0);
+                dense(s, rows, b.ff, d, h, d, b.l1w, b.l1_s, b.l1b, mid, b.ff, EPI_GELU, nullptr, 0, b.n2w, b.n2b, t);
                 dense(s, rows, d, b.ff, mid, b.ff, b.l2w, b.l2_s, b.l2b, h, d, EPI_RESID, h, d);
             }
             // the card works on layer l (queued above) while the sink takes layer l - 1's records; on the stream the
