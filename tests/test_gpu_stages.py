@@ -81,7 +81,7 @@ def test_embed_with_label_digits_and_missing_cells(gpu, tiny_model):
 
 
 @pytest.mark.parametrize("features,n", [(100, 24), (150, 24), (100, 1), (100, 3), (100, 64), (100, 130), (124, 130),
-                                        (100, 520), (100, 800), (100, 1030)])
+                                        (100, 520), (100, 800), (100, 801), (100, 1030)])
 def test_stages_full_size(gpu, full_model, full_weights, features, n):
     """Full-size column stage (3 blocks, 8 x 16 heads, 128 inducing points per group) and row stage (104, 128 or
     154 tokens, RoPE) against the oracle, then all three stages with a stored in-context cache. One row takes the
@@ -89,7 +89,7 @@ def test_stages_full_size(gpu, full_model, full_weights, features, n):
     from 128 rows the fused column and row blocks, the column stage written into the tokens and each block forming
     the next one's keys and values (130 rows: up to 128 tokens, the row block's largest row); from 512 rows the last
     row block's class-token attention; from 768 rows a prediction's column and row stages as two halves on two
-    streams (800 rows: 400 each); from 1,024 rows the input layer a workgroup per table row."""
+    streams (800 rows: 400 each; 801 rows: 400 and 401); from 1,024 rows the input layer a workgroup per table row."""
     say(f"stages full features={features} n={n}")
     m = full_model
     rng = np.random.default_rng(features + n)
