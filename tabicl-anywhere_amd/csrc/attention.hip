@@ -9,12 +9,15 @@
 // (Soft::merge, src/nn.rs:261-276) and divided through (Soft::finish).
 //
 // The kernels:
-//  * k_attn_split64: head width 64, at least 32 queries, over tile images (below; any cache format). Every f32
+//  * k_attn_split64: head width 64 over tile images (below; any cache format: f32 from 17 queries, i8 from one,
+//    i16 from 4), 32 queries a wavefront. Every f32
 //    product runs on the fp16 matrix cores as three products of fp16 halves (device_math.hpp): the error is that
 //    of an f32 dot product, at v_mfma_f32_32x32x16_f16's rate (2 PFLOP/s sustained, 16x that of the f32 matrix
 //    instructions). Operands are scaled by powers of two first (exact): each query to a maximum near 2^14, each
 //    head's keys and values by the layer's maximum, and the softmax weights to at most 2^15, so that no half
 //    overflows and the low halves stay normal for all but negligible elements.
+//  * k_attn_few: head width 64, 1 to 16 queries over f32 images: the four wavefronts of a workgroup split each key
+//    block, with the queries as the 16 columns of 16 x 16 products, and merge their softmax states at the end.
 //  * k_attn_decode_w: head width 64 and few queries (or no images), from the records: 256 threads per (six key
 //    blocks, head, 8 queries), each wavefront streaming a key block at a time with no barrier (lane = key for the
 //    scores, lane = coordinate for the weighted sum), integer codes scaled through the query and the sums.
@@ -1171,6 +1174,245 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows
     }
 }
 
+// ---- few-query kernel: head width 64, 1 to FEW_Q queries, over f32 split images --------------------------------
+// grid heads x splits (workgroup i: head i % heads, key range i / heads); 256 threads. With few queries the 32-query
+// products of k_attn_split64 leave most of their columns (and whole wavefronts) idle while the kernel waits on
+// memory; here the four wavefronts share each 64-key block and split it, wavefront w taking keys 16 w .. 16 w + 15,
+// with the queries as the columns of 16 x 16 products, G groups of 16:
+//  * S = K Q^T with v_mfma_f32_16x16x32_f16, three products of split halves per 32 coordinates: lane l then holds
+//    query 16 g + l % 16 against keys 16 w + 4 (l / 16) + 0..3, which is exactly the B operand of
+//  * O^T += V^T P^T with v_mfma_f32_16x16x16_f16 over the wavefront's 16 keys, for four blocks of 16 coordinates.
+// The keys' and values' operands are read once a block for all G groups. Each wavefront runs its own online softmax
+// over its keys (as k_attn_split64: log2 units, the reference maximum raised when a block passes it by more than 3);
+// at the end the four are merged through LDS into the same partials, or output, as k_attn_split64 leaves. The
+// blocks stream through a ring of four 32 KB LDS slots by DMA, three blocks in flight while one is used, one barrier
+// a block. Launched for one group (up to 16 queries): with two or four groups (17 to 64 queries) it measured slower
+// than k_attn_split64 (17 / 33 / 64 rows 0.836 / 0.852 / 0.884 -> 0.852 / 0.922 / 0.977 ms a prediction), whose
+// 32-query products then have work for their columns.
+constexpr int FEW_Q = 16;
+
+typedef _Float16 halfx4 __attribute__((ext_vector_type(4)));
+
+// s_waitcnt immediates that wait for at most n vector-memory operations in flight (gfx9 encoding: vmcnt bits 3:0 and
+// 15:14, export and LDS counts left at their maxima)
+constexpr int vmcnt_at_most(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// the maximum (sum) of x over lanes l, l ^ 16 (rows of 16 swapped in pairs) and over lanes l, l ^ 32
+__device__ __forceinline__ float max16(float x) {
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+__device__ __forceinline__ float max32(float x) {
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+__device__ __forceinline__ float sum16(float x) {
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+__device__ __forceinline__ float sum32(float x) {
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+
+template <int G>
+__global__ __launch_bounds__(256, 1) void k_attn_few(int nq, int rows, int chunk, int d, int heads,
+                                                      const float *__restrict__ q, const uint8_t *__restrict__ images,
+                                                      const uint32_t *__restrict__ kvmax, int kb_per_split, int splits,
+                                                      float *__restrict__ part_o, float *__restrict__ part_ml,
+                                                      float *__restrict__ out) {
+    constexpr int SLOTS = 4, PER_BLOCK = IMG / (16 * 256);  // a block: 8 copies of 16 bytes a thread
+    constexpr int NQ = 16 * G;
+    static_assert(4 * 64 * NQ * 4 + 2 * 4 * NQ * 4 <= IMG * SLOTS, "the merge fits in the ring");
+    __shared__ __align__(16) uint8_t ring[SLOTS][IMG];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int qi = lane & 15, lg = lane >> 4;
+    const int h = blockIdx.x % heads, split = blockIdx.x / heads;
+    const KeyBlocks kbs = key_blocks(rows, chunk);
+    const int kb0 = split * kb_per_split, kb1 = min(kbs.n_kb, kb0 + kb_per_split);
+    const uint8_t *head_images = images + (size_t)h * IMG;
+    const size_t kb_stride = (size_t)heads * IMG;
+
+    // query 16 g + qi's coordinates 32 ks + 8 lg + t (the B operand of the scores), loaded without a branch (a lane
+    // past the last query reads query 0 and zeroes it), then the first blocks' copies issued
+    float4 raw[G][4];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const float *src = q + (size_t)min(16 * g + qi, nq - 1) * d + h * 64 + 8 * lg;
+#pragma unroll
+        for (int j = 0; j < 4; j++) raw[g][j] = *reinterpret_cast<const float4 *>(src + 32 * (j >> 1) + 4 * (j & 1));
+    }
+#pragma unroll
+    for (int i = 0; i < SLOTS - 1; i++)
+        if (kb0 + i < kb1) half_image_to_lds<4, IMG>(head_images + (kb0 + i) * kb_stride, ring[i], tid);
+    // each query scaled to a maximum near 2^14 and split
+    halfx8 qh[G][2], ql[G][2];
+    float to_log2[G];
+    const int sk = shift_for(kvmax[h * 2]), sv = shift_for(kvmax[h * 2 + 1]);
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const float live = 16 * g + qi < nq ? 1.0f : 0.0f;
+        float qv[2][8];
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            const float4 a = raw[g][2 * ks], b = raw[g][2 * ks + 1];
+            qv[ks][0] = a.x * live; qv[ks][1] = a.y * live; qv[ks][2] = a.z * live; qv[ks][3] = a.w * live;
+            qv[ks][4] = b.x * live; qv[ks][5] = b.y * live; qv[ks][6] = b.z * live; qv[ks][7] = b.w * live;
+        }
+        float qmax = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+            for (int t = 0; t < 8; t++) qmax = fmaxf(qmax, fabsf(qv[ks][t]));
+        const int eq = shift_for_max(max32(max16(qmax)));
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) split8(qv[ks], ldexpf(1.0f, eq), qh[g][ks], ql[g][ks]);
+        to_log2[g] = ldexpf(LOG2E, -(sk + eq));
+    }
+
+    float ref[G], l[G];
+    floatx4 acc[G][4];  // O^T: coordinate 16 m + 4 lg + i of query 16 g + qi, in units of 2^sv
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        ref[g] = -INFINITY;
+        l[g] = 0.0f;
+#pragma unroll
+        for (int m = 0; m < 4; m++) acc[g][m] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    const int krow = 16 * wave + (lane & 15);                      // the scores' A row: key krow
+    const int vchunk = 2 * wave + (lg >> 1), voff = 8 * (lg & 1);  // the values' A operand: keys 16 wave + 4 lg + ..
+    for (int kb = kb0; kb < kb1; kb++) {
+        // block kb's copies have landed (the ones after it may still be in flight), everyone's, and everyone is done
+        // with block kb - 1, whose slot the copy of block kb + 3 then takes
+        const int ahead = min(kb1 - 1, kb + SLOTS - 2) - kb;
+        if (ahead >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_at_most(2 * PER_BLOCK));
+        else if (ahead == 1) __builtin_amdgcn_s_waitcnt(vmcnt_at_most(PER_BLOCK));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_at_most(0));
+        __syncthreads();
+        if (kb + SLOTS - 1 < kb1)
+            half_image_to_lds<4, IMG>(head_images + (kb + SLOTS - 1) * kb_stride, ring[(kb + SLOTS - 1 - kb0) % SLOTS], tid);
+        const int ci = kb / kbs.bpc;
+        const int nk = min(KB, (ci == kbs.n_chunks - 1 ? kbs.last_rc : chunk) - (kb % kbs.bpc) * KB);
+        if (16 * wave >= nk) continue;  // this wavefront's keys are all past the block's end
+        const uint8_t *img = ring[(kb - kb0) % SLOTS];
+        halfx8 khi[2], klo[2];
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            const int off = krow * 128 + swz(krow, 4 * ks + lg) * 16;
+            khi[ks] = *reinterpret_cast<const halfx8 *>(img + off);
+            klo[ks] = *reinterpret_cast<const halfx8 *>(img + 8192 + off);
+        }
+        halfx4 vhi[4], vlo[4];
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const int r = 16 * m + (lane & 15);
+            const int vo = r * 128 + swz(r, vchunk) * 16 + voff;
+            vhi[m] = *reinterpret_cast<const halfx4 *>(img + 16384 + vo);
+            vlo[m] = *reinterpret_cast<const halfx4 *>(img + 24576 + vo);
+        }
+        floatx4 sc[G];
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            sc[g] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                sc[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(khi[ks], qh[g][ks], sc[g], 0, 0, 0);
+                sc[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(khi[ks], ql[g][ks], sc[g], 0, 0, 0);
+                sc[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(klo[ks], qh[g][ks], sc[g], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            if (nk < KB) {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (16 * wave + 4 * lg + i >= nk) sc[g][i] = -INFINITY;
+            }
+            const float mb = max32(max16(fmaxf(fmaxf(sc[g][0], sc[g][1]), fmaxf(sc[g][2], sc[g][3])))) * to_log2[g];
+            const bool grow = mb > ref[g] + 3.0f;
+            if (__any(grow)) {
+                const float nref = grow ? mb : ref[g];
+                const float alpha = exp2_hw(ref[g] - nref);
+                l[g] *= alpha;
+#pragma unroll
+                for (int m = 0; m < 4; m++) acc[g][m] *= alpha;
+                ref[g] = nref;
+            }
+            const float off = 12.0f - ref[g];
+            float p[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) p[i] = exp2_hw(fmaf(sc[g][i], to_log2[g], off));
+            l[g] += (p[0] + p[1]) + (p[2] + p[3]);
+            uint32_t h01, l01, h23, l23;
+            split2(p[0], p[1], h01, l01);
+            split2(p[2], p[3], h23, l23);
+            const halfx4 ph = __builtin_bit_cast(halfx4, make_uint2(h01, h23));
+            const halfx4 pl = __builtin_bit_cast(halfx4, make_uint2(l01, l23));
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                acc[g][m] = __builtin_amdgcn_mfma_f32_16x16x16f16(vhi[m], ph, acc[g][m], 0, 0, 0);
+                acc[g][m] = __builtin_amdgcn_mfma_f32_16x16x16f16(vhi[m], pl, acc[g][m], 0, 0, 0);
+                acc[g][m] = __builtin_amdgcn_mfma_f32_16x16x16f16(vlo[m], ph, acc[g][m], 0, 0, 0);
+            }
+        }
+    }
+
+    // the four wavefronts' (maximum, sum, weighted sums) through LDS (the ring is free: the last block's wait was for
+    // every copy), merged as the split merge merges key ranges
+    __syncthreads();
+    float *mref = reinterpret_cast<float *>(&ring[0][0]);  // [wavefront][query]
+    float *msum = mref + 4 * NQ;                           // [wavefront][query]
+    float *macc = msum + 4 * NQ;                           // [wavefront][coordinate][query]
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        // the query's weight sum over the wavefront's keys (lanes l, l ^ 16, l ^ 32, l ^ 48 hold query 16 g + l % 16)
+        const float lw = sum32(sum16(l[g]));
+        if (lg == 0) {
+            mref[wave * NQ + 16 * g + qi] = ref[g];
+            msum[wave * NQ + 16 * g + qi] = lw;
+        }
+#pragma unroll
+        for (int m = 0; m < 4; m++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) macc[(wave * 64 + 16 * m + 4 * lg + i) * NQ + 16 * g + qi] = acc[g][m][i];
+    }
+    __syncthreads();
+    // thread t: queries t / 16 + 16 g, coordinates 4 (t % 16) .. + 3
+    const int oc = 4 * (tid & 15);
+    const float unscale = ldexpf(1.0f, -sv);
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const int oq = (tid >> 4) + 16 * g;
+        if (oq >= nq) break;
+        float m = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; w++)
+            if (msum[w * NQ + oq] > 0.0f) m = fmaxf(m, mref[w * NQ + oq]);
+        float L = 0.0f, o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const float ls = msum[w * NQ + oq];
+            const float f = ls > 0.0f ? exp2_hw(mref[w * NQ + oq] - m) : 0.0f;
+            L += ls * f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) o[j] += macc[(w * 64 + oc + j) * NQ + oq] * f;
+        }
+        if (splits == 1) {
+            const float fo = unscale / L;
+            *reinterpret_cast<float4 *>(out + (size_t)oq * d + h * 64 + oc) =
+                make_float4(o[0] * fo, o[1] * fo, o[2] * fo, o[3] * fo);
+        } else {
+            const size_t at = ((size_t)split * nq + oq) * heads + h;
+            *reinterpret_cast<float4 *>(part_o + at * 64 + oc) =
+                make_float4(o[0] * unscale, o[1] * unscale, o[2] * unscale, o[3] * unscale);
+            if (oc == 0) {
+                part_ml[at * 2] = m;
+                part_ml[at * 2 + 1] = L;
+            }
+        }
+    }
+}
+
 // ---- split merge: Soft::merge then Soft::finish ---------------------------------------------------------------
 // grid nq * heads; 64 threads. The largest running maximum first (lanes over splits), then one pass over the
 // splits accumulating each one's weight sum and weighted values rescaled to it; loads are independent across
@@ -1291,7 +1533,7 @@ void merge_splits(hipStream_t s, int nq, int d, int heads, int splits, const flo
 
 // ---- planning and launch --------------------------------------------------------------------------------------
 struct AttnPlan {
-    bool split16;
+    bool split16, few;  // few: k_attn_few (f32 tiles, at most FEW_Q queries)
     int splits, kb_per_split, groups, waves;
 };
 
@@ -1366,6 +1608,7 @@ static AttnPlan plan(const AttnShape &a, bool images) {
     p.waves = p.split16 && a.nq >= eight_from ? 8 : 4;
     const int per_group = p.split16 ? 32 * p.waves : QG;
     p.groups = (a.nq + per_group - 1) / per_group;
+    p.few = p.split16 && a.kv_format == TAH_KV_F32 && a.nq <= FEW_Q;
     // enough workgroups to fill the 256 compute units about once, each with at least 2 key blocks: more, shorter key
     // ranges measured slower at every batch (the merge and each workgroup's fixed costs grow with them; 64 queries:
     // 22 us at 256 workgroups against 36 at 632; f32 tiles at two workgroups a compute unit for two or more 128-query
@@ -1517,7 +1760,11 @@ void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t 
         part_o = static_cast<float *>(work);
         part_ml = part_o + (size_t)p.splits * a.nq * a.heads * hd;
     }
-    if (p.split16) {
+    if (p.few) {
+        hipLaunchKernelGGL(k_attn_few<FEW_Q / 16>, dim3(a.heads * p.splits), dim3(256), 0, s, a.nq, a.rows, a.chunk, a.d,
+                           a.heads, q, img->images, img->kvmax, p.kb_per_split, p.splits, part_o, part_ml, out);
+        TAH_LAUNCHED();
+    } else if (p.split16) {
         hipEvent_t *pe = probe_slot(s);
         if (pe) TAH_HIP(hipEventRecord(pe[0], s));
         switch (a.kv_format) {

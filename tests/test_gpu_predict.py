@@ -53,9 +53,11 @@ def random_layers(rng, layers, rows, chunk, d, kv_format, scale=1.0):
 
 @pytest.mark.parametrize("kv_format", [abi.KV_F32, abi.KV_I16, abi.KV_I8])
 @pytest.mark.parametrize("rows,chunk", [(10000, 256), (1000, 48), (37, 8), (50, 64)])
-@pytest.mark.parametrize("nq", [1, 3, 4, 7, 9, 16, 64, 130])
+@pytest.mark.parametrize("nq", [1, 3, 4, 7, 9, 16, 17, 33, 64, 130])
 def test_attention_full_width(gpu, full_model, full_weights, kv_format, rows, chunk, nq):
-    """AttendCached::attend at d = 512, 8 heads of 64: decode path below 64 queries, MFMA path above."""
+    """AttendCached::attend at d = 512, 8 heads of 64 over the layer's tiles: f32 up to 16 queries by the few-query
+    kernel (16 / 17 the boundary), beyond by the 32-query tiles (33: a second wavefront of queries); i16 below 4 queries
+    by the decode kernel; chunks of 8 and 48 rows leave some wavefronts' keys past a block's end."""
     say(f"attention d=512 fmt={kv_format} rows={rows} chunk={chunk} nq={nq}")
     rng = np.random.default_rng(rows * 7 + nq + kv_format)
     d, L = full_model.d, full_model.icl_layers
@@ -95,13 +97,15 @@ def test_attention_many_queries(gpu, full_model, full_weights, kv_format, nq):
 
 
 @pytest.mark.parametrize("kv_scale,q_scale", [(2000.0, 1e-4), (1e-3, 300.0), (1.0, 1.0)])
-def test_attention_magnitudes(gpu, full_model, full_weights, kv_scale, q_scale):
+@pytest.mark.parametrize("nq", [96, 5])
+def test_attention_magnitudes(gpu, full_model, full_weights, kv_scale, q_scale, nq):
     """Keys, values and queries far from unit size, and heads of different sizes (each head's coordinates scaled by
-    4^h): the split-fp16 path's power-of-two scaling keeps f32 accuracy, relative to the outputs' size."""
-    say(f"attention magnitudes kv={kv_scale} q={q_scale}")
+    4^h): the split-fp16 path's power-of-two scaling keeps f32 accuracy, relative to the outputs' size (96 queries:
+    the 32-query kernel; 5: the few-query kernel)."""
+    say(f"attention magnitudes kv={kv_scale} q={q_scale} nq={nq}")
     rng = np.random.default_rng(int(kv_scale * 10) + 3)
     d, L, heads = full_model.d, full_model.icl_layers, full_model.icl_heads
-    rows, chunk, nq = 3000, 256, 96
+    rows, chunk = 3000, 256
     per_dim = np.repeat(4.0 ** (np.arange(heads) - heads // 2), d // heads).astype(np.float32)
     parts = []
     for c0 in range(0, rows, chunk):
