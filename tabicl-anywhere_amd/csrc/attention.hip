@@ -10,14 +10,15 @@
 //
 // The kernels:
 //  * k_attn_split64: head width 64 over tile images (below; any cache format: f32 from 17 queries, i8 from one,
-//    i16 from 4), 32 queries a wavefront. Every f32
+//    i16 from 17), 32 queries a wavefront. Every f32
 //    product runs on the fp16 matrix cores as three products of fp16 halves (device_math.hpp): the error is that
 //    of an f32 dot product, at v_mfma_f32_32x32x16_f16's rate (2 PFLOP/s sustained, 16x that of the f32 matrix
 //    instructions). Operands are scaled by powers of two first (exact): each query to a maximum near 2^14, each
 //    head's keys and values by the layer's maximum, and the softmax weights to at most 2^15, so that no half
 //    overflows and the low halves stay normal for all but negligible elements.
-//  * k_attn_few: head width 64, 1 to 16 queries over f32 images: the four wavefronts of a workgroup split each key
-//    block, with the queries as the 16 columns of 16 x 16 products, and merge their softmax states at the end.
+//  * k_attn_few: head width 64, 1 to 16 queries over f32 images (2 to 16 over i16 code tiles, widened in registers):
+//    the four wavefronts of a workgroup split each key block, with the queries as the 16 columns of 16 x 16
+//    products, and merge their softmax states at the end.
 //  * k_attn_decode_w: head width 64 and few queries (or no images), from the records: 256 threads per (six key
 //    blocks, head, 8 queries), each wavefront streaming a key block at a time with no barrier (lane = key for the
 //    scores, lane = coordinate for the weighted sum), integer codes scaled through the query and the sums.
@@ -1174,7 +1175,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows
     }
 }
 
-// ---- few-query kernel: head width 64, 1 to FEW_Q queries, over f32 split images --------------------------------
+// ---- few-query kernel: head width 64, 1 to FEW_Q queries, over f32 split images or i16 code tiles ----------------
 // grid heads x splits (workgroup i: head i % heads, key range i / heads); 256 threads. With few queries the 32-query
 // products of k_attn_split64 leave most of their columns (and whole wavefronts) idle while the kernel waits on
 // memory; here the four wavefronts share each 64-key block and split it, wavefront w taking keys 16 w .. 16 w + 15,
@@ -1190,6 +1191,9 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows
 // than k_attn_split64 (17 / 33 / 64 rows 0.836 / 0.852 / 0.884 -> 0.852 / 0.922 / 0.977 ms a prediction), whose
 // 32-query products then have work for their columns.
 constexpr int FEW_Q = 16;
+// i16 code tiles from this many queries: one query measured faster by the decode kernel, two slower (2 / 3 / 4 / 8 /
+// 16 rows 0.625 / 0.692 / 0.763 / 0.798 / 0.877 -> 0.606 / 0.644 / 0.707 / 0.741 / 0.825 ms with this kernel)
+constexpr int FEW16_FROM = 2;
 
 typedef _Float16 halfx4 __attribute__((ext_vector_type(4)));
 
@@ -1215,23 +1219,42 @@ __device__ __forceinline__ float sum32(float x) {
     return __uint_as_float(s[0]) + __uint_as_float(s[1]);
 }
 
-template <int G>
+template <int G, int FMT>
 __global__ __launch_bounds__(256, 1) void k_attn_few(int nq, int rows, int chunk, int d, int heads,
                                                       const float *__restrict__ q, const uint8_t *__restrict__ images,
                                                       const uint32_t *__restrict__ kvmax, int kb_per_split, int splits,
                                                       float *__restrict__ part_o, float *__restrict__ part_ml,
                                                       float *__restrict__ out) {
-    constexpr int SLOTS = 4, PER_BLOCK = IMG / (16 * 256);  // a block: 8 copies of 16 bytes a thread
+    // CODES16: the layer's i16 code tiles (16.5 KB, a 20 KB slot), widened, scaled and split as each wavefront reads
+    // its operands; six slots, all of a typical range's blocks in flight at once
+    constexpr bool CODES16 = FMT == TAH_KV_I16;
+    static_assert(FMT == TAH_KV_F32 || CODES16, "f32 images or i16 code tiles");
+    constexpr int TB = img_bytes(FMT), SLOTS = CODES16 ? 6 : 4;
+    constexpr int PER_BLOCK = (TB + 4095) / 4096, SLOT = 4096 * PER_BLOCK;  // whole rounds of 256 x 16 bytes
     constexpr int NQ = 16 * G;
-    static_assert(4 * 64 * NQ * 4 + 2 * 4 * NQ * 4 <= IMG * SLOTS, "the merge fits in the ring");
-    __shared__ __align__(16) uint8_t ring[SLOTS][IMG];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    static_assert(4 * 64 * NQ * 4 + 2 * 4 * NQ * 4 <= SLOT * SLOTS, "the merge fits in the ring");
+    static_assert((SLOTS - 2) * PER_BLOCK < 64, "the waits' counts fit the counter");
+    __shared__ __align__(16) uint8_t ring[SLOTS][SLOT];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int qi = lane & 15, lg = lane >> 4;
     const int h = blockIdx.x % heads, split = blockIdx.x / heads;
     const KeyBlocks kbs = key_blocks(rows, chunk);
     const int kb0 = split * kb_per_split, kb1 = min(kbs.n_kb, kb0 + kb_per_split);
-    const uint8_t *head_images = images + (size_t)h * IMG;
-    const size_t kb_stride = (size_t)heads * IMG;
+    const uint8_t *head_images = images + (size_t)h * TB;
+    const size_t kb_stride = (size_t)heads * TB;
+    // tile kb into a ring slot: PER_BLOCK copies of 16 bytes a thread, none of them conditional, so that every
+    // wavefront's count of copies a block is the same for the waits below; the lanes past the tile copy its last 16
+    // bytes again into the slot's padding (an i16 code tile is 16.5 KB in a 20 KB slot). Over code tiles the compiler
+    // also waits for every copy in flight before the loop's first LDS read (its own wait, not one of the waits below):
+    // all of a range's blocks (five, typically) are then in flight from the start
+    auto tile_to_lds = [&](int kb, uint8_t *slot) {
+        const uint4 *src = reinterpret_cast<const uint4 *>(head_images + kb * kb_stride);
+#pragma unroll
+        for (int i = 0; i < PER_BLOCK; i++) {
+            const int base = 256 * i + 64 * wave;
+            __builtin_amdgcn_global_load_lds(src + min(base + lane, TB / 16 - 1), slot + 16 * base, 16, 0, 0);
+        }
+    };
 
     // query 16 g + qi's coordinates 32 ks + 8 lg + t (the B operand of the scores), loaded without a branch (a lane
     // past the last query reads query 0 and zeroes it), then the first blocks' copies issued
@@ -1244,7 +1267,7 @@ __global__ __launch_bounds__(256, 1) void k_attn_few(int nq, int rows, int chunk
     }
 #pragma unroll
     for (int i = 0; i < SLOTS - 1; i++)
-        if (kb0 + i < kb1) half_image_to_lds<4, IMG>(head_images + (kb0 + i) * kb_stride, ring[i], tid);
+        if (kb0 + i < kb1) tile_to_lds(kb0 + i, ring[i]);
     // each query scaled to a maximum near 2^14 and split
     halfx8 qh[G][2], ql[G][2];
     float to_log2[G];
@@ -1283,32 +1306,61 @@ __global__ __launch_bounds__(256, 1) void k_attn_few(int nq, int rows, int chunk
     const int vchunk = 2 * wave + (lg >> 1), voff = 8 * (lg & 1);  // the values' A operand: keys 16 wave + 4 lg + ..
     for (int kb = kb0; kb < kb1; kb++) {
         // block kb's copies have landed (the ones after it may still be in flight), everyone's, and everyone is done
-        // with block kb - 1, whose slot the copy of block kb + 3 then takes
+        // with block kb - 1, whose slot the copy of block kb + SLOTS - 1 then takes
         const int ahead = min(kb1 - 1, kb + SLOTS - 2) - kb;
-        if (ahead >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_at_most(2 * PER_BLOCK));
-        else if (ahead == 1) __builtin_amdgcn_s_waitcnt(vmcnt_at_most(PER_BLOCK));
-        else __builtin_amdgcn_s_waitcnt(vmcnt_at_most(0));
+        switch (ahead) {
+            case 0: __builtin_amdgcn_s_waitcnt(vmcnt_at_most(0)); break;
+            case 1: __builtin_amdgcn_s_waitcnt(vmcnt_at_most(PER_BLOCK)); break;
+            case 2: __builtin_amdgcn_s_waitcnt(vmcnt_at_most(2 * PER_BLOCK)); break;
+            case 3: __builtin_amdgcn_s_waitcnt(vmcnt_at_most(3 * PER_BLOCK)); break;
+            default: __builtin_amdgcn_s_waitcnt(vmcnt_at_most((SLOTS - 2) * PER_BLOCK)); break;
+        }
         __syncthreads();
         if (kb + SLOTS - 1 < kb1)
-            half_image_to_lds<4, IMG>(head_images + (kb + SLOTS - 1) * kb_stride, ring[(kb + SLOTS - 1 - kb0) % SLOTS], tid);
+            tile_to_lds(kb + SLOTS - 1, ring[(kb + SLOTS - 1 - kb0) % SLOTS]);
         const int ci = kb / kbs.bpc;
         const int nk = min(KB, (ci == kbs.n_chunks - 1 ? kbs.last_rc : chunk) - (kb % kbs.bpc) * KB);
         if (16 * wave >= nk) continue;  // this wavefront's keys are all past the block's end
         const uint8_t *img = ring[(kb - kb0) % SLOTS];
         halfx8 khi[2], klo[2];
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-            const int off = krow * 128 + swz(krow, 4 * ks + lg) * 16;
-            khi[ks] = *reinterpret_cast<const halfx8 *>(img + off);
-            klo[ks] = *reinterpret_cast<const halfx8 *>(img + 8192 + off);
-        }
         halfx4 vhi[4], vlo[4];
+        if constexpr (CODES16) {
+            // key krow's codes at coordinates 32 ks + 8 lg + 0..7 times their factors; coordinate 16 m + lane % 16's
+            // codes of keys 16 wave + 4 lg + 0..3 times its factor (the tile's rows are not swizzled)
+            const float *kf = reinterpret_cast<const float *>(img + 8192);
 #pragma unroll
-        for (int m = 0; m < 4; m++) {
-            const int r = 16 * m + (lane & 15);
-            const int vo = r * 128 + swz(r, vchunk) * 16 + voff;
-            vhi[m] = *reinterpret_cast<const halfx4 *>(img + 16384 + vo);
-            vlo[m] = *reinterpret_cast<const halfx4 *>(img + 24576 + vo);
+            for (int ks = 0; ks < 2; ks++) {
+                float f[8];
+                load8(kf + 32 * ks + 8 * lg, f);
+                dequant_split8(*reinterpret_cast<const uint4 *>(img + krow * 128 + (4 * ks + lg) * 16), f, khi[ks], klo[ks]);
+            }
+            const uint8_t *vt = img + HALF16;
+            const float *vf = reinterpret_cast<const float *>(vt + 8192);
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                const int r = 16 * m + (lane & 15);
+                const uint2 c = *reinterpret_cast<const uint2 *>(vt + r * 128 + 32 * wave + 8 * lg);
+                const float fv = vf[r];
+                uint32_t h01, l01, h23, l23;
+                split2((float)(int16_t)(c.x & 0xffffu) * fv, (float)(int16_t)(c.x >> 16) * fv, h01, l01);
+                split2((float)(int16_t)(c.y & 0xffffu) * fv, (float)(int16_t)(c.y >> 16) * fv, h23, l23);
+                vhi[m] = __builtin_bit_cast(halfx4, make_uint2(h01, h23));
+                vlo[m] = __builtin_bit_cast(halfx4, make_uint2(l01, l23));
+            }
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                const int off = krow * 128 + swz(krow, 4 * ks + lg) * 16;
+                khi[ks] = *reinterpret_cast<const halfx8 *>(img + off);
+                klo[ks] = *reinterpret_cast<const halfx8 *>(img + 8192 + off);
+            }
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                const int r = 16 * m + (lane & 15);
+                const int vo = r * 128 + swz(r, vchunk) * 16 + voff;
+                vhi[m] = *reinterpret_cast<const halfx4 *>(img + 16384 + vo);
+                vlo[m] = *reinterpret_cast<const halfx4 *>(img + 24576 + vo);
+            }
         }
         floatx4 sc[G];
 #pragma unroll
@@ -1533,7 +1585,7 @@ void merge_splits(hipStream_t s, int nq, int d, int heads, int splits, const flo
 
 // ---- planning and launch --------------------------------------------------------------------------------------
 struct AttnPlan {
-    bool split16, few;  // few: k_attn_few (f32 tiles, at most FEW_Q queries)
+    bool split16, few;  // few: k_attn_few (f32 images or i16 code tiles, at most FEW_Q queries)
     int splits, kb_per_split, groups, waves;
 };
 
@@ -1597,7 +1649,9 @@ static AttnPlan plan(const AttnShape &a, bool images) {
     AttnPlan p;
     const KeyBlocks k = key_blocks(a.rows, a.chunk);
     const int hd = a.d / a.heads;
-    p.split16 = hd == 64 && a.nq >= split16_min_q(a.kv_format) && images && kv_images_apply(a.kv_format, a.d, a.heads);
+    const bool tiles = hd == 64 && images && kv_images_apply(a.kv_format, a.d, a.heads);
+    p.few = tiles && a.nq <= FEW_Q && (a.kv_format == TAH_KV_F32 || (a.kv_format == TAH_KV_I16 && a.nq >= FEW16_FROM));
+    p.split16 = tiles && (p.few || a.nq >= split16_min_q(a.kv_format));
     // k_attn_split64: 256 queries a workgroup (one a compute unit, one wave of them) from 768 queries on, else 128
     // (at 512 / 640 rows f32 1.376 / 1.740 -> 1.368 / 1.717 ms and i8 1.337 / 1.705 -> 1.330 / 1.676 ms with the
     // smaller tiles than from 512; from 1,024 or 1,536 queries f32 was slower at 768 to 1,280); an i16 layer's (whose
@@ -1608,7 +1662,6 @@ static AttnPlan plan(const AttnShape &a, bool images) {
     p.waves = p.split16 && a.nq >= eight_from ? 8 : 4;
     const int per_group = p.split16 ? 32 * p.waves : QG;
     p.groups = (a.nq + per_group - 1) / per_group;
-    p.few = p.split16 && a.kv_format == TAH_KV_F32 && a.nq <= FEW_Q;
     // enough workgroups to fill the 256 compute units about once, each with at least 2 key blocks: more, shorter key
     // ranges measured slower at every batch (the merge and each workgroup's fixed costs grow with them; 64 queries:
     // 22 us at 256 workgroups against 36 at 632; f32 tiles at two workgroups a compute unit for two or more 128-query
@@ -1761,8 +1814,14 @@ void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t 
         part_ml = part_o + (size_t)p.splits * a.nq * a.heads * hd;
     }
     if (p.few) {
-        hipLaunchKernelGGL(k_attn_few<FEW_Q / 16>, dim3(a.heads * p.splits), dim3(256), 0, s, a.nq, a.rows, a.chunk, a.d,
-                           a.heads, q, img->images, img->kvmax, p.kb_per_split, p.splits, part_o, part_ml, out);
+        if (a.kv_format == TAH_KV_I16)
+            hipLaunchKernelGGL((k_attn_few<FEW_Q / 16, TAH_KV_I16>), dim3(a.heads * p.splits), dim3(256), 0, s, a.nq, a.rows,
+                               a.chunk, a.d, a.heads, q, img->images, img->kvmax, p.kb_per_split, p.splits, part_o,
+                               part_ml, out);
+        else
+            hipLaunchKernelGGL((k_attn_few<FEW_Q / 16, TAH_KV_F32>), dim3(a.heads * p.splits), dim3(256), 0, s, a.nq, a.rows,
+                               a.chunk, a.d, a.heads, q, img->images, img->kvmax, p.kb_per_split, p.splits, part_o,
+                               part_ml, out);
         TAH_LAUNCHED();
     } else if (p.split16) {
         hipEvent_t *pe = probe_slot(s);

@@ -53,11 +53,11 @@ def random_layers(rng, layers, rows, chunk, d, kv_format, scale=1.0):
 
 @pytest.mark.parametrize("kv_format", [abi.KV_F32, abi.KV_I16, abi.KV_I8])
 @pytest.mark.parametrize("rows,chunk", [(10000, 256), (1000, 48), (37, 8), (50, 64)])
-@pytest.mark.parametrize("nq", [1, 3, 4, 7, 9, 16, 17, 33, 64, 130])
+@pytest.mark.parametrize("nq", [1, 2, 3, 4, 7, 9, 16, 17, 33, 64, 130])
 def test_attention_full_width(gpu, full_model, full_weights, kv_format, rows, chunk, nq):
     """AttendCached::attend at d = 512, 8 heads of 64 over the layer's tiles: f32 up to 16 queries by the few-query
-    kernel (16 / 17 the boundary), beyond by the 32-query tiles (33: a second wavefront of queries); i16 below 4 queries
-    by the decode kernel; chunks of 8 and 48 rows leave some wavefronts' keys past a block's end."""
+    kernel (16 / 17 the boundary), beyond by the 32-query tiles (33: a second wavefront of queries); i16 the same from
+    2 queries, one by the decode kernel; chunks of 8 and 48 rows leave some wavefronts' keys past a block's end."""
     say(f"attention d=512 fmt={kv_format} rows={rows} chunk={chunk} nq={nq}")
     rng = np.random.default_rng(rows * 7 + nq + kv_format)
     d, L = full_model.d, full_model.icl_layers
