@@ -1186,13 +1186,13 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows
 // The keys' and values' operands are read once a block for all G groups. Each wavefront runs its own online softmax
 // over its keys (as k_attn_split64: log2 units, the reference maximum raised when a block passes it by more than 3);
 // at the end the four are merged through LDS into the same partials, or output, as k_attn_split64 leaves. The
-// blocks stream through a ring of four 32 KB LDS slots by DMA, three blocks in flight while one is used, one barrier
-// a block. Launched for one group (up to 16 queries): with two or four groups (17 to 64 queries) it measured slower
+// blocks stream through a ring of LDS slots by DMA (f32: four 32 KB slots, three blocks in flight while one is used;
+// i16: six 20 KB slots), one barrier a block. Launched for one group (up to 16 queries): with two or four groups (17 to 64 queries) it measured slower
 // than k_attn_split64 (17 / 33 / 64 rows 0.836 / 0.852 / 0.884 -> 0.852 / 0.922 / 0.977 ms a prediction), whose
 // 32-query products then have work for their columns.
 constexpr int FEW_Q = 16;
-// i16 code tiles from this many queries: one query measured faster by the decode kernel, two slower (2 / 3 / 4 / 8 /
-// 16 rows 0.625 / 0.692 / 0.763 / 0.798 / 0.877 -> 0.606 / 0.644 / 0.707 / 0.741 / 0.825 ms with this kernel)
+// i16 code tiles from this many queries: the decode kernel measured faster at one query and slower from two (2 / 3 /
+// 4 / 8 / 16 rows 0.625 / 0.692 / 0.763 / 0.798 / 0.877 -> 0.606 / 0.644 / 0.707 / 0.741 / 0.825 ms with this kernel)
 constexpr int FEW16_FROM = 2;
 
 typedef _Float16 halfx4 __attribute__((ext_vector_type(4)));
