@@ -9,14 +9,14 @@
 // (Soft::merge, src/nn.rs:261-276) and divided through (Soft::finish).
 //
 // The kernels:
-//  * k_attn_split64: head width 64 over tile images (below; any cache format: f32 from 17 queries, i8 from one,
-//    i16 from 17), 32 queries a wavefront. Every f32
+//  * k_attn_split64: head width 64 over tile images (below; any cache format) from 17 queries, 32 queries a
+//    wavefront. Every f32
 //    product runs on the fp16 matrix cores as three products of fp16 halves (device_math.hpp): the error is that
 //    of an f32 dot product, at v_mfma_f32_32x32x16_f16's rate (2 PFLOP/s sustained, 16x that of the f32 matrix
 //    instructions). Operands are scaled by powers of two first (exact): each query to a maximum near 2^14, each
 //    head's keys and values by the layer's maximum, and the softmax weights to at most 2^15, so that no half
 //    overflows and the low halves stay normal for all but negligible elements.
-//  * k_attn_few: head width 64, 1 to 16 queries over f32 images (2 to 16 over i16 code tiles, widened in registers):
+//  * k_attn_few: head width 64, 1 to 16 queries over f32 images and i8 code images (2 to 16 over i16 code tiles):
 //    the four wavefronts of a workgroup split each key block, with the queries as the 16 columns of 16 x 16
 //    products, and merge their softmax states at the end.
 //  * k_attn_decode_w: head width 64 and few queries (or no images), from the records: 256 threads per (six key
@@ -1175,7 +1175,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows
     }
 }
 
-// ---- few-query kernel: head width 64, 1 to FEW_Q queries, over f32 split images or i16 code tiles ----------------
+// ---- few-query kernel: head width 64, 1 to FEW_Q queries, over f32 split images or i16 / i8 codes --------------
 // grid heads x splits (workgroup i: head i % heads, key range i / heads); 256 threads. With few queries the 32-query
 // products of k_attn_split64 leave most of their columns (and whole wavefronts) idle while the kernel waits on
 // memory; here the four wavefronts share each 64-key block and split it, wavefront w taking keys 16 w .. 16 w + 15,
@@ -1187,7 +1187,7 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows
 // over its keys (as k_attn_split64: log2 units, the reference maximum raised when a block passes it by more than 3);
 // at the end the four are merged through LDS into the same partials, or output, as k_attn_split64 leaves. The
 // blocks stream through a ring of LDS slots by DMA (f32: four 32 KB slots, three blocks in flight while one is used;
-// i16: six 20 KB slots), one barrier a block. Launched for one group (up to 16 queries): with two or four groups (17 to 64 queries) it measured slower
+// i16 and i8: six 20 KB slots), one barrier a block. Launched for one group (up to 16 queries): with two or four groups (17 to 64 queries) it measured slower
 // than k_attn_split64 (17 / 33 / 64 rows 0.836 / 0.852 / 0.884 -> 0.852 / 0.922 / 0.977 ms a prediction), whose
 // 32-query products then have work for their columns.
 constexpr int FEW_Q = 16;
@@ -1222,15 +1222,20 @@ __device__ __forceinline__ float sum32(float x) {
 template <int G, int FMT>
 __global__ __launch_bounds__(256, 1) void k_attn_few(int nq, int rows, int chunk, int d, int heads,
                                                       const float *__restrict__ q, const uint8_t *__restrict__ images,
-                                                      const uint32_t *__restrict__ kvmax, int kb_per_split, int splits,
-                                                      float *__restrict__ part_o, float *__restrict__ part_ml,
-                                                      float *__restrict__ out) {
+                                                      const uint32_t *__restrict__ kvmax, const float *__restrict__ scl,
+                                                      int kb_per_split, int splits, float *__restrict__ part_o,
+                                                      float *__restrict__ part_ml, float *__restrict__ out) {
     // CODES16: the layer's i16 code tiles (16.5 KB, a 20 KB slot), widened, scaled and split as each wavefront reads
-    // its operands; six slots, all of a typical range's blocks in flight at once
-    constexpr bool CODES16 = FMT == TAH_KV_I16;
-    static_assert(FMT == TAH_KV_F32 || CODES16, "f32 images or i16 code tiles");
-    constexpr int TB = img_bytes(FMT), SLOTS = CODES16 ? 6 : 4;
-    constexpr int PER_BLOCK = (TB + 4095) / 4096, SLOT = 4096 * PER_BLOCK;  // whole rounds of 256 x 16 bytes
+    // its operands. CODES8: the layer's i8 code images (16 KB, exact in fp16), each block copied with its chunk's
+    // scales after it (key scales, value scales, ratios: 768 bytes, in a 20 KB slot); the scores are two products of
+    // the query times the chunk's key scales (split again when a block begins a chunk) with the key codes, the weighted
+    // sums two products of the split weights with the value codes, kept in units of the current chunk's value scales
+    // (times the ratios when a block begins a chunk, times the last chunk's value scales at the end). Both: six slots,
+    // all of a typical range's blocks in flight at once.
+    constexpr bool CODES16 = FMT == TAH_KV_I16, CODES8 = FMT == TAH_KV_I8;
+    constexpr int TB = img_bytes(FMT), SLOTS = CODES16 || CODES8 ? 6 : 4;
+    constexpr int EXTRA = CODES8 ? SCL / 16 : 1;  // copies past the tile: the chunk's scales, or its last 16 bytes again
+    constexpr int PER_BLOCK = (TB + (CODES8 ? SCL : 0) + 4095) / 4096, SLOT = 4096 * PER_BLOCK;  // whole rounds
     constexpr int NQ = 16 * G;
     static_assert(4 * 64 * NQ * 4 + 2 * 4 * NQ * 4 <= SLOT * SLOTS, "the merge fits in the ring");
     static_assert((SLOTS - 2) * PER_BLOCK < 64, "the waits' counts fit the counter");
@@ -1243,16 +1248,20 @@ __global__ __launch_bounds__(256, 1) void k_attn_few(int nq, int rows, int chunk
     const uint8_t *head_images = images + (size_t)h * TB;
     const size_t kb_stride = (size_t)heads * TB;
     // tile kb into a ring slot: PER_BLOCK copies of 16 bytes a thread, none of them conditional, so that every
-    // wavefront's count of copies a block is the same for the waits below; the lanes past the tile copy its last 16
-    // bytes again into the slot's padding (an i16 code tile is 16.5 KB in a 20 KB slot). Over code tiles the compiler
-    // also waits for every copy in flight before the loop's first LDS read (its own wait, not one of the waits below):
-    // all of a range's blocks (five, typically) are then in flight from the start
+    // wavefront's count of copies a block is the same for the waits below; the lanes past the tile copy the block's
+    // chunk's scales (CODES8) or the tile's last 16 bytes again, the ones past those the last 16 bytes of them again,
+    // into the slot's padding. Over code tiles the compiler also waits for every copy in flight before the loop's
+    // first LDS read (its own wait, not one of the waits below): all of a range's blocks (five, typically) are then
+    // in flight from the start
     auto tile_to_lds = [&](int kb, uint8_t *slot) {
         const uint4 *src = reinterpret_cast<const uint4 *>(head_images + kb * kb_stride);
+        const uint4 *extra = src + TB / 16 - 1;
+        if constexpr (CODES8) extra = reinterpret_cast<const uint4 *>(scl + ((size_t)(kb / kbs.bpc) * heads + h) * 192);
 #pragma unroll
         for (int i = 0; i < PER_BLOCK; i++) {
-            const int base = 256 * i + 64 * wave;
-            __builtin_amdgcn_global_load_lds(src + min(base + lane, TB / 16 - 1), slot + 16 * base, 16, 0, 0);
+            const int base = 256 * i + 64 * wave, at = base + lane;
+            const uint4 *p = at < TB / 16 ? src + at : extra + min(at - TB / 16, EXTRA - 1);
+            __builtin_amdgcn_global_load_lds(p, slot + 16 * base, 16, 0, 0);
         }
     };
 
@@ -1268,33 +1277,50 @@ __global__ __launch_bounds__(256, 1) void k_attn_few(int nq, int rows, int chunk
 #pragma unroll
     for (int i = 0; i < SLOTS - 1; i++)
         if (kb0 + i < kb1) tile_to_lds(kb0 + i, ring[i]);
-    // each query scaled to a maximum near 2^14 and split
-    halfx8 qh[G][2], ql[G][2];
-    float to_log2[G];
-    const int sk = shift_for(kvmax[h * 2]), sv = shift_for(kvmax[h * 2 + 1]);
+    // each query (CODES8: times the chunk's key scales ksc, at coordinates 32 ks + 8 lg + t) scaled to a maximum near
+    // 2^14 and split
+    float qraw[G][2][8];
 #pragma unroll
     for (int g = 0; g < G; g++) {
         const float live = 16 * g + qi < nq ? 1.0f : 0.0f;
-        float qv[2][8];
 #pragma unroll
         for (int ks = 0; ks < 2; ks++) {
             const float4 a = raw[g][2 * ks], b = raw[g][2 * ks + 1];
-            qv[ks][0] = a.x * live; qv[ks][1] = a.y * live; qv[ks][2] = a.z * live; qv[ks][3] = a.w * live;
-            qv[ks][4] = b.x * live; qv[ks][5] = b.y * live; qv[ks][6] = b.z * live; qv[ks][7] = b.w * live;
+            qraw[g][ks][0] = a.x * live; qraw[g][ks][1] = a.y * live; qraw[g][ks][2] = a.z * live;
+            qraw[g][ks][3] = a.w * live; qraw[g][ks][4] = b.x * live; qraw[g][ks][5] = b.y * live;
+            qraw[g][ks][6] = b.z * live; qraw[g][ks][7] = b.w * live;
         }
-        float qmax = 0.0f;
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++)
-#pragma unroll
-            for (int t = 0; t < 8; t++) qmax = fmaxf(qmax, fabsf(qv[ks][t]));
-        const int eq = shift_for_max(max32(max16(qmax)));
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++) split8(qv[ks], ldexpf(1.0f, eq), qh[g][ks], ql[g][ks]);
-        to_log2[g] = ldexpf(LOG2E, -(sk + eq));
     }
+    halfx8 qh[G][2], ql[G][2];
+    float to_log2[G];
+    const int sk = CODES8 ? 0 : shift_for(kvmax[h * 2]), sv = CODES8 ? 0 : shift_for(kvmax[h * 2 + 1]);
+    auto split_queries = [&](const float *ksc) {
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float qv[2][8];
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                float f[8];
+                if constexpr (CODES8) load8(ksc + 32 * ks + 8 * lg, f);
+#pragma unroll
+                for (int t = 0; t < 8; t++) qv[ks][t] = CODES8 ? qraw[g][ks][t] * f[t] : qraw[g][ks][t];
+            }
+            float qmax = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+                for (int t = 0; t < 8; t++) qmax = fmaxf(qmax, fabsf(qv[ks][t]));
+            const int eq = shift_for_max(max32(max16(qmax)));
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) split8(qv[ks], ldexpf(1.0f, eq), qh[g][ks], ql[g][ks]);
+            to_log2[g] = ldexpf(LOG2E, -(sk + eq));
+        }
+    };
+    if constexpr (!CODES8) split_queries(nullptr);
 
     float ref[G], l[G];
-    floatx4 acc[G][4];  // O^T: coordinate 16 m + 4 lg + i of query 16 g + qi, in units of 2^sv
+    floatx4 acc[G][4];  // O^T: coordinate 16 m + 4 lg + i of query 16 g + qi, in units of 2^sv (CODES8: of the chunk's
+                        // value scales)
 #pragma unroll
     for (int g = 0; g < G; g++) {
         ref[g] = -INFINITY;
@@ -1320,11 +1346,37 @@ __global__ __launch_bounds__(256, 1) void k_attn_few(int nq, int rows, int chunk
             tile_to_lds(kb + SLOTS - 1, ring[(kb + SLOTS - 1 - kb0) % SLOTS]);
         const int ci = kb / kbs.bpc;
         const int nk = min(KB, (ci == kbs.n_chunks - 1 ? kbs.last_rc : chunk) - (kb % kbs.bpc) * KB);
-        if (16 * wave >= nk) continue;  // this wavefront's keys are all past the block's end
         const uint8_t *img = ring[(kb - kb0) % SLOTS];
+        if constexpr (CODES8) {
+            // a block that begins the range or a chunk: the sums into this chunk's value units (after the first), the
+            // queries split with its key scales (every wavefront, whether or not its keys are past the block's end)
+            const float *sct = reinterpret_cast<const float *>(img + TB);
+            if (kb == kb0 || kb % kbs.bpc == 0) {
+                if (kb > kb0) {
+#pragma unroll
+                    for (int m = 0; m < 4; m++) {
+                        const float4 r4 = *reinterpret_cast<const float4 *>(sct + 128 + 16 * m + 4 * lg);
+#pragma unroll
+                        for (int g = 0; g < G; g++) acc[g][m] *= floatx4{r4.x, r4.y, r4.z, r4.w};
+                    }
+                }
+                split_queries(sct);
+            }
+        }
+        if (16 * wave >= nk) continue;  // this wavefront's keys are all past the block's end
         halfx8 khi[2], klo[2];
         halfx4 vhi[4], vlo[4];
-        if constexpr (CODES16) {
+        if constexpr (CODES8) {
+            // the codes as they are (exact in fp16): one plane each, laid out as the f32 images' high planes
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++)
+                khi[ks] = *reinterpret_cast<const halfx8 *>(img + krow * 128 + swz(krow, 4 * ks + lg) * 16);
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                const int r = 16 * m + (lane & 15);
+                vhi[m] = *reinterpret_cast<const halfx4 *>(img + 8192 + r * 128 + swz(r, vchunk) * 16 + voff);
+            }
+        } else if constexpr (CODES16) {
             // key krow's codes at coordinates 32 ks + 8 lg + 0..7 times their factors; coordinate 16 m + lane % 16's
             // codes of keys 16 wave + 4 lg + 0..3 times its factor (the tile's rows are not swizzled)
             const float *kf = reinterpret_cast<const float *>(img + 8192);
@@ -1370,7 +1422,7 @@ __global__ __launch_bounds__(256, 1) void k_attn_few(int nq, int rows, int chunk
             for (int ks = 0; ks < 2; ks++) {
                 sc[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(khi[ks], qh[g][ks], sc[g], 0, 0, 0);
                 sc[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(khi[ks], ql[g][ks], sc[g], 0, 0, 0);
-                sc[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(klo[ks], qh[g][ks], sc[g], 0, 0, 0);
+                if constexpr (!CODES8) sc[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(klo[ks], qh[g][ks], sc[g], 0, 0, 0);
             }
         }
 #pragma unroll
@@ -1404,11 +1456,21 @@ __global__ __launch_bounds__(256, 1) void k_attn_few(int nq, int rows, int chunk
             for (int m = 0; m < 4; m++) {
                 acc[g][m] = __builtin_amdgcn_mfma_f32_16x16x16f16(vhi[m], ph, acc[g][m], 0, 0, 0);
                 acc[g][m] = __builtin_amdgcn_mfma_f32_16x16x16f16(vhi[m], pl, acc[g][m], 0, 0, 0);
-                acc[g][m] = __builtin_amdgcn_mfma_f32_16x16x16f16(vlo[m], ph, acc[g][m], 0, 0, 0);
+                if constexpr (!CODES8) acc[g][m] = __builtin_amdgcn_mfma_f32_16x16x16f16(vlo[m], ph, acc[g][m], 0, 0, 0);
             }
         }
     }
 
+    if constexpr (CODES8) {
+        // the sums into true units: the last block's chunk's value scales (its slot is intact until the barrier below)
+        const float *sct = reinterpret_cast<const float *>(ring[(kb1 - 1 - kb0) % SLOTS] + TB);
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const float4 v4 = *reinterpret_cast<const float4 *>(sct + 64 + 16 * m + 4 * lg);
+#pragma unroll
+            for (int g = 0; g < G; g++) acc[g][m] *= floatx4{v4.x, v4.y, v4.z, v4.w};
+        }
+    }
     // the four wavefronts' (maximum, sum, weighted sums) through LDS (the ring is free: the last block's wait was for
     // every copy), merged as the split merge merges key ranges
     __syncthreads();
@@ -1585,7 +1647,7 @@ void merge_splits(hipStream_t s, int nq, int d, int heads, int splits, const flo
 
 // ---- planning and launch --------------------------------------------------------------------------------------
 struct AttnPlan {
-    bool split16, few;  // few: k_attn_few (f32 images or i16 code tiles, at most FEW_Q queries)
+    bool split16, few;  // few: k_attn_few (any tiles, at most FEW_Q queries; i16 from FEW16_FROM)
     int splits, kb_per_split, groups, waves;
 };
 
@@ -1650,7 +1712,7 @@ static AttnPlan plan(const AttnShape &a, bool images) {
     const KeyBlocks k = key_blocks(a.rows, a.chunk);
     const int hd = a.d / a.heads;
     const bool tiles = hd == 64 && images && kv_images_apply(a.kv_format, a.d, a.heads);
-    p.few = tiles && a.nq <= FEW_Q && (a.kv_format == TAH_KV_F32 || (a.kv_format == TAH_KV_I16 && a.nq >= FEW16_FROM));
+    p.few = tiles && a.nq <= FEW_Q && (a.kv_format != TAH_KV_I16 || a.nq >= FEW16_FROM);
     p.split16 = tiles && (p.few || a.nq >= split16_min_q(a.kv_format));
     // k_attn_split64: 256 queries a workgroup (one a compute unit, one wave of them) from 768 queries on, else 128
     // (at 512 / 640 rows f32 1.376 / 1.740 -> 1.368 / 1.717 ms and i8 1.337 / 1.705 -> 1.330 / 1.676 ms with the
@@ -1814,13 +1876,18 @@ void attention(hipStream_t s, const AttnShape &a, const float *q, const uint8_t 
         part_ml = part_o + (size_t)p.splits * a.nq * a.heads * hd;
     }
     if (p.few) {
+        const dim3 grid(a.heads * p.splits);
         if (a.kv_format == TAH_KV_I16)
-            hipLaunchKernelGGL((k_attn_few<FEW_Q / 16, TAH_KV_I16>), dim3(a.heads * p.splits), dim3(256), 0, s, a.nq, a.rows,
-                               a.chunk, a.d, a.heads, q, img->images, img->kvmax, p.kb_per_split, p.splits, part_o,
+            hipLaunchKernelGGL((k_attn_few<FEW_Q / 16, TAH_KV_I16>), grid, dim3(256), 0, s, a.nq, a.rows, a.chunk, a.d,
+                               a.heads, q, img->images, img->kvmax, img->scales, p.kb_per_split, p.splits, part_o,
+                               part_ml, out);
+        else if (a.kv_format == TAH_KV_I8)
+            hipLaunchKernelGGL((k_attn_few<FEW_Q / 16, TAH_KV_I8>), grid, dim3(256), 0, s, a.nq, a.rows, a.chunk, a.d,
+                               a.heads, q, img->images, img->kvmax, img->scales, p.kb_per_split, p.splits, part_o,
                                part_ml, out);
         else
-            hipLaunchKernelGGL((k_attn_few<FEW_Q / 16, TAH_KV_F32>), dim3(a.heads * p.splits), dim3(256), 0, s, a.nq, a.rows,
-                               a.chunk, a.d, a.heads, q, img->images, img->kvmax, p.kb_per_split, p.splits, part_o,
+            hipLaunchKernelGGL((k_attn_few<FEW_Q / 16, TAH_KV_F32>), grid, dim3(256), 0, s, a.nq, a.rows, a.chunk, a.d,
+                               a.heads, q, img->images, img->kvmax, img->scales, p.kb_per_split, p.splits, part_o,
                                part_ml, out);
         TAH_LAUNCHED();
     } else if (p.split16) {

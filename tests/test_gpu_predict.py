@@ -56,8 +56,9 @@ def random_layers(rng, layers, rows, chunk, d, kv_format, scale=1.0):
 @pytest.mark.parametrize("nq", [1, 2, 3, 4, 7, 9, 16, 17, 33, 64, 130])
 def test_attention_full_width(gpu, full_model, full_weights, kv_format, rows, chunk, nq):
     """AttendCached::attend at d = 512, 8 heads of 64 over the layer's tiles: f32 up to 16 queries by the few-query
-    kernel (16 / 17 the boundary), beyond by the 32-query tiles (33: a second wavefront of queries); i16 the same from
-    2 queries, one by the decode kernel; chunks of 8 and 48 rows leave some wavefronts' keys past a block's end."""
+    kernel (16 / 17 the boundary), beyond by the 32-query tiles (33: a second wavefront of queries); i8 the same (its
+    chunks' scales copied with each block; chunks of 48 rows: every block begins one), i16 from 2 queries, one by the
+    decode kernel; chunks of 8 and 48 rows leave some wavefronts' keys past a block's end."""
     say(f"attention d=512 fmt={kv_format} rows={rows} chunk={chunk} nq={nq}")
     rng = np.random.default_rng(rows * 7 + nq + kv_format)
     d, L = full_model.d, full_model.icl_layers
