@@ -238,8 +238,8 @@ int tah_calibrate(tah_dev *dev, double ms, double *rate);
  * tah_fit_represent call counts as two, the column and the row stage). */
 uint64_t tah_stages(const tah_dev *dev);
 /* No counterpart in the reference: a measurement hook for benchmarks. Arms HIP events around each launch of the
- * many-query attention kernel (the in-context attention over a layer's tiles from 17 queries) on this device's stream, for up to `launches` launches (0 disarms); one probe per process, arming
- * again resets it. */
+ * many-query attention kernel (the in-context attention over a layer's tiles from 17 queries) on this device's
+ * stream, for up to `launches` launches (0 disarms); one probe per process, arming again resets it. */
 int tah_probe_attention(tah_dev *dev, int32_t launches);
 /* Synchronises the device's stream; *launches = the launches recorded since arming or the last read, *ms = their
  * summed duration in milliseconds. TAH_E_ARG if the probe is not armed for this device. */
