@@ -1188,8 +1188,9 @@ __global__ __launch_bounds__(64 * WAVES, 2) void k_attn_split64(int nq, int rows
 // at the end the four are merged through LDS into the same partials, or output, as k_attn_split64 leaves. The
 // blocks stream through a ring of LDS slots by DMA (f32: four 32 KB slots, three blocks in flight while one is used;
 // i16 and i8: six 20 KB slots), one barrier a block. Launched for one group (up to 16 queries): with two or four groups (17 to 64 queries) it measured slower
-// than k_attn_split64 (17 / 33 / 64 rows 0.836 / 0.852 / 0.884 -> 0.852 / 0.922 / 0.977 ms a prediction), whose
-// 32-query products then have work for their columns.
+// than k_attn_split64 (f32, 17 / 33 / 64 rows 0.836 / 0.852 / 0.884 -> 0.852 / 0.922 / 0.977 ms a prediction; i8 with
+// two groups, 17 / 24 / 32 rows 0.841 / 0.848 / 0.870 -> 0.844 / 0.852 / 0.876 ms), whose 32-query products then have
+// work for their columns.
 constexpr int FEW_Q = 16;
 // i16 code tiles from this many queries: the decode kernel measured faster at one query and slower from two (2 / 3 /
 // 4 / 8 / 16 rows 0.625 / 0.692 / 0.763 / 0.798 / 0.877 -> 0.606 / 0.644 / 0.707 / 0.741 / 0.825 ms with this kernel)
